@@ -1,0 +1,151 @@
+/*
+ * sophia_kda.h -- C ABI of the MI355X (gfx950) Kimi Delta Attention hot path.
+ *
+ * Plain pointers and sizes only: every tensor argument is a device pointer
+ * into HBM, every size is an element count, and `stream` is a hipStream_t
+ * passed as void* (NULL = the default stream).  Calls are asynchronous on
+ * `stream`; no call allocates device memory or synchronises the device.
+ *
+ * Each entry point returns SOPHIA_OK (0) or an error code; the message of the
+ * last failure on the calling thread is returned by sophia_last_error().
+ * Shape / dtype / pointer errors are detected on the host before any launch.
+ *
+ * Reference interfaces replaced (Arain119/Sophia):
+ *   sophia_short_conv_fwd   CausalDepthwiseConv1d.forward
+ *                           (ml/runtime/model/attention.py:32-60) as driven by
+ *                           SophiaKDA._short_convolution (attention.py:226-258),
+ *                           and causal_conv1d_fn
+ *                           (ml/training/pretrain/engine/sm120_concurrent_ffn.py:199-207)
+ *   sophia_short_conv_step  the same forward with T == 1 and the cached
+ *                           history conv_state[:B] (attention.py:236-237,251-257)
+ *   sophia_kda_chunk_fwd    fla.ops.kda.chunk_kda as called at attention.py:349-365
+ *                           with the varlen contract of FlashKDA
+ *                           (sm120_concurrent_ffn.py:209-268,375-423: cu_seqlens,
+ *                           chunk_size = 64, safe_gate, lower_bound, A_log, dt_bias)
+ *   sophia_kda_decode_step  fla.ops.kda.fused_recurrent_kda as called at
+ *                           attention.py:330-348 (T == 1 with a cached state)
+ */
+#ifndef SOPHIA_KDA_H
+#define SOPHIA_KDA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes -------------------------------------------------------- */
+#define SOPHIA_OK 0
+#define SOPHIA_ERR_INVALID 1   /* bad shape, dtype, size or NULL pointer      */
+#define SOPHIA_ERR_HIP 2       /* HIP runtime reported an error on launch      */
+#define SOPHIA_ERR_WORKSPACE 3 /* workspace smaller than the size query says  */
+
+/* ---- element types ------------------------------------------------------- */
+#define SOPHIA_DTYPE_F32 0
+#define SOPHIA_DTYPE_BF16 1
+
+/* ---- KDA core switches (the use_*_in_kernel flags of chunk_kda) ---------- */
+#define SOPHIA_KDA_QK_L2NORM 1u      /* q,k <- q/|q|, k/|k| (eps 1e-12)        */
+#define SOPHIA_KDA_GATE_IN_KERNEL 2u /* g <- lb*sigmoid(exp(A_log[h])*(g+dt_bias)) */
+#define SOPHIA_KDA_BETA_SIGMOID 4u   /* beta <- sigmoid(beta)                   */
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *sophia_last_error(void);
+
+/* ABI version of this library (major * 100 + minor). */
+int sophia_abi_version(void);
+
+/*
+ * Depthwise causal conv (kernel K, SiLU) over a packed ragged batch.
+ *   x, y        : [total_tokens, channels] rows; row strides in elements.
+ *                 dtype SOPHIA_DTYPE_F32 or _BF16 (same for x and y).
+ *   weight      : [channels, K] fp32, weight[:, K-1] multiplies the newest token.
+ *   cu_seqlens  : [n_seqs + 1] int32 device offsets, cu_seqlens[0] == 0,
+ *                 cu_seqlens[n_seqs] == total_tokens.
+ *   conv_state  : [n_state_slots, channels, K-1] fp32 or NULL.  Sequence s uses
+ *                 slot state_slots[s] (or s when state_slots is NULL); a slot
+ *                 outside [0, n_state_slots) means no history: zeros are read
+ *                 and nothing is written.
+ *   read_history: 1 = the K-1 samples before each sequence come from
+ *                 conv_state, 0 = zeros.
+ *   write_history: 1 = conv_state[slot] <- last K-1 samples of cat(history, x).
+ * y[t, c] = silu(sum_j weight[c, j] * seq[t + j]), seq = cat(history, x).
+ */
+int sophia_short_conv_fwd(const void *x, int64_t x_row_stride, void *y, int64_t y_row_stride,
+                          int dtype, const float *weight, float *conv_state, int n_state_slots,
+                          const int32_t *state_slots, const int32_t *cu_seqlens, int n_seqs,
+                          int64_t total_tokens, int channels, int kernel_size, int read_history,
+                          int write_history, void *stream);
+
+/*
+ * One-token conv step for `batch` sequences (decode).  x, y: [batch, channels]
+ * rows; conv_state / slots as above, read when read_history != 0 and always
+ * updated (rows whose slot is out of range run with zero history, no update).
+ */
+int sophia_short_conv_step(const void *x, int64_t x_row_stride, void *y, int64_t y_row_stride,
+                           int dtype, const float *weight, float *conv_state, int n_state_slots,
+                           const int32_t *state_slots, int batch, int channels, int kernel_size,
+                           int read_history, void *stream);
+
+/*
+ * Workspace bytes needed by sophia_kda_chunk_fwd for a packed batch of
+ * `total_tokens` tokens in `n_seqs` sequences with `num_heads` heads
+ * (head_dim 128).  Depends only on these sizes, never on the offsets.
+ */
+size_t sophia_kda_chunk_workspace_size(int64_t total_tokens, int n_seqs, int num_heads,
+                                       int head_dim);
+
+/*
+ * Chunkwise (C = 64) gated delta-rule prefill over a packed ragged batch.
+ *   q, k        : [total_tokens, H, 128] rows of stride qkv_row_stride elements
+ *                 (head h at element offset h*128 inside a row); dtype qkv_dtype.
+ *   v           : same layout as q, value dim 128.
+ *   g           : [total_tokens, H, 128], row stride g_row_stride, dtype g_dtype;
+ *                 decay logits when SOPHIA_KDA_GATE_IN_KERNEL is set, else the
+ *                 log-decay itself.  The log-decay must lie in [lower_bound, 0]
+ *                 with lower_bound >= -5 (the safe-gate range of the kernel).
+ *   beta        : [total_tokens, H], row stride beta_row_stride, dtype beta_dtype.
+ *   A_log, dt_bias: [H] and [H*128] fp32 (read only with GATE_IN_KERNEL).
+ *   scale       : multiplier of q (chunk_kda default 128^-0.5).
+ *   initial_state, final_state: [n_state_slots, H, 128, 128] fp32 (state[k][v])
+ *                 or NULL (zero initial state / final state not written);
+ *                 sequence s uses slot state_slots[s] (or s); they may alias.
+ *                 A slot outside [0, n_state_slots) starts from zero and is
+ *                 not written.
+ *   o           : [total_tokens, H, 128] rows of stride o_row_stride, dtype qkv_dtype.
+ *   workspace   : device scratch of sophia_kda_chunk_workspace_size() bytes,
+ *                 256-byte aligned; contents need not be initialised.
+ */
+int sophia_kda_chunk_fwd(const void *q, const void *k, const void *v, int64_t qkv_row_stride,
+                         int qkv_dtype, const void *g, int64_t g_row_stride, int g_dtype,
+                         const void *beta, int64_t beta_row_stride, int beta_dtype,
+                         const float *A_log, const float *dt_bias, float scale, float lower_bound,
+                         unsigned flags, const int32_t *cu_seqlens, int n_seqs,
+                         int64_t total_tokens, int num_heads, int head_dim,
+                         const float *initial_state, float *final_state, int n_state_slots,
+                         const int32_t *state_slots, void *o, int64_t o_row_stride,
+                         void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * One recurrent step for `batch` sequences, state updated in place.
+ *   q, k, v, g : [batch, H, 128] rows (strides in elements), beta: [batch, H].
+ *   state      : [n_state_slots, H, 128, 128] fp32; row b uses slot
+ *                state_slots[b] (or b); an out-of-range slot leaves the state
+ *                untouched and the row's output 0.  read_state == 0 treats
+ *                the incoming state as zero.
+ *   o          : [batch, H, 128] rows of stride o_row_stride, dtype qkv_dtype.
+ */
+int sophia_kda_decode_step(const void *q, const void *k, const void *v, int64_t qkv_row_stride,
+                           int qkv_dtype, const void *g, int64_t g_row_stride, int g_dtype,
+                           const void *beta, int64_t beta_row_stride, int beta_dtype,
+                           const float *A_log, const float *dt_bias, float scale,
+                           float lower_bound, unsigned flags, float *state, int n_state_slots,
+                           const int32_t *state_slots, int read_state, int batch, int num_heads,
+                           int head_dim, void *o, int64_t o_row_stride, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SOPHIA_KDA_H */

@@ -1,0 +1,387 @@
+// ShortConv: depthwise causal conv1d (kernel K <= 4) + SiLU with a rolling
+// fp32 history cache, over a packed ragged batch.
+//
+// Semantics follow CausalDepthwiseConv1d.forward (ml/runtime/model/attention.py:32-60):
+//   seq = cat(history[c, 0:K-1], x[:, c]);  y[t, c] = silu(sum_j w[c, j] * seq[t + j]);
+//   next_history = seq[-(K-1):].
+// One launch covers every channel of the fused q|k|v projection output
+// (3 x 2048 channels at Sophia's shape), which is how SophiaKDA._short_convolution
+// (attention.py:226-258) applies three convs and writes conv_state[:, 0..2].
+//
+// Memory-bound: each thread owns 8 consecutive channels (16 B of bf16) and
+// walks 16 consecutive packed rows, keeping the K-1 previous samples in
+// registers, so every x element is read from HBM once and y written once.
+#include "common.hpp"
+
+namespace sophia {
+namespace {
+
+constexpr int kVec = 8;        // channels per thread
+constexpr int kRows = 16;      // packed rows per thread
+constexpr int kVecsPerBlock = 64;
+constexpr int kRowTilesPerBlock = 4;
+
+template <int DT>
+struct Vec8 {
+  float v[kVec];
+  __device__ __forceinline__ void load(const void *base, int64_t idx) {
+    if constexpr (DT == SOPHIA_DTYPE_BF16) {
+      u4 w = *reinterpret_cast<const u4 *>(static_cast<const uint16_t *>(base) + idx);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[2 * i] = __uint_as_float(w[i] << 16);
+        v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+      }
+    } else {
+      const f4 *p = reinterpret_cast<const f4 *>(static_cast<const float *>(base) + idx);
+      f4 a = p[0], b = p[1];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[i] = a[i];
+        v[4 + i] = b[i];
+      }
+    }
+  }
+  __device__ __forceinline__ void store(void *base, int64_t idx) const {
+    if constexpr (DT == SOPHIA_DTYPE_BF16) {
+      u4 w;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
+      *reinterpret_cast<u4 *>(static_cast<uint16_t *>(base) + idx) = w;
+    } else {
+      f4 *p = reinterpret_cast<f4 *>(static_cast<float *>(base) + idx);
+      f4 a, b;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        a[i] = v[i];
+        b[i] = v[4 + i];
+      }
+      p[0] = a;
+      p[1] = b;
+    }
+  }
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int i = 0; i < kVec; ++i) v[i] = 0.f;
+  }
+};
+
+// Rounds a history value the way the reference does before convolving: the
+// cached fp32 history is cast to x's dtype (attention.py:48).
+template <int DT>
+__device__ __forceinline__ float as_input_dtype(float h) {
+  if constexpr (DT == SOPHIA_DTYPE_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(h));
+  return h;
+}
+
+// Largest s in [0, n) with cu[s] <= row.
+__device__ __forceinline__ int find_seq(const int32_t *cu, int n, int64_t row) {
+  int lo = 0, hi = n - 1;
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if (cu[mid] <= row)
+      lo = mid;
+    else
+      hi = mid - 1;
+  }
+  return lo;
+}
+
+// Loads the K-1 samples preceding packed row `row` of sequence `seq`
+// (prev[d-1] = sample at row - d) from x or from the history cache.
+template <int K, int DT>
+__device__ __forceinline__ void init_window(Vec8<DT> (&prev)[K > 1 ? K - 1 : 1], const void *x,
+                                            int64_t xs, const float *hist, int64_t row,
+                                            int64_t seq_start, int c0, int channels) {
+#pragma unroll
+  for (int d = 1; d < K; ++d) {
+    int64_t tau = row - d;
+    if (tau >= seq_start) {
+      prev[d - 1].load(x, tau * xs + c0);
+    } else if (hist != nullptr) {
+      int idx = (K - 1) + static_cast<int>(tau - seq_start);  // 0 .. K-2
+#pragma unroll
+      for (int i = 0; i < kVec; ++i)
+        prev[d - 1].v[i] = as_input_dtype<DT>(hist[static_cast<int64_t>(c0 + i) * (K - 1) + idx]);
+    } else {
+      prev[d - 1].zero();
+    }
+  }
+}
+
+template <int K, int DT>
+__global__ __launch_bounds__(256) void short_conv_fwd_kernel(
+    const void *__restrict__ x, int64_t xs, void *__restrict__ y, int64_t ys,
+    const float *__restrict__ weight, const float *__restrict__ conv_state, int n_slots,
+    const int32_t *__restrict__ slots, const int32_t *__restrict__ cu, int n_seqs, int64_t total,
+    int channels, int read_history) {
+  const int cv = blockIdx.x * kVecsPerBlock + threadIdx.x;
+  const int c0 = cv * kVec;
+  const int64_t r0 = (static_cast<int64_t>(blockIdx.y) * kRowTilesPerBlock + threadIdx.y) * kRows;
+  if (c0 >= channels || r0 >= total) return;
+  const int64_t r1 = min(r0 + kRows, total);
+
+  float w[kVec][K];
+#pragma unroll
+  for (int i = 0; i < kVec; ++i)
+#pragma unroll
+    for (int j = 0; j < K; ++j) w[i][j] = weight[static_cast<int64_t>(c0 + i) * K + j];
+
+  int s = find_seq(cu, n_seqs, r0);
+  int64_t seq_start = cu[s], seq_end = cu[s + 1];
+  auto hist_of = [&](int seq) -> const float * {
+    if (!read_history || conv_state == nullptr || K == 1) return nullptr;
+    int slot = slots ? slots[seq] : seq;
+    if (slot < 0 || slot >= n_slots) return nullptr;
+    return conv_state + static_cast<int64_t>(slot) * channels * (K - 1);
+  };
+  Vec8<DT> prev[K > 1 ? K - 1 : 1];
+  init_window<K, DT>(prev, x, xs, hist_of(s), r0, seq_start, c0, channels);
+  for (int64_t r = r0; r < r1; ++r) {
+    if (r >= seq_end) {
+      do {
+        ++s;
+        seq_start = cu[s];
+        seq_end = cu[s + 1];
+      } while (r >= seq_end);
+      init_window<K, DT>(prev, x, xs, hist_of(s), r, seq_start, c0, channels);
+    }
+    Vec8<DT> cur;
+    cur.load(x, r * xs + c0);
+    Vec8<DT> out;
+#pragma unroll
+    for (int i = 0; i < kVec; ++i) {
+      float acc = w[i][K - 1] * cur.v[i];
+#pragma unroll
+      for (int d = 1; d < K; ++d) acc = fmaf(w[i][K - 1 - d], prev[d - 1].v[i], acc);
+      out.v[i] = acc * sigmoid_f(acc);
+    }
+    out.store(y, r * ys + c0);
+#pragma unroll
+    for (int d = K - 1; d >= 2; --d) prev[d - 1] = prev[d - 2];
+    if constexpr (K > 1) prev[0] = cur;
+  }
+}
+
+// conv_state[slot(s)] <- last K-1 samples of cat(history, x_s).  Runs after
+// short_conv_fwd_kernel on the same stream, so the old history has been read.
+template <int K, int DT>
+__global__ __launch_bounds__(256) void short_conv_history_kernel(
+    const void *__restrict__ x, int64_t xs, float *__restrict__ conv_state, int n_slots,
+    const int32_t *__restrict__ slots, const int32_t *__restrict__ cu, int n_seqs, int channels,
+    int read_history) {
+  const int cv = blockIdx.x * blockDim.x + threadIdx.x;
+  const int s = blockIdx.y;
+  const int c0 = cv * kVec;
+  if (c0 >= channels || s >= n_seqs) return;
+  const int64_t start = cu[s], end = cu[s + 1];
+  const int slot = slots ? slots[s] : s;
+  if (slot < 0 || slot >= n_slots) return;
+  float *hist = conv_state + static_cast<int64_t>(slot) * channels * (K - 1);
+  float nh[kVec][K - 1];
+#pragma unroll
+  for (int j = 0; j < K - 1; ++j) {
+    const int64_t tau = end - (K - 1) + j;
+    if (tau >= start) {
+      Vec8<DT> v;
+      v.load(x, tau * xs + c0);
+#pragma unroll
+      for (int i = 0; i < kVec; ++i) nh[i][j] = v.v[i];
+    } else {
+      const int idx = (K - 1) + static_cast<int>(tau - start);
+#pragma unroll
+      for (int i = 0; i < kVec; ++i)
+        nh[i][j] = read_history
+                       ? as_input_dtype<DT>(hist[static_cast<int64_t>(c0 + i) * (K - 1) + idx])
+                       : 0.f;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kVec; ++i)
+#pragma unroll
+    for (int j = 0; j < K - 1; ++j) hist[static_cast<int64_t>(c0 + i) * (K - 1) + j] = nh[i][j];
+}
+
+// One token per sequence: read history, convolve, write the shifted history.
+template <int K, int DT>
+__global__ __launch_bounds__(256) void short_conv_step_kernel(
+    const void *__restrict__ x, int64_t xs, void *__restrict__ y, int64_t ys,
+    const float *__restrict__ weight, float *__restrict__ conv_state, int n_slots,
+    const int32_t *__restrict__ slots, int batch, int channels, int read_history) {
+  const int cv = blockIdx.x * blockDim.x + threadIdx.x;
+  const int b = blockIdx.y;
+  const int c0 = cv * kVec;
+  if (c0 >= channels || b >= batch) return;
+  const int slot = slots ? slots[b] : b;
+  const bool has_slot = slot >= 0 && slot < n_slots;
+  if (!has_slot) read_history = 0;
+  float *hist = conv_state + static_cast<int64_t>(has_slot ? slot : 0) * channels * (K - 1);
+  Vec8<DT> cur;
+  cur.load(x, static_cast<int64_t>(b) * xs + c0);
+  float h[kVec][K > 1 ? K - 1 : 1];
+  if constexpr (K > 1) {
+    if (read_history) {
+      // 8 channels x (K-1) fp32 history values are contiguous.
+      const float *hp = hist + static_cast<int64_t>(c0) * (K - 1);
+#pragma unroll
+      for (int i = 0; i < kVec; ++i)
+#pragma unroll
+        for (int j = 0; j < K - 1; ++j) h[i][j] = as_input_dtype<DT>(hp[i * (K - 1) + j]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kVec; ++i)
+#pragma unroll
+        for (int j = 0; j < K - 1; ++j) h[i][j] = 0.f;
+    }
+  }
+  Vec8<DT> out;
+#pragma unroll
+  for (int i = 0; i < kVec; ++i) {
+    float acc = weight[static_cast<int64_t>(c0 + i) * K + (K - 1)] * cur.v[i];
+#pragma unroll
+    for (int j = 0; j < K - 1; ++j)
+      acc = fmaf(weight[static_cast<int64_t>(c0 + i) * K + j], h[i][j], acc);
+    out.v[i] = acc * sigmoid_f(acc);
+  }
+  out.store(y, static_cast<int64_t>(b) * ys + c0);
+  if (!has_slot) return;
+  if constexpr (K > 1) {
+    float *hp = hist + static_cast<int64_t>(c0) * (K - 1);
+#pragma unroll
+    for (int i = 0; i < kVec; ++i) {
+#pragma unroll
+      for (int j = 0; j + 1 < K - 1; ++j) hp[i * (K - 1) + j] = h[i][j + 1];
+      hp[i * (K - 1) + (K - 2)] = cur.v[i];
+    }
+  }
+}
+
+template <int K, int DT>
+int launch_fwd(const void *x, int64_t xs, void *y, int64_t ys, const float *w, float *state,
+               int n_slots, const int32_t *slots, const int32_t *cu, int n, int64_t total, int channels,
+               int read_history, int write_history, hipStream_t st) {
+  const int nvec = channels / kVec;
+  dim3 block(kVecsPerBlock, kRowTilesPerBlock);
+  const int64_t row_tiles = (total + kRows - 1) / kRows;
+  dim3 grid((nvec + kVecsPerBlock - 1) / kVecsPerBlock,
+            static_cast<unsigned>((row_tiles + kRowTilesPerBlock - 1) / kRowTilesPerBlock));
+  if (total > 0) {
+    hipLaunchKernelGGL((short_conv_fwd_kernel<K, DT>), grid, block, 0, st, x, xs, y, ys, w, state,
+                       n_slots, slots, cu, n, total, channels, read_history && state != nullptr);
+    int rc = check_launch("short_conv_fwd");
+    if (rc) return rc;
+  }
+  if constexpr (K > 1) {
+    if (write_history && state != nullptr && n > 0) {
+      dim3 g2((nvec + 255) / 256, n);
+      hipLaunchKernelGGL((short_conv_history_kernel<K, DT>), g2, dim3(256), 0, st, x, xs, state,
+                         n_slots, slots, cu, n, channels, read_history);
+      return check_launch("short_conv_history");
+    }
+  }
+  return SOPHIA_OK;
+}
+
+template <int K, int DT>
+int launch_step(const void *x, int64_t xs, void *y, int64_t ys, const float *w, float *state,
+                int n_slots, const int32_t *slots, int batch, int channels, int read_history, hipStream_t st) {
+  const int nvec = channels / kVec;
+  dim3 grid((nvec + 255) / 256, batch);
+  hipLaunchKernelGGL((short_conv_step_kernel<K, DT>), grid, dim3(256), 0, st, x, xs, y, ys, w,
+                     state, n_slots, slots, batch, channels, read_history);
+  return check_launch("short_conv_step");
+}
+
+template <int DT>
+int dispatch_fwd(int K, const void *x, int64_t xs, void *y, int64_t ys, const float *w,
+                 float *state, int ns, const int32_t *slots, const int32_t *cu, int n, int64_t total,
+                 int channels, int rh, int wh, hipStream_t st) {
+  switch (K) {
+    case 1: return launch_fwd<1, DT>(x, xs, y, ys, w, state, ns, slots, cu, n, total, channels, rh, wh, st);
+    case 2: return launch_fwd<2, DT>(x, xs, y, ys, w, state, ns, slots, cu, n, total, channels, rh, wh, st);
+    case 3: return launch_fwd<3, DT>(x, xs, y, ys, w, state, ns, slots, cu, n, total, channels, rh, wh, st);
+    case 4: return launch_fwd<4, DT>(x, xs, y, ys, w, state, ns, slots, cu, n, total, channels, rh, wh, st);
+  }
+  return set_error(SOPHIA_ERR_INVALID, "short_conv: kernel_size %d not in 1..4", K);
+}
+
+template <int DT>
+int dispatch_step(int K, const void *x, int64_t xs, void *y, int64_t ys, const float *w,
+                  float *state, int ns, const int32_t *slots, int batch, int channels, int rh,
+                  hipStream_t st) {
+  switch (K) {
+    case 2: return launch_step<2, DT>(x, xs, y, ys, w, state, ns, slots, batch, channels, rh, st);
+    case 3: return launch_step<3, DT>(x, xs, y, ys, w, state, ns, slots, batch, channels, rh, st);
+    case 4: return launch_step<4, DT>(x, xs, y, ys, w, state, ns, slots, batch, channels, rh, st);
+  }
+  return set_error(SOPHIA_ERR_INVALID, "short_conv_step: kernel_size %d not in 2..4", K);
+}
+
+}  // namespace
+}  // namespace sophia
+
+using namespace sophia;
+
+extern "C" int sophia_short_conv_fwd(const void *x, int64_t x_row_stride, void *y,
+                                     int64_t y_row_stride, int dtype, const float *weight,
+                                     float *conv_state, int n_state_slots,
+                                     const int32_t *state_slots, const int32_t *cu_seqlens, int n_seqs, int64_t total_tokens,
+                                     int channels, int kernel_size, int read_history,
+                                     int write_history, void *stream) {
+  SOPHIA_REQUIRE(dtype == SOPHIA_DTYPE_F32 || dtype == SOPHIA_DTYPE_BF16,
+                 "short_conv_fwd: dtype %d not supported", dtype);
+  SOPHIA_REQUIRE(channels > 0 && channels % kVec == 0,
+                 "short_conv_fwd: channels (%d) must be a positive multiple of %d", channels, kVec);
+  SOPHIA_REQUIRE(n_seqs > 0 && total_tokens >= 0, "short_conv_fwd: bad n_seqs/total_tokens");
+  SOPHIA_REQUIRE(kernel_size >= 1 && kernel_size <= 4, "short_conv_fwd: kernel_size must be 1..4");
+  SOPHIA_REQUIRE(weight && cu_seqlens && (total_tokens == 0 || (x && y)),
+                 "short_conv_fwd: NULL pointer");
+  SOPHIA_REQUIRE(x_row_stride >= channels && y_row_stride >= channels,
+                 "short_conv_fwd: row stride smaller than channels");
+  SOPHIA_REQUIRE(x_row_stride % kVec == 0 && y_row_stride % kVec == 0,
+                 "short_conv_fwd: row strides must be multiples of %d", kVec);
+  SOPHIA_REQUIRE(((uintptr_t)x % 16) == 0 && ((uintptr_t)y % 16) == 0,
+                 "short_conv_fwd: x and y must be 16-byte aligned");
+  SOPHIA_REQUIRE(!(read_history || write_history) || conv_state || kernel_size == 1,
+                 "short_conv_fwd: history requested without conv_state");
+  SOPHIA_REQUIRE(conv_state == nullptr || n_state_slots >= 0,
+                 "short_conv_fwd: n_state_slots must be >= 0");
+  SOPHIA_REQUIRE(total_tokens / 64 < 65535, "short_conv_fwd: too many tokens for one launch");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == SOPHIA_DTYPE_BF16)
+    return dispatch_fwd<SOPHIA_DTYPE_BF16>(kernel_size, x, x_row_stride, y, y_row_stride, weight,
+                                           conv_state, n_state_slots, state_slots, cu_seqlens,
+                                           n_seqs, total_tokens, channels, read_history,
+                                           write_history, st);
+  return dispatch_fwd<SOPHIA_DTYPE_F32>(kernel_size, x, x_row_stride, y, y_row_stride, weight,
+                                        conv_state, n_state_slots, state_slots, cu_seqlens, n_seqs,
+                                        total_tokens, channels, read_history, write_history, st);
+}
+
+extern "C" int sophia_short_conv_step(const void *x, int64_t x_row_stride, void *y,
+                                      int64_t y_row_stride, int dtype, const float *weight,
+                                      float *conv_state, int n_state_slots,
+                                      const int32_t *state_slots, int batch,
+                                      int channels, int kernel_size, int read_history,
+                                      void *stream) {
+  SOPHIA_REQUIRE(dtype == SOPHIA_DTYPE_F32 || dtype == SOPHIA_DTYPE_BF16,
+                 "short_conv_step: dtype %d not supported", dtype);
+  SOPHIA_REQUIRE(channels > 0 && channels % kVec == 0,
+                 "short_conv_step: channels (%d) must be a positive multiple of %d", channels, kVec);
+  SOPHIA_REQUIRE(batch > 0 && batch <= 65535, "short_conv_step: batch must be 1..65535");
+  SOPHIA_REQUIRE(kernel_size >= 2 && kernel_size <= 4, "short_conv_step: kernel_size must be 2..4");
+  SOPHIA_REQUIRE(x && y && weight && conv_state, "short_conv_step: NULL pointer");
+  SOPHIA_REQUIRE(x_row_stride >= channels && y_row_stride >= channels &&
+                     x_row_stride % kVec == 0 && y_row_stride % kVec == 0,
+                 "short_conv_step: bad row strides");
+  SOPHIA_REQUIRE(((uintptr_t)x % 16) == 0 && ((uintptr_t)y % 16) == 0,
+                 "short_conv_step: x and y must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == SOPHIA_DTYPE_BF16)
+    return dispatch_step<SOPHIA_DTYPE_BF16>(kernel_size, x, x_row_stride, y, y_row_stride, weight,
+                                            conv_state, n_state_slots, state_slots, batch,
+                                            channels, read_history, st);
+  return dispatch_step<SOPHIA_DTYPE_F32>(kernel_size, x, x_row_stride, y, y_row_stride, weight,
+                                         conv_state, n_state_slots, state_slots, batch, channels,
+                                         read_history, st);
+}

@@ -1,0 +1,409 @@
+"""The KDA token mixer on MI355X: a drop-in for the reference's ``SophiaKDA``.
+
+Same parameter names, shapes and initialisation order as
+ml/runtime/model/attention.py:66-143 (so a reference state_dict loads as is
+and seeded initialisation draws the same stream), the same cache buffers and
+cache/snapshot methods (attention.py:145-224), and the same
+``forward(x, *, start_pos)`` semantics including the pad mask
+(attention.py:373-420, 660-670).  ``forward_packed`` adds the packed ragged
+entry (cu_seqlens + cache slots) used for continuous batching.
+
+Compute: the input projections run as one fused GEMM (q|k|v|decay_down|beta|
+output_gate, hipBLASLt through torch), the ShortConv and the KDA core run in
+the gfx950 HIP kernels of ``sophia_amd/csrc`` (chunk-64 prefill, in-place
+decode step), then RMSNorm * sigmoid(gate) and o_proj.  Tensors on the CPU are
+rejected: the per-token reference recurrence is not part of this package.
+"""
+
+from __future__ import annotations
+
+import functools
+import math
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from . import ops
+from .config import ModelArgs
+from .state import LayerCacheSnapshot
+
+PAD_LOGIT = -1.0e4  # attention.py:17
+
+
+def _inverse_softplus(value: torch.Tensor) -> torch.Tensor:
+    """attention.py:20-21."""
+    return value + torch.log(-torch.expm1(-value))
+
+
+def _require_gpu(x: torch.Tensor) -> None:
+    if x.device.type != "cuda":
+        raise RuntimeError(
+            "sophia_amd KDA runs on a ROCm GPU only; move the module and inputs to 'cuda' "
+            "(the per-token CPU recurrence is the test oracle, not a product path)")
+
+
+class RuntimeLinear(nn.Module):
+    """Bias-free linear with N(0, 0.02) init (ml/runtime/model/runtime_linear.py:10-33)."""
+
+    def __init__(self, in_features: int, out_features: int, *, bias: bool = False) -> None:
+        super().__init__()
+        self.in_features = int(in_features)
+        self.out_features = int(out_features)
+        self.weight = nn.Parameter(torch.empty(self.out_features, self.in_features))
+        self.bias = nn.Parameter(torch.empty(self.out_features)) if bias else None
+        nn.init.normal_(self.weight, mean=0.0, std=0.02)
+        if self.bias is not None:
+            nn.init.zeros_(self.bias)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return F.linear(x, self.weight, self.bias)
+
+
+class RMSNorm(nn.Module):
+    """ops.py:49-64: functional.rms_norm over the last dim, fp32 weight."""
+
+    def __init__(self, dim: int, eps: float = 1e-6) -> None:
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(dim, dtype=torch.float32))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return F.rms_norm(x, (int(x.size(-1)),), self.weight.to(x.dtype), float(self.eps))
+
+
+class CausalDepthwiseConv1d(nn.Module):
+    """attention.py:24-60 on the HIP ShortConv kernel."""
+
+    def __init__(self, channels: int, kernel_size: int) -> None:
+        super().__init__()
+        self.channels = int(channels)
+        self.kernel_size = int(kernel_size)
+        self.weight = nn.Parameter(torch.empty(self.channels, self.kernel_size))
+        nn.init.normal_(self.weight, mean=0.0, std=0.02)
+
+    def forward(self, x: torch.Tensor, *, history: torch.Tensor | None = None):
+        """x: [B, T, C]; history: [B, C, K-1] or None.  Returns
+        (silu(conv) [B, T, C], next_history [B, C, K-1] in x.dtype)."""
+        _require_gpu(x)
+        bsz, seqlen, channels = x.shape
+        hist_len = self.kernel_size - 1
+        flat = x.reshape(bsz * seqlen, channels)
+        cu = torch.arange(0, (bsz + 1) * seqlen, seqlen, dtype=torch.int32, device=x.device)
+        state = None
+        if hist_len > 0:
+            state = torch.zeros((bsz, channels, hist_len), dtype=torch.float32, device=x.device)
+            if history is not None:
+                state.copy_(history.to(dtype=x.dtype).float())
+        y = ops.short_conv_fwd(flat, self.weight, cu, conv_state=state,
+                               read_history=history is not None and hist_len > 0,
+                               write_history=hist_len > 0)
+        next_history = (state.to(x.dtype) if state is not None
+                        else x.new_zeros((bsz, channels, 0)))
+        return y.view(bsz, seqlen, channels), next_history
+
+
+class SophiaKDA(nn.Module):
+    """Kimi Delta Attention mixer (attention.py:63-420) on gfx950 kernels."""
+
+    def __init__(self, args: ModelArgs) -> None:
+        super().__init__()
+        self.dim = int(args.dim)
+        self.num_heads = int(args.num_heads)
+        self.head_dim = int(args.head_dim)
+        self.inner_dim = self.num_heads * self.head_dim
+        self.decay_rank = int(args.kda_decay_rank)
+        self.output_gate_rank = int(args.kda_output_gate_rank)
+        self.output_gate_full_rank = bool(args.kda_output_gate_full_rank)
+        self.lower_bound = float(args.kda_decay_lower_bound)
+        self.dt_min = float(args.kda_dt_min)
+        self.dt_max = float(args.kda_dt_max)
+        self.dt_floor = float(args.kda_dt_floor)
+        self.backend = str(args.kda_backend)
+        self.use_cache = bool(args.use_cache)
+        self.conv_kernel = int(args.short_conv_kernel)
+        self.norm_eps = float(args.norm_eps)
+
+        # Parameter creation order = the reference's RNG draw order.
+        self.q_proj = RuntimeLinear(self.dim, self.inner_dim)
+        self.k_proj = RuntimeLinear(self.dim, self.inner_dim)
+        self.v_proj = RuntimeLinear(self.dim, self.inner_dim)
+        self.q_conv = CausalDepthwiseConv1d(self.inner_dim, self.conv_kernel)
+        self.k_conv = CausalDepthwiseConv1d(self.inner_dim, self.conv_kernel)
+        self.v_conv = CausalDepthwiseConv1d(self.inner_dim, self.conv_kernel)
+        self.decay_down = RuntimeLinear(self.dim, self.decay_rank)
+        self.decay_up = RuntimeLinear(self.decay_rank, self.inner_dim)
+        self.beta_proj = RuntimeLinear(self.dim, self.num_heads)
+        self.A_log = nn.Parameter(torch.full((self.num_heads,), float(args.kda_a_log_init),
+                                             dtype=torch.float32))
+        dt = torch.exp(torch.rand(self.inner_dim, dtype=torch.float32)
+                       * (math.log(self.dt_max) - math.log(self.dt_min))
+                       + math.log(self.dt_min)).clamp_min(self.dt_floor)
+        self.dt_bias = nn.Parameter(_inverse_softplus(dt))
+        self.A_log._no_weight_decay = True  # type: ignore[attr-defined]
+        self.dt_bias._no_weight_decay = True  # type: ignore[attr-defined]
+        if self.output_gate_full_rank:
+            self.output_gate = RuntimeLinear(self.dim, self.inner_dim)
+        else:
+            self.output_gate_down = RuntimeLinear(self.dim, self.output_gate_rank)
+            self.output_gate_up = RuntimeLinear(self.output_gate_rank, self.inner_dim)
+        self.output_norm = RMSNorm(self.head_dim, args.norm_eps)
+        self.o_proj = RuntimeLinear(self.inner_dim, self.dim)
+
+        self.register_buffer("recurrent_state", torch.zeros(
+            int(args.max_batch_size), self.num_heads, self.head_dim, self.head_dim,
+            dtype=torch.float32), persistent=False)
+        self.register_buffer("conv_state", torch.zeros(
+            int(args.max_batch_size), 3, self.inner_dim, self.conv_kernel - 1,
+            dtype=torch.float32), persistent=False)
+        self._fused_cache: dict[str, tuple[tuple, torch.Tensor]] = {}
+
+    # ------------------------------------------------------------- caches
+    def ensure_batch_capacity(self, batch_size: int) -> None:
+        """attention.py:145-158."""
+        required = int(batch_size)
+        if required <= int(self.recurrent_state.size(0)):
+            return
+        recurrent = self.recurrent_state.new_zeros(required, self.num_heads, self.head_dim,
+                                                   self.head_dim)
+        recurrent[: self.recurrent_state.size(0)].copy_(self.recurrent_state)
+        conv = self.conv_state.new_zeros(required, 3, self.inner_dim, self.conv_kernel - 1)
+        conv[: self.conv_state.size(0)].copy_(self.conv_state)
+        self.recurrent_state = recurrent
+        self.conv_state = conv
+
+    def ensure_sequence_capacity(self, max_seq_len: int) -> None:
+        del max_seq_len  # the recurrent state does not grow with length
+
+    def rebuild_runtime_buffers(self, max_seq_len: int) -> None:
+        del max_seq_len
+        device = self.q_proj.weight.device
+        self.recurrent_state = torch.zeros(int(self.recurrent_state.size(0)), self.num_heads,
+                                           self.head_dim, self.head_dim, device=device,
+                                           dtype=torch.float32)
+        self.conv_state = torch.zeros(int(self.conv_state.size(0)), 3, self.inner_dim,
+                                      self.conv_kernel - 1, device=device, dtype=torch.float32)
+
+    def reset(self) -> None:
+        if self.recurrent_state.is_inference() or self.conv_state.is_inference():
+            self.recurrent_state = torch.zeros_like(self.recurrent_state)
+            self.conv_state = torch.zeros_like(self.conv_state)
+        else:
+            self.recurrent_state.zero_()
+            self.conv_state.zero_()
+
+    def refresh_state_buffers(self) -> None:
+        self.rebuild_runtime_buffers(0)
+
+    def reset_slots(self, slots: torch.Tensor) -> None:
+        """Zero the recurrent and conv caches of the given slots (new sequences)."""
+        idx = slots.to(device=self.recurrent_state.device, dtype=torch.long)
+        self.recurrent_state.index_fill_(0, idx, 0.0)
+        self.conv_state.index_fill_(0, idx, 0.0)
+
+    def cache_snapshot(self, *, device: str, batch_size: int, cache_pos: int | None):
+        del cache_pos
+        return LayerCacheSnapshot(recurrent=self.recurrent_state[:batch_size].to(device).clone(),
+                                  conv=self.conv_state[:batch_size].to(device).clone())
+
+    def validate_cache_snapshot(self, snapshot: LayerCacheSnapshot) -> None:
+        if snapshot.latent is not None:
+            raise ValueError("KDA cache cannot contain MLA latent state")
+        if (snapshot.recurrent is not None
+                and tuple(snapshot.recurrent.shape[1:]) != tuple(self.recurrent_state.shape[1:])):
+            raise ValueError("KDA recurrent cache shape mismatch")
+        if (snapshot.conv is not None
+                and tuple(snapshot.conv.shape[1:]) != tuple(self.conv_state.shape[1:])):
+            raise ValueError("KDA convolution cache shape mismatch")
+
+    def load_cache_snapshot(self, snapshot: LayerCacheSnapshot) -> None:
+        self.validate_cache_snapshot(snapshot)
+        required = snapshot.batch_size()
+        self.ensure_batch_capacity(required)
+        if snapshot.recurrent is not None:
+            self.recurrent_state[:required].copy_(
+                snapshot.recurrent.to(self.recurrent_state.device, dtype=torch.float32))
+        if snapshot.conv is not None:
+            self.conv_state[:required].copy_(
+                snapshot.conv.to(self.conv_state.device, dtype=torch.float32))
+
+    # ------------------------------------------------------------- fused weights
+    def _cached(self, key: str, params: tuple[torch.Tensor, ...], build, dtype: torch.dtype):
+        stamp = tuple((p.data_ptr(), p._version) for p in params) + (dtype,)
+        hit = self._fused_cache.get(key)
+        if hit is not None and hit[0] == stamp:
+            return hit[1]
+        with torch.no_grad():
+            value = build().to(dtype).contiguous()
+        self._fused_cache[key] = (stamp, value)
+        return value
+
+    def _input_weight(self, dtype: torch.dtype) -> torch.Tensor:
+        """[3*inner + decay_rank + heads (+ inner | + gate_rank), dim]: every
+        projection of x in one GEMM."""
+        mods = [self.q_proj, self.k_proj, self.v_proj, self.decay_down, self.beta_proj]
+        mods.append(self.output_gate if self.output_gate_full_rank else self.output_gate_down)
+        params = tuple(m.weight for m in mods)
+        return self._cached("in", params, lambda: torch.cat([p.detach() for p in params], 0), dtype)
+
+    def _conv_weight(self) -> torch.Tensor:
+        params = (self.q_conv.weight, self.k_conv.weight, self.v_conv.weight)
+        return self._cached("conv", params, lambda: torch.cat([p.detach() for p in params], 0),
+                            torch.float32)
+
+    def _project(self, x2: torch.Tensor):
+        """x2: [N, dim] -> views (qkv [N, 3*inner], decay_down, beta, gate_logits)."""
+        y = F.linear(x2, self._input_weight(x2.dtype))
+        i, r, h = self.inner_dim, self.decay_rank, self.num_heads
+        qkv = y[:, : 3 * i]
+        dd = y[:, 3 * i: 3 * i + r]
+        beta = y[:, 3 * i + r: 3 * i + r + h]
+        gate = y[:, 3 * i + r + h:]
+        if not self.output_gate_full_rank:
+            gate = self.output_gate_up(gate)
+        return qkv, dd, beta, gate
+
+    # ------------------------------------------------------------- kernel seam
+    @staticmethod
+    def _fla_chunk_kda():
+        """Chunk prefill callable (seam of attention.py:305-312)."""
+        return ops.chunk_kda
+
+    @staticmethod
+    def _fla_fused_recurrent_kda():
+        """One-token recurrent step (seam of attention.py:296-303); updates the
+        cached state in place, the mixer's copy-back then has nothing to do."""
+        return functools.partial(ops.fused_recurrent_kda, inplace_state=True)
+
+    def _run_kda(self, q, k, v, decay_logits, beta_logits, initial_state):
+        """attention.py:314-371 with the HIP kernels behind the same seam."""
+        if self.backend == "reference":
+            raise RuntimeError("kda_backend='reference' selects the per-token CPU recurrence, "
+                               "which sophia_amd does not ship (it is the test oracle)")
+        _require_gpu(q)
+        if int(q.size(1)) == 1 and initial_state is not None:
+            return self._fla_fused_recurrent_kda()(
+                q=q, k=k, v=v, g=decay_logits, beta=beta_logits, A_log=self.A_log,
+                dt_bias=self.dt_bias, initial_state=initial_state, output_final_state=True,
+                use_qk_l2norm_in_kernel=True, use_gate_in_kernel=True,
+                use_beta_sigmoid_in_kernel=True, lower_bound=self.lower_bound)
+        output, final_state = self._fla_chunk_kda()(
+            q=q, k=k, v=v, g=decay_logits, beta=beta_logits, initial_state=initial_state,
+            output_final_state=bool(self.use_cache), use_qk_l2norm_in_kernel=True,
+            use_gate_in_kernel=True, use_beta_sigmoid_in_kernel=True, safe_gate=True,
+            lower_bound=self.lower_bound, A_log=self.A_log, dt_bias=self.dt_bias)
+        if final_state is None:
+            final_state = q.new_zeros(int(q.size(0)), self.num_heads, self.head_dim,
+                                      self.head_dim, dtype=torch.float32)
+        return output, final_state
+
+    # ------------------------------------------------------------- forward
+    def _short_convolution_flat(self, qkv: torch.Tensor, cu: torch.Tensor, slots, *,
+                                read: bool, write: bool, step: bool) -> torch.Tensor:
+        """All three ShortConvs (q|k|v channels) in one launch; conv_state[:, i]
+        is the history of projection i (attention.py:226-258)."""
+        state = self.conv_state.view(self.conv_state.size(0), 3 * self.inner_dim,
+                                     self.conv_kernel - 1) if self.conv_kernel > 1 else None
+        if step:
+            return ops.short_conv_step(qkv, self._conv_weight(), state, state_slots=slots,
+                                       read_history=read)
+        return ops.short_conv_fwd(qkv, self._conv_weight(), cu, conv_state=state,
+                                  state_slots=slots, read_history=read, write_history=write)
+
+    def _output(self, o: torch.Tensor, gate_logits: torch.Tensor, dtype) -> torch.Tensor:
+        """attention.py:411-420: o_proj(RMSNorm(o) * sigmoid(gate))."""
+        n = o.size(0)
+        gate = torch.sigmoid(gate_logits).view(n, self.num_heads, self.head_dim)
+        out = self.output_norm(o.to(dtype)) * gate
+        return self.o_proj(out.reshape(n, self.inner_dim))
+
+    def forward(self, x: torch.Tensor, *, start_pos: int = 0) -> torch.Tensor:
+        """attention.py:373-420."""
+        _require_gpu(x)
+        bsz, seqlen, _ = x.shape
+        if self.use_cache:
+            self.ensure_batch_capacity(int(bsz))
+        pad_mask = getattr(self, "_pad_mask", None) if int(start_pos) == 0 else None
+        if pad_mask is not None:
+            keep = pad_mask[:, :seqlen].to(device=x.device, dtype=x.dtype).unsqueeze(-1)
+            x = x * keep
+        n = bsz * seqlen
+        x2 = x.reshape(n, self.dim)
+        qkv, dd, beta_logits, gate_logits = self._project(x2)
+        cached = self.use_cache and int(start_pos) > 0
+        cu = torch.arange(0, (bsz + 1) * seqlen, seqlen, dtype=torch.int32, device=x.device)
+        qkv = self._short_convolution_flat(qkv, cu, None, read=cached, write=self.use_cache,
+                                           step=(seqlen == 1 and cached and self.use_cache))
+        i = self.inner_dim
+        shape4 = (bsz, seqlen, self.num_heads, self.head_dim)
+        q = qkv[:, :i].view(shape4) if qkv.is_contiguous() else qkv[:, :i].reshape(shape4)
+        k = qkv[:, i: 2 * i].reshape(shape4)
+        v = qkv[:, 2 * i:].reshape(shape4)
+        decay = self.decay_up(dd).view(shape4)
+        beta_logits = beta_logits.reshape(bsz, seqlen, self.num_heads)
+        if pad_mask is not None:
+            drop = ~pad_mask[:, :seqlen].to(device=x.device).bool()
+            decay = decay.masked_fill(drop[:, :, None, None], PAD_LOGIT)
+            beta_logits = beta_logits.masked_fill(drop[:, :, None], PAD_LOGIT)
+        initial_state = self.recurrent_state[:bsz] if cached else None
+        output, final_state = self._run_kda(q, k, v, decay, beta_logits, initial_state)
+        if self.use_cache and final_state.data_ptr() != self.recurrent_state.data_ptr():
+            with torch.no_grad():
+                self.recurrent_state[:bsz].copy_(final_state.detach().to(dtype=torch.float32))
+        out = self._output(output.reshape(n, self.num_heads, self.head_dim), gate_logits, x.dtype)
+        return out.view(bsz, seqlen, self.dim)
+
+    def forward_packed(self, x: torch.Tensor, cu_seqlens: torch.Tensor, *,
+                       state_slots: torch.Tensor | None = None, use_state: bool = True,
+                       max_seqlen: int | None = None) -> torch.Tensor:
+        """Packed ragged batch: x [total, dim] (or [1, total, dim]) holding the
+        sequences delimited by int32 ``cu_seqlens`` [N+1].  Sequence s reads
+        (when ``use_state``) and writes (when ``use_cache``) cache slot
+        ``state_slots[s]`` (default s) of ``recurrent_state`` / ``conv_state``;
+        zero a slot with ``reset_slots`` before a new sequence uses it.
+        ``max_seqlen == 1`` (decode only) selects the one-step kernels.
+        Returns [total, dim] (or [1, total, dim])."""
+        _require_gpu(x)
+        squeeze = x.dim() == 3
+        x2 = x.reshape(-1, self.dim)
+        n = int(x2.size(0))
+        cu = cu_seqlens.to(device=x.device, dtype=torch.int32).contiguous()
+        nseq = int(cu.numel()) - 1
+        slots = None if state_slots is None else state_slots.to(
+            device=x.device, dtype=torch.int32).contiguous()
+        if self.use_cache and slots is None:
+            self.ensure_batch_capacity(nseq)  # with explicit slots the caller sizes the caches
+        qkv, dd, beta_logits, gate_logits = self._project(x2)
+        read = bool(use_state) and self.use_cache
+        step = max_seqlen == 1 and n == nseq and read
+        qkv = self._short_convolution_flat(qkv, cu, slots, read=read, write=self.use_cache,
+                                           step=step)
+        i, h, d = self.inner_dim, self.num_heads, self.head_dim
+        q = qkv[:, :i].unflatten(1, (h, d))
+        k = qkv[:, i: 2 * i].unflatten(1, (h, d))
+        v = qkv[:, 2 * i:].unflatten(1, (h, d))
+        decay = self.decay_up(dd).view(n, h, d)
+        state = self.recurrent_state if self.use_cache else None
+        if step:
+            o = ops.kda_decode_step(q, k, v, decay, beta_logits, state, A_log=self.A_log,
+                                    dt_bias=self.dt_bias, lower_bound=self.lower_bound,
+                                    state_slots=slots, read_state=True)
+        else:
+            o = ops.kda_chunk_fwd(q, k, v, decay, beta_logits, cu, A_log=self.A_log,
+                                  dt_bias=self.dt_bias, lower_bound=self.lower_bound,
+                                  initial_state=state if read else None, final_state=state,
+                                  state_slots=slots)
+        out = self._output(o, gate_logits, x.dtype)
+        return out.view(1, n, self.dim) if squeeze else out
+
+
+def set_pad_mask(model: nn.Module, mask: torch.Tensor | None) -> None:
+    """attention.py:660-670: hang a [B, T] bool mask (True = real token) on
+    every KDA mixer, or clear it."""
+    for module in model.modules():
+        if isinstance(module, SophiaKDA):
+            module._pad_mask = mask
+
+
+__all__ = ["CausalDepthwiseConv1d", "PAD_LOGIT", "RMSNorm", "RuntimeLinear", "SophiaKDA",
+           "set_pad_mask"]

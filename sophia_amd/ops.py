@@ -1,0 +1,354 @@
+"""Torch-facing entry points of the HIP kernels.
+
+Each function checks devices, dtypes and shapes (raising ``RuntimeError`` the
+way the reference's custom ops do, ml/training/pretrain/engine/
+sm120_concurrent_ffn.py:49-59), allocates outputs and scratch from torch's
+caching allocator, and launches the C ABI of ``include/sophia_kda.h`` on the
+current stream.  Nothing here synchronises the device or reads device data on
+the host, so every call can be captured in a HIP graph.
+
+``chunk_kda`` and ``fused_recurrent_kda`` keep the signatures of the
+flash-linear-attention functions that the reference mixer calls
+(ml/runtime/model/attention.py:330-365) plus the varlen arguments of the
+FlashKDA seam (sm120_concurrent_ffn.py:375-423), so they drop into
+``SophiaKDA._fla_chunk_kda`` / ``_fla_fused_recurrent_kda``.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _native as nat
+
+HEAD_DIM = 128
+CHUNK_SIZE = 64
+
+
+def _gpu(t: torch.Tensor, name: str) -> None:
+    if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
+        raise RuntimeError(f"{name} must be a tensor on a ROCm GPU (sophia_amd has no CPU path)")
+
+
+def _rows(t: torch.Tensor, name: str, width: int) -> int:
+    """Row stride (elements) of a [N, width] view whose rows are dense."""
+    if t.dim() != 2 or t.size(1) != width:
+        raise RuntimeError(f"{name} must be [N, {width}], got {tuple(t.shape)}")
+    if t.size(1) > 1 and t.stride(1) != 1:
+        raise RuntimeError(f"{name} rows must be contiguous")
+    return int(t.stride(0)) if t.size(0) > 1 else width
+
+
+def _heads_rows(t: torch.Tensor, name: str, heads: int, dim: int) -> int:
+    """Row stride of a [N, H, D] view with dense [H, D] rows."""
+    if t.dim() != 3 or t.size(1) != heads or t.size(2) != dim:
+        raise RuntimeError(f"{name} must be [N, {heads}, {dim}], got {tuple(t.shape)}")
+    if (heads > 1 and t.stride(1) != dim) or t.stride(2) != 1:
+        raise RuntimeError(f"{name} must have dense [heads, dim] rows")
+    return int(t.stride(0)) if t.size(0) > 1 else heads * dim
+
+
+def _int32(t: torch.Tensor | None, name: str, device) -> torch.Tensor | None:
+    if t is None:
+        return None
+    if t.dtype != torch.int32 or t.device != device or not t.is_contiguous():
+        raise RuntimeError(f"{name} must be a contiguous int32 tensor on {device}")
+    return t
+
+
+def _workspace(nbytes: int, device) -> tuple[torch.Tensor, int, int]:
+    buf = torch.empty(nbytes + 256, dtype=torch.uint8, device=device)
+    addr = buf.data_ptr()
+    pad = (-addr) % 256
+    return buf, addr + pad, nbytes
+
+
+# ------------------------------------------------------------------ ShortConv
+def short_conv_fwd(x: torch.Tensor, weight: torch.Tensor, cu_seqlens: torch.Tensor, *,
+                   conv_state: torch.Tensor | None = None,
+                   state_slots: torch.Tensor | None = None, read_history: bool = False,
+                   write_history: bool = False, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Causal depthwise conv + SiLU over a packed batch (CausalDepthwiseConv1d.forward,
+    attention.py:32-60, applied per sequence of ``cu_seqlens``).
+
+    x: [total, C] (rows may be strided); weight: [C, K] (cast to x.dtype then
+    fp32, as the reference casts the weight to x's dtype); conv_state:
+    [slots, C, K-1] fp32, read when ``read_history`` and written when
+    ``write_history``.  Returns y [total, C] in x.dtype.
+    """
+    _gpu(x, "x")
+    channels = int(x.size(1))
+    xs = _rows(x, "x", channels)
+    kernel = int(weight.size(1))
+    if weight.dim() != 2 or int(weight.size(0)) != channels:
+        raise RuntimeError(f"weight must be [{channels}, K], got {tuple(weight.shape)}")
+    w = weight.detach().to(device=x.device, dtype=x.dtype).float().contiguous()
+    cu = _int32(cu_seqlens, "cu_seqlens", x.device)
+    n = int(cu.numel()) - 1
+    if conv_state is not None:
+        _gpu(conv_state, "conv_state")
+        if (conv_state.dtype != torch.float32 or not conv_state.is_contiguous()
+                or tuple(conv_state.shape[1:]) != (channels, kernel - 1)):
+            raise RuntimeError(f"conv_state must be contiguous fp32 [slots, {channels}, "
+                               f"{kernel - 1}], got {tuple(conv_state.shape)}")
+    slots = _int32(state_slots, "state_slots", x.device)
+    y = out if out is not None else torch.empty((x.size(0), channels), dtype=x.dtype,
+                                                device=x.device)
+    ys = _rows(y, "out", channels)
+    rc = nat.lib().sophia_short_conv_fwd(
+        nat.ptr(x), xs, nat.ptr(y), ys, nat.dtype_code(x.dtype), nat.ptr(w), nat.ptr(conv_state),
+        0 if conv_state is None else int(conv_state.size(0)),
+        nat.ptr(slots), nat.ptr(cu), n, int(x.size(0)), channels, kernel, int(bool(read_history)),
+        int(bool(write_history)), nat.stream_handle(x.device))
+    nat.check(rc, "sophia_short_conv_fwd")
+    return y
+
+
+def short_conv_step(x: torch.Tensor, weight: torch.Tensor, conv_state: torch.Tensor, *,
+                    state_slots: torch.Tensor | None = None, read_history: bool = True,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """One-token conv step for a batch of sequences (decode), history updated in place.
+    x: [B, C]; conv_state: [slots, C, K-1] fp32."""
+    _gpu(x, "x")
+    _gpu(conv_state, "conv_state")
+    channels = int(x.size(1))
+    xs = _rows(x, "x", channels)
+    kernel = int(weight.size(1))
+    if (conv_state.dtype != torch.float32 or not conv_state.is_contiguous()
+            or tuple(conv_state.shape[1:]) != (channels, kernel - 1)):
+        raise RuntimeError("conv_state must be contiguous fp32 [slots, C, K-1]")
+    w = weight.detach().to(device=x.device, dtype=x.dtype).float().contiguous()
+    slots = _int32(state_slots, "state_slots", x.device)
+    y = out if out is not None else torch.empty_like(x, memory_format=torch.contiguous_format)
+    ys = _rows(y, "out", channels)
+    rc = nat.lib().sophia_short_conv_step(
+        nat.ptr(x), xs, nat.ptr(y), ys, nat.dtype_code(x.dtype), nat.ptr(w), nat.ptr(conv_state),
+        int(conv_state.size(0)), nat.ptr(slots), int(x.size(0)), channels, kernel,
+        int(bool(read_history)),
+        nat.stream_handle(x.device))
+    nat.check(rc, "sophia_short_conv_step")
+    return y
+
+
+# ------------------------------------------------------------------ KDA core
+def _flags(use_qk_l2norm: bool, use_gate: bool, use_beta_sigmoid: bool) -> int:
+    return ((nat.QK_L2NORM if use_qk_l2norm else 0) | (nat.GATE_IN_KERNEL if use_gate else 0)
+            | (nat.BETA_SIGMOID if use_beta_sigmoid else 0))
+
+
+def _gate_params(use_gate, A_log, dt_bias, heads, device):
+    if not use_gate:
+        return None, None
+    if A_log is None or dt_bias is None:
+        raise RuntimeError("use_gate_in_kernel needs A_log and dt_bias")
+    a = A_log.detach().to(device=device, dtype=torch.float32).reshape(-1).contiguous()
+    b = dt_bias.detach().to(device=device, dtype=torch.float32).reshape(-1).contiguous()
+    if a.numel() != heads or b.numel() != heads * HEAD_DIM:
+        raise RuntimeError(f"A_log must have {heads} and dt_bias {heads * HEAD_DIM} elements")
+    return a, b
+
+
+def _state(t: torch.Tensor | None, name: str, heads: int, device) -> None:
+    if t is None:
+        return
+    _gpu(t, name)
+    if (t.dtype != torch.float32 or not t.is_contiguous() or t.dim() != 4
+            or tuple(t.shape[1:]) != (heads, HEAD_DIM, HEAD_DIM) or t.device != device):
+        raise RuntimeError(f"{name} must be contiguous fp32 [slots, {heads}, 128, 128]")
+
+
+def kda_chunk_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
+                  beta: torch.Tensor, cu_seqlens: torch.Tensor, *, A_log=None, dt_bias=None,
+                  scale: float | None = None, lower_bound: float = -5.0,
+                  use_qk_l2norm: bool = True, use_gate: bool = True,
+                  use_beta_sigmoid: bool = True, initial_state: torch.Tensor | None = None,
+                  final_state: torch.Tensor | None = None,
+                  state_slots: torch.Tensor | None = None,
+                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """Chunk-64 KDA prefill over a packed batch.
+
+    q, k, v, g: [total, H, 128] (rows may be strided views of a wider
+    buffer); beta: [total, H]; cu_seqlens: int32 [N+1] on the device.
+    initial_state / final_state: fp32 [slots, H, 128, 128] or None, indexed
+    by ``state_slots`` (default: sequence index); they may be the same tensor.
+    Returns o [total, H, 128] in q.dtype.
+    """
+    for t, name in ((q, "q"), (k, "k"), (v, "v"), (g, "g"), (beta, "beta")):
+        _gpu(t, name)
+    device = q.device
+    total, heads = int(q.size(0)), int(q.size(1))
+    qs = _heads_rows(q, "q", heads, HEAD_DIM)
+    if k.stride() != q.stride() or v.stride() != q.stride():
+        raise RuntimeError("q, k and v must share one row layout")
+    _heads_rows(k, "k", heads, HEAD_DIM)
+    _heads_rows(v, "v", heads, HEAD_DIM)
+    if not (q.dtype == k.dtype == v.dtype):
+        raise RuntimeError("q, k and v must share one dtype")
+    if int(k.size(0)) != total or int(v.size(0)) != total or int(g.size(0)) != total:
+        raise RuntimeError("q, k, v and g must have the same number of tokens")
+    gs = _heads_rows(g, "g", heads, HEAD_DIM)
+    bs = _rows(beta, "beta", heads)
+    cu = _int32(cu_seqlens, "cu_seqlens", device)
+    n = int(cu.numel()) - 1
+    if n < 1:
+        raise RuntimeError("cu_seqlens must hold at least one sequence")
+    _state(initial_state, "initial_state", heads, device)
+    _state(final_state, "final_state", heads, device)
+    n_slots = [int(t.size(0)) for t in (initial_state, final_state) if t is not None]
+    if len(n_slots) == 2 and n_slots[0] != n_slots[1]:
+        raise RuntimeError("initial_state and final_state must have the same number of slots")
+    n_slots = n_slots[0] if n_slots else 0
+    if state_slots is None and n_slots and n_slots < int(cu_seqlens.numel()) - 1:
+        raise RuntimeError("state tensors have fewer slots than sequences")
+    slots = _int32(state_slots, "state_slots", device)
+    a_log, dtb = _gate_params(use_gate, A_log, dt_bias, heads, device)
+    if scale is None:
+        scale = HEAD_DIM ** -0.5
+    o = out if out is not None else torch.empty((total, heads, HEAD_DIM), dtype=q.dtype,
+                                                device=device)
+    os_ = _heads_rows(o, "out", heads, HEAD_DIM)
+    lib = nat.lib()
+    need = int(lib.sophia_kda_chunk_workspace_size(total, n, heads, HEAD_DIM))
+    buf, ws_addr, ws_bytes = _workspace(need, device)
+    rc = lib.sophia_kda_chunk_fwd(
+        nat.ptr(q), nat.ptr(k), nat.ptr(v), qs, nat.dtype_code(q.dtype), nat.ptr(g), gs,
+        nat.dtype_code(g.dtype), nat.ptr(beta), bs, nat.dtype_code(beta.dtype), nat.ptr(a_log),
+        nat.ptr(dtb), float(scale), float(lower_bound),
+        _flags(use_qk_l2norm, use_gate, use_beta_sigmoid), nat.ptr(cu), n, total, heads, HEAD_DIM,
+        nat.ptr(initial_state), nat.ptr(final_state), n_slots, nat.ptr(slots), nat.ptr(o), os_,
+        ws_addr, ws_bytes, nat.stream_handle(device))
+    nat.check(rc, "sophia_kda_chunk_fwd")
+    del buf  # stream-ordered reuse by the caching allocator is safe
+    return o
+
+
+def kda_decode_step(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
+                    beta: torch.Tensor, state: torch.Tensor, *, A_log=None, dt_bias=None,
+                    scale: float | None = None, lower_bound: float = -5.0,
+                    use_qk_l2norm: bool = True, use_gate: bool = True,
+                    use_beta_sigmoid: bool = True, state_slots: torch.Tensor | None = None,
+                    read_state: bool = True, out: torch.Tensor | None = None) -> torch.Tensor:
+    """One recurrent step for B sequences; ``state`` is updated in place.
+    q, k, v, g: [B, H, 128]; beta: [B, H]; state: fp32 [slots, H, 128, 128]."""
+    for t, name in ((q, "q"), (k, "k"), (v, "v"), (g, "g"), (beta, "beta")):
+        _gpu(t, name)
+    device = q.device
+    batch, heads = int(q.size(0)), int(q.size(1))
+    qs = _heads_rows(q, "q", heads, HEAD_DIM)
+    if k.stride() != q.stride() or v.stride() != q.stride() or not (q.dtype == k.dtype == v.dtype):
+        raise RuntimeError("q, k and v must share one row layout and dtype")
+    _heads_rows(k, "k", heads, HEAD_DIM)
+    _heads_rows(v, "v", heads, HEAD_DIM)
+    gs = _heads_rows(g, "g", heads, HEAD_DIM)
+    bs = _rows(beta, "beta", heads)
+    _state(state, "state", heads, device)
+    slots = _int32(state_slots, "state_slots", device)
+    if slots is None and int(state.size(0)) < batch:
+        raise RuntimeError("state has fewer slots than the batch")
+    a_log, dtb = _gate_params(use_gate, A_log, dt_bias, heads, device)
+    if scale is None:
+        scale = HEAD_DIM ** -0.5
+    o = out if out is not None else torch.empty((batch, heads, HEAD_DIM), dtype=q.dtype,
+                                                device=device)
+    os_ = _heads_rows(o, "out", heads, HEAD_DIM)
+    rc = nat.lib().sophia_kda_decode_step(
+        nat.ptr(q), nat.ptr(k), nat.ptr(v), qs, nat.dtype_code(q.dtype), nat.ptr(g), gs,
+        nat.dtype_code(g.dtype), nat.ptr(beta), bs, nat.dtype_code(beta.dtype), nat.ptr(a_log),
+        nat.ptr(dtb), float(scale), float(lower_bound),
+        _flags(use_qk_l2norm, use_gate, use_beta_sigmoid), nat.ptr(state), int(state.size(0)),
+        nat.ptr(slots),
+        int(bool(read_state)), batch, heads, HEAD_DIM, nat.ptr(o), os_,
+        nat.stream_handle(device))
+    nat.check(rc, "sophia_kda_decode_step")
+    return o
+
+
+# -------------------------------------------- flash-linear-attention signatures
+def _cu_for_batch(bsz: int, seqlen: int, device) -> torch.Tensor:
+    return torch.arange(0, (bsz + 1) * seqlen, seqlen, dtype=torch.int32, device=device)
+
+
+def chunk_kda(q, k, v, g, beta, *, scale=None, initial_state=None, output_final_state=False,
+              use_qk_l2norm_in_kernel=False, use_gate_in_kernel=False,
+              use_beta_sigmoid_in_kernel=False, safe_gate=False, lower_bound=None, A_log=None,
+              dt_bias=None, cu_seqlens=None, cu_seqlens_cpu=None, chunk_size=64,
+              allow_neg_eigval=False, state_v_first=False, **kwargs):
+    """fla.ops.kda.chunk_kda as called at attention.py:349-365 (and FlashKDA's
+    varlen form, sm120_concurrent_ffn.py:375-423).
+
+    q, k, g: [B, T, H, 128]; v: [B, T, H, 128]; beta: [B, T, H].  With
+    ``cu_seqlens`` B must be 1 and states are per sequence.  Returns
+    (o [B, T, H, 128] in q.dtype, final_state fp32 [N, H, 128, 128] or None).
+    The log-decay must stay in [-5, 0]: the gate computed in the kernel always
+    does; a precomputed g needs ``safe_gate`` with ``lower_bound >= -5``.
+    """
+    if kwargs:
+        raise TypeError(f"unexpected arguments: {sorted(kwargs)}")
+    if int(chunk_size) != CHUNK_SIZE:
+        raise RuntimeError("sophia_amd chunk_kda supports chunk_size=64 only")
+    if allow_neg_eigval or state_v_first:
+        raise RuntimeError("allow_neg_eigval / state_v_first are not supported")
+    lb = -5.0 if lower_bound is None else float(lower_bound)
+    if not use_gate_in_kernel and not safe_gate:
+        raise RuntimeError("a precomputed gate needs safe_gate=True (log-decay in [lower_bound, 0])")
+    if q.dim() != 4:
+        raise RuntimeError(f"q must be [B, T, H, K], got {tuple(q.shape)}")
+    bsz, seqlen, heads, _ = q.shape
+    if cu_seqlens is not None:
+        if bsz != 1:
+            raise RuntimeError("varlen chunk_kda needs a packed batch of size 1")
+        cu = cu_seqlens.to(device=q.device, dtype=torch.int32).contiguous()
+    else:
+        cu = _cu_for_batch(bsz, seqlen, q.device)
+    n = int(cu.numel()) - 1
+    total = bsz * seqlen
+
+    def flat(t, width):
+        return t.reshape(total, heads, width) if t.dim() == 4 else t.reshape(total, heads)
+
+    h0 = None
+    if initial_state is not None:
+        h0 = initial_state if (initial_state.dtype == torch.float32
+                               and initial_state.is_contiguous()) else initial_state.float().contiguous()
+    ht = torch.empty((n, heads, HEAD_DIM, HEAD_DIM), dtype=torch.float32, device=q.device) \
+        if output_final_state else None
+    o = kda_chunk_fwd(flat(q, HEAD_DIM), flat(k, HEAD_DIM), flat(v, HEAD_DIM), flat(g, HEAD_DIM),
+                      beta.reshape(total, heads), cu,
+                      A_log=A_log, dt_bias=dt_bias, scale=scale, lower_bound=lb,
+                      use_qk_l2norm=use_qk_l2norm_in_kernel, use_gate=use_gate_in_kernel,
+                      use_beta_sigmoid=use_beta_sigmoid_in_kernel, initial_state=h0,
+                      final_state=ht)
+    return o.view(bsz, seqlen, heads, HEAD_DIM), ht
+
+
+def fused_recurrent_kda(q, k, v, g, beta, *, A_log=None, dt_bias=None, scale=None,
+                        initial_state=None, output_final_state=True,
+                        use_qk_l2norm_in_kernel=False, use_gate_in_kernel=False,
+                        use_beta_sigmoid_in_kernel=False, lower_bound=None, inplace_state=False,
+                        **kwargs):
+    """fla.ops.kda.fused_recurrent_kda for one token (attention.py:330-348).
+
+    q, k, v, g: [B, 1, H, 128]; beta: [B, 1, H]; initial_state fp32
+    [B, H, 128, 128] or None.  With ``inplace_state`` the step updates
+    ``initial_state`` itself and returns it as the final state (the mixer
+    copies the final state back into that same buffer, attention.py:406-410).
+    """
+    if kwargs:
+        raise TypeError(f"unexpected arguments: {sorted(kwargs)}")
+    if q.dim() != 4 or int(q.size(1)) != 1:
+        raise RuntimeError("sophia_amd fused_recurrent_kda advances one token: q must be [B, 1, H, K]")
+    bsz, _, heads, _ = q.shape
+    lb = -5.0 if lower_bound is None else float(lower_bound)
+    if initial_state is None:
+        state = torch.empty((bsz, heads, HEAD_DIM, HEAD_DIM), dtype=torch.float32, device=q.device)
+        read = False
+    elif inplace_state:
+        state, read = initial_state, True
+    else:
+        state, read = initial_state.float().clone(memory_format=torch.contiguous_format), True
+    o = kda_decode_step(q.reshape(bsz, heads, HEAD_DIM), k.reshape(bsz, heads, HEAD_DIM),
+                        v.reshape(bsz, heads, HEAD_DIM), g.reshape(bsz, heads, HEAD_DIM),
+                        beta.reshape(bsz, heads), state, A_log=A_log, dt_bias=dt_bias,
+                        scale=scale, lower_bound=lb, use_qk_l2norm=use_qk_l2norm_in_kernel,
+                        use_gate=use_gate_in_kernel, use_beta_sigmoid=use_beta_sigmoid_in_kernel,
+                        read_state=read)
+    return o.view(bsz, 1, heads, HEAD_DIM), (state if output_final_state else None)
