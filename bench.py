@@ -1,0 +1,236 @@
+"""Benchmark of the KDA mixer hot path on one MI355X.
+
+Headline workload (the value of the JSON line): chunk-64 KDA prefill over a
+packed ragged batch -- 8 sequences with lengths uniform in [256, 4096]
+(seeded), 16 heads x 128, bf16 q/k/v/o, fp32 log-decay g in [-5, 0], fp32
+beta = sigmoid(N(0,1)), fp32 state, zero initial state.  One step = one
+``sophia_kda_chunk_fwd`` call (prep + intra-chunk + scan kernels) over the
+whole batch with inputs resident in HBM.
+
+Also reported: the batch-256 decode step (fp32 state N(0, 0.02), one bf16
+token per sequence) in microseconds and HBM GB/s, the ShortConv prefill over
+the same packed batch, and the CPU baseline (the C restatement of the
+reference's per-token recurrence, timed on this host's cores).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+if HERE not in sys.path:
+    sys.path.insert(0, HERE)
+
+HEADS, DIM = 16, 128
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+# Algorithmic traffic of the prefill core per token: q, k, v, o bf16 + g fp32
+# + beta fp32 over 16 heads.
+PREFILL_BYTES_PER_TOKEN = HEADS * (4 * DIM * 2 + DIM * 4 + 4)          # 24,640
+# Causal chunk-form flops per token at C = 64: H * (5 C d + 6 d^2).
+PREFILL_FLOPS_PER_TOKEN = HEADS * (5 * 64 * DIM + 6 * DIM * DIM)      # 2,228,224
+METRIC = "KDA prefill tokens/s + % MFMA peak; decode-step µs and HBM GB/s at B=256"
+
+
+def prefill_lengths(seed: int = 0, n: int = 8, lo: int = 256, hi: int = 4096) -> list[int]:
+    rng = np.random.default_rng(seed)
+    return [int(x) for x in rng.integers(lo, hi + 1, size=n)]
+
+
+def make_prefill_inputs(torch, dev, lengths, seed=1):
+    gen = torch.Generator().manual_seed(seed)
+    total = int(sum(lengths))
+    shape = (total, HEADS, DIM)
+    q = torch.nn.functional.normalize(torch.randn(shape, generator=gen), dim=-1).to(torch.bfloat16)
+    k = torch.nn.functional.normalize(torch.randn(shape, generator=gen), dim=-1).to(torch.bfloat16)
+    v = torch.randn(shape, generator=gen).to(torch.bfloat16)
+    g = torch.rand(shape, generator=gen) * -5.0
+    beta = torch.sigmoid(torch.randn((total, HEADS), generator=gen))
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lengths)]), dtype=torch.int32)
+    return {name: t.to(dev) for name, t in
+            dict(q=q, k=k, v=v, g=g, beta=beta, cu=cu).items()}
+
+
+def time_events(torch, fn, steps: int, warmup: int, stream) -> tuple[float, list[float]]:
+    """Average per-call duration (ms) from HIP events recorded on `stream`
+    around each call, plus the wall time of the whole timed region."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record(stream)
+        fn()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3
+    per = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    return wall, per
+
+
+def cpu_baseline(inputs, lengths, budget_s: float = 20.0):
+    """The oracle's C restatement of the reference's per-token recurrence on
+    this host's cores, over a bounded prefix of the same workload."""
+    from oracle import c_oracle
+    cores = len(os.sched_getaffinity(0))
+    q = inputs["q"].float().cpu().numpy()
+    k = inputs["k"].float().cpu().numpy()
+    v = inputs["v"].float().cpu().numpy()
+    g = inputs["g"].cpu().numpy()
+    beta = inputs["beta"].cpu().numpy()
+    # Sample: every sequence truncated to its first `m` tokens (all 16 heads),
+    # m grown until the run costs a few seconds.
+    m = 64
+    while True:
+        sub = [min(n, m) for n in lengths]
+        idx = np.concatenate([np.arange(a, a + s) for a, s in
+                              zip(np.concatenate([[0], np.cumsum(lengths)[:-1]]), sub)])
+        cu = np.concatenate([[0], np.cumsum(sub)]).astype(np.int32)
+        t0 = time.perf_counter()
+        c_oracle.kda_varlen(q[idx], k[idx], v[idx], g[idx], beta[idx], cu, use_gate=False,
+                            use_beta_sigmoid=False, nthreads=cores)
+        dt = time.perf_counter() - t0
+        if dt > 2.0 or m >= max(lengths) or dt * (2 ** 3) > budget_s:
+            break
+        m *= 2
+    tokens = int(cu[-1])
+    return {"value": tokens / dt, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"C per-token fp32 recurrence (oracle/kda_ref.c, OpenMP over seq x head) on "
+                      f"the first {m} tokens of each of the 8 sequences ({tokens} tokens, 16 heads), "
+                      f"{dt:.2f} s; os.cpu_count()={os.cpu_count()}"}
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", choices=["all", "prefill", "decode"], default="all")
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
+              f"--gpus {args.gpus}); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+    from sophia_amd import ops, _native
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    _native.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream(dev)
+
+    lengths = prefill_lengths()
+    total = int(sum(lengths))
+    inp = make_prefill_inputs(torch, dev, lengths)
+    final = torch.zeros((len(lengths), HEADS, DIM, DIM), dtype=torch.float32, device=dev)
+    out = torch.empty((total, HEADS, DIM), dtype=torch.bfloat16, device=dev)
+
+    def prefill():
+        ops.kda_chunk_fwd(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], inp["cu"],
+                          use_qk_l2norm=True, use_gate=False, use_beta_sigmoid=False,
+                          final_state=final, out=out)
+
+    result = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+              "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+              "data": "synthetic"}
+
+    wall, per = time_events(torch, prefill, args.steps, args.warmup, stream)
+    avg_ms = float(np.mean(per))
+    tokens_per_s = total / (avg_ms / 1e3)
+    achieved_gbs = total * PREFILL_BYTES_PER_TOKEN / (avg_ms / 1e3) / 1e9
+    tflops = total * PREFILL_FLOPS_PER_TOKEN / (avg_ms / 1e3) / 1e12
+    ai = PREFILL_FLOPS_PER_TOKEN / PREFILL_BYTES_PER_TOKEN
+    attainable = min(BF16_PEAK_TFLOPS, HBM_PEAK_GBS * ai / 1e3)
+    result.update({
+        "value": round(tokens_per_s, 1), "unit": "tokens/s",
+        "ms_per_step": round(wall / args.steps, 4),
+        "config": {"workload": "KDA varlen chunk prefill (chunk 64): 8 sequences, lengths "
+                               "U[256,4096] seed 0, 16 heads x 128, bf16 q/k/v/o, fp32 g in "
+                               "[-5,0] / beta / state, zero initial state",
+                   "lengths": lengths, "total_tokens": total, "heads": HEADS, "head_dim": DIM,
+                   "kernel_ms": round(avg_ms, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None,
+                     "kernel": "kda_chunk_prep + kda_chunk_intra + kda_chunk_scan (one call)",
+                     "algorithmic_bytes_per_launch": total * PREFILL_BYTES_PER_TOKEN},
+        "mfma": {"achieved_tflops": round(tflops, 2), "peak_tflops": BF16_PEAK_TFLOPS,
+                 "frac_of_peak": round(tflops / BF16_PEAK_TFLOPS, 4),
+                 "attainable_tflops": round(attainable, 1),
+                 "frac_of_attainable": round(tflops / attainable, 4),
+                 "flops_per_token": PREFILL_FLOPS_PER_TOKEN},
+    })
+    if not torch.isfinite(out.float()).all():
+        print("non-finite prefill output", file=sys.stderr)
+        return 1
+
+    # ShortConv over the same packed batch (3 x 2048 channels, bf16).
+    gen = torch.Generator().manual_seed(2)
+    xconv = torch.randn((total, 3 * HEADS * DIM), generator=gen).to(torch.bfloat16).to(dev)
+    wconv = (torch.randn((3 * HEADS * DIM, 4), generator=gen) * 0.02).to(dev)
+    conv_state = torch.zeros((len(lengths), 3 * HEADS * DIM, 3), device=dev)
+    yconv = torch.empty_like(xconv)
+
+    def conv():
+        ops.short_conv_fwd(xconv, wconv, inp["cu"], conv_state=conv_state, read_history=False,
+                           write_history=True, out=yconv)
+
+    _, cper = time_events(torch, conv, args.steps, args.warmup, stream)
+    cms = float(np.mean(cper))
+    cbytes = total * 3 * HEADS * DIM * 2 * 2
+    result["short_conv"] = {"us": round(cms * 1e3, 2), "GBps": round(cbytes / (cms / 1e3) / 1e9, 1),
+                            "algorithmic_bytes": cbytes}
+    del xconv, yconv, conv_state
+
+    # Decode step at B = 256.
+    batch = 256
+    gen = torch.Generator().manual_seed(3)
+    shape = (batch, HEADS, DIM)
+    dq = torch.nn.functional.normalize(torch.randn(shape, generator=gen), dim=-1).to(torch.bfloat16).to(dev)
+    dk = torch.nn.functional.normalize(torch.randn(shape, generator=gen), dim=-1).to(torch.bfloat16).to(dev)
+    dv = torch.randn(shape, generator=gen).to(torch.bfloat16).to(dev)
+    dg = (torch.rand(shape, generator=gen) * -5.0).to(dev)
+    db = torch.sigmoid(torch.randn((batch, HEADS), generator=gen)).to(dev)
+    dstate = (torch.randn((batch, HEADS, DIM, DIM), generator=gen) * 0.02).to(dev)
+    dout = torch.empty(shape, dtype=torch.bfloat16, device=dev)
+
+    def decode():
+        ops.kda_decode_step(dq, dk, dv, dg, db, dstate, use_gate=False, use_beta_sigmoid=False,
+                            out=dout)
+
+    dsteps = max(args.steps * 5, 50)
+    _, dper = time_events(torch, decode, dsteps, args.warmup * 2, stream)
+    dms = float(np.mean(dper))
+    dbytes = 2 * batch * HEADS * DIM * DIM * 4 + batch * HEADS * (3 * DIM * 2 + DIM * 4 + 4 + DIM * 2)
+    dgbs = dbytes / (dms / 1e3) / 1e9
+    result["decode"] = {"batch": batch, "us_per_step": round(dms * 1e3, 2),
+                        "GBps": round(dgbs, 1), "frac_of_hbm_peak": round(dgbs / HBM_PEAK_GBS, 4),
+                        "algorithmic_bytes": dbytes, "steps": dsteps,
+                        "kernel": "kda_decode_kernel"}
+    del dstate
+
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(inp, lengths)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

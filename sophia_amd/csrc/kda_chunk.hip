@@ -124,22 +124,37 @@ __global__ __launch_bounds__(256) void kda_chunk_prep_kernel(const int32_t *__re
 }
 
 // ---- intra-chunk kernel ----------------------------------------------------
-// LDS layout (bytes).  sKtT / sVT hold beta K e^G and beta V transposed
-// ([channel][row]) with the 16-byte row segments XOR-swizzled by channel.
+// LDS regions (bytes).  Lifetimes (steps below) let regions A and B be reused.
+//  E: e^{sub-block totals}          float [128][4]           steps 3-8
+//  A: key-side rows KD (6 copies)   bf16  [96][136]           steps 4-5
+//     -> solve scratch Y            float [3][16][16]         step 6
+//     -> beta K e^G, transposed     bf16  [128][64] swizzled  steps 7-8
+//  B: beta V, transposed            bf16  [128][64] swizzled  steps 1-8
+//     -> -W rows                    bf16  [64][136]           steps 9-10
+//  C: Kbar, transposed              bf16  [128][64] swizzled  steps 4-4b
+//     -> A_kk -> T = (I + A_kk)^-1  float [64][68]            steps 5-8
+//  D: A_qk                          bf16  [64][72]            steps 5-10
 constexpr int kLdT = 68;    // fp32 row stride of T
-constexpr int kLdKD = 136;  // bf16 row stride of K-side rows / -W
+constexpr int kLdKD = 136;  // bf16 row stride of key-side rows / -W
 constexpr int kLdQK = 72;   // bf16 row stride of A_qk
-constexpr size_t kSmTot = 0;                               // float [128][4]: e^{sub-block totals}
-constexpr size_t kSmKD = kSmTot + 128 * 4 * 4;             // bf16 [64][136]  (later: -W, solve scratch)
-constexpr size_t kSmT = kSmKD + 64 * kLdKD * 2;            // float [64][68]
-constexpr size_t kSmQK = kSmT + 64 * kLdT * 4;             // bf16 [64][72]
-constexpr size_t kSmKt = kSmQK + 64 * kLdQK * 2;           // bf16 [128][64] swizzled (later: Kbar^T)
-constexpr size_t kSmV = kSmKt + 128 * 64 * 2;              // bf16 [128][64] swizzled
-constexpr size_t kSmIntra = kSmV + 128 * 64 * 2;           // 78848
+constexpr size_t kSmE = 0;
+constexpr size_t kSmA = kSmE + 128 * 4 * 4;
+constexpr size_t kSmB = kSmA + 96 * kLdKD * 2;
+constexpr size_t kSmC = kSmB + 64 * kLdKD * 2;
+constexpr size_t kSmD = kSmC + 64 * kLdT * 4;
+constexpr size_t kSmIntra = kSmD + 64 * kLdQK * 2;           // 73216
+static_assert(128 * 64 * 2 <= 96 * kLdKD * 2, "region A holds a swizzled [128][64] bf16 tile");
+static_assert(128 * 64 * 2 <= 64 * kLdKD * 2, "region B holds a swizzled [128][64] bf16 tile");
+static_assert(3 * 256 * 4 <= 96 * kLdKD * 2, "region A holds the solve scratch");
+static_assert(128 * 64 * 2 <= 64 * kLdT * 4, "region C holds a swizzled [128][64] bf16 tile");
 
 __device__ __forceinline__ int swz(int ch, int row) {
   return ch * 64 + ((((row >> 3) ^ (ch & 7))) << 3) + (row & 7);
 }
+
+// Row block of region A holding key block ib scaled for query block ib+1+v
+// (v = 0: KD itself, v = 1: KD E_{ib+1}, v = 2: KD E_{ib+1} E_{ib+2}).
+__device__ __forceinline__ int kd_slot(int ib, int v) { return v == 0 ? ib : (v == 1 ? 3 + ib : 5); }
 
 struct IntraArgs {
   const void *q, *k, *v;
@@ -163,17 +178,26 @@ struct IntraArgs {
   uint8_t *records;
 };
 
+__device__ __forceinline__ float fast_sigmoid(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __expf(-x));
+}
+
+__device__ __forceinline__ u2 pack4_bf16(f4 v) {
+  return u2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+}
+
 template <int QKV_DT, int G_DT>
 __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  float *s_E = reinterpret_cast<float *>(smem + kSmTot);
-  uint16_t *sKD = reinterpret_cast<uint16_t *>(smem + kSmKD);
-  float *sT = reinterpret_cast<float *>(smem + kSmT);
-  uint16_t *sQK = reinterpret_cast<uint16_t *>(smem + kSmQK);
-  uint16_t *sKt = reinterpret_cast<uint16_t *>(smem + kSmKt);
-  uint16_t *sV = reinterpret_cast<uint16_t *>(smem + kSmV);
-  float *sR = reinterpret_cast<float *>(smem + kSmKD);      // solve scratch [16][48]
-  uint16_t *sW = sKD;                                        // -W rows, after the solve
+  float *s_E = reinterpret_cast<float *>(smem + kSmE);
+  uint16_t *sKD = reinterpret_cast<uint16_t *>(smem + kSmA);
+  float *sY = reinterpret_cast<float *>(smem + kSmA);
+  uint16_t *sKt = reinterpret_cast<uint16_t *>(smem + kSmA);
+  uint16_t *sV = reinterpret_cast<uint16_t *>(smem + kSmB);
+  uint16_t *sW = reinterpret_cast<uint16_t *>(smem + kSmB);
+  uint16_t *sKb = reinterpret_cast<uint16_t *>(smem + kSmC);
+  float *sT = reinterpret_cast<float *>(smem + kSmC);
+  uint16_t *sQK = reinterpret_cast<uint16_t *>(smem + kSmD);
 
   const int c = blockIdx.x;
   const int h = blockIdx.y;
@@ -193,14 +217,15 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
   const int row = 16 * w + lr;   // chunk row of this lane
   const bool valid = row < len;
   const int64_t tok = t0 + row;
+  uint8_t *rec = p.records + (static_cast<size_t>(c) * p.num_heads + h) * kRecBytes;
 
-  // ---- 1. load q, k, g (32 channels per lane, 16x16x32 operand order), beta;
-  //         beta V goes straight to LDS (transposed), it needs no decay.
+  // ---- 1. load q, k, g (32 channels per lane, 16x16x32 operand order), v, beta.
+  // Slot (ks, e) of a lane holds channel perm_k(ks, gq, e).
   float qv[32], kv[32], gv[32];
   float bt = 0.f;
   if (valid) {
     bt = load_elem(p.beta, tok * p.beta_stride + h, p.beta_dtype);
-    if (p.flags & SOPHIA_KDA_BETA_SIGMOID) bt = sigmoid_f(bt);
+    if (p.flags & SOPHIA_KDA_BETA_SIGMOID) bt = fast_sigmoid(bt);
   }
   {
     const int64_t qrow = tok * p.qkv_stride + static_cast<int64_t>(h) * kD;
@@ -223,12 +248,12 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
           qv[e] = a[i];
           kv[e] = b[i];
           gv[e] = d[i];
-          sV[swz(ch + i, row)] = f32_to_bf16_bits(bt * cc[i]);
+          sV[swz(ch + i, row)] = f32_to_bf16_bits(bt * cc[i]);   // beta V, transposed
         }
       }
   }
 
-  // ---- 2. l2 norms (row spread over the 4 lane groups), gate
+  // ---- 2. l2 norms (a row is spread over the 4 lane groups), gate
   {
     float sq = 0.f, sk = 0.f;
 #pragma unroll
@@ -252,18 +277,24 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
     }
     if (p.flags & SOPHIA_KDA_GATE_IN_KERNEL) {
       const float hs = __expf(p.A_log[h]);
+      const float *bias = p.dt_bias + h * kD;
 #pragma unroll
-      for (int e = 0; e < 32; ++e) {
-        const int ch = perm_k(e >> 3, gq, e & 7);
-        gv[e] = valid ? kda_log_decay(gv[e], hs, p.dt_bias[h * kD + ch], p.lb) : 0.f;
-      }
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const f4 bv = *reinterpret_cast<const f4 *>(bias + 32 * ks + 16 * hf + 4 * gq);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int e = 8 * ks + 4 * hf + i;
+            gv[e] = valid ? p.lb * fast_sigmoid(hs * (gv[e] + bv[i])) : 0.f;
+          }
+        }
     }
   }
 
-  // ---- 3. within-sub-block cumulative log-decay, sub-block totals
+  // ---- 3. within-sub-block cumulative log-decay; E[ch][i] = e^{tot_i}
 #pragma unroll
   for (int e = 0; e < 32; ++e) gv[e] = row_scan16(gv[e]);
-  // s_E[ch][i] = e^{tot_i}: decay over sub-block i (in [e^-80, 1]).
   if (lr == 15) {
 #pragma unroll
     for (int e = 0; e < 32; ++e) s_E[perm_k(e >> 3, gq, e & 7) * 4 + w] = __expf(gv[e]);
@@ -274,92 +305,100 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
   // Per channel, with Gloc the within-sub-block cumulative log-decay and
   // E_i = e^{tot_i}: a = e^{Gloc} (<= 1), b = e^{-Gloc} (<= e^80),
   // d = b E_w (<= 1), eref = e^{ref_w} = prod_{i<w} E_i,
-  // etail = e^{G_C - ref_{w+1}} = prod_{i>w} E_i.
-  bf8 QSf[4], KSf[4];           // query side, reused for the key block w-1
-  u4 kbar_bits[4];              // K e^{G_C - G}, bf16, operand order
+  // etail = e^{G_C - ref_{w+1}} = prod_{i>w} E_i.  All products are of
+  // factors <= 1, so they can only underflow where the true value is < 2^-126.
+  bf8 QSf[4], KSf[4];           // query side (A operands), all key blocks
+  u4 kt_bits[4];                // beta K e^G, bf16, operand order
   f4 aqk_d = {0.f, 0.f, 0.f, 0.f}, akk_d = aqk_d;
-  uint8_t *rec = p.records + (static_cast<size_t>(c) * p.num_heads + h) * kRecBytes;
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
-    float qa[8], ka[8], kb[8], kd[8], kbar[8], qe[8];
+    float qa[8], ka[8], kb[8], kd[8], kd1[8], kd2[8], kbar[8], qe[8], kt[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int e = 8 * ks + i;
-      const int ch = perm_k(ks, gq, i);
-      const f4 E = *reinterpret_cast<const f4 *>(&s_E[ch * 4]);
+      const f4 E = *reinterpret_cast<const f4 *>(&s_E[perm_k(ks, gq, i) * 4]);
       const float a = __expf(gv[e]);
       const float b = __expf(-gv[e]);
       const float eref = (w > 0 ? E[0] : 1.f) * (w > 1 ? E[1] : 1.f) * (w > 2 ? E[2] : 1.f);
       const float etl = (w < 1 ? E[1] : 1.f) * (w < 2 ? E[2] : 1.f) * (w < 3 ? E[3] : 1.f);
       const float ew = w == 0 ? E[0] : (w == 1 ? E[1] : (w == 2 ? E[2] : E[3]));
+      const float e1 = w == 0 ? E[1] : E[2];      // E_{w+1} (waves 0, 1)
       qa[i] = qv[e] * a;
       ka[i] = kv[e] * a;
       kb[i] = kv[e] * b;
       kd[i] = kb[i] * ew;
+      kd1[i] = kd[i] * e1;                        // for query block w+2
+      kd2[i] = kd1[i] * E[2];                     // for query block w+3 (wave 0)
       kbar[i] = kd[i] * etl;
-      qe[i] = qa[i] * eref;                                      // Q e^G
-      sKt[swz(ch, row)] = f32_to_bf16_bits(bt * ka[i] * eref);   // beta K e^G
+      qe[i] = qa[i] * eref;                       // Q e^G
+      kt[i] = bt * ka[i] * eref;                  // beta K e^G
     }
     QSf[ks] = pack8(qa);
     KSf[ks] = pack8(ka);
     const bf8 kbf = pack8(kb);
     aqk_d = mfma32(QSf[ks], kbf, aqk_d);
     akk_d = mfma32(KSf[ks], kbf, akk_d);
-    kbar_bits[ks] = bf8_to_bits(pack8(kbar));
+    kt_bits[ks] = bf8_to_bits(pack8(kt));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sKb[swz(perm_k(ks, gq, i), row)] = f32_to_bf16_bits(kbar[i]);
     // Q e^G goes straight to the workspace in A-operand order (mb = w).
     *reinterpret_cast<u4 *>(rec + kOffQ + ((w * 4 + ks) * 64 + l) * 16) = bf8_to_bits(pack8(qe));
-    // K-side rows for the off-diagonal blocks, row-major bf16.
+    // Key-side rows of this block for the later query blocks, row-major bf16.
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
-      u2 wv;
-      wv.x = pack_bf16x2(kd[4 * hf], kd[4 * hf + 1]);
-      wv.y = pack_bf16x2(kd[4 * hf + 2], kd[4 * hf + 3]);
-      *reinterpret_cast<u2 *>(&sKD[row * kLdKD + 32 * ks + 16 * hf + 4 * gq]) = wv;
+      const int col = 32 * ks + 16 * hf + 4 * gq;
+      const int i0 = 4 * hf;
+      if (w < 3)
+        *reinterpret_cast<u2 *>(&sKD[(kd_slot(w, 0) * 16 + lr) * kLdKD + col]) =
+            u2{pack_bf16x2(kd[i0], kd[i0 + 1]), pack_bf16x2(kd[i0 + 2], kd[i0 + 3])};
+      if (w < 2)
+        *reinterpret_cast<u2 *>(&sKD[(kd_slot(w, 1) * 16 + lr) * kLdKD + col]) =
+            u2{pack_bf16x2(kd1[i0], kd1[i0 + 1]), pack_bf16x2(kd1[i0 + 2], kd1[i0 + 3])};
+      if (w < 1)
+        *reinterpret_cast<u2 *>(&sKD[(kd_slot(w, 2) * 16 + lr) * kLdKD + col]) =
+            u2{pack_bf16x2(kd2[i0], kd2[i0 + 1]), pack_bf16x2(kd2[i0 + 2], kd2[i0 + 3])};
     }
-    __builtin_amdgcn_sched_barrier(0);  // keep the next K-step's LDS reads from being hoisted
   }
   __syncthreads();
 
-  // ---- 5. off-diagonal blocks of A_qk / A_kk for query sub-block w
-  // Key block ib < w: A_*[r, j] = sum_c (q,k)_r e^{Gloc_r} f_c KD_j with
-  // f = e^{ref_w - ref_{ib+1}} = prod_{ib<i<w} E_i (<= 1, 1 for ib = w-1).
+  // ---- 4b. Kbar^T fragments (m = channels 16mb + lr for mb = 2w, 2w+1,
+  //          k = chunk rows perm_k(ks, gq, .)) to the workspace; region C is
+  //          then free for A_kk.
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi) {
+    const int mb = 2 * w + mi;
+    const int ch = 16 * mb + lr;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int r0 = 32 * ks + 4 * gq;
+      const u2 lo = *reinterpret_cast<const u2 *>(&sKb[swz(ch, r0)]);
+      const u2 hi = *reinterpret_cast<const u2 *>(&sKb[swz(ch, r0 + 16)]);
+      *reinterpret_cast<u4 *>(rec + kOffKt + ((mb * 2 + ks) * 64 + l) * 16) = u4{lo.x, lo.y, hi.x, hi.y};
+    }
+  }
+  __syncthreads();
+
+  // ---- 5. off-diagonal blocks: key block ib < w uses copy v = w-1-ib of
+  // its key-side rows (already scaled by prod_{ib<i<w} E_i).
   {
     float brow[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) brow[e] = __shfl(bt, 4 * gq + e, 64);
-#pragma unroll 1
+#pragma unroll
     for (int ib = 0; ib < 4; ++ib) {
-      f4 aqk = aqk_d, akk = akk_d;
-      if (ib != w) aqk = akk = f4{0.f, 0.f, 0.f, 0.f};
-      if (ib == w - 1) {
+      f4 aqk = {0.f, 0.f, 0.f, 0.f}, akk = aqk;
+      if (ib == w) {
+        aqk = aqk_d;
+        akk = akk_d;
+      } else if (ib < w) {
+        const uint16_t *base = &sKD[(kd_slot(ib, w - 1 - ib) * 16 + lr) * kLdKD + 4 * gq];
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-          const uint16_t *src = &sKD[(16 * ib + lr) * kLdKD + 32 * ks + 4 * gq];
-          const u2 lo = *reinterpret_cast<const u2 *>(src);
-          const u2 hi = *reinterpret_cast<const u2 *>(src + 16);
+          const u2 lo = *reinterpret_cast<const u2 *>(base + 32 * ks);
+          const u2 hi = *reinterpret_cast<const u2 *>(base + 32 * ks + 16);
           const bf8 bk = bits_to_bf8(u4{lo.x, lo.y, hi.x, hi.y});
           aqk = mfma32(QSf[ks], bk, aqk);
           akk = mfma32(KSf[ks], bk, akk);
-        }
-      } else if (ib < w - 1) {
-#pragma unroll 1
-        for (int ks = 0; ks < 4; ++ks) {
-          const uint16_t *src = &sKD[(16 * ib + lr) * kLdKD + 32 * ks + 4 * gq];
-          const u2 lo = *reinterpret_cast<const u2 *>(src);
-          const u2 hi = *reinterpret_cast<const u2 *>(src + 16);
-          const bf8 bk = bits_to_bf8(u4{lo.x, lo.y, hi.x, hi.y});
-          const bf8 aq0 = QSf[ks], ak0 = KSf[ks];
-          float tq[8], tk[8];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const f4 E = *reinterpret_cast<const f4 *>(&s_E[perm_k(ks, gq, i) * 4]);
-            const float e1 = w == 2 ? E[1] : E[2];             // E_{w-1}, w in {2, 3}
-            const float f = (ib == w - 2) ? e1 : E[1] * E[2];     // w = 3, ib = 0
-            tq[i] = static_cast<float>(aq0[i]) * f;
-            tk[i] = static_cast<float>(ak0[i]) * f;
-          }
-          aqk = mfma32(pack8(tq), bk, aqk);
-          akk = mfma32(pack8(tk), bk, akk);
         }
       }
       // C tile: rows 16w + 4gq + e, column 16ib + lr.
@@ -374,14 +413,15 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
   }
   __syncthreads();
 
-  // ---- 6. T = (I + A_kk)^-1 (fp32), 16x16 diagonal inverses then block rows
+  // ---- 6. T = (I + A_kk)^-1 in fp32.  Diagonal 16x16 blocks by forward
+  // substitution (one wave each), then the block rows by sub-diagonal level:
+  //   X_ij = -D_i Y_ij,  Y_ij = sum_{k=j}^{i-1} L_ik X_kj.
   {
     float x[16];
     if (l < 16) {
-      const int n = l;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        float acc = (r == n) ? 1.f : 0.f;
+        float acc = (r == l) ? 1.f : 0.f;
 #pragma unroll
         for (int j = 0; j < r; ++j) acc = fmaf(-sT[(16 * w + r) * kLdT + 16 * w + j], x[j], acc);
         x[r] = acc;
@@ -393,32 +433,61 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
       for (int r = 0; r < 16; ++r) sT[(16 * w + r) * kLdT + 16 * w + l] = x[r];
     }
     __syncthreads();
+    // Block row ib: Y_{ib,j} = sum_{kb=j}^{ib-1} L_{ib,kb} X_{kb,j} (X_{j,j} = D_j),
+    // then X_{ib,j} = -D_ib Y_{ib,j}.  Row block ib's L entries are replaced
+    // only after all of its Y blocks have been formed.
+    const int ri = tid >> 4, cj = tid & 15;
+#pragma unroll
     for (int ib = 1; ib < 4; ++ib) {
-      // R = sum_{kb=jb}^{ib-1} L[ib][kb] X[kb][jb]  for columns 0 .. 16 ib - 1
-      for (int idx = tid; idx < 16 * 16 * ib; idx += kThreads) {
-        const int ri = idx / (16 * ib), cj = idx % (16 * ib);
-        const int m0 = 16 * (cj >> 4);
+#pragma unroll
+      for (int j = 0; j < ib; ++j) {
         float acc = 0.f;
-        for (int m = m0; m < 16 * ib; ++m) acc = fmaf(sT[(16 * ib + ri) * kLdT + m], sT[m * kLdT + cj], acc);
-        sR[ri * 48 + cj] = acc;
+        const float *lrow = sT + (16 * ib + ri) * kLdT;
+        for (int kb = j; kb < ib; ++kb) {
+#pragma unroll
+          for (int m4 = 0; m4 < 4; ++m4) {
+            const f4 lv = *reinterpret_cast<const f4 *>(lrow + 16 * kb + 4 * m4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              acc = fmaf(lv[i], sT[(16 * kb + 4 * m4 + i) * kLdT + 16 * j + cj], acc);
+          }
+        }
+        sY[j * 256 + tid] = acc;
       }
       __syncthreads();
-      for (int idx = tid; idx < 16 * 16 * ib; idx += kThreads) {
-        const int ri = idx / (16 * ib), cj = idx % (16 * ib);
+#pragma unroll
+      for (int j = 0; j < ib; ++j) {
         float acc = 0.f;
-        for (int m = 0; m <= ri; ++m) acc = fmaf(sT[(16 * ib + ri) * kLdT + 16 * ib + m], sR[m * 48 + cj], acc);
-        sT[(16 * ib + ri) * kLdT + cj] = -acc;
+#pragma unroll
+        for (int m = 0; m < 16; ++m)
+          acc = fmaf(sT[(16 * ib + ri) * kLdT + 16 * ib + m], sY[j * 256 + m * 16 + cj], acc);
+        sT[(16 * ib + ri) * kLdT + 16 * j + cj] = -acc;
       }
       __syncthreads();
     }
   }
+  __syncthreads();   // the scratch in region A has been read
 
-  // ---- 7. W = T (beta K e^G), Ut = T (beta V) for rows 16w .. 16w+15
-  {
-    f4 accW[8], accU[8];
+  // ---- 7. beta K e^G, transposed, into region A (its scratch reads ended
+  //         at the last barrier of the solve).
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) accW[nt] = accU[nt] = f4{0.f, 0.f, 0.f, 0.f};
-    const int nks = (w < 2) ? 1 : 2;
+  for (int ks = 0; ks < 4; ++ks) {
+    const u4 kw = kt_bits[ks];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t kword = kw[i >> 1];
+      sKt[swz(perm_k(ks, gq, i), row)] =
+          static_cast<uint16_t>((i & 1) ? (kword >> 16) : (kword & 0xffffu));
+    }
+  }
+  __syncthreads();
+
+  // ---- 8. W = T (beta K e^G), Ut = T (beta V) for rows 16w .. 16w+15
+  f4 accW[8], accU[8];
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) accW[nt] = accU[nt] = f4{0.f, 0.f, 0.f, 0.f};
+  {
+    const int nks = (w < 2) ? 1 : 2;   // T is lower triangular
     for (int ks = 0; ks < nks; ++ks) {
       const float *tr = &sT[(16 * w + lr) * kLdT + 32 * ks + 8 * gq];
       float ta[8];
@@ -439,29 +508,16 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
         accU[nt] = mfma32(af, bv, accU[nt]);
       }
     }
-    // Ut in C-tile order; -W row-major into LDS.
-#pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
-      u2 uw;
-      uw.x = pack_bf16x2(accU[nt][0], accU[nt][1]);
-      uw.y = pack_bf16x2(accU[nt][2], accU[nt][3]);
-      *reinterpret_cast<u2 *>(rec + kOffU + ((w * 8 + nt) * 64 + l) * 8) = uw;
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        sW[(16 * w + 4 * gq + e) * kLdKD + 16 * nt + lr] = f32_to_bf16_bits(-accW[nt][e]);
-    }
   }
-  __syncthreads();
+  __syncthreads();   // regions A and B are rewritten below
 
-  // ---- 8. Kbar^T (transposed into the sKt region) and e^{G_C}
+  // ---- 9. Ut in C-tile order to the workspace; -W rows to region B; e^{G_C}.
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    const u4 kw = kbar_bits[ks];
+  for (int nt = 0; nt < 8; ++nt) {
+    *reinterpret_cast<u2 *>(rec + kOffU + ((w * 8 + nt) * 64 + l) * 8) = pack4_bf16(accU[nt]);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t word = kw[i >> 1];
-      sKt[swz(perm_k(ks, gq, i), row)] = static_cast<uint16_t>((i & 1) ? (word >> 16) : (word & 0xffffu));
-    }
+    for (int e = 0; e < 4; ++e)
+      sW[(16 * w + 4 * gq + e) * kLdKD + 16 * nt + lr] = f32_to_bf16_bits(-accW[nt][e]);
   }
   if (tid < kD) {
     const f4 E = *reinterpret_cast<const f4 *>(&s_E[tid * 4]);
@@ -469,29 +525,14 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
   }
   __syncthreads();
 
-  // ---- 9. A-operand fragments from LDS to the workspace
+  // ---- 10. A-operand fragments from LDS to the workspace
   // -W: m = chunk rows 16w + lr, k = channels perm_k(ks, gq, .)
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
     const uint16_t *src = &sW[(16 * w + lr) * kLdKD + 32 * ks + 4 * gq];
     const u2 lo = *reinterpret_cast<const u2 *>(src);
     const u2 hi = *reinterpret_cast<const u2 *>(src + 16);
-    u4 o = {lo.x, lo.y, hi.x, hi.y};
-    *reinterpret_cast<u4 *>(rec + kOffW + ((w * 4 + ks) * 64 + l) * 16) = o;
-  }
-  // Kbar^T: m = channels 16mb + lr (mb = 2w, 2w+1), k = chunk rows perm_k(ks, gq, .)
-#pragma unroll
-  for (int mi = 0; mi < 2; ++mi) {
-    const int mb = 2 * w + mi;
-    const int ch = 16 * mb + lr;
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const int r0 = 32 * ks + 4 * gq;
-      const u2 lo = *reinterpret_cast<const u2 *>(&sKt[swz(ch, r0)]);
-      const u2 hi = *reinterpret_cast<const u2 *>(&sKt[swz(ch, r0 + 16)]);
-      u4 o = {lo.x, lo.y, hi.x, hi.y};
-      *reinterpret_cast<u4 *>(rec + kOffKt + ((mb * 2 + ks) * 64 + l) * 16) = o;
-    }
+    *reinterpret_cast<u4 *>(rec + kOffW + ((w * 4 + ks) * 64 + l) * 16) = u4{lo.x, lo.y, hi.x, hi.y};
   }
   // A_qk: m = chunk rows 16w + lr, k = chunk rows perm_k(ks, gq, .)
 #pragma unroll
@@ -499,8 +540,7 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
     const uint16_t *src = &sQK[(16 * w + lr) * kLdQK + 32 * ks + 4 * gq];
     const u2 lo = *reinterpret_cast<const u2 *>(src);
     const u2 hi = *reinterpret_cast<const u2 *>(src + 16);
-    u4 o = {lo.x, lo.y, hi.x, hi.y};
-    *reinterpret_cast<u4 *>(rec + kOffA + ((w * 2 + ks) * 64 + l) * 16) = o;
+    *reinterpret_cast<u4 *>(rec + kOffA + ((w * 2 + ks) * 64 + l) * 16) = u4{lo.x, lo.y, hi.x, hi.y};
   }
 }
 
@@ -519,157 +559,184 @@ struct ScanArgs {
   const int32_t *slots;
   void *o;
   int64_t o_stride;
-  int o_dtype;
+  int splits;   // blocks per (sequence, head): 128 / NVB
 };
 
-// One wavefront per (sequence, head, NV value columns); 4 wavefronts per block.
-template <int NV, int O_DT>
-__global__ __launch_bounds__(kThreads) void kda_chunk_scan_kernel(ScanArgs p) {
-  constexpr int NT = NV / 16;                 // 16-column tiles per wave
-  constexpr int WAVES_PER_HEAD = kD / NV;
-  const int l = threadIdx.x & 63;
+// Per-chunk operands of one wavefront (its 16 chunk rows / 32 state rows).
+template <int NT>
+struct ScanFrags {
+  u4 wn[4];       // -W, A operand, mb = w, ks 0..3
+  u4 qb[4];       // Q e^G, A operand, mb = w, ks 0..3
+  u4 aq[2];       // A_qk, A operand, mb = w, ks 0..1
+  u4 kt[2][2];    // Kbar^T, A operand, mb = 2w + mi, ks 0..1
+  u2 ut[NT];      // Ut, C tile (mb = w, column tile nt0 + nt), bf16
+  f4 gm[2];       // e^{G_C} for state rows 32w + 16mi + 4gq + e
+};
+
+template <int NT>
+__device__ __forceinline__ void load_frags(ScanFrags<NT> &f, const uint8_t *rec, int w, int l,
+                                           int gq, int nt0) {
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    f.wn[ks] = *reinterpret_cast<const u4 *>(rec + kOffW + ((w * 4 + ks) * 64 + l) * 16);
+    f.qb[ks] = *reinterpret_cast<const u4 *>(rec + kOffQ + ((w * 4 + ks) * 64 + l) * 16);
+  }
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    f.aq[ks] = *reinterpret_cast<const u4 *>(rec + kOffA + ((w * 2 + ks) * 64 + l) * 16);
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+      f.kt[mi][ks] = *reinterpret_cast<const u4 *>(rec + kOffKt + (((2 * w + mi) * 2 + ks) * 64 + l) * 16);
+  }
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+    f.ut[nt] = *reinterpret_cast<const u2 *>(rec + kOffU + ((w * 8 + nt0 + nt) * 64 + l) * 8);
+  const float *gam = reinterpret_cast<const float *>(rec + kOffG);
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi) f.gm[mi] = *reinterpret_cast<const f4 *>(&gam[32 * w + 16 * mi + 4 * gq]);
+}
+
+// One block of 4 wavefronts per (sequence, head, NVB value columns).  Wave w
+// owns chunk rows 16w..16w+15 of U and O and state rows 32w..32w+31; the
+// state and U are exchanged between the waves as bf16 B operands in LDS.
+template <int NVB, int O_DT>
+__global__ __launch_bounds__(kThreads, 1) void kda_chunk_scan_kernel(ScanArgs p) {
+  constexpr int NT = NVB / 16;               // 16-column tiles per block
+  __shared__ __attribute__((aligned(16))) uint8_t sSb[4 * NT * 64 * 16];   // S, [ks][nt][lane]
+  __shared__ __attribute__((aligned(16))) uint8_t sUb[2 * NT * 64 * 16];   // U, [ks][nt][lane]
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l = tid & 63;
   const int lr = l & 15, gq = l >> 4;
-  const int gw = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
-  const int vt = gw % WAVES_PER_HEAD;
-  const int sh = gw / WAVES_PER_HEAD;
+  // XCD-aware order: the `splits` blocks of one (sequence, head) share the
+  // same blockIdx % 8, i.e. the same XCD and L2, so they share operand reads.
+  const int b = blockIdx.x;
+  const int group = b / (8 * p.splits);
+  const int half = (b / 8) % p.splits;
+  const int sh = group * 8 + (b % 8);
   const int h = sh % p.num_heads;
   const int s = sh / p.num_heads;
   if (s >= p.n_seqs) return;
-  const int v0 = vt * NV;
+  const int nt0 = half * NT;                  // first 16-column tile of this block
   const int64_t seq_a = min<int64_t>(max<int64_t>(p.cu[s], 0), p.total);
   const int64_t seq_b = min<int64_t>(max<int64_t>(p.cu[s + 1], seq_a), p.total);
-  const int nchunks = static_cast<int>((seq_b - seq_a + kC - 1) / kC);
+  const int nchunks = static_cast<int>(min<int64_t>((seq_b - seq_a + kC - 1) / kC,
+                                                    p.max_ch - p.chunk_start[s]));
   const int cbase = p.chunk_start[s];
   const int slot = p.slots ? p.slots[s] : s;
   const bool has_slot = slot >= 0 && slot < p.n_slots;  // else: zero start, nothing written
   const int64_t state_off = (static_cast<int64_t>(has_slot ? slot : 0) * p.num_heads + h) * kD * kD;
 
-  // S tiles: [mb 8][nt NT], lane holds rows 16mb + 4gq + e, column v0 + 16nt + lr.
-  f4 S[8][NT];
+  // S tiles: [mi 2][nt NT], rows 32w + 16mi + 4gq + e, column 16(nt0 + nt) + lr.
+  f4 S[2][NT];
 #pragma unroll
-  for (int mb = 0; mb < 8; ++mb)
+  for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       f4 v = {0.f, 0.f, 0.f, 0.f};
       if (p.h0 && has_slot) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          v[e] = p.h0[state_off + static_cast<int64_t>(16 * mb + 4 * gq + e) * kD + v0 + 16 * nt + lr];
+          v[e] = p.h0[state_off + static_cast<int64_t>(32 * w + 16 * mi + 4 * gq + e) * kD +
+                      16 * (nt0 + nt) + lr];
       }
-      S[mb][nt] = v;
+      S[mi][nt] = v;
     }
 
+  ScanFrags<NT> cur, nxt;
+  if (nchunks > 0)
+    load_frags<NT>(cur, p.records + (static_cast<size_t>(cbase) * p.num_heads + h) * kRecBytes, w, l,
+                   gq, nt0);
   for (int cc = 0; cc < nchunks; ++cc) {
-    const int64_t gc = cbase + cc;
-    if (gc >= p.max_ch) break;
-    const uint8_t *rec = p.records + (static_cast<size_t>(gc) * p.num_heads + h) * kRecBytes;
+    if (cc + 1 < nchunks)
+      load_frags<NT>(nxt, p.records + (static_cast<size_t>(cbase + cc + 1) * p.num_heads + h) * kRecBytes,
+                     w, l, gq, nt0);
 
-    // S as bf16 B operands: K-step ks pairs tiles 2ks and 2ks+1.
-    bf8 Sb[4][NT];
+    // 1. publish this wave's state rows as K-step w of the bf16 B operand.
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
+    for (int nt = 0; nt < NT; ++nt) {
+      float t[8];
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        float t[8];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          t[e] = S[2 * ks][nt][e];
-          t[4 + e] = S[2 * ks + 1][nt][e];
-        }
-        Sb[ks][nt] = pack8(t);
+      for (int e = 0; e < 4; ++e) {
+        t[e] = S[0][nt][e];
+        t[4 + e] = S[1][nt][e];
       }
+      *reinterpret_cast<u4 *>(sSb + ((w * NT + nt) * 64 + l) * 16) = bf8_to_bits(pack8(t));
+    }
+    __syncthreads();
 
-    // U = Ut - W S
-    f4 U[4][NT];
+    // 2. U = Ut - W S and O = (Q e^G) S for chunk rows 16w..16w+15.
+    f4 U[NT], O[NT];
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
+    for (int nt = 0; nt < NT; ++nt) {
+      bf8 sb[4];
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const u2 uw = *reinterpret_cast<const u2 *>(rec + kOffU + ((mb * 8 + v0 / 16 + nt) * 64 + l) * 8);
-        U[mb][nt] = f4{__uint_as_float(uw.x << 16), __uint_as_float(uw.x & 0xffff0000u),
-                       __uint_as_float(uw.y << 16), __uint_as_float(uw.y & 0xffff0000u)};
-      }
+      for (int ks = 0; ks < 4; ++ks)
+        sb[ks] = bits_to_bf8(*reinterpret_cast<const u4 *>(sSb + ((ks * NT + nt) * 64 + l) * 16));
+      const u2 uw = cur.ut[nt];
+      f4 u = {__uint_as_float(uw.x << 16), __uint_as_float(uw.x & 0xffff0000u),
+              __uint_as_float(uw.y << 16), __uint_as_float(uw.y & 0xffff0000u)};
+      f4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const bf8 a = bits_to_bf8(*reinterpret_cast<const u4 *>(rec + kOffW + ((mb * 4 + ks) * 64 + l) * 16));
+        u = mfma32(bits_to_bf8(cur.wn[ks]), sb[ks], u);
+        o = mfma32(bits_to_bf8(cur.qb[ks]), sb[ks], o);
+      }
+      U[nt] = u;
+      O[nt] = o;
+    }
+    // 3. publish U rows 16w.. as half (w & 1) of K-step w/2 of the U operand.
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) U[mb][nt] = mfma32(a, Sb[ks][nt], U[mb][nt]);
+    for (int nt = 0; nt < NT; ++nt)
+      *reinterpret_cast<u2 *>(sUb + (((w >> 1) * NT + nt) * 64 + l) * 16 + (w & 1) * 8) = pack4_bf16(U[nt]);
+    __syncthreads();
+
+    // 4. O += A_qk U (A_qk is lower triangular: K-steps <= w/2);
+    //    S = Diag(e^{G_C}) S + Kbar^T U.
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      bf8 ub[2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        ub[ks] = bits_to_bf8(*reinterpret_cast<const u4 *>(sUb + ((ks * NT + nt) * 64 + l) * 16));
+      O[nt] = mfma32(bits_to_bf8(cur.aq[0]), ub[0], O[nt]);
+      if (w >= 2) O[nt] = mfma32(bits_to_bf8(cur.aq[1]), ub[1], O[nt]);
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi) {
+        f4 sv = S[mi][nt] * cur.gm[mi];
+        sv = mfma32(bits_to_bf8(cur.kt[mi][0]), ub[0], sv);
+        sv = mfma32(bits_to_bf8(cur.kt[mi][1]), ub[1], sv);
+        S[mi][nt] = sv;
       }
     }
-    bf8 Ub[2][NT];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        float t[8];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          t[e] = U[2 * ks][nt][e];
-          t[4 + e] = U[2 * ks + 1][nt][e];
-        }
-        Ub[ks][nt] = pack8(t);
-      }
 
-    // O = (Q e^G) S + A_qk U, stored for the valid rows of the chunk.
+    // 5. store O for the valid rows of the chunk.
     const int64_t tok0 = seq_a + static_cast<int64_t>(cc) * kC;
     const int rows_valid = static_cast<int>(min<int64_t>(kC, seq_b - tok0));
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-      f4 O[NT];
+    for (int e = 0; e < 4; ++e) {
+      const int r = 16 * w + 4 * gq + e;
+      if (r < rows_valid) {
+        const int64_t base = (tok0 + r) * p.o_stride + static_cast<int64_t>(h) * kD + 16 * nt0 + lr;
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) O[nt] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const bf8 a = bits_to_bf8(*reinterpret_cast<const u4 *>(rec + kOffQ + ((mb * 4 + ks) * 64 + l) * 16));
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) O[nt] = mfma32(a, Sb[ks][nt], O[nt]);
-      }
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        if (ks == 1 && mb < 2) continue;  // A_qk is lower triangular
-        const bf8 a = bits_to_bf8(*reinterpret_cast<const u4 *>(rec + kOffA + ((mb * 2 + ks) * 64 + l) * 16));
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) O[nt] = mfma32(a, Ub[ks][nt], O[nt]);
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int r = 16 * mb + 4 * gq + e;
-        if (r < rows_valid) {
-          const int64_t base = (tok0 + r) * p.o_stride + static_cast<int64_t>(h) * kD + v0 + lr;
-#pragma unroll
-          for (int nt = 0; nt < NT; ++nt) store_elem(p.o, base + 16 * nt, O_DT, O[nt][e]);
-        }
+        for (int nt = 0; nt < NT; ++nt) store_elem(p.o, base + 16 * nt, O_DT, O[nt][e]);
       }
     }
-
-    // S = Diag(e^{G_C}) S + Kbar^T U
-    const float *gam = reinterpret_cast<const float *>(rec + kOffG);
-#pragma unroll
-    for (int mb = 0; mb < 8; ++mb) {
-      const f4 gm = *reinterpret_cast<const f4 *>(&gam[16 * mb + 4 * gq]);
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) S[mb][nt] *= gm;
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const bf8 a = bits_to_bf8(*reinterpret_cast<const u4 *>(rec + kOffKt + ((mb * 2 + ks) * 64 + l) * 16));
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) S[mb][nt] = mfma32(a, Ub[ks][nt], S[mb][nt]);
-      }
-    }
+    if (cc + 1 < nchunks) cur = nxt;
   }
 
   if (p.ht && has_slot) {
 #pragma unroll
-    for (int mb = 0; mb < 8; ++mb)
+    for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          p.ht[state_off + static_cast<int64_t>(16 * mb + 4 * gq + e) * kD + v0 + 16 * nt + lr] = S[mb][nt][e];
+          p.ht[state_off + static_cast<int64_t>(32 * w + 16 * mi + 4 * gq + e) * kD + 16 * (nt0 + nt) + lr] =
+              S[mi][nt][e];
   }
 }
 
-constexpr int kScanNV = 32;
 
 template <int QKV_DT, int G_DT>
 int launch_intra(dim3 grid, hipStream_t st, const IntraArgs &ia) {
@@ -763,16 +830,29 @@ extern "C" int sophia_kda_chunk_fwd(const void *q, const void *k, const void *v,
       rc = launch_intra<SOPHIA_DTYPE_F32, SOPHIA_DTYPE_BF16>(grid, st, ia);
     if (rc) return rc;
   }
+  // Two blocks (64 value columns each) per (sequence, head) when the pairs
+  // alone would leave CUs idle; one block of 128 columns otherwise.
+  int device = 0, cus = 256;
+  if (hipGetDevice(&device) == hipSuccess)
+    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+  const int64_t pairs = static_cast<int64_t>(n_seqs) * num_heads;
+  const int splits = pairs < cus ? 2 : 1;
   ScanArgs sa{cu_seqlens, n_seqs, total_tokens, num_heads, max_ch, chunk_start, records,
-              initial_state, final_state, n_state_slots, state_slots, o, o_row_stride, qkv_dtype};
-  const int64_t waves = static_cast<int64_t>(n_seqs) * num_heads * (kD / kScanNV);
-  const int64_t blocks = (waves + 3) / 4;
+              initial_state, final_state, n_state_slots, state_slots, o, o_row_stride, splits};
+  const int64_t groups = (pairs + 7) / 8;
+  const int64_t blocks = groups * 8 * splits;
   SOPHIA_REQUIRE(blocks <= 0x7fffffff, "kda_chunk_fwd: grid too large");
-  if (qkv_dtype == SOPHIA_DTYPE_BF16)
-    hipLaunchKernelGGL((kda_chunk_scan_kernel<kScanNV, SOPHIA_DTYPE_BF16>),
-                       dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, st, sa);
-  else
-    hipLaunchKernelGGL((kda_chunk_scan_kernel<kScanNV, SOPHIA_DTYPE_F32>),
-                       dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, st, sa);
+  const dim3 sgrid(static_cast<unsigned>(blocks));
+  if (qkv_dtype == SOPHIA_DTYPE_BF16) {
+    if (splits == 2)
+      hipLaunchKernelGGL((kda_chunk_scan_kernel<64, SOPHIA_DTYPE_BF16>), sgrid, dim3(kThreads), 0, st, sa);
+    else
+      hipLaunchKernelGGL((kda_chunk_scan_kernel<128, SOPHIA_DTYPE_BF16>), sgrid, dim3(kThreads), 0, st, sa);
+  } else {
+    if (splits == 2)
+      hipLaunchKernelGGL((kda_chunk_scan_kernel<64, SOPHIA_DTYPE_F32>), sgrid, dim3(kThreads), 0, st, sa);
+    else
+      hipLaunchKernelGGL((kda_chunk_scan_kernel<128, SOPHIA_DTYPE_F32>), sgrid, dim3(kThreads), 0, st, sa);
+  }
   return check_launch("kda_chunk_scan");
 }
