@@ -93,6 +93,17 @@ __device__ __forceinline__ float kda_log_decay(float z, float head_scale, float 
   return lb * sigmoid_f(head_scale * (z + bias));
 }
 
+// Work-group barrier that orders LDS accesses only.  __syncthreads() is a
+// release/acquire fence over all address spaces, which makes every wave wait
+// for its outstanding global loads and stores (s_waitcnt vmcnt(0)) before the
+// barrier -- that would serialise register prefetches and workspace stores.
+// Use only where the barrier protects LDS data.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Butterfly sum over the whole 64-lane wavefront.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -299,7 +299,7 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
 #pragma unroll
     for (int e = 0; e < 32; ++e) s_E[perm_k(e >> 3, gq, e & 7) * 4 + w] = __expf(gv[e]);
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- 4. scaled operands; diagonal 16x16 blocks of A_qk / A_kk
   // Per channel, with Gloc the within-sub-block cumulative log-decay and
@@ -359,7 +359,7 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
             u2{pack_bf16x2(kd2[i0], kd2[i0 + 1]), pack_bf16x2(kd2[i0 + 2], kd2[i0 + 3])};
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- 4b. Kbar^T fragments (m = channels 16mb + lr for mb = 2w, 2w+1,
   //          k = chunk rows perm_k(ks, gq, .)) to the workspace; region C is
@@ -376,7 +376,7 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
       *reinterpret_cast<u4 *>(rec + kOffKt + ((mb * 2 + ks) * 64 + l) * 16) = u4{lo.x, lo.y, hi.x, hi.y};
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- 5. off-diagonal blocks: key block ib < w uses copy v = w-1-ib of
   // its key-side rows (already scaled by prod_{ib<i<w} E_i).
@@ -411,7 +411,7 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- 6. T = (I + A_kk)^-1 in fp32.  Diagonal 16x16 blocks by forward
   // substitution (one wave each), then the block rows by sub-diagonal level:
@@ -427,12 +427,12 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
         x[r] = acc;
       }
     }
-    __syncthreads();
+    lds_barrier();
     if (l < 16) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) sT[(16 * w + r) * kLdT + 16 * w + l] = x[r];
     }
-    __syncthreads();
+    lds_barrier();
     // Block row ib: Y_{ib,j} = sum_{kb=j}^{ib-1} L_{ib,kb} X_{kb,j} (X_{j,j} = D_j),
     // then X_{ib,j} = -D_ib Y_{ib,j}.  Row block ib's L entries are replaced
     // only after all of its Y blocks have been formed.
@@ -454,7 +454,7 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
         }
         sY[j * 256 + tid] = acc;
       }
-      __syncthreads();
+      lds_barrier();
 #pragma unroll
       for (int j = 0; j < ib; ++j) {
         float acc = 0.f;
@@ -463,10 +463,10 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
           acc = fmaf(sT[(16 * ib + ri) * kLdT + 16 * ib + m], sY[j * 256 + m * 16 + cj], acc);
         sT[(16 * ib + ri) * kLdT + 16 * j + cj] = -acc;
       }
-      __syncthreads();
+      lds_barrier();
     }
   }
-  __syncthreads();   // the scratch in region A has been read
+  lds_barrier();   // the scratch in region A has been read
 
   // ---- 7. beta K e^G, transposed, into region A (its scratch reads ended
   //         at the last barrier of the solve).
@@ -480,7 +480,7 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
           static_cast<uint16_t>((i & 1) ? (kword >> 16) : (kword & 0xffffu));
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- 8. W = T (beta K e^G), Ut = T (beta V) for rows 16w .. 16w+15
   f4 accW[8], accU[8];
@@ -509,7 +509,7 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
       }
     }
   }
-  __syncthreads();   // regions A and B are rewritten below
+  lds_barrier();   // regions A and B are rewritten below
 
   // ---- 9. Ut in C-tile order to the workspace; -W rows to region B; e^{G_C}.
 #pragma unroll
@@ -523,7 +523,7 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
     const f4 E = *reinterpret_cast<const f4 *>(&s_E[tid * 4]);
     reinterpret_cast<float *>(rec + kOffG)[tid] = E[0] * E[1] * E[2] * E[3];
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- 10. A-operand fragments from LDS to the workspace
   // -W: m = chunk rows 16w + lr, k = channels perm_k(ks, gq, .)
@@ -663,7 +663,7 @@ __global__ __launch_bounds__(kThreads, 1) void kda_chunk_scan_kernel(ScanArgs p)
       }
       *reinterpret_cast<u4 *>(sSb + ((w * NT + nt) * 64 + l) * 16) = bf8_to_bits(pack8(t));
     }
-    __syncthreads();
+    lds_barrier();
 
     // 2. U = Ut - W S and O = (Q e^G) S for chunk rows 16w..16w+15.
     f4 U[NT], O[NT];
@@ -689,7 +689,7 @@ __global__ __launch_bounds__(kThreads, 1) void kda_chunk_scan_kernel(ScanArgs p)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
       *reinterpret_cast<u2 *>(sUb + (((w >> 1) * NT + nt) * 64 + l) * 16 + (w & 1) * 8) = pack4_bf16(U[nt]);
-    __syncthreads();
+    lds_barrier();
 
     // 4. O += A_qk U (A_qk is lower triangular: K-steps <= w/2);
     //    S = Diag(e^{G_C}) S + Kbar^T U.

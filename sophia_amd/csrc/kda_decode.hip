@@ -82,7 +82,7 @@ __global__ __launch_bounds__(kThreads) void kda_decode_kernel(
     s_red[wave][1] = sk;
     s_red[wave][2] = sqk;
   }
-  __syncthreads();
+  lds_barrier();
   float qs = scale, ks = 1.f;
   if (flags & SOPHIA_KDA_QK_L2NORM) {
     const float nq = sqrtf(s_red[0][0] + s_red[1][0]);
@@ -97,7 +97,7 @@ __global__ __launch_bounds__(kThreads) void kda_decode_kernel(
     s_q[t] = qv * qs;
     s_k[t] = kv * ks;
   }
-  __syncthreads();
+  lds_barrier();
 
   // Decay the held rows and form the two partial column reductions.
   f4 p = {0.f, 0.f, 0.f, 0.f}, rq = {0.f, 0.f, 0.f, 0.f};
@@ -121,7 +121,7 @@ __global__ __launch_bounds__(kThreads) void kda_decode_kernel(
       s_r[wave][4 * cg + c] = rq[c];
     }
   }
-  __syncthreads();
+  lds_barrier();
   if (t < kD) {
     const float pj = s_p[0][t] + s_p[1][t] + s_p[2][t] + s_p[3][t];
     const float rj = s_r[0][t] + s_r[1][t] + s_r[2][t] + s_r[3][t];
@@ -130,7 +130,7 @@ __global__ __launch_bounds__(kThreads) void kda_decode_kernel(
     store_elem(o, static_cast<int64_t>(b) * o_stride + static_cast<int64_t>(h) * kD + t, qkv_dtype,
                rj + qk * u);
   }
-  __syncthreads();
+  lds_barrier();
   const f4 u4v = *reinterpret_cast<const f4 *>(&s_u[4 * cg]);
 #pragma unroll
   for (int r = 0; r < kRowsPerThread; ++r) {
