@@ -834,7 +834,7 @@ extern "C" int sophia_kda_chunk_fwd(const void *q, const void *k, const void *v,
   // alone would leave CUs idle; one block of 128 columns otherwise.
   int device = 0, cus = 256;
   if (hipGetDevice(&device) == hipSuccess)
-    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) cus = 256;
   const int64_t pairs = static_cast<int64_t>(n_seqs) * num_heads;
   const int splits = pairs < cus ? 2 : 1;
   ScanArgs sa{cu_seqlens, n_seqs, total_tokens, num_heads, max_ch, chunk_start, records,

@@ -127,8 +127,16 @@ __global__ __launch_bounds__(256) void short_conv_fwd_kernel(
 #pragma unroll
     for (int j = 0; j < K; ++j) w[i][j] = weight[static_cast<int64_t>(c0 + i) * K + j];
 
+  // Offsets are clamped to [0, total] and made monotone, so malformed
+  // cu_seqlens can never move a read or write outside x, y or conv_state;
+  // rows outside every sequence are left untouched.
   int s = find_seq(cu, n_seqs, r0);
-  int64_t seq_start = cu[s], seq_end = cu[s + 1];
+  int64_t seq_start = 0, seq_end = 0;
+  auto bounds = [&](int seq) {
+    seq_start = min<int64_t>(max<int64_t>(cu[seq], 0), total);
+    seq_end = min<int64_t>(max<int64_t>(cu[seq + 1], seq_start), total);
+  };
+  bounds(s);
   auto hist_of = [&](int seq) -> const float * {
     if (!read_history || conv_state == nullptr || K == 1) return nullptr;
     int slot = slots ? slots[seq] : seq;
@@ -136,15 +144,19 @@ __global__ __launch_bounds__(256) void short_conv_fwd_kernel(
     return conv_state + static_cast<int64_t>(slot) * channels * (K - 1);
   };
   Vec8<DT> prev[K > 1 ? K - 1 : 1];
-  init_window<K, DT>(prev, x, xs, hist_of(s), r0, seq_start, c0, channels);
+  bool fresh = true;  // the window must be (re)loaded before the next row
   for (int64_t r = r0; r < r1; ++r) {
-    if (r >= seq_end) {
-      do {
-        ++s;
-        seq_start = cu[s];
-        seq_end = cu[s + 1];
-      } while (r >= seq_end);
+    while (r >= seq_end && s + 1 < n_seqs) {
+      bounds(++s);
+      fresh = true;
+    }
+    if (r < seq_start || r >= seq_end) {
+      fresh = true;
+      continue;
+    }
+    if (fresh) {
       init_window<K, DT>(prev, x, xs, hist_of(s), r, seq_start, c0, channels);
+      fresh = false;
     }
     Vec8<DT> cur;
     cur.load(x, r * xs + c0);
@@ -168,13 +180,14 @@ __global__ __launch_bounds__(256) void short_conv_fwd_kernel(
 template <int K, int DT>
 __global__ __launch_bounds__(256) void short_conv_history_kernel(
     const void *__restrict__ x, int64_t xs, float *__restrict__ conv_state, int n_slots,
-    const int32_t *__restrict__ slots, const int32_t *__restrict__ cu, int n_seqs, int channels,
-    int read_history) {
+    const int32_t *__restrict__ slots, const int32_t *__restrict__ cu, int n_seqs, int64_t total,
+    int channels, int read_history) {
   const int cv = blockIdx.x * blockDim.x + threadIdx.x;
   const int s = blockIdx.y;
   const int c0 = cv * kVec;
   if (c0 >= channels || s >= n_seqs) return;
-  const int64_t start = cu[s], end = cu[s + 1];
+  const int64_t start = min<int64_t>(max<int64_t>(cu[s], 0), total);
+  const int64_t end = min<int64_t>(max<int64_t>(cu[s + 1], start), total);
   const int slot = slots ? slots[s] : s;
   if (slot < 0 || slot >= n_slots) return;
   float *hist = conv_state + static_cast<int64_t>(slot) * channels * (K - 1);
@@ -275,7 +288,7 @@ int launch_fwd(const void *x, int64_t xs, void *y, int64_t ys, const float *w, f
     if (write_history && state != nullptr && n > 0) {
       dim3 g2((nvec + 255) / 256, n);
       hipLaunchKernelGGL((short_conv_history_kernel<K, DT>), g2, dim3(256), 0, st, x, xs, state,
-                         n_slots, slots, cu, n, channels, read_history);
+                         n_slots, slots, cu, n, total, channels, read_history);
       return check_launch("short_conv_history");
     }
   }

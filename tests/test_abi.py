@@ -1,0 +1,92 @@
+"""The C-ABI library loads and exports every entry point that
+include/sophia_kda.h declares, with the argument counts the ctypes binding
+uses.  CPU only: the calls made here are host-side (version, workspace-size
+query, argument validation) and never launch a kernel.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "sophia_kda.h")
+
+
+def _declarations() -> dict[str, int]:
+    """name -> number of parameters, for every function the header declares."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    decls = {}
+    for m in re.finditer(r"\b(sophia_\w+)\s*\(([^;{]*?)\)\s*;", text, flags=re.S):
+        name, params = m.group(1), m.group(2).strip()
+        decls[name] = 0 if params in ("", "void") else len(params.split(","))
+    return decls
+
+
+def _lib():
+    from sophia_amd import _native
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.skip("HIP library not built (run `python -m sophia_amd.build`)")
+    return _native
+
+
+def test_header_declares_the_entry_points():
+    decls = _declarations()
+    for name in ("sophia_short_conv_fwd", "sophia_short_conv_step", "sophia_kda_chunk_fwd",
+                 "sophia_kda_chunk_workspace_size", "sophia_kda_decode_step",
+                 "sophia_last_error", "sophia_abi_version"):
+        assert name in decls, name
+
+
+def test_library_exports_every_declared_symbol():
+    nat = _lib()
+    handle = ctypes.CDLL(nat.LIB_PATH)
+    decls = _declarations()
+    for name, nparams in decls.items():
+        assert hasattr(handle, name), f"{name} not exported"
+        assert name in nat.SIGNATURES, f"{name} has no ctypes signature"
+        assert len(nat.SIGNATURES[name][1]) == nparams, f"{name}: argument count differs"
+    assert set(nat.SIGNATURES) == set(decls)
+
+
+def test_host_side_queries_and_validation():
+    nat = _lib()
+    lib = nat.lib()
+    assert lib.sophia_abi_version() >= 100
+    # 8 sequences, 17,408 tokens, 16 heads: header + one record per (chunk, head).
+    ws = lib.sophia_kda_chunk_workspace_size(17408, 8, 16, 128)
+    assert ws > 0
+    assert lib.sophia_kda_chunk_workspace_size(2 * 17408, 8, 16, 128) > ws
+    assert lib.sophia_kda_chunk_workspace_size(17408, 8, 16, 64) == 0
+    assert lib.sophia_kda_chunk_workspace_size(100, 0, 16, 128) == 0
+    # head_dim 64 is rejected on the host before any launch.
+    rc = lib.sophia_kda_decode_step(None, None, None, 2048, 1, None, 2048, 0, None, 16, 0, None,
+                                    None, 1.0, -5.0, 7, None, 1, None, 1, 1, 16, 64, None, 2048,
+                                    None)
+    assert rc == nat.SOPHIA_ERR_INVALID
+    assert "head_dim" in nat.last_error()
+    rc = lib.sophia_short_conv_fwd(None, 6144, None, 6144, 1, None, None, 0, None, None, 1, 10,
+                                   6143, 4, 0, 0, None)
+    assert rc == nat.SOPHIA_ERR_INVALID
+    assert "channels" in nat.last_error()
+    rc = lib.sophia_kda_chunk_fwd(None, None, None, 2048, 1, None, 2048, 0, None, 16, 0, None,
+                                  None, 1.0, -6.0, 7, None, 1, 0, 16, 128, None, None, 0, None,
+                                  None, 2048, None, 0, None)
+    assert rc == nat.SOPHIA_ERR_INVALID
+
+
+def test_ops_reject_cpu_tensors():
+    import torch
+    from sophia_amd import ops
+    x = torch.zeros(4, 16, 128)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.kda_chunk_fwd(x, x, x, x, torch.zeros(4, 16), torch.tensor([0, 4], dtype=torch.int32))
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.kda_decode_step(x, x, x, x, torch.zeros(4, 16), torch.zeros(4, 16, 128, 128))
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.short_conv_fwd(torch.zeros(4, 8), torch.zeros(8, 4),
+                           torch.tensor([0, 4], dtype=torch.int32))
