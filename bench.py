@@ -38,6 +38,10 @@ PREFILL_BYTES_PER_TOKEN = HEADS * (4 * DIM * 2 + DIM * 4 + 4)          # 24,640
 # Causal chunk-form flops per token at C = 64: H * (5 C d + 6 d^2).
 PREFILL_FLOPS_PER_TOKEN = HEADS * (5 * 64 * DIM + 6 * DIM * DIM)      # 2,228,224
 METRIC = "KDA prefill tokens/s + % MFMA peak; decode-step µs and HBM GB/s at B=256"
+# HBM bytes per launch measured with rocprofv3 on this workload (FETCH_SIZE and
+# WRITE_SIZE in separate passes; FETCH_SIZE doubled, the factor a plain 1 GiB
+# device copy gives on MI355X).  Re-measured whenever a kernel changes.
+MEASURED_TRAFFIC_BYTES = {"prefill": 801.3e6, "decode": 543.5e6, "short_conv": 318.7e6}
 
 
 def prefill_lengths(seed: int = 0, n: int = 8, lo: int = 256, hi: int = 4096) -> list[int]:
@@ -78,9 +82,11 @@ def time_events(torch, fn, steps: int, warmup: int, stream) -> tuple[float, list
     return wall, per
 
 
-def cpu_baseline(inputs, lengths, budget_s: float = 20.0):
-    """The oracle's C restatement of the reference's per-token recurrence on
-    this host's cores, over a bounded prefix of the same workload."""
+def cpu_baseline(inputs, lengths, budget_s: float = 10.0):
+    """The oracle's C restatement of the reference's per-token recurrence
+    (oracle/kda_ref.c, fp32, OpenMP over sequence x head) on this host's
+    cores, over the same packed batch, repeated until about `budget_s`
+    seconds of CPU work have been timed."""
     from oracle import c_oracle
     cores = len(os.sched_getaffinity(0))
     q = inputs["q"].float().cpu().numpy()
@@ -88,26 +94,31 @@ def cpu_baseline(inputs, lengths, budget_s: float = 20.0):
     v = inputs["v"].float().cpu().numpy()
     g = inputs["g"].cpu().numpy()
     beta = inputs["beta"].cpu().numpy()
-    # Sample: every sequence truncated to its first `m` tokens (all 16 heads),
-    # m grown until the run costs a few seconds.
-    m = 64
-    while True:
-        sub = [min(n, m) for n in lengths]
-        idx = np.concatenate([np.arange(a, a + s) for a, s in
-                              zip(np.concatenate([[0], np.cumsum(lengths)[:-1]]), sub)])
-        cu = np.concatenate([[0], np.cumsum(sub)]).astype(np.int32)
+    cu = inputs["cu"].cpu().numpy()
+    reps, elapsed = 0, 0.0
+    while elapsed < budget_s:
         t0 = time.perf_counter()
-        c_oracle.kda_varlen(q[idx], k[idx], v[idx], g[idx], beta[idx], cu, use_gate=False,
-                            use_beta_sigmoid=False, nthreads=cores)
-        dt = time.perf_counter() - t0
-        if dt > 2.0 or m >= max(lengths) or dt * (2 ** 3) > budget_s:
-            break
-        m *= 2
+        c_oracle.kda_varlen(q, k, v, g, beta, cu, use_gate=False, use_beta_sigmoid=False,
+                            nthreads=cores)
+        elapsed += time.perf_counter() - t0
+        reps += 1
     tokens = int(cu[-1])
-    return {"value": tokens / dt, "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"C per-token fp32 recurrence (oracle/kda_ref.c, OpenMP over seq x head) on "
-                      f"the first {m} tokens of each of the 8 sequences ({tokens} tokens, 16 heads), "
-                      f"{dt:.2f} s; os.cpu_count()={os.cpu_count()}"}
+    return {"value": round(tokens * reps / elapsed, 1), "unit": "tokens/s", "cores": cores,
+            "kind": "port",
+            "sample": f"whole workload ({tokens} tokens x 16 heads) run {reps} times in "
+                      f"{elapsed:.1f} s by the C per-token fp32 recurrence of the reference's "
+                      f"CPU path (OpenMP over sequence x head, {cores} threads); "
+                      f"os.cpu_count()={os.cpu_count()}"}
+
+
+def copy_bandwidth(torch, dev, stream, nbytes: int = 1 << 30) -> float:
+    """Device-to-device copy rate (GB/s, read + write bytes) of a plain
+    torch copy kernel on this GPU: the practical HBM ceiling beside the
+    8 TB/s vendor figure."""
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    _, per = time_events(torch, lambda: dst.copy_(src), 10, 3, stream)
+    return 2 * nbytes / (float(np.median(per)) / 1e3) / 1e9
 
 
 def main(argv=None) -> int:
@@ -116,7 +127,9 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["all", "prefill", "decode"], default="all")
+    ap.add_argument("--only", choices=["all", "prefill", "conv", "decode", "copy"], default="all",
+                    help="run one workload only (for kernel profiling); the JSON line then "
+                         "carries that workload's fields alone")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
@@ -134,6 +147,14 @@ def main(argv=None) -> int:
     torch.cuda.set_device(dev)
     stream = torch.cuda.current_stream(dev)
 
+    if args.only == "copy":
+        # Calibration workload for the memory counters: a plain 1 GiB device copy.
+        gbs = copy_bandwidth(torch, dev, stream)
+        print(json.dumps({"metric": "device copy GB/s (read + write bytes)", "value": round(gbs, 1),
+                          "unit": "GB/s", "bytes_read_per_copy": 1 << 30,
+                          "bytes_written_per_copy": 1 << 30}), flush=True)
+        return 0
+
     lengths = prefill_lengths()
     total = int(sum(lengths))
     inp = make_prefill_inputs(torch, dev, lengths)
@@ -149,7 +170,9 @@ def main(argv=None) -> int:
               "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
               "data": "synthetic"}
 
-    wall, per = time_events(torch, prefill, args.steps, args.warmup, stream)
+    run_prefill = args.only in ("all", "prefill")
+    wall, per = time_events(torch, prefill, args.steps if run_prefill else 1,
+                            args.warmup if run_prefill else 0, stream)
     avg_ms = float(np.mean(per))
     tokens_per_s = total / (avg_ms / 1e3)
     achieved_gbs = total * PREFILL_BYTES_PER_TOKEN / (avg_ms / 1e3) / 1e9
@@ -166,7 +189,7 @@ def main(argv=None) -> int:
                    "kernel_ms": round(avg_ms, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None,
+                     "traffic": MEASURED_TRAFFIC_BYTES["prefill"],
                      "kernel": "kda_chunk_prep + kda_chunk_intra + kda_chunk_scan (one call)",
                      "algorithmic_bytes_per_launch": total * PREFILL_BYTES_PER_TOKEN},
         "mfma": {"achieved_tflops": round(tflops, 2), "peak_tflops": BF16_PEAK_TFLOPS,
@@ -179,6 +202,10 @@ def main(argv=None) -> int:
         print("non-finite prefill output", file=sys.stderr)
         return 1
 
+    if not run_prefill:
+        for key in ("value", "ms_per_step", "roofline", "mfma"):
+            result.pop(key, None)
+
     # ShortConv over the same packed batch (3 x 2048 channels, bf16).
     gen = torch.Generator().manual_seed(2)
     xconv = torch.randn((total, 3 * HEADS * DIM), generator=gen).to(torch.bfloat16).to(dev)
@@ -190,11 +217,14 @@ def main(argv=None) -> int:
         ops.short_conv_fwd(xconv, wconv, inp["cu"], conv_state=conv_state, read_history=False,
                            write_history=True, out=yconv)
 
-    _, cper = time_events(torch, conv, args.steps, args.warmup, stream)
-    cms = float(np.mean(cper))
-    cbytes = total * 3 * HEADS * DIM * 2 * 2
-    result["short_conv"] = {"us": round(cms * 1e3, 2), "GBps": round(cbytes / (cms / 1e3) / 1e9, 1),
-                            "algorithmic_bytes": cbytes}
+    if args.only in ("all", "conv"):
+        _, cper = time_events(torch, conv, args.steps, args.warmup, stream)
+        cms = float(np.mean(cper))
+        cbytes = total * 3 * HEADS * DIM * 2 * 2
+        result["short_conv"] = {"us": round(cms * 1e3, 2),
+                                "GBps": round(cbytes / (cms / 1e3) / 1e9, 1),
+                                "algorithmic_bytes": cbytes,
+                                "traffic": MEASURED_TRAFFIC_BYTES["short_conv"]}
     del xconv, yconv, conv_state
 
     # Decode step at B = 256.
@@ -213,18 +243,24 @@ def main(argv=None) -> int:
         ops.kda_decode_step(dq, dk, dv, dg, db, dstate, use_gate=False, use_beta_sigmoid=False,
                             out=dout)
 
-    dsteps = max(args.steps * 5, 50)
-    _, dper = time_events(torch, decode, dsteps, args.warmup * 2, stream)
-    dms = float(np.mean(dper))
-    dbytes = 2 * batch * HEADS * DIM * DIM * 4 + batch * HEADS * (3 * DIM * 2 + DIM * 4 + 4 + DIM * 2)
-    dgbs = dbytes / (dms / 1e3) / 1e9
-    result["decode"] = {"batch": batch, "us_per_step": round(dms * 1e3, 2),
-                        "GBps": round(dgbs, 1), "frac_of_hbm_peak": round(dgbs / HBM_PEAK_GBS, 4),
-                        "algorithmic_bytes": dbytes, "steps": dsteps,
-                        "kernel": "kda_decode_kernel"}
+    if args.only in ("all", "decode"):
+        dsteps = max(args.steps * 5, 50)
+        _, dper = time_events(torch, decode, dsteps, args.warmup * 2, stream)
+        dms = float(np.mean(dper))
+        dbytes = (2 * batch * HEADS * DIM * DIM * 4
+                  + batch * HEADS * (3 * DIM * 2 + DIM * 4 + 4 + DIM * 2))
+        dgbs = dbytes / (dms / 1e3) / 1e9
+        result["decode"] = {"batch": batch, "us_per_step": round(dms * 1e3, 2),
+                            "GBps": round(dgbs, 1),
+                            "frac_of_hbm_peak": round(dgbs / HBM_PEAK_GBS, 4),
+                            "algorithmic_bytes": dbytes, "steps": dsteps,
+                            "traffic": MEASURED_TRAFFIC_BYTES["decode"],
+                            "kernel": "kda_decode_kernel"}
     del dstate
 
-    if not args.no_cpu:
+    if args.only == "all":
+        result["hbm_copy_GBps"] = round(copy_bandwidth(torch, dev, stream), 1)
+    if not args.no_cpu and args.only == "all":
         result["cpu_baseline"] = cpu_baseline(inp, lengths)
     else:
         result["cpu_baseline"] = None

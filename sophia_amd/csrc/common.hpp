@@ -52,6 +52,16 @@ __device__ __forceinline__ float load_elem(const void *base, int64_t idx, int dt
   return static_cast<const float *>(base)[idx];
 }
 
+// Loads one element of either dtype as raw bits (bf16 zero-extended), to be
+// converted with raw_to_f32 once the loads of a batch have been issued.
+__device__ __forceinline__ uint32_t load_raw(const void *base, int64_t idx, int dtype) {
+  if (dtype == SOPHIA_DTYPE_BF16) return static_cast<const uint16_t *>(base)[idx];
+  return static_cast<const uint32_t *>(base)[idx];
+}
+__device__ __forceinline__ float raw_to_f32(uint32_t raw, int dtype) {
+  return __uint_as_float(dtype == SOPHIA_DTYPE_BF16 ? (raw << 16) : raw);
+}
+
 // Loads 4 consecutive elements (idx multiple of 4) as floats.
 __device__ __forceinline__ f4 load4(const void *base, int64_t idx, int dtype) {
   if (dtype == SOPHIA_DTYPE_BF16) {
@@ -83,6 +93,15 @@ __device__ __forceinline__ void store_elem(void *base, int64_t idx, int dtype, f
     static_cast<uint16_t *>(base)[idx] = f32_to_bf16_bits(v);
   else
     static_cast<float *>(base)[idx] = v;
+}
+
+// ---------------------------------------------------------------- integers
+// Integer min / max / clamp.  (Unqualified min/max with explicit template
+// arguments resolve to the HIP math overloads, which compute in double.)
+__host__ __device__ __forceinline__ int64_t imin64(int64_t a, int64_t b) { return a < b ? a : b; }
+__host__ __device__ __forceinline__ int64_t imax64(int64_t a, int64_t b) { return a > b ? a : b; }
+__host__ __device__ __forceinline__ int64_t iclamp64(int64_t v, int64_t lo, int64_t hi) {
+  return imin64(imax64(v, lo), hi);
 }
 
 // ---------------------------------------------------------------- math

@@ -98,8 +98,8 @@ __global__ __launch_bounds__(256) void kda_chunk_prep_kernel(const int32_t *__re
   const int per = (n + 255) / 256;
   const int s0 = min(n, t * per), s1 = min(n, s0 + per);
   auto nchunks = [&](int s) -> int32_t {
-    int64_t a = min<int64_t>(max<int64_t>(cu[s], 0), total);
-    int64_t b = min<int64_t>(max<int64_t>(cu[s + 1], a), total);
+    int64_t a = iclamp64(cu[s], 0, total);
+    int64_t b = iclamp64(cu[s + 1], a, total);
     return static_cast<int32_t>((b - a + kC - 1) / kC);
   };
   int32_t sum = 0;
@@ -186,6 +186,30 @@ __device__ __forceinline__ u2 pack4_bf16(f4 v) {
   return u2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
 }
 
+// Four consecutive elements as loaded from memory (bf16 pairs or fp32),
+// converted to fp32 only when used, so that loads can be batched.
+template <int DT>
+struct Raw4;
+template <>
+struct Raw4<SOPHIA_DTYPE_BF16> {
+  u2 w;
+  __device__ __forceinline__ void load(const void *base, int64_t idx) {
+    w = *reinterpret_cast<const u2 *>(static_cast<const uint16_t *>(base) + idx);
+  }
+  __device__ __forceinline__ f4 get() const {
+    return f4{__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
+              __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u)};
+  }
+};
+template <>
+struct Raw4<SOPHIA_DTYPE_F32> {
+  f4 w;
+  __device__ __forceinline__ void load(const void *base, int64_t idx) {
+    w = *reinterpret_cast<const f4 *>(static_cast<const float *>(base) + idx);
+  }
+  __device__ __forceinline__ f4 get() const { return w; }
+};
+
 template <int QKV_DT, int G_DT>
 __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -201,13 +225,13 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
 
   const int c = blockIdx.x;
   const int h = blockIdx.y;
-  const int nch = min<int64_t>(p.chunk_start[p.n_seqs], p.max_ch);
+  const int nch = imin64(p.chunk_start[p.n_seqs], p.max_ch);
   if (c >= nch) return;
   const int s = p.chunk_seq[c];
-  const int64_t seq_a = min<int64_t>(max<int64_t>(p.cu[s], 0), p.total);
-  const int64_t seq_b = min<int64_t>(max<int64_t>(p.cu[s + 1], seq_a), p.total);
+  const int64_t seq_a = iclamp64(p.cu[s], 0, p.total);
+  const int64_t seq_b = iclamp64(p.cu[s + 1], seq_a, p.total);
   const int64_t t0 = seq_a + static_cast<int64_t>(c - p.chunk_start[s]) * kC;
-  const int len = static_cast<int>(min<int64_t>(kC, seq_b - t0));
+  const int len = static_cast<int>(imin64(kC, seq_b - t0));
 
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave = 16-row sub-block (uniform)
@@ -220,37 +244,63 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
   uint8_t *rec = p.records + (static_cast<size_t>(c) * p.num_heads + h) * kRecBytes;
 
   // ---- 1. load q, k, g (32 channels per lane, 16x16x32 operand order), v, beta.
-  // Slot (ks, e) of a lane holds channel perm_k(ks, gq, e).
+  // Slot (ks, e) of a lane holds channel perm_k(ks, gq, e).  Every global load
+  // of the block is issued before the first use, so the block pays one memory
+  // round trip; rows past the end of the sequence load row t0 (always inside
+  // it) and are zeroed afterwards.
   float qv[32], kv[32], gv[32];
   float bt = 0.f;
-  if (valid) {
-    bt = load_elem(p.beta, tok * p.beta_stride + h, p.beta_dtype);
-    if (p.flags & SOPHIA_KDA_BETA_SIGMOID) bt = fast_sigmoid(bt);
-  }
   {
-    const int64_t qrow = tok * p.qkv_stride + static_cast<int64_t>(h) * kD;
-    const int64_t grow = tok * p.g_stride + static_cast<int64_t>(h) * kD;
+    const int64_t ltok = valid ? tok : t0;
+    const int64_t qrow = ltok * p.qkv_stride + static_cast<int64_t>(h) * kD;
+    const int64_t grow = ltok * p.g_stride + static_cast<int64_t>(h) * kD;
+    // Gate parameters and beta are issued first (memory returns in issue
+    // order), and beta is kept as raw bits until after the loads: converting
+    // it inside the dtype branch would make the wave wait right there.
+    const bool gate = (p.flags & SOPHIA_KDA_GATE_IN_KERNEL) != 0;
+    float hs = 1.f;
+    f4 rb[8];
+    if (gate) {
+      hs = p.A_log[h];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
+      for (int i = 0; i < 8; ++i)
+        rb[i] = *reinterpret_cast<const f4 *>(p.dt_bias + h * kD + 32 * (i >> 1) + 16 * (i & 1) + 4 * gq);
+    }
+    uint32_t braw;
+    const int64_t bidx = ltok * p.beta_stride + h;
+    if (p.beta_dtype == SOPHIA_DTYPE_BF16)
+      braw = static_cast<const uint16_t *>(p.beta)[bidx];
+    else
+      braw = static_cast<const uint32_t *>(p.beta)[bidx];
+    Raw4<QKV_DT> rq[8], rk[8], rv[8];
+    Raw4<G_DT> rg[8];
 #pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        const int ch = 32 * ks + 16 * hf + 4 * gq;
-        f4 a = {0.f, 0.f, 0.f, 0.f}, b = a, cc = a, d = a;
-        if (valid) {
-          a = load4(p.q, qrow + ch, QKV_DT);
-          b = load4(p.k, qrow + ch, QKV_DT);
-          cc = load4(p.v, qrow + ch, QKV_DT);
-          d = load4(p.g, grow + ch, G_DT);
-        }
+    for (int i = 0; i < 8; ++i) {
+      const int ch = 32 * (i >> 1) + 16 * (i & 1) + 4 * gq;
+      rq[i].load(p.q, qrow + ch);
+      rk[i].load(p.k, qrow + ch);
+      rv[i].load(p.v, qrow + ch);
+      rg[i].load(p.g, grow + ch);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (valid) {
+      bt = __uint_as_float(p.beta_dtype == SOPHIA_DTYPE_BF16 ? (braw << 16) : braw);
+      if (p.flags & SOPHIA_KDA_BETA_SIGMOID) bt = fast_sigmoid(bt);
+    }
+    if (gate) hs = __expf(hs);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int e = 8 * ks + 4 * hf + i;
-          qv[e] = a[i];
-          kv[e] = b[i];
-          gv[e] = d[i];
-          sV[swz(ch + i, row)] = f32_to_bf16_bits(bt * cc[i]);   // beta V, transposed
-        }
+    for (int i = 0; i < 8; ++i) {
+      const int ch = 32 * (i >> 1) + 16 * (i & 1) + 4 * gq;
+      const f4 a = rq[i].get(), b = rk[i].get(), cc = rv[i].get(), d = rg[i].get();
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int e = 4 * i + j;
+        qv[e] = valid ? a[j] : 0.f;
+        kv[e] = valid ? b[j] : 0.f;
+        gv[e] = valid ? (gate ? p.lb * fast_sigmoid(hs * (d[j] + rb[i][j])) : d[j]) : 0.f;
+        sV[swz(ch + j, row)] = f32_to_bf16_bits(bt * cc[j]);   // beta V, transposed
       }
+    }
   }
 
   // ---- 2. l2 norms (a row is spread over the 4 lane groups), gate
@@ -274,21 +324,6 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
     for (int e = 0; e < 32; ++e) {
       qv[e] *= qs;
       kv[e] *= ksc;
-    }
-    if (p.flags & SOPHIA_KDA_GATE_IN_KERNEL) {
-      const float hs = __expf(p.A_log[h]);
-      const float *bias = p.dt_bias + h * kD;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          const f4 bv = *reinterpret_cast<const f4 *>(bias + 32 * ks + 16 * hf + 4 * gq);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int e = 8 * ks + 4 * hf + i;
-            gv[e] = valid ? p.lb * fast_sigmoid(hs * (gv[e] + bv[i])) : 0.f;
-          }
-        }
     }
   }
 
@@ -596,6 +631,100 @@ __device__ __forceinline__ void load_frags(ScanFrags<NT> &f, const uint8_t *rec,
   for (int mi = 0; mi < 2; ++mi) f.gm[mi] = *reinterpret_cast<const f4 *>(&gam[32 * w + 16 * mi + 4 * gq]);
 }
 
+// Makes the wave wait for the loads of `f` here: an empty asm statement that
+// reads every register of the buffer.
+template <int NT>
+__device__ __forceinline__ void touch_frags(const ScanFrags<NT> &f) {
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) asm volatile("" ::"v"(f.wn[ks]), "v"(f.qb[ks]));
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) asm volatile("" ::"v"(f.aq[ks]), "v"(f.kt[0][ks]), "v"(f.kt[1][ks]));
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) asm volatile("" ::"v"(f.ut[nt]));
+  asm volatile("" ::"v"(f.gm[0]), "v"(f.gm[1]));
+}
+
+// One chunk of the state scan for the 4 wavefronts of a block: U = Ut - W S,
+// O = (Q e^G) S + A_qk U (stored), S = Diag(e^{G_C}) S + Kbar^T U.  Wave w
+// owns chunk rows 16w..16w+15 of U and O and state rows 32w..32w+31; S and U
+// are exchanged between the waves as bf16 B operands in LDS.
+template <int NT, int O_DT>
+__device__ __forceinline__ void scan_step(const ScanArgs &p, const ScanFrags<NT> &cur, f4 (&S)[2][NT],
+                                          uint8_t *sSb, uint8_t *sUb, int w, int l, int gq, int nt0,
+                                          int h, int64_t seq_a, int64_t seq_b, int cc) {
+  const int lr = l & 15;
+  // 1. publish this wave's state rows as K-step w of the bf16 B operand.
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    float t[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      t[e] = S[0][nt][e];
+      t[4 + e] = S[1][nt][e];
+    }
+    *reinterpret_cast<u4 *>(sSb + ((w * NT + nt) * 64 + l) * 16) = bf8_to_bits(pack8(t));
+  }
+  lds_barrier();
+
+  // 2. U = Ut - W S and O = (Q e^G) S for chunk rows 16w..16w+15.
+  f4 U[NT], O[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    bf8 sb[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      sb[ks] = bits_to_bf8(*reinterpret_cast<const u4 *>(sSb + ((ks * NT + nt) * 64 + l) * 16));
+    const u2 uw = cur.ut[nt];
+    f4 u = {__uint_as_float(uw.x << 16), __uint_as_float(uw.x & 0xffff0000u),
+            __uint_as_float(uw.y << 16), __uint_as_float(uw.y & 0xffff0000u)};
+    f4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      u = mfma32(bits_to_bf8(cur.wn[ks]), sb[ks], u);
+      o = mfma32(bits_to_bf8(cur.qb[ks]), sb[ks], o);
+    }
+    U[nt] = u;
+    O[nt] = o;
+  }
+  // 3. publish U rows 16w.. as half (w & 1) of K-step w/2 of the U operand.
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+    *reinterpret_cast<u2 *>(sUb + (((w >> 1) * NT + nt) * 64 + l) * 16 + (w & 1) * 8) = pack4_bf16(U[nt]);
+  lds_barrier();
+
+  // 4. O += A_qk U (A_qk is lower triangular: K-steps <= w/2);
+  //    S = Diag(e^{G_C}) S + Kbar^T U.
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    bf8 ub[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+      ub[ks] = bits_to_bf8(*reinterpret_cast<const u4 *>(sUb + ((ks * NT + nt) * 64 + l) * 16));
+    O[nt] = mfma32(bits_to_bf8(cur.aq[0]), ub[0], O[nt]);
+    if (w >= 2) O[nt] = mfma32(bits_to_bf8(cur.aq[1]), ub[1], O[nt]);
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi) {
+      f4 sv = S[mi][nt] * cur.gm[mi];
+      sv = mfma32(bits_to_bf8(cur.kt[mi][0]), ub[0], sv);
+      sv = mfma32(bits_to_bf8(cur.kt[mi][1]), ub[1], sv);
+      S[mi][nt] = sv;
+    }
+  }
+
+  // 5. store O for the valid rows of the chunk.
+  const int64_t tok0 = seq_a + static_cast<int64_t>(cc) * kC;
+  const int rows_valid = static_cast<int>(imin64(kC, seq_b - tok0));
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int r = 16 * w + 4 * gq + e;
+    if (r < rows_valid) {
+      const int64_t base = (tok0 + r) * p.o_stride + static_cast<int64_t>(h) * kD + 16 * nt0 + lr;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) store_elem(p.o, base + 16 * nt, O_DT, O[nt][e]);
+    }
+  }
+}
+
 // One block of 4 wavefronts per (sequence, head, NVB value columns).  Wave w
 // owns chunk rows 16w..16w+15 of U and O and state rows 32w..32w+31; the
 // state and U are exchanged between the waves as bf16 B operands in LDS.
@@ -618,9 +747,9 @@ __global__ __launch_bounds__(kThreads, 1) void kda_chunk_scan_kernel(ScanArgs p)
   const int s = sh / p.num_heads;
   if (s >= p.n_seqs) return;
   const int nt0 = half * NT;                  // first 16-column tile of this block
-  const int64_t seq_a = min<int64_t>(max<int64_t>(p.cu[s], 0), p.total);
-  const int64_t seq_b = min<int64_t>(max<int64_t>(p.cu[s + 1], seq_a), p.total);
-  const int nchunks = static_cast<int>(min<int64_t>((seq_b - seq_a + kC - 1) / kC,
+  const int64_t seq_a = iclamp64(p.cu[s], 0, p.total);
+  const int64_t seq_b = iclamp64(p.cu[s + 1], seq_a, p.total);
+  const int nchunks = static_cast<int>(imin64((seq_b - seq_a + kC - 1) / kC,
                                                     p.max_ch - p.chunk_start[s]));
   const int cbase = p.chunk_start[s];
   const int slot = p.slots ? p.slots[s] : s;
@@ -643,86 +772,31 @@ __global__ __launch_bounds__(kThreads, 1) void kda_chunk_scan_kernel(ScanArgs p)
       S[mi][nt] = v;
     }
 
-  ScanFrags<NT> cur, nxt;
-  if (nchunks > 0)
-    load_frags<NT>(cur, p.records + (static_cast<size_t>(cbase) * p.num_heads + h) * kRecBytes, w, l,
-                   gq, nt0);
-  for (int cc = 0; cc < nchunks; ++cc) {
-    if (cc + 1 < nchunks)
-      load_frags<NT>(nxt, p.records + (static_cast<size_t>(cbase + cc + 1) * p.num_heads + h) * kRecBytes,
-                     w, l, gq, nt0);
-
-    // 1. publish this wave's state rows as K-step w of the bf16 B operand.
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      float t[8];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        t[e] = S[0][nt][e];
-        t[4 + e] = S[1][nt][e];
-      }
-      *reinterpret_cast<u4 *>(sSb + ((w * NT + nt) * 64 + l) * 16) = bf8_to_bits(pack8(t));
+  // Two operand buffers in ping-pong order: the loads of chunk cc + 2 are
+  // issued as soon as chunk cc has been consumed, so each load has a whole
+  // chunk step of the other buffer to complete, and no buffer is ever copied
+  // (a copy would wait for the loads in flight).
+  const uint8_t *rec0 = p.records + (static_cast<size_t>(cbase) * p.num_heads + h) * kRecBytes;
+  const size_t rec_stride = static_cast<size_t>(p.num_heads) * kRecBytes;
+  // Buffer fa is waited for at the end of the previous iteration (touch_frags),
+  // where only the younger loads of fb are in flight; a wait placed by the
+  // compiler at the loop header would also drain fb.  Loads are never under
+  // a branch (a branch makes the compiler drain every load at the join):
+  // past the last chunk they re-read the last chunk and go unused.
+  if (nchunks > 0) {
+    const int last = nchunks - 1;
+    ScanFrags<NT> fa, fb;
+    load_frags<NT>(fa, rec0, w, l, gq, nt0);
+    load_frags<NT>(fb, rec0 + min(1, last) * rec_stride, w, l, gq, nt0);
+    touch_frags<NT>(fa);
+    for (int cc = 0; cc < nchunks; cc += 2) {
+      scan_step<NT, O_DT>(p, fa, S, sSb, sUb, w, l, gq, nt0, h, seq_a, seq_b, cc);
+      load_frags<NT>(fa, rec0 + min(cc + 2, last) * rec_stride, w, l, gq, nt0);
+      if (cc + 1 < nchunks)
+        scan_step<NT, O_DT>(p, fb, S, sSb, sUb, w, l, gq, nt0, h, seq_a, seq_b, cc + 1);
+      load_frags<NT>(fb, rec0 + min(cc + 3, last) * rec_stride, w, l, gq, nt0);
+      touch_frags<NT>(fa);
     }
-    lds_barrier();
-
-    // 2. U = Ut - W S and O = (Q e^G) S for chunk rows 16w..16w+15.
-    f4 U[NT], O[NT];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      bf8 sb[4];
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        sb[ks] = bits_to_bf8(*reinterpret_cast<const u4 *>(sSb + ((ks * NT + nt) * 64 + l) * 16));
-      const u2 uw = cur.ut[nt];
-      f4 u = {__uint_as_float(uw.x << 16), __uint_as_float(uw.x & 0xffff0000u),
-              __uint_as_float(uw.y << 16), __uint_as_float(uw.y & 0xffff0000u)};
-      f4 o = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        u = mfma32(bits_to_bf8(cur.wn[ks]), sb[ks], u);
-        o = mfma32(bits_to_bf8(cur.qb[ks]), sb[ks], o);
-      }
-      U[nt] = u;
-      O[nt] = o;
-    }
-    // 3. publish U rows 16w.. as half (w & 1) of K-step w/2 of the U operand.
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
-      *reinterpret_cast<u2 *>(sUb + (((w >> 1) * NT + nt) * 64 + l) * 16 + (w & 1) * 8) = pack4_bf16(U[nt]);
-    lds_barrier();
-
-    // 4. O += A_qk U (A_qk is lower triangular: K-steps <= w/2);
-    //    S = Diag(e^{G_C}) S + Kbar^T U.
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      bf8 ub[2];
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        ub[ks] = bits_to_bf8(*reinterpret_cast<const u4 *>(sUb + ((ks * NT + nt) * 64 + l) * 16));
-      O[nt] = mfma32(bits_to_bf8(cur.aq[0]), ub[0], O[nt]);
-      if (w >= 2) O[nt] = mfma32(bits_to_bf8(cur.aq[1]), ub[1], O[nt]);
-#pragma unroll
-      for (int mi = 0; mi < 2; ++mi) {
-        f4 sv = S[mi][nt] * cur.gm[mi];
-        sv = mfma32(bits_to_bf8(cur.kt[mi][0]), ub[0], sv);
-        sv = mfma32(bits_to_bf8(cur.kt[mi][1]), ub[1], sv);
-        S[mi][nt] = sv;
-      }
-    }
-
-    // 5. store O for the valid rows of the chunk.
-    const int64_t tok0 = seq_a + static_cast<int64_t>(cc) * kC;
-    const int rows_valid = static_cast<int>(min<int64_t>(kC, seq_b - tok0));
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int r = 16 * w + 4 * gq + e;
-      if (r < rows_valid) {
-        const int64_t base = (tok0 + r) * p.o_stride + static_cast<int64_t>(h) * kD + 16 * nt0 + lr;
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) store_elem(p.o, base + 16 * nt, O_DT, O[nt][e]);
-      }
-    }
-    if (cc + 1 < nchunks) cur = nxt;
   }
 
   if (p.ht && has_slot) {
@@ -751,6 +825,16 @@ int launch_intra(dim3 grid, hipStream_t st, const IntraArgs &ia) {
   }
   hipLaunchKernelGGL((kda_chunk_intra_kernel<QKV_DT, G_DT>), grid, dim3(kThreads), kSmIntra, st, ia);
   return check_launch("kda_chunk_intra");
+}
+
+template <int O_DT>
+void launch_scan(int splits, dim3 grid, hipStream_t st, const ScanArgs &sa) {
+  switch (splits) {
+    case 1: hipLaunchKernelGGL((kda_chunk_scan_kernel<128, O_DT>), grid, dim3(kThreads), 0, st, sa); break;
+    case 2: hipLaunchKernelGGL((kda_chunk_scan_kernel<64, O_DT>), grid, dim3(kThreads), 0, st, sa); break;
+    case 4: hipLaunchKernelGGL((kda_chunk_scan_kernel<32, O_DT>), grid, dim3(kThreads), 0, st, sa); break;
+    default: hipLaunchKernelGGL((kda_chunk_scan_kernel<16, O_DT>), grid, dim3(kThreads), 0, st, sa); break;
+  }
 }
 
 }  // namespace
@@ -830,29 +914,25 @@ extern "C" int sophia_kda_chunk_fwd(const void *q, const void *k, const void *v,
       rc = launch_intra<SOPHIA_DTYPE_F32, SOPHIA_DTYPE_BF16>(grid, st, ia);
     if (rc) return rc;
   }
-  // Two blocks (64 value columns each) per (sequence, head) when the pairs
-  // alone would leave CUs idle; one block of 128 columns otherwise.
+  // The state scan is sequential over the chunks of a sequence: split the 128
+  // value columns of each (sequence, head) over 1, 2, 4 or 8 blocks until the
+  // grid holds about two blocks per CU, so that short batches still spread
+  // the critical path over the chip.
   int device = 0, cus = 256;
   if (hipGetDevice(&device) == hipSuccess)
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) cus = 256;
   const int64_t pairs = static_cast<int64_t>(n_seqs) * num_heads;
-  const int splits = pairs < cus ? 2 : 1;
+  int splits = 1;
+  while (splits < 8 && pairs * splits < 2 * static_cast<int64_t>(cus)) splits *= 2;
   ScanArgs sa{cu_seqlens, n_seqs, total_tokens, num_heads, max_ch, chunk_start, records,
               initial_state, final_state, n_state_slots, state_slots, o, o_row_stride, splits};
   const int64_t groups = (pairs + 7) / 8;
   const int64_t blocks = groups * 8 * splits;
   SOPHIA_REQUIRE(blocks <= 0x7fffffff, "kda_chunk_fwd: grid too large");
   const dim3 sgrid(static_cast<unsigned>(blocks));
-  if (qkv_dtype == SOPHIA_DTYPE_BF16) {
-    if (splits == 2)
-      hipLaunchKernelGGL((kda_chunk_scan_kernel<64, SOPHIA_DTYPE_BF16>), sgrid, dim3(kThreads), 0, st, sa);
-    else
-      hipLaunchKernelGGL((kda_chunk_scan_kernel<128, SOPHIA_DTYPE_BF16>), sgrid, dim3(kThreads), 0, st, sa);
-  } else {
-    if (splits == 2)
-      hipLaunchKernelGGL((kda_chunk_scan_kernel<64, SOPHIA_DTYPE_F32>), sgrid, dim3(kThreads), 0, st, sa);
-    else
-      hipLaunchKernelGGL((kda_chunk_scan_kernel<128, SOPHIA_DTYPE_F32>), sgrid, dim3(kThreads), 0, st, sa);
-  }
+  if (qkv_dtype == SOPHIA_DTYPE_BF16)
+    launch_scan<SOPHIA_DTYPE_BF16>(splits, sgrid, st, sa);
+  else
+    launch_scan<SOPHIA_DTYPE_F32>(splits, sgrid, st, sa);
   return check_launch("kda_chunk_scan");
 }

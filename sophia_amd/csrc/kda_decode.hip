@@ -23,10 +23,14 @@ constexpr int kD = 128;
 constexpr int kThreads = 256;
 constexpr int kRowsPerThread = kD / 8;
 
+// Dtypes and the gate switch are template parameters so that the load batch
+// below has no branches: the wave then waits for the token inputs alone
+// (issued first) before the prologue, while the state is still in flight.
+template <int QKV_DT, int G_DT, int B_DT, bool GATE>
 __global__ __launch_bounds__(kThreads) void kda_decode_kernel(
     const void *__restrict__ q, const void *__restrict__ k, const void *__restrict__ v,
-    int64_t qkv_stride, int qkv_dtype, const void *__restrict__ g, int64_t g_stride, int g_dtype,
-    const void *__restrict__ beta, int64_t beta_stride, int beta_dtype,
+    int64_t qkv_stride, const void *__restrict__ g, int64_t g_stride,
+    const void *__restrict__ beta, int64_t beta_stride,
     const float *__restrict__ A_log, const float *__restrict__ dt_bias, float scale, float lb,
     unsigned flags, float *__restrict__ state, int n_slots, const int32_t *__restrict__ slots,
     int read_state, int num_heads, void *__restrict__ o, int64_t o_stride) {
@@ -38,7 +42,7 @@ __global__ __launch_bounds__(kThreads) void kda_decode_kernel(
   const int cg = t & 31;         // column group: columns 4cg .. 4cg+3
   const int rg = t >> 5;         // row group: rows rg + 8r
 
-  __shared__ float s_q[kD], s_k[kD], s_a[kD], s_v[kD];
+  __shared__ float s_q[kD], s_k[kD], s_a[kThreads], s_v[kThreads];
   __shared__ float s_red[4][3];
   __shared__ float s_p[4][kD], s_r[4][kD];
   __shared__ float s_u[kD];
@@ -47,35 +51,51 @@ __global__ __launch_bounds__(kThreads) void kda_decode_kernel(
   if (slot < 0 || slot >= n_slots) {  // no cache slot: output 0, no state touched
     if (t < kD)
       store_elem(o, static_cast<int64_t>(b) * o_stride + static_cast<int64_t>(h) * kD + t,
-                 qkv_dtype, 0.f);
+                 QKV_DT, 0.f);
     return;
   }
   float *S = state + (static_cast<int64_t>(slot) * num_heads + h) * kD * kD;
 
-  // Issue the state loads first: they do not depend on the token prologue.
-  f4 st[kRowsPerThread];
-  if (read_state) {
-#pragma unroll
-    for (int r = 0; r < kRowsPerThread; ++r)
-      st[r] = __builtin_nontemporal_load(
-          reinterpret_cast<const f4 *>(S + (rg + 8 * r) * kD + 4 * cg));
-  } else {
-#pragma unroll
-    for (int r = 0; r < kRowsPerThread; ++r) st[r] = f4{0.f, 0.f, 0.f, 0.f};
+  // Every load of the block is issued before the first use: the token inputs
+  // as raw bits (a dtype conversion inside the dtype branch would make the
+  // wave wait there), then the 64 KB state.  One memory round trip per block.
+  const int64_t row = static_cast<int64_t>(b) * qkv_stride + static_cast<int64_t>(h) * kD;
+  const int64_t grow = static_cast<int64_t>(b) * g_stride + static_cast<int64_t>(h) * kD;
+  const int c = t & (kD - 1);   // threads 128..255 load the same channels again
+  const uint32_t raw_q = load_raw(q, row + c, QKV_DT);
+  const uint32_t raw_k = load_raw(k, row + c, QKV_DT);
+  const uint32_t raw_v = load_raw(v, row + c, QKV_DT);
+  const uint32_t raw_g = load_raw(g, grow + c, G_DT);
+  const uint32_t raw_b = load_raw(beta, static_cast<int64_t>(b) * beta_stride + h, B_DT);
+  float alog = 0.f, bias = 0.f;
+  if constexpr (GATE) {
+    bias = dt_bias[h * kD + c];
+    alog = A_log[h];
   }
+  // Compiler-only fence: keeps the token loads issued ahead of the state
+  // loads (memory returns in issue order, and the prologue needs only them).
+  asm volatile("" ::: "memory");
+  // The state is loaded unconditionally (a branch here would make the wave
+  // drain every load at the join) and replaced by zeros afterwards when the
+  // incoming state is to be ignored.
+  f4 st[kRowsPerThread];
+#pragma unroll
+  for (int r = 0; r < kRowsPerThread; ++r)
+    st[r] = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(S + (rg + 8 * r) * kD + 4 * cg));
+  __builtin_amdgcn_sched_barrier(0);
 
   // Token prologue: threads 0..127 own one key/value channel each.
-  const int64_t row = static_cast<int64_t>(b) * qkv_stride + static_cast<int64_t>(h) * kD;
-  float qv = 0.f, kv = 0.f;
-  if (t < kD) {
-    qv = load_elem(q, row + t, qkv_dtype);
-    kv = load_elem(k, row + t, qkv_dtype);
-    float gv = load_elem(g, static_cast<int64_t>(b) * g_stride + static_cast<int64_t>(h) * kD + t,
-                         g_dtype);
-    if (flags & SOPHIA_KDA_GATE_IN_KERNEL) gv = kda_log_decay(gv, __expf(A_log[h]), dt_bias[h * kD + t], lb);
-    s_a[t] = __expf(gv);
-    s_v[t] = load_elem(v, row + t, qkv_dtype);
-  }
+  // Computed by every thread (selects, not branches: a load used only under
+  // a branch would be sunk into it, behind the state loads).
+  const bool own = t < kD;
+  const float qv = own ? raw_to_f32(raw_q, QKV_DT) : 0.f;
+  const float kv = own ? raw_to_f32(raw_k, QKV_DT) : 0.f;
+  float gv = raw_to_f32(raw_g, G_DT);
+  if constexpr (GATE) gv = kda_log_decay(gv, __expf(alog), bias, lb);
+  const float av = __expf(gv);
+  const float vv = raw_to_f32(raw_v, QKV_DT);
+  s_a[t] = av;   // threads 128..255 write the unused upper halves
+  s_v[t] = vv;
   float sq = wave_sum(qv * qv), sk = wave_sum(kv * kv), sqk = wave_sum(qv * kv);
   if (lane == 0) {
     s_red[wave][0] = sq;
@@ -91,13 +111,18 @@ __global__ __launch_bounds__(kThreads) void kda_decode_kernel(
     ks = 1.f / fmaxf(nk, 1e-12f);
   }
   const float qk = (s_red[0][2] + s_red[1][2]) * qs * ks;
-  float bt = load_elem(beta, static_cast<int64_t>(b) * beta_stride + h, beta_dtype);
+  float bt = raw_to_f32(raw_b, B_DT);
   if (flags & SOPHIA_KDA_BETA_SIGMOID) bt = sigmoid_f(bt);
   if (t < kD) {
     s_q[t] = qv * qs;
     s_k[t] = kv * ks;
   }
   lds_barrier();
+
+  if (!read_state) {
+#pragma unroll
+    for (int r = 0; r < kRowsPerThread; ++r) st[r] = f4{0.f, 0.f, 0.f, 0.f};
+  }
 
   // Decay the held rows and form the two partial column reductions.
   f4 p = {0.f, 0.f, 0.f, 0.f}, rq = {0.f, 0.f, 0.f, 0.f};
@@ -127,7 +152,7 @@ __global__ __launch_bounds__(kThreads) void kda_decode_kernel(
     const float rj = s_r[0][t] + s_r[1][t] + s_r[2][t] + s_r[3][t];
     const float u = bt * (s_v[t] - pj);
     s_u[t] = u;
-    store_elem(o, static_cast<int64_t>(b) * o_stride + static_cast<int64_t>(h) * kD + t, qkv_dtype,
+    store_elem(o, static_cast<int64_t>(b) * o_stride + static_cast<int64_t>(h) * kD + t, QKV_DT,
                rj + qk * u);
   }
   lds_barrier();
@@ -172,9 +197,36 @@ extern "C" int sophia_kda_decode_step(const void *q, const void *k, const void *
   SOPHIA_REQUIRE(((uintptr_t)state % 16) == 0, "kda_decode_step: state must be 16-byte aligned");
   SOPHIA_REQUIRE(n_state_slots >= 0, "kda_decode_step: n_state_slots must be >= 0");
   dim3 grid(num_heads, batch);
-  hipLaunchKernelGGL(kda_decode_kernel, grid, dim3(kThreads), 0, static_cast<hipStream_t>(stream),
-                     q, k, v, qkv_row_stride, qkv_dtype, g, g_row_stride, g_dtype, beta,
-                     beta_row_stride, beta_dtype, A_log, dt_bias, scale, lower_bound, flags, state,
-                     n_state_slots, state_slots, read_state, num_heads, o, o_row_stride);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool gate = (flags & SOPHIA_KDA_GATE_IN_KERNEL) != 0;
+  const int key = (qkv_dtype == SOPHIA_DTYPE_BF16) * 8 + (g_dtype == SOPHIA_DTYPE_BF16) * 4 +
+                  (beta_dtype == SOPHIA_DTYPE_BF16) * 2 + (gate ? 1 : 0);
+#define SOPHIA_DECODE_CASE(KEY, QD, GD, BD, GT)                                                  \
+  case KEY:                                                                                      \
+    hipLaunchKernelGGL((kda_decode_kernel<QD, GD, BD, GT>), grid, dim3(kThreads), 0, st, q, k, v, \
+                       qkv_row_stride, g, g_row_stride, beta, beta_row_stride, A_log, dt_bias,   \
+                       scale, lower_bound, flags, state, n_state_slots, state_slots, read_state, \
+                       num_heads, o, o_row_stride);                                              \
+    break;
+  constexpr int F = SOPHIA_DTYPE_F32, B = SOPHIA_DTYPE_BF16;
+  switch (key) {
+    SOPHIA_DECODE_CASE(0, F, F, F, false)
+    SOPHIA_DECODE_CASE(1, F, F, F, true)
+    SOPHIA_DECODE_CASE(2, F, F, B, false)
+    SOPHIA_DECODE_CASE(3, F, F, B, true)
+    SOPHIA_DECODE_CASE(4, F, B, F, false)
+    SOPHIA_DECODE_CASE(5, F, B, F, true)
+    SOPHIA_DECODE_CASE(6, F, B, B, false)
+    SOPHIA_DECODE_CASE(7, F, B, B, true)
+    SOPHIA_DECODE_CASE(8, B, F, F, false)
+    SOPHIA_DECODE_CASE(9, B, F, F, true)
+    SOPHIA_DECODE_CASE(10, B, F, B, false)
+    SOPHIA_DECODE_CASE(11, B, F, B, true)
+    SOPHIA_DECODE_CASE(12, B, B, F, false)
+    SOPHIA_DECODE_CASE(13, B, B, F, true)
+    SOPHIA_DECODE_CASE(14, B, B, B, false)
+    SOPHIA_DECODE_CASE(15, B, B, B, true)
+  }
+#undef SOPHIA_DECODE_CASE
   return check_launch("kda_decode_step");
 }

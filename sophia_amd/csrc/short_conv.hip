@@ -17,7 +17,6 @@ namespace sophia {
 namespace {
 
 constexpr int kVec = 8;        // channels per thread
-constexpr int kRows = 16;      // packed rows per thread
 constexpr int kVecsPerBlock = 64;
 constexpr int kRowTilesPerBlock = 4;
 
@@ -87,26 +86,23 @@ __device__ __forceinline__ int find_seq(const int32_t *cu, int n, int64_t row) {
   return lo;
 }
 
-// Loads the K-1 samples preceding packed row `row` of sequence `seq`
-// (prev[d-1] = sample at row - d) from x or from the history cache.
+// Packed rows per thread: the whole window of a thread (its rows plus the K-1
+// before them) is loaded before any arithmetic, so a thread pays one memory
+// round trip; fp32 rows are twice as wide, so fp32 threads take half as many.
+template <int DT>
+constexpr int rows_per_thread() { return DT == SOPHIA_DTYPE_BF16 ? 16 : 8; }
+
 template <int K, int DT>
-__device__ __forceinline__ void init_window(Vec8<DT> (&prev)[K > 1 ? K - 1 : 1], const void *x,
-                                            int64_t xs, const float *hist, int64_t row,
-                                            int64_t seq_start, int c0, int channels) {
+__device__ __forceinline__ Vec8<DT> conv_row(const float (&w)[kVec][K], const Vec8<DT> (&win)[K]) {
+  Vec8<DT> out;
 #pragma unroll
-  for (int d = 1; d < K; ++d) {
-    int64_t tau = row - d;
-    if (tau >= seq_start) {
-      prev[d - 1].load(x, tau * xs + c0);
-    } else if (hist != nullptr) {
-      int idx = (K - 1) + static_cast<int>(tau - seq_start);  // 0 .. K-2
+  for (int ci = 0; ci < kVec; ++ci) {
+    float acc = 0.f;
 #pragma unroll
-      for (int i = 0; i < kVec; ++i)
-        prev[d - 1].v[i] = as_input_dtype<DT>(hist[static_cast<int64_t>(c0 + i) * (K - 1) + idx]);
-    } else {
-      prev[d - 1].zero();
-    }
+    for (int j = 0; j < K; ++j) acc = fmaf(w[ci][j], win[j].v[ci], acc);
+    out.v[ci] = acc * sigmoid_f(acc);
   }
+  return out;
 }
 
 template <int K, int DT>
@@ -115,63 +111,78 @@ __global__ __launch_bounds__(256) void short_conv_fwd_kernel(
     const float *__restrict__ weight, const float *__restrict__ conv_state, int n_slots,
     const int32_t *__restrict__ slots, const int32_t *__restrict__ cu, int n_seqs, int64_t total,
     int channels, int read_history) {
+  constexpr int R = rows_per_thread<DT>();
+  constexpr int HL = K - 1;       // history length
+  constexpr int NR = R + HL;      // window rows r0 - HL .. r0 + R - 1
   const int cv = blockIdx.x * kVecsPerBlock + threadIdx.x;
   const int c0 = cv * kVec;
-  const int64_t r0 = (static_cast<int64_t>(blockIdx.y) * kRowTilesPerBlock + threadIdx.y) * kRows;
+  // threadIdx.y is constant over a wavefront (blockDim.x == 64): r0 and the
+  // sequence bookkeeping below are wave-uniform and read cu_seqlens through
+  // the scalar cache, off the vector-memory counter the window loads use.
+  const int ty = __builtin_amdgcn_readfirstlane(threadIdx.y);
+  const int64_t r0 = (static_cast<int64_t>(blockIdx.y) * kRowTilesPerBlock + ty) * R;
   if (c0 >= channels || r0 >= total) return;
-  const int64_t r1 = min(r0 + kRows, total);
-
+  const int64_t r1 = imin64(r0 + R, total);
+  // The window is loaded first, before the sequence lookup (whose scalar
+  // loads are a chain of dependent round trips); window rows are clamped into
+  // [0, total) and are used only when the whole window lies in one sequence.
+  Vec8<DT> win[NR];
+#pragma unroll
+  for (int j = 0; j < NR; ++j) win[j].load(x, iclamp64(r0 - HL + j, 0, total - 1) * xs + c0);
   float w[kVec][K];
 #pragma unroll
   for (int i = 0; i < kVec; ++i)
 #pragma unroll
     for (int j = 0; j < K; ++j) w[i][j] = weight[static_cast<int64_t>(c0 + i) * K + j];
-
   // Offsets are clamped to [0, total] and made monotone, so malformed
   // cu_seqlens can never move a read or write outside x, y or conv_state;
   // rows outside every sequence are left untouched.
   int s = find_seq(cu, n_seqs, r0);
   int64_t seq_start = 0, seq_end = 0;
   auto bounds = [&](int seq) {
-    seq_start = min<int64_t>(max<int64_t>(cu[seq], 0), total);
-    seq_end = min<int64_t>(max<int64_t>(cu[seq + 1], seq_start), total);
+    seq_start = iclamp64(cu[seq], 0, total);
+    seq_end = iclamp64(cu[seq + 1], seq_start, total);
   };
   bounds(s);
-  auto hist_of = [&](int seq) -> const float * {
-    if (!read_history || conv_state == nullptr || K == 1) return nullptr;
-    int slot = slots ? slots[seq] : seq;
-    if (slot < 0 || slot >= n_slots) return nullptr;
-    return conv_state + static_cast<int64_t>(slot) * channels * (K - 1);
-  };
-  Vec8<DT> prev[K > 1 ? K - 1 : 1];
-  bool fresh = true;  // the window must be (re)loaded before the next row
+
+  if (r0 - HL >= seq_start && r1 <= seq_end) {
+    // Fast path (almost every thread of a long-sequence batch): the window
+    // lies inside one sequence.
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      if (r0 + i >= r1) break;
+      Vec8<DT> taps[K];
+#pragma unroll
+      for (int j = 0; j < K; ++j) taps[j] = win[i + j];
+      conv_row<K, DT>(w, taps).store(y, (r0 + i) * ys + c0);
+    }
+    return;
+  }
+  // General path: rows near a sequence start (history or zeros before it) or
+  // windows that span several sequences.  Taps are reloaded per row.
   for (int64_t r = r0; r < r1; ++r) {
-    while (r >= seq_end && s + 1 < n_seqs) {
-      bounds(++s);
-      fresh = true;
+    while (r >= seq_end && s + 1 < n_seqs) bounds(++s);
+    if (r < seq_start || r >= seq_end) continue;
+    const float *hist = nullptr;
+    if (HL > 0 && r - seq_start < HL && read_history && conv_state != nullptr) {
+      const int slot = slots ? slots[s] : s;
+      if (slot >= 0 && slot < n_slots) hist = conv_state + static_cast<int64_t>(slot) * channels * HL;
     }
-    if (r < seq_start || r >= seq_end) {
-      fresh = true;
-      continue;
-    }
-    if (fresh) {
-      init_window<K, DT>(prev, x, xs, hist_of(s), r, seq_start, c0, channels);
-      fresh = false;
-    }
-    Vec8<DT> cur;
-    cur.load(x, r * xs + c0);
-    Vec8<DT> out;
+    Vec8<DT> taps[K];
 #pragma unroll
-    for (int i = 0; i < kVec; ++i) {
-      float acc = w[i][K - 1] * cur.v[i];
+    for (int j = 0; j < K; ++j) {
+      const int64_t tau = r - HL + j;      // taps[K-1] is the current row
+      if (tau >= seq_start) {
+        taps[j].load(x, tau * xs + c0);
+      } else if (hist != nullptr) {
 #pragma unroll
-      for (int d = 1; d < K; ++d) acc = fmaf(w[i][K - 1 - d], prev[d - 1].v[i], acc);
-      out.v[i] = acc * sigmoid_f(acc);
+        for (int ci = 0; ci < kVec; ++ci)
+          taps[j].v[ci] = as_input_dtype<DT>(hist[static_cast<int64_t>(c0 + ci) * HL + HL + (tau - seq_start)]);
+      } else {
+        taps[j].zero();
+      }
     }
-    out.store(y, r * ys + c0);
-#pragma unroll
-    for (int d = K - 1; d >= 2; --d) prev[d - 1] = prev[d - 2];
-    if constexpr (K > 1) prev[0] = cur;
+    conv_row<K, DT>(w, taps).store(y, r * ys + c0);
   }
 }
 
@@ -186,8 +197,8 @@ __global__ __launch_bounds__(256) void short_conv_history_kernel(
   const int s = blockIdx.y;
   const int c0 = cv * kVec;
   if (c0 >= channels || s >= n_seqs) return;
-  const int64_t start = min<int64_t>(max<int64_t>(cu[s], 0), total);
-  const int64_t end = min<int64_t>(max<int64_t>(cu[s + 1], start), total);
+  const int64_t start = iclamp64(cu[s], 0, total);
+  const int64_t end = iclamp64(cu[s + 1], start, total);
   const int slot = slots ? slots[s] : s;
   if (slot < 0 || slot >= n_slots) return;
   float *hist = conv_state + static_cast<int64_t>(slot) * channels * (K - 1);
@@ -275,7 +286,8 @@ int launch_fwd(const void *x, int64_t xs, void *y, int64_t ys, const float *w, f
                int read_history, int write_history, hipStream_t st) {
   const int nvec = channels / kVec;
   dim3 block(kVecsPerBlock, kRowTilesPerBlock);
-  const int64_t row_tiles = (total + kRows - 1) / kRows;
+  constexpr int R = rows_per_thread<DT>();
+  const int64_t row_tiles = (total + R - 1) / R;
   dim3 grid((nvec + kVecsPerBlock - 1) / kVecsPerBlock,
             static_cast<unsigned>((row_tiles + kRowTilesPerBlock - 1) / kRowTilesPerBlock));
   if (total > 0) {
@@ -359,7 +371,7 @@ extern "C" int sophia_short_conv_fwd(const void *x, int64_t x_row_stride, void *
                  "short_conv_fwd: history requested without conv_state");
   SOPHIA_REQUIRE(conv_state == nullptr || n_state_slots >= 0,
                  "short_conv_fwd: n_state_slots must be >= 0");
-  SOPHIA_REQUIRE(total_tokens / 64 < 65535, "short_conv_fwd: too many tokens for one launch");
+  SOPHIA_REQUIRE(total_tokens / 32 < 65535, "short_conv_fwd: too many tokens for one launch");
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == SOPHIA_DTYPE_BF16)
     return dispatch_fwd<SOPHIA_DTYPE_BF16>(kernel_size, x, x_row_stride, y, y_row_stride, weight,

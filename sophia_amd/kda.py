@@ -89,7 +89,7 @@ class CausalDepthwiseConv1d(nn.Module):
         bsz, seqlen, channels = x.shape
         hist_len = self.kernel_size - 1
         flat = x.reshape(bsz * seqlen, channels)
-        cu = torch.arange(0, (bsz + 1) * seqlen, seqlen, dtype=torch.int32, device=x.device)
+        cu = ops.cu_for_batch(bsz, seqlen, x.device)
         state = None
         if hist_len > 0:
             state = torch.zeros((bsz, channels, hist_len), dtype=torch.float32, device=x.device)
@@ -239,12 +239,20 @@ class SophiaKDA(nn.Module):
         return value
 
     def _input_weight(self, dtype: torch.dtype) -> torch.Tensor:
-        """[3*inner + decay_rank + heads (+ inner | + gate_rank), dim]: every
-        projection of x in one GEMM."""
+        """[3*inner + decay_rank + heads (+ inner | + gate_rank), dim], padded
+        with zero rows to a multiple of 8: every projection of x in one GEMM,
+        whose output rows then start on 16-byte boundaries (the ShortConv
+        kernel reads the q|k|v columns with 16-byte vector loads)."""
         mods = [self.q_proj, self.k_proj, self.v_proj, self.decay_down, self.beta_proj]
         mods.append(self.output_gate if self.output_gate_full_rank else self.output_gate_down)
         params = tuple(m.weight for m in mods)
-        return self._cached("in", params, lambda: torch.cat([p.detach() for p in params], 0), dtype)
+
+        def build():
+            w = torch.cat([p.detach() for p in params], 0)
+            pad = (-int(w.size(0))) % 8
+            return torch.cat([w, w.new_zeros(pad, w.size(1))], 0) if pad else w
+
+        return self._cached("in", params, build, dtype)
 
     def _conv_weight(self) -> torch.Tensor:
         params = (self.q_conv.weight, self.k_conv.weight, self.v_conv.weight)
@@ -258,7 +266,8 @@ class SophiaKDA(nn.Module):
         qkv = y[:, : 3 * i]
         dd = y[:, 3 * i: 3 * i + r]
         beta = y[:, 3 * i + r: 3 * i + r + h]
-        gate = y[:, 3 * i + r + h:]
+        gate = y[:, 3 * i + r + h: 3 * i + r + h + (i if self.output_gate_full_rank
+                                                     else self.output_gate_rank)]
         if not self.output_gate_full_rank:
             gate = self.output_gate_up(gate)
         return qkv, dd, beta, gate
@@ -331,14 +340,15 @@ class SophiaKDA(nn.Module):
         x2 = x.reshape(n, self.dim)
         qkv, dd, beta_logits, gate_logits = self._project(x2)
         cached = self.use_cache and int(start_pos) > 0
-        cu = torch.arange(0, (bsz + 1) * seqlen, seqlen, dtype=torch.int32, device=x.device)
+        cu = ops.cu_for_batch(bsz, seqlen, x.device)
         qkv = self._short_convolution_flat(qkv, cu, None, read=cached, write=self.use_cache,
                                            step=(seqlen == 1 and cached and self.use_cache))
         i = self.inner_dim
         shape4 = (bsz, seqlen, self.num_heads, self.head_dim)
-        q = qkv[:, :i].view(shape4) if qkv.is_contiguous() else qkv[:, :i].reshape(shape4)
-        k = qkv[:, i: 2 * i].reshape(shape4)
-        v = qkv[:, 2 * i:].reshape(shape4)
+        # Strided views of the conv output (no copies): the kernels take row strides.
+        q = qkv[:, :i].view(shape4)
+        k = qkv[:, i: 2 * i].view(shape4)
+        v = qkv[:, 2 * i:].view(shape4)
         decay = self.decay_up(dd).view(shape4)
         beta_logits = beta_logits.reshape(bsz, seqlen, self.num_heads)
         if pad_mask is not None:

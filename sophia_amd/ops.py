@@ -263,7 +263,8 @@ def kda_decode_step(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.
 
 
 # -------------------------------------------- flash-linear-attention signatures
-def _cu_for_batch(bsz: int, seqlen: int, device) -> torch.Tensor:
+def cu_for_batch(bsz: int, seqlen: int, device) -> torch.Tensor:
+    """cu_seqlens of a rectangular [bsz, seqlen] batch viewed as packed rows."""
     return torch.arange(0, (bsz + 1) * seqlen, seqlen, dtype=torch.int32, device=device)
 
 
@@ -298,7 +299,7 @@ def chunk_kda(q, k, v, g, beta, *, scale=None, initial_state=None, output_final_
             raise RuntimeError("varlen chunk_kda needs a packed batch of size 1")
         cu = cu_seqlens.to(device=q.device, dtype=torch.int32).contiguous()
     else:
-        cu = _cu_for_batch(bsz, seqlen, q.device)
+        cu = cu_for_batch(bsz, seqlen, q.device)
     n = int(cu.numel()) - 1
     total = bsz * seqlen
 
