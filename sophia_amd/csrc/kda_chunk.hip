@@ -210,7 +210,87 @@ struct Raw4<SOPHIA_DTYPE_F32> {
   __device__ __forceinline__ f4 get() const { return w; }
 };
 
-template <int QKV_DT, int G_DT>
+// Bases of the swizzled [128 channel][64 row] bf16 tiles for the channels a
+// lane owns (ch = 32 ks + 16 hf + 4 gq + j): swz(ch, row) = base[j] +
+// 64 * (32 ks + 16 hf), since adding a multiple of 8 to ch leaves ch & 7 and
+// the swizzle unchanged.  Stores then use compile-time offsets.
+struct SwzBases {
+  int b[4];
+};
+__device__ __forceinline__ SwzBases swz_bases(int gq, int row) {
+  SwzBases s;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) s.b[j] = swz(4 * gq + j, row);
+  return s;
+}
+
+// Step 4 of the intra kernel for sub-block W (a compile-time wave index, so
+// the products of sub-block totals below need no selects).  Per channel, with
+// Gloc the within-sub-block cumulative log-decay and E_i = e^{tot_i}:
+// a = e^{Gloc} (<= 1), b = e^{-Gloc} (<= e^80), kd = b E_W (<= 1),
+// eref = e^{ref_W} = prod_{i<W} E_i, etail = e^{G_C - ref_{W+1}} = prod_{i>W} E_i.
+// All products are of factors <= 1, so they can only underflow where the true
+// value is below 2^-126.
+template <int W>
+__device__ __forceinline__ void intra_scaled_operands(
+    const float (&qv)[32], const float (&kv)[32], const float (&gv)[32], float bt,
+    const float *s_E, uint16_t *sKD, uint16_t *sKb, uint8_t *rec, const SwzBases &sb, int l,
+    int lr, int gq, bf8 (&QSf)[4], bf8 (&KSf)[4], u4 (&kt_bits)[4], f4 &aqk_d, f4 &akk_d) {
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    float qa[8], ka[8], kb[8], kd[8], kd1[8], kd2[8], kbar[8], qe[8], kt[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int e = 8 * ks + i;
+      const f4 E = *reinterpret_cast<const f4 *>(&s_E[perm_k(ks, gq, i) * 4]);
+      const float a = __expf(gv[e]);
+      const float b = __expf(-gv[e]);
+      float eref = 1.f, etl = 1.f;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        if (m < W) eref *= E[m];
+        if (m > W) etl *= E[m];
+      }
+      qa[i] = qv[e] * a;
+      ka[i] = kv[e] * a;
+      kb[i] = kv[e] * b;
+      kd[i] = kb[i] * E[W];
+      if constexpr (W < 2) kd1[i] = kd[i] * E[W + 1];   // for query block W+2
+      if constexpr (W < 1) kd2[i] = kd1[i] * E[W + 2];  // for query block W+3
+      kbar[i] = kd[i] * etl;
+      qe[i] = qa[i] * eref;                             // Q e^G
+      kt[i] = (bt * eref) * ka[i];                      // beta K e^G
+    }
+    QSf[ks] = pack8(qa);
+    KSf[ks] = pack8(ka);
+    const bf8 kbf = pack8(kb);
+    aqk_d = mfma32(QSf[ks], kbf, aqk_d);
+    akk_d = mfma32(KSf[ks], kbf, akk_d);
+    kt_bits[ks] = bf8_to_bits(pack8(kt));
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      sKb[sb.b[i & 3] + 64 * (32 * ks + 16 * (i >> 2))] = f32_to_bf16_bits(kbar[i]);
+    // Q e^G goes straight to the workspace in A-operand order (mb = W).
+    *reinterpret_cast<u4 *>(rec + kOffQ + ((W * 4 + ks) * 64 + l) * 16) = bf8_to_bits(pack8(qe));
+    // Key-side rows of this block for the later query blocks, row-major bf16.
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int col = 32 * ks + 16 * hf + 4 * gq;
+      const int i0 = 4 * hf;
+      if constexpr (W < 3)
+        *reinterpret_cast<u2 *>(&sKD[(kd_slot(W, 0) * 16 + lr) * kLdKD + col]) =
+            u2{pack_bf16x2(kd[i0], kd[i0 + 1]), pack_bf16x2(kd[i0 + 2], kd[i0 + 3])};
+      if constexpr (W < 2)
+        *reinterpret_cast<u2 *>(&sKD[(kd_slot(W, 1) * 16 + lr) * kLdKD + col]) =
+            u2{pack_bf16x2(kd1[i0], kd1[i0 + 1]), pack_bf16x2(kd1[i0 + 2], kd1[i0 + 3])};
+      if constexpr (W < 1)
+        *reinterpret_cast<u2 *>(&sKD[(kd_slot(W, 2) * 16 + lr) * kLdKD + col]) =
+            u2{pack_bf16x2(kd2[i0], kd2[i0 + 1]), pack_bf16x2(kd2[i0 + 2], kd2[i0 + 3])};
+    }
+  }
+}
+
+template <int QKV_DT, int G_DT, bool GATE>
 __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   float *s_E = reinterpret_cast<float *>(smem + kSmE);
@@ -242,25 +322,27 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
   const bool valid = row < len;
   const int64_t tok = t0 + row;
   uint8_t *rec = p.records + (static_cast<size_t>(c) * p.num_heads + h) * kRecBytes;
+  const SwzBases sb = swz_bases(gq, row);
 
   // ---- 1. load q, k, g (32 channels per lane, 16x16x32 operand order), v, beta.
   // Slot (ks, e) of a lane holds channel perm_k(ks, gq, e).  Every global load
   // of the block is issued before the first use, so the block pays one memory
-  // round trip; rows past the end of the sequence load row t0 (always inside
-  // it) and are zeroed afterwards.
+  // round trip.  Rows past the end of the sequence load row t0 (always inside
+  // it) and are masked afterwards through scale factors: beta and the q/k
+  // norm scales become 0 and g is multiplied by 0 (no per-element branch).
   float qv[32], kv[32], gv[32];
-  float bt = 0.f;
+  float bt;
+  const float vmask = valid ? 1.f : 0.f;
   {
     const int64_t ltok = valid ? tok : t0;
     const int64_t qrow = ltok * p.qkv_stride + static_cast<int64_t>(h) * kD;
     const int64_t grow = ltok * p.g_stride + static_cast<int64_t>(h) * kD;
     // Gate parameters and beta are issued first (memory returns in issue
-    // order), and beta is kept as raw bits until after the loads: converting
-    // it inside the dtype branch would make the wave wait right there.
-    const bool gate = (p.flags & SOPHIA_KDA_GATE_IN_KERNEL) != 0;
+    // order); beta is kept as raw bits until after the loads: converting it
+    // inside the dtype branch would make the wave wait right there.
     float hs = 1.f;
     f4 rb[8];
-    if (gate) {
+    if constexpr (GATE) {
       hs = p.A_log[h];
 #pragma unroll
       for (int i = 0; i < 8; ++i)
@@ -283,27 +365,29 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
       rg[i].load(p.g, grow + ch);
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (valid) {
-      bt = __uint_as_float(p.beta_dtype == SOPHIA_DTYPE_BF16 ? (braw << 16) : braw);
-      if (p.flags & SOPHIA_KDA_BETA_SIGMOID) bt = fast_sigmoid(bt);
-    }
-    if (gate) hs = __expf(hs);
+    bt = __uint_as_float(p.beta_dtype == SOPHIA_DTYPE_BF16 ? (braw << 16) : braw);
+    if (p.flags & SOPHIA_KDA_BETA_SIGMOID) bt = fast_sigmoid(bt);
+    bt *= vmask;
+    if constexpr (GATE) hs = __expf(hs);
+    const float glb = GATE ? p.lb * vmask : vmask;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int ch = 32 * (i >> 1) + 16 * (i & 1) + 4 * gq;
       const f4 a = rq[i].get(), b = rk[i].get(), cc = rv[i].get(), d = rg[i].get();
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int e = 4 * i + j;
-        qv[e] = valid ? a[j] : 0.f;
-        kv[e] = valid ? b[j] : 0.f;
-        gv[e] = valid ? (gate ? p.lb * fast_sigmoid(hs * (d[j] + rb[i][j])) : d[j]) : 0.f;
-        sV[swz(ch + j, row)] = f32_to_bf16_bits(bt * cc[j]);   // beta V, transposed
+        qv[e] = a[j];
+        kv[e] = b[j];
+        if constexpr (GATE)
+          gv[e] = glb * fast_sigmoid(hs * (d[j] + rb[i][j]));
+        else
+          gv[e] = glb * d[j];
+        sV[sb.b[j] + 64 * (32 * (i >> 1) + 16 * (i & 1))] = f32_to_bf16_bits(bt * cc[j]);  // beta V^T
       }
     }
   }
 
-  // ---- 2. l2 norms (a row is spread over the 4 lane groups), gate
+  // ---- 2. l2 norms (a row is spread over the 4 lane groups)
   {
     float sq = 0.f, sk = 0.f;
 #pragma unroll
@@ -315,10 +399,10 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
     sq += __shfl_xor(sq, 32, 64);
     sk += __shfl_xor(sk, 16, 64);
     sk += __shfl_xor(sk, 32, 64);
-    float qs = p.scale, ksc = 1.f;
+    float qs = p.scale * vmask, ksc = vmask;
     if (p.flags & SOPHIA_KDA_QK_L2NORM) {
-      qs = p.scale / fmaxf(sqrtf(sq), 1e-12f);
-      ksc = 1.f / fmaxf(sqrtf(sk), 1e-12f);
+      qs *= __builtin_amdgcn_rcpf(fmaxf(sqrtf(sq), 1e-12f));
+      ksc *= __builtin_amdgcn_rcpf(fmaxf(sqrtf(sk), 1e-12f));
     }
 #pragma unroll
     for (int e = 0; e < 32; ++e) {
@@ -337,62 +421,14 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
   lds_barrier();
 
   // ---- 4. scaled operands; diagonal 16x16 blocks of A_qk / A_kk
-  // Per channel, with Gloc the within-sub-block cumulative log-decay and
-  // E_i = e^{tot_i}: a = e^{Gloc} (<= 1), b = e^{-Gloc} (<= e^80),
-  // d = b E_w (<= 1), eref = e^{ref_w} = prod_{i<w} E_i,
-  // etail = e^{G_C - ref_{w+1}} = prod_{i>w} E_i.  All products are of
-  // factors <= 1, so they can only underflow where the true value is < 2^-126.
   bf8 QSf[4], KSf[4];           // query side (A operands), all key blocks
   u4 kt_bits[4];                // beta K e^G, bf16, operand order
   f4 aqk_d = {0.f, 0.f, 0.f, 0.f}, akk_d = aqk_d;
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    float qa[8], ka[8], kb[8], kd[8], kd1[8], kd2[8], kbar[8], qe[8], kt[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int e = 8 * ks + i;
-      const f4 E = *reinterpret_cast<const f4 *>(&s_E[perm_k(ks, gq, i) * 4]);
-      const float a = __expf(gv[e]);
-      const float b = __expf(-gv[e]);
-      const float eref = (w > 0 ? E[0] : 1.f) * (w > 1 ? E[1] : 1.f) * (w > 2 ? E[2] : 1.f);
-      const float etl = (w < 1 ? E[1] : 1.f) * (w < 2 ? E[2] : 1.f) * (w < 3 ? E[3] : 1.f);
-      const float ew = w == 0 ? E[0] : (w == 1 ? E[1] : (w == 2 ? E[2] : E[3]));
-      const float e1 = w == 0 ? E[1] : E[2];      // E_{w+1} (waves 0, 1)
-      qa[i] = qv[e] * a;
-      ka[i] = kv[e] * a;
-      kb[i] = kv[e] * b;
-      kd[i] = kb[i] * ew;
-      kd1[i] = kd[i] * e1;                        // for query block w+2
-      kd2[i] = kd1[i] * E[2];                     // for query block w+3 (wave 0)
-      kbar[i] = kd[i] * etl;
-      qe[i] = qa[i] * eref;                       // Q e^G
-      kt[i] = bt * ka[i] * eref;                  // beta K e^G
-    }
-    QSf[ks] = pack8(qa);
-    KSf[ks] = pack8(ka);
-    const bf8 kbf = pack8(kb);
-    aqk_d = mfma32(QSf[ks], kbf, aqk_d);
-    akk_d = mfma32(KSf[ks], kbf, akk_d);
-    kt_bits[ks] = bf8_to_bits(pack8(kt));
-#pragma unroll
-    for (int i = 0; i < 8; ++i) sKb[swz(perm_k(ks, gq, i), row)] = f32_to_bf16_bits(kbar[i]);
-    // Q e^G goes straight to the workspace in A-operand order (mb = w).
-    *reinterpret_cast<u4 *>(rec + kOffQ + ((w * 4 + ks) * 64 + l) * 16) = bf8_to_bits(pack8(qe));
-    // Key-side rows of this block for the later query blocks, row-major bf16.
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      const int col = 32 * ks + 16 * hf + 4 * gq;
-      const int i0 = 4 * hf;
-      if (w < 3)
-        *reinterpret_cast<u2 *>(&sKD[(kd_slot(w, 0) * 16 + lr) * kLdKD + col]) =
-            u2{pack_bf16x2(kd[i0], kd[i0 + 1]), pack_bf16x2(kd[i0 + 2], kd[i0 + 3])};
-      if (w < 2)
-        *reinterpret_cast<u2 *>(&sKD[(kd_slot(w, 1) * 16 + lr) * kLdKD + col]) =
-            u2{pack_bf16x2(kd1[i0], kd1[i0 + 1]), pack_bf16x2(kd1[i0 + 2], kd1[i0 + 3])};
-      if (w < 1)
-        *reinterpret_cast<u2 *>(&sKD[(kd_slot(w, 2) * 16 + lr) * kLdKD + col]) =
-            u2{pack_bf16x2(kd2[i0], kd2[i0 + 1]), pack_bf16x2(kd2[i0 + 2], kd2[i0 + 3])};
-    }
+  switch (w) {
+    case 0: intra_scaled_operands<0>(qv, kv, gv, bt, s_E, sKD, sKb, rec, sb, l, lr, gq, QSf, KSf, kt_bits, aqk_d, akk_d); break;
+    case 1: intra_scaled_operands<1>(qv, kv, gv, bt, s_E, sKD, sKb, rec, sb, l, lr, gq, QSf, KSf, kt_bits, aqk_d, akk_d); break;
+    case 2: intra_scaled_operands<2>(qv, kv, gv, bt, s_E, sKD, sKb, rec, sb, l, lr, gq, QSf, KSf, kt_bits, aqk_d, akk_d); break;
+    default: intra_scaled_operands<3>(qv, kv, gv, bt, s_E, sKD, sKb, rec, sb, l, lr, gq, QSf, KSf, kt_bits, aqk_d, akk_d); break;
   }
   lds_barrier();
 
@@ -511,7 +547,7 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const uint32_t kword = kw[i >> 1];
-      sKt[swz(perm_k(ks, gq, i), row)] =
+      sKt[sb.b[i & 3] + 64 * (32 * ks + 16 * (i >> 2))] =
           static_cast<uint16_t>((i & 1) ? (kword >> 16) : (kword & 0xffffu));
     }
   }
@@ -597,63 +633,134 @@ struct ScanArgs {
   int splits;   // blocks per (sequence, head): 128 / NVB
 };
 
-// Per-chunk operands of one wavefront (its 16 chunk rows / 32 state rows).
+// ---- scan kernel: two roles per work-group ----------------------------------
+// Wavefronts 0..3 ("U/O" role) own chunk rows 16w..16w+15: U = Ut - W S and
+// O = (Q e^G) S + A_qk U.  Wavefronts 4..7 ("state" role) own state rows
+// 32sw..32sw+31 (sw = wave - 4) and the fp32 state: S <- Diag(e^{G_C}) S +
+// Kbar^T U.  Per chunk: the state waves publish S (bf16 B operand) -> barrier ->
+// the U/O waves form U and publish it -> barrier -> the state waves update S
+// while the U/O waves finish O and store it.  Each role streams only its own
+// record fragments, through a ring of register buffers of its own.
+constexpr int kScanThreads = 512;
+// Ring depths (record buffers in flight): the U/O buffers grow with the
+// number of value-column tiles, so the widest work-group keeps two.
 template <int NT>
-struct ScanFrags {
-  u4 wn[4];       // -W, A operand, mb = w, ks 0..3
-  u4 qb[4];       // Q e^G, A operand, mb = w, ks 0..3
-  u4 aq[2];       // A_qk, A operand, mb = w, ks 0..1
-  u4 kt[2][2];    // Kbar^T, A operand, mb = 2w + mi, ks 0..1
-  u2 ut[NT];      // Ut, C tile (mb = w, column tile nt0 + nt), bf16
-  f4 gm[2];       // e^{G_C} for state rows 32w + 16mi + 4gq + e
+constexpr int ring_uo() { return NT >= 8 ? 2 : 3; }
+constexpr int kRingS = 4;
+
+template <int NT>
+struct UOFrags {
+  u4 wn[4];   // -W, A operand, m = rows 16w.., k = channels perm_k(ks, gq, .)
+  u4 qb[4];   // Q e^G, A operand
+  u4 aq[2];   // A_qk, A operand, k = chunk rows perm_k(ks, gq, .)
+  u2 ut[NT];  // Ut, C tile (rows 16w + 4gq + e, column 16(nt0 + nt) + lr), bf16
+};
+
+struct SFrags {
+  u4 kt[2][2];  // Kbar^T, A operand, m = channels 16(2sw + mi) + lr, ks 0..1
+  f4 gm[2];     // e^{G_C} of state rows 32sw + 16mi + 4gq + e
 };
 
 template <int NT>
-__device__ __forceinline__ void load_frags(ScanFrags<NT> &f, const uint8_t *rec, int w, int l,
-                                           int gq, int nt0) {
+__device__ __forceinline__ void load_uo(UOFrags<NT> &f, const uint8_t *rec, int w, int l, int nt0) {
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
     f.wn[ks] = *reinterpret_cast<const u4 *>(rec + kOffW + ((w * 4 + ks) * 64 + l) * 16);
     f.qb[ks] = *reinterpret_cast<const u4 *>(rec + kOffQ + ((w * 4 + ks) * 64 + l) * 16);
   }
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
+  for (int ks = 0; ks < 2; ++ks)
     f.aq[ks] = *reinterpret_cast<const u4 *>(rec + kOffA + ((w * 2 + ks) * 64 + l) * 16);
-#pragma unroll
-    for (int mi = 0; mi < 2; ++mi)
-      f.kt[mi][ks] = *reinterpret_cast<const u4 *>(rec + kOffKt + (((2 * w + mi) * 2 + ks) * 64 + l) * 16);
-  }
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt)
     f.ut[nt] = *reinterpret_cast<const u2 *>(rec + kOffU + ((w * 8 + nt0 + nt) * 64 + l) * 8);
-  const float *gam = reinterpret_cast<const float *>(rec + kOffG);
-#pragma unroll
-  for (int mi = 0; mi < 2; ++mi) f.gm[mi] = *reinterpret_cast<const f4 *>(&gam[32 * w + 16 * mi + 4 * gq]);
 }
 
-// Makes the wave wait for the loads of `f` here: an empty asm statement that
-// reads every register of the buffer.
+__device__ __forceinline__ void load_s(SFrags &f, const uint8_t *rec, int sw, int l, int gq) {
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+      f.kt[mi][ks] = *reinterpret_cast<const u4 *>(rec + kOffKt + (((2 * sw + mi) * 2 + ks) * 64 + l) * 16);
+  const float *gam = reinterpret_cast<const float *>(rec + kOffG);
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi) f.gm[mi] = *reinterpret_cast<const f4 *>(&gam[32 * sw + 16 * mi + 4 * gq]);
+}
+
+// Makes the wave wait for the loads of a buffer here: an empty asm statement
+// that reads every register of it.
 template <int NT>
-__device__ __forceinline__ void touch_frags(const ScanFrags<NT> &f) {
+__device__ __forceinline__ void touch(const UOFrags<NT> &f) {
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) asm volatile("" ::"v"(f.wn[ks]), "v"(f.qb[ks]));
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) asm volatile("" ::"v"(f.aq[ks]), "v"(f.kt[0][ks]), "v"(f.kt[1][ks]));
+  asm volatile("" ::"v"(f.aq[0]), "v"(f.aq[1]));
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) asm volatile("" ::"v"(f.ut[nt]));
+}
+__device__ __forceinline__ void touch(const SFrags &f) {
+  asm volatile("" ::"v"(f.kt[0][0]), "v"(f.kt[0][1]), "v"(f.kt[1][0]), "v"(f.kt[1][1]));
   asm volatile("" ::"v"(f.gm[0]), "v"(f.gm[1]));
 }
 
-// One chunk of the state scan for the 4 wavefronts of a block: U = Ut - W S,
-// O = (Q e^G) S + A_qk U (stored), S = Diag(e^{G_C}) S + Kbar^T U.  Wave w
-// owns chunk rows 16w..16w+15 of U and O and state rows 32w..32w+31; S and U
-// are exchanged between the waves as bf16 B operands in LDS.
+struct ScanGeom {
+  int h, nt0, nchunks;
+  int64_t seq_a, seq_b;
+  const uint8_t *rec0;
+  size_t rec_stride;
+};
+
+// One chunk of the U/O role (two barriers).
 template <int NT, int O_DT>
-__device__ __forceinline__ void scan_step(const ScanArgs &p, const ScanFrags<NT> &cur, f4 (&S)[2][NT],
-                                          uint8_t *sSb, uint8_t *sUb, int w, int l, int gq, int nt0,
-                                          int h, int64_t seq_a, int64_t seq_b, int cc) {
-  const int lr = l & 15;
-  // 1. publish this wave's state rows as K-step w of the bf16 B operand.
+__device__ __forceinline__ void uo_step(const ScanArgs &p, const ScanGeom &g, const UOFrags<NT> &f,
+                                        const uint8_t *sSb, uint8_t *sUb, int w, int l, int cc) {
+  const int lr = l & 15, gq = l >> 4;
+  lds_barrier();  // S of this chunk is published
+  f4 U[NT], O[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    bf8 sb[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      sb[ks] = bits_to_bf8(*reinterpret_cast<const u4 *>(sSb + ((ks * NT + nt) * 64 + l) * 16));
+    const u2 uw = f.ut[nt];
+    f4 u = {__uint_as_float(uw.x << 16), __uint_as_float(uw.x & 0xffff0000u),
+            __uint_as_float(uw.y << 16), __uint_as_float(uw.y & 0xffff0000u)};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) u = mfma32(bits_to_bf8(f.wn[ks]), sb[ks], u);
+    U[nt] = u;
+    // U rows 16w.. are half (w & 1) of K-step w / 2 of the U operand.
+    *reinterpret_cast<u2 *>(sUb + (((w >> 1) * NT + nt) * 64 + l) * 16 + (w & 1) * 8) = pack4_bf16(u);
+    f4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) o = mfma32(bits_to_bf8(f.qb[ks]), sb[ks], o);
+    O[nt] = o;
+  }
+  lds_barrier();  // U is published
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const bf8 u0 = bits_to_bf8(*reinterpret_cast<const u4 *>(sUb + ((0 * NT + nt) * 64 + l) * 16));
+    O[nt] = mfma32(bits_to_bf8(f.aq[0]), u0, O[nt]);
+    if (w >= 2) {  // A_qk is lower triangular
+      const bf8 u1 = bits_to_bf8(*reinterpret_cast<const u4 *>(sUb + ((1 * NT + nt) * 64 + l) * 16));
+      O[nt] = mfma32(bits_to_bf8(f.aq[1]), u1, O[nt]);
+    }
+  }
+  const int64_t tok0 = g.seq_a + static_cast<int64_t>(cc) * kC;
+  const int rows_valid = static_cast<int>(imin64(kC, g.seq_b - tok0));
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int r = 16 * w + 4 * gq + e;
+    if (r < rows_valid) {
+      const int64_t base = (tok0 + r) * p.o_stride + static_cast<int64_t>(g.h) * kD + 16 * g.nt0 + lr;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) store_elem(p.o, base + 16 * nt, O_DT, O[nt][e]);
+    }
+  }
+}
+
+// Publishes this wave's state rows as K-step sw of the bf16 B operand of S.
+template <int NT>
+__device__ __forceinline__ void publish_state(const f4 (&S)[2][NT], uint8_t *sSb, int sw, int l) {
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     float t[8];
@@ -662,83 +769,53 @@ __device__ __forceinline__ void scan_step(const ScanArgs &p, const ScanFrags<NT>
       t[e] = S[0][nt][e];
       t[4 + e] = S[1][nt][e];
     }
-    *reinterpret_cast<u4 *>(sSb + ((w * NT + nt) * 64 + l) * 16) = bf8_to_bits(pack8(t));
+    *reinterpret_cast<u4 *>(sSb + ((sw * NT + nt) * 64 + l) * 16) = bf8_to_bits(pack8(t));
   }
-  lds_barrier();
+}
 
-  // 2. U = Ut - W S and O = (Q e^G) S for chunk rows 16w..16w+15.
-  f4 U[NT], O[NT];
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    bf8 sb[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-      sb[ks] = bits_to_bf8(*reinterpret_cast<const u4 *>(sSb + ((ks * NT + nt) * 64 + l) * 16));
-    const u2 uw = cur.ut[nt];
-    f4 u = {__uint_as_float(uw.x << 16), __uint_as_float(uw.x & 0xffff0000u),
-            __uint_as_float(uw.y << 16), __uint_as_float(uw.y & 0xffff0000u)};
-    f4 o = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      u = mfma32(bits_to_bf8(cur.wn[ks]), sb[ks], u);
-      o = mfma32(bits_to_bf8(cur.qb[ks]), sb[ks], o);
-    }
-    U[nt] = u;
-    O[nt] = o;
-  }
-  // 3. publish U rows 16w.. as half (w & 1) of K-step w/2 of the U operand.
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt)
-    *reinterpret_cast<u2 *>(sUb + (((w >> 1) * NT + nt) * 64 + l) * 16 + (w & 1) * 8) = pack4_bf16(U[nt]);
-  lds_barrier();
-
-  // 4. O += A_qk U (A_qk is lower triangular: K-steps <= w/2);
-  //    S = Diag(e^{G_C}) S + Kbar^T U.
+// One chunk of the state role (two barriers): S <- Diag(e^{G_C}) S + Kbar^T U,
+// then publish S for the next chunk.
+template <int NT>
+__device__ __forceinline__ void state_step(const SFrags &f, f4 (&S)[2][NT], uint8_t *sSb,
+                                           const uint8_t *sUb, int sw, int l) {
+  lds_barrier();  // S published (by this role, before)
+  lds_barrier();  // U published
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     bf8 ub[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
       ub[ks] = bits_to_bf8(*reinterpret_cast<const u4 *>(sUb + ((ks * NT + nt) * 64 + l) * 16));
-    O[nt] = mfma32(bits_to_bf8(cur.aq[0]), ub[0], O[nt]);
-    if (w >= 2) O[nt] = mfma32(bits_to_bf8(cur.aq[1]), ub[1], O[nt]);
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi) {
-      f4 sv = S[mi][nt] * cur.gm[mi];
-      sv = mfma32(bits_to_bf8(cur.kt[mi][0]), ub[0], sv);
-      sv = mfma32(bits_to_bf8(cur.kt[mi][1]), ub[1], sv);
+      f4 sv = S[mi][nt] * f.gm[mi];
+      sv = mfma32(bits_to_bf8(f.kt[mi][0]), ub[0], sv);
+      sv = mfma32(bits_to_bf8(f.kt[mi][1]), ub[1], sv);
       S[mi][nt] = sv;
     }
   }
-
-  // 5. store O for the valid rows of the chunk.
-  const int64_t tok0 = seq_a + static_cast<int64_t>(cc) * kC;
-  const int rows_valid = static_cast<int>(imin64(kC, seq_b - tok0));
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int r = 16 * w + 4 * gq + e;
-    if (r < rows_valid) {
-      const int64_t base = (tok0 + r) * p.o_stride + static_cast<int64_t>(h) * kD + 16 * nt0 + lr;
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) store_elem(p.o, base + 16 * nt, O_DT, O[nt][e]);
-    }
-  }
+  publish_state<NT>(S, sSb, sw, l);
 }
 
-// One block of 4 wavefronts per (sequence, head, NVB value columns).  Wave w
-// owns chunk rows 16w..16w+15 of U and O and state rows 32w..32w+31; the
-// state and U are exchanged between the waves as bf16 B operands in LDS.
+// One work-group of 8 wavefronts per (sequence, head, NVB value columns).
+// Record operands of chunk cc + ring are loaded as soon as chunk cc has been
+// consumed, so every load has ring - 1 chunk steps to arrive.  The buffer of
+// the next step is waited for right after the newest loads are issued
+// (touch), where the wait can leave exactly those in flight; a wait placed by
+// the compiler at a loop header would drain everything.  Loads are never
+// under a branch (the compiler then drains every load at the join): past the
+// last chunk they re-read the last chunk, unused.
 template <int NVB, int O_DT>
-__global__ __launch_bounds__(kThreads, 1) void kda_chunk_scan_kernel(ScanArgs p) {
-  constexpr int NT = NVB / 16;               // 16-column tiles per block
+__global__ __launch_bounds__(kScanThreads) void kda_chunk_scan_kernel(ScanArgs p) {
+  constexpr int NT = NVB / 16;               // 16-column tiles per work-group
   __shared__ __attribute__((aligned(16))) uint8_t sSb[4 * NT * 64 * 16];   // S, [ks][nt][lane]
   __shared__ __attribute__((aligned(16))) uint8_t sUb[2 * NT * 64 * 16];   // U, [ks][nt][lane]
   const int tid = threadIdx.x;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l = tid & 63;
   const int lr = l & 15, gq = l >> 4;
-  // XCD-aware order: the `splits` blocks of one (sequence, head) share the
-  // same blockIdx % 8, i.e. the same XCD and L2, so they share operand reads.
+  // XCD-aware order: the `splits` work-groups of one (sequence, head) share
+  // the same blockIdx % 8, i.e. the same XCD and L2, so they share record reads.
   const int b = blockIdx.x;
   const int group = b / (8 * p.splits);
   const int half = (b / 8) % p.splits;
@@ -746,17 +823,43 @@ __global__ __launch_bounds__(kThreads, 1) void kda_chunk_scan_kernel(ScanArgs p)
   const int h = sh % p.num_heads;
   const int s = sh / p.num_heads;
   if (s >= p.n_seqs) return;
-  const int nt0 = half * NT;                  // first 16-column tile of this block
-  const int64_t seq_a = iclamp64(p.cu[s], 0, p.total);
-  const int64_t seq_b = iclamp64(p.cu[s + 1], seq_a, p.total);
-  const int nchunks = static_cast<int>(imin64((seq_b - seq_a + kC - 1) / kC,
-                                                    p.max_ch - p.chunk_start[s]));
-  const int cbase = p.chunk_start[s];
+  ScanGeom g;
+  g.h = h;
+  g.nt0 = half * NT;
+  g.seq_a = iclamp64(p.cu[s], 0, p.total);
+  g.seq_b = iclamp64(p.cu[s + 1], g.seq_a, p.total);
+  g.nchunks = static_cast<int>(imin64((g.seq_b - g.seq_a + kC - 1) / kC, p.max_ch - p.chunk_start[s]));
+  g.rec0 = p.records + (static_cast<size_t>(p.chunk_start[s]) * p.num_heads + h) * kRecBytes;
+  g.rec_stride = static_cast<size_t>(p.num_heads) * kRecBytes;
+  const int nchunks = g.nchunks;
+  const int last = nchunks - 1;
+
+  if (wave < 4) {
+    // ---- U/O role
+    const int w = wave;
+    if (nchunks <= 0) return;
+    constexpr int R = ring_uo<NT>();
+    UOFrags<NT> f[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) load_uo<NT>(f[r], g.rec0 + min(r, last) * g.rec_stride, w, l, g.nt0);
+    touch<NT>(f[0]);
+    for (int cc = 0; cc < nchunks; cc += R) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if (cc + r < nchunks) uo_step<NT, O_DT>(p, g, f[r], sSb, sUb, w, l, cc + r);
+        load_uo<NT>(f[r], g.rec0 + min(cc + r + R, last) * g.rec_stride, w, l, g.nt0);
+        touch<NT>(f[(r + 1) % R]);
+      }
+    }
+    return;
+  }
+
+  // ---- state role: S tiles [mi 2][nt NT], rows 32sw + 16mi + 4gq + e,
+  // column 16(nt0 + nt) + lr.
+  const int sw = wave - 4;
   const int slot = p.slots ? p.slots[s] : s;
   const bool has_slot = slot >= 0 && slot < p.n_slots;  // else: zero start, nothing written
   const int64_t state_off = (static_cast<int64_t>(has_slot ? slot : 0) * p.num_heads + h) * kD * kD;
-
-  // S tiles: [mi 2][nt NT], rows 32w + 16mi + 4gq + e, column 16(nt0 + nt) + lr.
   f4 S[2][NT];
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi)
@@ -766,39 +869,26 @@ __global__ __launch_bounds__(kThreads, 1) void kda_chunk_scan_kernel(ScanArgs p)
       if (p.h0 && has_slot) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          v[e] = p.h0[state_off + static_cast<int64_t>(32 * w + 16 * mi + 4 * gq + e) * kD +
-                      16 * (nt0 + nt) + lr];
+          v[e] = p.h0[state_off + static_cast<int64_t>(32 * sw + 16 * mi + 4 * gq + e) * kD +
+                      16 * (g.nt0 + nt) + lr];
       }
       S[mi][nt] = v;
     }
-
-  // Two operand buffers in ping-pong order: the loads of chunk cc + 2 are
-  // issued as soon as chunk cc has been consumed, so each load has a whole
-  // chunk step of the other buffer to complete, and no buffer is ever copied
-  // (a copy would wait for the loads in flight).
-  const uint8_t *rec0 = p.records + (static_cast<size_t>(cbase) * p.num_heads + h) * kRecBytes;
-  const size_t rec_stride = static_cast<size_t>(p.num_heads) * kRecBytes;
-  // Buffer fa is waited for at the end of the previous iteration (touch_frags),
-  // where only the younger loads of fb are in flight; a wait placed by the
-  // compiler at the loop header would also drain fb.  Loads are never under
-  // a branch (a branch makes the compiler drain every load at the join):
-  // past the last chunk they re-read the last chunk and go unused.
   if (nchunks > 0) {
-    const int last = nchunks - 1;
-    ScanFrags<NT> fa, fb;
-    load_frags<NT>(fa, rec0, w, l, gq, nt0);
-    load_frags<NT>(fb, rec0 + min(1, last) * rec_stride, w, l, gq, nt0);
-    touch_frags<NT>(fa);
-    for (int cc = 0; cc < nchunks; cc += 2) {
-      scan_step<NT, O_DT>(p, fa, S, sSb, sUb, w, l, gq, nt0, h, seq_a, seq_b, cc);
-      load_frags<NT>(fa, rec0 + min(cc + 2, last) * rec_stride, w, l, gq, nt0);
-      if (cc + 1 < nchunks)
-        scan_step<NT, O_DT>(p, fb, S, sSb, sUb, w, l, gq, nt0, h, seq_a, seq_b, cc + 1);
-      load_frags<NT>(fb, rec0 + min(cc + 3, last) * rec_stride, w, l, gq, nt0);
-      touch_frags<NT>(fa);
+    publish_state<NT>(S, sSb, sw, l);
+    SFrags f[kRingS];
+#pragma unroll
+    for (int r = 0; r < kRingS; ++r) load_s(f[r], g.rec0 + min(r, last) * g.rec_stride, sw, l, gq);
+    touch(f[0]);
+    for (int cc = 0; cc < nchunks; cc += kRingS) {
+#pragma unroll
+      for (int r = 0; r < kRingS; ++r) {
+        if (cc + r < nchunks) state_step<NT>(f[r], S, sSb, sUb, sw, l);
+        load_s(f[r], g.rec0 + min(cc + r + kRingS, last) * g.rec_stride, sw, l, gq);
+        touch(f[(r + 1) % kRingS]);
+      }
     }
   }
-
   if (p.ht && has_slot) {
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi)
@@ -806,34 +896,34 @@ __global__ __launch_bounds__(kThreads, 1) void kda_chunk_scan_kernel(ScanArgs p)
       for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          p.ht[state_off + static_cast<int64_t>(32 * w + 16 * mi + 4 * gq + e) * kD + 16 * (nt0 + nt) + lr] =
+          p.ht[state_off + static_cast<int64_t>(32 * sw + 16 * mi + 4 * gq + e) * kD + 16 * (g.nt0 + nt) + lr] =
               S[mi][nt][e];
   }
 }
 
 
-template <int QKV_DT, int G_DT>
+template <int QKV_DT, int G_DT, bool GATE>
 int launch_intra(dim3 grid, hipStream_t st, const IntraArgs &ia) {
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void *>(&kda_chunk_intra_kernel<QKV_DT, G_DT>),
+        reinterpret_cast<const void *>(&kda_chunk_intra_kernel<QKV_DT, G_DT, GATE>),
         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kSmIntra));
     if (e != hipSuccess)
       return set_error(SOPHIA_ERR_HIP, "kda_chunk_fwd: cannot set LDS size: %s", hipGetErrorString(e));
     attr_set = true;
   }
-  hipLaunchKernelGGL((kda_chunk_intra_kernel<QKV_DT, G_DT>), grid, dim3(kThreads), kSmIntra, st, ia);
+  hipLaunchKernelGGL((kda_chunk_intra_kernel<QKV_DT, G_DT, GATE>), grid, dim3(kThreads), kSmIntra, st, ia);
   return check_launch("kda_chunk_intra");
 }
 
 template <int O_DT>
 void launch_scan(int splits, dim3 grid, hipStream_t st, const ScanArgs &sa) {
   switch (splits) {
-    case 1: hipLaunchKernelGGL((kda_chunk_scan_kernel<128, O_DT>), grid, dim3(kThreads), 0, st, sa); break;
-    case 2: hipLaunchKernelGGL((kda_chunk_scan_kernel<64, O_DT>), grid, dim3(kThreads), 0, st, sa); break;
-    case 4: hipLaunchKernelGGL((kda_chunk_scan_kernel<32, O_DT>), grid, dim3(kThreads), 0, st, sa); break;
-    default: hipLaunchKernelGGL((kda_chunk_scan_kernel<16, O_DT>), grid, dim3(kThreads), 0, st, sa); break;
+    case 1: hipLaunchKernelGGL((kda_chunk_scan_kernel<128, O_DT>), grid, dim3(kScanThreads), 0, st, sa); break;
+    case 2: hipLaunchKernelGGL((kda_chunk_scan_kernel<64, O_DT>), grid, dim3(kScanThreads), 0, st, sa); break;
+    case 4: hipLaunchKernelGGL((kda_chunk_scan_kernel<32, O_DT>), grid, dim3(kScanThreads), 0, st, sa); break;
+    default: hipLaunchKernelGGL((kda_chunk_scan_kernel<16, O_DT>), grid, dim3(kScanThreads), 0, st, sa); break;
   }
 }
 
@@ -904,26 +994,33 @@ extern "C" int sophia_kda_chunk_fwd(const void *q, const void *k, const void *v,
                  cu_seqlens, n_seqs, total_tokens, num_heads, max_ch, chunk_start, chunk_seq,
                  records};
     const dim3 grid(static_cast<unsigned>(max_ch), num_heads);
-    if (qkv_dtype == SOPHIA_DTYPE_BF16 && g_dtype == SOPHIA_DTYPE_F32)
-      rc = launch_intra<SOPHIA_DTYPE_BF16, SOPHIA_DTYPE_F32>(grid, st, ia);
-    else if (qkv_dtype == SOPHIA_DTYPE_BF16)
-      rc = launch_intra<SOPHIA_DTYPE_BF16, SOPHIA_DTYPE_BF16>(grid, st, ia);
-    else if (g_dtype == SOPHIA_DTYPE_F32)
-      rc = launch_intra<SOPHIA_DTYPE_F32, SOPHIA_DTYPE_F32>(grid, st, ia);
-    else
-      rc = launch_intra<SOPHIA_DTYPE_F32, SOPHIA_DTYPE_BF16>(grid, st, ia);
+    const bool gate = (flags & SOPHIA_KDA_GATE_IN_KERNEL) != 0;
+    const int key = (qkv_dtype == SOPHIA_DTYPE_BF16) * 4 + (g_dtype == SOPHIA_DTYPE_BF16) * 2 + gate;
+    constexpr int F = SOPHIA_DTYPE_F32, B = SOPHIA_DTYPE_BF16;
+    switch (key) {
+      case 0: rc = launch_intra<F, F, false>(grid, st, ia); break;
+      case 1: rc = launch_intra<F, F, true>(grid, st, ia); break;
+      case 2: rc = launch_intra<F, B, false>(grid, st, ia); break;
+      case 3: rc = launch_intra<F, B, true>(grid, st, ia); break;
+      case 4: rc = launch_intra<B, F, false>(grid, st, ia); break;
+      case 5: rc = launch_intra<B, F, true>(grid, st, ia); break;
+      case 6: rc = launch_intra<B, B, false>(grid, st, ia); break;
+      default: rc = launch_intra<B, B, true>(grid, st, ia); break;
+    }
     if (rc) return rc;
   }
   // The state scan is sequential over the chunks of a sequence: split the 128
-  // value columns of each (sequence, head) over 1, 2, 4 or 8 blocks until the
-  // grid holds about two blocks per CU, so that short batches still spread
-  // the critical path over the chip.
+  // value columns of each (sequence, head) over 1, 2, 4 or 8 work-groups, as
+  // many as keep every work-group resident at once (one per CU: its 8
+  // wavefronts hold rings of record buffers and fill half of each SIMD's
+  // register file), so a small batch still spreads its critical path over
+  // the chip.
   int device = 0, cus = 256;
   if (hipGetDevice(&device) == hipSuccess)
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) cus = 256;
   const int64_t pairs = static_cast<int64_t>(n_seqs) * num_heads;
   int splits = 1;
-  while (splits < 8 && pairs * splits < 2 * static_cast<int64_t>(cus)) splits *= 2;
+  while (splits < 8 && pairs * splits * 2 <= static_cast<int64_t>(cus)) splits *= 2;
   ScanArgs sa{cu_seqlens, n_seqs, total_tokens, num_heads, max_ch, chunk_start, records,
               initial_state, final_state, n_state_slots, state_slots, o, o_row_stride, splits};
   const int64_t groups = (pairs + 7) / 8;
