@@ -1,6 +1,6 @@
-"""Model arguments of the KDA mixer (the KDA-relevant part of the reference's
-``ModelArgs``, ml/runtime/model/config.py:8-45, with the value checks of
-ml/core/spec/semantics/__init__.py:55-124 that concern the mixer)."""
+"""Model arguments of the Sophia hybrid decoder and its KDA mixer (the
+reference's ``ModelArgs``, ml/runtime/model/config.py:8-45, with the value
+checks of ml/core/spec/semantics/__init__.py:55-124 that concern them)."""
 
 from __future__ import annotations
 
@@ -10,6 +10,15 @@ from dataclasses import dataclass
 
 @dataclass
 class ModelArgs:
+    vocab_size: int = 65536
+    n_layers: int = 28
+    ffn_hidden: int = 3968
+    mla_q_rank: int = 384
+    mla_kv_rank: int = 128
+    attn_res_block_size: int = 4
+    situ_gate_softcap: float = 4.0
+    situ_up_softcap: float = 25.0
+    dropout: float = 0.0
     dim: int = 1536
     num_heads: int = 16
     head_dim: int = 128
@@ -30,8 +39,9 @@ class ModelArgs:
     use_cache: bool = True
 
     def __post_init__(self) -> None:
-        for name in ("dim", "num_heads", "head_dim", "kda_decay_rank", "kda_output_gate_rank",
-                     "short_conv_kernel", "max_seq_len", "max_batch_size"):
+        for name in ("vocab_size", "n_layers", "ffn_hidden", "mla_q_rank", "mla_kv_rank",
+                     "attn_res_block_size", "dim", "num_heads", "head_dim", "kda_decay_rank",
+                     "kda_output_gate_rank", "short_conv_kernel", "max_seq_len", "max_batch_size"):
             value = int(getattr(self, name))
             if value <= 0:
                 raise ValueError(f"{name} must be > 0, got {value}")
@@ -57,6 +67,10 @@ class ModelArgs:
             raise ValueError("short_conv_kernel must be <= 4 on this build")
         if int(self.head_dim) != 128:
             raise ValueError("the gfx950 KDA kernels are built for head_dim = 128")
+
+    def layer_type(self, layer_idx: int) -> str:
+        """config.py:51-52 of the reference: layer i is MLA iff i % 4 == 3."""
+        return "mla" if int(layer_idx) % 4 == 3 else "kda"
 
     @property
     def attention_inner_dim(self) -> int:

@@ -1,0 +1,433 @@
+"""The Sophia hybrid decoder around the MI355X KDA mixer, and its captured
+continuous-batching step.
+
+Modules keep the reference's names, parameter shapes and semantics
+(ml/runtime/model/attention.py:423-657 ``SophiaMLA``; blocks.py:12-87
+``FeedForward`` / ``AttentionResidualMixer`` / ``SophiaBlock``;
+transformer.py:17-207 and transformer_setup.py:33-79 ``Transformer``), so a
+reference state_dict loads as is.  Layer i is MLA iff i % 4 == 3, the rest are
+``sophia_amd.kda.SophiaKDA`` (gfx950 kernels).  MLA and the FFN run on library
+GEMMs and attention (hipBLASLt / SDPA through torch).
+
+Besides the reference-shaped ``Transformer.forward(input_ids, start_pos)``,
+``Transformer.forward_mixed`` runs one continuous-batching step that the
+reference cannot express (it has one start_pos per batch,
+transformer.py:146-160): new sequences prefilled in a rectangular group,
+packed with one decode token for each of many running sequences, every
+sequence in its own cache slot.  ``MixedStepGraph`` captures that step in a
+HIP graph after a warm-up on a side stream (the capture pattern of
+ml/training/pretrain/engine/sm120_graph_runner.py:318-371) and replays it.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from .config import ModelArgs
+from .kda import RMSNorm, RuntimeLinear, SophiaKDA, _require_gpu
+from .state import LayerCacheSnapshot
+
+
+class SophiaMLA(nn.Module):
+    """NoPE multi-head latent attention with a full-rank output gate
+    (attention.py:423-657)."""
+
+    def __init__(self, args: ModelArgs) -> None:
+        super().__init__()
+        self.dim = int(args.dim)
+        self.num_heads = int(args.num_heads)
+        self.head_dim = int(args.head_dim)
+        self.inner_dim = self.num_heads * self.head_dim
+        self.q_rank = int(args.mla_q_rank)
+        self.kv_rank = int(args.mla_kv_rank)
+        self.use_cache = bool(args.use_cache)
+        self.q_down = RuntimeLinear(self.dim, self.q_rank)
+        self.q_norm = RMSNorm(self.q_rank, args.norm_eps)
+        self.q_up = RuntimeLinear(self.q_rank, self.inner_dim)
+        self.kv_down = RuntimeLinear(self.dim, self.kv_rank)
+        self.kv_norm = RMSNorm(self.kv_rank, args.norm_eps)
+        self.k_up = RuntimeLinear(self.kv_rank, self.inner_dim)
+        self.v_up = RuntimeLinear(self.kv_rank, self.inner_dim)
+        self.output_gate = RuntimeLinear(self.dim, self.inner_dim)
+        self.o_proj = RuntimeLinear(self.inner_dim, self.dim)
+        self.register_buffer("latent_cache", torch.zeros(
+            int(args.max_batch_size), int(args.max_seq_len), self.kv_rank), persistent=False)
+
+    # ------------------------------------------------------------- caches
+    def ensure_batch_capacity(self, batch_size: int) -> None:
+        required = int(batch_size)
+        if required <= int(self.latent_cache.size(0)):
+            return
+        grown = self.latent_cache.new_zeros(required, int(self.latent_cache.size(1)), self.kv_rank)
+        grown[: self.latent_cache.size(0)].copy_(self.latent_cache)
+        self.latent_cache = grown
+
+    def ensure_sequence_capacity(self, max_seq_len: int) -> None:
+        required = int(max_seq_len)
+        if required <= int(self.latent_cache.size(1)):
+            return
+        grown = self.latent_cache.new_zeros(int(self.latent_cache.size(0)), required, self.kv_rank)
+        grown[:, : self.latent_cache.size(1)].copy_(self.latent_cache)
+        self.latent_cache = grown
+
+    def reset(self) -> None:
+        if self.latent_cache.is_inference():
+            self.latent_cache = torch.zeros_like(self.latent_cache)
+        else:
+            self.latent_cache.zero_()
+
+    def cache_snapshot(self, *, device: str, batch_size: int, cache_pos: int | None):
+        end = int(self.latent_cache.size(1) if cache_pos is None else cache_pos)
+        return LayerCacheSnapshot(latent=self.latent_cache[:batch_size, :end].to(device).clone())
+
+    def validate_cache_snapshot(self, snapshot: LayerCacheSnapshot) -> None:
+        if snapshot.recurrent is not None or snapshot.conv is not None:
+            raise ValueError("MLA cache cannot contain KDA state")
+        if snapshot.latent is not None and int(snapshot.latent.size(-1)) != self.kv_rank:
+            raise ValueError("MLA latent cache shape mismatch")
+
+    def load_cache_snapshot(self, snapshot: LayerCacheSnapshot) -> None:
+        self.validate_cache_snapshot(snapshot)
+        if snapshot.latent is None:
+            return
+        batch, length = int(snapshot.latent.size(0)), int(snapshot.latent.size(1))
+        self.ensure_batch_capacity(batch)
+        self.ensure_sequence_capacity(length)
+        self.latent_cache[:batch, :length].copy_(
+            snapshot.latent.to(self.latent_cache.device, dtype=self.latent_cache.dtype))
+
+    # ------------------------------------------------------------- forward
+    def _gate_out(self, x: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+        gate = torch.sigmoid(self.output_gate(x)).view_as(out)
+        gated = (out.float() * gate.float()).to(dtype=x.dtype)
+        return self.o_proj(gated.reshape(*gated.shape[:-2], self.inner_dim))
+
+    def forward(self, x: torch.Tensor, *, start_pos: int = 0) -> torch.Tensor:
+        """attention.py:609-657 (pad-mask path: attention.py:585-600,635-654)."""
+        bsz, seqlen, _ = x.shape
+        q = self.q_up(self.q_norm(self.q_down(x))).view(bsz, seqlen, self.num_heads, self.head_dim)
+        latent = self.kv_norm(self.kv_down(x))
+        if self.use_cache:
+            end = int(start_pos) + int(seqlen)
+            self.ensure_batch_capacity(int(bsz))
+            self.ensure_sequence_capacity(end)
+            with torch.no_grad():
+                self.latent_cache[:bsz, int(start_pos):end].copy_(latent.detach())
+            latent_full = self.latent_cache[:bsz, :end].to(x.dtype)
+        else:
+            latent_full = latent
+        klen = int(latent_full.size(1))
+        k = self.k_up(latent_full).view(bsz, klen, self.num_heads, self.head_dim)
+        v = self.v_up(latent_full).view_as(k)
+        q_t, k_t, v_t = (t.transpose(1, 2) for t in (q, k, v))
+        key_pad = self._resolve_key_pad(int(start_pos), bsz, klen, x.device)
+        if key_pad is None and int(start_pos) == 0 and seqlen == klen:
+            out = F.scaled_dot_product_attention(q_t, k_t, v_t, is_causal=True)
+        else:
+            allow = torch.ones((seqlen, klen), dtype=torch.bool, device=x.device).tril(klen - seqlen)
+            allow = allow[None, None].expand(bsz, 1, seqlen, klen)
+            if key_pad is not None:
+                allow = allow & key_pad[:, None, None, :]
+            mask = torch.zeros((bsz, 1, seqlen, klen), dtype=q_t.dtype, device=x.device)
+            mask = mask.masked_fill(~allow, float("-inf"))
+            out = F.scaled_dot_product_attention(q_t, k_t, v_t, attn_mask=mask)
+        return self._gate_out(x, out.transpose(1, 2))
+
+    def _resolve_key_pad(self, start_pos: int, bsz: int, k_len: int, device):
+        """attention.py:585-600: which key positions are real."""
+        if int(start_pos) == 0:
+            mask = getattr(self, "_pad_mask", None)
+            self._key_pad = None if mask is None else mask[:bsz].bool().to(device)
+            return self._key_pad
+        cached = getattr(self, "_key_pad", None)
+        if cached is None:
+            return None
+        prompt_len = int(cached.size(1))
+        if k_len <= prompt_len:
+            return cached[:bsz, :k_len]
+        grown = torch.ones((bsz, k_len), dtype=torch.bool, device=device)
+        grown[:, :prompt_len] = cached[:bsz]
+        return grown
+
+    def forward_mixed(self, x: torch.Tensor, n_prefill_seqs: int, prefill_len: int,
+                      prefill_slots: torch.Tensor, decode_slots: torch.Tensor,
+                      decode_pos: torch.Tensor, max_decode_len: int) -> torch.Tensor:
+        """Packed step: rows [0, P*Tp) are P new sequences of Tp tokens
+        (causal attention over their own tokens, latents written to their
+        slots at positions 0..Tp-1); the remaining D rows are one token each
+        for running sequences at positions ``decode_pos`` (int64, device) of
+        slots ``decode_slots``, attending to their cached latents 0..pos.
+
+        The decode part attends in latent space: with NoPE, q . (W_k,h c) =
+        (W_k,h^T q) . c, so scores and the value sum are taken directly over
+        the cached latents c and W_v,h is applied after the sum -- the same
+        result as expanding K and V, without recomputing them every step.
+        ``max_decode_len`` (host int) bounds pos + 1 for every decode row.
+        """
+        n = int(x.size(0))
+        npre = int(n_prefill_seqs) * int(prefill_len)
+        nd = n - npre
+        h, d, r = self.num_heads, self.head_dim, self.kv_rank
+        q = self.q_up(self.q_norm(self.q_down(x))).view(n, h, d)
+        latent = self.kv_norm(self.kv_down(x))
+        cache = self.latent_cache
+        out = torch.empty((n, h, d), dtype=x.dtype, device=x.device)
+        if npre > 0:
+            P, T = int(n_prefill_seqs), int(prefill_len)
+            lat_p = latent[:npre].view(P, T, r)
+            cache[prefill_slots.long(), :T] = lat_p.to(cache.dtype)
+            k = self.k_up(lat_p).view(P, T, h, d).transpose(1, 2)
+            v = self.v_up(lat_p).view(P, T, h, d).transpose(1, 2)
+            o = F.scaled_dot_product_attention(q[:npre].view(P, T, h, d).transpose(1, 2), k, v,
+                                               is_causal=True)
+            out[:npre] = o.transpose(1, 2).reshape(npre, h, d)
+        if nd > 0:
+            slots = decode_slots.long()
+            cache[slots, decode_pos] = latent[npre:].to(cache.dtype)
+            L = int(max_decode_len)
+            lat = cache[slots, :L].to(x.dtype)                                   # [D, L, r]
+            w_k = self.k_up.weight.view(h, d, r).to(x.dtype)
+            w_v = self.v_up.weight.view(h, d, r).to(x.dtype)
+            qa = torch.bmm(q[npre:].transpose(0, 1).contiguous(), w_k).transpose(0, 1)   # [D, h, r]
+            scores = torch.bmm(qa.contiguous(), lat.transpose(1, 2).contiguous()).float()
+            scores = scores * (d ** -0.5)
+            valid = torch.arange(L, device=x.device)[None, :] <= decode_pos[:, None]
+            scores = scores.masked_fill(~valid[:, None, :], float("-inf"))
+            prob = scores.softmax(dim=-1).to(x.dtype)
+            ctx = torch.bmm(prob, lat)                                                 # [D, h, r]
+            o = torch.bmm(ctx.transpose(0, 1).contiguous(), w_v.transpose(1, 2).contiguous())
+            out[npre:] = o.transpose(0, 1)
+        return self._gate_out(x, out)
+
+
+class FeedForward(nn.Module):
+    """SiTU-GLU (blocks.py:12-27)."""
+
+    def __init__(self, args: ModelArgs) -> None:
+        super().__init__()
+        self.hidden = int(args.ffn_hidden)
+        self.gate_softcap = float(args.situ_gate_softcap)
+        self.up_softcap = float(args.situ_up_softcap)
+        self.gate_up_proj = RuntimeLinear(int(args.dim), 2 * self.hidden)
+        self.down_proj = RuntimeLinear(self.hidden, int(args.dim))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        gate, up = self.gate_up_proj(x).split(self.hidden, dim=-1)
+        bounded_gate = self.gate_softcap * torch.tanh(gate / self.gate_softcap)
+        bounded_up = self.up_softcap * torch.tanh(up / self.up_softcap)
+        return self.down_proj(bounded_gate * torch.sigmoid(gate) * bounded_up)
+
+
+class AttentionResidualMixer(nn.Module):
+    """Content-dependent mixing over completed depth blocks and a partial
+    block (blocks.py:30-48).  Works on any leading shape: values [..., blocks, dim]."""
+
+    def __init__(self, args: ModelArgs) -> None:
+        super().__init__()
+        self.norm = RMSNorm(args.dim, args.norm_eps)
+        self.query = RuntimeLinear(args.dim, 1)
+
+    def forward(self, partial_block: torch.Tensor, completed_blocks: torch.Tensor) -> torch.Tensor:
+        values = torch.cat((completed_blocks, partial_block.unsqueeze(-2)), dim=-2)
+        keys = self.norm(values)
+        scores = keys.float() @ self.query.weight.squeeze(0).float()
+        weights = scores.softmax(dim=-1).unsqueeze(-1).to(dtype=values.dtype)
+        return (weights * values).sum(dim=-2).to(dtype=values.dtype)
+
+
+class SophiaBlock(nn.Module):
+    """blocks.py:51-87."""
+
+    def __init__(self, args: ModelArgs, layer_idx: int) -> None:
+        super().__init__()
+        self.layer_idx = int(layer_idx)
+        self.layer_type = args.layer_type(self.layer_idx)
+        self.attn_norm = RMSNorm(args.dim, args.norm_eps)
+        self.attn = SophiaMLA(args) if self.layer_type == "mla" else SophiaKDA(args)
+        self.ffn_norm = RMSNorm(args.dim, args.norm_eps)
+        self.ffn = FeedForward(args)
+        self.attn_res_block_size = int(args.attn_res_block_size)
+        self.attn_residual = AttentionResidualMixer(args)
+        self.ffn_residual = AttentionResidualMixer(args)
+
+    def _mix(self, partial_block, completed_blocks, attn):
+        attn_input = self.attn_residual(partial_block, completed_blocks)
+        if self.layer_idx % self.attn_res_block_size == 0:
+            completed_blocks = torch.cat((completed_blocks, partial_block.unsqueeze(-2)), dim=-2)
+            partial_block = attn(self.attn_norm(attn_input))
+        else:
+            partial_block = partial_block + attn(self.attn_norm(attn_input))
+        ffn_input = self.ffn_residual(partial_block, completed_blocks)
+        partial_block = partial_block + self.ffn(self.ffn_norm(ffn_input))
+        return partial_block, completed_blocks
+
+    def forward(self, partial_block, completed_blocks, *, start_pos: int = 0):
+        return self._mix(partial_block, completed_blocks,
+                         lambda y: self.attn(y, start_pos=int(start_pos)))
+
+    def forward_mixed(self, partial_block, completed_blocks, step: dict):
+        if self.layer_type == "mla":
+            attn = lambda y: self.attn.forward_mixed(
+                y, step["n_prefill_seqs"], step["prefill_len"], step["prefill_slots"],
+                step["decode_slots"], step["decode_pos"], step["max_decode_len"])
+        else:
+            attn = lambda y: self.attn.forward_mixed(
+                y, step["n_prefill_seqs"] * step["prefill_len"], step["cu_prefill"],
+                step["prefill_slots"], step["decode_slots"])
+        return self._mix(partial_block, completed_blocks, attn)
+
+
+def init_weights(model: nn.Module, args: ModelArgs) -> None:
+    """transformer_setup.py:39-64: N(0, 0.02) for every linear, embedding and
+    conv weight; residual-branch outputs at 0.02 / sqrt(2 n_layers); attention
+    residual queries zero."""
+    base_std = float(args.initializer_range)
+    residual_std = base_std / math.sqrt(2.0 * max(int(args.n_layers), 1))
+    from .kda import CausalDepthwiseConv1d
+    for module in model.modules():
+        if isinstance(module, (nn.Linear, RuntimeLinear)):
+            nn.init.normal_(module.weight, mean=0.0, std=base_std)
+            if module.bias is not None:
+                nn.init.zeros_(module.bias)
+        elif isinstance(module, nn.Embedding):
+            nn.init.normal_(module.weight, mean=0.0, std=base_std)
+        elif isinstance(module, CausalDepthwiseConv1d):
+            nn.init.normal_(module.weight, mean=0.0, std=base_std)
+    for layer in getattr(model, "layers", ()):
+        nn.init.normal_(layer.attn.o_proj.weight, mean=0.0, std=residual_std)
+        nn.init.normal_(layer.ffn.down_proj.weight, mean=0.0, std=residual_std)
+        nn.init.zeros_(layer.attn_residual.query.weight)
+        nn.init.zeros_(layer.ffn_residual.query.weight)
+    nn.init.zeros_(model.output_attn_residual.query.weight)
+
+
+class Transformer(nn.Module):
+    """The [KDA, KDA, KDA, MLA] x (n_layers / 4) hybrid decoder
+    (transformer.py:17-207, transformer_setup.py:67-79), tied embedding."""
+
+    def __init__(self, args: ModelArgs) -> None:
+        super().__init__()
+        self.args = args
+        self.tok_embeddings = nn.Embedding(args.vocab_size, args.dim)
+        self.layers = nn.ModuleList([SophiaBlock(args, i) for i in range(args.n_layers)])
+        self.norm = RMSNorm(args.dim, args.norm_eps)
+        self.output_attn_residual = AttentionResidualMixer(args)
+        self.output = RuntimeLinear(args.dim, args.vocab_size)
+        self.output.weight = self.tok_embeddings.weight  # tie_word_embeddings
+        init_weights(self, args)
+
+    def reset_runtime_cache(self) -> None:
+        for layer in self.layers:
+            layer.attn.reset()
+
+    def _validate(self, input_ids: torch.Tensor, start_pos: int) -> None:
+        """transformer.py:146-160."""
+        if input_ids.dim() != 2:
+            raise ValueError("input_ids must be [B, S]")
+        if int(start_pos) < 0:
+            raise ValueError(f"start_pos must be >= 0, got {start_pos}")
+        if int(start_pos) > 0 and int(input_ids.size(1)) > 1:
+            raise ValueError("incremental forward accepts one token when start_pos > 0")
+        if int(start_pos) + int(input_ids.size(1)) > int(self.args.max_seq_len):
+            raise ValueError("sequence exceeds max_seq_len")
+
+    def forward(self, input_ids: torch.Tensor, start_pos: int = 0) -> torch.Tensor:
+        """transformer.py:169-207: logits [B, S, vocab]."""
+        _require_gpu(input_ids)
+        self._validate(input_ids, start_pos)
+        hidden = self.tok_embeddings(input_ids)
+        completed = hidden.new_empty(int(hidden.size(0)), int(hidden.size(1)), 0, int(hidden.size(2)))
+        for layer in self.layers:
+            hidden, completed = layer(hidden, completed, start_pos=start_pos)
+        hidden = self.output_attn_residual(hidden, completed)
+        return self.output(self.norm(hidden))
+
+    def forward_mixed(self, prefill_ids: torch.Tensor, decode_ids: torch.Tensor, *,
+                      prefill_slots: torch.Tensor, decode_slots: torch.Tensor,
+                      decode_pos: torch.Tensor, max_decode_len: int,
+                      cu_prefill: torch.Tensor | None = None) -> torch.Tensor:
+        """One continuous-batching step: ``prefill_ids`` [P, Tp] new sequences
+        (cache slots ``prefill_slots`` [P] int32), ``decode_ids`` [D] one token
+        for each running sequence (slots ``decode_slots`` [D] int32, positions
+        ``decode_pos`` [D] int64 = tokens already cached).  All tensors on the
+        device; nothing is read back on the host, so the step is capturable.
+        Returns the logits of each sequence's last token, [P + D, vocab]
+        (prefill sequences first)."""
+        _require_gpu(decode_ids)
+        P, T = int(prefill_ids.size(0)), int(prefill_ids.size(1))
+        D = int(decode_ids.size(0))
+        if cu_prefill is None:
+            cu_prefill = torch.arange(0, (P + 1) * T, T, dtype=torch.int32, device=decode_ids.device)
+        step = dict(n_prefill_seqs=P, prefill_len=T, prefill_slots=prefill_slots,
+                    decode_slots=decode_slots, decode_pos=decode_pos,
+                    max_decode_len=int(max_decode_len), cu_prefill=cu_prefill)
+        ids = torch.cat((prefill_ids.reshape(-1), decode_ids.reshape(-1)))
+        hidden = self.tok_embeddings(ids)
+        completed = hidden.new_empty(int(hidden.size(0)), 0, int(hidden.size(1)))
+        for layer in self.layers:
+            hidden, completed = layer.forward_mixed(hidden, completed, step)
+        last = torch.cat((torch.arange(T - 1, P * T, T, device=hidden.device),
+                          torch.arange(P * T, P * T + D, device=hidden.device)))
+        hidden = self.output_attn_residual(hidden[last], completed[last])
+        return self.output(self.norm(hidden))
+
+
+class MixedStepGraph:
+    """A captured ``Transformer.forward_mixed`` step with static inputs.
+
+    Warm-up runs on a side stream, then one capture (the pattern of
+    sm120_graph_runner.py:318-371); ``run`` copies the step's inputs into the
+    static buffers and replays.  Every call advances the caches of the
+    sequences it names, like the eager step.
+    """
+
+    def __init__(self, model: Transformer, n_prefill_seqs: int, prefill_len: int,
+                 n_decode: int, max_decode_len: int, *, warmup: int = 2,
+                 example: dict | None = None) -> None:
+        dev = model.tok_embeddings.weight.device
+        self.model = model
+        self.max_decode_len = int(max_decode_len)
+        P, T, D = int(n_prefill_seqs), int(prefill_len), int(n_decode)
+        self.prefill_ids = torch.zeros((P, T), dtype=torch.long, device=dev)
+        self.decode_ids = torch.zeros((D,), dtype=torch.long, device=dev)
+        self.prefill_slots = torch.zeros((P,), dtype=torch.int32, device=dev)
+        self.decode_slots = torch.zeros((D,), dtype=torch.int32, device=dev)
+        self.decode_pos = torch.zeros((D,), dtype=torch.long, device=dev)
+        self.cu_prefill = torch.arange(0, (P + 1) * T, T, dtype=torch.int32, device=dev)
+        if example is not None:
+            self._load(example)
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side), torch.no_grad():
+            for _ in range(int(warmup)):
+                self._step()
+        torch.cuda.current_stream(dev).wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph), torch.no_grad():
+            self.logits = self._step()
+
+    def _step(self) -> torch.Tensor:
+        return self.model.forward_mixed(
+            self.prefill_ids, self.decode_ids, prefill_slots=self.prefill_slots,
+            decode_slots=self.decode_slots, decode_pos=self.decode_pos,
+            max_decode_len=self.max_decode_len, cu_prefill=self.cu_prefill)
+
+    def _load(self, inputs: dict) -> None:
+        for name in ("prefill_ids", "decode_ids", "prefill_slots", "decode_slots", "decode_pos"):
+            if name in inputs:
+                getattr(self, name).copy_(inputs[name], non_blocking=True)
+
+    def run(self, **inputs) -> torch.Tensor:
+        """Copy the given inputs (same names and shapes as the buffers) and
+        replay; returns the static logits buffer [P + D, vocab]."""
+        self._load(inputs)
+        self.graph.replay()
+        return self.logits
+
+
+__all__ = ["AttentionResidualMixer", "FeedForward", "MixedStepGraph", "SophiaBlock",
+           "SophiaMLA", "Transformer", "init_weights"]

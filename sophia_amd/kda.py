@@ -407,6 +407,59 @@ class SophiaKDA(nn.Module):
         return out.view(1, n, self.dim) if squeeze else out
 
 
+    def forward_mixed(self, x: torch.Tensor, n_prefill: int, cu_prefill: torch.Tensor,
+                      prefill_slots: torch.Tensor | None, decode_slots: torch.Tensor | None
+                      ) -> torch.Tensor:
+        """One continuous-batching step over packed rows x [N, dim].
+
+        Rows [0, n_prefill) hold new sequences delimited by int32
+        ``cu_prefill`` (device, offsets from row 0); they start from empty
+        caches and leave their final recurrent and conv state in cache slots
+        ``prefill_slots``.  Rows [n_prefill, N) are one decode token each for
+        the sequences in ``decode_slots``, whose caches are read and advanced
+        in place (decode kernels).  One fused projection GEMM and one output
+        epilogue cover all rows.  Returns [N, dim].
+        """
+        _require_gpu(x)
+        x2 = x.reshape(-1, self.dim)
+        n = int(x2.size(0))
+        n_prefill = int(n_prefill)
+        n_decode = n - n_prefill
+        if not self.use_cache:
+            raise RuntimeError("forward_mixed needs use_cache=True (it writes cache slots)")
+        qkv, dd, beta_logits, gate_logits = self._project(x2)
+        i, h, d = self.inner_dim, self.num_heads, self.head_dim
+        hist = self.conv_kernel - 1
+        conv_state = (self.conv_state.view(self.conv_state.size(0), 3 * i, hist)
+                      if hist > 0 else None)
+        conv_w = self._conv_weight()
+        conv_out = torch.empty((n, 3 * i), dtype=qkv.dtype, device=qkv.device)
+        if n_prefill > 0:
+            ops.short_conv_fwd(qkv[:n_prefill], conv_w, cu_prefill, conv_state=conv_state,
+                               state_slots=prefill_slots, read_history=False,
+                               write_history=hist > 0, out=conv_out[:n_prefill])
+        if n_decode > 0:
+            ops.short_conv_step(qkv[n_prefill:], conv_w, conv_state, state_slots=decode_slots,
+                                read_history=True, out=conv_out[n_prefill:])
+        q = conv_out[:, :i].unflatten(1, (h, d))
+        k = conv_out[:, i: 2 * i].unflatten(1, (h, d))
+        v = conv_out[:, 2 * i:].unflatten(1, (h, d))
+        decay = self.decay_up(dd).view(n, h, d)
+        o = torch.empty((n, h, d), dtype=x2.dtype, device=x2.device)
+        gate_args = dict(A_log=self.A_log, dt_bias=self.dt_bias, lower_bound=self.lower_bound)
+        if n_prefill > 0:
+            ops.kda_chunk_fwd(q[:n_prefill], k[:n_prefill], v[:n_prefill], decay[:n_prefill],
+                              beta_logits[:n_prefill], cu_prefill, initial_state=None,
+                              final_state=self.recurrent_state, state_slots=prefill_slots,
+                              out=o[:n_prefill], **gate_args)
+        if n_decode > 0:
+            ops.kda_decode_step(q[n_prefill:], k[n_prefill:], v[n_prefill:], decay[n_prefill:],
+                                beta_logits[n_prefill:], self.recurrent_state,
+                                state_slots=decode_slots, read_state=True, out=o[n_prefill:],
+                                **gate_args)
+        return self._output(o, gate_logits, x2.dtype)
+
+
 def set_pad_mask(model: nn.Module, mask: torch.Tensor | None) -> None:
     """attention.py:660-670: hang a [B, T] bool mask (True = real token) on
     every KDA mixer, or clear it."""

@@ -1,0 +1,150 @@
+"""GPU parity of the hybrid decoder (sophia_amd.decoder) against the oracle's
+restatement of the reference decoder (transformer.py:169-207, blocks.py,
+attention.py:423-657), on a small seeded configuration in fp32, plus the
+continuous-batching mixed step and its HIP-graph capture.
+
+Tolerance: max|y - y_ref| / max|y_ref| <= 2e-2 on the logits against the
+float64 oracle.  Graph replays are checked against the eager step at the same
+cache state, with eager work and host synchronisation between replays.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import decoder_oracle as do
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 2e-2
+SMALL = dict(vocab_size=512, n_layers=4, ffn_hidden=320, mla_q_rank=64, mla_kv_rank=32, dim=256,
+             num_heads=2, max_seq_len=128, max_batch_size=6)
+
+
+def _dev():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+    return torch.device("cuda:0")
+
+
+def _rel(a, b) -> float:
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    return float(np.max(np.abs(a - b)) / max(float(np.max(np.abs(b))), 1e-30))
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _model(dev, seed=0):
+    from sophia_amd.config import ModelArgs
+    from sophia_amd.decoder import Transformer
+    torch.manual_seed(seed)
+    args = ModelArgs(**SMALL)
+    model = Transformer(args)
+    # non-zero residual queries so the depth mixing is exercised
+    with torch.no_grad():
+        for m in model.modules():
+            if m.__class__.__name__ == "AttentionResidualMixer":
+                m.query.weight.normal_(0.0, 0.05)
+    model = model.to(dev)
+    params = {k: _np(v).astype(np.float64) for k, v in model.state_dict().items()}
+    cfg = dict(n_layers=4, num_heads=2, norm_eps=1e-5, attn_res_block_size=4,
+               situ_gate_softcap=4.0, situ_up_softcap=25.0, mla_kv_rank=32, short_conv_kernel=4)
+    return model, params, cfg
+
+
+def test_decoder_forward_matches_oracle_and_cached_decode():
+    dev = _dev()
+    model, params, cfg = _model(dev)
+    ids = torch.randint(0, 512, (2, 40), generator=torch.Generator().manual_seed(1))
+    with torch.no_grad():
+        logits = model(ids.to(dev), start_pos=0)
+        model.reset_runtime_cache()
+        steps = [model(ids[:, :33].to(dev), start_pos=0)]
+        for t in range(33, 40):
+            steps.append(model(ids[:, t:t + 1].to(dev), start_pos=t))
+    ref = do.decoder_forward(params, ids.numpy(), cfg=cfg)
+    err = _rel(_np(logits), ref)
+    print(f"decoder logits rel err {err:.2e}")
+    assert err < REL_TOL
+    assert _rel(_np(torch.cat(steps, 1)), ref) < REL_TOL
+    with pytest.raises(ValueError):
+        model(ids[:, :2].to(dev), start_pos=3)   # transformer.py:150-153
+
+
+def _mixed_case(dev, model):
+    """Three running sequences (histories of 37, 12 and 1 tokens in slots 0-2)
+    and two new 30-token sequences (slots 3, 4)."""
+    gen = torch.Generator().manual_seed(2)
+    hist = [torch.randint(0, 512, (n,), generator=gen) for n in (37, 12, 1)]
+    new_tok = torch.randint(0, 512, (3,), generator=gen)
+    prefill = torch.randint(0, 512, (2, 30), generator=gen)
+    i32 = lambda xs: torch.tensor(xs, dtype=torch.int32, device=dev)
+    with torch.no_grad():
+        model.reset_runtime_cache()
+        for slot, h in enumerate(hist):
+            model.forward_mixed(h[None].to(dev), torch.empty(0, dtype=torch.long, device=dev),
+                                prefill_slots=i32([slot]), decode_slots=i32([]),
+                                decode_pos=torch.empty(0, dtype=torch.long, device=dev),
+                                max_decode_len=1)
+    step = dict(prefill_ids=prefill.to(dev), decode_ids=new_tok.to(dev),
+                prefill_slots=i32([3, 4]), decode_slots=i32([0, 1, 2]),
+                decode_pos=torch.tensor([37, 12, 1], dtype=torch.long, device=dev))
+    full = [prefill[0], prefill[1]] + [torch.cat([h, new_tok[i:i + 1]]) for i, h in enumerate(hist)]
+    return step, full
+
+
+def _snapshot(model):
+    return [(layer.attn.recurrent_state.clone(), layer.attn.conv_state.clone())
+            if layer.layer_type == "kda" else (layer.attn.latent_cache.clone(),)
+            for layer in model.layers]
+
+
+def _restore(model, snap):
+    for layer, s in zip(model.layers, snap):
+        if layer.layer_type == "kda":
+            layer.attn.recurrent_state.copy_(s[0])
+            layer.attn.conv_state.copy_(s[1])
+        else:
+            layer.attn.latent_cache.copy_(s[0])
+
+
+def test_mixed_step_matches_each_sequence_run_alone():
+    dev = _dev()
+    model, params, cfg = _model(dev)
+    step, full = _mixed_case(dev, model)
+    with torch.no_grad():
+        logits = model.forward_mixed(max_decode_len=40, **step)
+    assert tuple(logits.shape) == (5, 512)
+    for row, seq in enumerate(full):
+        ref = do.decoder_forward(params, seq.numpy()[None], cfg=cfg)[0, -1]
+        err = _rel(_np(logits[row]), ref)
+        assert err < REL_TOL, f"sequence {row}: {err}"
+
+
+def test_mixed_step_graph_replays_match_eager():
+    from sophia_amd.decoder import MixedStepGraph
+    dev = _dev()
+    model, _, _ = _model(dev)
+    step, _ = _mixed_case(dev, model)
+    start = _snapshot(model)
+    with torch.no_grad():
+        eager = model.forward_mixed(max_decode_len=40, **step).clone()
+        after = _snapshot(model)
+    _restore(model, start)
+    graph = MixedStepGraph(model, 2, 30, 3, 40, example=step)
+    for replay in range(3):
+        _restore(model, start)
+        torch.cuda.synchronize()
+        out = graph.run(**step)
+        torch.cuda.synchronize()
+        assert torch.allclose(out, eager, rtol=1e-4, atol=1e-4), f"replay {replay}"
+        for a, b in zip(_snapshot(model), after):
+            for x, y in zip(a, b):
+                assert torch.allclose(x, y, rtol=1e-4, atol=1e-5), f"replay {replay} caches"
+        with torch.no_grad():  # eager work between replays
+            model(torch.zeros(1, 3, dtype=torch.long, device=dev), start_pos=0)
