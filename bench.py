@@ -121,13 +121,88 @@ def copy_bandwidth(torch, dev, stream, nbytes: int = 1 << 30) -> float:
     return 2 * nbytes / (float(np.median(per)) / 1e3) / 1e9
 
 
+def mixed_step_bench(torch, dev, stream, steps: int, warmup: int, seed: int = 4) -> dict:
+    """The whole hybrid decoder (28 layers [KDA, KDA, KDA, MLA] x 7, dim 1536,
+    16 heads x 128, SiTU-GLU 3968, MLA ranks 384 / 128, vocab 65,536, tied;
+    random init, bf16 GEMM weights, fp32 caches) in one continuous-batching
+    step: 16 new sequences of 1,024 tokens prefilled together with one decode
+    token for each of 240 running sequences (cached lengths U[1, 1023],
+    seeded; random latent caches, zero recurrent state).  The step is
+    captured in a HIP graph after two warm-up runs on a side stream and
+    replayed; the eager step is timed beside it."""
+    from sophia_amd.config import ModelArgs
+    from sophia_amd.decoder import MixedStepGraph, Transformer
+    from sophia_amd.kda import RuntimeLinear
+
+    P, T, D, L = 16, 1024, 240, 1024
+    args = ModelArgs(max_batch_size=P + D, max_seq_len=2048)
+    torch.manual_seed(seed)
+    with torch.device(dev):
+        model = Transformer(args)
+    model.cast_weights_(torch.bfloat16).eval()
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    for layer in model.layers:
+        if layer.layer_type == "mla":
+            layer.attn.latent_cache.normal_(generator=gen)
+    cpu_gen = torch.Generator().manual_seed(seed)
+    step = dict(
+        prefill_ids=torch.randint(0, args.vocab_size, (P, T), generator=cpu_gen).to(dev),
+        decode_ids=torch.randint(0, args.vocab_size, (D,), generator=cpu_gen).to(dev),
+        prefill_slots=torch.arange(P, dtype=torch.int32).to(dev),
+        decode_slots=torch.arange(P, P + D, dtype=torch.int32).to(dev),
+        decode_pos=torch.randint(1, L, (D,), generator=cpu_gen).to(dev))
+
+    def eager():
+        with torch.no_grad():
+            return model.forward_mixed(max_decode_len=L, **step)
+
+    _, eper = time_events(torch, eager, max(steps // 4, 3), 2, stream)
+    graph = MixedStepGraph(model, P, T, D, L, warmup=2, example=step)
+    _, gper = time_events(torch, graph.run, steps, warmup, stream)
+    if not torch.isfinite(graph.logits.float()).all():
+        raise RuntimeError("non-finite logits from the captured mixed step")
+    gms, ems = float(np.mean(gper)), float(np.mean(eper))
+    tokens = P * T + D
+
+    # Work per step: every per-token GEMM (MLA k_up / v_up on prefill rows
+    # only; decode rows attend in latent space), the last-token head, causal
+    # MLA attention, the absorbed decode attention over L cached latents, and
+    # the KDA chunk core on the prefill rows.  Decode recurrences (HBM-bound)
+    # are not counted.
+    h, d, r = args.num_heads, args.head_dim, args.mla_kv_rank
+    flops = 0.0
+    for layer in model.layers:
+        for name, mod in layer.named_modules():
+            if not isinstance(mod, RuntimeLinear) or name.endswith("query"):
+                continue
+            rows = P * T if name in ("attn.k_up", "attn.v_up") else tokens
+            flops += 2.0 * rows * mod.weight.numel()
+        if layer.layer_type == "mla":
+            flops += 2.0 * P * h * T * T * d + D * h * 4.0 * (d * r + L * r)
+        else:
+            flops += P * T * PREFILL_FLOPS_PER_TOKEN
+    flops += 2.0 * (P + D) * args.vocab_size * args.dim
+    tflops = flops / (gms / 1e3) / 1e12
+    out = {"workload": "hybrid decoder, 28 layers [KDA,KDA,KDA,MLA]x7, dim 1536, bf16, one "
+                       "mixed step: 16x1024 prefill + 240x1 decode, HIP-graph replay",
+           "tokens_per_step": tokens, "ms_per_step": round(gms, 3),
+           "tokens_per_s": round(tokens / (gms / 1e3), 1),
+           "eager_ms_per_step": round(ems, 3), "graph_speedup": round(ems / gms, 3),
+           "approx_tflops": round(tflops, 1),
+           "frac_of_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4),
+           "flops_per_step": flops, "steps": steps}
+    del graph, model
+    torch.cuda.empty_cache()
+    return out
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["all", "prefill", "conv", "decode", "copy"], default="all",
+    ap.add_argument("--only", choices=["all", "prefill", "conv", "decode", "copy", "mixed"], default="all",
                     help="run one workload only (for kernel profiling); the JSON line then "
                          "carries that workload's fields alone")
     args = ap.parse_args(argv)
@@ -258,6 +333,9 @@ def main(argv=None) -> int:
                             "kernel": "kda_decode_kernel"}
     del dstate
 
+    if args.only in ("all", "mixed"):
+        result["mixed_step"] = mixed_step_bench(torch, dev, stream, max(args.steps // 2, 5),
+                                                max(args.warmup // 2, 2))
     if args.only == "all":
         result["hbm_copy_GBps"] = round(copy_bandwidth(torch, dev, stream), 1)
     if not args.no_cpu and args.only == "all":

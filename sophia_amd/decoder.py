@@ -324,6 +324,17 @@ class Transformer(nn.Module):
         for layer in self.layers:
             layer.attn.reset()
 
+    def cast_weights_(self, dtype: torch.dtype) -> "Transformer":
+        """Cast the GEMM weights (every RuntimeLinear and the tied embedding)
+        to ``dtype`` in place.  Norm weights, A_log, dt_bias, conv taps and the
+        recurrent, conv and latent caches stay fp32, as the reference keeps
+        them (attention.py:98-180,469-476)."""
+        for module in self.modules():
+            if isinstance(module, (RuntimeLinear, nn.Embedding)):
+                for param in module.parameters(recurse=False):
+                    param.data = param.data.to(dtype)
+        return self
+
     def _validate(self, input_ids: torch.Tensor, start_pos: int) -> None:
         """transformer.py:146-160."""
         if input_ids.dim() != 2:
