@@ -23,11 +23,12 @@
 //    fragments -W, Q e^G, (K e^{G_C-G})^T, A_qk (bf16, in the exact per-lane
 //    order of v_mfma_f32_16x16x32_bf16 A operands), Ut (bf16, C-tile order)
 //    and e^{G_C} (fp32) to the workspace.
-//  * kda_chunk_scan_kernel (one wavefront per sequence x head x 32 value
-//    columns): walks the chunks of its sequence with the fp32 state held in
-//    MFMA accumulator tiles.  The C tile of one product is reused as the B
-//    operand of the next (16x16x32 operands pair two C tiles; the A operands
-//    carry the matching k permutation), so S and U never leave registers.
+//  * kda_chunk_scan_kernel (one work-group of 8 wavefronts per sequence x
+//    head x 128/splits value columns): walks the chunks of its sequence.  Four
+//    wavefronts hold the fp32 state in MFMA accumulator tiles and update it;
+//    four form U and O.  S and U pass between them through LDS as bf16 MFMA
+//    operands (16x16x32 operands pair two C tiles; the A operands carry the
+//    matching k permutation).
 #include "common.hpp"
 
 namespace sophia {
@@ -48,6 +49,9 @@ constexpr size_t kOffG = kOffU + 32 * 64 * 8;      // e^{G_C} [128] fp32
 constexpr size_t kRecBytes = kOffG + kD * 4;       // 74240
 
 inline int64_t max_chunks(int64_t total, int n) { return total / kC + n; }
+// Scratch rows for the stores of chunk rows past the end of a sequence
+// (64 rows x 128 fp32 columns, contents never read).
+constexpr size_t kTrashBytes = kC * kD * 4;
 inline size_t header_bytes(int64_t total, int n) {
   size_t b = sizeof(int32_t) * (static_cast<size_t>(n) + 1 + static_cast<size_t>(max_chunks(total, n)));
   return (b + 255) & ~static_cast<size_t>(255);
@@ -631,6 +635,7 @@ struct ScanArgs {
   void *o;
   int64_t o_stride;
   int splits;   // blocks per (sequence, head): 128 / NVB
+  void *trash;  // kTrashBytes of workspace: destination of rows past a sequence end
 };
 
 // ---- scan kernel: two roles per work-group ----------------------------------
@@ -661,19 +666,24 @@ struct SFrags {
   f4 gm[2];     // e^{G_C} of state rows 32sw + 16mi + 4gq + e
 };
 
+// The operands used before the U barrier (-W, Q e^G, Ut) ...
 template <int NT>
-__device__ __forceinline__ void load_uo(UOFrags<NT> &f, const uint8_t *rec, int w, int l, int nt0) {
+__device__ __forceinline__ void load_uo_main(UOFrags<NT> &f, const uint8_t *rec, int w, int l, int nt0) {
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
     f.wn[ks] = *reinterpret_cast<const u4 *>(rec + kOffW + ((w * 4 + ks) * 64 + l) * 16);
     f.qb[ks] = *reinterpret_cast<const u4 *>(rec + kOffQ + ((w * 4 + ks) * 64 + l) * 16);
   }
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks)
-    f.aq[ks] = *reinterpret_cast<const u4 *>(rec + kOffA + ((w * 2 + ks) * 64 + l) * 16);
-#pragma unroll
   for (int nt = 0; nt < NT; ++nt)
     f.ut[nt] = *reinterpret_cast<const u2 *>(rec + kOffU + ((w * 8 + nt0 + nt) * 64 + l) * 8);
+}
+// ... and A_qk, used after it.
+template <int NT>
+__device__ __forceinline__ void load_uo_aq(UOFrags<NT> &f, const uint8_t *rec, int w, int l) {
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+    f.aq[ks] = *reinterpret_cast<const u4 *>(rec + kOffA + ((w * 2 + ks) * 64 + l) * 16);
 }
 
 __device__ __forceinline__ void load_s(SFrags &f, const uint8_t *rec, int sw, int l, int gq) {
@@ -709,13 +719,18 @@ struct ScanGeom {
   size_t rec_stride;
 };
 
-// One chunk of the U/O role (two barriers).
-template <int NT, int O_DT>
-__device__ __forceinline__ void uo_step(const ScanArgs &p, const ScanGeom &g, const UOFrags<NT> &f,
-                                        const uint8_t *sSb, uint8_t *sUb, int w, int l, int cc) {
-  const int lr = l & 15, gq = l >> 4;
+// One chunk of the U/O role, in two parts around the U barrier (two
+// barriers in all).
+//
+// O is formed transposed: an A operand fragment of X (m x k) is, register for
+// register, the B operand fragment of X^T, so swapping the operands of the
+// products gives O^T = S^T (Q e^G)^T + U^T A_qk^T with the same fragments.  The
+// O^T C tile puts 4 consecutive value columns of one token row in each lane:
+// one 8-byte (bf16) or 16-byte (fp32) store per tile.
+template <int NT>
+__device__ __forceinline__ void uo_pre(const UOFrags<NT> &f, f4 (&O)[NT], const uint8_t *sSb, uint8_t *sUb,
+                                       int w, int l) {
   lds_barrier();  // S of this chunk is published
-  f4 U[NT], O[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     bf8 sb[4];
@@ -727,35 +742,41 @@ __device__ __forceinline__ void uo_step(const ScanArgs &p, const ScanGeom &g, co
             __uint_as_float(uw.y << 16), __uint_as_float(uw.y & 0xffff0000u)};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) u = mfma32(bits_to_bf8(f.wn[ks]), sb[ks], u);
-    U[nt] = u;
     // U rows 16w.. are half (w & 1) of K-step w / 2 of the U operand.
     *reinterpret_cast<u2 *>(sUb + (((w >> 1) * NT + nt) * 64 + l) * 16 + (w & 1) * 8) = pack4_bf16(u);
     f4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) o = mfma32(bits_to_bf8(f.qb[ks]), sb[ks], o);
-    O[nt] = o;
+    for (int ks = 0; ks < 4; ++ks) o = mfma32(sb[ks], bits_to_bf8(f.qb[ks]), o);
+    O[nt] = o;   // O^T tiles: value columns 16(nt0 + nt) + 4gq + e, token row 16w + lr
   }
   lds_barrier();  // U is published
+}
+
+// Second part: O^T += U^T A_qk^T, then the stores.  Stores are never under a
+// branch (a store under a branch makes the compiler drain the loads in flight
+// at the join): rows past the end of the sequence go to a scratch row block
+// in the workspace instead.
+template <int NT, int O_DT>
+__device__ __forceinline__ void uo_post(const ScanArgs &p, const ScanGeom &g, const UOFrags<NT> &f,
+                                        f4 (&O)[NT], const uint8_t *sUb, int w, int l, int cc) {
+  const int lr = l & 15, gq = l >> 4;
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const bf8 u0 = bits_to_bf8(*reinterpret_cast<const u4 *>(sUb + ((0 * NT + nt) * 64 + l) * 16));
-    O[nt] = mfma32(bits_to_bf8(f.aq[0]), u0, O[nt]);
+    O[nt] = mfma32(u0, bits_to_bf8(f.aq[0]), O[nt]);
     if (w >= 2) {  // A_qk is lower triangular
       const bf8 u1 = bits_to_bf8(*reinterpret_cast<const u4 *>(sUb + ((1 * NT + nt) * 64 + l) * 16));
-      O[nt] = mfma32(bits_to_bf8(f.aq[1]), u1, O[nt]);
+      O[nt] = mfma32(u1, bits_to_bf8(f.aq[1]), O[nt]);
     }
   }
   const int64_t tok0 = g.seq_a + static_cast<int64_t>(cc) * kC;
-  const int rows_valid = static_cast<int>(imin64(kC, g.seq_b - tok0));
+  const int r = 16 * w + lr;
+  const bool row_ok = static_cast<int64_t>(r) < g.seq_b - tok0;
+  const int64_t col = static_cast<int64_t>(g.h) * kD + 16 * g.nt0 + 4 * gq;
+  const int64_t elem = row_ok ? (tok0 + r) * p.o_stride + col : static_cast<int64_t>(r) * kD + 16 * g.nt0 + 4 * gq;
+  void *dst = row_ok ? p.o : p.trash;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int r = 16 * w + 4 * gq + e;
-    if (r < rows_valid) {
-      const int64_t base = (tok0 + r) * p.o_stride + static_cast<int64_t>(g.h) * kD + 16 * g.nt0 + lr;
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) store_elem(p.o, base + 16 * nt, O_DT, O[nt][e]);
-    }
-  }
+  for (int nt = 0; nt < NT; ++nt) store4(dst, elem + 16 * nt, O_DT, O[nt]);
 }
 
 // Publishes this wave's state rows as K-step sw of the bf16 B operand of S.
@@ -773,12 +794,12 @@ __device__ __forceinline__ void publish_state(const f4 (&S)[2][NT], uint8_t *sSb
   }
 }
 
-// One chunk of the state role (two barriers): S <- Diag(e^{G_C}) S + Kbar^T U,
-// then publish S for the next chunk.
+// Second half of a chunk of the state role: S <- Diag(e^{G_C}) S + Kbar^T U
+// once U is published, then publish S for the next chunk.  (The first half is
+// the barrier at which the U/O role picks S up.)
 template <int NT>
-__device__ __forceinline__ void state_step(const SFrags &f, f4 (&S)[2][NT], uint8_t *sSb,
-                                           const uint8_t *sUb, int sw, int l) {
-  lds_barrier();  // S published (by this role, before)
+__device__ __forceinline__ void state_update(const SFrags &f, f4 (&S)[2][NT], uint8_t *sSb,
+                                             const uint8_t *sUb, int sw, int l) {
   lds_barrier();  // U published
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
@@ -798,13 +819,20 @@ __device__ __forceinline__ void state_step(const SFrags &f, f4 (&S)[2][NT], uint
 }
 
 // One work-group of 8 wavefronts per (sequence, head, NVB value columns).
-// Record operands of chunk cc + ring are loaded as soon as chunk cc has been
-// consumed, so every load has ring - 1 chunk steps to arrive.  The buffer of
-// the next step is waited for right after the newest loads are issued
-// (touch), where the wait can leave exactly those in flight; a wait placed by
-// the compiler at a loop header would drain everything.  Loads are never
+// Record operands stream through per-role rings of register buffers, several
+// chunks ahead.  A wave that issues loads faster than the CU's memory queue
+// drains them stalls at the load, and a wave stalled there issues nothing
+// else, so each role refills its ring in the part of the chunk where the
+// other role is on the critical path: the state waves after the S barrier
+// (while U is formed), the U/O waves after the U barrier (while S is
+// updated).  The buffer of the next step is waited for right after the newest
+// loads are issued (touch), where the wait can leave exactly those in flight;
+// a wait placed by the compiler at a loop header would drain everything.  Loads are never
 // under a branch (the compiler then drains every load at the join): past the
-// last chunk they re-read the last chunk, unused.
+// last chunk they re-read the last chunk, unused.  The prologue issues the
+// ring buffers strictly in order: the wait counts in the loop are the minimum
+// over every path into it, so a prologue that interleaves the loads of two
+// buffers makes every later step wait for its newest buffer too.
 template <int NVB, int O_DT>
 __global__ __launch_bounds__(kScanThreads) void kda_chunk_scan_kernel(ScanArgs p) {
   constexpr int NT = NVB / 16;               // 16-column tiles per work-group
@@ -841,13 +869,25 @@ __global__ __launch_bounds__(kScanThreads) void kda_chunk_scan_kernel(ScanArgs p
     constexpr int R = ring_uo<NT>();
     UOFrags<NT> f[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) load_uo<NT>(f[r], g.rec0 + min(r, last) * g.rec_stride, w, l, g.nt0);
+    for (int r = 0; r < R; ++r) {
+      const uint8_t *rec = g.rec0 + min(r, last) * g.rec_stride;
+      load_uo_main<NT>(f[r], rec, w, l, g.nt0);
+      load_uo_aq<NT>(f[r], rec, w, l);
+      __builtin_amdgcn_sched_barrier(0);  // keep the ring order (see above)
+    }
     touch<NT>(f[0]);
     for (int cc = 0; cc < nchunks; cc += R) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        if (cc + r < nchunks) uo_step<NT, O_DT>(p, g, f[r], sSb, sUb, w, l, cc + r);
-        load_uo<NT>(f[r], g.rec0 + min(cc + r + R, last) * g.rec_stride, w, l, g.nt0);
+        const bool live = cc + r < nchunks;
+        const uint8_t *rec = g.rec0 + min(cc + r + R, last) * g.rec_stride;
+        f4 O[NT];
+        if (live) uo_pre<NT>(f[r], O, sSb, sUb, w, l);
+        // Refill while the state role works: the loads may wait for memory
+        // queue space here, off the critical path.
+        load_uo_main<NT>(f[r], rec, w, l, g.nt0);
+        if (live) uo_post<NT, O_DT>(p, g, f[r], O, sUb, w, l, cc + r);
+        load_uo_aq<NT>(f[r], rec, w, l);
         touch<NT>(f[(r + 1) % R]);
       }
     }
@@ -876,16 +916,23 @@ __global__ __launch_bounds__(kScanThreads) void kda_chunk_scan_kernel(ScanArgs p
     }
   if (nchunks > 0) {
     publish_state<NT>(S, sSb, sw, l);
+    // Buffer r holds chunk cc + r; after the S barrier of chunk c the buffer
+    // of chunk c - 1 is refilled with chunk c + kRingS - 1 while the U/O role
+    // forms U (the loads may wait for memory queue space there).
     SFrags f[kRingS];
 #pragma unroll
-    for (int r = 0; r < kRingS; ++r) load_s(f[r], g.rec0 + min(r, last) * g.rec_stride, sw, l, gq);
-    touch(f[0]);
+    for (int r = 0; r < kRingS - 1; ++r) {
+      load_s(f[r], g.rec0 + min(r, last) * g.rec_stride, sw, l, gq);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     for (int cc = 0; cc < nchunks; cc += kRingS) {
 #pragma unroll
       for (int r = 0; r < kRingS; ++r) {
-        if (cc + r < nchunks) state_step<NT>(f[r], S, sSb, sUb, sw, l);
-        load_s(f[r], g.rec0 + min(cc + r + kRingS, last) * g.rec_stride, sw, l, gq);
-        touch(f[(r + 1) % kRingS]);
+        const bool live = cc + r < nchunks;
+        if (live) lds_barrier();  // S published
+        load_s(f[(r + kRingS - 1) % kRingS], g.rec0 + min(cc + r + kRingS - 1, last) * g.rec_stride, sw, l, gq);
+        touch(f[r]);
+        if (live) state_update<NT>(f[r], S, sSb, sUb, sw, l);
       }
     }
   }
@@ -935,7 +982,7 @@ using namespace sophia;
 extern "C" size_t sophia_kda_chunk_workspace_size(int64_t total_tokens, int n_seqs, int num_heads,
                                                   int head_dim) {
   if (total_tokens < 0 || n_seqs <= 0 || num_heads <= 0 || head_dim != kD) return 0;
-  return header_bytes(total_tokens, n_seqs) +
+  return header_bytes(total_tokens, n_seqs) + kTrashBytes +
          static_cast<size_t>(max_chunks(total_tokens, n_seqs)) * num_heads * kRecBytes;
 }
 
@@ -968,8 +1015,11 @@ extern "C" int sophia_kda_chunk_fwd(const void *q, const void *k, const void *v,
   SOPHIA_REQUIRE(qkv_row_stride >= (int64_t)num_heads * kD && g_row_stride >= (int64_t)num_heads * kD &&
                      beta_row_stride >= num_heads && o_row_stride >= (int64_t)num_heads * kD,
                  "kda_chunk_fwd: row stride smaller than a row");
-  SOPHIA_REQUIRE(qkv_row_stride % 4 == 0 && g_row_stride % 4 == 0,
-                 "kda_chunk_fwd: q/k/v/g row strides must be multiples of 4 elements");
+  SOPHIA_REQUIRE(qkv_row_stride % 4 == 0 && g_row_stride % 4 == 0 && o_row_stride % 4 == 0,
+                 "kda_chunk_fwd: q/k/v/g/o row strides must be multiples of 4 elements");
+  SOPHIA_REQUIRE(total_tokens == 0 ||
+                     (reinterpret_cast<uintptr_t>(o) % (qkv_dtype == SOPHIA_DTYPE_BF16 ? 8 : 16)) == 0,
+                 "kda_chunk_fwd: o must be aligned to 4 elements");
   SOPHIA_REQUIRE(((uintptr_t)workspace % 256) == 0, "kda_chunk_fwd: workspace must be 256-byte aligned");
   SOPHIA_REQUIRE(n_state_slots >= 0, "kda_chunk_fwd: n_state_slots must be >= 0");
   const size_t need = sophia_kda_chunk_workspace_size(total_tokens, n_seqs, num_heads, head_dim);
@@ -981,7 +1031,8 @@ extern "C" int sophia_kda_chunk_fwd(const void *q, const void *k, const void *v,
   hipStream_t st = static_cast<hipStream_t>(stream);
   int32_t *chunk_start = static_cast<int32_t *>(workspace);
   int32_t *chunk_seq = chunk_start + n_seqs + 1;
-  uint8_t *records = static_cast<uint8_t *>(workspace) + header_bytes(total_tokens, n_seqs);
+  uint8_t *trash = static_cast<uint8_t *>(workspace) + header_bytes(total_tokens, n_seqs);
+  uint8_t *records = trash + kTrashBytes;
 
   hipLaunchKernelGGL(kda_chunk_prep_kernel, dim3(1), dim3(256), 0, st, cu_seqlens, n_seqs,
                      total_tokens, max_ch, chunk_start, chunk_seq);
@@ -1022,7 +1073,7 @@ extern "C" int sophia_kda_chunk_fwd(const void *q, const void *k, const void *v,
   int splits = 1;
   while (splits < 8 && pairs * splits * 2 <= static_cast<int64_t>(cus)) splits *= 2;
   ScanArgs sa{cu_seqlens, n_seqs, total_tokens, num_heads, max_ch, chunk_start, records,
-              initial_state, final_state, n_state_slots, state_slots, o, o_row_stride, splits};
+              initial_state, final_state, n_state_slots, state_slots, o, o_row_stride, splits, trash};
   const int64_t groups = (pairs + 7) / 8;
   const int64_t blocks = groups * 8 * splits;
   SOPHIA_REQUIRE(blocks <= 0x7fffffff, "kda_chunk_fwd: grid too large");
