@@ -41,7 +41,7 @@ METRIC = "KDA prefill tokens/s + % MFMA peak; decode-step µs and HBM GB/s at B=
 # HBM bytes per launch measured with rocprofv3 on this workload (FETCH_SIZE and
 # WRITE_SIZE in separate passes; FETCH_SIZE doubled, the factor a plain 1 GiB
 # device copy gives on MI355X).  Re-measured whenever a kernel changes.
-MEASURED_TRAFFIC_BYTES = {"prefill": 801.3e6, "decode": 543.5e6, "short_conv": 318.7e6}
+MEASURED_TRAFFIC_BYTES = {"prefill": 801.6e6, "decode": 543.5e6, "short_conv": 318.7e6}
 
 
 def prefill_lengths(seed: int = 0, n: int = 8, lo: int = 256, hi: int = 4096) -> list[int]:
@@ -202,9 +202,11 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["all", "prefill", "conv", "decode", "copy", "mixed"], default="all",
-                    help="run one workload only (for kernel profiling); the JSON line then "
-                         "carries that workload's fields alone")
+    ap.add_argument("--only", choices=["all", "kda", "prefill", "conv", "decode", "copy", "mixed"],
+                    default="all",
+                    help="run one workload only (for kernel profiling; 'kda' = prefill, ShortConv "
+                         "and decode without the decoder step); the JSON line then carries that "
+                         "workload's fields alone")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
@@ -245,7 +247,7 @@ def main(argv=None) -> int:
               "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
               "data": "synthetic"}
 
-    run_prefill = args.only in ("all", "prefill")
+    run_prefill = args.only in ("all", "kda", "prefill")
     wall, per = time_events(torch, prefill, args.steps if run_prefill else 1,
                             args.warmup if run_prefill else 0, stream)
     avg_ms = float(np.mean(per))
@@ -292,7 +294,7 @@ def main(argv=None) -> int:
         ops.short_conv_fwd(xconv, wconv, inp["cu"], conv_state=conv_state, read_history=False,
                            write_history=True, out=yconv)
 
-    if args.only in ("all", "conv"):
+    if args.only in ("all", "kda", "conv"):
         _, cper = time_events(torch, conv, args.steps, args.warmup, stream)
         cms = float(np.mean(cper))
         cbytes = total * 3 * HEADS * DIM * 2 * 2
@@ -318,7 +320,7 @@ def main(argv=None) -> int:
         ops.kda_decode_step(dq, dk, dv, dg, db, dstate, use_gate=False, use_beta_sigmoid=False,
                             out=dout)
 
-    if args.only in ("all", "decode"):
+    if args.only in ("all", "kda", "decode"):
         dsteps = max(args.steps * 5, 50)
         _, dper = time_events(torch, decode, dsteps, args.warmup * 2, stream)
         dms = float(np.mean(dper))
