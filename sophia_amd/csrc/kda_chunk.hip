@@ -294,9 +294,13 @@ __device__ __forceinline__ void intra_scaled_operands(
   }
 }
 
+// One (chunk c, head h) of the intra phase on 256 threads (tid 0..255, four
+// wavefronts) with kSmIntra bytes of LDS at smem; writes the record at rec.
+// Every barrier inside is a work-group barrier: a work-group running two
+// items at once runs them in lock step.
 template <int QKV_DT, int G_DT, bool GATE>
-__global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs p) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+__device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int h, uint8_t *smem, int tid,
+                                           uint8_t *rec) {
   float *s_E = reinterpret_cast<float *>(smem + kSmE);
   uint16_t *sKD = reinterpret_cast<uint16_t *>(smem + kSmA);
   float *sY = reinterpret_cast<float *>(smem + kSmA);
@@ -307,17 +311,12 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
   float *sT = reinterpret_cast<float *>(smem + kSmC);
   uint16_t *sQK = reinterpret_cast<uint16_t *>(smem + kSmD);
 
-  const int c = blockIdx.x;
-  const int h = blockIdx.y;
-  const int nch = imin64(p.chunk_start[p.n_seqs], p.max_ch);
-  if (c >= nch) return;
   const int s = p.chunk_seq[c];
   const int64_t seq_a = iclamp64(p.cu[s], 0, p.total);
   const int64_t seq_b = iclamp64(p.cu[s + 1], seq_a, p.total);
   const int64_t t0 = seq_a + static_cast<int64_t>(c - p.chunk_start[s]) * kC;
   const int len = static_cast<int>(imin64(kC, seq_b - t0));
 
-  const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave = 16-row sub-block (uniform)
   const int l = tid & 63;
   const int lr = l & 15;         // row within the sub-block
@@ -325,7 +324,6 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
   const int row = 16 * w + lr;   // chunk row of this lane
   const bool valid = row < len;
   const int64_t tok = t0 + row;
-  uint8_t *rec = p.records + (static_cast<size_t>(c) * p.num_heads + h) * kRecBytes;
   const SwzBases sb = swz_bases(gq, row);
 
   // ---- 1. load q, k, g (32 channels per lane, 16x16x32 operand order), v, beta.
@@ -619,6 +617,17 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
   }
 }
 
+template <int QKV_DT, int G_DT, bool GATE>
+__global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs p) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int c = blockIdx.x;
+  const int h = blockIdx.y;
+  const int nch = imin64(p.chunk_start[p.n_seqs], p.max_ch);
+  if (c >= nch) return;
+  intra_item<QKV_DT, G_DT, GATE>(p, c, h, smem, threadIdx.x,
+                                 p.records + (static_cast<size_t>(c) * p.num_heads + h) * kRecBytes);
+}
+
 // ---- scan kernel -------------------------------------------------------------
 struct ScanArgs {
   const int32_t *cu;
@@ -833,24 +842,53 @@ __device__ __forceinline__ void state_update(const SFrags &f, f4 (&S)[2][NT], ui
 // ring buffers strictly in order: the wait counts in the loop are the minimum
 // over every path into it, so a prologue that interleaves the loads of two
 // buffers makes every later step wait for its newest buffer too.
-template <int NVB, int O_DT>
-__global__ __launch_bounds__(kScanThreads) void kda_chunk_scan_kernel(ScanArgs p) {
+// Where a scan that runs beside the intra items (the fused kernel) learns
+// that a record is complete: flags[h * fstride + c] != 0 for global chunk c.
+struct Ready {
+  const int *flags;
+  int64_t fstride;
+  int *err;          // set when a wait gives up (the result is then invalid)
+};
+constexpr int kSpinLimit = 1 << 18;   // polls of ~8 x 64 clocks: ~50 ms, far above any real wait
+
+typedef int i4 __attribute__((ext_vector_type(4)));
+
+// Waits until the records of relative chunks 0..k of one (sequence, head) are
+// published; `ready` (wave-uniform) caches the highest relative chunk known
+// to be.  Flags are read with scalar loads that bypass the scalar cache, so
+// the wait never touches the vector memory counter and leaves the ring loads
+// in flight.  Every wait ends: after kSpinLimit empty polls it records an
+// error and stops waiting.
+__device__ __forceinline__ void wait_records(const Ready &rd, const int *fl, int k, int last, int &ready) {
+  int spins = 0;
+  while (ready < k) {
+    const int *a = fl + ready + 1;
+    i4 v;
+    asm volatile("s_load_dwordx4 %0, %1, 0x0 glc\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(a) : "memory");
+    const int n = v.x == 0 ? 0 : (v.y == 0 ? 1 : (v.z == 0 ? 2 : (v.w == 0 ? 3 : 4)));
+    ready = min(ready + n, last);
+    if (n == 0) {
+      if (++spins > kSpinLimit) {
+        __hip_atomic_store(rd.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ready = last;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(8);
+    }
+  }
+}
+
+// One (sequence s, head h, value-column slice `half`) of the scan on 512
+// threads, with the S and U exchange buffers at sSb / sUb.  With FUSED the
+// record loads of each chunk first wait for its published flag.
+template <int NVB, int O_DT, bool FUSED>
+__device__ __forceinline__ void scan_item(const ScanArgs &p, int s, int h, int half, uint8_t *sSb, uint8_t *sUb,
+                                          const Ready &rd) {
   constexpr int NT = NVB / 16;               // 16-column tiles per work-group
-  __shared__ __attribute__((aligned(16))) uint8_t sSb[4 * NT * 64 * 16];   // S, [ks][nt][lane]
-  __shared__ __attribute__((aligned(16))) uint8_t sUb[2 * NT * 64 * 16];   // U, [ks][nt][lane]
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l = tid & 63;
   const int lr = l & 15, gq = l >> 4;
-  // XCD-aware order: the `splits` work-groups of one (sequence, head) share
-  // the same blockIdx % 8, i.e. the same XCD and L2, so they share record reads.
-  const int b = blockIdx.x;
-  const int group = b / (8 * p.splits);
-  const int half = (b / 8) % p.splits;
-  const int sh = group * 8 + (b % 8);
-  const int h = sh % p.num_heads;
-  const int s = sh / p.num_heads;
-  if (s >= p.n_seqs) return;
   ScanGeom g;
   g.h = h;
   g.nt0 = half * NT;
@@ -861,6 +899,8 @@ __global__ __launch_bounds__(kScanThreads) void kda_chunk_scan_kernel(ScanArgs p
   g.rec_stride = static_cast<size_t>(p.num_heads) * kRecBytes;
   const int nchunks = g.nchunks;
   const int last = nchunks - 1;
+  const int *fl = FUSED ? rd.flags + h * rd.fstride + p.chunk_start[s] : nullptr;
+  int ready = -1;
 
   if (wave < 4) {
     // ---- U/O role
@@ -868,6 +908,7 @@ __global__ __launch_bounds__(kScanThreads) void kda_chunk_scan_kernel(ScanArgs p
     if (nchunks <= 0) return;
     constexpr int R = ring_uo<NT>();
     UOFrags<NT> f[R];
+    if constexpr (FUSED) wait_records(rd, fl, min(R - 1, last), last, ready);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const uint8_t *rec = g.rec0 + min(r, last) * g.rec_stride;
@@ -883,6 +924,7 @@ __global__ __launch_bounds__(kScanThreads) void kda_chunk_scan_kernel(ScanArgs p
         const uint8_t *rec = g.rec0 + min(cc + r + R, last) * g.rec_stride;
         f4 O[NT];
         if (live) uo_pre<NT>(f[r], O, sSb, sUb, w, l);
+        if constexpr (FUSED) wait_records(rd, fl, min(cc + r + R, last), last, ready);
         // Refill while the state role works: the loads may wait for memory
         // queue space here, off the critical path.
         load_uo_main<NT>(f[r], rec, w, l, g.nt0);
@@ -920,6 +962,7 @@ __global__ __launch_bounds__(kScanThreads) void kda_chunk_scan_kernel(ScanArgs p
     // of chunk c - 1 is refilled with chunk c + kRingS - 1 while the U/O role
     // forms U (the loads may wait for memory queue space there).
     SFrags f[kRingS];
+    if constexpr (FUSED) wait_records(rd, fl, min(kRingS - 2, last), last, ready);
 #pragma unroll
     for (int r = 0; r < kRingS - 1; ++r) {
       load_s(f[r], g.rec0 + min(r, last) * g.rec_stride, sw, l, gq);
@@ -930,6 +973,7 @@ __global__ __launch_bounds__(kScanThreads) void kda_chunk_scan_kernel(ScanArgs p
       for (int r = 0; r < kRingS; ++r) {
         const bool live = cc + r < nchunks;
         if (live) lds_barrier();  // S published
+        if constexpr (FUSED) wait_records(rd, fl, min(cc + r + kRingS - 1, last), last, ready);
         load_s(f[(r + kRingS - 1) % kRingS], g.rec0 + min(cc + r + kRingS - 1, last) * g.rec_stride, sw, l, gq);
         touch(f[r]);
         if (live) state_update<NT>(f[r], S, sSb, sUb, sw, l);
@@ -946,6 +990,23 @@ __global__ __launch_bounds__(kScanThreads) void kda_chunk_scan_kernel(ScanArgs p
           p.ht[state_off + static_cast<int64_t>(32 * sw + 16 * mi + 4 * gq + e) * kD + 16 * (g.nt0 + nt) + lr] =
               S[mi][nt][e];
   }
+}
+
+template <int NVB, int O_DT>
+__global__ __launch_bounds__(kScanThreads) void kda_chunk_scan_kernel(ScanArgs p) {
+  constexpr int NT = NVB / 16;
+  __shared__ __attribute__((aligned(16))) uint8_t sSb[4 * NT * 64 * 16];   // S, [ks][nt][lane]
+  __shared__ __attribute__((aligned(16))) uint8_t sUb[2 * NT * 64 * 16];   // U, [ks][nt][lane]
+  // XCD-aware order: the `splits` work-groups of one (sequence, head) share
+  // the same blockIdx % 8, i.e. the same XCD and L2, so they share record reads.
+  const int b = blockIdx.x;
+  const int group = b / (8 * p.splits);
+  const int half = (b / 8) % p.splits;
+  const int sh = group * 8 + (b % 8);
+  const int h = sh % p.num_heads;
+  const int s = sh / p.num_heads;
+  if (s >= p.n_seqs) return;
+  scan_item<NVB, O_DT, false>(p, s, h, half, sSb, sUb, Ready{nullptr, 0, nullptr});
 }
 
 
