@@ -1,0 +1,65 @@
+/*
+ * sophia_decoder.h -- C ABI of the decoder-side kernels of the MI355X build:
+ * the layers between the KDA mixers of the hybrid decoder.
+ *
+ * Conventions as in sophia_kda.h: device pointers, strides in elements, an
+ * explicit hipStream_t passed as void*, an int status (SOPHIA_OK or an error
+ * code; sophia_last_error() describes the last failure).  Nothing here
+ * allocates or synchronises.  dtype is SOPHIA_DTYPE_F32 or SOPHIA_DTYPE_BF16
+ * for every activation tensor; weights are fp32.
+ */
+#ifndef SOPHIA_DECODER_H
+#define SOPHIA_DECODER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "sophia_kda.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/*
+ * Depth mixing of the attention-residual blocks; replaces
+ * AttentionResidualMixer.forward (ml/runtime/model/blocks.py:38-48), and, when
+ * out_norm_weight is not NULL, also the RMSNorm that consumes its output
+ * (SophiaBlock's attn_norm / ffn_norm, blocks.py:72-87, and the final norm
+ * of the logits path, ml/runtime/model/transformer.py:189,210 and
+ * ml/runtime/model/ops.py:67-77):
+ *   values = [completed[:, 0], ..., completed[:, n_blocks-1], partial]
+ *   score_b = RMSNorm(values_b; norm_weight, eps) . query_weight
+ *   mix = sum_b softmax_b(score) * values_b
+ *   out = mix, or RMSNorm(mix; out_norm_weight, out_eps)
+ *   partial   : [rows, dim], row stride partial_stride.
+ *   completed : [rows, n_blocks, dim] with strides (completed_row_stride,
+ *               completed_block_stride, 1); unused when n_blocks == 0.
+ *   norm_weight, query_weight, out_norm_weight : [dim] fp32.
+ *   out       : [rows, dim], row stride out_stride (may not alias the inputs).
+ * Sums, scores, softmax and the output norm run in fp32; out is rounded once.
+ * dim a multiple of 8 and at most 4096; 0 <= n_blocks < 16; strides multiples
+ * of 8; every pointer 16-byte aligned.
+ */
+int sophia_attn_res_mix(const void *partial, int64_t partial_stride, const void *completed,
+                        int64_t completed_row_stride, int64_t completed_block_stride, int n_blocks,
+                        const float *norm_weight, const float *query_weight, float eps,
+                        const float *out_norm_weight, float out_eps, void *out, int64_t out_stride,
+                        int64_t rows, int dim, int dtype, void *stream);
+
+/*
+ * SiTU-GLU hidden of FeedForward.forward (ml/runtime/model/blocks.py:23-27):
+ *   g, u = gate_up[:, :hidden], gate_up[:, hidden:]
+ *   out = gate_softcap tanh(g / gate_softcap) sigmoid(g) * up_softcap tanh(u / up_softcap)
+ *   gate_up : [rows, 2 * hidden], row stride gate_up_stride.
+ *   out     : [rows, hidden], row stride out_stride.
+ * Computed in fp32, rounded once.  hidden a multiple of 8; strides multiples
+ * of 8; pointers 16-byte aligned.
+ */
+int sophia_situ_glu(const void *gate_up, int64_t gate_up_stride, void *out, int64_t out_stride, int64_t rows,
+                    int hidden, float gate_softcap, float up_softcap, int dtype, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SOPHIA_DECODER_H */

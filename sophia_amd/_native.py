@@ -1,6 +1,7 @@
 """ctypes binding of the HIP library ``sophia_amd/_lib/libsophia_kda.so``.
 
-The library exports the C ABI declared in ``include/sophia_kda.h``.  torch is
+The library exports the C ABI declared in ``include/sophia_kda.h`` and
+``include/sophia_decoder.h``.  torch is
 imported first so that the library binds to the HIP runtime torch already
 loaded (same soname), which keeps torch streams and device pointers valid for
 the kernels.  There is no fallback: if the library is missing or fails to
@@ -30,7 +31,8 @@ QK_L2NORM = 1
 GATE_IN_KERNEL = 2
 BETA_SIGMOID = 4
 
-# Every symbol of include/sophia_kda.h, with its ctypes signature.
+# Every symbol of include/sophia_kda.h and include/sophia_decoder.h, with its
+# ctypes signature.
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int
@@ -51,6 +53,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "sophia_kda_decode_step": (_i32, [_vp, _vp, _vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64, _i32,
                                       _vp, _vp, _f32, _f32, _u32, _vp, _i32, _vp, _i32, _i32, _i32,
                                       _i32, _vp, _i64, _vp]),
+    "sophia_attn_res_mix": (_i32, [_vp, _i64, _vp, _i64, _i64, _i32, _vp, _vp, _f32, _vp, _f32,
+                                   _vp, _i64, _i64, _i32, _i32, _vp]),
+    "sophia_situ_glu": (_i32, [_vp, _i64, _vp, _i64, _i64, _i32, _f32, _f32, _i32, _vp]),
 }
 
 _lib = None

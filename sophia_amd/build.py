@@ -2,7 +2,7 @@
 
 hipcc for gfx950 only; each translation unit is compiled to an object in
 sophia_amd/_build/ and linked into one shared library exporting the C ABI of
-include/sophia_kda.h.  Run ``python -m sophia_amd.build``.
+include/sophia_kda.h and include/sophia_decoder.h.  Run ``python -m sophia_amd.build``.
 """
 
 from __future__ import annotations
@@ -20,7 +20,7 @@ LIB_DIR = os.path.join(HERE, "_lib")
 LIB_NAME = "libsophia_kda.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 ARCH = "gfx950"
-SOURCES = ("errors.cpp", "short_conv.hip", "kda_decode.hip", "kda_chunk.hip")
+SOURCES = ("errors.cpp", "short_conv.hip", "kda_decode.hip", "kda_chunk.hip", "decoder_ops.hip")
 
 # Packed-fp32 VALU ops are switched off for all device code.
 COMMON_FLAGS = [

@@ -6,8 +6,11 @@ Modules keep the reference's names, parameter shapes and semantics
 ``FeedForward`` / ``AttentionResidualMixer`` / ``SophiaBlock``;
 transformer.py:17-207 and transformer_setup.py:33-79 ``Transformer``), so a
 reference state_dict loads as is.  Layer i is MLA iff i % 4 == 3, the rest are
-``sophia_amd.kda.SophiaKDA`` (gfx950 kernels).  MLA and the FFN run on library
-GEMMs and attention (hipBLASLt / SDPA through torch).
+``sophia_amd.kda.SophiaKDA`` (gfx950 kernels).  The SiTU-GLU activation and
+each attention-residual depth mix, with the RMSNorm that consumes it, run as
+single HIP kernels (``ops.situ_glu``, ``ops.attn_res_mix``); depth blocks are
+appended in place into one store per forward.  The projections of MLA and the
+FFN run on library GEMMs and attention (hipBLASLt / SDPA through torch).
 
 Besides the reference-shaped ``Transformer.forward(input_ids, start_pos)``,
 ``Transformer.forward_mixed`` runs one continuous-batching step that the
@@ -28,6 +31,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from .config import ModelArgs
+from . import ops
 from .kda import RMSNorm, RuntimeLinear, SophiaKDA, _require_gpu
 from .state import LayerCacheSnapshot
 
@@ -216,27 +220,70 @@ class FeedForward(nn.Module):
         self.down_proj = RuntimeLinear(self.hidden, int(args.dim))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        gate, up = self.gate_up_proj(x).split(self.hidden, dim=-1)
-        bounded_gate = self.gate_softcap * torch.tanh(gate / self.gate_softcap)
-        bounded_up = self.up_softcap * torch.tanh(up / self.up_softcap)
-        return self.down_proj(bounded_gate * torch.sigmoid(gate) * bounded_up)
+        # gate_softcap tanh(g / gate_softcap) sigmoid(g) * up_softcap tanh(u / up_softcap)
+        # as one HIP kernel over the fused [gate | up] projection.
+        hidden = ops.situ_glu(self.gate_up_proj(x), self.gate_softcap, self.up_softcap)
+        return self.down_proj(hidden)
 
 
 class AttentionResidualMixer(nn.Module):
     """Content-dependent mixing over completed depth blocks and a partial
-    block (blocks.py:30-48).  Works on any leading shape: values [..., blocks, dim]."""
+    block (blocks.py:30-48), as one HIP kernel (ops.attn_res_mix).  Works on
+    any leading shape: partial [..., dim], completed [..., blocks, dim]."""
 
     def __init__(self, args: ModelArgs) -> None:
         super().__init__()
         self.norm = RMSNorm(args.dim, args.norm_eps)
         self.query = RuntimeLinear(args.dim, 1)
+        self._query_f32 = None
+        self._query_key = None
 
-    def forward(self, partial_block: torch.Tensor, completed_blocks: torch.Tensor) -> torch.Tensor:
-        values = torch.cat((completed_blocks, partial_block.unsqueeze(-2)), dim=-2)
-        keys = self.norm(values)
-        scores = keys.float() @ self.query.weight.squeeze(0).float()
-        weights = scores.softmax(dim=-1).unsqueeze(-1).to(dtype=values.dtype)
-        return (weights * values).sum(dim=-2).to(dtype=values.dtype)
+    def _query(self) -> torch.Tensor:
+        """The query as fp32 [dim] (the reference upcasts it per call); kept
+        until the weight changes, so that no cast runs per step."""
+        w = self.query.weight
+        key = (w.data_ptr(), w.dtype, w._version)
+        if self._query_key != key:
+            self._query_f32 = w.detach().reshape(-1).float().contiguous()
+            self._query_key = key
+        return self._query_f32
+
+    def forward(self, partial_block: torch.Tensor, completed_blocks: torch.Tensor,
+                out_norm: RMSNorm | None = None) -> torch.Tensor:
+        """The mix; with ``out_norm``, ``out_norm(mix)`` from the same kernel."""
+        return ops.attn_res_mix(
+            partial_block, completed_blocks, self.norm.weight, self._query(), self.norm.eps,
+            out_norm_weight=None if out_norm is None else out_norm.weight,
+            out_eps=1e-6 if out_norm is None else out_norm.eps)
+
+
+def _append_block(completed: torch.Tensor, partial: torch.Tensor) -> torch.Tensor:
+    """torch.cat((completed, partial.unsqueeze(-2)), dim=-2) (blocks.py:73-76).
+    When ``completed`` is a view of a depth store with room for one more block
+    (rows spaced at least one block apart and the storage long enough), the
+    block is written in place and the enlarged view returned, so that the
+    earlier blocks are not copied again."""
+    n, dim = int(completed.size(-2)), int(completed.size(-1))
+    strides = completed.stride()
+    sizes = list(completed.shape)
+    sizes[-2] = n + 1
+    rows_ok = all(strides[i] >= (n + 1) * dim for i in range(completed.dim() - 2) if sizes[i] > 1)
+    if completed.dim() >= 3 and strides[-1] == 1 and strides[-2] == dim and rows_ok:
+        extent = completed.storage_offset() + 1 + sum((sz - 1) * st for sz, st in zip(sizes, strides))
+        if all(sz > 0 for sz in sizes) and extent * completed.element_size() <= \
+                completed.untyped_storage().nbytes():
+            grown = completed.as_strided(sizes, strides, completed.storage_offset())
+            grown.select(-2, n).copy_(partial)
+            return grown
+    return torch.cat((completed, partial.unsqueeze(-2)), dim=-2)
+
+
+def depth_store(hidden: torch.Tensor, n_layers: int, block_size: int) -> torch.Tensor:
+    """An empty ``completed`` view [..., 0, dim] over storage for every depth
+    block the layers will append (one per ``block_size`` layers)."""
+    n_max = max(1, -(-int(n_layers) // int(block_size)))
+    store = hidden.new_empty(*hidden.shape[:-1], n_max, int(hidden.size(-1)))
+    return store.narrow(-2, 0, 0)
 
 
 class SophiaBlock(nn.Module):
@@ -255,14 +302,16 @@ class SophiaBlock(nn.Module):
         self.ffn_residual = AttentionResidualMixer(args)
 
     def _mix(self, partial_block, completed_blocks, attn):
-        attn_input = self.attn_residual(partial_block, completed_blocks)
+        # attn_norm(attn_residual(...)) and ffn_norm(ffn_residual(...)) each run
+        # as one kernel: the mixes feed nothing but these norms.
+        attn_input = self.attn_residual(partial_block, completed_blocks, self.attn_norm)
         if self.layer_idx % self.attn_res_block_size == 0:
-            completed_blocks = torch.cat((completed_blocks, partial_block.unsqueeze(-2)), dim=-2)
-            partial_block = attn(self.attn_norm(attn_input))
+            completed_blocks = _append_block(completed_blocks, partial_block)
+            partial_block = attn(attn_input)
         else:
-            partial_block = partial_block + attn(self.attn_norm(attn_input))
-        ffn_input = self.ffn_residual(partial_block, completed_blocks)
-        partial_block = partial_block + self.ffn(self.ffn_norm(ffn_input))
+            partial_block = partial_block + attn(attn_input)
+        ffn_input = self.ffn_residual(partial_block, completed_blocks, self.ffn_norm)
+        partial_block = partial_block + self.ffn(ffn_input)
         return partial_block, completed_blocks
 
     def forward(self, partial_block, completed_blocks, *, start_pos: int = 0):
@@ -351,11 +400,10 @@ class Transformer(nn.Module):
         _require_gpu(input_ids)
         self._validate(input_ids, start_pos)
         hidden = self.tok_embeddings(input_ids)
-        completed = hidden.new_empty(int(hidden.size(0)), int(hidden.size(1)), 0, int(hidden.size(2)))
+        completed = depth_store(hidden, self.args.n_layers, self.args.attn_res_block_size)
         for layer in self.layers:
             hidden, completed = layer(hidden, completed, start_pos=start_pos)
-        hidden = self.output_attn_residual(hidden, completed)
-        return self.output(self.norm(hidden))
+        return self.output(self.output_attn_residual(hidden, completed, self.norm))
 
     def forward_mixed(self, prefill_ids: torch.Tensor, decode_ids: torch.Tensor, *,
                       prefill_slots: torch.Tensor, decode_slots: torch.Tensor,
@@ -378,13 +426,12 @@ class Transformer(nn.Module):
                     max_decode_len=int(max_decode_len), cu_prefill=cu_prefill)
         ids = torch.cat((prefill_ids.reshape(-1), decode_ids.reshape(-1)))
         hidden = self.tok_embeddings(ids)
-        completed = hidden.new_empty(int(hidden.size(0)), 0, int(hidden.size(1)))
+        completed = depth_store(hidden, self.args.n_layers, self.args.attn_res_block_size)
         for layer in self.layers:
             hidden, completed = layer.forward_mixed(hidden, completed, step)
         last = torch.cat((torch.arange(T - 1, P * T, T, device=hidden.device),
                           torch.arange(P * T, P * T + D, device=hidden.device)))
-        hidden = self.output_attn_residual(hidden[last], completed[last])
-        return self.output(self.norm(hidden))
+        return self.output(self.output_attn_residual(hidden[last], completed[last], self.norm))
 
 
 class MixedStepGraph:

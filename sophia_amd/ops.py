@@ -353,3 +353,105 @@ def fused_recurrent_kda(q, k, v, g, beta, *, A_log=None, dt_bias=None, scale=Non
                         use_gate=use_gate_in_kernel, use_beta_sigmoid=use_beta_sigmoid_in_kernel,
                         read_state=read)
     return o.view(bsz, 1, heads, HEAD_DIM), (state if output_final_state else None)
+
+
+# ------------------------------------------------------------------ decoder layers
+def _aligned(t: torch.Tensor, name: str) -> None:
+    if t.data_ptr() % 16:
+        raise RuntimeError(f"{name} must be 16-byte aligned")
+
+
+def attn_res_mix(partial: torch.Tensor, completed: torch.Tensor, norm_weight: torch.Tensor,
+                 query_weight: torch.Tensor, eps: float, *,
+                 out_norm_weight: torch.Tensor | None = None, out_eps: float = 1e-6,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """AttentionResidualMixer.forward (ml/runtime/model/blocks.py:38-48) in one
+    kernel: softmax over the depth axis of [completed blocks..., partial] with
+    scores RMSNorm(value) . query, then the weighted sum of the values; with
+    ``out_norm_weight``, also the RMSNorm that consumes the mix (attn_norm /
+    ffn_norm of blocks.py:72-87, the final norm of transformer.py:210).
+
+    partial: [..., D]; completed: [..., n_blocks, D] with the same leading
+    dims and dense rows; norm_weight, query_weight, out_norm_weight: [D] (or
+    [1, D]), converted to fp32 as the reference upcasts the query.  Sums,
+    scores, softmax and the output norm run in fp32 and the result is rounded
+    once to partial.dtype (the reference rounds the softmax weights, the
+    products and the mix to the activation dtype on the way).  Returns [..., D].
+    """
+    _gpu(partial, "partial")
+    _gpu(completed, "completed")
+    dim = int(partial.size(-1))
+    lead = tuple(partial.shape[:-1])
+    if completed.dim() != partial.dim() + 1 or tuple(completed.shape[:-2]) != lead \
+            or int(completed.size(-1)) != dim:
+        raise RuntimeError(f"completed must be [*{lead}, n_blocks, {dim}], got {tuple(completed.shape)}")
+    if completed.dtype != partial.dtype:
+        raise RuntimeError("partial and completed must share a dtype")
+    n_blocks = int(completed.size(-2))
+    p2 = partial.reshape(-1, dim)
+    rows = int(p2.size(0))
+    ps = _rows(p2, "partial", dim)
+    c3 = completed.reshape(rows, n_blocks, dim)
+    if n_blocks and dim > 1 and c3.stride(2) != 1:
+        raise RuntimeError("completed rows must be contiguous")
+    c_row = int(c3.stride(0)) if rows > 1 else n_blocks * dim
+    c_blk = int(c3.stride(1)) if n_blocks > 1 else dim
+
+    def f32(t: torch.Tensor, name: str) -> torch.Tensor:
+        t = t.detach().reshape(-1).to(device=partial.device, dtype=torch.float32).contiguous()
+        if int(t.numel()) != dim:
+            raise RuntimeError(f"{name} must hold {dim} values")
+        _aligned(t, name)
+        return t
+
+    w = f32(norm_weight, "norm_weight")
+    q = f32(query_weight, "query_weight")
+    wo = None if out_norm_weight is None else f32(out_norm_weight, "out_norm_weight")
+    if out is not None and not out.is_contiguous():
+        raise RuntimeError("out must be contiguous")
+    y = out if out is not None else torch.empty((rows, dim), dtype=partial.dtype, device=partial.device)
+    if y.dtype != partial.dtype or int(y.numel()) != rows * dim:
+        raise RuntimeError(f"out must be {partial.dtype} with {rows * dim} elements")
+    y2 = y.view(rows, dim)
+    _aligned(p2, "partial")
+    _aligned(y2, "out")
+    if n_blocks:
+        _aligned(c3, "completed")
+    rc = nat.lib().sophia_attn_res_mix(
+        nat.ptr(p2), ps, nat.ptr(c3) if n_blocks else None, c_row, c_blk, n_blocks, nat.ptr(w),
+        nat.ptr(q), float(eps), nat.ptr(wo), float(out_eps), nat.ptr(y2), dim, rows, dim,
+        nat.dtype_code(partial.dtype), nat.stream_handle(partial.device))
+    nat.check(rc, "sophia_attn_res_mix")
+    return y2.view(*lead, dim)
+
+
+def situ_glu(gate_up: torch.Tensor, gate_softcap: float, up_softcap: float, *,
+             out: torch.Tensor | None = None) -> torch.Tensor:
+    """The SiTU-GLU hidden of FeedForward.forward (ml/runtime/model/blocks.py:23-27)
+    in one pass: with [gate | up] = gate_up,
+    gate_softcap tanh(gate / gate_softcap) sigmoid(gate) * up_softcap tanh(up / up_softcap).
+    gate_up: [..., 2H] with dense rows; returns [..., H] in gate_up.dtype,
+    computed in fp32 and rounded once."""
+    _gpu(gate_up, "gate_up")
+    width = int(gate_up.size(-1))
+    if width % 2:
+        raise RuntimeError("gate_up must have an even last dimension")
+    hidden = width // 2
+    lead = tuple(gate_up.shape[:-1])
+    g2 = gate_up.reshape(-1, width)
+    rows = int(g2.size(0))
+    gs = _rows(g2, "gate_up", width)
+    if out is not None and not out.is_contiguous():
+        raise RuntimeError("out must be contiguous")
+    y = out if out is not None else torch.empty((rows, hidden), dtype=gate_up.dtype,
+                                                device=gate_up.device)
+    if y.dtype != gate_up.dtype or int(y.numel()) != rows * hidden:
+        raise RuntimeError(f"out must be {gate_up.dtype} with {rows * hidden} elements")
+    y2 = y.view(rows, hidden)
+    _aligned(g2, "gate_up")
+    _aligned(y2, "out")
+    rc = nat.lib().sophia_situ_glu(nat.ptr(g2), gs, nat.ptr(y2), hidden, rows, hidden,
+                                   float(gate_softcap), float(up_softcap),
+                                   nat.dtype_code(gate_up.dtype), nat.stream_handle(gate_up.device))
+    nat.check(rc, "sophia_situ_glu")
+    return y2.view(*lead, hidden)

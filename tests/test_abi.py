@@ -1,29 +1,31 @@
-"""The C-ABI library loads and exports every entry point that
-include/sophia_kda.h declares, with the argument counts the ctypes binding
-uses.  CPU only: the calls made here are host-side (version, workspace-size
+"""The C-ABI library loads and exports every entry point that the headers
+under include/ declare, with the argument counts the ctypes binding uses.  CPU only: the calls made here are host-side (version, workspace-size
 query, argument validation) and never launch a kernel.
 """
 
 from __future__ import annotations
 
 import ctypes
+import glob
 import os
 import re
 
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "sophia_kda.h")
+HEADERS = sorted(glob.glob(os.path.join(ROOT, "include", "*.h")))
 
 
 def _declarations() -> dict[str, int]:
-    """name -> number of parameters, for every function the header declares."""
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    """name -> number of parameters, for every function the headers declare."""
     decls = {}
-    for m in re.finditer(r"\b(sophia_\w+)\s*\(([^;{]*?)\)\s*;", text, flags=re.S):
-        name, params = m.group(1), m.group(2).strip()
-        decls[name] = 0 if params in ("", "void") else len(params.split(","))
+    for header in HEADERS:
+        text = open(header).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"\b(sophia_\w+)\s*\(([^;{]*?)\)\s*;", text, flags=re.S):
+            name, params = m.group(1), m.group(2).strip()
+            assert name not in decls, f"{name} declared twice"
+            decls[name] = 0 if params in ("", "void") else len(params.split(","))
     return decls
 
 
@@ -38,7 +40,8 @@ def test_header_declares_the_entry_points():
     decls = _declarations()
     for name in ("sophia_short_conv_fwd", "sophia_short_conv_step", "sophia_kda_chunk_fwd",
                  "sophia_kda_chunk_workspace_size", "sophia_kda_decode_step",
-                 "sophia_last_error", "sophia_abi_version"):
+                 "sophia_last_error", "sophia_abi_version", "sophia_attn_res_mix",
+                 "sophia_situ_glu"):
         assert name in decls, name
 
 
@@ -77,6 +80,29 @@ def test_host_side_queries_and_validation():
                                   None, 1.0, -6.0, 7, None, 1, 0, 16, 128, None, None, 0, None,
                                   None, 2048, None, 0, None)
     assert rc == nat.SOPHIA_ERR_INVALID
+    # Decoder kernels: dim not a multiple of 8, too deep, too wide, misaligned.
+    rc = lib.sophia_attn_res_mix(None, 1536, None, 0, 0, 0, None, None, 1e-5, None, 1e-5, None,
+                                 1536, 4, 1532, 1, None)
+    assert rc == nat.SOPHIA_ERR_INVALID and "dim" in nat.last_error()
+    rc = lib.sophia_attn_res_mix(None, 1536, None, 0, 0, 16, None, None, 1e-5, None, 1e-5, None,
+                                 1536, 4, 1536, 1, None)
+    assert rc == nat.SOPHIA_ERR_INVALID and "n_blocks" in nat.last_error()
+    rc = lib.sophia_attn_res_mix(None, 8192, None, 0, 0, 0, None, None, 1e-5, None, 1e-5, None,
+                                 8192, 4, 8192, 1, None)
+    assert rc == nat.SOPHIA_ERR_INVALID and "dim" in nat.last_error()
+    rc = lib.sophia_attn_res_mix(8, 1536, None, 0, 0, 0, 16, 32, 1e-5, None, 1e-5, 64, 1536, 4,
+                                 1536, 1, None)
+    assert rc == nat.SOPHIA_ERR_INVALID and "aligned" in nat.last_error()
+    # No rows: nothing to launch, no pointer needed.
+    assert lib.sophia_attn_res_mix(None, 1536, None, 3 * 1536, 1536, 3, None, None, 1e-5, None,
+                                   1e-5, None, 1536, 0, 1536, 1, None) == nat.SOPHIA_OK
+    rc = lib.sophia_situ_glu(None, 7936, None, 3968, 4, 3964, 4.0, 25.0, 1, None)
+    assert rc == nat.SOPHIA_ERR_INVALID and "hidden" in nat.last_error()
+    rc = lib.sophia_situ_glu(None, 7936, None, 3968, 4, 3968, 0.0, 25.0, 1, None)
+    assert rc == nat.SOPHIA_ERR_INVALID
+    # Non-null addresses that are never dereferenced: the stride check fails first.
+    rc = lib.sophia_situ_glu(16, 3968, 32, 3968, 4, 3968, 4.0, 25.0, 1, None)
+    assert rc == nat.SOPHIA_ERR_INVALID and "stride" in nat.last_error()
 
 
 def test_ops_reject_cpu_tensors():
@@ -90,3 +116,8 @@ def test_ops_reject_cpu_tensors():
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         ops.short_conv_fwd(torch.zeros(4, 8), torch.zeros(8, 4),
                            torch.tensor([0, 4], dtype=torch.int32))
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.attn_res_mix(torch.zeros(4, 64), torch.zeros(4, 2, 64), torch.ones(64),
+                         torch.zeros(64), 1e-5)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.situ_glu(torch.zeros(4, 64), 4.0, 25.0)

@@ -1,0 +1,185 @@
+"""GPU parity of the decoder-side HIP kernels (sophia_decoder.h) through the
+C ABI: the attention-residual depth mixer (blocks.py:38-48, optionally with
+the RMSNorm that consumes it) and the SiTU-GLU activation (blocks.py:23-27).
+
+References are computed in float64 on the host from the same (rounded)
+inputs: the module's formulas written with torch ops, and, for the mixer, the
+oracle's restatement (oracle/decoder_oracle.attn_res_mix).
+
+Tolerances (written per case): fp32 inputs, max|y - y_ref| <= 2e-5 max|y_ref|
+(fp32 sums over at most 4096 x 16 terms); bf16 inputs, the kernel rounds its
+fp32 result once, so |y - y_ref| <= 2^-8 |y_ref| + 1e-6 element-wise (half a
+bf16 ulp is 2^-9; the extra factor covers the fp32 arithmetic before the
+rounding).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import decoder_oracle as do
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+    return torch.device("cuda:0")
+
+
+def _mix_ref(partial, completed, w, q, eps, wo=None, out_eps=1e-6):
+    """blocks.py:38-48 (then ops.py:49-64 RMSNorm when wo is given) in float64."""
+    values = torch.cat((completed, partial.unsqueeze(-2)), dim=-2).double().cpu()
+    w, q = w.double().cpu(), q.double().cpu()
+    keys = values * torch.rsqrt(values.pow(2).mean(-1, keepdim=True) + eps) * w
+    p = torch.softmax(keys @ q, dim=-1)
+    y = (p.unsqueeze(-1) * values).sum(-2)
+    if wo is not None:
+        y = y * torch.rsqrt(y.pow(2).mean(-1, keepdim=True) + out_eps) * wo.double().cpu()
+    return y
+
+
+def _check(y, ref, dtype):
+    y = y.double().cpu()
+    if dtype == torch.float32:
+        err = float((y - ref).abs().max()) / max(float(ref.abs().max()), 1e-30)
+        assert err <= 2e-5, err
+    else:
+        bad = (y - ref).abs() > ref.abs() * 2.0 ** -8 + 1e-6
+        assert not bool(bad.any()), float((y - ref).abs().max())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rows,n_blocks,dim", [(1, 0, 8), (5, 1, 24), (300, 3, 256),
+                                               (257, 7, 1536), (64, 15, 1536), (33, 2, 4096),
+                                               (17, 4, 2056)])
+@pytest.mark.parametrize("normed", [False, True])
+def test_attn_res_mix_matches_fp64_reference(dtype, rows, n_blocks, dim, normed):
+    from sophia_amd import ops
+    dev = _dev()
+    g = torch.Generator(device="cpu").manual_seed(rows * 131 + n_blocks * 7 + dim)
+    partial = torch.randn(rows, dim, generator=g).to(dev, dtype)
+    completed = (torch.randn(rows, n_blocks, dim, generator=g) * 2).to(dev, dtype)
+    w = (1 + 0.2 * torch.randn(dim, generator=g)).to(dev)
+    # queries large enough that the softmax is far from uniform
+    q = (torch.randn(dim, generator=g) * 3 / dim ** 0.5).to(dev)
+    wo = (1 + 0.2 * torch.randn(dim, generator=g)).to(dev) if normed else None
+    y = ops.attn_res_mix(partial, completed, w, q, 1e-5, out_norm_weight=wo, out_eps=1e-5)
+    torch.cuda.synchronize()
+    assert y.shape == partial.shape and y.dtype == dtype
+    _check(y, _mix_ref(partial, completed, w, q, 1e-5, wo, 1e-5), dtype)
+
+
+def test_attn_res_mix_matches_oracle_on_strided_store_views():
+    """Leading dims [B, S], completed a narrow view of a wider depth store and
+    partial a strided slice, as the decoder passes them; checked against the
+    oracle's restatement."""
+    from sophia_amd import ops
+    dev = _dev()
+    g = torch.Generator(device="cpu").manual_seed(5)
+    B, S, D, nb = 3, 37, 256, 5
+    store = torch.randn(B, S, 8, D, generator=g).to(dev)
+    completed = store.narrow(-2, 0, nb)
+    wide = torch.randn(B, S, 2 * D, generator=g).to(dev)
+    partial = wide[..., D:]
+    w = (1 + 0.1 * torch.randn(D, generator=g)).to(dev)
+    q = (0.2 * torch.randn(1, D, generator=g)).to(dev)
+    y = ops.attn_res_mix(partial, completed, w, q, 1e-5)
+    torch.cuda.synchronize()
+    params = {"m.norm.weight": w.double().cpu().numpy(), "m.query.weight": q.double().cpu().numpy()}
+    ref = do.attn_res_mix(params, "m", partial.double().cpu().numpy(),
+                          completed.double().cpu().numpy(), norm_eps=1e-5)
+    err = np.max(np.abs(y.double().cpu().numpy() - ref)) / np.max(np.abs(ref))
+    assert err <= 2e-5, err
+
+
+def test_attn_res_mix_bf16_query_weight_is_upcast():
+    """A bf16 query weight (after a bf16 weight cast) is used at its bf16 value."""
+    from sophia_amd import ops
+    dev = _dev()
+    g = torch.Generator(device="cpu").manual_seed(9)
+    partial = torch.randn(40, 512, generator=g).to(dev, torch.bfloat16)
+    completed = torch.randn(40, 3, 512, generator=g).to(dev, torch.bfloat16)
+    w = torch.ones(512, device=dev)
+    q = (0.1 * torch.randn(1, 512, generator=g)).to(dev, torch.bfloat16)
+    y = ops.attn_res_mix(partial, completed, w, q, 1e-5)
+    torch.cuda.synchronize()
+    _check(y, _mix_ref(partial, completed, w, q.float().reshape(-1), 1e-5), torch.bfloat16)
+
+
+def _situ_ref(gu, cg=4.0, cu=25.0):
+    gu = gu.double().cpu()
+    gate, up = gu.chunk(2, dim=-1)
+    return cg * torch.tanh(gate / cg) * torch.sigmoid(gate) * (cu * torch.tanh(up / cu))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rows,hidden", [(1, 8), (3, 24), (1000, 3968), (129, 320)])
+def test_situ_glu_matches_fp64_reference(dtype, rows, hidden):
+    from sophia_amd import ops
+    dev = _dev()
+    g = torch.Generator(device="cpu").manual_seed(rows + hidden)
+    # spread over both soft caps' saturation regions and sigmoid's tails
+    gu = torch.randn(rows, 2 * hidden, generator=g) * torch.tensor([6.0, 40.0]).repeat_interleave(hidden)
+    gu[0, :4] = torch.tensor([-90.0, 90.0, 0.0, -1e-3])
+    gu = gu.to(dev, dtype)
+    y = ops.situ_glu(gu, 4.0, 25.0)
+    torch.cuda.synchronize()
+    assert y.shape == (rows, hidden) and y.dtype == dtype
+    ref = _situ_ref(gu)
+    yd = y.double().cpu()
+    if dtype == torch.float32:
+        # tanh and sigmoid from fp32 exponentials: a few ulp of the 100-sized output
+        assert float((yd - ref).abs().max()) <= 2e-5 * max(float(ref.abs().max()), 1.0)
+    else:
+        assert not bool(((yd - ref).abs() > ref.abs() * 2.0 ** -8 + 1e-5).any())
+
+
+def test_situ_glu_strided_input_and_leading_dims():
+    from sophia_amd import ops
+    dev = _dev()
+    g = torch.Generator(device="cpu").manual_seed(2)
+    big = (torch.randn(2, 7, 3 * 64, generator=g) * 5).to(dev)
+    gu = big[..., :128]  # rows of 128 values spaced 192 apart
+    y = ops.situ_glu(gu, 4.0, 25.0)
+    torch.cuda.synchronize()
+    assert y.shape == (2, 7, 64)
+    ref = _situ_ref(gu)
+    assert float((y.double().cpu() - ref).abs().max()) <= 2e-5 * float(ref.abs().max())
+
+
+def test_feed_forward_and_mixer_modules_match_reference_formulas():
+    """FeedForward and AttentionResidualMixer (with and without the consuming
+    norm) on the kernels against the reference modules' torch formulas."""
+    from sophia_amd.config import ModelArgs
+    from sophia_amd.decoder import AttentionResidualMixer, FeedForward
+    from sophia_amd.kda import RMSNorm
+    dev = _dev()
+    torch.manual_seed(0)
+    args = ModelArgs(dim=256, ffn_hidden=320)
+    ffn = FeedForward(args).to(dev)
+    mixer = AttentionResidualMixer(args).to(dev)
+    norm = RMSNorm(256, 1e-5).to(dev)
+    with torch.no_grad():
+        for lin in (ffn.gate_up_proj, ffn.down_proj):
+            lin.weight.normal_(0, 0.1)
+        mixer.query.weight.normal_(0, 0.2)
+        mixer.norm.weight.normal_(1, 0.1)
+        norm.weight.normal_(1, 0.1)
+        x = torch.randn(2, 9, 256, device=dev)
+        completed = torch.randn(2, 9, 3, 256, device=dev)
+        y = ffn(x)
+        gate, up = (x @ ffn.gate_up_proj.weight.t()).split(320, dim=-1)
+        h = 4.0 * torch.tanh(gate / 4.0) * torch.sigmoid(gate) * 25.0 * torch.tanh(up / 25.0)
+        ref = h @ ffn.down_proj.weight.t()
+        assert float((y - ref).abs().max()) <= 1e-4 * float(ref.abs().max())
+        m = mixer(x, completed)
+        ref = _mix_ref(x, completed, mixer.norm.weight, mixer.query.weight.reshape(-1), 1e-5)
+        _check(m, ref, torch.float32)
+        mn = mixer(x, completed, norm)
+        ref = _mix_ref(x, completed, mixer.norm.weight, mixer.query.weight.reshape(-1), 1e-5,
+                       norm.weight, 1e-5)
+        _check(mn, ref, torch.float32)
