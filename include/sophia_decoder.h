@@ -58,6 +58,23 @@ int sophia_attn_res_mix(const void *partial, int64_t partial_stride, const void 
 int sophia_situ_glu(const void *gate_up, int64_t gate_up_stride, void *out, int64_t out_stride, int64_t rows,
                     int hidden, float gate_softcap, float up_softcap, int dtype, void *stream);
 
+/*
+ * Gated per-head output of the token mixers; replaces
+ *   KDA: output_norm(o.to(dtype)) * sigmoid(gate)   (ml/runtime/model/attention.py:411-420)
+ *   MLA: (o.float() * sigmoid(gate).float()).to(dtype)   (attention.py:655-656)
+ * with norm_weight [head_dim] fp32 for the first form and NULL for the second:
+ *   out[r, h, :] = (RMSNorm(o[r, h, :]; norm_weight, eps) or o[r, h, :]) * sigmoid(gate[r, h, :])
+ *   o    : [rows, heads * head_dim], row stride o_stride, dtype o_dtype (fp32 or
+ *          dtype; an fp32 o is rounded to dtype first, as the reference casts it).
+ *   gate : [rows, heads * head_dim] logits, row stride gate_stride, dtype.
+ *   out  : [rows, heads * head_dim], row stride out_stride, dtype.
+ * head_dim a power of two in [8, 512]; strides multiples of 8; pointers
+ * 16-byte aligned.  Computed in fp32, rounded once.
+ */
+int sophia_gated_head_norm(const void *o, int64_t o_stride, int o_dtype, const void *gate, int64_t gate_stride,
+                           const float *norm_weight, float eps, void *out, int64_t out_stride, int64_t rows,
+                           int heads, int head_dim, int dtype, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -56,6 +56,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "sophia_attn_res_mix": (_i32, [_vp, _i64, _vp, _i64, _i64, _i32, _vp, _vp, _f32, _vp, _f32,
                                    _vp, _i64, _i64, _i32, _i32, _vp]),
     "sophia_situ_glu": (_i32, [_vp, _i64, _vp, _i64, _i64, _i32, _f32, _f32, _i32, _vp]),
+    "sophia_gated_head_norm": (_i32, [_vp, _i64, _i32, _vp, _i64, _vp, _f32, _vp, _i64, _i64, _i32,
+                                      _i32, _i32, _vp]),
 }
 
 _lib = None

@@ -11,10 +11,14 @@
 //  * situ_glu_kernel -- the SiTU-GLU hidden of FeedForward.forward
 //    (blocks.py:23-27): h = cg tanh(g/cg) sigmoid(g) * cu tanh(u/cu) from the
 //    fused [gate | up] projection, in one pass.
+//  * gated_head_norm_kernel -- the gated outputs of the mixers: KDA's
+//    RMSNorm(o per head) * sigmoid(gate) (ml/runtime/model/attention.py:
+//    411-420) and MLA's o * sigmoid(gate) (attention.py:655-656).
 //
-// Both compute in fp32 and round once on output (the reference rounds the
+// All compute in fp32 and round once on output (the reference rounds the
 // normalised keys, the softmax weights and the products to the activation
-// dtype in between).
+// dtype in between).  Every kernel is bound by HBM traffic: each input byte
+// is read once and each output byte written once.
 #include "common.hpp"
 
 #include "../../include/sophia_decoder.h"
@@ -42,6 +46,14 @@ __device__ __forceinline__ void load8(const void *base, int64_t idx, int dtype, 
       v[i] = a[i];
       v[4 + i] = b[i];
     }
+  }
+}
+
+__device__ __forceinline__ void unpack8(const u4 w, float (&v)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __uint_as_float(w[i] << 16);
+    v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
   }
 }
 
@@ -82,24 +94,33 @@ __device__ __forceinline__ const void *depth_value(const MixArgs &a, int64_t row
   return static_cast<const uint8_t *>(a.partial) + row * a.partial_stride * esz;
 }
 
-// One row per workgroup; thread t owns the 8-element chunks t and t + blockDim
-// (dim <= 16 * blockDim).  DEPTH = completed blocks + 1, a template argument
-// so that the per-block sums stay in registers.
-template <int DEPTH>
+// One row per workgroup; thread t owns the 8-element chunks t + k blockDim,
+// k < CPT (dim <= 8 CPT blockDim).  DEPTH = completed blocks + 1.  Both are
+// template arguments so that the per-block sums, and for bf16 the values
+// themselves (4 VGPRs per chunk and block), stay in registers between the
+// score pass and the mix pass; fp32 values are read again (cache hits).
+template <int DEPTH, int CPT, bool BF16>
 __global__ __launch_bounds__(256) void attn_res_mix_kernel(MixArgs a) {
+  constexpr int kDt = BF16 ? SOPHIA_DTYPE_BF16 : SOPHIA_DTYPE_F32;
   __shared__ float red[2 * DEPTH + 1][4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nw = blockDim.x >> 6;
   const int64_t row = blockIdx.x;
   const int chunks = a.dim >> 3;
-  // Pass 1: per depth block, sum v^2 and v . (w_norm * q) over this thread's chunks.
+  u4 raw[BF16 ? DEPTH : 1][CPT];
   float ss[DEPTH], dq[DEPTH];
 #pragma unroll
   for (int b = 0; b < DEPTH; ++b) ss[b] = dq[b] = 0.f;
+  // Pass 1: per depth block, sum v^2 and v . (w_norm * q) over this thread's chunks.
 #pragma unroll
-  for (int k = 0; k < kMixChunksPerThread; ++k) {
+  for (int k = 0; k < CPT; ++k) {
     const int c = tid + k * blockDim.x;
     if (c < chunks) {
+#pragma unroll
+      for (int b = 0; b < DEPTH; ++b) {
+        if constexpr (BF16)
+          raw[b][k] = *reinterpret_cast<const u4 *>(static_cast<const uint16_t *>(depth_value(a, row, b)) + 8 * c);
+      }
       float wq[8];
       const f4 n0 = *reinterpret_cast<const f4 *>(a.norm_w + 8 * c);
       const f4 n1 = *reinterpret_cast<const f4 *>(a.norm_w + 8 * c + 4);
@@ -113,7 +134,10 @@ __global__ __launch_bounds__(256) void attn_res_mix_kernel(MixArgs a) {
 #pragma unroll
       for (int b = 0; b < DEPTH; ++b) {
         float v[8];
-        load8(depth_value(a, row, b), 8 * c, a.dtype, v);
+        if constexpr (BF16)
+          unpack8(raw[b][k], v);
+        else
+          load8(depth_value(a, row, b), 8 * c, kDt, v);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           ss[b] = fmaf(v[i], v[i], ss[b]);
@@ -154,11 +178,11 @@ __global__ __launch_bounds__(256) void attn_res_mix_kernel(MixArgs a) {
   const float rz = 1.0f / z;
 #pragma unroll
   for (int b = 0; b < DEPTH; ++b) p[b] *= rz;
-  // Pass 2: the weighted sum (the values were just read by this thread: cache hits).
-  float o[kMixChunksPerThread][8];
+  // Pass 2: the weighted sum.
+  float o[CPT][8];
   float sq = 0.f;
 #pragma unroll
-  for (int k = 0; k < kMixChunksPerThread; ++k) {
+  for (int k = 0; k < CPT; ++k) {
     const int c = tid + k * blockDim.x;
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[k][i] = 0.f;
@@ -166,7 +190,10 @@ __global__ __launch_bounds__(256) void attn_res_mix_kernel(MixArgs a) {
 #pragma unroll
       for (int b = 0; b < DEPTH; ++b) {
         float v[8];
-        load8(depth_value(a, row, b), 8 * c, a.dtype, v);
+        if constexpr (BF16)
+          unpack8(raw[b][k], v);
+        else
+          load8(depth_value(a, row, b), 8 * c, kDt, v);
 #pragma unroll
         for (int i = 0; i < 8; ++i) o[k][i] = fmaf(p[b], v[i], o[k][i]);
       }
@@ -182,7 +209,7 @@ __global__ __launch_bounds__(256) void attn_res_mix_kernel(MixArgs a) {
     for (int w = 0; w < nw; ++w) tot += red[2 * DEPTH][w];
     const float r = rsqrtf(tot / static_cast<float>(a.dim) + a.out_eps);
 #pragma unroll
-    for (int k = 0; k < kMixChunksPerThread; ++k) {
+    for (int k = 0; k < CPT; ++k) {
       const int c = tid + k * blockDim.x;
       if (c < chunks) {
         const f4 w0 = *reinterpret_cast<const f4 *>(a.out_norm_w + 8 * c);
@@ -195,44 +222,121 @@ __global__ __launch_bounds__(256) void attn_res_mix_kernel(MixArgs a) {
       }
     }
   }
-  uint8_t *dst = static_cast<uint8_t *>(a.out) + row * a.out_stride * (a.dtype == SOPHIA_DTYPE_BF16 ? 2 : 4);
+  uint8_t *dst = static_cast<uint8_t *>(a.out) + row * a.out_stride * (BF16 ? 2 : 4);
 #pragma unroll
-  for (int k = 0; k < kMixChunksPerThread; ++k) {
+  for (int k = 0; k < CPT; ++k) {
     const int c = tid + k * blockDim.x;
-    if (c < chunks) store8(dst, 8 * c, a.dtype, o[k]);
+    if (c < chunks) store8(dst, 8 * c, kDt, o[k]);
   }
 }
 
-// tanh from one exponential: t = e^{-2|x|}, tanh(x) = sign(x) (1 - t) / (1 + t);
-// below |x| = 1/8, where 1 - t cancels, the Taylor series
-// x (1 - x^2/3 + 2x^4/15 - 17x^6/315) (truncation below 2e-9 relative).
-__device__ __forceinline__ float tanh_f(float x) {
-  const float ax = fabsf(x);
-  const float t = __expf(-2.0f * ax);
-  const float big = (1.0f - t) / (1.0f + t);
+// tanh(x) for x = |z| / cap >= 0 as a fraction num / den: with t = e^{-2x},
+// (1 - t) / (1 + t); below x = 1/8, where 1 - t cancels, the Taylor series
+// x (1 - x^2/3 + 2x^4/15 - 17x^6/315) over 1 (truncation below 2e-9
+// relative).  t is returned for the sigmoid (cap 4: e^{-|z|} = t^2).
+struct Frac {
+  float num, den, t;
+};
+
+__device__ __forceinline__ Frac tanh_frac(float x) {
+  constexpr float kM2Log2e = -2.0f * 1.44269504088896341f;
+  const float t = __builtin_amdgcn_exp2f(kM2Log2e * x);
   const float x2 = x * x;
-  const float small = ax * fmaf(x2, fmaf(x2, fmaf(x2, -17.0f / 315.0f, 2.0f / 15.0f), -1.0f / 3.0f), 1.0f);
-  return copysignf(ax < 0.125f ? small : big, x);
+  const float poly = x * fmaf(x2, fmaf(x2, fmaf(x2, -17.0f / 315.0f, 2.0f / 15.0f), -1.0f / 3.0f), 1.0f);
+  const bool small = x < 0.125f;
+  return Frac{small ? poly : 1.0f - t, small ? 1.0f : 1.0f + t, t};
 }
 
+// One 8-element chunk per thread; a block covers 256 chunks of one row.
+//   h = cg tanh(g/cg) sigmoid(g) * cu tanh(u/cu)
+//     = cg cu sgn(g) sgn(u) num_g num_u s / (den_g den_u (1 + e))
+// with e = e^{-|g|} <= 1 and s = 1 (g >= 0) or e (g < 0): every factor of the
+// denominator lies in [1, 2], so one reciprocal serves the element.
 __global__ __launch_bounds__(256) void situ_glu_kernel(const void *gu, int64_t gu_stride, void *h, int64_t h_stride,
-                                                       int64_t rows, int hidden, float gate_cap, float up_cap,
+                                                       int hidden, int blocks_per_row, float gate_cap, float up_cap,
                                                        int dtype) {
-  const int chunks = hidden / 8;
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t row = t / chunks;
-  const int c = static_cast<int>(t % chunks);
-  if (row >= rows) return;
+  const int row = blockIdx.x / blocks_per_row;  // scalar
+  const int c = (blockIdx.x - row * blocks_per_row) * 256 + threadIdx.x;
+  if (8 * c >= hidden) return;
   const int esz = dtype == SOPHIA_DTYPE_BF16 ? 2 : 4;
-  const uint8_t *base = static_cast<const uint8_t *>(gu) + row * gu_stride * esz;
+  const uint8_t *base = static_cast<const uint8_t *>(gu) + static_cast<int64_t>(row) * gu_stride * esz;
   float g[8], u[8], o[8];
   load8(base, 8 * c, dtype, g);
   load8(base, hidden + 8 * c, dtype, u);
-  const float rcg = 1.0f / gate_cap, rcu = 1.0f / up_cap;
+  const float rcg = 1.0f / gate_cap, rcu = 1.0f / up_cap, scale = gate_cap * up_cap;
+  const bool cap4 = gate_cap == 4.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float ag = fabsf(g[i]);
+    const Frac fg = tanh_frac(ag * rcg);
+    const Frac fu = tanh_frac(fabsf(u[i]) * rcu);
+    const float e = cap4 ? fg.t * fg.t : __builtin_amdgcn_exp2f(-1.44269504088896341f * ag);
+    const float s = g[i] >= 0.f ? 1.0f : e;
+    const float mag = scale * fg.num * fu.num * s * __builtin_amdgcn_rcpf(fg.den * fu.den * (1.0f + e));
+    o[i] = copysignf(mag, g[i]) * (u[i] < 0.f ? -1.0f : 1.0f);
+  }
+  store8(static_cast<uint8_t *>(h) + static_cast<int64_t>(row) * h_stride * esz, 8 * c, dtype, o);
+}
+
+// Gated per-head output: y = (RMSNorm_head(o; w, eps) or o) * sigmoid(gate).
+// One 8-element chunk per thread, G = head_dim / 8 consecutive lanes per head
+// (G a power of two <= 64, so a head never straddles a wavefront); a block
+// covers 256 chunks of one row.
+struct GateArgs {
+  const void *o;
+  int64_t o_stride;
+  int o_dtype;
+  const void *gate;
+  int64_t gate_stride;
+  const float *norm_w;  // [head_dim] or NULL
+  float eps;
+  void *out;
+  int64_t out_stride;
+  int width;  // heads * head_dim
+  int head_dim;
+  int blocks_per_row;
+  int dtype;  // of gate and out
+};
+
+__global__ __launch_bounds__(256) void gated_head_norm_kernel(GateArgs a) {
+  const int row = blockIdx.x / a.blocks_per_row;  // scalar
+  const int c = (blockIdx.x - row * a.blocks_per_row) * 256 + threadIdx.x;
+  const int G = a.head_dim >> 3;
+  const bool valid = 8 * c < a.width;  // whole heads are valid or not
+  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, g[8];
+  if (valid) {
+    load8(static_cast<const uint8_t *>(a.o) + static_cast<int64_t>(row) * a.o_stride * (a.o_dtype == SOPHIA_DTYPE_BF16 ? 2 : 4),
+          8 * c, a.o_dtype, o);
+    load8(static_cast<const uint8_t *>(a.gate) + static_cast<int64_t>(row) * a.gate_stride * (a.dtype == SOPHIA_DTYPE_BF16 ? 2 : 4),
+          8 * c, a.dtype, g);
+    if (a.o_dtype != a.dtype) {  // the reference casts o to the activation dtype first
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = __uint_as_float(static_cast<uint32_t>(f32_to_bf16_bits(o[i])) << 16);
+    }
+  }
+  if (a.norm_w != nullptr) {  // uniform
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss = fmaf(o[i], o[i], ss);
+    for (int off = G >> 1; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    const float r = rsqrtf(ss / static_cast<float>(a.head_dim) + a.eps);
+    if (valid) {
+      const int e0 = 8 * (c & (G - 1));
+      const f4 w0 = *reinterpret_cast<const f4 *>(a.norm_w + e0);
+      const f4 w1 = *reinterpret_cast<const f4 *>(a.norm_w + e0 + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        o[i] *= r * w0[i];
+        o[4 + i] *= r * w1[i];
+      }
+    }
+  }
+  if (!valid) return;
 #pragma unroll
   for (int i = 0; i < 8; ++i)
-    o[i] = gate_cap * tanh_f(g[i] * rcg) * sigmoid_f(g[i]) * (up_cap * tanh_f(u[i] * rcu));
-  store8(static_cast<uint8_t *>(h) + row * h_stride * esz, 8 * c, dtype, o);
+    o[i] *= __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.44269504088896341f * g[i]));
+  store8(static_cast<uint8_t *>(a.out) + static_cast<int64_t>(row) * a.out_stride * (a.dtype == SOPHIA_DTYPE_BF16 ? 2 : 4),
+         8 * c, a.dtype, o);
 }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -271,14 +375,22 @@ extern "C" int sophia_attn_res_mix(const void *partial, int64_t partial_stride, 
   const int threads = ((chunks + per_thread - 1) / per_thread + 63) / 64 * 64;
   const dim3 grid(static_cast<unsigned>(rows)), block(threads);
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  switch (n_blocks + 1) {
-#define SOPHIA_MIX_CASE(d) \
-  case d: hipLaunchKernelGGL(attn_res_mix_kernel<d>, grid, block, 0, st, a); break;
-    SOPHIA_MIX_CASE(1) SOPHIA_MIX_CASE(2) SOPHIA_MIX_CASE(3) SOPHIA_MIX_CASE(4)
-    SOPHIA_MIX_CASE(5) SOPHIA_MIX_CASE(6) SOPHIA_MIX_CASE(7) SOPHIA_MIX_CASE(8)
-    SOPHIA_MIX_CASE(9) SOPHIA_MIX_CASE(10) SOPHIA_MIX_CASE(11) SOPHIA_MIX_CASE(12)
-    SOPHIA_MIX_CASE(13) SOPHIA_MIX_CASE(14) SOPHIA_MIX_CASE(15) SOPHIA_MIX_CASE(16)
+  const int key = (n_blocks + 1) * 4 + (per_thread - 1) * 2 + (dtype == SOPHIA_DTYPE_BF16 ? 1 : 0);
+  switch (key) {
+#define SOPHIA_MIX_CASE(d, cpt, bf)                                                              \
+  case d * 4 + (cpt - 1) * 2 + bf:                                                                \
+    hipLaunchKernelGGL((attn_res_mix_kernel<d, cpt, bf != 0>), grid, block, 0, st, a);           \
+    break;
+#define SOPHIA_MIX_DEPTH(d) \
+  SOPHIA_MIX_CASE(d, 1, 0) SOPHIA_MIX_CASE(d, 1, 1) SOPHIA_MIX_CASE(d, 2, 0) SOPHIA_MIX_CASE(d, 2, 1)
+    SOPHIA_MIX_DEPTH(1) SOPHIA_MIX_DEPTH(2) SOPHIA_MIX_DEPTH(3) SOPHIA_MIX_DEPTH(4)
+    SOPHIA_MIX_DEPTH(5) SOPHIA_MIX_DEPTH(6) SOPHIA_MIX_DEPTH(7) SOPHIA_MIX_DEPTH(8)
+    SOPHIA_MIX_DEPTH(9) SOPHIA_MIX_DEPTH(10) SOPHIA_MIX_DEPTH(11) SOPHIA_MIX_DEPTH(12)
+    SOPHIA_MIX_DEPTH(13) SOPHIA_MIX_DEPTH(14) SOPHIA_MIX_DEPTH(15) SOPHIA_MIX_DEPTH(16)
+#undef SOPHIA_MIX_DEPTH
 #undef SOPHIA_MIX_CASE
+    default:
+      return set_error(SOPHIA_ERR_INVALID, "attn_res_mix: no kernel for depth %d", n_blocks + 1);
   }
   return check_launch("attn_res_mix");
 }
@@ -294,12 +406,44 @@ extern "C" int sophia_situ_glu(const void *gate_up, int64_t gate_up_stride, void
                  "situ_glu: bad strides");
   SOPHIA_REQUIRE(gate_softcap > 0.f && up_softcap > 0.f, "situ_glu: soft caps must be positive");
   SOPHIA_REQUIRE(aligned16(gate_up) && aligned16(hidden_out), "situ_glu: pointers must be 16-byte aligned");
+  SOPHIA_REQUIRE(rows <= 0x7fffffff, "situ_glu: too many rows");
   if (rows == 0) return SOPHIA_OK;
-  const int64_t threads = rows * (hidden / 8);
-  const int64_t blocks = (threads + 255) / 256;
+  const int blocks_per_row = (hidden / 8 + 255) / 256;
+  const int64_t blocks = rows * blocks_per_row;
   SOPHIA_REQUIRE(blocks <= 0x7fffffff, "situ_glu: too many rows");
   hipLaunchKernelGGL(situ_glu_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), gate_up, gate_up_stride, hidden_out, out_stride, rows, hidden,
-                     gate_softcap, up_softcap, dtype);
+                     static_cast<hipStream_t>(stream), gate_up, gate_up_stride, hidden_out, out_stride, hidden,
+                     blocks_per_row, gate_softcap, up_softcap, dtype);
   return check_launch("situ_glu");
+}
+
+extern "C" int sophia_gated_head_norm(const void *o, int64_t o_stride, int o_dtype, const void *gate,
+                                      int64_t gate_stride, const float *norm_weight, float eps, void *out,
+                                      int64_t out_stride, int64_t rows, int heads, int head_dim, int dtype,
+                                      void *stream) {
+  SOPHIA_REQUIRE((dtype == SOPHIA_DTYPE_F32 || dtype == SOPHIA_DTYPE_BF16) &&
+                     (o_dtype == SOPHIA_DTYPE_F32 || o_dtype == SOPHIA_DTYPE_BF16),
+                 "gated_head_norm: dtype not supported");
+  SOPHIA_REQUIRE(o_dtype == dtype || o_dtype == SOPHIA_DTYPE_F32, "gated_head_norm: o may be fp32 or the gate's dtype");
+  SOPHIA_REQUIRE(head_dim >= 8 && head_dim <= 512 && (head_dim & (head_dim - 1)) == 0,
+                 "gated_head_norm: head_dim must be a power of two in [8, 512]");
+  SOPHIA_REQUIRE(heads > 0 && rows >= 0 && static_cast<int64_t>(heads) * head_dim <= (1 << 24),
+                 "gated_head_norm: bad heads / rows");
+  const int64_t width = static_cast<int64_t>(heads) * head_dim;
+  SOPHIA_REQUIRE(o_stride % 8 == 0 && gate_stride % 8 == 0 && out_stride % 8 == 0 && o_stride >= width &&
+                     gate_stride >= width && out_stride >= width,
+                 "gated_head_norm: strides must be multiples of 8 elements and cover a row");
+  SOPHIA_REQUIRE(rows == 0 || (o && gate && out), "gated_head_norm: NULL pointer");
+  SOPHIA_REQUIRE(aligned16(o) && aligned16(gate) && aligned16(out) && aligned16(norm_weight),
+                 "gated_head_norm: pointers must be 16-byte aligned");
+  SOPHIA_REQUIRE(rows <= 0x7fffffff, "gated_head_norm: too many rows");
+  if (rows == 0) return SOPHIA_OK;
+  const int blocks_per_row = static_cast<int>((width / 8 + 255) / 256);
+  const int64_t blocks = rows * blocks_per_row;
+  SOPHIA_REQUIRE(blocks <= 0x7fffffff, "gated_head_norm: too many rows");
+  GateArgs a{o, o_stride, o_dtype, gate, gate_stride, norm_weight, eps, out, out_stride, static_cast<int>(width),
+             head_dim, blocks_per_row, dtype};
+  hipLaunchKernelGGL(gated_head_norm_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return check_launch("gated_head_norm");
 }

@@ -106,9 +106,11 @@ class SophiaMLA(nn.Module):
 
     # ------------------------------------------------------------- forward
     def _gate_out(self, x: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
-        gate = torch.sigmoid(self.output_gate(x)).view_as(out)
-        gated = (out.float() * gate.float()).to(dtype=x.dtype)
-        return self.o_proj(gated.reshape(*gated.shape[:-2], self.inner_dim))
+        """attention.py:655-657: o_proj((o.float() * sigmoid(gate).float()).to(dtype)),
+        the gate as one HIP kernel (ops.gated_head_norm without a norm)."""
+        gate = self.output_gate(x)
+        gated = ops.gated_head_norm(out.to(x.dtype), gate, self.num_heads, self.head_dim)
+        return self.o_proj(gated.view(*x.shape[:-1], self.inner_dim))
 
     def forward(self, x: torch.Tensor, *, start_pos: int = 0) -> torch.Tensor:
         """attention.py:609-657 (pad-mask path: attention.py:585-600,635-654)."""

@@ -239,12 +239,14 @@ class SophiaKDA(nn.Module):
         return value
 
     def _input_weight(self, dtype: torch.dtype) -> torch.Tensor:
-        """[3*inner + decay_rank + heads (+ inner | + gate_rank), dim], padded
+        """[3*inner + (inner | gate_rank) + decay_rank + heads, dim], padded
         with zero rows to a multiple of 8: every projection of x in one GEMM,
-        whose output rows then start on 16-byte boundaries (the ShortConv
-        kernel reads the q|k|v columns with 16-byte vector loads)."""
-        mods = [self.q_proj, self.k_proj, self.v_proj, self.decay_down, self.beta_proj]
-        mods.append(self.output_gate if self.output_gate_full_rank else self.output_gate_down)
+        whose output rows then start on 16-byte boundaries.  The q|k|v and
+        gate columns come first, at multiples of 8 columns, because the
+        ShortConv and gated-norm kernels read them with 16-byte vector loads."""
+        mods = [self.q_proj, self.k_proj, self.v_proj,
+                self.output_gate if self.output_gate_full_rank else self.output_gate_down,
+                self.decay_down, self.beta_proj]
         params = tuple(m.weight for m in mods)
 
         def build():
@@ -263,11 +265,11 @@ class SophiaKDA(nn.Module):
         """x2: [N, dim] -> views (qkv [N, 3*inner], decay_down, beta, gate_logits)."""
         y = F.linear(x2, self._input_weight(x2.dtype))
         i, r, h = self.inner_dim, self.decay_rank, self.num_heads
+        g = i if self.output_gate_full_rank else self.output_gate_rank
         qkv = y[:, : 3 * i]
-        dd = y[:, 3 * i: 3 * i + r]
-        beta = y[:, 3 * i + r: 3 * i + r + h]
-        gate = y[:, 3 * i + r + h: 3 * i + r + h + (i if self.output_gate_full_rank
-                                                     else self.output_gate_rank)]
+        gate = y[:, 3 * i: 3 * i + g]
+        dd = y[:, 3 * i + g: 3 * i + g + r]
+        beta = y[:, 3 * i + g + r: 3 * i + g + r + h]
         if not self.output_gate_full_rank:
             gate = self.output_gate_up(gate)
         return qkv, dd, beta, gate
@@ -320,11 +322,13 @@ class SophiaKDA(nn.Module):
                                   state_slots=slots, read_history=read, write_history=write)
 
     def _output(self, o: torch.Tensor, gate_logits: torch.Tensor, dtype) -> torch.Tensor:
-        """attention.py:411-420: o_proj(RMSNorm(o) * sigmoid(gate))."""
-        n = o.size(0)
-        gate = torch.sigmoid(gate_logits).view(n, self.num_heads, self.head_dim)
-        out = self.output_norm(o.to(dtype)) * gate
-        return self.o_proj(out.reshape(n, self.inner_dim))
+        """attention.py:411-420: o_proj(RMSNorm(o) * sigmoid(gate)), the gated
+        per-head norm as one HIP kernel (ops.gated_head_norm)."""
+        if gate_logits.dtype != dtype:
+            gate_logits = gate_logits.to(dtype)
+        out = ops.gated_head_norm(o, gate_logits, self.num_heads, self.head_dim,
+                                  norm_weight=self.output_norm.weight, eps=self.output_norm.eps)
+        return self.o_proj(out)
 
     def forward(self, x: torch.Tensor, *, start_pos: int = 0) -> torch.Tensor:
         """attention.py:373-420."""

@@ -455,3 +455,49 @@ def situ_glu(gate_up: torch.Tensor, gate_softcap: float, up_softcap: float, *,
                                    nat.dtype_code(gate_up.dtype), nat.stream_handle(gate_up.device))
     nat.check(rc, "sophia_situ_glu")
     return y2.view(*lead, hidden)
+
+
+def gated_head_norm(o: torch.Tensor, gate: torch.Tensor, heads: int, head_dim: int, *,
+                    norm_weight: torch.Tensor | None = None, eps: float = 1e-6,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """The gated outputs of the token mixers in one pass over [rows, heads * head_dim]:
+    with ``norm_weight``, KDA's output_norm(o.to(dtype)) * sigmoid(gate)
+    (ml/runtime/model/attention.py:411-420, RMSNorm over each head); without,
+    MLA's (o.float() * sigmoid(gate).float()).to(dtype) (attention.py:655-656).
+
+    o: [..., heads * head_dim] (or [..., heads, head_dim]) in fp32 or gate's
+    dtype; gate: [..., heads * head_dim] logits with dense rows (a column
+    slice of a fused projection is fine).  Returns [rows, heads * head_dim] in
+    gate.dtype, computed in fp32 and rounded once."""
+    _gpu(o, "o")
+    _gpu(gate, "gate")
+    width = int(heads) * int(head_dim)
+    o2 = o.reshape(-1, width)
+    g2 = gate.reshape(-1, width)
+    rows = int(g2.size(0))
+    if int(o2.size(0)) != rows:
+        raise RuntimeError(f"o has {int(o2.size(0))} rows, gate {rows}")
+    os_ = _rows(o2, "o", width)
+    gs = _rows(g2, "gate", width)
+    if o.dtype not in (torch.float32, gate.dtype):
+        raise RuntimeError("o must be float32 or gate's dtype")
+    w = None
+    if norm_weight is not None:
+        w = norm_weight.detach().reshape(-1).to(device=gate.device, dtype=torch.float32).contiguous()
+        if int(w.numel()) != int(head_dim):
+            raise RuntimeError(f"norm_weight must hold {head_dim} values")
+        _aligned(w, "norm_weight")
+    if out is not None and not out.is_contiguous():
+        raise RuntimeError("out must be contiguous")
+    y = out if out is not None else torch.empty((rows, width), dtype=gate.dtype, device=gate.device)
+    if y.dtype != gate.dtype or int(y.numel()) != rows * width:
+        raise RuntimeError(f"out must be {gate.dtype} with {rows * width} elements")
+    y2 = y.view(rows, width)
+    for t, name in ((o2, "o"), (g2, "gate"), (y2, "out")):
+        _aligned(t, name)
+    rc = nat.lib().sophia_gated_head_norm(
+        nat.ptr(o2), os_, nat.dtype_code(o.dtype), nat.ptr(g2), gs, nat.ptr(w), float(eps),
+        nat.ptr(y2), width, rows, int(heads), int(head_dim), nat.dtype_code(gate.dtype),
+        nat.stream_handle(gate.device))
+    nat.check(rc, "sophia_gated_head_norm")
+    return y2

@@ -41,7 +41,7 @@ def test_header_declares_the_entry_points():
     for name in ("sophia_short_conv_fwd", "sophia_short_conv_step", "sophia_kda_chunk_fwd",
                  "sophia_kda_chunk_workspace_size", "sophia_kda_decode_step",
                  "sophia_last_error", "sophia_abi_version", "sophia_attn_res_mix",
-                 "sophia_situ_glu"):
+                 "sophia_situ_glu", "sophia_gated_head_norm"):
         assert name in decls, name
 
 
@@ -103,6 +103,14 @@ def test_host_side_queries_and_validation():
     # Non-null addresses that are never dereferenced: the stride check fails first.
     rc = lib.sophia_situ_glu(16, 3968, 32, 3968, 4, 3968, 4.0, 25.0, 1, None)
     assert rc == nat.SOPHIA_ERR_INVALID and "stride" in nat.last_error()
+    rc = lib.sophia_gated_head_norm(16, 2048, 1, 32, 2048, None, 1e-5, 48, 2048, 4, 16, 96, 1, None)
+    assert rc == nat.SOPHIA_ERR_INVALID and "head_dim" in nat.last_error()
+    rc = lib.sophia_gated_head_norm(16, 2048, 1, 40, 2048, None, 1e-5, 48, 2048, 4, 16, 128, 1, None)
+    assert rc == nat.SOPHIA_ERR_INVALID and "aligned" in nat.last_error()
+    rc = lib.sophia_gated_head_norm(16, 2048, 1, 32, 2047, None, 1e-5, 48, 2048, 4, 16, 128, 1, None)
+    assert rc == nat.SOPHIA_ERR_INVALID and "stride" in nat.last_error()
+    rc = lib.sophia_gated_head_norm(16, 2048, 1, 32, 2048, None, 1e-5, 48, 2048, 4, 16, 128, 0, None)
+    assert rc == nat.SOPHIA_ERR_INVALID and "dtype" in nat.last_error()
 
 
 def test_ops_reject_cpu_tensors():
@@ -121,3 +129,5 @@ def test_ops_reject_cpu_tensors():
                          torch.zeros(64), 1e-5)
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         ops.situ_glu(torch.zeros(4, 64), 4.0, 25.0)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.gated_head_norm(torch.zeros(4, 256), torch.zeros(4, 256), 2, 128)

@@ -1,6 +1,8 @@
 """GPU parity of the decoder-side HIP kernels (sophia_decoder.h) through the
 C ABI: the attention-residual depth mixer (blocks.py:38-48, optionally with
-the RMSNorm that consumes it) and the SiTU-GLU activation (blocks.py:23-27).
+the RMSNorm that consumes it), the SiTU-GLU activation (blocks.py:23-27) and
+the gated per-head outputs of the KDA and MLA mixers (attention.py:411-420,
+655-656).
 
 References are computed in float64 on the host from the same (rounded)
 inputs: the module's formulas written with torch ops, and, for the mixer, the
@@ -183,3 +185,47 @@ def test_feed_forward_and_mixer_modules_match_reference_formulas():
         ref = _mix_ref(x, completed, mixer.norm.weight, mixer.query.weight.reshape(-1), 1e-5,
                        norm.weight, 1e-5)
         _check(mn, ref, torch.float32)
+
+
+def _gated_ref(o, gate, heads, head_dim, w=None, eps=1e-6):
+    """attention.py:411-420 (with w) / 655-656 (without) in float64, o first
+    rounded to the gate's dtype as the reference casts it."""
+    rows = gate.reshape(-1, heads * head_dim).size(0)
+    o = o.to(gate.dtype).double().cpu().reshape(rows, heads, head_dim)
+    g = gate.double().cpu().reshape(rows, heads, head_dim)
+    if w is not None:
+        o = o * torch.rsqrt(o.pow(2).mean(-1, keepdim=True) + eps) * w.double().cpu()
+    return (o * torch.sigmoid(g)).reshape(rows, heads * head_dim)
+
+
+@pytest.mark.parametrize("dtype,o_dtype", [(torch.float32, torch.float32),
+                                           (torch.bfloat16, torch.bfloat16),
+                                           (torch.bfloat16, torch.float32)])
+@pytest.mark.parametrize("rows,heads,head_dim", [(1, 16, 128), (300, 16, 128), (7, 3, 8),
+                                                 (33, 2, 512), (64, 5, 64)])
+@pytest.mark.parametrize("normed", [True, False])
+def test_gated_head_norm_matches_fp64_reference(dtype, o_dtype, rows, heads, head_dim, normed):
+    from sophia_amd import ops
+    dev = _dev()
+    g = torch.Generator(device="cpu").manual_seed(rows * 3 + heads * 5 + head_dim)
+    width = heads * head_dim
+    o = (torch.randn(rows, heads, head_dim, generator=g) * 3).to(dev, o_dtype)
+    # gate logits as a column slice of a wider fused projection (row stride > width)
+    fused = (torch.randn(rows, width + 24, generator=g) * 4).to(dev, dtype)
+    gate = fused[:, 16:16 + width]
+    w = (1 + 0.3 * torch.randn(head_dim, generator=g)).to(dev) if normed else None
+    y = ops.gated_head_norm(o, gate, heads, head_dim, norm_weight=w, eps=1e-5)
+    torch.cuda.synchronize()
+    assert y.shape == (rows, width) and y.dtype == dtype
+    _check(y, _gated_ref(o, gate, heads, head_dim, w, 1e-5), dtype)
+
+
+def test_gated_head_norm_rejects_misaligned_and_bad_shapes():
+    from sophia_amd import ops
+    dev = _dev()
+    o = torch.zeros(4, 2 * 128, device=dev)
+    fused = torch.zeros(4, 2 * 128 + 8, device=dev)
+    with pytest.raises(RuntimeError, match="aligned"):
+        ops.gated_head_norm(o, fused[:, 2:2 + 256], 2, 128)
+    with pytest.raises(RuntimeError, match="head_dim"):
+        ops.gated_head_norm(torch.zeros(4, 2 * 96, device=dev), torch.zeros(4, 2 * 96, device=dev), 2, 96)
