@@ -121,7 +121,8 @@ def copy_bandwidth(torch, dev, stream, nbytes: int = 1 << 30) -> float:
     return 2 * nbytes / (float(np.median(per)) / 1e3) / 1e9
 
 
-def mixed_step_bench(torch, dev, stream, steps: int, warmup: int, seed: int = 4) -> dict:
+def mixed_step_bench(torch, dev, stream, steps: int, warmup: int, seed: int = 4,
+                     tune_gemms: str | None = None) -> dict:
     """The whole hybrid decoder (28 layers [KDA, KDA, KDA, MLA] x 7, dim 1536,
     16 heads x 128, SiTU-GLU 3968, MLA ranks 384 / 128, vocab 65,536, tied;
     random init, bf16 GEMM weights, fp32 caches) in one continuous-batching
@@ -129,7 +130,12 @@ def mixed_step_bench(torch, dev, stream, steps: int, warmup: int, seed: int = 4)
     token for each of 240 running sequences (cached lengths U[1, 1023],
     seeded; random latent caches, zero recurrent state).  The step is
     captured in a HIP graph after two warm-up runs on a side stream and
-    replayed; the eager step is timed beside it."""
+    replayed; the eager step is timed beside it.  The library GEMMs run first
+    with hipBLASLt's default per-shape heuristics, then with the per-shape
+    selection of sophia_amd/gemm_tuning_gfx950.csv (torch TunableOp, no timing
+    runs) when that file matches this software stack; the step figures are
+    those of the faster of the two, and both are reported.  With
+    ``tune_gemms``, the selection is timed here and written to that file."""
     from sophia_amd.config import ModelArgs
     from sophia_amd.decoder import MixedStepGraph, Transformer
     from sophia_amd.kda import RuntimeLinear
@@ -156,12 +162,27 @@ def mixed_step_bench(torch, dev, stream, steps: int, warmup: int, seed: int = 4)
         with torch.no_grad():
             return model.forward_mixed(max_decode_len=L, **step)
 
-    _, eper = time_events(torch, eager, max(steps // 4, 3), 2, stream)
-    graph = MixedStepGraph(model, P, T, D, L, warmup=2, example=step)
-    _, gper = time_events(torch, graph.run, steps, warmup, stream)
-    if not torch.isfinite(graph.logits.float()).all():
-        raise RuntimeError("non-finite logits from the captured mixed step")
-    gms, ems = float(np.mean(gper)), float(np.mean(eper))
+    from sophia_amd import gemm_tuning
+
+    def measure():
+        _, eper = time_events(torch, eager, max(steps // 4, 3), 2, stream)
+        graph = MixedStepGraph(model, P, T, D, L, warmup=2, example=step)
+        _, gper = time_events(torch, graph.run, steps, warmup, stream)
+        if not torch.isfinite(graph.logits.float()).all():
+            raise RuntimeError("non-finite logits from the captured mixed step")
+        del graph
+        return float(np.mean(gper)), float(np.mean(eper))
+
+    gemm_runs = {"default": measure()}
+    if tune_gemms:
+        gemm_tuning.use_tuned_gemms(tune_gemms, tune=True)
+        eager()  # times every GEMM shape of the step once
+        gemm_runs["tuned"] = measure()
+    elif gemm_tuning.use_tuned_gemms():
+        gemm_runs["tuned"] = measure()
+    gemm_tuning.use_default_gemms()
+    selection = min(gemm_runs, key=lambda k: gemm_runs[k][0])
+    gms, ems = gemm_runs[selection]
     tokens = P * T + D
 
     # Work per step: every per-token GEMM (MLA k_up / v_up on prefill rows
@@ -190,8 +211,10 @@ def mixed_step_bench(torch, dev, stream, steps: int, warmup: int, seed: int = 4)
            "eager_ms_per_step": round(ems, 3), "graph_speedup": round(ems / gms, 3),
            "approx_tflops": round(tflops, 1),
            "frac_of_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4),
-           "flops_per_step": flops, "steps": steps}
-    del graph, model
+           "flops_per_step": flops, "steps": steps,
+           "gemm_selection": selection,
+           "ms_per_step_by_gemm_selection": {k: round(v[0], 3) for k, v in gemm_runs.items()}}
+    del model
     torch.cuda.empty_cache()
     return out
 
@@ -202,6 +225,9 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--tune-gemms", metavar="CSV", default=None,
+                    help="time the mixed step's library GEMM candidates and write the "
+                         "per-shape selection to CSV (torch TunableOp)")
     ap.add_argument("--only", choices=["all", "kda", "prefill", "conv", "decode", "copy", "mixed"],
                     default="all",
                     help="run one workload only (for kernel profiling; 'kda' = prefill, ShortConv "
@@ -337,7 +363,8 @@ def main(argv=None) -> int:
 
     if args.only in ("all", "mixed"):
         result["mixed_step"] = mixed_step_bench(torch, dev, stream, max(args.steps // 2, 5),
-                                                max(args.warmup // 2, 2))
+                                                max(args.warmup // 2, 2),
+                                                tune_gemms=args.tune_gemms)
     if args.only == "all":
         result["hbm_copy_GBps"] = round(copy_bandwidth(torch, dev, stream), 1)
     if not args.no_cpu and args.only == "all":

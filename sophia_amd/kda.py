@@ -256,9 +256,13 @@ class SophiaKDA(nn.Module):
 
         return self._cached("in", params, build, dtype)
 
-    def _conv_weight(self) -> torch.Tensor:
+    def _conv_weight(self, dtype: torch.dtype) -> torch.Tensor:
+        """The q|k|v conv taps [3*inner, K] rounded to the activation dtype and
+        held as fp32 (what the ShortConv kernels take), rebuilt only when a
+        weight changes."""
         params = (self.q_conv.weight, self.k_conv.weight, self.v_conv.weight)
-        return self._cached("conv", params, lambda: torch.cat([p.detach() for p in params], 0),
+        return self._cached(f"conv_{dtype}", params,
+                            lambda: torch.cat([p.detach() for p in params], 0).to(dtype),
                             torch.float32)
 
     def _project(self, x2: torch.Tensor):
@@ -315,11 +319,12 @@ class SophiaKDA(nn.Module):
         is the history of projection i (attention.py:226-258)."""
         state = self.conv_state.view(self.conv_state.size(0), 3 * self.inner_dim,
                                      self.conv_kernel - 1) if self.conv_kernel > 1 else None
+        conv_w = self._conv_weight(qkv.dtype)
         if step:
-            return ops.short_conv_step(qkv, self._conv_weight(), state, state_slots=slots,
-                                       read_history=read)
-        return ops.short_conv_fwd(qkv, self._conv_weight(), cu, conv_state=state,
-                                  state_slots=slots, read_history=read, write_history=write)
+            return ops.short_conv_step(qkv, conv_w, state, state_slots=slots, read_history=read,
+                                       weight_rounded=True)
+        return ops.short_conv_fwd(qkv, conv_w, cu, conv_state=state, state_slots=slots,
+                                  read_history=read, write_history=write, weight_rounded=True)
 
     def _output(self, o: torch.Tensor, gate_logits: torch.Tensor, dtype) -> torch.Tensor:
         """attention.py:411-420: o_proj(RMSNorm(o) * sigmoid(gate)), the gated
@@ -436,15 +441,16 @@ class SophiaKDA(nn.Module):
         hist = self.conv_kernel - 1
         conv_state = (self.conv_state.view(self.conv_state.size(0), 3 * i, hist)
                       if hist > 0 else None)
-        conv_w = self._conv_weight()
+        conv_w = self._conv_weight(qkv.dtype)
         conv_out = torch.empty((n, 3 * i), dtype=qkv.dtype, device=qkv.device)
         if n_prefill > 0:
             ops.short_conv_fwd(qkv[:n_prefill], conv_w, cu_prefill, conv_state=conv_state,
                                state_slots=prefill_slots, read_history=False,
-                               write_history=hist > 0, out=conv_out[:n_prefill])
+                               write_history=hist > 0, out=conv_out[:n_prefill],
+                               weight_rounded=True)
         if n_decode > 0:
             ops.short_conv_step(qkv[n_prefill:], conv_w, conv_state, state_slots=decode_slots,
-                                read_history=True, out=conv_out[n_prefill:])
+                                read_history=True, out=conv_out[n_prefill:], weight_rounded=True)
         q = conv_out[:, :i].unflatten(1, (h, d))
         k = conv_out[:, i: 2 * i].unflatten(1, (h, d))
         v = conv_out[:, 2 * i:].unflatten(1, (h, d))

@@ -63,17 +63,30 @@ def _workspace(nbytes: int, device) -> tuple[torch.Tensor, int, int]:
 
 
 # ------------------------------------------------------------------ ShortConv
+def _conv_taps(weight: torch.Tensor, x: torch.Tensor, rounded: bool) -> torch.Tensor:
+    """The conv taps as the kernels take them: fp32 [C, K] holding the weight
+    rounded to x.dtype (the reference casts the weight to x's dtype)."""
+    if not rounded:
+        return weight.detach().to(device=x.device, dtype=x.dtype).float().contiguous()
+    if weight.dtype != torch.float32 or not weight.is_contiguous() or weight.device != x.device:
+        raise RuntimeError("a rounded conv weight must be contiguous fp32 on x's device")
+    return weight
+
+
 def short_conv_fwd(x: torch.Tensor, weight: torch.Tensor, cu_seqlens: torch.Tensor, *,
                    conv_state: torch.Tensor | None = None,
                    state_slots: torch.Tensor | None = None, read_history: bool = False,
-                   write_history: bool = False, out: torch.Tensor | None = None) -> torch.Tensor:
+                   write_history: bool = False, out: torch.Tensor | None = None,
+                   weight_rounded: bool = False) -> torch.Tensor:
     """Causal depthwise conv + SiLU over a packed batch (CausalDepthwiseConv1d.forward,
     attention.py:32-60, applied per sequence of ``cu_seqlens``).
 
     x: [total, C] (rows may be strided); weight: [C, K] (cast to x.dtype then
     fp32, as the reference casts the weight to x's dtype); conv_state:
     [slots, C, K-1] fp32, read when ``read_history`` and written when
-    ``write_history``.  Returns y [total, C] in x.dtype.
+    ``write_history``.  ``weight_rounded``: weight is already the contiguous
+    fp32 [C, K] copy of its x.dtype rounding (no cast is launched).
+    Returns y [total, C] in x.dtype.
     """
     _gpu(x, "x")
     channels = int(x.size(1))
@@ -81,7 +94,7 @@ def short_conv_fwd(x: torch.Tensor, weight: torch.Tensor, cu_seqlens: torch.Tens
     kernel = int(weight.size(1))
     if weight.dim() != 2 or int(weight.size(0)) != channels:
         raise RuntimeError(f"weight must be [{channels}, K], got {tuple(weight.shape)}")
-    w = weight.detach().to(device=x.device, dtype=x.dtype).float().contiguous()
+    w = _conv_taps(weight, x, weight_rounded)
     cu = _int32(cu_seqlens, "cu_seqlens", x.device)
     n = int(cu.numel()) - 1
     if conv_state is not None:
@@ -105,7 +118,7 @@ def short_conv_fwd(x: torch.Tensor, weight: torch.Tensor, cu_seqlens: torch.Tens
 
 def short_conv_step(x: torch.Tensor, weight: torch.Tensor, conv_state: torch.Tensor, *,
                     state_slots: torch.Tensor | None = None, read_history: bool = True,
-                    out: torch.Tensor | None = None) -> torch.Tensor:
+                    out: torch.Tensor | None = None, weight_rounded: bool = False) -> torch.Tensor:
     """One-token conv step for a batch of sequences (decode), history updated in place.
     x: [B, C]; conv_state: [slots, C, K-1] fp32."""
     _gpu(x, "x")
@@ -116,7 +129,7 @@ def short_conv_step(x: torch.Tensor, weight: torch.Tensor, conv_state: torch.Ten
     if (conv_state.dtype != torch.float32 or not conv_state.is_contiguous()
             or tuple(conv_state.shape[1:]) != (channels, kernel - 1)):
         raise RuntimeError("conv_state must be contiguous fp32 [slots, C, K-1]")
-    w = weight.detach().to(device=x.device, dtype=x.dtype).float().contiguous()
+    w = _conv_taps(weight, x, weight_rounded)
     slots = _int32(state_slots, "state_slots", x.device)
     y = out if out is not None else torch.empty_like(x, memory_format=torch.contiguous_format)
     ys = _rows(y, "out", channels)
