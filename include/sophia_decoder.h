@@ -75,6 +75,30 @@ int sophia_gated_head_norm(const void *o, int64_t o_stride, int o_dtype, const v
                            const float *norm_weight, float eps, void *out, int64_t out_stride, int64_t rows,
                            int heads, int head_dim, int dtype, void *stream);
 
+/*
+ * Absorbed MLA decode attention over the fp32 latent cache; replaces the
+ * decode-row attention of SophiaMLA with NoPE (ml/runtime/model/attention.py:
+ * 609-657 with a cache, keys = k_up(c), values = v_up(c)), written in latent
+ * space: for each decode row b and head h, with qa[b, h] = W_k,h^T q[b, h],
+ *   p = softmax_k(scale * qa[b, h] . latent[slot_b, k]),  k = 0 .. pos_b
+ *   out[b, h] = sum_k p_k latent[slot_b, k]      (W_v,h is applied by the caller)
+ *   qa      : [rows, heads, rank], row stride qa_stride (bf16 or fp32).
+ *   latent  : [n_slots, max_seq, rank] fp32, slot stride slot_stride, rows of rank.
+ *   slots   : [rows] int32; pos : [rows] int64 (keys 0..pos, clamped to max_seq;
+ *             a row whose slot is outside [0, n_slots) gets zeros).
+ *   out     : [rows, heads, rank], row stride out_stride (bf16 or fp32).
+ * qa and the latents are rounded to bf16 for the products (the reference
+ * casts both to the activation dtype); scores, softmax and sums are fp32.
+ * rank in {32, 64, 128, 256}; heads <= 16.  splits > 1 divides each row's keys
+ * among that many work-groups and needs a workspace of
+ * sophia_mla_decode_workspace_size(rows, rank, splits) bytes.
+ */
+size_t sophia_mla_decode_workspace_size(int64_t rows, int rank, int splits);
+int sophia_mla_decode_attn(const void *qa, int64_t qa_stride, int qa_dtype, const float *latent, int64_t slot_stride,
+                           int n_slots, int max_seq, const int32_t *slots, const int64_t *pos, float scale, void *out,
+                           int64_t out_stride, int out_dtype, int64_t rows, int heads, int rank, int splits,
+                           void *workspace, size_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

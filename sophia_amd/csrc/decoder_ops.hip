@@ -339,6 +339,234 @@ __global__ __launch_bounds__(256) void gated_head_norm_kernel(GateArgs a) {
          8 * c, a.dtype, o);
 }
 
+// ---------------------------------------------------------------------------
+// Absorbed MLA decode attention over fp32 latent caches.
+//
+// One work-group (4 wavefronts) per (decode row, key split).  A wavefront takes
+// 16-key tiles of its range in turn and, per tile, on bf16 MFMAs:
+//   S^T[16 keys x 16 heads] = lat[16 x R] . qa^T          (R / 32 MFMAs, K = rank)
+//   lat^T blocks for the value sum: D = lat . I_sel        (one MFMA per 16 ranks)
+//   ctx[16 heads x 16 ranks] += P[16 x 16 keys] . lat      (16x16x16 MFMAs, K = keys)
+// The accumulator layout of S^T (lane: head = lane % 16, keys 4 (lane / 16) + i)
+// is exactly the A-operand layout of P for the 16x16x16 product, and the
+// accumulator layout of lat . I_sel (lane: rank column, keys 4 (lane / 16) + i) is
+// its B operand, so no value passes through LDS inside the loop.  Softmax is
+// online (running max and sum per head); the four wavefronts merge through LDS
+// at the end, and key splits, when there are several, in a second kernel.
+struct MlaArgs {
+  const void *qa;        // [rows, heads, R]
+  int64_t qa_stride;     // elements between rows
+  int qa_dtype;
+  const float *latent;   // [slots, max_seq, R] fp32
+  int64_t slot_stride;   // elements between slots
+  int max_seq;
+  int n_slots;
+  const int32_t *slots;  // [rows]
+  const int64_t *pos;    // [rows]: keys 0..pos are attended
+  float scale;
+  void *out;             // [rows, heads, R]
+  int64_t out_stride;
+  int out_dtype;
+  float *part;           // [rows, splits, 16, R + 2] when splits > 1
+  int heads;
+  int splits;
+};
+
+__device__ __forceinline__ f4 mfma32(const bf8 &a, const bf8 &b, const f4 &c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f4 mfma16(const bf4 &a, const bf4 &b, const f4 &c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s4, a), __builtin_bit_cast(s4, b), c, 0, 0,
+                                                    0);
+}
+
+// Keys of a row: 0 for an out-of-range slot (its output is then zero).
+__device__ __forceinline__ int mla_keys(const MlaArgs &a, int row, int64_t &slot) {
+  slot = a.slots[row];
+  if (slot < 0 || slot >= a.n_slots) return 0;
+  const int64_t p = a.pos[row];
+  return static_cast<int>(p < 0 ? 0 : (p + 1 > a.max_seq ? a.max_seq : p + 1));
+}
+
+template <int R>
+__global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
+  constexpr int KS = R / 32, NT = R / 16;
+  __shared__ float s_acc[4][16][R];
+  __shared__ float s_ml[4][2][16];
+  const int row = blockIdx.x, split = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ln = lane & 15, g = lane >> 4;
+  int64_t slot;
+  const int n = mla_keys(a, row, slot);
+  const int tiles = (n + 15) >> 4;
+  const int per = (tiles + a.splits - 1) / a.splits;
+  const int t0 = split * per, t1 = min(tiles, t0 + per);
+  const float *lat = a.latent + slot * a.slot_stride;
+
+  // qa^T as B operands (lane: head ln, ranks 32 ks + 8 g + j); heads >= a.heads are zero.
+  bf8 qb[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (ln < a.heads)
+      load8(static_cast<const uint8_t *>(a.qa) +
+                (static_cast<int64_t>(row) * a.qa_stride + static_cast<int64_t>(ln) * R) *
+                    (a.qa_dtype == SOPHIA_DTYPE_BF16 ? 2 : 4),
+            32 * ks + 8 * g, a.qa_dtype, v);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qb[ks][j] = static_cast<__bf16>(v[j]);
+  }
+  // Selection operands: I_h picks ranks 16 h + n of a 32-rank block.
+  bf8 sel[2];
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      sel[hf][j] = static_cast<__bf16>((8 * g + j == 16 * hf + ln) ? 1.0f : 0.0f);
+
+  f4 acc[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) acc[nt] = f4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  f4 raw[2][KS][2];
+  auto load_tile = [&](int t, f4 (&dst)[KS][2]) {
+    const int key = min(16 * t + ln, n - 1);  // rows past the end are read in bounds and masked
+    const float *rp = lat + static_cast<int64_t>(key) * R + 8 * g;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      dst[ks][0] = *reinterpret_cast<const f4 *>(rp + 32 * ks);
+      dst[ks][1] = *reinterpret_cast<const f4 *>(rp + 32 * ks + 4);
+    }
+  };
+  int t = t0 + wave;
+  if (t < t1) load_tile(t, raw[0]);
+  for (; t < t1; t += 4) {
+    if (t + 4 < t1) load_tile(t + 4, raw[1]);
+    bf8 af[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        af[ks][j] = static_cast<__bf16>(raw[0][ks][0][j]);
+        af[ks][4 + j] = static_cast<__bf16>(raw[0][ks][1][j]);
+      }
+    f4 st = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) st = mfma32(af[ks], qb[ks], st);
+    // st[i] = score of key 16 t + 4 g + i for head ln.
+    float p[4], mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[i] = (16 * t + 4 * g + i < n) ? st[i] * a.scale : -INFINITY;
+      mx = fmaxf(mx, p[i]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);  // finite: every tile holds a key < n
+    const float alpha = __expf(m_run - m_new);
+    float ps = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[i] = __expf(p[i] - m_new);
+      ps += p[i];
+    }
+    ps += __shfl_xor(ps, 16, 64);
+    ps += __shfl_xor(ps, 32, 64);
+    l_run = l_run * alpha + ps;
+    m_run = m_new;
+    // ctx rows of this lane are heads 4 g + i: their factors live in lanes 4 g + i.
+    float al[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * g + i, 64);
+    const bf4 pa = bf4{static_cast<__bf16>(p[0]), static_cast<__bf16>(p[1]), static_cast<__bf16>(p[2]),
+                       static_cast<__bf16>(p[3])};
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const f4 tr = mfma32(af[nt >> 1], sel[nt & 1], f4{0.f, 0.f, 0.f, 0.f});
+      const bf4 lb = bf4{static_cast<__bf16>(tr[0]), static_cast<__bf16>(tr[1]), static_cast<__bf16>(tr[2]),
+                         static_cast<__bf16>(tr[3])};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[nt][i] *= al[i];
+      acc[nt] = mfma16(pa, lb, acc[nt]);
+    }
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      raw[0][ks][0] = raw[1][ks][0];
+      raw[0][ks][1] = raw[1][ks][1];
+    }
+  }
+  // Merge the four wavefronts: acc[nt][i] is ctx[head 4 g + i][rank 16 nt + ln].
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s_acc[wave][4 * g + i][16 * nt + ln] = acc[nt][i];
+  if (g == 0) {
+    s_ml[wave][0][ln] = m_run;
+    s_ml[wave][1][ln] = l_run;
+  }
+  __syncthreads();
+  const int heads = a.splits > 1 ? 16 : a.heads;
+  for (int idx = tid; idx < heads * R; idx += 256) {
+    const int h = idx / R, r = idx - h * R;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, s_ml[w][0][h]);
+    float num = 0.f, den = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float e = __expf(s_ml[w][0][h] - M);
+        num = fmaf(e, s_acc[w][h][r], num);
+        den = fmaf(e, s_ml[w][1][h], den);
+      }
+    }
+    if (a.splits > 1) {
+      float *pp = a.part + ((static_cast<int64_t>(row) * a.splits + split) * 16 + h) * (R + 2);
+      pp[r] = num;
+      if (r == 0) {
+        pp[R] = M;
+        pp[R + 1] = den;
+      }
+    } else {
+      const float y = den > 0.f ? num / den : 0.f;
+      const int64_t o = static_cast<int64_t>(row) * a.out_stride + static_cast<int64_t>(h) * R + r;
+      if (a.out_dtype == SOPHIA_DTYPE_BF16)
+        static_cast<uint16_t *>(a.out)[o] = f32_to_bf16_bits(y);
+      else
+        static_cast<float *>(a.out)[o] = y;
+    }
+  }
+}
+
+// Merge of the key splits of one row: ctx = sum_s e^{m_s - M} acc_s / sum_s e^{m_s - M} l_s.
+template <int R>
+__global__ __launch_bounds__(256) void mla_decode_merge_kernel(MlaArgs a) {
+  const int row = blockIdx.x;
+  for (int idx = threadIdx.x; idx < a.heads * R; idx += 256) {
+    const int h = idx / R, r = idx - h * R;
+    const float *pp = a.part + (static_cast<int64_t>(row) * a.splits * 16 + h) * (R + 2);
+    const int64_t step = 16 * static_cast<int64_t>(R + 2);
+    float M = -INFINITY;
+    for (int s = 0; s < a.splits; ++s) M = fmaxf(M, pp[s * step + R]);
+    float num = 0.f, den = 0.f;
+    if (M != -INFINITY) {
+      for (int s = 0; s < a.splits; ++s) {
+        const float e = __expf(pp[s * step + R] - M);
+        num = fmaf(e, pp[s * step + r], num);
+        den = fmaf(e, pp[s * step + R + 1], den);
+      }
+    }
+    const float y = den > 0.f ? num / den : 0.f;
+    const int64_t o = static_cast<int64_t>(row) * a.out_stride + static_cast<int64_t>(h) * R + r;
+    if (a.out_dtype == SOPHIA_DTYPE_BF16)
+      static_cast<uint16_t *>(a.out)[o] = f32_to_bf16_bits(y);
+    else
+      static_cast<float *>(a.out)[o] = y;
+  }
+}
+
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 }  // namespace
@@ -446,4 +674,49 @@ extern "C" int sophia_gated_head_norm(const void *o, int64_t o_stride, int o_dty
   hipLaunchKernelGGL(gated_head_norm_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), a);
   return check_launch("gated_head_norm");
+}
+
+extern "C" size_t sophia_mla_decode_workspace_size(int64_t rows, int rank, int splits) {
+  if (rows < 0 || rank <= 0 || splits < 1) return 0;
+  return splits > 1 ? static_cast<size_t>(rows) * splits * 16 * (rank + 2) * sizeof(float) : 0;
+}
+
+extern "C" int sophia_mla_decode_attn(const void *qa, int64_t qa_stride, int qa_dtype, const float *latent,
+                                      int64_t slot_stride, int n_slots, int max_seq, const int32_t *slots,
+                                      const int64_t *pos, float scale, void *out, int64_t out_stride,
+                                      int out_dtype, int64_t rows, int heads, int rank, int splits,
+                                      void *workspace, size_t workspace_bytes, void *stream) {
+  SOPHIA_REQUIRE((qa_dtype == SOPHIA_DTYPE_F32 || qa_dtype == SOPHIA_DTYPE_BF16) &&
+                     (out_dtype == SOPHIA_DTYPE_F32 || out_dtype == SOPHIA_DTYPE_BF16),
+                 "mla_decode_attn: dtype not supported");
+  SOPHIA_REQUIRE(rank == 32 || rank == 64 || rank == 128 || rank == 256,
+                 "mla_decode_attn: rank %d not supported (32, 64, 128 or 256)", rank);
+  SOPHIA_REQUIRE(heads >= 1 && heads <= 16, "mla_decode_attn: heads must be in [1, 16]");
+  SOPHIA_REQUIRE(rows >= 0 && rows <= 0x7fffffff && splits >= 1 && splits <= 65535,
+                 "mla_decode_attn: bad rows / splits");
+  SOPHIA_REQUIRE(n_slots >= 0 && max_seq >= 0 && slot_stride >= static_cast<int64_t>(max_seq) * rank,
+                 "mla_decode_attn: slot stride smaller than a slot");
+  SOPHIA_REQUIRE(qa_stride >= static_cast<int64_t>(heads) * rank && out_stride >= static_cast<int64_t>(heads) * rank &&
+                     qa_stride % 8 == 0 && slot_stride % 8 == 0,
+                 "mla_decode_attn: bad strides");
+  SOPHIA_REQUIRE(rows == 0 || (qa && latent && slots && pos && out), "mla_decode_attn: NULL pointer");
+  SOPHIA_REQUIRE(aligned16(qa) && aligned16(latent), "mla_decode_attn: qa and latent must be 16-byte aligned");
+  SOPHIA_REQUIRE(splits == 1 || (workspace && workspace_bytes >= sophia_mla_decode_workspace_size(rows, rank, splits)),
+                 "mla_decode_attn: workspace too small");
+  if (rows == 0) return SOPHIA_OK;
+  MlaArgs a{qa, qa_stride, qa_dtype, latent, slot_stride, max_seq, n_slots, slots, pos, scale,
+            out, out_stride, out_dtype, static_cast<float *>(workspace), heads, splits};
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>(rows), static_cast<unsigned>(splits));
+  switch (rank) {
+#define SOPHIA_MLA_CASE(r)                                                                         \
+  case r:                                                                                          \
+    hipLaunchKernelGGL(mla_decode_kernel<r>, grid, dim3(256), 0, st, a);                           \
+    if (splits > 1) hipLaunchKernelGGL(mla_decode_merge_kernel<r>, dim3(static_cast<unsigned>(rows)), \
+                                       dim3(256), 0, st, a);                                       \
+    break;
+    SOPHIA_MLA_CASE(32) SOPHIA_MLA_CASE(64) SOPHIA_MLA_CASE(128) SOPHIA_MLA_CASE(256)
+#undef SOPHIA_MLA_CASE
+  }
+  return check_launch("mla_decode_attn");
 }

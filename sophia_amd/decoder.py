@@ -172,7 +172,10 @@ class SophiaMLA(nn.Module):
         (W_k,h^T q) . c, so scores and the value sum are taken directly over
         the cached latents c and W_v,h is applied after the sum -- the same
         result as expanding K and V, without recomputing them every step.
-        ``max_decode_len`` (host int) bounds pos + 1 for every decode row.
+        The softmax over the cached latents and their weighted sum run as one
+        HIP kernel (``ops.mla_decode_attn``) that reads the fp32 cache in
+        place.  ``max_decode_len`` (host int) bounds pos + 1 for every decode
+        row; it sizes the kernel's key splits.
         """
         n = int(x.size(0))
         npre = int(n_prefill_seqs) * int(prefill_len)
@@ -194,17 +197,12 @@ class SophiaMLA(nn.Module):
         if nd > 0:
             slots = decode_slots.long()
             cache[slots, decode_pos] = latent[npre:].to(cache.dtype)
-            L = int(max_decode_len)
-            lat = cache[slots, :L].to(x.dtype)                                   # [D, L, r]
             w_k = self.k_up.weight.view(h, d, r).to(x.dtype)
             w_v = self.v_up.weight.view(h, d, r).to(x.dtype)
             qa = torch.bmm(q[npre:].transpose(0, 1).contiguous(), w_k).transpose(0, 1)   # [D, h, r]
-            scores = torch.bmm(qa.contiguous(), lat.transpose(1, 2).contiguous()).float()
-            scores = scores * (d ** -0.5)
-            valid = torch.arange(L, device=x.device)[None, :] <= decode_pos[:, None]
-            scores = scores.masked_fill(~valid[:, None, :], float("-inf"))
-            prob = scores.softmax(dim=-1).to(x.dtype)
-            ctx = torch.bmm(prob, lat)                                                 # [D, h, r]
+            # softmax over cached latents 0..pos and their weighted sum, one kernel
+            ctx = ops.mla_decode_attn(qa.contiguous(), cache, decode_slots, decode_pos,
+                                      d ** -0.5, max_len=int(max_decode_len))            # [D, h, r]
             o = torch.bmm(ctx.transpose(0, 1).contiguous(), w_v.transpose(1, 2).contiguous())
             out[npre:] = o.transpose(0, 1)
         return self._gate_out(x, out)

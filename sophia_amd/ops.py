@@ -514,3 +514,57 @@ def gated_head_norm(o: torch.Tensor, gate: torch.Tensor, heads: int, head_dim: i
         nat.stream_handle(gate.device))
     nat.check(rc, "sophia_gated_head_norm")
     return y2
+
+
+def mla_decode_attn(qa: torch.Tensor, latent_cache: torch.Tensor, slots: torch.Tensor,
+                    pos: torch.Tensor, scale: float, *, max_len: int | None = None,
+                    splits: int | None = None, out_dtype: torch.dtype | None = None,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """Absorbed MLA decode attention in latent space (the decode rows of
+    SophiaMLA, ml/runtime/model/attention.py:609-657, with k = W_k c and
+    v = W_v c folded out): for row b and head h,
+    softmax_k(scale * qa[b, h] . latent[slots[b], k]) over k = 0..pos[b], then
+    the probability-weighted sum of those latents.
+
+    qa: [rows, heads, rank] (bf16 or fp32, heads <= 16, rank in 32/64/128/256);
+    latent_cache: [n_slots, max_seq, rank] fp32 with dense rows; slots int32
+    [rows]; pos int64 [rows].  ``max_len`` (host int, an upper bound on
+    pos + 1) sizes the key splits; ``splits`` overrides them.  Returns
+    [rows, heads, rank] in ``out_dtype`` (default qa.dtype)."""
+    _gpu(qa, "qa")
+    _gpu(latent_cache, "latent_cache")
+    if qa.dim() != 3:
+        raise RuntimeError(f"qa must be [rows, heads, rank], got {tuple(qa.shape)}")
+    rows, heads, rank = (int(v) for v in qa.shape)
+    if (latent_cache.dim() != 3 or latent_cache.dtype != torch.float32
+            or int(latent_cache.size(2)) != rank or latent_cache.stride(2) != 1
+            or latent_cache.stride(1) != rank):
+        raise RuntimeError(f"latent_cache must be fp32 [slots, max_seq, {rank}] with dense rows")
+    if qa.stride(2) != 1 or (heads > 1 and qa.stride(1) != rank):
+        qa = qa.contiguous()
+    qs = int(qa.stride(0)) if rows > 1 else heads * rank
+    sl = _int32(slots, "slots", qa.device)
+    if pos.dtype != torch.int64 or pos.device != qa.device or not pos.is_contiguous():
+        raise RuntimeError("pos must be a contiguous int64 tensor on the device")
+    if int(sl.numel()) != rows or int(pos.numel()) != rows:
+        raise RuntimeError("slots and pos must hold one entry per row")
+    n_slots, max_seq = int(latent_cache.size(0)), int(latent_cache.size(1))
+    if splits is None:
+        bound = max_seq if max_len is None else min(int(max_len), max_seq)
+        splits = max(1, min(-(-512 // max(rows, 1)), -(-bound // 128)))
+    dt = qa.dtype if out_dtype is None else out_dtype
+    if out is not None and (not out.is_contiguous() or out.dtype != dt
+                            or tuple(out.shape) != (rows, heads, rank)):
+        raise RuntimeError(f"out must be contiguous {dt} [{rows}, {heads}, {rank}]")
+    y = out if out is not None else torch.empty((rows, heads, rank), dtype=dt, device=qa.device)
+    ws_bytes = int(nat.lib().sophia_mla_decode_workspace_size(rows, rank, int(splits)))
+    ws = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=qa.device) if ws_bytes else None
+    _aligned(qa, "qa")
+    _aligned(latent_cache, "latent_cache")
+    rc = nat.lib().sophia_mla_decode_attn(
+        nat.ptr(qa), qs, nat.dtype_code(qa.dtype), nat.ptr(latent_cache),
+        int(latent_cache.stride(0)) if n_slots > 1 else max_seq * rank, n_slots, max_seq,
+        nat.ptr(sl), nat.ptr(pos), float(scale), nat.ptr(y), heads * rank, nat.dtype_code(dt), rows,
+        heads, rank, int(splits), nat.ptr(ws), ws_bytes, nat.stream_handle(qa.device))
+    nat.check(rc, "sophia_mla_decode_attn")
+    return y

@@ -41,7 +41,8 @@ def test_header_declares_the_entry_points():
     for name in ("sophia_short_conv_fwd", "sophia_short_conv_step", "sophia_kda_chunk_fwd",
                  "sophia_kda_chunk_workspace_size", "sophia_kda_decode_step",
                  "sophia_last_error", "sophia_abi_version", "sophia_attn_res_mix",
-                 "sophia_situ_glu", "sophia_gated_head_norm"):
+                 "sophia_situ_glu", "sophia_gated_head_norm", "sophia_mla_decode_attn",
+                 "sophia_mla_decode_workspace_size"):
         assert name in decls, name
 
 
@@ -111,6 +112,18 @@ def test_host_side_queries_and_validation():
     assert rc == nat.SOPHIA_ERR_INVALID and "stride" in nat.last_error()
     rc = lib.sophia_gated_head_norm(16, 2048, 1, 32, 2048, None, 1e-5, 48, 2048, 4, 16, 128, 0, None)
     assert rc == nat.SOPHIA_ERR_INVALID and "dtype" in nat.last_error()
+    # MLA decode: rank 96 and 17 heads are rejected; splits need a workspace.
+    assert lib.sophia_mla_decode_workspace_size(240, 128, 1) == 0
+    assert lib.sophia_mla_decode_workspace_size(240, 128, 3) == 240 * 3 * 16 * 130 * 4
+    rc = lib.sophia_mla_decode_attn(16, 2048, 1, 32, 2048 * 96, 8, 2048, 48, 64, 0.1, 80, 2048, 1, 4,
+                                    16, 96, 1, None, 0, None)
+    assert rc == nat.SOPHIA_ERR_INVALID and "rank" in nat.last_error()
+    rc = lib.sophia_mla_decode_attn(16, 4096, 1, 32, 2048 * 128, 8, 2048, 48, 64, 0.1, 80, 4096, 1,
+                                    4, 17, 128, 1, None, 0, None)
+    assert rc == nat.SOPHIA_ERR_INVALID and "heads" in nat.last_error()
+    rc = lib.sophia_mla_decode_attn(16, 2048, 1, 32, 2048 * 128, 8, 2048, 48, 64, 0.1, 80, 2048, 1, 4,
+                                    16, 128, 3, None, 0, None)
+    assert rc == nat.SOPHIA_ERR_INVALID and "workspace" in nat.last_error()
 
 
 def test_ops_reject_cpu_tensors():
@@ -131,3 +144,6 @@ def test_ops_reject_cpu_tensors():
         ops.situ_glu(torch.zeros(4, 64), 4.0, 25.0)
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         ops.gated_head_norm(torch.zeros(4, 256), torch.zeros(4, 256), 2, 128)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.mla_decode_attn(torch.zeros(4, 2, 32), torch.zeros(4, 8, 32),
+                            torch.zeros(4, dtype=torch.int32), torch.zeros(4, dtype=torch.int64), 0.1)

@@ -229,3 +229,60 @@ def test_gated_head_norm_rejects_misaligned_and_bad_shapes():
         ops.gated_head_norm(o, fused[:, 2:2 + 256], 2, 128)
     with pytest.raises(RuntimeError, match="head_dim"):
         ops.gated_head_norm(torch.zeros(4, 2 * 96, device=dev), torch.zeros(4, 2 * 96, device=dev), 2, 96)
+
+
+def _mla_ref(qa, cache, slots, pos, scale):
+    """Latent-space decode attention (the decode rows of attention.py:609-657
+    with W_k / W_v folded out) in float64 from bf16-rounded qa and latents,
+    as the reference casts both to the activation dtype."""
+    qa = qa.to(torch.bfloat16).double().cpu()
+    lat = cache.to(torch.bfloat16).double().cpu()
+    rows, heads, rank = qa.shape
+    out = torch.zeros(rows, heads, rank, dtype=torch.float64)
+    for b in range(rows):
+        s = int(slots[b])
+        if not 0 <= s < cache.size(0):
+            continue
+        n = min(int(pos[b]) + 1, cache.size(1))
+        if n <= 0:
+            continue
+        keys = lat[s, :n]                                   # [n, rank]
+        p = torch.softmax(scale * qa[b] @ keys.t(), dim=-1)  # [heads, n]
+        out[b] = p @ keys
+    return out
+
+
+@pytest.mark.parametrize("rank,heads,rows,splits", [(32, 2, 5, 1), (64, 3, 9, 2), (128, 16, 240, None),
+                                                    (128, 16, 3, 7), (256, 16, 17, 3), (128, 1, 1, 1)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_mla_decode_attn_matches_fp64_reference(rank, heads, rows, splits, dtype):
+    """Positions from a single key to the whole cache (including lengths that
+    end mid-tile), permuted slots, more splits than tiles, a slot outside the
+    cache (zeros), against the float64 latent-space reference.  Tolerance: the
+    probabilities are rounded to bf16 before the value sum (as the reference
+    rounds them to the activation dtype), so max|y - ref| <= 1e-2 max|ref|."""
+    from sophia_amd import ops
+    dev = _dev()
+    g = torch.Generator(device="cpu").manual_seed(rank + heads * 7 + rows)
+    n_slots, max_seq = rows + 3, 300
+    cache = torch.randn(n_slots, max_seq, rank, generator=g).to(dev)
+    qa = (torch.randn(rows, heads, rank, generator=g) * 0.3).to(dev, dtype)
+    slots = torch.randperm(n_slots, generator=g)[:rows].to(torch.int32)
+    pos = torch.randint(0, max_seq, (rows,), generator=g)
+    pos[0] = 0
+    if rows > 2:
+        pos[1] = max_seq - 1
+        pos[2] = 16 * 5 + 6
+    if rows > 4:
+        slots[3] = -1       # not a cache slot: zero output
+        pos[4] = max_seq + 40  # clamped to the cache length
+    scale = 128 ** -0.5
+    y = ops.mla_decode_attn(qa, cache, slots.to(dev), pos.to(dev), scale, max_len=max_seq,
+                            splits=splits)
+    torch.cuda.synchronize()
+    assert y.shape == (rows, heads, rank) and y.dtype == dtype
+    ref = _mla_ref(qa, cache, slots, pos, scale)
+    err = float((y.double().cpu() - ref).abs().max()) / float(ref.abs().max())
+    assert err <= 1e-2, err
+    if rows > 4:
+        assert float(y[3].abs().max()) == 0.0
