@@ -122,7 +122,7 @@ def copy_bandwidth(torch, dev, stream, nbytes: int = 1 << 30) -> float:
 
 
 def mixed_step_bench(torch, dev, stream, steps: int, warmup: int, seed: int = 4,
-                     tune_gemms: str | None = None) -> dict:
+                     tune_gemms: str | None = None, gemms: str = "both") -> dict:
     """The whole hybrid decoder (28 layers [KDA, KDA, KDA, MLA] x 7, dim 1536,
     16 heads x 128, SiTU-GLU 3968, MLA ranks 384 / 128, vocab 65,536, tied;
     random init, bf16 GEMM weights, fp32 caches) in one continuous-batching
@@ -134,8 +134,9 @@ def mixed_step_bench(torch, dev, stream, steps: int, warmup: int, seed: int = 4,
     with hipBLASLt's default per-shape heuristics, then with the per-shape
     selection of sophia_amd/gemm_tuning_gfx950.csv (torch TunableOp, no timing
     runs) when that file matches this software stack; the step figures are
-    those of the faster of the two, and both are reported.  With
-    ``tune_gemms``, the selection is timed here and written to that file."""
+    those of the faster of the two, and both are reported (``gemms``:
+    "default" or "tuned" runs one of them only).  With ``tune_gemms``, the
+    selection is timed here and written to that file."""
     from sophia_amd.config import ModelArgs
     from sophia_amd.decoder import MixedStepGraph, Transformer
     from sophia_amd.kda import RuntimeLinear
@@ -173,14 +174,18 @@ def mixed_step_bench(torch, dev, stream, steps: int, warmup: int, seed: int = 4,
         del graph
         return float(np.mean(gper)), float(np.mean(eper))
 
-    gemm_runs = {"default": measure()}
+    gemm_runs = {}
+    if gemms in ("both", "default") and not tune_gemms:
+        gemm_runs["default"] = measure()
     if tune_gemms:
         gemm_tuning.use_tuned_gemms(tune_gemms, tune=True)
         eager()  # times every GEMM shape of the step once
         gemm_runs["tuned"] = measure()
-    elif gemm_tuning.use_tuned_gemms():
+    elif gemms in ("both", "tuned") and gemm_tuning.use_tuned_gemms():
         gemm_runs["tuned"] = measure()
     gemm_tuning.use_default_gemms()
+    if not gemm_runs:
+        gemm_runs["default"] = measure()
     selection = min(gemm_runs, key=lambda k: gemm_runs[k][0])
     gms, ems = gemm_runs[selection]
     tokens = P * T + D
@@ -225,6 +230,8 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--mixed-gemms", choices=["both", "default", "tuned"], default="both",
+                    help="library GEMM selection(s) timed in the mixed step")
     ap.add_argument("--tune-gemms", metavar="CSV", default=None,
                     help="time the mixed step's library GEMM candidates and write the "
                          "per-shape selection to CSV (torch TunableOp)")
@@ -364,7 +371,7 @@ def main(argv=None) -> int:
     if args.only in ("all", "mixed"):
         result["mixed_step"] = mixed_step_bench(torch, dev, stream, max(args.steps // 2, 5),
                                                 max(args.warmup // 2, 2),
-                                                tune_gemms=args.tune_gemms)
+                                                tune_gemms=args.tune_gemms, gemms=args.mixed_gemms)
     if args.only == "all":
         result["hbm_copy_GBps"] = round(copy_bandwidth(torch, dev, stream), 1)
     if not args.no_cpu and args.only == "all":
