@@ -69,6 +69,12 @@ __device__ __forceinline__ void store8(void *base, int64_t idx, int dtype, const
   }
 }
 
+__device__ __forceinline__ bf8 bits_to_bf8(u4 w) { return __builtin_bit_cast(bf8, w); }
+
+__device__ __forceinline__ u2 pack4_bf16(f4 v) {
+  return u2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+}
+
 struct MixArgs {
   const void *partial;
   int64_t partial_stride;
@@ -567,6 +573,183 @@ __global__ __launch_bounds__(256) void mla_decode_merge_kernel(MlaArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Causal attention over packed sequences (the MLA prefill rows, head_dim 128).
+//
+// One work-group (4 wavefronts) per (128-query block, head, sequence); a
+// wavefront owns 32 queries.  Per 64-key block, K (row-major) and V (transposed,
+// keys along rows) are staged in LDS by the four wavefronts, then each
+// wavefront forms
+//   S^T[keys x queries] = K . Q^T            (A = K rows from LDS, B = Q^T in registers)
+//   O^T[d x queries]   += V^T . P^T          (A = V^T from LDS, B = P^T from the S^T tiles)
+// with v_mfma_f32_16x16x32_bf16.  The S^T accumulators of two 16-key tiles pair
+// into the B operand of the second product (k order 4g..4g+3, 16+4g..16+4g+3,
+// matched by the V^T reads), and O^T puts 4 consecutive head dims of one query
+// in a lane, so the softmax state is per lane and the stores are 8 bytes.  V is
+// transposed on its way into LDS by products with a 0/1 selection matrix.
+constexpr int kFaD = 128;          // head dim
+constexpr int kFaQ = 128;          // queries per work-group
+constexpr int kFaK = 64;           // keys per block
+constexpr int kFaLdK = kFaD + 8;   // bf16 row stride of the K tile
+constexpr int kFaLdV = kFaK + 8;   // bf16 row stride of the V^T tile
+
+struct FaArgs {
+  const uint16_t *q, *k, *v;       // bf16 rows: token t, head h at t * stride + h * 128
+  int64_t q_stride, k_stride, v_stride;
+  uint16_t *out;
+  int64_t out_stride;
+  const int32_t *cu;
+  int n_seqs;
+  int64_t total;
+  int q_blocks;                    // grid.x
+  float scale_log2;                // softmax scale * log2(e)
+};
+
+__global__ __launch_bounds__(256, 2) void causal_attn_kernel(FaArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t sK[kFaK * kFaLdK];
+  __shared__ __attribute__((aligned(16))) uint16_t sVt[kFaD * kFaLdV];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int ln = lane & 15, g = lane >> 4;
+  const int h = blockIdx.y, sq = blockIdx.z;
+  const int64_t start = iclamp64(a.cu[sq], 0, a.total);
+  const int len = static_cast<int>(iclamp64(a.cu[sq + 1], start, a.total) - start);
+  const int q0 = (a.q_blocks - 1 - static_cast<int>(blockIdx.x)) * kFaQ;  // heavy blocks first
+  if (q0 >= len) return;
+  const int kend = min(len, q0 + kFaQ);           // keys needed by this work-group
+  const int nkb = (kend + kFaK - 1) / kFaK;
+  const int wq0 = q0 + 32 * w;                    // first query of this wavefront
+  const int wq_last = min(wq0 + 31, len - 1);     // last query it stores
+
+  // Q^T as B operands: lane (query ln of tile qt, g) holds dims 32 ks + 8 g .. +7.
+  bf8 qf[2][4];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int qi = min(wq0 + 16 * qt + ln, len - 1);
+    const uint16_t *qp = a.q + (start + qi) * a.q_stride + static_cast<int64_t>(h) * kFaD + 8 * g;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qf[qt][ks] = bits_to_bf8(*reinterpret_cast<const u4 *>(qp + 32 * ks));
+  }
+  bf8 sel[2];
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sel[hf][j] = static_cast<__bf16>((8 * g + j == 16 * hf + ln) ? 1.0f : 0.0f);
+
+  f4 ot[2][8];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) ot[qt][dt] = f4{0.f, 0.f, 0.f, 0.f};
+  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+
+  // This lane's K / V rows of a block: key 16 w + ln, dims 32 ks + 8 g .. +7.
+  u4 kr[4], vr[4];
+  auto load_block = [&](int kb) {
+    const int key = min(kb * kFaK + 16 * w + ln, len - 1);
+    const uint16_t *kp = a.k + (start + key) * a.k_stride + static_cast<int64_t>(h) * kFaD + 8 * g;
+    const uint16_t *vp = a.v + (start + key) * a.v_stride + static_cast<int64_t>(h) * kFaD + 8 * g;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      kr[ks] = *reinterpret_cast<const u4 *>(kp + 32 * ks);
+      vr[ks] = *reinterpret_cast<const u4 *>(vp + 32 * ks);
+    }
+  };
+  load_block(0);
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int k0 = kb * kFaK;
+    __syncthreads();  // the previous block's LDS reads are done
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      *reinterpret_cast<u4 *>(&sK[(16 * w + ln) * kFaLdK + 32 * ks + 8 * g]) = kr[ks];
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const f4 tr = mfma32(bits_to_bf8(vr[ks]), sel[hf], f4{0.f, 0.f, 0.f, 0.f});
+        // tr[i] = V[key 16 w + 4 g + i][dim 32 ks + 16 hf + ln]
+        *reinterpret_cast<u2 *>(&sVt[(32 * ks + 16 * hf + ln) * kFaLdV + 16 * w + 4 * g]) = pack4_bf16(tr);
+      }
+    }
+    __syncthreads();
+    if (kb + 1 < nkb) load_block(kb + 1);
+    if (k0 > wq_last) continue;  // every key of the block is after this wavefront's queries
+    // S^T tiles: st[kt][qt][i] = score(key k0 + 16 kt + 4 g + i, query wq0 + 16 qt + ln).
+    f4 st[4][2];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      st[kt][0] = st[kt][1] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const bf8 kf = bits_to_bf8(*reinterpret_cast<const u4 *>(&sK[(16 * kt + ln) * kFaLdK + 32 * ks + 8 * g]));
+        st[kt][0] = mfma32(kf, qf[0][ks], st[kt][0]);
+        st[kt][1] = mfma32(kf, qf[1][ks], st[kt][1]);
+      }
+    }
+    bf8 pf[2][2];  // [kp][qt]: P^T as B operands of the value product
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      const int qi = wq0 + 16 * qt + ln;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = k0 + 16 * kt + 4 * g + i;
+          const float sv = (key <= qi && key < len) ? st[kt][qt][i] * a.scale_log2 : -INFINITY;
+          st[kt][qt][i] = sv;
+          mx = fmaxf(mx, sv);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m_run[qt], mx);
+      // m_new is finite once key 0 has been seen, and key 0 is in the first block.
+      const float alpha = __builtin_amdgcn_exp2f(m_run[qt] - m_new);
+      float ps = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float pv = __builtin_amdgcn_exp2f(st[kt][qt][i] - m_new);
+          st[kt][qt][i] = pv;
+          ps += pv;
+        }
+      ps += __shfl_xor(ps, 16, 64);
+      ps += __shfl_xor(ps, 32, 64);
+      l_run[qt] = l_run[qt] * alpha + ps;
+      m_run[qt] = m_new;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) ot[qt][dt] *= alpha;
+#pragma unroll
+      for (int kp = 0; kp < 2; ++kp)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pf[kp][qt][i] = static_cast<__bf16>(st[2 * kp][qt][i]);
+          pf[kp][qt][4 + i] = static_cast<__bf16>(st[2 * kp + 1][qt][i]);
+        }
+    }
+    // O^T += V^T P^T: A = V^T rows dims 16 dt + ln, keys 32 kp + {4g..4g+3, 16+4g..16+4g+3}.
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int kp = 0; kp < 2; ++kp) {
+        const uint16_t *vrow = &sVt[(16 * dt + ln) * kFaLdV + 32 * kp + 4 * g];
+        const u2 lo = *reinterpret_cast<const u2 *>(vrow);
+        const u2 hi = *reinterpret_cast<const u2 *>(vrow + 16);
+        const bf8 vf = bits_to_bf8(u4{lo.x, lo.y, hi.x, hi.y});
+        ot[0][dt] = mfma32(vf, pf[kp][0], ot[0][dt]);
+        ot[1][dt] = mfma32(vf, pf[kp][1], ot[1][dt]);
+      }
+  }
+  // ot[qt][dt][i] = O[query wq0 + 16 qt + ln][dim 16 dt + 4 g + i] before the 1 / l.
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int qi = wq0 + 16 * qt + ln;
+    if (qi >= len) continue;
+    const float rl = 1.0f / l_run[qt];
+    uint16_t *op = a.out + (start + qi) * a.out_stride + static_cast<int64_t>(h) * kFaD + 4 * g;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<u2 *>(op + 16 * dt) = pack4_bf16(ot[qt][dt] * rl);
+  }
+}
+
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 }  // namespace
@@ -719,4 +902,28 @@ extern "C" int sophia_mla_decode_attn(const void *qa, int64_t qa_stride, int qa_
 #undef SOPHIA_MLA_CASE
   }
   return check_launch("mla_decode_attn");
+}
+
+extern "C" int sophia_causal_attention(const void *q, int64_t q_stride, const void *k, int64_t k_stride,
+                                       const void *v, int64_t v_stride, void *out, int64_t out_stride,
+                                       const int32_t *cu_seqlens, int n_seqs, int64_t total, int max_len, int heads,
+                                       int head_dim, float scale, int dtype, void *stream) {
+  SOPHIA_REQUIRE(dtype == SOPHIA_DTYPE_BF16, "causal_attention: bf16 only");
+  SOPHIA_REQUIRE(head_dim == kFaD, "causal_attention: head_dim must be %d", kFaD);
+  SOPHIA_REQUIRE(heads >= 1 && heads <= 65535 && n_seqs >= 0 && n_seqs <= 65535 && total >= 0 && max_len >= 0,
+                 "causal_attention: bad heads / sequences");
+  const int64_t width = static_cast<int64_t>(heads) * head_dim;
+  SOPHIA_REQUIRE(q_stride >= width && k_stride >= width && v_stride >= width && out_stride >= width &&
+                     q_stride % 8 == 0 && k_stride % 8 == 0 && v_stride % 8 == 0 && out_stride % 4 == 0,
+                 "causal_attention: bad strides");
+  SOPHIA_REQUIRE(n_seqs == 0 || total == 0 || (q && k && v && out && cu_seqlens), "causal_attention: NULL pointer");
+  SOPHIA_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && (reinterpret_cast<uintptr_t>(out) & 7) == 0,
+                 "causal_attention: q, k, v must be 16-byte and out 8-byte aligned");
+  if (n_seqs == 0 || total == 0 || max_len == 0) return SOPHIA_OK;
+  FaArgs a{static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k), static_cast<const uint16_t *>(v),
+           q_stride, k_stride, v_stride, static_cast<uint16_t *>(out), out_stride, cu_seqlens, n_seqs, total,
+           (max_len + kFaQ - 1) / kFaQ, scale * 1.44269504088896341f};
+  hipLaunchKernelGGL(causal_attn_kernel, dim3(static_cast<unsigned>(a.q_blocks), heads, n_seqs), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return check_launch("causal_attention");
 }

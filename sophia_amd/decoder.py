@@ -112,6 +112,19 @@ class SophiaMLA(nn.Module):
         gated = ops.gated_head_norm(out.to(x.dtype), gate, self.num_heads, self.head_dim)
         return self.o_proj(gated.view(*x.shape[:-1], self.inner_dim))
 
+    def _causal(self, q, k, v, cu, max_len: int, out):
+        """Causal attention within each of the equal-length (``max_len``)
+        sequences packed in [rows, heads, 128] tensors, into ``out``: the HIP
+        kernel (``ops.causal_attention``) for bf16 activations, torch SDPA for
+        fp32 ones."""
+        if q.dtype == torch.bfloat16:
+            ops.causal_attention(q, k, v, cu, max_len, scale=self.head_dim ** -0.5, out=out)
+            return
+        n = int(q.size(0)) // max_len
+        o = F.scaled_dot_product_attention(*(t.reshape(n, max_len, self.num_heads, self.head_dim)
+                                             .transpose(1, 2) for t in (q, k, v)), is_causal=True)
+        out.copy_(o.transpose(1, 2).reshape_as(out))
+
     def forward(self, x: torch.Tensor, *, start_pos: int = 0) -> torch.Tensor:
         """attention.py:609-657 (pad-mask path: attention.py:585-600,635-654)."""
         bsz, seqlen, _ = x.shape
@@ -132,7 +145,13 @@ class SophiaMLA(nn.Module):
         q_t, k_t, v_t = (t.transpose(1, 2) for t in (q, k, v))
         key_pad = self._resolve_key_pad(int(start_pos), bsz, klen, x.device)
         if key_pad is None and int(start_pos) == 0 and seqlen == klen:
-            out = F.scaled_dot_product_attention(q_t, k_t, v_t, is_causal=True)
+            rows = bsz * seqlen
+            cu = torch.arange(0, rows + 1, seqlen, dtype=torch.int32, device=x.device)
+            out = torch.empty((rows, self.num_heads, self.head_dim), dtype=x.dtype, device=x.device)
+            self._causal(q.reshape(rows, self.num_heads, self.head_dim),
+                         k.reshape(rows, self.num_heads, self.head_dim),
+                         v.reshape(rows, self.num_heads, self.head_dim), cu, seqlen, out)
+            return self._gate_out(x, out.view(bsz, seqlen, self.num_heads, self.head_dim))
         else:
             allow = torch.ones((seqlen, klen), dtype=torch.bool, device=x.device).tril(klen - seqlen)
             allow = allow[None, None].expand(bsz, 1, seqlen, klen)
@@ -161,7 +180,8 @@ class SophiaMLA(nn.Module):
 
     def forward_mixed(self, x: torch.Tensor, n_prefill_seqs: int, prefill_len: int,
                       prefill_slots: torch.Tensor, decode_slots: torch.Tensor,
-                      decode_pos: torch.Tensor, max_decode_len: int) -> torch.Tensor:
+                      decode_pos: torch.Tensor, max_decode_len: int,
+                      cu_prefill: torch.Tensor | None = None) -> torch.Tensor:
         """Packed step: rows [0, P*Tp) are P new sequences of Tp tokens
         (causal attention over their own tokens, latents written to their
         slots at positions 0..Tp-1); the remaining D rows are one token each
@@ -189,11 +209,11 @@ class SophiaMLA(nn.Module):
             P, T = int(n_prefill_seqs), int(prefill_len)
             lat_p = latent[:npre].view(P, T, r)
             cache[prefill_slots.long(), :T] = lat_p.to(cache.dtype)
-            k = self.k_up(lat_p).view(P, T, h, d).transpose(1, 2)
-            v = self.v_up(lat_p).view(P, T, h, d).transpose(1, 2)
-            o = F.scaled_dot_product_attention(q[:npre].view(P, T, h, d).transpose(1, 2), k, v,
-                                               is_causal=True)
-            out[:npre] = o.transpose(1, 2).reshape(npre, h, d)
+            k = self.k_up(lat_p).view(npre, h, d)
+            v = self.v_up(lat_p).view(npre, h, d)
+            if cu_prefill is None:
+                cu_prefill = torch.arange(0, (P + 1) * T, T, dtype=torch.int32, device=x.device)
+            self._causal(q[:npre], k, v, cu_prefill, T, out[:npre])
         if nd > 0:
             slots = decode_slots.long()
             cache[slots, decode_pos] = latent[npre:].to(cache.dtype)
@@ -322,7 +342,8 @@ class SophiaBlock(nn.Module):
         if self.layer_type == "mla":
             attn = lambda y: self.attn.forward_mixed(
                 y, step["n_prefill_seqs"], step["prefill_len"], step["prefill_slots"],
-                step["decode_slots"], step["decode_pos"], step["max_decode_len"])
+                step["decode_slots"], step["decode_pos"], step["max_decode_len"],
+                cu_prefill=step["cu_prefill"])
         else:
             attn = lambda y: self.attn.forward_mixed(
                 y, step["n_prefill_seqs"] * step["prefill_len"], step["cu_prefill"],

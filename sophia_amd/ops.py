@@ -568,3 +568,41 @@ def mla_decode_attn(qa: torch.Tensor, latent_cache: torch.Tensor, slots: torch.T
         heads, rank, int(splits), nat.ptr(ws), ws_bytes, nat.stream_handle(qa.device))
     nat.check(rc, "sophia_mla_decode_attn")
     return y
+
+
+def causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor,
+                     max_len: int, *, scale: float | None = None,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """Causal self-attention within each packed sequence (the no-cache prefill
+    attention of SophiaMLA, ml/runtime/model/attention.py:630-639,
+    ``scaled_dot_product_attention(q, k, v, is_causal=True)``).
+
+    q, k, v: [total, heads, 128] bf16 with dense [heads, 128] rows (row
+    strides free); cu_seqlens int32 [n + 1] on the device; ``max_len`` (host
+    int) must bound every sequence length.  Returns [total, heads, 128] bf16
+    (or writes ``out``, which may be a row-strided view)."""
+    for t, name in ((q, "q"), (k, "k"), (v, "v")):
+        _gpu(t, name)
+        if t.dtype != torch.bfloat16:
+            raise RuntimeError(f"{name} must be bfloat16")
+    total, heads, hd = (int(x) for x in q.shape)
+    if hd != 128:
+        raise RuntimeError("causal_attention is built for head_dim 128")
+    qs = _heads_rows(q, "q", heads, hd)
+    ks = _heads_rows(k, "k", heads, hd)
+    vs = _heads_rows(v, "v", heads, hd)
+    if int(k.size(0)) != total or int(v.size(0)) != total:
+        raise RuntimeError("q, k and v must have the same number of rows")
+    cu = _int32(cu_seqlens, "cu_seqlens", q.device)
+    y = out if out is not None else torch.empty((total, heads, hd), dtype=q.dtype, device=q.device)
+    if y.dtype != torch.bfloat16 or tuple(y.shape) != (total, heads, hd):
+        raise RuntimeError(f"out must be bfloat16 [{total}, {heads}, {hd}]")
+    os_ = _heads_rows(y, "out", heads, hd)
+    for t, name in ((q, "q"), (k, "k"), (v, "v")):
+        _aligned(t, name)
+    rc = nat.lib().sophia_causal_attention(
+        nat.ptr(q), qs, nat.ptr(k), ks, nat.ptr(v), vs, nat.ptr(y), os_, nat.ptr(cu),
+        int(cu.numel()) - 1, total, int(max_len), heads, hd,
+        float(hd ** -0.5 if scale is None else scale), nat.DTYPE_BF16, nat.stream_handle(q.device))
+    nat.check(rc, "sophia_causal_attention")
+    return y

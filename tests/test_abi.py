@@ -42,7 +42,7 @@ def test_header_declares_the_entry_points():
                  "sophia_kda_chunk_workspace_size", "sophia_kda_decode_step",
                  "sophia_last_error", "sophia_abi_version", "sophia_attn_res_mix",
                  "sophia_situ_glu", "sophia_gated_head_norm", "sophia_mla_decode_attn",
-                 "sophia_mla_decode_workspace_size"):
+                 "sophia_mla_decode_workspace_size", "sophia_causal_attention"):
         assert name in decls, name
 
 
@@ -124,6 +124,13 @@ def test_host_side_queries_and_validation():
     rc = lib.sophia_mla_decode_attn(16, 2048, 1, 32, 2048 * 128, 8, 2048, 48, 64, 0.1, 80, 2048, 1, 4,
                                     16, 128, 3, None, 0, None)
     assert rc == nat.SOPHIA_ERR_INVALID and "workspace" in nat.last_error()
+    # Causal attention: bf16 and head_dim 128 only.
+    rc = lib.sophia_causal_attention(16, 2048, 32, 2048, 48, 2048, 64, 2048, 80, 2, 100, 64, 16, 128,
+                                     0.08, 0, None)
+    assert rc == nat.SOPHIA_ERR_INVALID and "bf16" in nat.last_error()
+    rc = lib.sophia_causal_attention(16, 1024, 32, 1024, 48, 1024, 64, 1024, 80, 2, 100, 64, 16, 64,
+                                     0.08, 1, None)
+    assert rc == nat.SOPHIA_ERR_INVALID and "head_dim" in nat.last_error()
 
 
 def test_ops_reject_cpu_tensors():

@@ -286,3 +286,78 @@ def test_mla_decode_attn_matches_fp64_reference(rank, heads, rows, splits, dtype
     assert err <= 1e-2, err
     if rows > 4:
         assert float(y[3].abs().max()) == 0.0
+
+
+def _causal_ref(q, k, v, cu, scale):
+    """Causal softmax attention per packed sequence, float32 on the host from
+    the same bf16 inputs (scaled_dot_product_attention(is_causal=True) per
+    sequence, attention.py:630-639)."""
+    q, k, v = (t.float().cpu() for t in (q, k, v))
+    out = torch.zeros_like(q)
+    for a, b in zip(cu[:-1].tolist(), cu[1:].tolist()):
+        n = b - a
+        if n == 0:
+            continue
+        s = torch.einsum("thd,shd->hts", q[a:b], k[a:b]) * scale
+        s = s.masked_fill(torch.ones(n, n, dtype=torch.bool).triu(1), float("-inf"))
+        out[a:b] = torch.einsum("hts,shd->thd", torch.softmax(s, dim=-1), v[a:b])
+    return out
+
+
+@pytest.mark.parametrize("lengths,heads", [((1,), 1), ((77, 300, 128, 129, 0, 5), 3),
+                                           ((1024, 1024), 16), ((1000,), 2)])
+def test_causal_attention_matches_reference(lengths, heads):
+    """Ragged packed sequences (an empty one, lengths at and around the 64-key
+    and 128-query block edges), row-strided q (a slice of a fused projection)
+    and an output view, against the float32 reference.  Tolerance: the
+    probabilities enter the value product as bf16, so
+    max|y - ref| <= 1e-2 max|ref|."""
+    from sophia_amd import ops
+    dev = _dev()
+    g = torch.Generator(device="cpu").manual_seed(sum(lengths) + heads)
+    total = sum(lengths)
+    cu = torch.tensor([0] + list(np.cumsum(lengths)), dtype=torch.int32)
+    width = heads * 128
+    fused = (torch.randn(total, 3 * width + 64, generator=g)).to(dev, torch.bfloat16)
+    q = fused[:, 64:64 + width].view(total, heads, 128)
+    k = fused[:, 64 + width:64 + 2 * width].view(total, heads, 128)
+    v = (torch.randn(total, heads, 128, generator=g)).to(dev, torch.bfloat16)
+    big = torch.full((total, heads + 1, 128), 7.0, dtype=torch.bfloat16, device=dev)
+    out = big[:, 1:]
+    scale = 128 ** -0.5
+    y = ops.causal_attention(q, k, v, cu.to(dev), max(lengths), scale=scale, out=out)
+    torch.cuda.synchronize()
+    assert y.data_ptr() == out.data_ptr()
+    ref = _causal_ref(q, k, v, cu, scale)
+    err = float((y.float().cpu() - ref).abs().max()) / float(ref.abs().max())
+    assert err <= 1e-2, err
+    assert bool((big[:, 0].float() == 7.0).all()), "wrote outside the output view"
+
+
+def test_mla_prefill_bf16_kernel_matches_sdpa_path():
+    """SophiaMLA.forward in bf16 (HIP causal kernel) against the same module in
+    fp32 (torch SDPA) on the same weights and input."""
+    from sophia_amd.config import ModelArgs
+    from sophia_amd.decoder import SophiaMLA
+    dev = _dev()
+    torch.manual_seed(3)
+    args = ModelArgs(dim=256, num_heads=2, mla_q_rank=64, mla_kv_rank=32, max_seq_len=512,
+                     max_batch_size=2)
+    m32 = SophiaMLA(args).to(dev).eval()
+    m32.use_cache = False
+    with torch.no_grad():  # scores of order one, so that the softmax is far from uniform
+        m32.q_up.weight.mul_(12.0)
+        m32.k_up.weight.mul_(12.0)
+    m16 = SophiaMLA(args).to(dev).eval()
+    m16.load_state_dict(m32.state_dict())
+    m16.use_cache = False
+    for mod in m16.modules():
+        if mod.__class__.__name__ == "RuntimeLinear":
+            mod.weight.data = mod.weight.data.to(torch.bfloat16)
+    x = torch.randn(2, 300, 256, device=dev)
+    with torch.no_grad():
+        y32 = m32(x)
+        y16 = m16(x.to(torch.bfloat16))
+    torch.cuda.synchronize()
+    err = float((y16.float() - y32).abs().max()) / float(y32.abs().max())
+    assert err <= 3e-2, err
