@@ -319,13 +319,14 @@ def main(argv=None) -> int:
     # ShortConv over the same packed batch (3 x 2048 channels, bf16).
     gen = torch.Generator().manual_seed(2)
     xconv = torch.randn((total, 3 * HEADS * DIM), generator=gen).to(torch.bfloat16).to(dev)
-    wconv = (torch.randn((3 * HEADS * DIM, 4), generator=gen) * 0.02).to(dev)
+    # taps rounded to the activation dtype once, as the decoder keeps them
+    wconv = (torch.randn((3 * HEADS * DIM, 4), generator=gen) * 0.02).to(torch.bfloat16).float().to(dev)
     conv_state = torch.zeros((len(lengths), 3 * HEADS * DIM, 3), device=dev)
     yconv = torch.empty_like(xconv)
 
     def conv():
         ops.short_conv_fwd(xconv, wconv, inp["cu"], conv_state=conv_state, read_history=False,
-                           write_history=True, out=yconv)
+                           write_history=True, out=yconv, weight_rounded=True)
 
     if args.only in ("all", "kda", "conv"):
         _, cper = time_events(torch, conv, args.steps, args.warmup, stream)

@@ -105,7 +105,9 @@ __host__ __device__ __forceinline__ int64_t iclamp64(int64_t v, int64_t lo, int6
 }
 
 // ---------------------------------------------------------------- math
-__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + __expf(-x)); }
+// 1 / (1 + e^{-x}) with the hardware reciprocal (1 ulp) instead of an IEEE
+// division sequence; e^{-x} = inf gives exactly 0.
+__device__ __forceinline__ float sigmoid_f(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
 // Log-decay of the KDA gate: lb * sigmoid(exp(A_log[h]) * (z + dt_bias)).
 __device__ __forceinline__ float kda_log_decay(float z, float head_scale, float bias, float lb) {
