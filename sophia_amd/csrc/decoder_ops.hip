@@ -113,6 +113,7 @@ __global__ __launch_bounds__(256) void attn_res_mix_kernel(MixArgs a) {
   const int nw = blockDim.x >> 6;
   const int64_t row = blockIdx.x;
   const int chunks = a.dim >> 3;
+  const float inv_dim = 1.0f / static_cast<float>(a.dim);
   u4 raw[BF16 ? DEPTH : 1][CPT];
   float ss[DEPTH], dq[DEPTH];
 #pragma unroll
@@ -172,7 +173,7 @@ __global__ __launch_bounds__(256) void attn_res_mix_kernel(MixArgs a) {
       s2 += red[2 * b][w];
       d += red[2 * b + 1][w];
     }
-    p[b] = d * rsqrtf(s2 / static_cast<float>(a.dim) + a.eps);
+    p[b] = d * rsqrtf(s2 * inv_dim + a.eps);
     mx = fmaxf(mx, p[b]);
   }
   float z = 0.f;
@@ -181,7 +182,7 @@ __global__ __launch_bounds__(256) void attn_res_mix_kernel(MixArgs a) {
     p[b] = __expf(p[b] - mx);
     z += p[b];
   }
-  const float rz = 1.0f / z;
+  const float rz = __builtin_amdgcn_rcpf(z);
 #pragma unroll
   for (int b = 0; b < DEPTH; ++b) p[b] *= rz;
   // Pass 2: the weighted sum.
@@ -213,7 +214,7 @@ __global__ __launch_bounds__(256) void attn_res_mix_kernel(MixArgs a) {
     lds_barrier();
     float tot = 0.f;
     for (int w = 0; w < nw; ++w) tot += red[2 * DEPTH][w];
-    const float r = rsqrtf(tot / static_cast<float>(a.dim) + a.out_eps);
+    const float r = rsqrtf(tot * inv_dim + a.out_eps);
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       const int c = tid + k * blockDim.x;
@@ -257,31 +258,39 @@ __device__ __forceinline__ Frac tanh_frac(float x) {
 //   h = cg tanh(g/cg) sigmoid(g) * cu tanh(u/cu)
 //     = cg cu sgn(g) sgn(u) num_g num_u s / (den_g den_u (1 + e))
 // with e = e^{-|g|} <= 1 and s = 1 (g >= 0) or e (g < 0): every factor of the
-// denominator lies in [1, 2], so one reciprocal serves the element.
+// denominator lies in [1, 2], so one reciprocal serves the element.  With the
+// reference's gate cap of 4 (CAP4), e = t_g^2 and no third exponential is
+// needed.  Arguments are pre-scaled on the host: xg = -2 log2(e) / cg,
+// xu = -2 log2(e) / cu (exponent factors) and rcg = 1 / cg, rcu = 1 / cu.
+template <bool BF16, bool CAP4>
 __global__ __launch_bounds__(256) void situ_glu_kernel(const void *gu, int64_t gu_stride, void *h, int64_t h_stride,
-                                                       int hidden, int blocks_per_row, float gate_cap, float up_cap,
-                                                       int dtype) {
+                                                       int hidden, int blocks_per_row, float rcg, float rcu,
+                                                       float scale) {
+  constexpr int kDt = BF16 ? SOPHIA_DTYPE_BF16 : SOPHIA_DTYPE_F32;
   const int row = blockIdx.x / blocks_per_row;  // scalar
   const int c = (blockIdx.x - row * blocks_per_row) * 256 + threadIdx.x;
   if (8 * c >= hidden) return;
-  const int esz = dtype == SOPHIA_DTYPE_BF16 ? 2 : 4;
-  const uint8_t *base = static_cast<const uint8_t *>(gu) + static_cast<int64_t>(row) * gu_stride * esz;
+  const uint8_t *base = static_cast<const uint8_t *>(gu) + static_cast<int64_t>(row) * gu_stride * (BF16 ? 2 : 4);
   float g[8], u[8], o[8];
-  load8(base, 8 * c, dtype, g);
-  load8(base, hidden + 8 * c, dtype, u);
-  const float rcg = 1.0f / gate_cap, rcu = 1.0f / up_cap, scale = gate_cap * up_cap;
-  const bool cap4 = gate_cap == 4.0f;
+  load8(base, 8 * c, kDt, g);
+  load8(base, hidden + 8 * c, kDt, u);
+  constexpr float kM2Log2e = -2.0f * 1.44269504088896341f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const float ag = fabsf(g[i]);
     const Frac fg = tanh_frac(ag * rcg);
     const Frac fu = tanh_frac(fabsf(u[i]) * rcu);
-    const float e = cap4 ? fg.t * fg.t : __builtin_amdgcn_exp2f(-1.44269504088896341f * ag);
+    float e;
+    if constexpr (CAP4)
+      e = fg.t * fg.t;
+    else
+      e = __builtin_amdgcn_exp2f(0.5f * kM2Log2e * ag);
     const float s = g[i] >= 0.f ? 1.0f : e;
     const float mag = scale * fg.num * fu.num * s * __builtin_amdgcn_rcpf(fg.den * fu.den * (1.0f + e));
-    o[i] = copysignf(mag, g[i]) * (u[i] < 0.f ? -1.0f : 1.0f);
+    // sign of g times sign of u, as a flip of the sign bit
+    o[i] = __uint_as_float(__float_as_uint(mag) ^ ((__float_as_uint(g[i]) ^ __float_as_uint(u[i])) & 0x80000000u));
   }
-  store8(static_cast<uint8_t *>(h) + static_cast<int64_t>(row) * h_stride * esz, 8 * c, dtype, o);
+  store8(static_cast<uint8_t *>(h) + static_cast<int64_t>(row) * h_stride * (BF16 ? 2 : 4), 8 * c, kDt, o);
 }
 
 // Gated per-head output: y = (RMSNorm_head(o; w, eps) or o) * sigmoid(gate).
@@ -822,9 +831,22 @@ extern "C" int sophia_situ_glu(const void *gate_up, int64_t gate_up_stride, void
   const int blocks_per_row = (hidden / 8 + 255) / 256;
   const int64_t blocks = rows * blocks_per_row;
   SOPHIA_REQUIRE(blocks <= 0x7fffffff, "situ_glu: too many rows");
-  hipLaunchKernelGGL(situ_glu_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), gate_up, gate_up_stride, hidden_out, out_stride, hidden,
-                     blocks_per_row, gate_softcap, up_softcap, dtype);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>(blocks)), block(256);
+  const float rcg = 1.0f / gate_softcap, rcu = 1.0f / up_softcap, scale = gate_softcap * up_softcap;
+  const bool bf = dtype == SOPHIA_DTYPE_BF16, cap4 = gate_softcap == 4.0f;
+  if (bf && cap4)
+    hipLaunchKernelGGL((situ_glu_kernel<true, true>), grid, block, 0, st, gate_up, gate_up_stride, hidden_out,
+                       out_stride, hidden, blocks_per_row, rcg, rcu, scale);
+  else if (bf)
+    hipLaunchKernelGGL((situ_glu_kernel<true, false>), grid, block, 0, st, gate_up, gate_up_stride, hidden_out,
+                       out_stride, hidden, blocks_per_row, rcg, rcu, scale);
+  else if (cap4)
+    hipLaunchKernelGGL((situ_glu_kernel<false, true>), grid, block, 0, st, gate_up, gate_up_stride, hidden_out,
+                       out_stride, hidden, blocks_per_row, rcg, rcu, scale);
+  else
+    hipLaunchKernelGGL((situ_glu_kernel<false, false>), grid, block, 0, st, gate_up, gate_up_stride, hidden_out,
+                       out_stride, hidden, blocks_per_row, rcg, rcu, scale);
   return check_launch("situ_glu");
 }
 
