@@ -27,11 +27,16 @@ extern "C" {
  * (SophiaBlock's attn_norm / ffn_norm, blocks.py:72-87, and the final norm
  * of the logits path, ml/runtime/model/transformer.py:189,210 and
  * ml/runtime/model/ops.py:67-77):
+ *   partial  <- partial + residual, written to partial_out, when residual is not NULL
+ *              (the residual add SophiaBlock does before the mix, blocks.py:78-86)
  *   values = [completed[:, 0], ..., completed[:, n_blocks-1], partial]
  *   score_b = RMSNorm(values_b; norm_weight, eps) . query_weight
  *   mix = sum_b softmax_b(score) * values_b
  *   out = mix, or RMSNorm(mix; out_norm_weight, out_eps)
  *   partial   : [rows, dim], row stride partial_stride.
+ *   residual, partial_out : [rows, dim] or NULL (both or neither), row strides
+ *               residual_stride, partial_out_stride; partial_out may not alias
+ *               partial, residual or out.
  *   completed : [rows, n_blocks, dim] with strides (completed_row_stride,
  *               completed_block_stride, 1); unused when n_blocks == 0.
  *   norm_weight, query_weight, out_norm_weight : [dim] fp32.
@@ -40,7 +45,8 @@ extern "C" {
  * dim a multiple of 8 and at most 4096; 0 <= n_blocks < 16; strides multiples
  * of 8; every pointer 16-byte aligned.
  */
-int sophia_attn_res_mix(const void *partial, int64_t partial_stride, const void *completed,
+int sophia_attn_res_mix(const void *partial, int64_t partial_stride, const void *residual, int64_t residual_stride,
+                        void *partial_out, int64_t partial_out_stride, const void *completed,
                         int64_t completed_row_stride, int64_t completed_block_stride, int n_blocks,
                         const float *norm_weight, const float *query_weight, float eps,
                         const float *out_norm_weight, float out_eps, void *out, int64_t out_stride,

@@ -78,6 +78,10 @@ __device__ __forceinline__ u2 pack4_bf16(f4 v) {
 struct MixArgs {
   const void *partial;
   int64_t partial_stride;
+  const void *residual;     // NULL, or added to the partial block first (then written to partial_out)
+  int64_t residual_stride;
+  void *partial_out;
+  int64_t partial_out_stride;
   const void *completed;
   int64_t completed_row_stride, completed_block_stride;
   int n_blocks;
@@ -98,6 +102,20 @@ __device__ __forceinline__ const void *depth_value(const MixArgs &a, int64_t row
     return static_cast<const uint8_t *>(a.completed) +
            (row * a.completed_row_stride + static_cast<int64_t>(b) * a.completed_block_stride) * esz;
   return static_cast<const uint8_t *>(a.partial) + row * a.partial_stride * esz;
+}
+
+// Chunk c of depth block b as floats; the partial block is partial + residual
+// when a residual is given (an fp32 sum, rounded to bf16 for bf16 data, as the
+// reference adds in the activation dtype).
+__device__ __forceinline__ void load_depth(const MixArgs &a, int64_t row, int b, int c, int dtype, float (&v)[8]) {
+  load8(depth_value(a, row, b), 8 * c, dtype, v);
+  if (b == a.n_blocks && a.residual != nullptr) {
+    float r[8];
+    load8(static_cast<const uint8_t *>(a.residual) + row * a.residual_stride * (dtype == SOPHIA_DTYPE_BF16 ? 2 : 4),
+          8 * c, dtype, r);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] += r[i];
+  }
 }
 
 // One row per workgroup; thread t owns the 8-element chunks t + k blockDim,
@@ -128,6 +146,23 @@ __global__ __launch_bounds__(256) void attn_res_mix_kernel(MixArgs a) {
         if constexpr (BF16)
           raw[b][k] = *reinterpret_cast<const u4 *>(static_cast<const uint16_t *>(depth_value(a, row, b)) + 8 * c);
       }
+      if (a.residual != nullptr) {  // uniform: partial <- partial + residual, written out once
+        float v[8];
+        if constexpr (BF16) {
+          float r[8];
+          unpack8(raw[DEPTH - 1][k], v);
+          load8(static_cast<const uint8_t *>(a.residual) + row * a.residual_stride * 2, 8 * c, kDt, r);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) v[i] += r[i];
+          u4 w;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) w[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
+          raw[DEPTH - 1][k] = w;
+        } else {
+          load_depth(a, row, DEPTH - 1, c, kDt, v);
+        }
+        store8(static_cast<uint8_t *>(a.partial_out) + row * a.partial_out_stride * (BF16 ? 2 : 4), 8 * c, kDt, v);
+      }
       float wq[8];
       const f4 n0 = *reinterpret_cast<const f4 *>(a.norm_w + 8 * c);
       const f4 n1 = *reinterpret_cast<const f4 *>(a.norm_w + 8 * c + 4);
@@ -144,7 +179,7 @@ __global__ __launch_bounds__(256) void attn_res_mix_kernel(MixArgs a) {
         if constexpr (BF16)
           unpack8(raw[b][k], v);
         else
-          load8(depth_value(a, row, b), 8 * c, kDt, v);
+          load_depth(a, row, b, c, kDt, v);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           ss[b] = fmaf(v[i], v[i], ss[b]);
@@ -200,7 +235,7 @@ __global__ __launch_bounds__(256) void attn_res_mix_kernel(MixArgs a) {
         if constexpr (BF16)
           unpack8(raw[b][k], v);
         else
-          load8(depth_value(a, row, b), 8 * c, kDt, v);
+          load_depth(a, row, b, c, kDt, v);
 #pragma unroll
         for (int i = 0; i < 8; ++i) o[k][i] = fmaf(p[b], v[i], o[k][i]);
       }
@@ -766,7 +801,9 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 using namespace sophia;
 
-extern "C" int sophia_attn_res_mix(const void *partial, int64_t partial_stride, const void *completed,
+extern "C" int sophia_attn_res_mix(const void *partial, int64_t partial_stride, const void *residual,
+                                   int64_t residual_stride, void *partial_out, int64_t partial_out_stride,
+                                   const void *completed,
                                    int64_t completed_row_stride, int64_t completed_block_stride, int n_blocks,
                                    const float *norm_weight, const float *query_weight, float eps,
                                    const float *out_norm_weight, float out_eps, void *out, int64_t out_stride,
@@ -786,10 +823,15 @@ extern "C" int sophia_attn_res_mix(const void *partial, int64_t partial_stride, 
   SOPHIA_REQUIRE(aligned16(partial) && aligned16(out) && aligned16(norm_weight) && aligned16(query_weight) &&
                      aligned16(out_norm_weight) && (n_blocks == 0 || aligned16(completed)),
                  "attn_res_mix: pointers must be 16-byte aligned");
+  SOPHIA_REQUIRE(residual == nullptr || (partial_out != nullptr && aligned16(residual) && aligned16(partial_out) &&
+                                          residual_stride % 8 == 0 && partial_out_stride % 8 == 0 &&
+                                          residual_stride >= dim && partial_out_stride >= dim),
+                 "attn_res_mix: a residual needs a partial_out; both 16-byte aligned with strides of 8");
   SOPHIA_REQUIRE(rows <= 0x7fffffff, "attn_res_mix: too many rows");
   if (rows == 0) return SOPHIA_OK;
-  MixArgs a{partial, partial_stride, completed, completed_row_stride, completed_block_stride, n_blocks, norm_weight,
-            query_weight, eps, out_norm_weight, out_eps, out, out_stride, dim, dtype};
+  MixArgs a{partial, partial_stride, residual, residual_stride, partial_out, partial_out_stride, completed,
+            completed_row_stride, completed_block_stride, n_blocks, norm_weight, query_weight, eps, out_norm_weight,
+            out_eps, out, out_stride, dim, dtype};
   const int chunks = dim / 8;
   const int per_thread = (chunks + 255) / 256;
   const int threads = ((chunks + per_thread - 1) / per_thread + 63) / 64 * 64;

@@ -269,12 +269,14 @@ class AttentionResidualMixer(nn.Module):
         return self._query_f32
 
     def forward(self, partial_block: torch.Tensor, completed_blocks: torch.Tensor,
-                out_norm: RMSNorm | None = None) -> torch.Tensor:
-        """The mix; with ``out_norm``, ``out_norm(mix)`` from the same kernel."""
+                out_norm: RMSNorm | None = None, *, residual: torch.Tensor | None = None):
+        """The mix; with ``out_norm``, ``out_norm(mix)`` from the same kernel.
+        With ``residual``, the partial block is partial_block + residual (added
+        in the same kernel) and ``(partial_block + residual, mix)`` is returned."""
         return ops.attn_res_mix(
             partial_block, completed_blocks, self.norm.weight, self._query(), self.norm.eps,
             out_norm_weight=None if out_norm is None else out_norm.weight,
-            out_eps=1e-6 if out_norm is None else out_norm.eps)
+            out_eps=1e-6 if out_norm is None else out_norm.eps, residual=residual)
 
 
 def _append_block(completed: torch.Tensor, partial: torch.Tensor) -> torch.Tensor:
@@ -321,24 +323,38 @@ class SophiaBlock(nn.Module):
         self.attn_residual = AttentionResidualMixer(args)
         self.ffn_residual = AttentionResidualMixer(args)
 
-    def _mix(self, partial_block, completed_blocks, attn):
-        # attn_norm(attn_residual(...)) and ffn_norm(ffn_residual(...)) each run
-        # as one kernel: the mixes feed nothing but these norms.
-        attn_input = self.attn_residual(partial_block, completed_blocks, self.attn_norm)
+    def _mix(self, partial_block, completed_blocks, attn, pending=None, defer=False):
+        """blocks.py:66-87.  ``pending``: an FFN output of the previous layer
+        not yet added to ``partial_block``; the add runs inside this layer's
+        first depth mix.  With ``defer``, this layer's own FFN output is
+        returned unadded as a third value, for the next layer (or the final
+        mix) to add the same way.  attn_norm(attn_residual(...)) and
+        ffn_norm(ffn_residual(...)) each run as one kernel: the mixes feed
+        nothing but these norms."""
+        if pending is None:
+            attn_input = self.attn_residual(partial_block, completed_blocks, self.attn_norm)
+        else:
+            partial_block, attn_input = self.attn_residual(partial_block, completed_blocks,
+                                                           self.attn_norm, residual=pending)
         if self.layer_idx % self.attn_res_block_size == 0:
             completed_blocks = _append_block(completed_blocks, partial_block)
             partial_block = attn(attn_input)
+            ffn_input = self.ffn_residual(partial_block, completed_blocks, self.ffn_norm)
         else:
-            partial_block = partial_block + attn(attn_input)
-        ffn_input = self.ffn_residual(partial_block, completed_blocks, self.ffn_norm)
-        partial_block = partial_block + self.ffn(ffn_input)
-        return partial_block, completed_blocks
+            partial_block, ffn_input = self.ffn_residual(partial_block, completed_blocks,
+                                                         self.ffn_norm, residual=attn(attn_input))
+        ffn_out = self.ffn(ffn_input)
+        if defer:
+            return partial_block, completed_blocks, ffn_out
+        return partial_block + ffn_out, completed_blocks
 
-    def forward(self, partial_block, completed_blocks, *, start_pos: int = 0):
+    def forward(self, partial_block, completed_blocks, *, start_pos: int = 0, pending=None,
+                defer: bool = False):
         return self._mix(partial_block, completed_blocks,
-                         lambda y: self.attn(y, start_pos=int(start_pos)))
+                         lambda y: self.attn(y, start_pos=int(start_pos)), pending, defer)
 
-    def forward_mixed(self, partial_block, completed_blocks, step: dict):
+    def forward_mixed(self, partial_block, completed_blocks, step: dict, *, pending=None,
+                      defer: bool = False):
         if self.layer_type == "mla":
             attn = lambda y: self.attn.forward_mixed(
                 y, step["n_prefill_seqs"], step["prefill_len"], step["prefill_slots"],
@@ -348,7 +364,7 @@ class SophiaBlock(nn.Module):
             attn = lambda y: self.attn.forward_mixed(
                 y, step["n_prefill_seqs"] * step["prefill_len"], step["cu_prefill"],
                 step["prefill_slots"], step["decode_slots"])
-        return self._mix(partial_block, completed_blocks, attn)
+        return self._mix(partial_block, completed_blocks, attn, pending, defer)
 
 
 def init_weights(model: nn.Module, args: ModelArgs) -> None:
@@ -422,9 +438,17 @@ class Transformer(nn.Module):
         self._validate(input_ids, start_pos)
         hidden = self.tok_embeddings(input_ids)
         completed = depth_store(hidden, self.args.n_layers, self.args.attn_res_block_size)
+        pending = None  # each layer's FFN output is added inside the next depth mix
         for layer in self.layers:
-            hidden, completed = layer(hidden, completed, start_pos=start_pos)
-        return self.output(self.output_attn_residual(hidden, completed, self.norm))
+            hidden, completed, pending = layer(hidden, completed, start_pos=start_pos,
+                                               pending=pending, defer=True)
+        return self.output(self._final_mix(hidden, completed, pending))
+
+    def _final_mix(self, hidden, completed, pending):
+        """norm(output_attn_residual(hidden + pending, completed)) as one kernel."""
+        if pending is None:
+            return self.output_attn_residual(hidden, completed, self.norm)
+        return self.output_attn_residual(hidden, completed, self.norm, residual=pending)[1]
 
     def forward_mixed(self, prefill_ids: torch.Tensor, decode_ids: torch.Tensor, *,
                       prefill_slots: torch.Tensor, decode_slots: torch.Tensor,
@@ -448,11 +472,14 @@ class Transformer(nn.Module):
         ids = torch.cat((prefill_ids.reshape(-1), decode_ids.reshape(-1)))
         hidden = self.tok_embeddings(ids)
         completed = depth_store(hidden, self.args.n_layers, self.args.attn_res_block_size)
+        pending = None
         for layer in self.layers:
-            hidden, completed = layer.forward_mixed(hidden, completed, step)
+            hidden, completed, pending = layer.forward_mixed(hidden, completed, step,
+                                                             pending=pending, defer=True)
         last = torch.cat((torch.arange(T - 1, P * T, T, device=hidden.device),
                           torch.arange(P * T, P * T + D, device=hidden.device)))
-        return self.output(self.output_attn_residual(hidden[last], completed[last], self.norm))
+        return self.output(self._final_mix(hidden[last], completed[last],
+                                           None if pending is None else pending[last]))
 
 
 class MixedStepGraph:

@@ -377,7 +377,8 @@ def _aligned(t: torch.Tensor, name: str) -> None:
 def attn_res_mix(partial: torch.Tensor, completed: torch.Tensor, norm_weight: torch.Tensor,
                  query_weight: torch.Tensor, eps: float, *,
                  out_norm_weight: torch.Tensor | None = None, out_eps: float = 1e-6,
-                 out: torch.Tensor | None = None) -> torch.Tensor:
+                 residual: torch.Tensor | None = None,
+                 out: torch.Tensor | None = None):
     """AttentionResidualMixer.forward (ml/runtime/model/blocks.py:38-48) in one
     kernel: softmax over the depth axis of [completed blocks..., partial] with
     scores RMSNorm(value) . query, then the weighted sum of the values; with
@@ -390,6 +391,11 @@ def attn_res_mix(partial: torch.Tensor, completed: torch.Tensor, norm_weight: to
     scores, softmax and the output norm run in fp32 and the result is rounded
     once to partial.dtype (the reference rounds the softmax weights, the
     products and the mix to the activation dtype on the way).  Returns [..., D].
+
+    ``residual`` ([..., D], same dtype): the partial block is first replaced
+    by partial + residual (the residual add of SophiaBlock, blocks.py:78-86,
+    rounded to the activation dtype as there); the call then returns
+    ``(partial + residual, mix)``.
     """
     _gpu(partial, "partial")
     _gpu(completed, "completed")
@@ -430,11 +436,23 @@ def attn_res_mix(partial: torch.Tensor, completed: torch.Tensor, norm_weight: to
     _aligned(y2, "out")
     if n_blocks:
         _aligned(c3, "completed")
+    r2 = po = None
+    rs = 0
+    if residual is not None:
+        _gpu(residual, "residual")
+        if residual.dtype != partial.dtype or tuple(residual.shape) != tuple(partial.shape):
+            raise RuntimeError("residual must match partial's shape and dtype")
+        r2 = residual.reshape(-1, dim)
+        rs = _rows(r2, "residual", dim)
+        _aligned(r2, "residual")
+        po = torch.empty((rows, dim), dtype=partial.dtype, device=partial.device)
     rc = nat.lib().sophia_attn_res_mix(
-        nat.ptr(p2), ps, nat.ptr(c3) if n_blocks else None, c_row, c_blk, n_blocks, nat.ptr(w),
-        nat.ptr(q), float(eps), nat.ptr(wo), float(out_eps), nat.ptr(y2), dim, rows, dim,
-        nat.dtype_code(partial.dtype), nat.stream_handle(partial.device))
+        nat.ptr(p2), ps, nat.ptr(r2), rs, nat.ptr(po), dim, nat.ptr(c3) if n_blocks else None, c_row,
+        c_blk, n_blocks, nat.ptr(w), nat.ptr(q), float(eps), nat.ptr(wo), float(out_eps),
+        nat.ptr(y2), dim, rows, dim, nat.dtype_code(partial.dtype), nat.stream_handle(partial.device))
     nat.check(rc, "sophia_attn_res_mix")
+    if po is not None:
+        return po.view(*lead, dim), y2.view(*lead, dim)
     return y2.view(*lead, dim)
 
 

@@ -82,21 +82,26 @@ def test_host_side_queries_and_validation():
                                   None, 2048, None, 0, None)
     assert rc == nat.SOPHIA_ERR_INVALID
     # Decoder kernels: dim not a multiple of 8, too deep, too wide, misaligned.
-    rc = lib.sophia_attn_res_mix(None, 1536, None, 0, 0, 0, None, None, 1e-5, None, 1e-5, None,
-                                 1536, 4, 1532, 1, None)
+    mix = lambda *a: lib.sophia_attn_res_mix(*a)  # noqa: E731
+    rc = mix(None, 1536, None, 0, None, 0, None, 0, 0, 0, None, None, 1e-5, None, 1e-5, None,
+             1536, 4, 1532, 1, None)
     assert rc == nat.SOPHIA_ERR_INVALID and "dim" in nat.last_error()
-    rc = lib.sophia_attn_res_mix(None, 1536, None, 0, 0, 16, None, None, 1e-5, None, 1e-5, None,
-                                 1536, 4, 1536, 1, None)
+    rc = mix(None, 1536, None, 0, None, 0, None, 0, 0, 16, None, None, 1e-5, None, 1e-5, None,
+             1536, 4, 1536, 1, None)
     assert rc == nat.SOPHIA_ERR_INVALID and "n_blocks" in nat.last_error()
-    rc = lib.sophia_attn_res_mix(None, 8192, None, 0, 0, 0, None, None, 1e-5, None, 1e-5, None,
-                                 8192, 4, 8192, 1, None)
+    rc = mix(None, 8192, None, 0, None, 0, None, 0, 0, 0, None, None, 1e-5, None, 1e-5, None,
+             8192, 4, 8192, 1, None)
     assert rc == nat.SOPHIA_ERR_INVALID and "dim" in nat.last_error()
-    rc = lib.sophia_attn_res_mix(8, 1536, None, 0, 0, 0, 16, 32, 1e-5, None, 1e-5, 64, 1536, 4,
-                                 1536, 1, None)
+    rc = mix(8, 1536, None, 0, None, 0, None, 0, 0, 0, 16, 32, 1e-5, None, 1e-5, 64, 1536, 4,
+             1536, 1, None)
     assert rc == nat.SOPHIA_ERR_INVALID and "aligned" in nat.last_error()
+    # A residual needs somewhere to write the new partial block.
+    rc = mix(16, 1536, 32, 1536, None, 0, None, 0, 0, 0, 48, 64, 1e-5, None, 1e-5, 80, 1536, 4,
+             1536, 1, None)
+    assert rc == nat.SOPHIA_ERR_INVALID and "partial_out" in nat.last_error()
     # No rows: nothing to launch, no pointer needed.
-    assert lib.sophia_attn_res_mix(None, 1536, None, 3 * 1536, 1536, 3, None, None, 1e-5, None,
-                                   1e-5, None, 1536, 0, 1536, 1, None) == nat.SOPHIA_OK
+    assert mix(None, 1536, None, 0, None, 0, None, 3 * 1536, 1536, 3, None, None, 1e-5, None,
+               1e-5, None, 1536, 0, 1536, 1, None) == nat.SOPHIA_OK
     rc = lib.sophia_situ_glu(None, 7936, None, 3968, 4, 3964, 4.0, 25.0, 1, None)
     assert rc == nat.SOPHIA_ERR_INVALID and "hidden" in nat.last_error()
     rc = lib.sophia_situ_glu(None, 7936, None, 3968, 4, 3968, 0.0, 25.0, 1, None)

@@ -361,3 +361,26 @@ def test_mla_prefill_bf16_kernel_matches_sdpa_path():
     torch.cuda.synchronize()
     err = float((y16.float() - y32).abs().max()) / float(y32.abs().max())
     assert err <= 3e-2, err
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rows,n_blocks,dim", [(3, 0, 8), (300, 3, 256), (257, 7, 1536), (33, 2, 4096)])
+def test_attn_res_mix_with_residual_add(dtype, rows, n_blocks, dim):
+    """The residual add folded into the mix: the new partial block equals
+    torch's partial + residual in the activation dtype bit for bit, and the
+    mix (with the consuming norm) is taken over it."""
+    from sophia_amd import ops
+    dev = _dev()
+    g = torch.Generator(device="cpu").manual_seed(rows + 5 * n_blocks + dim)
+    partial = torch.randn(rows, dim, generator=g).to(dev, dtype)
+    residual = (torch.randn(rows, dim, generator=g) * 0.5).to(dev, dtype)
+    completed = (torch.randn(rows, n_blocks, dim, generator=g) * 2).to(dev, dtype)
+    w = (1 + 0.2 * torch.randn(dim, generator=g)).to(dev)
+    q = (torch.randn(dim, generator=g) * 3 / dim ** 0.5).to(dev)
+    wo = (1 + 0.2 * torch.randn(dim, generator=g)).to(dev)
+    new_partial, y = ops.attn_res_mix(partial, completed, w, q, 1e-5, out_norm_weight=wo,
+                                      out_eps=1e-5, residual=residual)
+    torch.cuda.synchronize()
+    summed = partial + residual
+    assert torch.equal(new_partial, summed)
+    _check(y, _mix_ref(summed, completed, w, q, 1e-5, wo, 1e-5), dtype)
