@@ -148,3 +148,48 @@ def test_mixed_step_graph_replays_match_eager():
                 assert torch.allclose(x, y, rtol=1e-4, atol=1e-5), f"replay {replay} caches"
         with torch.no_grad():  # eager work between replays
             model(torch.zeros(1, 3, dtype=torch.long, device=dev), start_pos=0)
+
+
+FULL_DIMS = dict(vocab_size=1024, n_layers=4, ffn_hidden=3968, mla_q_rank=384, mla_kv_rank=128,
+                 dim=1536, num_heads=16, max_seq_len=256, max_batch_size=4)
+
+
+def test_decoder_at_production_widths_matches_oracle():
+    """Every width of the benchmark decoder (dim 1536, 16 heads x 128, SiTU-GLU
+    3968, MLA ranks 384/128; 4 layers, vocab 1,024) in fp32 against the float64
+    oracle (<= 2e-2 of max |logit|), then the same weights in bf16 through the
+    mixed step (HIP causal attention, bf16 kernels throughout) against the same
+    oracle: <= 6e-2 of max |logit| (bf16 activations through four layers)."""
+    from sophia_amd.config import ModelArgs
+    from sophia_amd.decoder import Transformer
+    dev = _dev()
+    torch.manual_seed(5)
+    args = ModelArgs(**FULL_DIMS)
+    model = Transformer(args)
+    with torch.no_grad():
+        for m in model.modules():
+            if m.__class__.__name__ == "AttentionResidualMixer":
+                m.query.weight.normal_(0.0, 0.05)
+    model = model.to(dev)
+    params = {k: _np(v).astype(np.float64) for k, v in model.state_dict().items()}
+    cfg = dict(n_layers=4, num_heads=16, norm_eps=1e-5, attn_res_block_size=4, situ_gate_softcap=4.0,
+               situ_up_softcap=25.0, mla_kv_rank=128, short_conv_kernel=4)
+    ids = torch.randint(0, 1024, (2, 80), generator=torch.Generator().manual_seed(6))
+    with torch.no_grad():
+        logits = model(ids.to(dev), start_pos=0)
+    ref = do.decoder_forward(params, ids.numpy(), cfg=cfg)
+    err = _rel(_np(logits), ref)
+    print(f"fp32 production-width logits rel err {err:.2e}")
+    assert err < REL_TOL
+
+    model.cast_weights_(torch.bfloat16)
+    model.reset_runtime_cache()
+    i32 = lambda xs: torch.tensor(xs, dtype=torch.int32, device=dev)
+    with torch.no_grad():
+        last = model.forward_mixed(ids.to(dev), torch.empty(0, dtype=torch.long, device=dev),
+                                   prefill_slots=i32([0, 1]), decode_slots=i32([]),
+                                   decode_pos=torch.empty(0, dtype=torch.long, device=dev),
+                                   max_decode_len=1)
+    err16 = _rel(_np(last.float()), ref[:, -1])
+    print(f"bf16 mixed-step last-token logits rel err {err16:.2e}")
+    assert err16 < 6e-2
