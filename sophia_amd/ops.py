@@ -568,8 +568,11 @@ def mla_decode_attn(qa: torch.Tensor, latent_cache: torch.Tensor, slots: torch.T
         raise RuntimeError("slots and pos must hold one entry per row")
     n_slots, max_seq = int(latent_cache.size(0)), int(latent_cache.size(1))
     if splits is None:
+        # One work-group per row once the rows fill the chip (the merge of
+        # split partials costs more than it saves there); fewer rows split
+        # their keys so that about 256 work-groups run.
         bound = max_seq if max_len is None else min(int(max_len), max_seq)
-        splits = max(1, min(-(-512 // max(rows, 1)), -(-bound // 128)))
+        splits = 1 if rows >= 128 else max(1, min(-(-256 // max(rows, 1)), -(-bound // 256)))
     dt = qa.dtype if out_dtype is None else out_dtype
     if out is not None and (not out.is_contiguous() or out.dtype != dt
                             or tuple(out.shape) != (rows, heads, rank)):
