@@ -645,7 +645,8 @@ struct FaArgs {
   const int32_t *cu;
   int n_seqs;
   int64_t total;
-  int q_blocks;                    // grid.x
+  int q_blocks;                    // 128-query blocks per sequence (of max_len)
+  int heads;
   float scale_log2;                // softmax scale * log2(e)
 };
 
@@ -654,10 +655,18 @@ __global__ __launch_bounds__(256, 2) void causal_attn_kernel(FaArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t sVt[kFaD * kFaLdV];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int ln = lane & 15, g = lane >> 4;
-  const int h = blockIdx.y, sq = blockIdx.z;
+  // XCD-aware order: work-group b runs on XCD b % 8, and every query block of
+  // one (sequence, head) gets the same b % 8, so its K and V rows are fetched
+  // from HBM once and then served by that XCD's L2.  Heavy (late) query blocks
+  // are dispatched first.
+  const int b = blockIdx.x;
+  const int r = b >> 3;
+  const int pair = (r / a.q_blocks) * 8 + (b & 7);
+  if (pair >= a.heads * a.n_seqs) return;
+  const int h = pair % a.heads, sq = pair / a.heads;
   const int64_t start = iclamp64(a.cu[sq], 0, a.total);
   const int len = static_cast<int>(iclamp64(a.cu[sq + 1], start, a.total) - start);
-  const int q0 = (a.q_blocks - 1 - static_cast<int>(blockIdx.x)) * kFaQ;  // heavy blocks first
+  const int q0 = (a.q_blocks - 1 - r % a.q_blocks) * kFaQ;
   if (q0 >= len) return;
   const int kend = min(len, q0 + kFaQ);           // keys needed by this work-group
   const int nkb = (kend + kFaK - 1) / kFaK;
@@ -986,8 +995,11 @@ extern "C" int sophia_causal_attention(const void *q, int64_t q_stride, const vo
   if (n_seqs == 0 || total == 0 || max_len == 0) return SOPHIA_OK;
   FaArgs a{static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k), static_cast<const uint16_t *>(v),
            q_stride, k_stride, v_stride, static_cast<uint16_t *>(out), out_stride, cu_seqlens, n_seqs, total,
-           (max_len + kFaQ - 1) / kFaQ, scale * 1.44269504088896341f};
-  hipLaunchKernelGGL(causal_attn_kernel, dim3(static_cast<unsigned>(a.q_blocks), heads, n_seqs), dim3(256), 0,
+           (max_len + kFaQ - 1) / kFaQ, heads, scale * 1.44269504088896341f};
+  const int64_t pair_groups = (static_cast<int64_t>(heads) * n_seqs + 7) / 8;
+  const int64_t blocks = pair_groups * 8 * a.q_blocks;
+  SOPHIA_REQUIRE(blocks <= 0x7fffffff, "causal_attention: grid too large");
+  hipLaunchKernelGGL(causal_attn_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), a);
   return check_launch("causal_attention");
 }
