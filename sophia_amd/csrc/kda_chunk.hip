@@ -52,10 +52,7 @@ inline int64_t max_chunks(int64_t total, int n) { return total / kC + n; }
 // Scratch rows for the stores of chunk rows past the end of a sequence
 // (64 rows x 128 fp32 columns, contents never read).
 constexpr size_t kTrashBytes = kC * kD * 4;
-inline size_t header_bytes(int64_t total, int n) {
-  size_t b = sizeof(int32_t) * (static_cast<size_t>(n) + 1 + static_cast<size_t>(max_chunks(total, n)));
-  return (b + 255) & ~static_cast<size_t>(255);
-}
+
 
 __device__ __forceinline__ f4 mfma32(const bf8 &a, const bf8 &b, const f4 &c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -90,41 +87,59 @@ __device__ __forceinline__ int perm_k(int ks, int gq, int e) {
   return 32 * ks + 16 * (e >> 2) + 4 * gq + (e & 3);
 }
 
-// ---- chunk table -----------------------------------------------------------
-// chunk_start[s] = first global chunk of sequence s, chunk_start[n] = total;
-// chunk_seq[c] = sequence of global chunk c.
-__global__ __launch_bounds__(256) void kda_chunk_prep_kernel(const int32_t *__restrict__ cu, int n,
-                                                             int64_t total, int64_t max_ch,
-                                                             int32_t *__restrict__ chunk_start,
-                                                             int32_t *__restrict__ chunk_seq) {
-  __shared__ int32_t part[256];
-  const int t = threadIdx.x;
-  const int per = (n + 255) / 256;
-  const int s0 = min(n, t * per), s1 = min(n, s0 + per);
-  auto nchunks = [&](int s) -> int32_t {
-    int64_t a = iclamp64(cu[s], 0, total);
-    int64_t b = iclamp64(cu[s + 1], a, total);
-    return static_cast<int32_t>((b - a + kC - 1) / kC);
-  };
-  int32_t sum = 0;
-  for (int s = s0; s < s1; ++s) sum += nchunks(s);
-  part[t] = sum;
-  __syncthreads();
-  for (int off = 1; off < 256; off <<= 1) {
-    int32_t v = t >= off ? part[t - off] : 0;
-    __syncthreads();
-    part[t] += v;
-    __syncthreads();
+// ---- chunk numbering -------------------------------------------------------
+// Chunks are numbered sequence by sequence, ceil(len / 64) per sequence.  Each
+// wavefront finds what it needs by a scan over cu_seqlens (64 sequences per
+// step), so no chunk table is built before the kernels; every lane gets the
+// same (wavefront-uniform) answer.  Offsets are clamped into [0, total] and
+// made monotone, so malformed cu_seqlens never move an access out of bounds.
+__device__ __forceinline__ int chunks_of_lane(const int32_t *cu, int n, int64_t total, int s) {
+  if (s >= n) return 0;
+  const int64_t a = iclamp64(cu[s], 0, total);
+  const int64_t b = iclamp64(cu[s + 1], a, total);
+  return static_cast<int>((b - a + kC - 1) / kC);
+}
+
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int u = __shfl_up(v, off, 64);
+    if (lane >= off) v += u;
   }
-  int32_t base = part[t] - sum;
-  for (int s = s0; s < s1; ++s) {
-    chunk_start[s] = base;
-    const int32_t nc = nchunks(s);
-    for (int32_t c = 0; c < nc; ++c)
-      if (base + c < max_ch) chunk_seq[base + c] = s;
-    base += nc;
+  return v;
+}
+
+// Sequence s of global chunk c and the number of the sequence's first chunk;
+// s = n when c is past the last chunk.
+__device__ __forceinline__ void chunk_of(const int32_t *cu, int n, int64_t total, int c, int &s_out,
+                                         int &first_out) {
+  const int lane = threadIdx.x & 63;
+  int done = 0;
+  for (int s0 = 0; s0 < n; s0 += 64) {
+    const int cnt = chunks_of_lane(cu, n, total, s0 + lane);
+    const int incl = wave_incl_scan(cnt, lane);
+    const uint64_t hit = __ballot(s0 + lane < n && c < done + incl);
+    if (hit) {
+      const int l = __builtin_ctzll(hit);
+      s_out = s0 + l;
+      first_out = done + __shfl(incl - cnt, l, 64);
+      return;
+    }
+    done += __shfl(incl, 63, 64);
   }
-  if (t == 255) chunk_start[n] = part[255];
+  s_out = n;
+  first_out = done;
+}
+
+// Number of the first chunk of sequence s (the chunks of the sequences before it).
+__device__ __forceinline__ int first_chunk(const int32_t *cu, int n, int64_t total, int s) {
+  const int lane = threadIdx.x & 63;
+  int done = 0;
+  for (int s0 = 0; s0 < s; s0 += 64) {
+    const int cnt = s0 + lane < s ? chunks_of_lane(cu, n, total, s0 + lane) : 0;
+    done += __shfl(wave_incl_scan(cnt, lane), 63, 64);
+  }
+  return done;
 }
 
 // ---- intra-chunk kernel ----------------------------------------------------
@@ -178,7 +193,6 @@ struct IntraArgs {
   int64_t total;
   int num_heads;
   int64_t max_ch;
-  const int32_t *chunk_start, *chunk_seq;
   uint8_t *records;
 };
 
@@ -299,8 +313,8 @@ __device__ __forceinline__ void intra_scaled_operands(
 // Every barrier inside is a work-group barrier: a work-group running two
 // items at once runs them in lock step.
 template <int QKV_DT, int G_DT, bool GATE>
-__device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int h, uint8_t *smem, int tid,
-                                           uint8_t *rec) {
+__device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int first, int h, uint8_t *smem,
+                                           int tid, uint8_t *rec) {
   float *s_E = reinterpret_cast<float *>(smem + kSmE);
   uint16_t *sKD = reinterpret_cast<uint16_t *>(smem + kSmA);
   float *sY = reinterpret_cast<float *>(smem + kSmA);
@@ -311,10 +325,9 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int h, uin
   float *sT = reinterpret_cast<float *>(smem + kSmC);
   uint16_t *sQK = reinterpret_cast<uint16_t *>(smem + kSmD);
 
-  const int s = p.chunk_seq[c];
   const int64_t seq_a = iclamp64(p.cu[s], 0, p.total);
   const int64_t seq_b = iclamp64(p.cu[s + 1], seq_a, p.total);
-  const int64_t t0 = seq_a + static_cast<int64_t>(c - p.chunk_start[s]) * kC;
+  const int64_t t0 = seq_a + static_cast<int64_t>(c - first) * kC;
   const int len = static_cast<int>(imin64(kC, seq_b - t0));
 
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave = 16-row sub-block (uniform)
@@ -622,9 +635,11 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int c = blockIdx.x;
   const int h = blockIdx.y;
-  const int nch = imin64(p.chunk_start[p.n_seqs], p.max_ch);
-  if (c >= nch) return;
-  intra_item<QKV_DT, G_DT, GATE>(p, c, h, smem, threadIdx.x,
+  if (c >= p.max_ch) return;
+  int s, first;
+  chunk_of(p.cu, p.n_seqs, p.total, c, s, first);
+  if (s >= p.n_seqs) return;  // past the last chunk (uniform over the work-group)
+  intra_item<QKV_DT, G_DT, GATE>(p, c, s, first, h, smem, threadIdx.x,
                                  p.records + (static_cast<size_t>(c) * p.num_heads + h) * kRecBytes);
 }
 
@@ -635,7 +650,6 @@ struct ScanArgs {
   int64_t total;
   int num_heads;
   int64_t max_ch;
-  const int32_t *chunk_start;
   const uint8_t *records;
   const float *h0;
   float *ht;
@@ -882,8 +896,8 @@ __device__ __forceinline__ void wait_records(const Ready &rd, const int *fl, int
 // threads, with the S and U exchange buffers at sSb / sUb.  With FUSED the
 // record loads of each chunk first wait for its published flag.
 template <int NVB, int O_DT, bool FUSED>
-__device__ __forceinline__ void scan_item(const ScanArgs &p, int s, int h, int half, uint8_t *sSb, uint8_t *sUb,
-                                          const Ready &rd) {
+__device__ __forceinline__ void scan_item(const ScanArgs &p, int s, int first, int h, int half, uint8_t *sSb,
+                                          uint8_t *sUb, const Ready &rd) {
   constexpr int NT = NVB / 16;               // 16-column tiles per work-group
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -894,12 +908,12 @@ __device__ __forceinline__ void scan_item(const ScanArgs &p, int s, int h, int h
   g.nt0 = half * NT;
   g.seq_a = iclamp64(p.cu[s], 0, p.total);
   g.seq_b = iclamp64(p.cu[s + 1], g.seq_a, p.total);
-  g.nchunks = static_cast<int>(imin64((g.seq_b - g.seq_a + kC - 1) / kC, p.max_ch - p.chunk_start[s]));
-  g.rec0 = p.records + (static_cast<size_t>(p.chunk_start[s]) * p.num_heads + h) * kRecBytes;
+  g.nchunks = static_cast<int>(imin64((g.seq_b - g.seq_a + kC - 1) / kC, p.max_ch - first));
+  g.rec0 = p.records + (static_cast<size_t>(first) * p.num_heads + h) * kRecBytes;
   g.rec_stride = static_cast<size_t>(p.num_heads) * kRecBytes;
   const int nchunks = g.nchunks;
   const int last = nchunks - 1;
-  const int *fl = FUSED ? rd.flags + h * rd.fstride + p.chunk_start[s] : nullptr;
+  const int *fl = FUSED ? rd.flags + h * rd.fstride + first : nullptr;
   int ready = -1;
 
   if (wave < 4) {
@@ -1006,7 +1020,8 @@ __global__ __launch_bounds__(kScanThreads) void kda_chunk_scan_kernel(ScanArgs p
   const int h = sh % p.num_heads;
   const int s = sh / p.num_heads;
   if (s >= p.n_seqs) return;
-  scan_item<NVB, O_DT, false>(p, s, h, half, sSb, sUb, Ready{nullptr, 0, nullptr});
+  scan_item<NVB, O_DT, false>(p, s, first_chunk(p.cu, p.n_seqs, p.total, s), h, half, sSb, sUb,
+                              Ready{nullptr, 0, nullptr});
 }
 
 
@@ -1043,7 +1058,7 @@ using namespace sophia;
 extern "C" size_t sophia_kda_chunk_workspace_size(int64_t total_tokens, int n_seqs, int num_heads,
                                                   int head_dim) {
   if (total_tokens < 0 || n_seqs <= 0 || num_heads <= 0 || head_dim != kD) return 0;
-  return header_bytes(total_tokens, n_seqs) + kTrashBytes +
+  return kTrashBytes +
          static_cast<size_t>(max_chunks(total_tokens, n_seqs)) * num_heads * kRecBytes;
 }
 
@@ -1090,21 +1105,14 @@ extern "C" int sophia_kda_chunk_fwd(const void *q, const void *k, const void *v,
   const int64_t max_ch = max_chunks(total_tokens, n_seqs);
   SOPHIA_REQUIRE(max_ch <= 0x7fffffff, "kda_chunk_fwd: too many chunks");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  int32_t *chunk_start = static_cast<int32_t *>(workspace);
-  int32_t *chunk_seq = chunk_start + n_seqs + 1;
-  uint8_t *trash = static_cast<uint8_t *>(workspace) + header_bytes(total_tokens, n_seqs);
+  uint8_t *trash = static_cast<uint8_t *>(workspace);
   uint8_t *records = trash + kTrashBytes;
-
-  hipLaunchKernelGGL(kda_chunk_prep_kernel, dim3(1), dim3(256), 0, st, cu_seqlens, n_seqs,
-                     total_tokens, max_ch, chunk_start, chunk_seq);
-  int rc = check_launch("kda_chunk_prep");
-  if (rc) return rc;
+  int rc = SOPHIA_OK;
 
   if (max_ch > 0 && total_tokens > 0) {
     IntraArgs ia{q, k, v, qkv_row_stride, qkv_dtype, g, g_row_stride, g_dtype, beta,
                  beta_row_stride, beta_dtype, A_log, dt_bias, scale, lower_bound, flags,
-                 cu_seqlens, n_seqs, total_tokens, num_heads, max_ch, chunk_start, chunk_seq,
-                 records};
+                 cu_seqlens, n_seqs, total_tokens, num_heads, max_ch, records};
     const dim3 grid(static_cast<unsigned>(max_ch), num_heads);
     const bool gate = (flags & SOPHIA_KDA_GATE_IN_KERNEL) != 0;
     const int key = (qkv_dtype == SOPHIA_DTYPE_BF16) * 4 + (g_dtype == SOPHIA_DTYPE_BF16) * 2 + gate;
@@ -1133,7 +1141,7 @@ extern "C" int sophia_kda_chunk_fwd(const void *q, const void *k, const void *v,
   const int64_t pairs = static_cast<int64_t>(n_seqs) * num_heads;
   int splits = 1;
   while (splits < 8 && pairs * splits * 2 <= static_cast<int64_t>(cus)) splits *= 2;
-  ScanArgs sa{cu_seqlens, n_seqs, total_tokens, num_heads, max_ch, chunk_start, records,
+  ScanArgs sa{cu_seqlens, n_seqs, total_tokens, num_heads, max_ch, records,
               initial_state, final_state, n_state_slots, state_slots, o, o_row_stride, splits, trash};
   const int64_t groups = (pairs + 7) / 8;
   const int64_t blocks = groups * 8 * splits;
