@@ -4,7 +4,7 @@ Headline workload (the value of the JSON line): chunk-64 KDA prefill over a
 packed ragged batch -- 8 sequences with lengths uniform in [256, 4096]
 (seeded), 16 heads x 128, bf16 q/k/v/o, fp32 log-decay g in [-5, 0], fp32
 beta = sigmoid(N(0,1)), fp32 state, zero initial state.  One step = one
-``sophia_kda_chunk_fwd`` call (prep + intra-chunk + scan kernels) over the
+``sophia_kda_chunk_fwd`` call (intra-chunk + scan kernels) over the
 whole batch with inputs resident in HBM.
 
 Also reported: the batch-256 decode step (fp32 state N(0, 0.02), one bf16
@@ -300,7 +300,7 @@ def main(argv=None) -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
                      "traffic": MEASURED_TRAFFIC_BYTES["prefill"],
-                     "kernel": "kda_chunk_prep + kda_chunk_intra + kda_chunk_scan (one call)",
+                     "kernel": "kda_chunk_intra + kda_chunk_scan (one call)",
                      "algorithmic_bytes_per_launch": total * PREFILL_BYTES_PER_TOKEN},
         "mfma": {"achieved_tflops": round(tflops, 2), "peak_tflops": BF16_PEAK_TFLOPS,
                  "frac_of_peak": round(tflops / BF16_PEAK_TFLOPS, 4),
