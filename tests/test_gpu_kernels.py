@@ -279,6 +279,34 @@ def test_chunk_prefill_packing_is_exact():
         assert torch.equal(state[s], one[0]), f"sequence {s} state"
 
 
+def test_chunk_prefill_many_sequences_packing_is_exact():
+    """150 packed sequences (empty ones included), so that the chunk lookup of
+    the kernels crosses several 64-sequence groups: sequences at and around
+    the group edges are bit-identical to running them alone."""
+    from sophia_amd import ops
+    dev = _dev()
+    rng = np.random.default_rng(17)
+    lens = [int(x) for x in rng.integers(0, 140, 150)]
+    lens[63] = 0
+    lens[64] = 65
+    cu = _cu(lens)
+    heads = 2
+    q, k, v, g, beta, a_log, dtb = _kda_inputs(rng, int(cu[-1]), heads)
+    bf = lambda a: torch.tensor(a).to(torch.bfloat16).to(dev)
+    f32 = lambda a: torch.tensor(a, device=dev)
+    kw = dict(A_log=torch.tensor(a_log), dt_bias=torch.tensor(dtb))
+    state = torch.zeros((len(lens), heads, 128, 128), device=dev)
+    o = ops.kda_chunk_fwd(bf(q), bf(k), bf(v), f32(g), f32(beta), f32(cu), final_state=state, **kw)
+    for s in (0, 62, 63, 64, 65, 127, 128, 129, 149):
+        a, b = int(cu[s]), int(cu[s + 1])
+        one = torch.zeros((1, heads, 128, 128), device=dev)
+        if b > a:
+            o1 = ops.kda_chunk_fwd(bf(q[a:b]), bf(k[a:b]), bf(v[a:b]), f32(g[a:b]), f32(beta[a:b]),
+                                   f32(np.array([0, b - a], dtype=np.int32)), final_state=one, **kw)
+            assert torch.equal(o[a:b], o1), f"sequence {s} output"
+        assert torch.equal(state[s], one[0]), f"sequence {s} state"
+
+
 def test_long_sequence_prefill_config4_drift():
     """One 65,536-token sequence (1,024 chunks), 16 heads, bf16 q/k/v with fp32
     state, gates biased to strong decay g ~ U[-5, -0.5] (config 4).  The
