@@ -856,48 +856,12 @@ __device__ __forceinline__ void state_update(const SFrags &f, f4 (&S)[2][NT], ui
 // ring buffers strictly in order: the wait counts in the loop are the minimum
 // over every path into it, so a prologue that interleaves the loads of two
 // buffers makes every later step wait for its newest buffer too.
-// Where a scan that runs beside the intra items (the fused kernel) learns
-// that a record is complete: flags[h * fstride + c] != 0 for global chunk c.
-struct Ready {
-  const int *flags;
-  int64_t fstride;
-  int *err;          // set when a wait gives up (the result is then invalid)
-};
-constexpr int kSpinLimit = 1 << 18;   // polls of ~8 x 64 clocks: ~50 ms, far above any real wait
-
-typedef int i4 __attribute__((ext_vector_type(4)));
-
-// Waits until the records of relative chunks 0..k of one (sequence, head) are
-// published; `ready` (wave-uniform) caches the highest relative chunk known
-// to be.  Flags are read with scalar loads that bypass the scalar cache, so
-// the wait never touches the vector memory counter and leaves the ring loads
-// in flight.  Every wait ends: after kSpinLimit empty polls it records an
-// error and stops waiting.
-__device__ __forceinline__ void wait_records(const Ready &rd, const int *fl, int k, int last, int &ready) {
-  int spins = 0;
-  while (ready < k) {
-    const int *a = fl + ready + 1;
-    i4 v;
-    asm volatile("s_load_dwordx4 %0, %1, 0x0 glc\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(a) : "memory");
-    const int n = v.x == 0 ? 0 : (v.y == 0 ? 1 : (v.z == 0 ? 2 : (v.w == 0 ? 3 : 4)));
-    ready = min(ready + n, last);
-    if (n == 0) {
-      if (++spins > kSpinLimit) {
-        __hip_atomic_store(rd.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        ready = last;
-        break;
-      }
-      __builtin_amdgcn_s_sleep(8);
-    }
-  }
-}
-
-// One (sequence s, head h, value-column slice `half`) of the scan on 512
-// threads, with the S and U exchange buffers at sSb / sUb.  With FUSED the
-// record loads of each chunk first wait for its published flag.
-template <int NVB, int O_DT, bool FUSED>
+//
+// scan_item: one (sequence s, head h, value-column slice `half`) of the scan
+// on 512 threads, with the S and U exchange buffers at sSb / sUb.
+template <int NVB, int O_DT>
 __device__ __forceinline__ void scan_item(const ScanArgs &p, int s, int first, int h, int half, uint8_t *sSb,
-                                          uint8_t *sUb, const Ready &rd) {
+                                          uint8_t *sUb) {
   constexpr int NT = NVB / 16;               // 16-column tiles per work-group
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -913,8 +877,6 @@ __device__ __forceinline__ void scan_item(const ScanArgs &p, int s, int first, i
   g.rec_stride = static_cast<size_t>(p.num_heads) * kRecBytes;
   const int nchunks = g.nchunks;
   const int last = nchunks - 1;
-  const int *fl = FUSED ? rd.flags + h * rd.fstride + first : nullptr;
-  int ready = -1;
 
   if (wave < 4) {
     // ---- U/O role
@@ -922,7 +884,6 @@ __device__ __forceinline__ void scan_item(const ScanArgs &p, int s, int first, i
     if (nchunks <= 0) return;
     constexpr int R = ring_uo<NT>();
     UOFrags<NT> f[R];
-    if constexpr (FUSED) wait_records(rd, fl, min(R - 1, last), last, ready);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const uint8_t *rec = g.rec0 + min(r, last) * g.rec_stride;
@@ -938,7 +899,6 @@ __device__ __forceinline__ void scan_item(const ScanArgs &p, int s, int first, i
         const uint8_t *rec = g.rec0 + min(cc + r + R, last) * g.rec_stride;
         f4 O[NT];
         if (live) uo_pre<NT>(f[r], O, sSb, sUb, w, l);
-        if constexpr (FUSED) wait_records(rd, fl, min(cc + r + R, last), last, ready);
         // Refill while the state role works: the loads may wait for memory
         // queue space here, off the critical path.
         load_uo_main<NT>(f[r], rec, w, l, g.nt0);
@@ -976,7 +936,6 @@ __device__ __forceinline__ void scan_item(const ScanArgs &p, int s, int first, i
     // of chunk c - 1 is refilled with chunk c + kRingS - 1 while the U/O role
     // forms U (the loads may wait for memory queue space there).
     SFrags f[kRingS];
-    if constexpr (FUSED) wait_records(rd, fl, min(kRingS - 2, last), last, ready);
 #pragma unroll
     for (int r = 0; r < kRingS - 1; ++r) {
       load_s(f[r], g.rec0 + min(r, last) * g.rec_stride, sw, l, gq);
@@ -987,7 +946,6 @@ __device__ __forceinline__ void scan_item(const ScanArgs &p, int s, int first, i
       for (int r = 0; r < kRingS; ++r) {
         const bool live = cc + r < nchunks;
         if (live) lds_barrier();  // S published
-        if constexpr (FUSED) wait_records(rd, fl, min(cc + r + kRingS - 1, last), last, ready);
         load_s(f[(r + kRingS - 1) % kRingS], g.rec0 + min(cc + r + kRingS - 1, last) * g.rec_stride, sw, l, gq);
         touch(f[r]);
         if (live) state_update<NT>(f[r], S, sSb, sUb, sw, l);
@@ -1020,8 +978,7 @@ __global__ __launch_bounds__(kScanThreads) void kda_chunk_scan_kernel(ScanArgs p
   const int h = sh % p.num_heads;
   const int s = sh / p.num_heads;
   if (s >= p.n_seqs) return;
-  scan_item<NVB, O_DT, false>(p, s, first_chunk(p.cu, p.n_seqs, p.total, s), h, half, sSb, sUb,
-                              Ready{nullptr, 0, nullptr});
+  scan_item<NVB, O_DT>(p, s, first_chunk(p.cu, p.n_seqs, p.total, s), h, half, sSb, sUb);
 }
 
 
