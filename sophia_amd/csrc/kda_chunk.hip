@@ -58,6 +58,12 @@ __device__ __forceinline__ f4 mfma32(const bf8 &a, const bf8 &b, const f4 &c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+// fp32 16x16x4 MFMA: lane l supplies a[l % 16][k] and b[k][l % 16] for k slot
+// l / 16; c holds rows 4 (l / 16) + i, column l % 16.
+__device__ __forceinline__ f4 mfma_f32x4(float a, float b, const f4 &c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
 __device__ __forceinline__ bf8 pack8(const float *x) {
   bf8 r;
 #pragma unroll
@@ -146,7 +152,6 @@ __device__ __forceinline__ int first_chunk(const int32_t *cu, int n, int64_t tot
 // LDS regions (bytes).  Lifetimes (steps below) let regions A and B be reused.
 //  E: e^{sub-block totals}          float [128][4]           steps 3-8
 //  A: key-side rows KD (6 copies)   bf16  [96][136]           steps 4-5
-//     -> solve scratch Y            float [3][16][16]         step 6
 //     -> beta K e^G, transposed     bf16  [128][64] swizzled  steps 7-8
 //  B: beta V, transposed            bf16  [128][64] swizzled  steps 1-8
 //     -> -W rows                    bf16  [64][136]           steps 9-10
@@ -164,7 +169,6 @@ constexpr size_t kSmD = kSmC + 64 * kLdT * 4;
 constexpr size_t kSmIntra = kSmD + 64 * kLdQK * 2;           // 73216
 static_assert(128 * 64 * 2 <= 96 * kLdKD * 2, "region A holds a swizzled [128][64] bf16 tile");
 static_assert(128 * 64 * 2 <= 64 * kLdKD * 2, "region B holds a swizzled [128][64] bf16 tile");
-static_assert(3 * 256 * 4 <= 96 * kLdKD * 2, "region A holds the solve scratch");
 static_assert(128 * 64 * 2 <= 64 * kLdT * 4, "region C holds a swizzled [128][64] bf16 tile");
 
 __device__ __forceinline__ int swz(int ch, int row) {
@@ -317,7 +321,6 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
                                            int tid, uint8_t *rec) {
   float *s_E = reinterpret_cast<float *>(smem + kSmE);
   uint16_t *sKD = reinterpret_cast<uint16_t *>(smem + kSmA);
-  float *sY = reinterpret_cast<float *>(smem + kSmA);
   uint16_t *sKt = reinterpret_cast<uint16_t *>(smem + kSmA);
   uint16_t *sV = reinterpret_cast<uint16_t *>(smem + kSmB);
   uint16_t *sW = reinterpret_cast<uint16_t *>(smem + kSmB);
@@ -499,9 +502,8 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
   }
   lds_barrier();
 
-  // ---- 6. T = (I + A_kk)^-1 in fp32.  Diagonal 16x16 blocks by forward
-  // substitution (one wave each), then the block rows by sub-diagonal level:
-  //   X_ij = -D_i Y_ij,  Y_ij = sum_{k=j}^{i-1} L_ik X_kj.
+  // ---- 6. T = (I + A_kk)^-1 in fp32.  Diagonal 16x16 blocks D_i by forward
+  // substitution (one wave each), then the off-diagonal blocks.
   {
     float x[16];
     if (l < 16) {
@@ -513,46 +515,48 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
         x[r] = acc;
       }
     }
-    lds_barrier();
+    // Each wave reads and rewrites only its own diagonal block.
     if (l < 16) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) sT[(16 * w + r) * kLdT + 16 * w + l] = x[r];
     }
     lds_barrier();
-    // Block row ib: Y_{ib,j} = sum_{kb=j}^{ib-1} L_{ib,kb} X_{kb,j} (X_{j,j} = D_j),
-    // then X_{ib,j} = -D_ib Y_{ib,j}.  Row block ib's L entries are replaced
-    // only after all of its Y blocks have been formed.
-    const int ri = tid >> 4, cj = tid & 15;
+    // Off-diagonal blocks by sub-diagonal level d on fp32 MFMA:
+    //   X_{i,i-d} = -D_i sum_{k=i-d}^{i-1} L_{i,k} X_{k,i-d},  X_{k,k} = D_k.
+    // Wave i forms block row i.  Its L_{i,k} are read (as A operands) before
+    // any X overwrites them; every other block it reads was written at a lower
+    // level, before the barrier that ends that level.  A 16-deep product is
+    // four 16x16x4 steps; step s of lane group g covers column 4g + s.
+    const int g4 = 4 * gq;
+    f4 Lrow[3], Dw;
 #pragma unroll
-    for (int ib = 1; ib < 4; ++ib) {
+    for (int k = 0; k < 3; ++k)
+      Lrow[k] = *reinterpret_cast<const f4 *>(&sT[(16 * w + lr) * kLdT + 16 * k + g4]);
+    Dw = *reinterpret_cast<const f4 *>(&sT[(16 * w + lr) * kLdT + 16 * w + g4]);
 #pragma unroll
-      for (int j = 0; j < ib; ++j) {
-        float acc = 0.f;
-        const float *lrow = sT + (16 * ib + ri) * kLdT;
-        for (int kb = j; kb < ib; ++kb) {
+    for (int d = 1; d < 4; ++d) {
+      if (w >= d) {
+        const int j = w - d;
+        f4 y = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int m4 = 0; m4 < 4; ++m4) {
-            const f4 lv = *reinterpret_cast<const f4 *>(lrow + 16 * kb + 4 * m4);
+        for (int k = 0; k < 3; ++k) {
+          if (k >= j && k < w) {
+            float bx[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-              acc = fmaf(lv[i], sT[(16 * kb + 4 * m4 + i) * kLdT + 16 * j + cj], acc);
+            for (int i = 0; i < 4; ++i) bx[i] = sT[(16 * k + g4 + i) * kLdT + 16 * j + lr];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) y = mfma_f32x4(Lrow[k][i], bx[i], y);
           }
         }
-        sY[j * 256 + tid] = acc;
-      }
-      lds_barrier();
+        f4 x = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int j = 0; j < ib; ++j) {
-        float acc = 0.f;
+        for (int i = 0; i < 4; ++i) x = mfma_f32x4(Dw[i], y[i], x);
 #pragma unroll
-        for (int m = 0; m < 16; ++m)
-          acc = fmaf(sT[(16 * ib + ri) * kLdT + 16 * ib + m], sY[j * 256 + m * 16 + cj], acc);
-        sT[(16 * ib + ri) * kLdT + 16 * j + cj] = -acc;
+        for (int i = 0; i < 4; ++i) sT[(16 * w + g4 + i) * kLdT + 16 * j + lr] = -x[i];
       }
       lds_barrier();
     }
   }
-  lds_barrier();   // the scratch in region A has been read
 
   // ---- 7. beta K e^G, transposed, into region A (its scratch reads ended
   //         at the last barrier of the solve).
