@@ -170,6 +170,12 @@ constexpr size_t kSmIntra = kSmD + 64 * kLdQK * 2;           // 73216
 static_assert(128 * 64 * 2 <= 96 * kLdKD * 2, "region A holds a swizzled [128][64] bf16 tile");
 static_assert(128 * 64 * 2 <= 64 * kLdKD * 2, "region B holds a swizzled [128][64] bf16 tile");
 static_assert(128 * 64 * 2 <= 64 * kLdT * 4, "region C holds a swizzled [128][64] bf16 tile");
+// Step 1 stages whole-line q, k, v rows, 4 KB per wave and tensor, where no
+// wave writes before step 3: q in region A, k in region C, v in the rest of A
+// (waves 0, 1) and in region D (waves 2, 3).
+__device__ __forceinline__ size_t stage_v(int w) { return w < 2 ? kSmA + 16384 + w * 4096 : kSmD + (w - 2) * 4096; }
+static_assert(16384 + 2 * 4096 <= 96 * kLdKD * 2 && 2 * 4096 <= 64 * kLdQK * 2 && 4 * 4096 <= 64 * kLdT * 4,
+              "step-1 staging fits regions A, C and D");
 
 __device__ __forceinline__ int swz(int ch, int row) {
   return ch * 64 + ((((row >> 3) ^ (ch & 7))) << 3) + (row & 7);
@@ -198,6 +204,7 @@ struct IntraArgs {
   int num_heads;
   int64_t max_ch;
   uint8_t *records;
+  int qkv_lines;  // bf16 q/k/v with 16-byte aligned rows: load whole lines through LDS
 };
 
 __device__ __forceinline__ float fast_sigmoid(float x) {
@@ -374,15 +381,49 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
       braw = static_cast<const uint32_t *>(p.beta)[bidx];
     Raw4<QKV_DT> rq[8], rk[8], rv[8];
     Raw4<G_DT> rg[8];
+    bool lines = false;
+    if constexpr (QKV_DT == SOPHIA_DTYPE_BF16) lines = p.qkv_lines != 0;
+    if (lines) {
+      // Whole cache lines: each wave copies its 16 rows of q, k, v (256 B per
+      // row and head) straight into LDS, four rows per instruction, 16-byte
+      // chunk j of row r at chunk position j ^ r (conflict-free reads below).
+      // The slots are read back after the loads of g below have been issued.
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int ch = 32 * (i >> 1) + 16 * (i & 1) + 4 * gq;
-      rq[i].load(p.q, qrow + ch);
-      rk[i].load(p.k, qrow + ch);
-      rv[i].load(p.v, qrow + ch);
-      rg[i].load(p.g, grow + ch);
+      for (int t = 0; t < 4; ++t) {
+        const int r = 4 * t + (l >> 4);
+        const int64_t rt = 16 * w + r < len ? t0 + 16 * w + r : t0;
+        const int64_t off = rt * p.qkv_stride + static_cast<int64_t>(h) * kD + 8 * ((l & 15) ^ r);
+        const int dst = w * 4096 + t * 1024;
+        __builtin_amdgcn_global_load_lds(static_cast<const uint16_t *>(p.q) + off, smem + kSmA + dst, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(static_cast<const uint16_t *>(p.k) + off, smem + kSmC + dst, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(static_cast<const uint16_t *>(p.v) + off, smem + stage_v(w) + t * 1024, 16,
+                                         0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int ch = 32 * (i >> 1) + 16 * (i & 1) + 4 * gq;
+        rq[i].load(p.q, qrow + ch);
+        rk[i].load(p.k, qrow + ch);
+        rv[i].load(p.v, qrow + ch);
+      }
     }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) rg[i].load(p.g, grow + 32 * (i >> 1) + 16 * (i & 1) + 4 * gq);
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (QKV_DT == SOPHIA_DTYPE_BF16) {
+      if (lines) {
+        // Slot i = 2 ks + a holds channels 32 ks + 16 a + 4 gq .. + 3: bytes
+        // 8 (gq & 1) of chunk 4 ks + 2 a + gq / 2 of row lr.
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int at = w * 4096 + lr * 256 + (((2 * i + (gq >> 1)) ^ lr) << 4) + 8 * (gq & 1);
+          rq[i].w = *reinterpret_cast<const u2 *>(smem + kSmA + at);
+          rk[i].w = *reinterpret_cast<const u2 *>(smem + kSmC + at);
+          rv[i].w = *reinterpret_cast<const u2 *>(smem + stage_v(w) + (at - w * 4096));
+        }
+      }
+    }
     bt = __uint_as_float(p.beta_dtype == SOPHIA_DTYPE_BF16 ? (braw << 16) : braw);
     if (p.flags & SOPHIA_KDA_BETA_SIGMOID) bt = fast_sigmoid(bt);
     bt *= vmask;
@@ -1074,9 +1115,11 @@ extern "C" int sophia_kda_chunk_fwd(const void *q, const void *k, const void *v,
   int rc = SOPHIA_OK;
 
   if (max_ch > 0 && total_tokens > 0) {
+    const auto a16 = [](const void *ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; };
+    const int lines = qkv_dtype == SOPHIA_DTYPE_BF16 && qkv_row_stride % 8 == 0 && a16(q) && a16(k) && a16(v);
     IntraArgs ia{q, k, v, qkv_row_stride, qkv_dtype, g, g_row_stride, g_dtype, beta,
                  beta_row_stride, beta_dtype, A_log, dt_bias, scale, lower_bound, flags,
-                 cu_seqlens, n_seqs, total_tokens, num_heads, max_ch, records};
+                 cu_seqlens, n_seqs, total_tokens, num_heads, max_ch, records, lines};
     SOPHIA_REQUIRE(max_ch * num_heads <= 0x7fffffff, "kda_chunk_fwd: grid too large");
     const dim3 grid(static_cast<unsigned>(max_ch * num_heads));
     const bool gate = (flags & SOPHIA_KDA_GATE_IN_KERNEL) != 0;

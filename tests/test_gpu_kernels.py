@@ -245,6 +245,41 @@ def test_chunk_prefill_saturated_gate():
     assert _rel(_np(o), o_ref) < REL_TOL
 
 
+def test_chunk_prefill_row_layouts_agree():
+    """bf16 q/k/v rows that are 16-byte aligned are loaded as whole cache lines
+    through LDS; other row strides and offsets take per-lane loads.  Both give
+    bit-identical results."""
+    from sophia_amd import ops
+    dev = _dev()
+    rng = np.random.default_rng(12)
+    lens = [70, 1, 130, 64]
+    cu = _cu(lens)
+    total, heads = int(cu[-1]), 3
+    q, k, v, g, beta, a_log, dtb = _kda_inputs(rng, total, heads)
+    width = heads * 128
+
+    def rows(a, pad, offset):
+        buf = torch.zeros(total, width + pad, dtype=torch.bfloat16, device=dev)
+        view = buf[:, offset:offset + width]
+        view.copy_(torch.tensor(a).reshape(total, width).to(torch.bfloat16))
+        return view.unflatten(1, (heads, 128))
+
+    outs = []
+    for pad, offset in ((0, 0), (8, 8), (4, 0), (12, 4)):
+        qt, kt, vt = (rows(a, pad, offset) for a in (q, k, v))
+        assert qt.stride(0) == width + pad
+        st = torch.zeros((len(lens), heads, 128, 128), device=dev)
+        o = ops.kda_chunk_fwd(qt, kt, vt, torch.tensor(g, device=dev), torch.tensor(beta, device=dev),
+                              torch.tensor(cu, device=dev), A_log=torch.tensor(a_log),
+                              dt_bias=torch.tensor(dtb), final_state=st)
+        outs.append((_np(o), _np(st)))
+    for o, st in outs[1:]:
+        assert np.array_equal(o, outs[0][0]) and np.array_equal(st, outs[0][1])
+    qb = lambda a: _np(torch.tensor(a).to(torch.bfloat16))
+    o_ref, h_ref = c_oracle.kda_varlen(qb(q), qb(k), qb(v), g, beta, cu, A_log=a_log, dt_bias=dtb)
+    assert _rel(outs[0][0], o_ref) < REL_TOL and _rel(outs[0][1], h_ref) < REL_TOL
+
+
 def test_chunk_prefill_is_deterministic():
     dev = _dev()
     runs = [_chunk_case(dev, [70, 5, 130], 2, qkv_dtype=torch.bfloat16, gate_in_kernel=True,
