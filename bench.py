@@ -60,8 +60,9 @@ def make_prefill_inputs(torch, dev, lengths, seed=1):
     g = torch.rand(shape, generator=gen) * -5.0
     beta = torch.sigmoid(torch.randn((total, HEADS), generator=gen))
     cu = torch.tensor(np.concatenate([[0], np.cumsum(lengths)]), dtype=torch.int32)
-    return {name: t.to(dev) for name, t in
-            dict(q=q, k=k, v=v, g=g, beta=beta, cu=cu).items()}
+    inputs = {name: t.to(dev) for name, t in dict(q=q, k=k, v=v, g=g, beta=beta, cu=cu).items()}
+    inputs["cu_cpu"] = cu  # the host copy of the offsets (FlashKDA's cu_seqlens_cpu)
+    return inputs
 
 
 def time_events(torch, fn, steps: int, warmup: int, stream) -> tuple[float, list[float]]:
@@ -275,7 +276,7 @@ def main(argv=None) -> int:
     def prefill():
         ops.kda_chunk_fwd(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], inp["cu"],
                           use_qk_l2norm=True, use_gate=False, use_beta_sigmoid=False,
-                          final_state=final, out=out)
+                          final_state=final, out=out, cu_seqlens_cpu=inp["cu_cpu"])
 
     result = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
               "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",

@@ -114,6 +114,12 @@ size_t sophia_kda_chunk_workspace_size(int64_t total_tokens, int n_seqs, int num
  *                 A slot outside [0, n_state_slots) starts from zero and is
  *                 not written.
  *   o           : [total_tokens, H, 128] rows of stride o_row_stride, dtype qkv_dtype.
+ *   cu_seqlens_host: NULL, or a host copy of cu_seqlens (FlashKDA's
+ *                 cu_seqlens_cpu, sm120_concurrent_ffn.py:231).  It only shapes
+ *                 the launch (more work-groups per chain for a batch whose
+ *                 longest sequence is at least twice the mean, longest
+ *                 sequences first); results are identical with or without it.
+ *                 Must be non-decreasing within [0, total_tokens].
  *   workspace   : device scratch of sophia_kda_chunk_workspace_size() bytes,
  *                 256-byte aligned; contents need not be initialised.
  */
@@ -121,7 +127,8 @@ int sophia_kda_chunk_fwd(const void *q, const void *k, const void *v, int64_t qk
                          int qkv_dtype, const void *g, int64_t g_row_stride, int g_dtype,
                          const void *beta, int64_t beta_row_stride, int beta_dtype,
                          const float *A_log, const float *dt_bias, float scale, float lower_bound,
-                         unsigned flags, const int32_t *cu_seqlens, int n_seqs,
+                         unsigned flags, const int32_t *cu_seqlens,
+                         const int32_t *cu_seqlens_host, int n_seqs,
                          int64_t total_tokens, int num_heads, int head_dim,
                          const float *initial_state, float *final_state, int n_state_slots,
                          const int32_t *state_slots, void *o, int64_t o_row_stride,

@@ -29,6 +29,8 @@
 //    four form U and O.  S and U pass between them through LDS as bf16 MFMA
 //    operands (16x16x32 operands pair two C tiles; the A operands carry the
 //    matching k permutation).
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace sophia {
@@ -692,6 +694,9 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
 }
 
 // ---- scan kernel -------------------------------------------------------------
+// Batches of at most kOrderMax sequences whose offsets the host also holds are
+// scanned longest sequence first.
+constexpr int kOrderMax = 64;
 struct ScanArgs {
   const int32_t *cu;
   int n_seqs;
@@ -707,6 +712,8 @@ struct ScanArgs {
   int64_t o_stride;
   int splits;   // blocks per (sequence, head): 128 / NVB
   void *trash;  // kTrashBytes of workspace: destination of rows past a sequence end
+  int ordered;  // 1: the work-groups take the sequences in the order of `order`
+  uint8_t order[kOrderMax];
 };
 
 // ---- scan kernel: two roles per work-group ----------------------------------
@@ -1024,8 +1031,9 @@ __global__ __launch_bounds__(kScanThreads) void kda_chunk_scan_kernel(ScanArgs p
   const int half = (b / 8) % p.splits;
   const int sh = group * 8 + (b % 8);
   const int h = sh % p.num_heads;
-  const int s = sh / p.num_heads;
-  if (s >= p.n_seqs) return;
+  const int rank = sh / p.num_heads;
+  if (rank >= p.n_seqs) return;
+  const int s = p.ordered ? p.order[rank] : rank;
   scan_item<NVB, O_DT>(p, s, first_chunk(p.cu, p.n_seqs, p.total, s), h, half, sSb, sUb);
 }
 
@@ -1072,7 +1080,8 @@ extern "C" int sophia_kda_chunk_fwd(const void *q, const void *k, const void *v,
                                     int64_t g_row_stride, int g_dtype, const void *beta,
                                     int64_t beta_row_stride, int beta_dtype, const float *A_log,
                                     const float *dt_bias, float scale, float lower_bound,
-                                    unsigned flags, const int32_t *cu_seqlens, int n_seqs,
+                                    unsigned flags, const int32_t *cu_seqlens,
+                                    const int32_t *cu_seqlens_host, int n_seqs,
                                     int64_t total_tokens, int num_heads, int head_dim,
                                     const float *initial_state, float *final_state,
                                     int n_state_slots, const int32_t *state_slots, void *o,
@@ -1103,6 +1112,11 @@ extern "C" int sophia_kda_chunk_fwd(const void *q, const void *k, const void *v,
                  "kda_chunk_fwd: o must be aligned to 4 elements");
   SOPHIA_REQUIRE(((uintptr_t)workspace % 256) == 0, "kda_chunk_fwd: workspace must be 256-byte aligned");
   SOPHIA_REQUIRE(n_state_slots >= 0, "kda_chunk_fwd: n_state_slots must be >= 0");
+  if (cu_seqlens_host) {
+    bool ok = cu_seqlens_host[0] >= 0 && cu_seqlens_host[n_seqs] <= total_tokens;
+    for (int i = 0; ok && i < n_seqs; ++i) ok = cu_seqlens_host[i] <= cu_seqlens_host[i + 1];
+    SOPHIA_REQUIRE(ok, "kda_chunk_fwd: cu_seqlens_host is not a non-decreasing offset array in [0, total]");
+  }
   const size_t need = sophia_kda_chunk_workspace_size(total_tokens, n_seqs, num_heads, head_dim);
   if (workspace_bytes < need)
     return set_error(SOPHIA_ERR_WORKSPACE, "kda_chunk_fwd: workspace %zu bytes < required %zu",
@@ -1150,7 +1164,33 @@ extern "C" int sophia_kda_chunk_fwd(const void *q, const void *k, const void *v,
   int splits = 1;
   while (splits < 8 && pairs * splits * 2 <= static_cast<int64_t>(cus)) splits *= 2;
   ScanArgs sa{cu_seqlens, n_seqs, total_tokens, num_heads, max_ch, records,
-              initial_state, final_state, n_state_slots, state_slots, o, o_row_stride, splits, trash};
+              initial_state, final_state, n_state_slots, state_slots, o, o_row_stride, splits, trash,
+              0, {}};
+  if (cu_seqlens_host) {
+    // The host copy of the offsets only shapes the launch; the results do not
+    // depend on it.  A batch whose longest sequence has at least twice the
+    // mean number of chunks spends most of its scan on a few sequential
+    // chains: twice the work-groups per (sequence, head) shortens those
+    // chains, and the shorter sequences queue behind them (one MI355X, the 8
+    // sequences of U[256, 4096] tokens: 118 -> 99 us).  Up to kOrderMax
+    // sequences are taken longest first, so the queue holds the short ones.
+    int64_t nmax = 0, sum = 0;
+    int64_t chunks[kOrderMax];
+    for (int i = 0; i < n_seqs; ++i) {
+      const int64_t c = (static_cast<int64_t>(cu_seqlens_host[i + 1]) - cu_seqlens_host[i] + kC - 1) / kC;
+      nmax = c > nmax ? c : nmax;
+      sum += c;
+      if (i < kOrderMax) chunks[i] = c;
+    }
+    if (splits < 8 && nmax * n_seqs >= 2 * sum && sum > 0) splits *= 2;
+    sa.splits = splits;
+    if (n_seqs <= kOrderMax) {
+      for (int i = 0; i < n_seqs; ++i) sa.order[i] = static_cast<uint8_t>(i);
+      std::stable_sort(sa.order, sa.order + n_seqs,
+                       [&](uint8_t a, uint8_t b) { return chunks[a] > chunks[b]; });
+      sa.ordered = 1;
+    }
+  }
   const int64_t groups = (pairs + 7) / 8;
   const int64_t blocks = groups * 8 * splits;
   SOPHIA_REQUIRE(blocks <= 0x7fffffff, "kda_chunk_fwd: grid too large");

@@ -411,7 +411,8 @@ class SophiaKDA(nn.Module):
             o = ops.kda_chunk_fwd(q, k, v, decay, beta_logits, cu, A_log=self.A_log,
                                   dt_bias=self.dt_bias, lower_bound=self.lower_bound,
                                   initial_state=state if read else None, final_state=state,
-                                  state_slots=slots)
+                                  state_slots=slots,
+                                  cu_seqlens_cpu=None if cu_seqlens.is_cuda else cu_seqlens)
         out = self._output(o, gate_logits, x.dtype)
         return out.view(1, n, self.dim) if squeeze else out
 

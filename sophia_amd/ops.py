@@ -176,13 +176,17 @@ def kda_chunk_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
                   use_beta_sigmoid: bool = True, initial_state: torch.Tensor | None = None,
                   final_state: torch.Tensor | None = None,
                   state_slots: torch.Tensor | None = None,
-                  out: torch.Tensor | None = None) -> torch.Tensor:
+                  out: torch.Tensor | None = None,
+                  cu_seqlens_cpu: torch.Tensor | None = None) -> torch.Tensor:
     """Chunk-64 KDA prefill over a packed batch.
 
     q, k, v, g: [total, H, 128] (rows may be strided views of a wider
-    buffer); beta: [total, H]; cu_seqlens: int32 [N+1] on the device.
-    initial_state / final_state: fp32 [slots, H, 128, 128] or None, indexed
-    by ``state_slots`` (default: sequence index); they may be the same tensor.
+    buffer); beta: [total, H]; cu_seqlens: int32 [N+1] (copied to the device
+    if needed).  initial_state / final_state: fp32 [slots, H, 128, 128] or
+    None, indexed by ``state_slots`` (default: sequence index); they may be
+    the same tensor.  ``cu_seqlens_cpu`` (FlashKDA's name; default: cu_seqlens
+    itself when it lives on the host) lets the launch be planned from the
+    sequence lengths; results are the same without it.
     Returns o [total, H, 128] in q.dtype.
     """
     for t, name in ((q, "q"), (k, "k"), (v, "v"), (g, "g"), (beta, "beta")):
@@ -200,10 +204,17 @@ def kda_chunk_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
         raise RuntimeError("q, k, v and g must have the same number of tokens")
     gs = _heads_rows(g, "g", heads, HEAD_DIM)
     bs = _rows(beta, "beta", heads)
+    if cu_seqlens_cpu is None and not cu_seqlens.is_cuda:
+        cu_seqlens_cpu = cu_seqlens
     cu = _int32(cu_seqlens, "cu_seqlens", device)
     n = int(cu.numel()) - 1
     if n < 1:
         raise RuntimeError("cu_seqlens must hold at least one sequence")
+    cu_host = None
+    if cu_seqlens_cpu is not None:
+        cu_host = torch.as_tensor(cu_seqlens_cpu).to(dtype=torch.int32).contiguous()
+        if cu_host.is_cuda or int(cu_host.numel()) != n + 1:
+            raise RuntimeError("cu_seqlens_cpu must be a host copy of cu_seqlens")
     _state(initial_state, "initial_state", heads, device)
     _state(final_state, "final_state", heads, device)
     n_slots = [int(t.size(0)) for t in (initial_state, final_state) if t is not None]
@@ -226,7 +237,8 @@ def kda_chunk_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
         nat.ptr(q), nat.ptr(k), nat.ptr(v), qs, nat.dtype_code(q.dtype), nat.ptr(g), gs,
         nat.dtype_code(g.dtype), nat.ptr(beta), bs, nat.dtype_code(beta.dtype), nat.ptr(a_log),
         nat.ptr(dtb), float(scale), float(lower_bound),
-        _flags(use_qk_l2norm, use_gate, use_beta_sigmoid), nat.ptr(cu), n, total, heads, HEAD_DIM,
+        _flags(use_qk_l2norm, use_gate, use_beta_sigmoid), nat.ptr(cu),
+        None if cu_host is None else cu_host.data_ptr(), n, total, heads, HEAD_DIM,
         nat.ptr(initial_state), nat.ptr(final_state), n_slots, nat.ptr(slots), nat.ptr(o), os_,
         ws_addr, ws_bytes, nat.stream_handle(device))
     nat.check(rc, "sophia_kda_chunk_fwd")
@@ -310,6 +322,8 @@ def chunk_kda(q, k, v, g, beta, *, scale=None, initial_state=None, output_final_
     if cu_seqlens is not None:
         if bsz != 1:
             raise RuntimeError("varlen chunk_kda needs a packed batch of size 1")
+        if cu_seqlens_cpu is None and not cu_seqlens.is_cuda:
+            cu_seqlens_cpu = cu_seqlens
         cu = cu_seqlens.to(device=q.device, dtype=torch.int32).contiguous()
     else:
         cu = cu_for_batch(bsz, seqlen, q.device)
@@ -330,7 +344,7 @@ def chunk_kda(q, k, v, g, beta, *, scale=None, initial_state=None, output_final_
                       A_log=A_log, dt_bias=dt_bias, scale=scale, lower_bound=lb,
                       use_qk_l2norm=use_qk_l2norm_in_kernel, use_gate=use_gate_in_kernel,
                       use_beta_sigmoid=use_beta_sigmoid_in_kernel, initial_state=h0,
-                      final_state=ht)
+                      final_state=ht, cu_seqlens_cpu=cu_seqlens_cpu)
     return o.view(bsz, seqlen, heads, HEAD_DIM), ht
 
 

@@ -78,9 +78,15 @@ def test_host_side_queries_and_validation():
     assert rc == nat.SOPHIA_ERR_INVALID
     assert "channels" in nat.last_error()
     rc = lib.sophia_kda_chunk_fwd(None, None, None, 2048, 1, None, 2048, 0, None, 16, 0, None,
-                                  None, 1.0, -6.0, 7, None, 1, 0, 16, 128, None, None, 0, None,
-                                  None, 2048, None, 0, None)
+                                  None, 1.0, -6.0, 7, None, None, 1, 0, 16, 128, None, None, 0,
+                                  None, None, 2048, None, 0, None)
     assert rc == nat.SOPHIA_ERR_INVALID
+    # A host copy of the offsets that is not non-decreasing within [0, total].
+    host = (ctypes.c_int32 * 3)(0, 70, 40)
+    rc = lib.sophia_kda_chunk_fwd(16, 32, 48, 2048, 1, 64, 2048, 0, 80, 16, 0, None, None, 1.0,
+                                  -5.0, 1, 96, ctypes.addressof(host), 2, 100, 16, 128, None,
+                                  None, 0, None, 256, 2048, 512, 1 << 30, None)
+    assert rc == nat.SOPHIA_ERR_INVALID and "cu_seqlens_host" in nat.last_error()
     # Decoder kernels: dim not a multiple of 8, too deep, too wide, misaligned.
     mix = lambda *a: lib.sophia_attn_res_mix(*a)  # noqa: E731
     rc = mix(None, 1536, None, 0, None, 0, None, 0, 0, 0, None, None, 1e-5, None, 1e-5, None,

@@ -280,6 +280,28 @@ def test_chunk_prefill_row_layouts_agree():
     assert _rel(outs[0][0], o_ref) < REL_TOL and _rel(outs[0][1], h_ref) < REL_TOL
 
 
+@pytest.mark.parametrize("lens", [[64, 130, 2000, 1, 0, 700, 63, 200], [256] * 8])
+def test_chunk_prefill_host_offsets_only_shape_the_launch(lens):
+    """A host copy of cu_seqlens changes the scan's launch (longest sequences
+    first; twice the work-groups per (sequence, head) for the ragged batch)
+    but not a single bit of the results."""
+    from sophia_amd import ops
+    dev = _dev()
+    rng = np.random.default_rng(13)
+    cu = _cu(lens)
+    total, heads = int(cu[-1]), 16
+    q, k, v, g, beta, a_log, dtb = _kda_inputs(rng, total, heads)
+    bf = lambda a: torch.tensor(a).to(torch.bfloat16).to(dev)
+    args = (bf(q), bf(k), bf(v), torch.tensor(g, device=dev), torch.tensor(beta, device=dev))
+    runs = []
+    for host in (None, torch.tensor(cu, dtype=torch.int32)):
+        st = torch.zeros((len(lens), heads, 128, 128), device=dev)
+        o = ops.kda_chunk_fwd(*args, torch.tensor(cu, device=dev), A_log=torch.tensor(a_log),
+                              dt_bias=torch.tensor(dtb), final_state=st, cu_seqlens_cpu=host)
+        runs.append((_np(o), _np(st)))
+    assert np.array_equal(runs[0][0], runs[1][0]) and np.array_equal(runs[0][1], runs[1][1])
+
+
 def test_chunk_prefill_is_deterministic():
     dev = _dev()
     runs = [_chunk_case(dev, [70, 5, 130], 2, qkv_dtype=torch.bfloat16, gate_in_kernel=True,
