@@ -696,7 +696,7 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
 // ---- scan kernel -------------------------------------------------------------
 // Batches of at most kOrderMax sequences whose offsets the host also holds are
 // scanned longest sequence first.
-constexpr int kOrderMax = 64;
+constexpr int kOrderMax = 16;
 struct ScanArgs {
   const int32_t *cu;
   int n_seqs;
@@ -712,8 +712,11 @@ struct ScanArgs {
   int64_t o_stride;
   int splits;   // blocks per (sequence, head): 128 / NVB
   void *trash;  // kTrashBytes of workspace: destination of rows past a sequence end
-  int ordered;  // 1: the work-groups take the sequences in the order of `order`
-  uint8_t order[kOrderMax];
+  // Sequence taken by the work-groups of rank r < kOrderMax: 4-bit field r
+  // (r itself from kOrderMax on).  Packed into one argument and extracted
+  // arithmetically: an indexed load here (even a scalar one) changes the
+  // registers the compiler gives the rings, and its wait counts drain them.
+  uint64_t order_bits;
 };
 
 // ---- scan kernel: two roles per work-group ----------------------------------
@@ -927,7 +930,11 @@ __device__ __forceinline__ void scan_item(const ScanArgs &p, int s, int first, i
   g.nt0 = half * NT;
   g.seq_a = iclamp64(p.cu[s], 0, p.total);
   g.seq_b = iclamp64(p.cu[s + 1], g.seq_a, p.total);
-  g.nchunks = static_cast<int>(imin64((g.seq_b - g.seq_a + kC - 1) / kC, p.max_ch - first));
+  // Wave-uniform by construction; readfirstlane makes the compiler see it, so
+  // that the per-chunk `live` tests below are scalar branches (a store under a
+  // divergent branch makes the compiler drain the ring loads at the join).
+  g.nchunks = __builtin_amdgcn_readfirstlane(
+      static_cast<int>(imin64((g.seq_b - g.seq_a + kC - 1) / kC, p.max_ch - first)));
   g.rec0 = p.records + (static_cast<size_t>(first) * p.num_heads + h) * kRecBytes;
   g.rec_stride = static_cast<size_t>(p.num_heads) * kRecBytes;
   const int nchunks = g.nchunks;
@@ -1033,7 +1040,7 @@ __global__ __launch_bounds__(kScanThreads) void kda_chunk_scan_kernel(ScanArgs p
   const int h = sh % p.num_heads;
   const int rank = sh / p.num_heads;
   if (rank >= p.n_seqs) return;
-  const int s = p.ordered ? p.order[rank] : rank;
+  const int s = rank < kOrderMax ? static_cast<int>((p.order_bits >> (4 * rank)) & 15u) : rank;
   scan_item<NVB, O_DT>(p, s, first_chunk(p.cu, p.n_seqs, p.total, s), h, half, sSb, sUb);
 }
 
@@ -1165,14 +1172,14 @@ extern "C" int sophia_kda_chunk_fwd(const void *q, const void *k, const void *v,
   while (splits < 8 && pairs * splits * 2 <= static_cast<int64_t>(cus)) splits *= 2;
   ScanArgs sa{cu_seqlens, n_seqs, total_tokens, num_heads, max_ch, records,
               initial_state, final_state, n_state_slots, state_slots, o, o_row_stride, splits, trash,
-              0, {}};
+              0xfedcba9876543210ull};
   if (cu_seqlens_host) {
     // The host copy of the offsets only shapes the launch; the results do not
     // depend on it.  A batch whose longest sequence has at least twice the
     // mean number of chunks spends most of its scan on a few sequential
     // chains: twice the work-groups per (sequence, head) shortens those
     // chains, and the shorter sequences queue behind them (one MI355X, the 8
-    // sequences of U[256, 4096] tokens: 118 -> 99 us).  Up to kOrderMax
+    // sequences of U[256, 4096] tokens: 117 -> 98 us).  Up to kOrderMax
     // sequences are taken longest first, so the queue holds the short ones.
     int64_t nmax = 0, sum = 0;
     int64_t chunks[kOrderMax];
@@ -1185,10 +1192,11 @@ extern "C" int sophia_kda_chunk_fwd(const void *q, const void *k, const void *v,
     if (splits < 8 && nmax * n_seqs >= 2 * sum && sum > 0) splits *= 2;
     sa.splits = splits;
     if (n_seqs <= kOrderMax) {
-      for (int i = 0; i < n_seqs; ++i) sa.order[i] = static_cast<uint8_t>(i);
-      std::stable_sort(sa.order, sa.order + n_seqs,
-                       [&](uint8_t a, uint8_t b) { return chunks[a] > chunks[b]; });
-      sa.ordered = 1;
+      int order[kOrderMax];
+      for (int i = 0; i < n_seqs; ++i) order[i] = i;
+      std::stable_sort(order, order + n_seqs, [&](int a, int b) { return chunks[a] > chunks[b]; });
+      for (int r = 0; r < n_seqs; ++r)
+        sa.order_bits = (sa.order_bits & ~(15ull << (4 * r))) | (static_cast<uint64_t>(order[r]) << (4 * r));
     }
   }
   const int64_t groups = (pairs + 7) / 8;
