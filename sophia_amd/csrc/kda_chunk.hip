@@ -156,7 +156,6 @@ __device__ __forceinline__ int first_chunk(const int32_t *cu, int n, int64_t tot
 //  A: key-side rows KD (6 copies)   bf16  [96][136]           steps 4-5
 //     -> beta K e^G, transposed     bf16  [128][64] swizzled  steps 7-8
 //  B: beta V, transposed            bf16  [128][64] swizzled  steps 1-8
-//     -> -W rows                    bf16  [64][136]           steps 9-10
 //  C: Kbar, transposed              bf16  [128][64] swizzled  steps 4-4b
 //     -> A_kk -> T = (I + A_kk)^-1  float [64][68]            steps 5-8
 //  D: A_qk                          bf16  [64][72]            steps 5-10
@@ -332,7 +331,6 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
   uint16_t *sKD = reinterpret_cast<uint16_t *>(smem + kSmA);
   uint16_t *sKt = reinterpret_cast<uint16_t *>(smem + kSmA);
   uint16_t *sV = reinterpret_cast<uint16_t *>(smem + kSmB);
-  uint16_t *sW = reinterpret_cast<uint16_t *>(smem + kSmB);
   uint16_t *sKb = reinterpret_cast<uint16_t *>(smem + kSmC);
   float *sT = reinterpret_cast<float *>(smem + kSmC);
   uint16_t *sQK = reinterpret_cast<uint16_t *>(smem + kSmD);
@@ -615,58 +613,78 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
   }
   lds_barrier();
 
-  // ---- 8. W = T (beta K e^G), Ut = T (beta V) for rows 16w .. 16w+15
-  f4 accW[8], accU[8];
+  // ---- 8. Ut = T (beta V) for rows 16w .. 16w+15, and W^T = (beta K e^G)^T T^T
+  //         for channels 32w .. 32w+31 and all 64 rows.  A C tile of W^T (rows =
+  //         channels 16mb + 4gq + e, column = chunk row 16nb + lr), paired with the
+  //         tile of channel block mb + 1, is the A-operand fragment of W for row
+  //         block nb and K-step mb / 2: -W goes to the workspace from registers.
+  //         Row r of T is zero past column r (lower triangular).
+  const auto t_frag = [&](int row, int col0) {
+    const f4 t0v = *reinterpret_cast<const f4 *>(&sT[row * kLdT + col0]);
+    const f4 t1v = *reinterpret_cast<const f4 *>(&sT[row * kLdT + col0 + 4]);
+    float ta[8];
 #pragma unroll
-  for (int nt = 0; nt < 8; ++nt) accW[nt] = accU[nt] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < 4; ++i) {
+      ta[i] = t0v[i];
+      ta[4 + i] = t1v[i];
+    }
+    return pack8(ta);
+  };
+  f4 accU[8];
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) accU[nt] = f4{0.f, 0.f, 0.f, 0.f};
   {
-    const int nks = (w < 2) ? 1 : 2;   // T is lower triangular
+    const int nks = (w < 2) ? 1 : 2;
     for (int ks = 0; ks < nks; ++ks) {
-      const float *tr = &sT[(16 * w + lr) * kLdT + 32 * ks + 8 * gq];
-      float ta[8];
-      const f4 t0v = *reinterpret_cast<const f4 *>(tr);
-      const f4 t1v = *reinterpret_cast<const f4 *>(tr + 4);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        ta[i] = t0v[i];
-        ta[4 + i] = t1v[i];
-      }
-      const bf8 af = pack8(ta);
+      const bf8 af = t_frag(16 * w + lr, 32 * ks + 8 * gq);
 #pragma unroll
       for (int nt = 0; nt < 8; ++nt) {
-        const int ch = 16 * nt + lr;
-        const bf8 bk = bits_to_bf8(*reinterpret_cast<const u4 *>(&sKt[swz(ch, 32 * ks + 8 * gq)]));
-        const bf8 bv = bits_to_bf8(*reinterpret_cast<const u4 *>(&sV[swz(ch, 32 * ks + 8 * gq)]));
-        accW[nt] = mfma32(af, bk, accW[nt]);
+        const bf8 bv = bits_to_bf8(*reinterpret_cast<const u4 *>(&sV[swz(16 * nt + lr, 32 * ks + 8 * gq)]));
         accU[nt] = mfma32(af, bv, accU[nt]);
       }
     }
   }
-  lds_barrier();   // regions A and B are rewritten below
-
-  // ---- 9. Ut in C-tile order to the workspace; -W rows to region B; e^{G_C}.
+  f4 accW[2][4];  // [channel block 2w + mi][row block nb]
+  {
+    bf8 kta[2][2];  // (beta K e^G)^T, A operand: m = channels 16(2w + mi) + lr
 #pragma unroll
-  for (int nt = 0; nt < 8; ++nt) {
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        kta[mi][ks] = bits_to_bf8(*reinterpret_cast<const u4 *>(&sKt[swz(16 * (2 * w + mi) + lr, 32 * ks + 8 * gq)]));
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      accW[0][nb] = accW[1][nb] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < (nb < 2 ? 1 : 2); ++ks) {
+        const bf8 tb = t_frag(16 * nb + lr, 32 * ks + 8 * gq);
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi) accW[mi][nb] = mfma32(kta[mi][ks], tb, accW[mi][nb]);
+      }
+    }
+  }
+
+  // ---- 9. Ut in C-tile order and -W as A-operand fragments (m = chunk rows
+  //         16nb + lr, k = channels perm_k(w, gq, .)) to the workspace; e^{G_C}.
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt)
     *reinterpret_cast<u2 *>(rec + kOffU + ((w * 8 + nt) * 64 + l) * 8) = pack4_bf16(accU[nt]);
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      sW[(16 * w + 4 * gq + e) * kLdKD + 16 * nt + lr] = f32_to_bf16_bits(-accW[nt][e]);
+  for (int nb = 0; nb < 4; ++nb) {
+    float t[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      t[e] = -accW[0][nb][e];
+      t[4 + e] = -accW[1][nb][e];
+    }
+    *reinterpret_cast<u4 *>(rec + kOffW + ((nb * 4 + w) * 64 + l) * 16) = bf8_to_bits(pack8(t));
   }
   if (tid < kD) {
     const f4 E = *reinterpret_cast<const f4 *>(&s_E[tid * 4]);
     reinterpret_cast<float *>(rec + kOffG)[tid] = E[0] * E[1] * E[2] * E[3];
   }
-  lds_barrier();
 
-  // ---- 10. A-operand fragments from LDS to the workspace
-  // -W: m = chunk rows 16w + lr, k = channels perm_k(ks, gq, .)
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    const uint16_t *src = &sW[(16 * w + lr) * kLdKD + 32 * ks + 4 * gq];
-    const u2 lo = *reinterpret_cast<const u2 *>(src);
-    const u2 hi = *reinterpret_cast<const u2 *>(src + 16);
-    *reinterpret_cast<u4 *>(rec + kOffW + ((w * 4 + ks) * 64 + l) * 16) = u4{lo.x, lo.y, hi.x, hi.y};
-  }
+  // ---- 10. A_qk fragments from LDS to the workspace
   // A_qk: m = chunk rows 16w + lr, k = chunk rows perm_k(ks, gq, .)
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
