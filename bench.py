@@ -13,7 +13,7 @@ the GPU's wait for the host to issue each call).
 Also reported: the batch-256 decode step (fp32 state N(0, 0.02), one bf16
 token per sequence) in microseconds and HBM GB/s (launched eagerly and as
 HIP-graph replays of 10 steps; the faster is the headline figure), the ShortConv prefill over
-the same packed batch, and the CPU baseline (the C restatement of the
+the same packed batch (timed the same two ways), and the CPU baseline (the C restatement of the
 reference's per-token recurrence, timed on this host's cores).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
@@ -66,6 +66,24 @@ def make_prefill_inputs(torch, dev, lengths, seed=1):
     inputs = {name: t.to(dev) for name, t in dict(q=q, k=k, v=v, g=g, beta=beta, cu=cu).items()}
     inputs["cu_cpu"] = cu  # the host copy of the offsets (FlashKDA's cu_seqlens_cpu)
     return inputs
+
+
+def graph_ms_per_call(torch, dev, fn, replays: int, stream, per_graph: int = 10) -> float:
+    """Average duration (ms) of one call of `fn` when `per_graph` calls are
+    captured in a HIP graph (after a warm-up on the capture stream) and the
+    graph is replayed: the events then bracket the kernels alone."""
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream(dev).wait_stream(side)
+    with torch.cuda.graph(graph, stream=side):
+        for _ in range(per_graph):
+            fn()
+    _, per = time_events(torch, graph.replay, replays, 2, stream)
+    del graph
+    return float(np.mean(per)) / per_graph
 
 
 def time_events(torch, fn, steps: int, warmup: int, stream) -> tuple[float, list[float]]:
@@ -291,23 +309,10 @@ def main(argv=None) -> int:
     eager_ms = float(np.mean(per))
     graph_ms = eager_ms
     if run_prefill:
-        # The same calls captured in a HIP graph (10 per graph) and replayed:
-        # the events then bracket the kernels alone, without the host's time
-        # to issue each call (which the eager events include when the GPU
-        # waits for it).
-        per_graph = 10
-        graph = torch.cuda.CUDAGraph()
-        side = torch.cuda.Stream(dev)
-        side.wait_stream(torch.cuda.current_stream(dev))
-        with torch.cuda.stream(side):
-            prefill()
-        torch.cuda.current_stream(dev).wait_stream(side)
-        with torch.cuda.graph(graph, stream=side):
-            for _ in range(per_graph):
-                prefill()
-        _, gper = time_events(torch, graph.replay, max(args.steps // 2, 5), 2, stream)
-        graph_ms = float(np.mean(gper)) / per_graph
-        del graph
+        # The same calls as replays of a HIP graph: the events then bracket the
+        # kernels alone, without the host's time to issue each call (which the
+        # eager events include when the GPU waits for it).
+        graph_ms = graph_ms_per_call(torch, dev, prefill, max(args.steps // 2, 5), stream)
     avg_ms = min(eager_ms, graph_ms)
     tokens_per_s = total / (avg_ms / 1e3)
     achieved_gbs = total * PREFILL_BYTES_PER_TOKEN / (avg_ms / 1e3) / 1e9
@@ -356,9 +361,12 @@ def main(argv=None) -> int:
 
     if args.only in ("all", "kda", "conv"):
         _, cper = time_events(torch, conv, args.steps, args.warmup, stream)
-        cms = float(np.mean(cper))
+        ceager = float(np.mean(cper))
+        cgraph = graph_ms_per_call(torch, dev, conv, max(args.steps // 2, 5), stream)
+        cms = min(ceager, cgraph)
         cbytes = total * 3 * HEADS * DIM * 2 * 2
-        result["short_conv"] = {"us": round(cms * 1e3, 2),
+        result["short_conv"] = {"us": round(cms * 1e3, 2), "us_eager": round(ceager * 1e3, 2),
+                                "us_graph": round(cgraph * 1e3, 2),
                                 "GBps": round(cbytes / (cms / 1e3) / 1e9, 1),
                                 "algorithmic_bytes": cbytes,
                                 "traffic": MEASURED_TRAFFIC_BYTES["short_conv"]}
@@ -384,21 +392,9 @@ def main(argv=None) -> int:
         dsteps = max(args.steps * 5, 50)
         _, dper = time_events(torch, decode, dsteps, args.warmup * 2, stream)
         eager_ms = float(np.mean(dper))
-        # The same steps as a serving loop runs them: captured in a HIP graph
-        # (10 steps per graph), timed per replay.
-        per_graph = 10
-        graph = torch.cuda.CUDAGraph()
-        side = torch.cuda.Stream(dev)
-        side.wait_stream(torch.cuda.current_stream(dev))
-        with torch.cuda.stream(side):
-            decode()
-        torch.cuda.current_stream(dev).wait_stream(side)
-        with torch.cuda.graph(graph, stream=side):
-            for _ in range(per_graph):
-                decode()
-        _, gper = time_events(torch, graph.replay, max(dsteps // per_graph, 5), 2, stream)
-        graph_ms = float(np.mean(gper)) / per_graph
-        del graph
+        # The same steps as a serving loop runs them: replays of a HIP graph of
+        # 10 steps.
+        graph_ms = graph_ms_per_call(torch, dev, decode, max(dsteps // 10, 5), stream)
         dms = min(eager_ms, graph_ms)
         dbytes = (2 * batch * HEADS * DIM * DIM * 4
                   + batch * HEADS * (3 * DIM * 2 + DIM * 4 + 4 + DIM * 2))

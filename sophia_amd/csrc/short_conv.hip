@@ -41,12 +41,15 @@ struct Vec8 {
       }
     }
   }
+  // Outputs are written once and not read back by this kernel: non-temporal
+  // stores (64 -> 74 us on the benchmark batch with ordinary stores).  The
+  // window loads stay ordinary: neighbouring row tiles re-read 3 rows each.
   __device__ __forceinline__ void store(void *base, int64_t idx) const {
     if constexpr (DT == SOPHIA_DTYPE_BF16) {
       u4 w;
 #pragma unroll
       for (int i = 0; i < 4; ++i) w[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
-      *reinterpret_cast<u4 *>(static_cast<uint16_t *>(base) + idx) = w;
+      __builtin_nontemporal_store(w, reinterpret_cast<u4 *>(static_cast<uint16_t *>(base) + idx));
     } else {
       f4 *p = reinterpret_cast<f4 *>(static_cast<float *>(base) + idx);
       f4 a, b;
@@ -55,8 +58,8 @@ struct Vec8 {
         a[i] = v[i];
         b[i] = v[4 + i];
       }
-      p[0] = a;
-      p[1] = b;
+      __builtin_nontemporal_store(a, p);
+      __builtin_nontemporal_store(b, p + 1);
     }
   }
   __device__ __forceinline__ void zero() {
