@@ -153,7 +153,8 @@ __device__ __forceinline__ int first_chunk(const int32_t *cu, int n, int64_t tot
 // ---- intra-chunk kernel ----------------------------------------------------
 // Record writes use non-temporal stores: the records are read back only by the
 // scan kernel, which then runs 99 -> 85 us on the 8-sequence benchmark batch
-// (and this kernel 119 -> 116 us).
+// (and this kernel 119 -> 116 us).  The inputs are read once, also with the
+// non-temporal hint (~1 %).
 // LDS regions (bytes).  Lifetimes (steps below) let regions A and B be reused.
 //  E: e^{sub-block totals}          float [128][4]           steps 3-8
 //  A: key-side rows KD (6 copies)   bf16  [96][136]           steps 4-5
@@ -238,7 +239,7 @@ template <>
 struct Raw4<SOPHIA_DTYPE_F32> {
   f4 w;
   __device__ __forceinline__ void load(const void *base, int64_t idx) {
-    w = *reinterpret_cast<const f4 *>(static_cast<const float *>(base) + idx);
+    w = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(static_cast<const float *>(base) + idx));
   }
   __device__ __forceinline__ f4 get() const { return w; }
 };
@@ -397,10 +398,10 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
         const int64_t rt = 16 * w + r < len ? t0 + 16 * w + r : t0;
         const int64_t off = rt * p.qkv_stride + static_cast<int64_t>(h) * kD + 8 * ((l & 15) ^ r);
         const int dst = w * 4096 + t * 1024;
-        __builtin_amdgcn_global_load_lds(static_cast<const uint16_t *>(p.q) + off, smem + kSmA + dst, 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(static_cast<const uint16_t *>(p.k) + off, smem + kSmC + dst, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(static_cast<const uint16_t *>(p.q) + off, smem + kSmA + dst, 16, 0, 2);
+        __builtin_amdgcn_global_load_lds(static_cast<const uint16_t *>(p.k) + off, smem + kSmC + dst, 16, 0, 2);
         __builtin_amdgcn_global_load_lds(static_cast<const uint16_t *>(p.v) + off, smem + stage_v(w) + t * 1024, 16,
-                                         0, 0);
+                                         0, 2);
       }
     } else {
 #pragma unroll
