@@ -18,11 +18,11 @@
 // the diagonal sub-blocks: finite in fp32 and bf16 for g >= -5.
 //
 // Two kernels:
-//  * kda_chunk_intra_kernel (grid: chunk x head, 256 threads): everything that
-//    does not depend on S0.  Writes, per (chunk, head), the MFMA operand
-//    fragments -W, Q e^G, (K e^{G_C-G})^T, A_qk (bf16, in the exact per-lane
-//    order of v_mfma_f32_16x16x32_bf16 A operands), Ut (bf16, C-tile order)
-//    and e^{G_C} (fp32) to the workspace.
+//  * kda_chunk_intra_kernel (one 256-thread work-group per (chunk, head),
+//    heads fastest): everything that does not depend on S0.  Writes, per
+//    (chunk, head), the MFMA operand fragments -W, Q e^G, (K e^{G_C-G})^T,
+//    A_qk (bf16, in the exact per-lane order of v_mfma_f32_16x16x32_bf16 A
+//    operands), Ut (bf16, C-tile order) and e^{G_C} (fp32) to the workspace.
 //  * kda_chunk_scan_kernel (one work-group of 8 wavefronts per sequence x
 //    head x 128/splits value columns): walks the chunks of its sequence.  Four
 //    wavefronts hold the fp32 state in MFMA accumulator tiles and update it;
@@ -1185,7 +1185,7 @@ extern "C" int sophia_kda_chunk_fwd(const void *q, const void *k, const void *v,
   // many as keep every work-group resident at once (one per CU: its 8
   // wavefronts hold rings of record buffers and fill half of each SIMD's
   // register file), so a small batch still spreads its critical path over
-  // the chip.
+  // the chip.  The host copy of the offsets can double that (below).
   int device = 0, cus = 256;
   if (hipGetDevice(&device) == hipSuccess)
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) cus = 256;
@@ -1201,7 +1201,8 @@ extern "C" int sophia_kda_chunk_fwd(const void *q, const void *k, const void *v,
     // mean number of chunks spends most of its scan on a few sequential
     // chains: twice the work-groups per (sequence, head) shortens those
     // chains, and the shorter sequences queue behind them (one MI355X, the 8
-    // sequences of U[256, 4096] tokens: 117 -> 98 us).  Up to kOrderMax
+    // sequences of U[256, 4096] tokens: 117 -> 98 us; with 8 work-groups
+    // per (sequence, head) instead, 131 us).  Up to kOrderMax
     // sequences are taken longest first, so the queue holds the short ones.
     int64_t nmax = 0, sum = 0;
     int64_t chunks[kOrderMax];
