@@ -9,11 +9,15 @@
 // so that one pass over S yields both reductions and the new state).
 //
 // HBM-bound: the state is 64 KiB per (sequence, head) and is read once and
-// written once, in place.  One 256-thread work-group owns one (sequence,
-// head): thread t holds columns 4*(t%32) .. +3 of rows (t/32) + 8*r,
-// r = 0..15, so each wavefront load/store instruction moves two adjacent
-// 512-byte rows.  The two column reductions go through the wavefront
-// halves (xor-32 shuffle) and 4 x 128 floats of LDS.
+// written once, in place.  Its value columns are independent, so two
+// 256-thread work-groups share one (sequence, head), 64 columns each (32 KiB
+// of state; 94 us instead of 97 us for the B = 256 step with one work-group
+// of 128 columns, 99 us with four of 32: shorter work-groups drain the grid's
+// tail sooner, and 68 instead of 96 VGPRs keep more of them resident).
+// Thread t holds columns col0 + 4*(t%16) .. +3 of rows (t/16) + 16*r,
+// r = 0..7, so each wavefront load/store instruction moves four 256-byte row
+// pieces.  The two column reductions go through the wavefront (xor-16 and
+// xor-32 shuffles) and 4 x 64 floats of LDS.
 #include "common.hpp"
 
 namespace sophia {
@@ -21,12 +25,12 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kThreads = 256;
-constexpr int kRowsPerThread = kD / 8;
+constexpr int kDecodeCols = 64;   // value columns per work-group
 
 // Dtypes and the gate switch are template parameters so that the load batch
 // below has no branches: the wave then waits for the token inputs alone
 // (issued first) before the prologue, while the state is still in flight.
-template <int QKV_DT, int G_DT, int B_DT, bool GATE>
+template <int QKV_DT, int G_DT, int B_DT, bool GATE, int NC>
 __global__ __launch_bounds__(kThreads) void kda_decode_kernel(
     const void *__restrict__ q, const void *__restrict__ k, const void *__restrict__ v,
     int64_t qkv_stride, const void *__restrict__ g, int64_t g_stride,
@@ -34,23 +38,27 @@ __global__ __launch_bounds__(kThreads) void kda_decode_kernel(
     const float *__restrict__ A_log, const float *__restrict__ dt_bias, float scale, float lb,
     unsigned flags, float *__restrict__ state, int n_slots, const int32_t *__restrict__ slots,
     int read_state, int num_heads, void *__restrict__ o, int64_t o_stride) {
-  const int h = blockIdx.x;
+  constexpr int CG = NC / 4;           // column groups of 4 columns
+  constexpr int RG = kThreads / CG;    // row groups
+  constexpr int RPT = kD / RG;         // rows per thread
+  const int h = blockIdx.x / (kD / NC);
+  const int col0 = (blockIdx.x % (kD / NC)) * NC;
   const int b = blockIdx.y;
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = t >> 6;
-  const int cg = t & 31;         // column group: columns 4cg .. 4cg+3
-  const int rg = t >> 5;         // row group: rows rg + 8r
+  const int cg = t % CG;         // column group: columns col0 + 4cg .. +3
+  const int rg = t / CG;         // row group: rows rg + RG r
 
   __shared__ float s_q[kD], s_k[kD], s_a[kThreads], s_v[kThreads];
   __shared__ float s_red[4][3];
-  __shared__ float s_p[4][kD], s_r[4][kD];
-  __shared__ float s_u[kD];
+  __shared__ float s_p[4][NC], s_r[4][NC];
+  __shared__ float s_u[NC];
 
   const int slot = slots ? slots[b] : b;
   if (slot < 0 || slot >= n_slots) {  // no cache slot: output 0, no state touched
-    if (t < kD)
-      store_elem(o, static_cast<int64_t>(b) * o_stride + static_cast<int64_t>(h) * kD + t,
+    if (t < NC)
+      store_elem(o, static_cast<int64_t>(b) * o_stride + static_cast<int64_t>(h) * kD + col0 + t,
                  QKV_DT, 0.f);
     return;
   }
@@ -78,10 +86,10 @@ __global__ __launch_bounds__(kThreads) void kda_decode_kernel(
   // The state is loaded unconditionally (a branch here would make the wave
   // drain every load at the join) and replaced by zeros afterwards when the
   // incoming state is to be ignored.
-  f4 st[kRowsPerThread];
+  f4 st[RPT];
 #pragma unroll
-  for (int r = 0; r < kRowsPerThread; ++r)
-    st[r] = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(S + (rg + 8 * r) * kD + 4 * cg));
+  for (int r = 0; r < RPT; ++r)
+    st[r] = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(S + (rg + RG * r) * kD + col0 + 4 * cg));
   __builtin_amdgcn_sched_barrier(0);
 
   // Token prologue: threads 0..127 own one key/value channel each.
@@ -121,25 +129,27 @@ __global__ __launch_bounds__(kThreads) void kda_decode_kernel(
 
   if (!read_state) {
 #pragma unroll
-    for (int r = 0; r < kRowsPerThread; ++r) st[r] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int r = 0; r < RPT; ++r) st[r] = f4{0.f, 0.f, 0.f, 0.f};
   }
 
   // Decay the held rows and form the two partial column reductions.
   f4 p = {0.f, 0.f, 0.f, 0.f}, rq = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int r = 0; r < kRowsPerThread; ++r) {
-    const int i = rg + 8 * r;
+  for (int r = 0; r < RPT; ++r) {
+    const int i = rg + RG * r;
     const float a = s_a[i];
     st[r] *= a;
     p += s_k[i] * st[r];
     rq += s_q[i] * st[r];
   }
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    p[c] += __shfl_xor(p[c], 32, 64);
-    rq[c] += __shfl_xor(rq[c], 32, 64);
-  }
-  if ((lane & 32) == 0) {
+  for (int m = CG; m < 64; m *= 2)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      p[c] += __shfl_xor(p[c], m, 64);
+      rq[c] += __shfl_xor(rq[c], m, 64);
+    }
+  if (lane < CG) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       s_p[wave][4 * cg + c] = p[c];
@@ -147,21 +157,21 @@ __global__ __launch_bounds__(kThreads) void kda_decode_kernel(
     }
   }
   lds_barrier();
-  if (t < kD) {
+  if (t < NC) {
     const float pj = s_p[0][t] + s_p[1][t] + s_p[2][t] + s_p[3][t];
     const float rj = s_r[0][t] + s_r[1][t] + s_r[2][t] + s_r[3][t];
-    const float u = bt * (s_v[t] - pj);
+    const float u = bt * (s_v[col0 + t] - pj);
     s_u[t] = u;
-    store_elem(o, static_cast<int64_t>(b) * o_stride + static_cast<int64_t>(h) * kD + t, QKV_DT,
+    store_elem(o, static_cast<int64_t>(b) * o_stride + static_cast<int64_t>(h) * kD + col0 + t, QKV_DT,
                rj + qk * u);
   }
   lds_barrier();
   const f4 u4v = *reinterpret_cast<const f4 *>(&s_u[4 * cg]);
 #pragma unroll
-  for (int r = 0; r < kRowsPerThread; ++r) {
-    const int i = rg + 8 * r;
+  for (int r = 0; r < RPT; ++r) {
+    const int i = rg + RG * r;
     f4 nv = st[r] + s_k[i] * u4v;
-    __builtin_nontemporal_store(nv, reinterpret_cast<f4 *>(S + i * kD + 4 * cg));
+    __builtin_nontemporal_store(nv, reinterpret_cast<f4 *>(S + i * kD + col0 + 4 * cg));
   }
 }
 
@@ -196,14 +206,14 @@ extern "C" int sophia_kda_decode_step(const void *q, const void *k, const void *
                  "kda_decode_step: row stride smaller than a row");
   SOPHIA_REQUIRE(((uintptr_t)state % 16) == 0, "kda_decode_step: state must be 16-byte aligned");
   SOPHIA_REQUIRE(n_state_slots >= 0, "kda_decode_step: n_state_slots must be >= 0");
-  dim3 grid(num_heads, batch);
+  dim3 grid(num_heads * (kD / kDecodeCols), batch);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool gate = (flags & SOPHIA_KDA_GATE_IN_KERNEL) != 0;
   const int key = (qkv_dtype == SOPHIA_DTYPE_BF16) * 8 + (g_dtype == SOPHIA_DTYPE_BF16) * 4 +
                   (beta_dtype == SOPHIA_DTYPE_BF16) * 2 + (gate ? 1 : 0);
 #define SOPHIA_DECODE_CASE(KEY, QD, GD, BD, GT)                                                  \
   case KEY:                                                                                      \
-    hipLaunchKernelGGL((kda_decode_kernel<QD, GD, BD, GT>), grid, dim3(kThreads), 0, st, q, k, v, \
+    hipLaunchKernelGGL((kda_decode_kernel<QD, GD, BD, GT, kDecodeCols>), grid, dim3(kThreads), 0, st, q, k, v, \
                        qkv_row_stride, g, g_row_stride, beta, beta_row_stride, A_log, dt_bias,   \
                        scale, lower_bound, flags, state, n_state_slots, state_slots, read_state, \
                        num_heads, o, o_row_stride);                                              \
