@@ -45,7 +45,7 @@ METRIC = "KDA prefill tokens/s + % MFMA peak; decode-step µs and HBM GB/s at B=
 # HBM bytes per launch measured with rocprofv3 on this workload (FETCH_SIZE and
 # WRITE_SIZE in separate passes; FETCH_SIZE doubled, the factor a plain 1 GiB
 # device copy gives on MI355X).  Re-measured whenever a kernel changes.
-MEASURED_TRAFFIC_BYTES = {"prefill": 794.7e6, "decode": 543.5e6, "short_conv": 318.7e6}
+MEASURED_TRAFFIC_BYTES = {"prefill": 794.9e6, "decode": 548.8e6, "short_conv": 321.2e6}
 
 
 def prefill_lengths(seed: int = 0, n: int = 8, lo: int = 256, hi: int = 4096) -> list[int]:
