@@ -280,11 +280,12 @@ def test_chunk_prefill_row_layouts_agree():
     assert _rel(outs[0][0], o_ref) < REL_TOL and _rel(outs[0][1], h_ref) < REL_TOL
 
 
-@pytest.mark.parametrize("lens", [[64, 130, 2000, 1, 0, 700, 63, 200], [256] * 8])
+@pytest.mark.parametrize("lens", [[64, 130, 2000, 1, 0, 700, 63, 200], [256] * 8, [70] * 9 + [1500] + [70] * 10])
 def test_chunk_prefill_host_offsets_only_shape_the_launch(lens):
     """A host copy of cu_seqlens changes the scan's launch (longest sequences
-    first; twice the work-groups per (sequence, head) for the ragged batch)
-    but not a single bit of the results."""
+    first for up to 16 sequences; twice the work-groups per (sequence, head)
+    for a ragged batch, also past 16 sequences where the order is kept) but
+    not a single bit of the results."""
     from sophia_amd import ops
     dev = _dev()
     rng = np.random.default_rng(13)
