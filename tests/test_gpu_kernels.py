@@ -153,6 +153,66 @@ def test_decode_step_zero_initial_state():
     assert _rel(_np(state), s_ref) < 1e-4
 
 
+def test_out_of_range_slots_run_without_a_cache():
+    """A cache slot outside [0, n_state_slots) means "no cache" in every entry
+    point: a decode row writes o = 0 and touches no state; a prefill sequence
+    starts from a zero state and writes none; a conv step row reads zero
+    history and writes none.  Slots in range behave as usual."""
+    from sophia_amd import ops
+    dev = _dev()
+    rng = np.random.default_rng(21)
+    heads = 2
+    dt = lambda a: torch.tensor(a, device=dev)
+
+    # decode: 3 slots; rows 1 (slot -1) and 3 (slot 3) have none
+    q, k, v, g, beta, a_log, dtb = _kda_inputs(rng, 4, heads)
+    slots = np.array([2, -1, 0, 3], dtype=np.int32)
+    s0 = (rng.standard_normal((3, heads, 128, 128)) * 0.02).astype(np.float32)
+    state = dt(s0)
+    o = ops.kda_decode_step(dt(q), dt(k), dt(v), dt(g), dt(beta), state, A_log=torch.tensor(a_log),
+                            dt_bias=torch.tensor(dtb), state_slots=dt(slots))
+    live = np.array([0, 2])
+    o_ref, s_ref = ko.kda_decode_step(q[live], k[live], v[live], g[live], beta[live], s0[slots[live]],
+                                      A_log=a_log, dt_bias=dtb, dtype=np.float64)
+    on, st = _np(o), _np(state)
+    assert np.all(on[[1, 3]] == 0.0)
+    assert _rel(on[live], o_ref) < 1e-4
+    assert _rel(st[slots[live]], s_ref) < 1e-4
+    assert np.array_equal(st[1], s0[1])
+
+    # prefill: 2 slots; sequences 1 (slot -1) and 2 (slot 5) have none
+    lens = [70, 130, 40]
+    cu = _cu(lens)
+    q, k, v, g, beta, a_log, dtb = _kda_inputs(rng, int(cu[-1]), heads)
+    slots = np.array([1, -1, 5], dtype=np.int32)
+    h0 = (rng.standard_normal((2, heads, 128, 128)) * 0.05).astype(np.float32)
+    fin = torch.full((2, heads, 128, 128), -7.0, device=dev)
+    o = ops.kda_chunk_fwd(dt(q), dt(k), dt(v), dt(g), dt(beta), dt(cu), A_log=torch.tensor(a_log),
+                          dt_bias=torch.tensor(dtb), initial_state=dt(h0), final_state=fin,
+                          state_slots=dt(slots))
+    zero = np.zeros_like(h0[0])
+    o_ref, h_ref = c_oracle.kda_varlen(q, k, v, g, beta, cu, A_log=a_log, dt_bias=dtb,
+                                       initial_states=np.stack([h0[1], zero, zero]))
+    f = _np(fin)
+    assert _rel(_np(o), o_ref) < REL_TOL
+    assert _rel(f[1], h_ref[0]) < REL_TOL
+    assert np.all(f[0] == -7.0)
+
+    # conv step: 2 slots; rows 1 (slot -1) and 2 (slot 2) have none
+    channels, kernel = 64, 4
+    x = rng.standard_normal((3, channels)).astype(np.float32)
+    w = (rng.standard_normal((channels, kernel)) * 0.5).astype(np.float32)
+    cs0 = rng.standard_normal((2, channels, kernel - 1)).astype(np.float32)
+    cs = dt(cs0)
+    y = ops.short_conv_step(dt(x), dt(w), cs, state_slots=dt(np.array([1, -1, 2], dtype=np.int32)))
+    hist = np.stack([cs0[1], np.zeros_like(cs0[0]), np.zeros_like(cs0[0])]).astype(np.float64)
+    yr, nh = ko.short_conv(x[:, None].astype(np.float64), w.astype(np.float64), hist)
+    np.testing.assert_allclose(_np(y), yr[:, 0], rtol=1e-5, atol=1e-5)
+    cs_new = _np(cs)
+    np.testing.assert_allclose(cs_new[1], nh[0], rtol=1e-6, atol=1e-6)
+    assert np.array_equal(cs_new[0], cs0[0])
+
+
 # ------------------------------------------------------------- chunk prefill
 def _chunk_case(dev, lens, heads, *, qkv_dtype, gate_in_kernel, with_h0, seed, slots=None):
     from sophia_amd import ops
