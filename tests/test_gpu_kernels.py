@@ -212,6 +212,22 @@ def test_out_of_range_slots_run_without_a_cache():
     np.testing.assert_allclose(cs_new[1], nh[0], rtol=1e-6, atol=1e-6)
     assert np.array_equal(cs_new[0], cs0[0])
 
+    # conv over a packed batch: sequences 1 (slot -1) and 2 (slot 4) have none
+    lens = [6, 9, 2]
+    cu = _cu(lens)
+    x = rng.standard_normal((int(cu[-1]), channels)).astype(np.float32)
+    cs = dt(cs0)
+    y = ops.short_conv_fwd(dt(x), dt(w), dt(cu), conv_state=cs,
+                           state_slots=dt(np.array([1, -1, 4], dtype=np.int32)),
+                           read_history=True, write_history=True)
+    for s, (a, b) in enumerate(zip(cu[:-1], cu[1:])):
+        hist = cs0[1][None].astype(np.float64) if s == 0 else None
+        yr, nh = ko.short_conv(x[None, a:b].astype(np.float64), w.astype(np.float64), hist)
+        np.testing.assert_allclose(_np(y[a:b]), yr[0], rtol=1e-5, atol=1e-5)
+        if s == 0:
+            np.testing.assert_allclose(_np(cs)[1], nh[0], rtol=1e-6, atol=1e-6)
+    assert np.array_equal(_np(cs)[0], cs0[0])
+
 
 # ------------------------------------------------------------- chunk prefill
 def _chunk_case(dev, lens, heads, *, qkv_dtype, gate_in_kernel, with_h0, seed, slots=None):
