@@ -30,6 +30,7 @@
 //    operands (16x16x32 operands pair two C tiles; the A operands carry the
 //    matching k permutation).
 #include <algorithm>
+#include <mutex>
 
 #include "common.hpp"
 
@@ -1067,17 +1068,30 @@ __global__ __launch_bounds__(kScanThreads) void kda_chunk_scan_kernel(ScanArgs p
 }
 
 
+// Dynamic LDS above the default limit is enabled once per (kernel, device),
+// under a lock: launches may come from several host threads and devices.
+constexpr int kMaxDevices = 64;
+template <int QKV_DT, int G_DT, bool GATE>
+int ensure_intra_lds() {
+  static std::mutex mu;
+  static bool done[kMaxDevices] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return set_error(SOPHIA_ERR_HIP, "kda_chunk_fwd: hipGetDevice: %s", hipGetErrorString(e));
+  std::lock_guard<std::mutex> lock(mu);
+  if (dev >= 0 && dev < kMaxDevices && done[dev]) return SOPHIA_OK;
+  e = hipFuncSetAttribute(reinterpret_cast<const void *>(&kda_chunk_intra_kernel<QKV_DT, G_DT, GATE>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kSmIntra));
+  if (e != hipSuccess)
+    return set_error(SOPHIA_ERR_HIP, "kda_chunk_fwd: cannot set LDS size: %s", hipGetErrorString(e));
+  if (dev >= 0 && dev < kMaxDevices) done[dev] = true;
+  return SOPHIA_OK;
+}
+
 template <int QKV_DT, int G_DT, bool GATE>
 int launch_intra(dim3 grid, hipStream_t st, const IntraArgs &ia) {
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void *>(&kda_chunk_intra_kernel<QKV_DT, G_DT, GATE>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kSmIntra));
-    if (e != hipSuccess)
-      return set_error(SOPHIA_ERR_HIP, "kda_chunk_fwd: cannot set LDS size: %s", hipGetErrorString(e));
-    attr_set = true;
-  }
+  if (const int rc = ensure_intra_lds<QKV_DT, G_DT, GATE>()) return rc;
   hipLaunchKernelGGL((kda_chunk_intra_kernel<QKV_DT, G_DT, GATE>), grid, dim3(kThreads), kSmIntra, st, ia);
   return check_launch("kda_chunk_intra");
 }

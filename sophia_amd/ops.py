@@ -55,6 +55,18 @@ def _int32(t: torch.Tensor | None, name: str, device) -> torch.Tensor | None:
     return t
 
 
+def _nrows(t: torch.Tensor, name: str, expect: int) -> None:
+    """Leading (row) dimension check: a mis-sized tensor must raise here, not
+    let a kernel index past its end."""
+    if int(t.size(0)) != int(expect):
+        raise RuntimeError(f"{name} has {int(t.size(0))} rows, expected {int(expect)}")
+
+
+def _slot_count(slots: torch.Tensor | None, expect: int) -> None:
+    if slots is not None and int(slots.numel()) != int(expect):
+        raise RuntimeError(f"state_slots must hold {int(expect)} entries, got {int(slots.numel())}")
+
+
 def _workspace(nbytes: int, device) -> tuple[torch.Tensor, int, int]:
     buf = torch.empty(nbytes + 256, dtype=torch.uint8, device=device)
     addr = buf.data_ptr()
@@ -104,9 +116,13 @@ def short_conv_fwd(x: torch.Tensor, weight: torch.Tensor, cu_seqlens: torch.Tens
             raise RuntimeError(f"conv_state must be contiguous fp32 [slots, {channels}, "
                                f"{kernel - 1}], got {tuple(conv_state.shape)}")
     slots = _int32(state_slots, "state_slots", x.device)
+    _slot_count(slots, n)
     y = out if out is not None else torch.empty((x.size(0), channels), dtype=x.dtype,
                                                 device=x.device)
     ys = _rows(y, "out", channels)
+    _nrows(y, "out", int(x.size(0)))
+    if y.dtype != x.dtype:
+        raise RuntimeError("out must have x's dtype")
     rc = nat.lib().sophia_short_conv_fwd(
         nat.ptr(x), xs, nat.ptr(y), ys, nat.dtype_code(x.dtype), nat.ptr(w), nat.ptr(conv_state),
         0 if conv_state is None else int(conv_state.size(0)),
@@ -131,8 +147,14 @@ def short_conv_step(x: torch.Tensor, weight: torch.Tensor, conv_state: torch.Ten
         raise RuntimeError("conv_state must be contiguous fp32 [slots, C, K-1]")
     w = _conv_taps(weight, x, weight_rounded)
     slots = _int32(state_slots, "state_slots", x.device)
+    _slot_count(slots, int(x.size(0)))
+    if slots is None and int(conv_state.size(0)) < int(x.size(0)):
+        raise RuntimeError("conv_state has fewer slots than the batch")
     y = out if out is not None else torch.empty_like(x, memory_format=torch.contiguous_format)
     ys = _rows(y, "out", channels)
+    _nrows(y, "out", int(x.size(0)))
+    if y.dtype != x.dtype:
+        raise RuntimeError("out must have x's dtype")
     rc = nat.lib().sophia_short_conv_step(
         nat.ptr(x), xs, nat.ptr(y), ys, nat.dtype_code(x.dtype), nat.ptr(w), nat.ptr(conv_state),
         int(conv_state.size(0)), nat.ptr(slots), int(x.size(0)), channels, kernel,
@@ -204,8 +226,14 @@ def kda_chunk_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
         raise RuntimeError("q, k, v and g must have the same number of tokens")
     gs = _heads_rows(g, "g", heads, HEAD_DIM)
     bs = _rows(beta, "beta", heads)
-    if cu_seqlens_cpu is None and not cu_seqlens.is_cuda:
-        cu_seqlens_cpu = cu_seqlens
+    _nrows(beta, "beta", total)
+    if not isinstance(cu_seqlens, torch.Tensor):
+        raise RuntimeError("cu_seqlens must be a tensor")
+    if not cu_seqlens.is_cuda:
+        # A host cu_seqlens is also the host copy that plans the launch.
+        if cu_seqlens_cpu is None:
+            cu_seqlens_cpu = cu_seqlens
+        cu_seqlens = cu_seqlens.to(device=device, dtype=torch.int32).contiguous()
     cu = _int32(cu_seqlens, "cu_seqlens", device)
     n = int(cu.numel()) - 1
     if n < 1:
@@ -221,15 +249,19 @@ def kda_chunk_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
     if len(n_slots) == 2 and n_slots[0] != n_slots[1]:
         raise RuntimeError("initial_state and final_state must have the same number of slots")
     n_slots = n_slots[0] if n_slots else 0
-    if state_slots is None and n_slots and n_slots < int(cu_seqlens.numel()) - 1:
+    if state_slots is None and n_slots and n_slots < n:
         raise RuntimeError("state tensors have fewer slots than sequences")
     slots = _int32(state_slots, "state_slots", device)
+    _slot_count(slots, n)
     a_log, dtb = _gate_params(use_gate, A_log, dt_bias, heads, device)
     if scale is None:
         scale = HEAD_DIM ** -0.5
     o = out if out is not None else torch.empty((total, heads, HEAD_DIM), dtype=q.dtype,
                                                 device=device)
     os_ = _heads_rows(o, "out", heads, HEAD_DIM)
+    _nrows(o, "out", total)
+    if o.dtype != q.dtype:
+        raise RuntimeError("out must have q's dtype")
     lib = nat.lib()
     need = int(lib.sophia_kda_chunk_workspace_size(total, n, heads, HEAD_DIM))
     buf, ws_addr, ws_bytes = _workspace(need, device)
@@ -265,8 +297,11 @@ def kda_decode_step(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.
     _heads_rows(v, "v", heads, HEAD_DIM)
     gs = _heads_rows(g, "g", heads, HEAD_DIM)
     bs = _rows(beta, "beta", heads)
+    for t, name in ((k, "k"), (v, "v"), (g, "g"), (beta, "beta")):
+        _nrows(t, name, batch)
     _state(state, "state", heads, device)
     slots = _int32(state_slots, "state_slots", device)
+    _slot_count(slots, batch)
     if slots is None and int(state.size(0)) < batch:
         raise RuntimeError("state has fewer slots than the batch")
     a_log, dtb = _gate_params(use_gate, A_log, dt_bias, heads, device)
@@ -275,6 +310,9 @@ def kda_decode_step(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.
     o = out if out is not None else torch.empty((batch, heads, HEAD_DIM), dtype=q.dtype,
                                                 device=device)
     os_ = _heads_rows(o, "out", heads, HEAD_DIM)
+    _nrows(o, "out", batch)
+    if o.dtype != q.dtype:
+        raise RuntimeError("out must have q's dtype")
     rc = nat.lib().sophia_kda_decode_step(
         nat.ptr(q), nat.ptr(k), nat.ptr(v), qs, nat.dtype_code(q.dtype), nat.ptr(g), gs,
         nat.dtype_code(g.dtype), nat.ptr(beta), bs, nat.dtype_code(beta.dtype), nat.ptr(a_log),

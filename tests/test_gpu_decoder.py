@@ -193,3 +193,23 @@ def test_decoder_at_production_widths_matches_oracle():
     err16 = _rel(_np(last.float()), ref[:, -1])
     print(f"bf16 mixed-step last-token logits rel err {err16:.2e}")
     assert err16 < 6e-2
+
+
+def test_decoder_with_trained_parameter_values_matches_oracle():
+    """The small decoder with every A_log, dt_bias and norm weight (attn/ffn
+    norms, depth-mix norms, MLA q/kv norms, KDA output norms, final norm)
+    drawn away from its init value, against the float64 oracle."""
+    from trained_params import perturb_like_trained
+    dev = _dev()
+    model, _, cfg = _model(dev, seed=3)
+    touched = perturb_like_trained(model, seed=4)
+    assert any(t.endswith("q_norm.weight") for t in touched)
+    assert any(t.endswith("attn.A_log") for t in touched)
+    params = {k: _np(v).astype(np.float64) for k, v in model.state_dict().items()}
+    ids = torch.randint(0, 512, (2, 40), generator=torch.Generator().manual_seed(5))
+    with torch.no_grad():
+        logits = model(ids.to(dev), start_pos=0)
+    ref = do.decoder_forward(params, ids.numpy(), cfg=cfg)
+    err = _rel(_np(logits), ref)
+    print(f"trained-value decoder logits rel err {err:.2e}")
+    assert err < REL_TOL

@@ -199,3 +199,25 @@ def test_packed_decode_step_matches_forward_decode():
     assert _rel(_np(y), _np(y_ref[:, 0])) < 1e-5
     assert _rel(_np(mod.recurrent_state), _np(rec_ref)) < 1e-5
     assert torch.equal(mod.conv_state, conv_ref)
+
+
+def test_mixer_with_trained_parameter_values_matches_oracle():
+    """Config-1 shape with A_log, dt_bias and the output norm weight drawn away
+    from their init values (a trained state_dict's situation): the per-head
+    gate scale exp(A_log) and the RMSNorm weight enter the comparison."""
+    from trained_params import perturb_like_trained
+    dev = _dev()
+    mod, _ = _module(dev, max_batch=1, seed=7)
+    touched = perturb_like_trained(mod, seed=8)
+    assert {"A_log", "dt_bias", "output_norm.weight"} <= set(touched)
+    params = {k: _np(v) for k, v in mod.state_dict().items()}
+    assert np.ptp(params["A_log"]) > 0.5 and np.ptp(params["output_norm.weight"]) > 0.5
+    x = torch.randn(1, 512, 1536, generator=torch.Generator().manual_seed(9))
+    with torch.no_grad():
+        y = mod(x.to(dev), start_pos=0)
+    cache = {"recurrent": np.zeros((1, 16, 128, 128)), "conv": np.zeros((1, 3, 2048, 3))}
+    y_ref = _oracle(params, _np(x), cache=cache)
+    err_y = _rel(_np(y), y_ref)
+    err_s = _rel(_np(mod.recurrent_state[:1]), cache["recurrent"])
+    print(f"trained-value mixer: output {err_y:.2e}, state {err_s:.2e}")
+    assert err_y < REL_TOL and err_s < REL_TOL

@@ -258,3 +258,34 @@ def test_chunk_algorithm_equals_recurrence(seed, length, lo):
     o, s1 = chunk_model.kda_chunked(qn, kn, v, g, beta, s0)
     np.testing.assert_allclose(o, o_ref[0, :, 0], rtol=1e-9, atol=1e-11)
     np.testing.assert_allclose(s1, s_ref[0, 0], rtol=1e-9, atol=1e-11)
+
+
+def test_gate_head_scale_closed_form():
+    """A_log = ln 2 doubles the logit: g = lb * sigmoid(2 (z + b)).  At
+    z + b = ln(3) / 2 that is lb * sigmoid(ln 3) = 3/4 lb exactly, while a
+    dropped exp(A_log) would give lb * sigmoid(ln(3) / 2) = lb * sqrt(3) / (1 + sqrt(3))."""
+    heads, d = 2, 4
+    z = np.full((1, heads, d), np.log(3.0) / 2 - 0.25)
+    dtb = np.full(heads * d, 0.25)
+    a_log = np.array([np.log(2.0), 0.0])
+    g = ko.kda_gate(z, a_log, dtb, -5.0)
+    np.testing.assert_allclose(g[0, 0], -5.0 * 0.75, rtol=1e-6)
+    np.testing.assert_allclose(g[0, 1], -5.0 * np.sqrt(3.0) / (1.0 + np.sqrt(3.0)), rtol=1e-6)
+    # a head-wide A_log of ln 4 with z + b = ln(3) / 4: sigmoid(ln 3) again
+    g4 = ko.kda_gate(np.full((1, 1, d), np.log(3.0) / 4), np.array([np.log(4.0)]), np.zeros(d), -2.0)
+    np.testing.assert_allclose(g4, -1.5, rtol=1e-6)
+
+
+def test_rms_norm_weight_matches_torch():
+    """rms_norm with a non-unit weight and eps against torch's functional rms_norm
+    (the routine the reference's RMSNorm calls, ml/runtime/model/ops.py:49-64)."""
+    import torch
+
+    rng = _rng(21)
+    x = rng.standard_normal((6, 128)) * 3.0
+    w = rng.uniform(0.25, 2.0, 128)
+    for eps in (1e-5, 1e-6, 0.5):
+        ref = torch.nn.functional.rms_norm(torch.tensor(x), (128,), torch.tensor(w), eps).numpy()
+        np.testing.assert_allclose(ko.rms_norm(x, w, eps), ref, rtol=1e-12, atol=1e-12)
+    # a scaled weight scales the output channel by channel
+    np.testing.assert_allclose(ko.rms_norm(x, 2.0 * w, 1e-5), 2.0 * ko.rms_norm(x, w, 1e-5), rtol=1e-12)
