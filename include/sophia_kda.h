@@ -135,6 +135,34 @@ int sophia_kda_chunk_fwd(const void *q, const void *k, const void *v, int64_t qk
                          void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * sophia_kda_chunk_fwd without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference: it
+ * exists for those callers only.  Same arguments, kernels and results as
+ * sophia_kda_chunk_fwd; the scratch is a static device array of
+ * SOPHIA_KDA_CHUNK_NO_ALLOC_MAX_BYTES bytes inside this library (one per
+ * device, held until the process ends), so a batch whose
+ * sophia_kda_chunk_workspace_size() exceeds that returns
+ * SOPHIA_ERR_WORKSPACE (16 heads: up to 903 (chunk, head) records, e.g. one
+ * sequence of 3,520 tokens, or 24 sequences totalling 2,048 tokens).  All
+ * calls on one device share that array: calls that overlap in time on one
+ * device (several streams, several host threads) race and must be ordered
+ * by the caller.  Allocates nothing and synchronises nothing.
+ */
+#define SOPHIA_KDA_CHUNK_NO_ALLOC_MAX_BYTES ((size_t)64 << 20)
+int sophia_kda_chunk_fwd_no_alloc(const void *q, const void *k, const void *v,
+                                  int64_t qkv_row_stride, int qkv_dtype, const void *g,
+                                  int64_t g_row_stride, int g_dtype, const void *beta,
+                                  int64_t beta_row_stride, int beta_dtype, const float *A_log,
+                                  const float *dt_bias, float scale, float lower_bound,
+                                  unsigned flags, const int32_t *cu_seqlens,
+                                  const int32_t *cu_seqlens_host, int n_seqs,
+                                  int64_t total_tokens, int num_heads, int head_dim,
+                                  const float *initial_state, float *final_state,
+                                  int n_state_slots, const int32_t *state_slots, void *o,
+                                  int64_t o_row_stride, void *stream);
+
+/*
  * One recurrent step for `batch` sequences, state updated in place.
  *   q, k, v, g : [batch, H, 128] rows (strides in elements), beta: [batch, H].
  *   state      : [n_state_slots, H, 128, 128] fp32; row b uses slot

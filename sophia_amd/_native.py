@@ -50,6 +50,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "sophia_kda_chunk_fwd": (_i32, [_vp, _vp, _vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64, _i32,
                                     _vp, _vp, _f32, _f32, _u32, _vp, _vp, _i32, _i64, _i32, _i32,
                                     _vp, _vp, _i32, _vp, _vp, _i64, _vp, _sz, _vp]),
+    "sophia_kda_chunk_fwd_no_alloc": (_i32, [_vp, _vp, _vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64,
+                                             _i32, _vp, _vp, _f32, _f32, _u32, _vp, _vp, _i32, _i64,
+                                             _i32, _i32, _vp, _vp, _i32, _vp, _vp, _i64, _vp]),
     "sophia_kda_decode_step": (_i32, [_vp, _vp, _vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64, _i32,
                                       _vp, _vp, _f32, _f32, _u32, _vp, _i32, _vp, _i32, _i32, _i32,
                                       _i32, _vp, _i64, _vp]),

@@ -1118,18 +1118,17 @@ extern "C" size_t sophia_kda_chunk_workspace_size(int64_t total_tokens, int n_se
          static_cast<size_t>(max_chunks(total_tokens, n_seqs)) * num_heads * kRecBytes;
 }
 
-extern "C" int sophia_kda_chunk_fwd(const void *q, const void *k, const void *v,
-                                    int64_t qkv_row_stride, int qkv_dtype, const void *g,
-                                    int64_t g_row_stride, int g_dtype, const void *beta,
-                                    int64_t beta_row_stride, int beta_dtype, const float *A_log,
-                                    const float *dt_bias, float scale, float lower_bound,
-                                    unsigned flags, const int32_t *cu_seqlens,
-                                    const int32_t *cu_seqlens_host, int n_seqs,
-                                    int64_t total_tokens, int num_heads, int head_dim,
-                                    const float *initial_state, float *final_state,
-                                    int n_state_slots, const int32_t *state_slots, void *o,
-                                    int64_t o_row_stride,
-                                    void *workspace, size_t workspace_bytes, void *stream) {
+namespace {
+// The body of both prefill entry points: `workspace` is either the caller's
+// buffer or this library's static scratch (sophia_kda_chunk_fwd_no_alloc).
+int chunk_fwd_impl(const void *q, const void *k, const void *v, int64_t qkv_row_stride, int qkv_dtype,
+                   const void *g, int64_t g_row_stride, int g_dtype, const void *beta,
+                   int64_t beta_row_stride, int beta_dtype, const float *A_log, const float *dt_bias,
+                   float scale, float lower_bound, unsigned flags, const int32_t *cu_seqlens,
+                   const int32_t *cu_seqlens_host, int n_seqs, int64_t total_tokens, int num_heads,
+                   int head_dim, const float *initial_state, float *final_state, int n_state_slots,
+                   const int32_t *state_slots, void *o, int64_t o_row_stride, void *workspace,
+                   size_t workspace_bytes, void *stream) {
   SOPHIA_REQUIRE(head_dim == kD, "kda_chunk_fwd: head_dim must be 128 (got %d)", head_dim);
   SOPHIA_REQUIRE(n_seqs > 0 && num_heads > 0 && num_heads <= 65535 && total_tokens >= 0,
                  "kda_chunk_fwd: bad n_seqs / num_heads / total_tokens");
@@ -1245,4 +1244,86 @@ extern "C" int sophia_kda_chunk_fwd(const void *q, const void *k, const void *v,
   else
     launch_scan<SOPHIA_DTYPE_F32>(splits, sgrid, st, sa);
   return check_launch("kda_chunk_scan");
+}
+
+// ---- static scratch for callers that cannot allocate -------------------------
+// One array per device (each device that loads this library holds its own
+// copy until the process ends).  Host code never passes `scratch` itself to a
+// kernel: its host-side name is not a device address.  The device address is
+// looked up once per device with hipGetSymbolAddress and kept in
+// g_scratch_ptr.  Nothing in it needs to start at zero: the intra kernel
+// writes every record before the scan reads it, and the scratch rows are
+// only written.
+constexpr size_t kStaticScratchBytes = SOPHIA_KDA_CHUNK_NO_ALLOC_MAX_BYTES;
+__device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+int static_scratch(void **out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return set_error(SOPHIA_ERR_HIP, "kda_chunk_fwd_no_alloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return set_error(SOPHIA_ERR_INVALID, "kda_chunk_fwd_no_alloc: device %d beyond %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return set_error(SOPHIA_ERR_HIP, "kda_chunk_fwd_no_alloc: hipGetSymbolAddress(scratch) failed: %s",
+                       hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return SOPHIA_OK;
+}
+}  // namespace
+
+extern "C" int sophia_kda_chunk_fwd(const void *q, const void *k, const void *v,
+                                    int64_t qkv_row_stride, int qkv_dtype, const void *g,
+                                    int64_t g_row_stride, int g_dtype, const void *beta,
+                                    int64_t beta_row_stride, int beta_dtype, const float *A_log,
+                                    const float *dt_bias, float scale, float lower_bound,
+                                    unsigned flags, const int32_t *cu_seqlens,
+                                    const int32_t *cu_seqlens_host, int n_seqs,
+                                    int64_t total_tokens, int num_heads, int head_dim,
+                                    const float *initial_state, float *final_state,
+                                    int n_state_slots, const int32_t *state_slots, void *o,
+                                    int64_t o_row_stride,
+                                    void *workspace, size_t workspace_bytes, void *stream) {
+  return chunk_fwd_impl(q, k, v, qkv_row_stride, qkv_dtype, g, g_row_stride, g_dtype, beta,
+                        beta_row_stride, beta_dtype, A_log, dt_bias, scale, lower_bound, flags,
+                        cu_seqlens, cu_seqlens_host, n_seqs, total_tokens, num_heads, head_dim,
+                        initial_state, final_state, n_state_slots, state_slots, o, o_row_stride,
+                        workspace, workspace_bytes, stream);
+}
+
+extern "C" int sophia_kda_chunk_fwd_no_alloc(const void *q, const void *k, const void *v,
+                                             int64_t qkv_row_stride, int qkv_dtype, const void *g,
+                                             int64_t g_row_stride, int g_dtype, const void *beta,
+                                             int64_t beta_row_stride, int beta_dtype,
+                                             const float *A_log, const float *dt_bias, float scale,
+                                             float lower_bound, unsigned flags,
+                                             const int32_t *cu_seqlens,
+                                             const int32_t *cu_seqlens_host, int n_seqs,
+                                             int64_t total_tokens, int num_heads, int head_dim,
+                                             const float *initial_state, float *final_state,
+                                             int n_state_slots, const int32_t *state_slots, void *o,
+                                             int64_t o_row_stride, void *stream) {
+  const size_t need = sophia_kda_chunk_workspace_size(total_tokens, n_seqs, num_heads, head_dim);
+  SOPHIA_REQUIRE(need > 0, "kda_chunk_fwd_no_alloc: bad total_tokens / n_seqs / num_heads / head_dim");
+  if (need > kStaticScratchBytes)
+    return set_error(SOPHIA_ERR_WORKSPACE,
+                     "kda_chunk_fwd_no_alloc: this batch needs %zu bytes of scratch, more than the "
+                     "%zu-byte static buffer (use sophia_kda_chunk_fwd with a workspace)",
+                     need, kStaticScratchBytes);
+  void *ws = nullptr;
+  if (const int rc = static_scratch(&ws)) return rc;
+  return chunk_fwd_impl(q, k, v, qkv_row_stride, qkv_dtype, g, g_row_stride, g_dtype, beta,
+                        beta_row_stride, beta_dtype, A_log, dt_bias, scale, lower_bound, flags,
+                        cu_seqlens, cu_seqlens_host, n_seqs, total_tokens, num_heads, head_dim,
+                        initial_state, final_state, n_state_slots, state_slots, o, o_row_stride, ws,
+                        kStaticScratchBytes, stream);
 }
