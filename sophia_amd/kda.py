@@ -24,7 +24,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
-from . import ops
+from . import ops, torch_ops
 from .config import ModelArgs
 from .state import LayerCacheSnapshot
 
@@ -95,9 +95,8 @@ class CausalDepthwiseConv1d(nn.Module):
             state = torch.zeros((bsz, channels, hist_len), dtype=torch.float32, device=x.device)
             if history is not None:
                 state.copy_(history.to(dtype=x.dtype).float())
-        y = ops.short_conv_fwd(flat, self.weight, cu, conv_state=state,
-                               read_history=history is not None and hist_len > 0,
-                               write_history=hist_len > 0)
+        y = torch_ops.short_conv_fwd(flat, self.weight.detach(), cu, state, None,
+                                     history is not None and hist_len > 0, hist_len > 0, False)
         next_history = (state.to(x.dtype) if state is not None
                         else x.new_zeros((bsz, channels, 0)))
         return y.view(bsz, seqlen, channels), next_history
@@ -229,6 +228,10 @@ class SophiaKDA(nn.Module):
 
     # ------------------------------------------------------------- fused weights
     def _cached(self, key: str, params: tuple[torch.Tensor, ...], build, dtype: torch.dtype):
+        if torch.compiler.is_compiling():
+            # Traced graphs rebuild the fused weight (no identity stamps there).
+            with torch.no_grad():
+                return build().to(dtype).contiguous()
         stamp = tuple((p.data_ptr(), p._version) for p in params) + (dtype,)
         hit = self._fused_cache.get(key)
         if hit is not None and hit[0] == stamp:
@@ -321,18 +324,16 @@ class SophiaKDA(nn.Module):
                                      self.conv_kernel - 1) if self.conv_kernel > 1 else None
         conv_w = self._conv_weight(qkv.dtype)
         if step:
-            return ops.short_conv_step(qkv, conv_w, state, state_slots=slots, read_history=read,
-                                       weight_rounded=True)
-        return ops.short_conv_fwd(qkv, conv_w, cu, conv_state=state, state_slots=slots,
-                                  read_history=read, write_history=write, weight_rounded=True)
+            return torch_ops.short_conv_step(qkv, conv_w, state, slots, read, True)
+        return torch_ops.short_conv_fwd(qkv, conv_w, cu, state, slots, read, write, True)
 
     def _output(self, o: torch.Tensor, gate_logits: torch.Tensor, dtype) -> torch.Tensor:
         """attention.py:411-420: o_proj(RMSNorm(o) * sigmoid(gate)), the gated
         per-head norm as one HIP kernel (ops.gated_head_norm)."""
         if gate_logits.dtype != dtype:
             gate_logits = gate_logits.to(dtype)
-        out = ops.gated_head_norm(o, gate_logits, self.num_heads, self.head_dim,
-                                  norm_weight=self.output_norm.weight, eps=self.output_norm.eps)
+        out = torch_ops.gated_head_norm(o, gate_logits, self.output_norm.weight.detach(),
+                                        self.num_heads, self.head_dim, float(self.output_norm.eps))
         return self.o_proj(out)
 
     def forward(self, x: torch.Tensor, *, start_pos: int = 0) -> torch.Tensor:
@@ -366,7 +367,7 @@ class SophiaKDA(nn.Module):
             beta_logits = beta_logits.masked_fill(drop[:, :, None], PAD_LOGIT)
         initial_state = self.recurrent_state[:bsz] if cached else None
         output, final_state = self._run_kda(q, k, v, decay, beta_logits, initial_state)
-        if self.use_cache and final_state.data_ptr() != self.recurrent_state.data_ptr():
+        if self.use_cache and final_state is not initial_state:
             with torch.no_grad():
                 self.recurrent_state[:bsz].copy_(final_state.detach().to(dtype=torch.float32))
         out = self._output(output.reshape(n, self.num_heads, self.head_dim), gate_logits, x.dtype)

@@ -326,6 +326,12 @@ def kda_decode_step(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.
 
 
 # -------------------------------------------- flash-linear-attention signatures
+def _detached(t):
+    """Gate parameters enter the kernels as values (the forward-only kernels
+    take no gradient through them)."""
+    return t.detach() if isinstance(t, torch.Tensor) else t
+
+
 def cu_for_batch(bsz: int, seqlen: int, device) -> torch.Tensor:
     """cu_seqlens of a rectangular [bsz, seqlen] batch viewed as packed rows."""
     return torch.arange(0, (bsz + 1) * seqlen, seqlen, dtype=torch.int32, device=device)
@@ -377,12 +383,14 @@ def chunk_kda(q, k, v, g, beta, *, scale=None, initial_state=None, output_final_
                                and initial_state.is_contiguous()) else initial_state.float().contiguous()
     ht = torch.empty((n, heads, HEAD_DIM, HEAD_DIM), dtype=torch.float32, device=q.device) \
         if output_final_state else None
-    o = kda_chunk_fwd(flat(q, HEAD_DIM), flat(k, HEAD_DIM), flat(v, HEAD_DIM), flat(g, HEAD_DIM),
-                      beta.reshape(total, heads), cu,
-                      A_log=A_log, dt_bias=dt_bias, scale=scale, lower_bound=lb,
-                      use_qk_l2norm=use_qk_l2norm_in_kernel, use_gate=use_gate_in_kernel,
-                      use_beta_sigmoid=use_beta_sigmoid_in_kernel, initial_state=h0,
-                      final_state=ht, cu_seqlens_cpu=cu_seqlens_cpu)
+    # Through the sophia::kda_chunk_fwd custom op, so that torch.compile traces
+    # the call as one node.
+    o = torch_ops.kda_chunk_fwd(
+        flat(q, HEAD_DIM), flat(k, HEAD_DIM), flat(v, HEAD_DIM), flat(g, HEAD_DIM),
+        beta.reshape(total, heads), cu, _detached(A_log), _detached(dt_bias),
+        float(HEAD_DIM ** -0.5 if scale is None else scale), lb, bool(use_qk_l2norm_in_kernel),
+        bool(use_gate_in_kernel), bool(use_beta_sigmoid_in_kernel), h0, ht, False, None,
+        cu_seqlens_cpu)
     return o.view(bsz, seqlen, heads, HEAD_DIM), ht
 
 
@@ -411,12 +419,12 @@ def fused_recurrent_kda(q, k, v, g, beta, *, A_log=None, dt_bias=None, scale=Non
         state, read = initial_state, True
     else:
         state, read = initial_state.float().clone(memory_format=torch.contiguous_format), True
-    o = kda_decode_step(q.reshape(bsz, heads, HEAD_DIM), k.reshape(bsz, heads, HEAD_DIM),
-                        v.reshape(bsz, heads, HEAD_DIM), g.reshape(bsz, heads, HEAD_DIM),
-                        beta.reshape(bsz, heads), state, A_log=A_log, dt_bias=dt_bias,
-                        scale=scale, lower_bound=lb, use_qk_l2norm=use_qk_l2norm_in_kernel,
-                        use_gate=use_gate_in_kernel, use_beta_sigmoid=use_beta_sigmoid_in_kernel,
-                        read_state=read)
+    o = torch_ops.kda_decode_step(
+        q.reshape(bsz, heads, HEAD_DIM), k.reshape(bsz, heads, HEAD_DIM),
+        v.reshape(bsz, heads, HEAD_DIM), g.reshape(bsz, heads, HEAD_DIM), beta.reshape(bsz, heads),
+        state, _detached(A_log), _detached(dt_bias),
+        float(HEAD_DIM ** -0.5 if scale is None else scale), lb, bool(use_qk_l2norm_in_kernel),
+        bool(use_gate_in_kernel), bool(use_beta_sigmoid_in_kernel), None, read)
     return o.view(bsz, 1, heads, HEAD_DIM), (state if output_final_state else None)
 
 
@@ -679,3 +687,6 @@ def causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqle
         float(hd ** -0.5 if scale is None else scale), nat.DTYPE_BF16, nat.stream_handle(q.device))
     nat.check(rc, "sophia_causal_attention")
     return y
+
+
+from . import torch_ops  # noqa: E402  (registers the sophia:: custom ops; imports this module)

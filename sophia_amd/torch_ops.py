@@ -1,0 +1,114 @@
+"""The HIP kernels as ``torch.library`` custom ops in the ``sophia::`` namespace.
+
+The reference registers its own kernels the same way
+(ml/training/pretrain/engine/sm120_concurrent_ffn.py:62-104): a CUDA/ROCm
+implementation plus a fake (meta) implementation for shape inference, so that
+``torch.compile`` traces a call as one opaque node instead of breaking the
+graph at a foreign-function call.  Tensors a kernel updates in place (the
+recurrent state, the conv history) are declared in ``mutates_args``.
+
+Ops (each implementation is the eager wrapper of ``sophia_amd.ops``, which
+checks every argument and launches through the C ABI on the current stream):
+  sophia::short_conv_fwd    (x, weight, cu_seqlens, conv_state!, ...) -> y
+  sophia::short_conv_step   (x, weight, conv_state!, ...) -> y
+  sophia::kda_chunk_fwd     (q, k, v, g, beta, cu_seqlens, ..., final_state!, ...) -> o
+  sophia::kda_decode_step   (q, k, v, g, beta, state!, ...) -> o
+  sophia::gated_head_norm   (o, gate, norm_weight, ...) -> y
+"""
+
+from typing import Optional
+
+import torch
+
+from . import ops
+
+_LIB = "sophia"
+
+
+@torch.library.custom_op(f"{_LIB}::short_conv_fwd", mutates_args=("conv_state",),
+                         device_types="cuda")
+def short_conv_fwd(x: torch.Tensor, weight: torch.Tensor, cu_seqlens: torch.Tensor,
+                   conv_state: Optional[torch.Tensor], state_slots: Optional[torch.Tensor],
+                   read_history: bool, write_history: bool, weight_rounded: bool) -> torch.Tensor:
+    return ops.short_conv_fwd(x, weight, cu_seqlens, conv_state=conv_state, state_slots=state_slots,
+                              read_history=read_history, write_history=write_history,
+                              weight_rounded=weight_rounded)
+
+
+@short_conv_fwd.register_fake
+def _(x, weight, cu_seqlens, conv_state, state_slots, read_history, write_history, weight_rounded):
+    return x.new_empty((x.shape[0], x.shape[1]))
+
+
+@torch.library.custom_op(f"{_LIB}::short_conv_step", mutates_args=("conv_state",),
+                         device_types="cuda")
+def short_conv_step(x: torch.Tensor, weight: torch.Tensor, conv_state: torch.Tensor,
+                    state_slots: Optional[torch.Tensor], read_history: bool,
+                    weight_rounded: bool) -> torch.Tensor:
+    return ops.short_conv_step(x, weight, conv_state, state_slots=state_slots,
+                               read_history=read_history, weight_rounded=weight_rounded)
+
+
+@short_conv_step.register_fake
+def _(x, weight, conv_state, state_slots, read_history, weight_rounded):
+    return x.new_empty((x.shape[0], x.shape[1]))
+
+
+@torch.library.custom_op(f"{_LIB}::kda_chunk_fwd", mutates_args=("final_state",),
+                         device_types="cuda")
+def kda_chunk_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
+                  beta: torch.Tensor, cu_seqlens: torch.Tensor, A_log: Optional[torch.Tensor],
+                  dt_bias: Optional[torch.Tensor], scale: float, lower_bound: float,
+                  use_qk_l2norm: bool, use_gate: bool, use_beta_sigmoid: bool,
+                  initial_state: Optional[torch.Tensor], final_state: Optional[torch.Tensor],
+                  read_final_state: bool, state_slots: Optional[torch.Tensor],
+                  cu_seqlens_cpu: Optional[torch.Tensor]) -> torch.Tensor:
+    """Chunk prefill.  ``read_final_state``: the initial state is read from
+    ``final_state`` itself (updated in place, the cached-prefill form); else
+    from ``initial_state`` (read only, must not alias ``final_state``)."""
+    h0 = final_state if read_final_state else initial_state
+    return ops.kda_chunk_fwd(q, k, v, g, beta, cu_seqlens, A_log=A_log, dt_bias=dt_bias,
+                             scale=scale, lower_bound=lower_bound, use_qk_l2norm=use_qk_l2norm,
+                             use_gate=use_gate, use_beta_sigmoid=use_beta_sigmoid,
+                             initial_state=h0, final_state=final_state, state_slots=state_slots,
+                             cu_seqlens_cpu=cu_seqlens_cpu)
+
+
+@kda_chunk_fwd.register_fake
+def _(q, k, v, g, beta, cu_seqlens, A_log, dt_bias, scale, lower_bound, use_qk_l2norm, use_gate,
+      use_beta_sigmoid, initial_state, final_state, read_final_state, state_slots, cu_seqlens_cpu):
+    return q.new_empty((q.shape[0], q.shape[1], v.shape[2]))
+
+
+@torch.library.custom_op(f"{_LIB}::kda_decode_step", mutates_args=("state",), device_types="cuda")
+def kda_decode_step(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
+                    beta: torch.Tensor, state: torch.Tensor, A_log: Optional[torch.Tensor],
+                    dt_bias: Optional[torch.Tensor], scale: float, lower_bound: float,
+                    use_qk_l2norm: bool, use_gate: bool, use_beta_sigmoid: bool,
+                    state_slots: Optional[torch.Tensor], read_state: bool) -> torch.Tensor:
+    return ops.kda_decode_step(q, k, v, g, beta, state, A_log=A_log, dt_bias=dt_bias, scale=scale,
+                               lower_bound=lower_bound, use_qk_l2norm=use_qk_l2norm,
+                               use_gate=use_gate, use_beta_sigmoid=use_beta_sigmoid,
+                               state_slots=state_slots, read_state=read_state)
+
+
+@kda_decode_step.register_fake
+def _(q, k, v, g, beta, state, A_log, dt_bias, scale, lower_bound, use_qk_l2norm, use_gate,
+      use_beta_sigmoid, state_slots, read_state):
+    return q.new_empty((q.shape[0], q.shape[1], v.shape[2]))
+
+
+@torch.library.custom_op(f"{_LIB}::gated_head_norm", mutates_args=(), device_types="cuda")
+def gated_head_norm(o: torch.Tensor, gate: torch.Tensor, norm_weight: Optional[torch.Tensor],
+                    heads: int, head_dim: int, eps: float) -> torch.Tensor:
+    return ops.gated_head_norm(o, gate, heads, head_dim, norm_weight=norm_weight, eps=eps)
+
+
+@gated_head_norm.register_fake
+def _(o, gate, norm_weight, heads, head_dim, eps):
+    rows = gate.numel() // (heads * head_dim)
+    return gate.new_empty((rows, heads * head_dim))
+
+
+__all__ = ["gated_head_norm", "kda_chunk_fwd", "kda_decode_step", "short_conv_fwd",
+           "short_conv_step"]
