@@ -733,14 +733,23 @@ struct ScanArgs {
   const int32_t *slots;
   void *o;
   int64_t o_stride;
-  int splits;   // blocks per (sequence, head): 128 / NVB
   void *trash;  // kTrashBytes of workspace: destination of rows past a sequence end
   // Sequence taken by the work-groups of rank r < kOrderMax: 4-bit field r
   // (r itself from kOrderMax on).  Packed into one argument and extracted
   // arithmetically: an indexed load here (even a scalar one) changes the
   // registers the compiler gives the rings, and its wait counts drain them.
   uint64_t order_bits;
+  // Launch plan: up to kMaxClasses classes of consecutive ranks.  Class c
+  // owns work-groups [cls_block[c], cls_block[c + 1]) and ranks [cls_rank[c],
+  // cls_rank[c + 1]); each of its (sequence, head) pairs runs on
+  // cls_splits[c] work-groups of 128 / cls_splits[c] value columns.  The
+  // fields are read by name and selected with compares (see above).
+  int n_cls;
+  int cls_block0, cls_block1, cls_block2, cls_block3;
+  int cls_rank0, cls_rank1, cls_rank2, cls_rank3, cls_rank4;
+  int cls_splits0, cls_splits1, cls_splits2, cls_splits3;
 };
+constexpr int kMaxClasses = 4;
 
 // ---- scan kernel: two roles per work-group ----------------------------------
 // Wavefronts 0..3 ("U/O" role) own chunk rows 16w..16w+15: U = Ut - W S and
@@ -1049,24 +1058,112 @@ __device__ __forceinline__ void scan_item(const ScanArgs &p, int s, int first, i
   }
 }
 
-template <int NVB, int O_DT>
+template <int O_DT>
 __global__ __launch_bounds__(kScanThreads) void kda_chunk_scan_kernel(ScanArgs p) {
-  constexpr int NT = NVB / 16;
-  __shared__ __attribute__((aligned(16))) uint8_t sSb[4 * NT * 64 * 16];   // S, [ks][nt][lane]
-  __shared__ __attribute__((aligned(16))) uint8_t sUb[2 * NT * 64 * 16];   // U, [ks][nt][lane]
-  // XCD-aware order: the `splits` work-groups of one (sequence, head) share
-  // the same blockIdx % 8, i.e. the same XCD and L2, so they share record reads.
+  // Exchange buffers sized for the widest slice (128 value columns).
+  __shared__ __attribute__((aligned(16))) uint8_t sSb[4 * 8 * 64 * 16];   // S, [ks][nt][lane]
+  __shared__ __attribute__((aligned(16))) uint8_t sUb[2 * 8 * 64 * 16];   // U, [ks][nt][lane]
   const int b = blockIdx.x;
-  const int group = b / (8 * p.splits);
-  const int half = (b / 8) % p.splits;
-  const int sh = group * 8 + (b % 8);
+  // Class of this work-group (uniform; scalar compares on kernel arguments).
+  const bool c1 = p.n_cls > 1 && b >= p.cls_block1;
+  const bool c2 = p.n_cls > 2 && b >= p.cls_block2;
+  const bool c3 = p.n_cls > 3 && b >= p.cls_block3;
+  const int start = c3 ? p.cls_block3 : c2 ? p.cls_block2 : c1 ? p.cls_block1 : p.cls_block0;
+  const int rank_lo = c3 ? p.cls_rank3 : c2 ? p.cls_rank2 : c1 ? p.cls_rank1 : p.cls_rank0;
+  const int rank_hi = c3 ? p.cls_rank4 : c2 ? p.cls_rank3 : c1 ? p.cls_rank2 : p.cls_rank1;
+  const int splits = c3 ? p.cls_splits3 : c2 ? p.cls_splits2 : c1 ? p.cls_splits1 : p.cls_splits0;
+  // XCD-aware order inside a class: the `splits` work-groups of one
+  // (sequence, head) share the same local % 8, i.e. (classes start at
+  // multiples of 8) the same XCD and L2, so they share record reads.
+  const int local = b - start;
+  const int group = local / (8 * splits);
+  const int half = (local / 8) % splits;
+  const int sh = group * 8 + (local % 8);
   const int h = sh % p.num_heads;
-  const int rank = sh / p.num_heads;
-  if (rank >= p.n_seqs) return;
+  const int rank = rank_lo + sh / p.num_heads;
+  if (rank >= rank_hi || rank >= p.n_seqs) return;
   const int s = rank < kOrderMax ? static_cast<int>((p.order_bits >> (4 * rank)) & 15u) : rank;
-  scan_item<NVB, O_DT>(p, s, first_chunk(p.cu, p.n_seqs, p.total, s), h, half, sSb, sUb);
+  const int first = first_chunk(p.cu, p.n_seqs, p.total, s);
+  switch (splits) {
+    case 8: scan_item<16, O_DT>(p, s, first, h, half, sSb, sUb); break;
+    case 4: scan_item<32, O_DT>(p, s, first, h, half, sSb, sUb); break;
+    case 2: scan_item<64, O_DT>(p, s, first, h, half, sSb, sUb); break;
+    default: scan_item<128, O_DT>(p, s, first, h, half, sSb, sUb); break;
+  }
 }
 
+// Host-side plan of the scan launch.  Every (sequence, head) pair of the
+// batch would get the same number of work-groups (slices of the 128 value
+// columns): as many as keep every work-group resident at once.  With the
+// host copy of the offsets (and at most kOrderMax sequences), sequences are
+// taken longest first, a batch whose longest sequence has at least twice the
+// mean number of chunks gets twice that number for its longest chains, and
+// shorter chains get fewer slices: half for a chain of under 60 % of the
+// longest, a quarter under 30 % (at least one).  Measured on one MI355X,
+// the 8 sequences of U[256, 4096] tokens (56 chunks at most, 16 heads):
+// 4/4/4/2/2/1/1/1 slices 197 us per prefill call, 4 everywhere 206 us,
+// 8 on the longest chain and 4 elsewhere 214 us (a slice's step reads the
+// pair's whole -W / Q e^G / Kbar^T / A_qk record parts, so more slices per
+// chain cost more in total than they save on the chain once the chip is full).
+struct ScanPlan {
+  int n_cls = 1;
+  int block[kMaxClasses + 1] = {};
+  int rank[kMaxClasses + 1] = {};
+  int splits[kMaxClasses] = {1, 1, 1, 1};
+  uint64_t order_bits = 0xfedcba9876543210ull;
+  int64_t blocks = 0;
+};
+
+ScanPlan plan_scan(const int32_t *cu_host, int n_seqs, int num_heads, int cus) {
+  ScanPlan pl;
+  const int64_t pairs = static_cast<int64_t>(n_seqs) * num_heads;
+  int top = 1;
+  while (top < 8 && pairs * top * 2 <= static_cast<int64_t>(cus)) top *= 2;
+  if (!cu_host || n_seqs > kOrderMax) {
+    pl.splits[0] = top;
+    pl.rank[1] = n_seqs;
+    pl.blocks = (pairs + 7) / 8 * 8 * top;
+    pl.block[1] = static_cast<int>(pl.blocks);
+    return pl;
+  }
+  int order[kOrderMax];
+  int64_t chunks[kOrderMax];
+  int64_t nmax = 0, sum = 0;
+  for (int i = 0; i < n_seqs; ++i) {
+    order[i] = i;
+    chunks[i] = (static_cast<int64_t>(cu_host[i + 1]) - cu_host[i] + kC - 1) / kC;
+    nmax = chunks[i] > nmax ? chunks[i] : nmax;
+    sum += chunks[i];
+  }
+  if (top < 8 && sum > 0 && nmax * n_seqs >= 2 * sum) top *= 2;
+  std::stable_sort(order, order + n_seqs, [&](int a, int b) { return chunks[a] > chunks[b]; });
+  for (int r = 0; r < n_seqs; ++r)
+    pl.order_bits = (pl.order_bits & ~(15ull << (4 * r))) | (static_cast<uint64_t>(order[r]) << (4 * r));
+  int sp[kOrderMax];
+  for (int r = 0; r < n_seqs; ++r) {
+    const int64_t c = chunks[order[r]];
+    int v = top;
+    if (10 * c < 6 * nmax) v = top / 2;
+    if (10 * c < 3 * nmax) v = top / 4;
+    sp[r] = v < 1 ? 1 : v;
+  }
+  pl.n_cls = 0;
+  int64_t block = 0;
+  for (int r = 0; r < n_seqs;) {
+    int e = r;
+    while (e < n_seqs && sp[e] == sp[r]) ++e;
+    const int c = pl.n_cls++;
+    pl.rank[c] = r;
+    pl.block[c] = static_cast<int>(block);
+    pl.splits[c] = sp[r];
+    block += (static_cast<int64_t>(e - r) * num_heads + 7) / 8 * 8 * sp[r];
+    r = e;
+  }
+  pl.rank[pl.n_cls] = n_seqs;
+  pl.block[pl.n_cls] = static_cast<int>(block);
+  pl.blocks = block;
+  return pl;
+}
 
 // Dynamic LDS above the default limit is enabled once per (kernel, device),
 // under a lock: launches may come from several host threads and devices.
@@ -1097,13 +1194,8 @@ int launch_intra(dim3 grid, hipStream_t st, const IntraArgs &ia) {
 }
 
 template <int O_DT>
-void launch_scan(int splits, dim3 grid, hipStream_t st, const ScanArgs &sa) {
-  switch (splits) {
-    case 1: hipLaunchKernelGGL((kda_chunk_scan_kernel<128, O_DT>), grid, dim3(kScanThreads), 0, st, sa); break;
-    case 2: hipLaunchKernelGGL((kda_chunk_scan_kernel<64, O_DT>), grid, dim3(kScanThreads), 0, st, sa); break;
-    case 4: hipLaunchKernelGGL((kda_chunk_scan_kernel<32, O_DT>), grid, dim3(kScanThreads), 0, st, sa); break;
-    default: hipLaunchKernelGGL((kda_chunk_scan_kernel<16, O_DT>), grid, dim3(kScanThreads), 0, st, sa); break;
-  }
+void launch_scan(dim3 grid, hipStream_t st, const ScanArgs &sa) {
+  hipLaunchKernelGGL((kda_chunk_scan_kernel<O_DT>), grid, dim3(kScanThreads), 0, st, sa);
 }
 
 }  // namespace
@@ -1193,56 +1285,27 @@ int chunk_fwd_impl(const void *q, const void *k, const void *v, int64_t qkv_row_
     }
     if (rc) return rc;
   }
-  // The state scan is sequential over the chunks of a sequence: split the 128
-  // value columns of each (sequence, head) over 1, 2, 4 or 8 work-groups, as
-  // many as keep every work-group resident at once (one per CU: its 8
-  // wavefronts hold rings of record buffers and fill half of each SIMD's
-  // register file), so a small batch still spreads its critical path over
-  // the chip.  The host copy of the offsets can double that (below).
+  // The state scan is sequential over the chunks of a sequence: the 128
+  // value columns of each (sequence, head) are split over 1, 2, 4 or 8
+  // work-groups (plan_scan), so that a small batch still spreads its
+  // critical path over the chip.  The host copy of the offsets only shapes
+  // this plan; results do not depend on it.
   int device = 0, cus = 256;
   if (hipGetDevice(&device) == hipSuccess)
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) cus = 256;
-  const int64_t pairs = static_cast<int64_t>(n_seqs) * num_heads;
-  int splits = 1;
-  while (splits < 8 && pairs * splits * 2 <= static_cast<int64_t>(cus)) splits *= 2;
+  const ScanPlan pl = plan_scan(cu_seqlens_host, n_seqs, num_heads, cus);
+  SOPHIA_REQUIRE(pl.blocks > 0 && pl.blocks <= 0x7fffffff, "kda_chunk_fwd: grid too large");
   ScanArgs sa{cu_seqlens, n_seqs, total_tokens, num_heads, max_ch, records,
-              initial_state, final_state, n_state_slots, state_slots, o, o_row_stride, splits, trash,
-              0xfedcba9876543210ull};
-  if (cu_seqlens_host) {
-    // The host copy of the offsets only shapes the launch; the results do not
-    // depend on it.  A batch whose longest sequence has at least twice the
-    // mean number of chunks spends most of its scan on a few sequential
-    // chains: twice the work-groups per (sequence, head) shortens those
-    // chains, and the shorter sequences queue behind them (one MI355X, the 8
-    // sequences of U[256, 4096] tokens: 117 -> 98 us; with 8 work-groups
-    // per (sequence, head) instead, 131 us).  Up to kOrderMax
-    // sequences are taken longest first, so the queue holds the short ones.
-    int64_t nmax = 0, sum = 0;
-    int64_t chunks[kOrderMax];
-    for (int i = 0; i < n_seqs; ++i) {
-      const int64_t c = (static_cast<int64_t>(cu_seqlens_host[i + 1]) - cu_seqlens_host[i] + kC - 1) / kC;
-      nmax = c > nmax ? c : nmax;
-      sum += c;
-      if (i < kOrderMax) chunks[i] = c;
-    }
-    if (splits < 8 && nmax * n_seqs >= 2 * sum && sum > 0) splits *= 2;
-    sa.splits = splits;
-    if (n_seqs <= kOrderMax) {
-      int order[kOrderMax];
-      for (int i = 0; i < n_seqs; ++i) order[i] = i;
-      std::stable_sort(order, order + n_seqs, [&](int a, int b) { return chunks[a] > chunks[b]; });
-      for (int r = 0; r < n_seqs; ++r)
-        sa.order_bits = (sa.order_bits & ~(15ull << (4 * r))) | (static_cast<uint64_t>(order[r]) << (4 * r));
-    }
-  }
-  const int64_t groups = (pairs + 7) / 8;
-  const int64_t blocks = groups * 8 * splits;
-  SOPHIA_REQUIRE(blocks <= 0x7fffffff, "kda_chunk_fwd: grid too large");
-  const dim3 sgrid(static_cast<unsigned>(blocks));
+              initial_state, final_state, n_state_slots, state_slots, o, o_row_stride, trash,
+              pl.order_bits, pl.n_cls,
+              pl.block[0], pl.block[1], pl.block[2], pl.block[3],
+              pl.rank[0], pl.rank[1], pl.rank[2], pl.rank[3], pl.rank[4],
+              pl.splits[0], pl.splits[1], pl.splits[2], pl.splits[3]};
+  const dim3 sgrid(static_cast<unsigned>(pl.blocks));
   if (qkv_dtype == SOPHIA_DTYPE_BF16)
-    launch_scan<SOPHIA_DTYPE_BF16>(splits, sgrid, st, sa);
+    launch_scan<SOPHIA_DTYPE_BF16>(sgrid, st, sa);
   else
-    launch_scan<SOPHIA_DTYPE_F32>(splits, sgrid, st, sa);
+    launch_scan<SOPHIA_DTYPE_F32>(sgrid, st, sa);
   return check_launch("kda_chunk_scan");
 }
 
