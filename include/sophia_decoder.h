@@ -107,20 +107,25 @@ int sophia_mla_decode_attn(const void *qa, int64_t qa_stride, int qa_dtype, cons
 
 /*
  * Causal self-attention over packed sequences, bf16, head_dim 128; replaces
- * the no-cache prefill attention of SophiaMLA (ml/runtime/model/attention.py:
- * 630-639, scaled_dot_product_attention(q, k, v, is_causal=True)):
- *   out[t, h] = sum_{s <= t} softmax_s(scale * q[t, h] . k[s, h]) v[s, h]
- * over the tokens t, s of one sequence (cu_seqlens [n_seqs + 1] int32 on the
- * device).  q, k, v, out: [total, heads, 128] rows with row strides in
- * elements (q, k, v 16-byte aligned with strides multiples of 8; out 8-byte
- * aligned).  max_len must bound every sequence length (it sizes the grid).
- * Scores, softmax and sums are fp32; the probabilities enter the value product
- * as bf16 (as they do in a bf16 SDPA).
+ * the prefill attention of SophiaMLA (ml/runtime/model/attention.py:630-654:
+ * scaled_dot_product_attention with is_causal=True, or with the
+ * tril(klen - seqlen) mask when the queries follow cached keys):
+ *   out[t, h] = sum_{s <= t + off} softmax_s(scale * q[t, h] . k[s, h]) v[s, h]
+ * over the query rows t of one sequence (cu_seqlens [n_seqs + 1] int32 on the
+ * device) and its key/value rows s (cu_seqlens_k, or the same rows when
+ * cu_seqlens_k is NULL), where off = keys - queries of that sequence: the
+ * queries are the last positions of the key range (off = 0 for a prefill from
+ * an empty cache).  total / total_k: rows of q / of k and v.  q, k, v, out:
+ * [rows, heads, 128] with row strides in elements (q, k, v 16-byte aligned
+ * with strides multiples of 8; out 8-byte aligned).  max_len must bound every
+ * sequence's query count (it sizes the grid).  Scores, softmax and sums are
+ * fp32; the probabilities enter the value product as bf16 (as they do in a
+ * bf16 SDPA).
  */
 int sophia_causal_attention(const void *q, int64_t q_stride, const void *k, int64_t k_stride, const void *v,
-                            int64_t v_stride, void *out, int64_t out_stride, const int32_t *cu_seqlens, int n_seqs,
-                            int64_t total, int max_len, int heads, int head_dim, float scale, int dtype,
-                            void *stream);
+                            int64_t v_stride, void *out, int64_t out_stride, const int32_t *cu_seqlens,
+                            const int32_t *cu_seqlens_k, int n_seqs, int64_t total, int64_t total_k, int max_len,
+                            int heads, int head_dim, float scale, int dtype, void *stream);
 
 #ifdef __cplusplus
 }

@@ -62,8 +62,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "sophia_gated_head_norm": (_i32, [_vp, _i64, _i32, _vp, _i64, _vp, _f32, _vp, _i64, _i64, _i32,
                                       _i32, _i32, _vp]),
     "sophia_mla_decode_workspace_size": (_sz, [_i64, _i32, _i32]),
-    "sophia_causal_attention": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i32, _i64,
-                                       _i32, _i32, _i32, _f32, _i32, _vp]),
+    "sophia_causal_attention": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i32,
+                                       _i64, _i64, _i32, _i32, _i32, _f32, _i32, _vp]),
     "sophia_mla_decode_attn": (_i32, [_vp, _i64, _i32, _vp, _i64, _i32, _i32, _vp, _vp, _f32, _vp,
                                       _i64, _i32, _i64, _i32, _i32, _i32, _vp, _sz, _vp]),
 }

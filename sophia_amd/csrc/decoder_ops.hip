@@ -619,6 +619,11 @@ __global__ __launch_bounds__(256) void mla_decode_merge_kernel(MlaArgs a) {
 
 // ---------------------------------------------------------------------------
 // Causal attention over packed sequences (the MLA prefill rows, head_dim 128).
+// The queries of sequence s are rows cu[s]..cu[s+1] of q; its keys and values
+// are rows cu_k[s]..cu_k[s+1] of k and v (cu_k == NULL: the same rows).  With
+// more keys than queries, the queries are the last positions of the key range
+// (a prefill that continues after cached tokens): query i sees keys
+// 0 .. i + (keys - queries).
 //
 // One work-group (4 wavefronts) per (128-query block, head, sequence); a
 // wavefront owns 32 queries.  Per 64-key block, K (row-major) and V (transposed,
@@ -643,8 +648,10 @@ struct FaArgs {
   uint16_t *out;
   int64_t out_stride;
   const int32_t *cu;
+  const int32_t *cu_k;             // key offsets (NULL: cu)
   int n_seqs;
   int64_t total;
+  int64_t total_k;                 // rows of k and v
   int q_blocks;                    // 128-query blocks per sequence (of max_len)
   int heads;
   float scale_log2;                // softmax scale * log2(e)
@@ -666,12 +673,20 @@ __global__ __launch_bounds__(256, 2) void causal_attn_kernel(FaArgs a) {
   const int h = pair % a.heads, sq = pair / a.heads;
   const int64_t start = iclamp64(a.cu[sq], 0, a.total);
   const int len = static_cast<int>(iclamp64(a.cu[sq + 1], start, a.total) - start);
+  int64_t kstart = start;
+  int klen = len;
+  if (a.cu_k) {
+    kstart = iclamp64(a.cu_k[sq], 0, a.total_k);
+    klen = static_cast<int>(iclamp64(a.cu_k[sq + 1], kstart, a.total_k) - kstart);
+  }
+  if (klen < 1) return;                           // no key to attend to
+  const int off = klen > len ? klen - len : 0;    // position of query 0 among the keys
   const int q0 = (a.q_blocks - 1 - r % a.q_blocks) * kFaQ;
   if (q0 >= len) return;
-  const int kend = min(len, q0 + kFaQ);           // keys needed by this work-group
+  const int kend = min(klen, q0 + off + kFaQ);    // keys needed by this work-group
   const int nkb = (kend + kFaK - 1) / kFaK;
   const int wq0 = q0 + 32 * w;                    // first query of this wavefront
-  const int wq_last = min(wq0 + 31, len - 1);     // last query it stores
+  const int wq_last = min(wq0 + 31, len - 1) + off;  // position of the last query it stores
 
   // Q^T as B operands: lane (query ln of tile qt, g) holds dims 32 ks + 8 g .. +7.
   bf8 qf[2][4];
@@ -698,9 +713,9 @@ __global__ __launch_bounds__(256, 2) void causal_attn_kernel(FaArgs a) {
   // This lane's K / V rows of a block: key 16 w + ln, dims 32 ks + 8 g .. +7.
   u4 kr[4], vr[4];
   auto load_block = [&](int kb) {
-    const int key = min(kb * kFaK + 16 * w + ln, len - 1);
-    const uint16_t *kp = a.k + (start + key) * a.k_stride + static_cast<int64_t>(h) * kFaD + 8 * g;
-    const uint16_t *vp = a.v + (start + key) * a.v_stride + static_cast<int64_t>(h) * kFaD + 8 * g;
+    const int key = min(kb * kFaK + 16 * w + ln, klen - 1);
+    const uint16_t *kp = a.k + (kstart + key) * a.k_stride + static_cast<int64_t>(h) * kFaD + 8 * g;
+    const uint16_t *vp = a.v + (kstart + key) * a.v_stride + static_cast<int64_t>(h) * kFaD + 8 * g;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       kr[ks] = *reinterpret_cast<const u4 *>(kp + 32 * ks);
@@ -739,14 +754,14 @@ __global__ __launch_bounds__(256, 2) void causal_attn_kernel(FaArgs a) {
     bf8 pf[2][2];  // [kp][qt]: P^T as B operands of the value product
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
-      const int qi = wq0 + 16 * qt + ln;
+      const int qpos = wq0 + 16 * qt + ln + off;
       float mx = -INFINITY;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int key = k0 + 16 * kt + 4 * g + i;
-          const float sv = (key <= qi && key < len) ? st[kt][qt][i] * a.scale_log2 : -INFINITY;
+          const float sv = (key <= qpos && key < klen) ? st[kt][qt][i] * a.scale_log2 : -INFINITY;
           st[kt][qt][i] = sv;
           mx = fmaxf(mx, sv);
         }
@@ -979,8 +994,9 @@ extern "C" int sophia_mla_decode_attn(const void *qa, int64_t qa_stride, int qa_
 
 extern "C" int sophia_causal_attention(const void *q, int64_t q_stride, const void *k, int64_t k_stride,
                                        const void *v, int64_t v_stride, void *out, int64_t out_stride,
-                                       const int32_t *cu_seqlens, int n_seqs, int64_t total, int max_len, int heads,
-                                       int head_dim, float scale, int dtype, void *stream) {
+                                       const int32_t *cu_seqlens, const int32_t *cu_seqlens_k, int n_seqs,
+                                       int64_t total, int64_t total_k, int max_len, int heads, int head_dim,
+                                       float scale, int dtype, void *stream) {
   SOPHIA_REQUIRE(dtype == SOPHIA_DTYPE_BF16, "causal_attention: bf16 only");
   SOPHIA_REQUIRE(head_dim == kFaD, "causal_attention: head_dim must be %d", kFaD);
   SOPHIA_REQUIRE(heads >= 1 && heads <= 65535 && n_seqs >= 0 && n_seqs <= 65535 && total >= 0 && max_len >= 0,
@@ -990,12 +1006,14 @@ extern "C" int sophia_causal_attention(const void *q, int64_t q_stride, const vo
                      q_stride % 8 == 0 && k_stride % 8 == 0 && v_stride % 8 == 0 && out_stride % 4 == 0,
                  "causal_attention: bad strides");
   SOPHIA_REQUIRE(n_seqs == 0 || total == 0 || (q && k && v && out && cu_seqlens), "causal_attention: NULL pointer");
+  SOPHIA_REQUIRE(!cu_seqlens_k || total_k >= 0, "causal_attention: bad total_k");
   SOPHIA_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && (reinterpret_cast<uintptr_t>(out) & 7) == 0,
                  "causal_attention: q, k, v must be 16-byte and out 8-byte aligned");
   if (n_seqs == 0 || total == 0 || max_len == 0) return SOPHIA_OK;
   FaArgs a{static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k), static_cast<const uint16_t *>(v),
-           q_stride, k_stride, v_stride, static_cast<uint16_t *>(out), out_stride, cu_seqlens, n_seqs, total,
-           (max_len + kFaQ - 1) / kFaQ, heads, scale * 1.44269504088896341f};
+           q_stride, k_stride, v_stride, static_cast<uint16_t *>(out), out_stride, cu_seqlens, cu_seqlens_k,
+           n_seqs, total, cu_seqlens_k ? total_k : total, (max_len + kFaQ - 1) / kFaQ, heads,
+           scale * 1.44269504088896341f};
   const int64_t pair_groups = (static_cast<int64_t>(heads) * n_seqs + 7) / 8;
   const int64_t blocks = pair_groups * 8 * a.q_blocks;
   SOPHIA_REQUIRE(blocks <= 0x7fffffff, "causal_attention: grid too large");

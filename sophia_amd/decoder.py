@@ -24,6 +24,7 @@ ml/training/pretrain/engine/sm120_graph_runner.py:318-371) and replays it.
 
 from __future__ import annotations
 
+import itertools
 import math
 
 import torch
@@ -33,7 +34,7 @@ from torch import nn
 from .config import ModelArgs
 from . import ops
 from .kda import RMSNorm, RuntimeLinear, SophiaKDA, _require_gpu
-from .state import LayerCacheSnapshot
+from .state import LayerCacheSnapshot, RuntimeCacheSnapshot
 
 
 class SophiaMLA(nn.Module):
@@ -84,8 +85,14 @@ class SophiaMLA(nn.Module):
         else:
             self.latent_cache.zero_()
 
-    def cache_snapshot(self, *, device: str, batch_size: int, cache_pos: int | None):
+    def cache_snapshot(self, *, device: str, batch_size: int, cache_pos: int | None,
+                       slots: torch.Tensor | None = None):
+        """Copies of latents [:cache_pos] of rows [:batch_size] (attention.py:
+        570-575), or of the cache slots ``slots`` in that order."""
         end = int(self.latent_cache.size(1) if cache_pos is None else cache_pos)
+        if slots is not None:
+            idx = slots.to(device=self.latent_cache.device, dtype=torch.long)
+            return LayerCacheSnapshot(latent=self.latent_cache[:, :end].index_select(0, idx).to(device))
         return LayerCacheSnapshot(latent=self.latent_cache[:batch_size, :end].to(device).clone())
 
     def validate_cache_snapshot(self, snapshot: LayerCacheSnapshot) -> None:
@@ -94,11 +101,20 @@ class SophiaMLA(nn.Module):
         if snapshot.latent is not None and int(snapshot.latent.size(-1)) != self.kv_rank:
             raise ValueError("MLA latent cache shape mismatch")
 
-    def load_cache_snapshot(self, snapshot: LayerCacheSnapshot) -> None:
+    def load_cache_snapshot(self, snapshot: LayerCacheSnapshot, *,
+                            slots: torch.Tensor | None = None) -> None:
+        """attention.py:577-583; with ``slots``, row i of the snapshot goes to
+        cache slot slots[i] (positions past the snapshot's length untouched)."""
         self.validate_cache_snapshot(snapshot)
         if snapshot.latent is None:
             return
         batch, length = int(snapshot.latent.size(0)), int(snapshot.latent.size(1))
+        if slots is not None:
+            self.ensure_sequence_capacity(length)
+            idx = slots.to(device=self.latent_cache.device, dtype=torch.long)
+            self.latent_cache[idx, :length] = snapshot.latent.to(self.latent_cache.device,
+                                                                  dtype=self.latent_cache.dtype)
+            return
         self.ensure_batch_capacity(batch)
         self.ensure_sequence_capacity(length)
         self.latent_cache[:batch, :length].copy_(
@@ -112,18 +128,35 @@ class SophiaMLA(nn.Module):
         gated = ops.gated_head_norm(out.to(x.dtype), gate, self.num_heads, self.head_dim)
         return self.o_proj(gated.view(*x.shape[:-1], self.inner_dim))
 
-    def _causal(self, q, k, v, cu, max_len: int, out):
-        """Causal attention within each of the equal-length (``max_len``)
-        sequences packed in [rows, heads, 128] tensors, into ``out``: the HIP
-        kernel (``ops.causal_attention``) for bf16 activations, torch SDPA for
-        fp32 ones."""
+    def _causal(self, q, k, v, cu, max_len: int, out, *, cu_k=None, cu_host=None, cu_k_host=None):
+        """Causal attention within each packed sequence, into ``out``.  Query
+        rows are delimited by ``cu``, key/value rows by ``cu_k`` (default: the
+        query rows); a sequence with more keys than queries continues after
+        cached tokens (its queries are the last key positions, the
+        tril(klen - seqlen) mask of attention.py:641-654).  The HIP kernel
+        (``ops.causal_attention``) runs for bf16 activations; fp32 ones use
+        torch SDPA, per sequence (host offsets ``cu_host`` / ``cu_k_host``)
+        unless the sequences are equal-length and start from empty caches."""
         if q.dtype == torch.bfloat16:
-            ops.causal_attention(q, k, v, cu, max_len, scale=self.head_dim ** -0.5, out=out)
+            ops.causal_attention(q, k, v, cu, max_len, scale=self.head_dim ** -0.5, cu_seqlens_k=cu_k,
+                                 out=out)
             return
-        n = int(q.size(0)) // max_len
-        o = F.scaled_dot_product_attention(*(t.reshape(n, max_len, self.num_heads, self.head_dim)
-                                             .transpose(1, 2) for t in (q, k, v)), is_causal=True)
-        out.copy_(o.transpose(1, 2).reshape_as(out))
+        if cu_host is None:
+            n = int(q.size(0)) // max_len
+            o = F.scaled_dot_product_attention(*(t.reshape(n, max_len, self.num_heads, self.head_dim)
+                                                 .transpose(1, 2) for t in (q, k, v)), is_causal=True)
+            out.copy_(o.transpose(1, 2).reshape_as(out))
+            return
+        qo = [int(c) for c in cu_host.tolist()]
+        ko = qo if cu_k_host is None else [int(c) for c in cu_k_host.tolist()]
+        for s in range(len(qo) - 1):
+            a, b, ka, kb = qo[s], qo[s + 1], ko[s], ko[s + 1]
+            if b == a:
+                continue
+            allow = torch.ones((b - a, kb - ka), dtype=torch.bool, device=q.device).tril(kb - ka - (b - a))
+            o = F.scaled_dot_product_attention(q[a:b].transpose(0, 1), k[ka:kb].transpose(0, 1),
+                                               v[ka:kb].transpose(0, 1), attn_mask=allow)
+            out[a:b] = o.transpose(0, 1)
 
     def forward(self, x: torch.Tensor, *, start_pos: int = 0) -> torch.Tensor:
         """attention.py:609-657 (pad-mask path: attention.py:585-600,635-654)."""
@@ -178,15 +211,17 @@ class SophiaMLA(nn.Module):
         grown[:, :prompt_len] = cached[:bsz]
         return grown
 
-    def forward_mixed(self, x: torch.Tensor, n_prefill_seqs: int, prefill_len: int,
-                      prefill_slots: torch.Tensor, decode_slots: torch.Tensor,
-                      decode_pos: torch.Tensor, max_decode_len: int,
-                      cu_prefill: torch.Tensor | None = None) -> torch.Tensor:
-        """Packed step: rows [0, P*Tp) are P new sequences of Tp tokens
-        (causal attention over their own tokens, latents written to their
-        slots at positions 0..Tp-1); the remaining D rows are one token each
-        for running sequences at positions ``decode_pos`` (int64, device) of
-        slots ``decode_slots``, attending to their cached latents 0..pos.
+    def forward_mixed(self, x: torch.Tensor, step: dict) -> torch.Tensor:
+        """Packed continuous-batching step (``step`` from Transformer.forward_step).
+
+        Rows [0, R) are prefill tokens of the sequences delimited by
+        ``step["cu_prefill"]``; each writes its latent into its slot at its
+        position and attends causally over the latents of its own sequence:
+        its new tokens, plus the cached ones before them when the sequence
+        continues (``step["reads_cache"]``: keys are gathered from the cache).
+        The remaining rows are one token each for running sequences at
+        positions ``decode_pos`` (int64, device) of slots ``decode_slots``,
+        attending to their cached latents 0..pos.
 
         The decode part attends in latent space: with NoPE, q . (W_k,h c) =
         (W_k,h^T q) . c, so scores and the value sum are taken directly over
@@ -198,7 +233,7 @@ class SophiaMLA(nn.Module):
         row; it sizes the kernel's key splits.
         """
         n = int(x.size(0))
-        npre = int(n_prefill_seqs) * int(prefill_len)
+        npre = int(step["n_prefill_rows"])
         nd = n - npre
         h, d, r = self.num_heads, self.head_dim, self.kv_rank
         q = self.q_up(self.q_norm(self.q_down(x))).view(n, h, d)
@@ -206,23 +241,31 @@ class SophiaMLA(nn.Module):
         cache = self.latent_cache
         out = torch.empty((n, h, d), dtype=x.dtype, device=x.device)
         if npre > 0:
-            P, T = int(n_prefill_seqs), int(prefill_len)
-            lat_p = latent[:npre].view(P, T, r)
-            cache[prefill_slots.long(), :T] = lat_p.to(cache.dtype)
-            k = self.k_up(lat_p).view(npre, h, d)
-            v = self.v_up(lat_p).view(npre, h, d)
-            if cu_prefill is None:
-                cu_prefill = torch.arange(0, (P + 1) * T, T, dtype=torch.int32, device=x.device)
-            self._causal(q[:npre], k, v, cu_prefill, T, out[:npre])
+            lat_p = latent[:npre]
+            cu_k = cu_k_host = None
+            if step["rectangular"]:
+                P, T = int(step["n_prefill_seqs"]), int(step["max_prefill_len"])
+                cache[step["prefill_slots"].long(), :T] = lat_p.view(P, T, r).to(cache.dtype)
+                lat_k = lat_p
+            else:
+                cache[step["row_slot"], step["row_pos"]] = lat_p.to(cache.dtype)
+                lat_k = lat_p
+                if step["reads_cache"]:
+                    lat_k = cache[step["key_slot"], step["key_pos"]].to(x.dtype)
+                    cu_k, cu_k_host = step["cu_keys"], step["cu_keys_host"]
+            k = self.k_up(lat_k).view(-1, h, d)
+            v = self.v_up(lat_k).view(-1, h, d)
+            self._causal(q[:npre], k, v, step["cu_prefill"], int(step["max_prefill_len"]), out[:npre],
+                         cu_k=cu_k, cu_host=step["cu_prefill_host"], cu_k_host=cu_k_host)
         if nd > 0:
-            slots = decode_slots.long()
-            cache[slots, decode_pos] = latent[npre:].to(cache.dtype)
+            slots = step["decode_slots"].long()
+            cache[slots, step["decode_pos"]] = latent[npre:].to(cache.dtype)
             w_k = self.k_up.weight.view(h, d, r).to(x.dtype)
             w_v = self.v_up.weight.view(h, d, r).to(x.dtype)
             qa = torch.bmm(q[npre:].transpose(0, 1).contiguous(), w_k).transpose(0, 1)   # [D, h, r]
             # softmax over cached latents 0..pos and their weighted sum, one kernel
-            ctx = ops.mla_decode_attn(qa.contiguous(), cache, decode_slots, decode_pos,
-                                      d ** -0.5, max_len=int(max_decode_len))            # [D, h, r]
+            ctx = ops.mla_decode_attn(qa.contiguous(), cache, step["decode_slots"], step["decode_pos"],
+                                      d ** -0.5, max_len=int(step["max_decode_len"]))   # [D, h, r]
             o = torch.bmm(ctx.transpose(0, 1).contiguous(), w_v.transpose(1, 2).contiguous())
             out[npre:] = o.transpose(0, 1)
         return self._gate_out(x, out)
@@ -356,14 +399,12 @@ class SophiaBlock(nn.Module):
     def forward_mixed(self, partial_block, completed_blocks, step: dict, *, pending=None,
                       defer: bool = False):
         if self.layer_type == "mla":
-            attn = lambda y: self.attn.forward_mixed(
-                y, step["n_prefill_seqs"], step["prefill_len"], step["prefill_slots"],
-                step["decode_slots"], step["decode_pos"], step["max_decode_len"],
-                cu_prefill=step["cu_prefill"])
+            attn = lambda y: self.attn.forward_mixed(y, step)
         else:
             attn = lambda y: self.attn.forward_mixed(
-                y, step["n_prefill_seqs"] * step["prefill_len"], step["cu_prefill"],
-                step["prefill_slots"], step["decode_slots"])
+                y, step["n_prefill_rows"], step["cu_prefill"], step["prefill_slots"],
+                step["decode_slots"], prefill_reads_cache=step["reads_cache"],
+                cu_prefill_host=step["cu_prefill_host"])
         return self._mix(partial_block, completed_blocks, attn, pending, defer)
 
 
@@ -436,6 +477,8 @@ class Transformer(nn.Module):
         """transformer.py:169-207: logits [B, S, vocab]."""
         _require_gpu(input_ids)
         self._validate(input_ids, start_pos)
+        if self.args.use_cache:
+            self.ensure_batch_capacity(int(input_ids.size(0)))
         hidden = self.tok_embeddings(input_ids)
         completed = depth_store(hidden, self.args.n_layers, self.args.attn_res_block_size)
         pending = None  # each layer's FFN output is added inside the next depth mix
@@ -450,36 +493,189 @@ class Transformer(nn.Module):
             return self.output_attn_residual(hidden, completed, self.norm)
         return self.output_attn_residual(hidden, completed, self.norm, residual=pending)[1]
 
-    def forward_mixed(self, prefill_ids: torch.Tensor, decode_ids: torch.Tensor, *,
-                      prefill_slots: torch.Tensor, decode_slots: torch.Tensor,
-                      decode_pos: torch.Tensor, max_decode_len: int,
-                      cu_prefill: torch.Tensor | None = None) -> torch.Tensor:
-        """One continuous-batching step: ``prefill_ids`` [P, Tp] new sequences
-        (cache slots ``prefill_slots`` [P] int32), ``decode_ids`` [D] one token
-        for each running sequence (slots ``decode_slots`` [D] int32, positions
-        ``decode_pos`` [D] int64 = tokens already cached).  All tensors on the
-        device; nothing is read back on the host, so the step is capturable.
-        Returns the logits of each sequence's last token, [P + D, vocab]
-        (prefill sequences first)."""
-        _require_gpu(decode_ids)
-        P, T = int(prefill_ids.size(0)), int(prefill_ids.size(1))
-        D = int(decode_ids.size(0))
-        if cu_prefill is None:
-            cu_prefill = torch.arange(0, (P + 1) * T, T, dtype=torch.int32, device=decode_ids.device)
-        step = dict(n_prefill_seqs=P, prefill_len=T, prefill_slots=prefill_slots,
+    # ------------------------------------------------------------- runtime caches
+    def runtime_batch_capacity(self) -> int:
+        """Cache slots every layer holds."""
+        return min(int(layer.attn.recurrent_state.size(0)) if layer.layer_type == "kda"
+                   else int(layer.attn.latent_cache.size(0)) for layer in self.layers)
+
+    def ensure_batch_capacity(self, batch_size: int) -> None:
+        """Grow every layer's caches to at least ``batch_size`` slots, keeping
+        the cached rows (the reference grows them on demand,
+        test_dynamic_batch_capacity.py:29-51)."""
+        required = self.args.ensure_runtime_batch_capacity(int(batch_size))
+        for layer in self.layers:
+            layer.attn.ensure_batch_capacity(required)
+
+    def reset_slots(self, slots: torch.Tensor) -> None:
+        """Zero the KDA recurrent state and conv history of cache slots
+        ``slots`` in every layer (new sequences; MLA latents need no reset:
+        attention never reads past a sequence's own length)."""
+        for layer in self.layers:
+            if layer.layer_type == "kda":
+                layer.attn.reset_slots(slots)
+
+    def cache_dump(self, *, device: str = "cpu", cache_pos: int | None = None,
+                   batch_size: int | None = None,
+                   slots: torch.Tensor | None = None) -> RuntimeCacheSnapshot:
+        """Copies of every layer's caches (runtime_host.py:179-194): rows
+        [:batch_size] (default: every slot), or the cache slots ``slots`` in
+        that order; MLA latents up to ``cache_pos``."""
+        if slots is None:
+            active = self.runtime_batch_capacity() if batch_size is None else int(batch_size)
+            if active <= 0:
+                raise ValueError(f"batch_size must be >= 1, got {active}")
+            self.ensure_batch_capacity(active)
+        else:
+            active = int(slots.numel())
+        return RuntimeCacheSnapshot(layers=tuple(
+            layer.attn.cache_snapshot(device=device, batch_size=active, cache_pos=cache_pos, slots=slots)
+            for layer in self.layers))
+
+    def cache_load(self, cache_snapshot: RuntimeCacheSnapshot, *,
+                   slots: torch.Tensor | None = None) -> None:
+        """Load a snapshot (runtime_host.py:196-212): every layer's snapshot is
+        validated first, then all caches are reset and loaded into rows
+        [:batch].  With ``slots``, snapshot row i goes to cache slot slots[i]
+        and every other slot keeps its contents (no reset)."""
+        if not isinstance(cache_snapshot, RuntimeCacheSnapshot):
+            raise TypeError("cache snapshot must be a RuntimeCacheSnapshot")
+        if len(cache_snapshot.layers) > len(self.layers):
+            raise ValueError("cache snapshot has more layers than the model")
+        if slots is not None and int(slots.numel()) != cache_snapshot.batch_size():
+            raise ValueError(f"{int(slots.numel())} slots for a snapshot of "
+                             f"{cache_snapshot.batch_size()} rows")
+        required = cache_snapshot.batch_size() if slots is None else \
+            (int(slots.max()) + 1 if slots.numel() else 0)
+        if required:
+            self.ensure_batch_capacity(required)
+        for index, snapshot in enumerate(cache_snapshot.layers):
+            if snapshot is not None:
+                self.layers[index].attn.validate_cache_snapshot(snapshot)
+        if slots is None:
+            self.reset_runtime_cache()
+        for index, snapshot in enumerate(cache_snapshot.layers):
+            if snapshot is not None:
+                self.layers[index].attn.load_cache_snapshot(snapshot, slots=slots)
+
+    # ------------------------------------------------------------- packed steps
+    def forward_step(self, *, prefill_ids: torch.Tensor | None = None, prefill_lens=(),
+                     prefill_pos=None, prefill_slots: torch.Tensor | None = None,
+                     decode_ids: torch.Tensor | None = None,
+                     decode_slots: torch.Tensor | None = None,
+                     decode_pos: torch.Tensor | None = None,
+                     max_decode_len: int = 0, all_logits: bool = False) -> torch.Tensor:
+        """One continuous-batching step over packed rows, which the reference
+        cannot express (one start_pos per batch there, T > 1 only at
+        start_pos 0, transformer.py:146-160).
+
+        Prefill part: ``prefill_ids`` [sum(prefill_lens)] int64 holds the new
+        tokens of len(prefill_lens) sequences back to back (any lengths >= 1),
+        sequence i in cache slot ``prefill_slots[i]`` (int32, device) with
+        ``prefill_pos[i]`` tokens already cached (host ints; 0 = a new
+        sequence, whose KDA caches are zeroed here; > 0 = a prefill that
+        continues, reading its slot's caches: a long prompt is prefilled in
+        pieces across steps).  Decode part: ``decode_ids`` [D] one token for
+        each running sequence, slots ``decode_slots`` [D] int32, positions
+        ``decode_pos`` [D] int64 (tokens already cached, on the device), and
+        ``max_decode_len`` (host int) bounding pos + 1.
+
+        Returns the logits of each sequence's last token, [N + D, vocab]
+        (prefill sequences first); with ``all_logits``, of every row,
+        [sum(prefill_lens) + D, vocab].  With equal lengths and no continuation
+        nothing is copied from the host, so the step is capturable
+        (MixedStepGraph); otherwise small index tensors are built on the host.
+        """
+        dev = self.tok_embeddings.weight.device
+        lens = [int(t) for t in prefill_lens]
+        n_p = len(lens)
+        pos = [0] * n_p if prefill_pos is None else [int(p) for p in prefill_pos]
+        if len(pos) != n_p:
+            raise ValueError("prefill_pos needs one entry per prefill sequence")
+        if any(t < 1 for t in lens) or any(p < 0 for p in pos):
+            raise ValueError("prefill lengths must be >= 1 and positions >= 0")
+        if any(p + t > int(self.args.max_seq_len) for p, t in zip(pos, lens)):
+            raise ValueError("a prefill sequence exceeds max_seq_len")
+        rows = sum(lens)
+        if n_p and (prefill_ids is None or int(prefill_ids.numel()) != rows or prefill_slots is None
+                    or int(prefill_slots.numel()) != n_p):
+            raise ValueError("prefill_ids must hold sum(prefill_lens) tokens and prefill_slots one "
+                             "slot per sequence")
+        D = 0 if decode_ids is None else int(decode_ids.numel())
+        if D and (decode_slots is None or decode_pos is None or int(decode_slots.numel()) != D
+                  or int(decode_pos.numel()) != D):
+            raise ValueError("decode_slots and decode_pos need one entry per decode token")
+        if n_p + D == 0:
+            raise ValueError("empty step")
+        _require_gpu(prefill_ids if n_p else decode_ids)
+        reads = any(p > 0 for p in pos)
+        rect = n_p > 0 and not reads and min(lens) == max(lens)
+        step = dict(n_prefill_rows=rows, n_prefill_seqs=n_p, max_prefill_len=max(lens, default=0),
+                    prefill_slots=prefill_slots, reads_cache=reads, rectangular=rect,
                     decode_slots=decode_slots, decode_pos=decode_pos,
-                    max_decode_len=int(max_decode_len), cu_prefill=cu_prefill)
-        ids = torch.cat((prefill_ids.reshape(-1), decode_ids.reshape(-1)))
+                    max_decode_len=int(max_decode_len), cu_prefill=None, cu_prefill_host=None)
+        if n_p and rect:
+            T = lens[0]
+            step["cu_prefill"] = torch.arange(0, (n_p + 1) * T, T, dtype=torch.int32, device=dev)
+            last_pre = torch.arange(T - 1, n_p * T, T, device=dev)
+        elif n_p:
+            cu_host = torch.tensor([0] + list(itertools.accumulate(lens)), dtype=torch.int32)
+            step["cu_prefill_host"] = cu_host
+            step["cu_prefill"] = cu_host.to(dev)
+            seq_of_row = torch.repeat_interleave(torch.arange(n_p), torch.tensor(lens)).to(dev)
+            step["row_slot"] = prefill_slots.long()[seq_of_row]
+            step["row_pos"] = torch.cat([torch.arange(p, p + t) for p, t in zip(pos, lens)]).to(dev)
+            if reads:
+                klens = [p + t for p, t in zip(pos, lens)]
+                cuk_host = torch.tensor([0] + list(itertools.accumulate(klens)), dtype=torch.int32)
+                step["cu_keys_host"] = cuk_host
+                step["cu_keys"] = cuk_host.to(dev)
+                seq_of_key = torch.repeat_interleave(torch.arange(n_p), torch.tensor(klens)).to(dev)
+                step["key_slot"] = prefill_slots.long()[seq_of_key]
+                step["key_pos"] = torch.cat([torch.arange(kl) for kl in klens]).to(dev)
+                new = [i for i in range(n_p) if pos[i] == 0]
+                if new:
+                    self.reset_slots(prefill_slots.long()[torch.tensor(new, device=dev)])
+            last_pre = (cu_host[1:].long() - 1).to(dev)
+        ids = []
+        if n_p:
+            ids.append(prefill_ids.reshape(-1))
+        if D:
+            ids.append(decode_ids.reshape(-1))
+        ids = torch.cat(ids) if len(ids) > 1 else ids[0]
         hidden = self.tok_embeddings(ids)
         completed = depth_store(hidden, self.args.n_layers, self.args.attn_res_block_size)
         pending = None
         for layer in self.layers:
             hidden, completed, pending = layer.forward_mixed(hidden, completed, step,
                                                              pending=pending, defer=True)
-        last = torch.cat((torch.arange(T - 1, P * T, T, device=hidden.device),
-                          torch.arange(P * T, P * T + D, device=hidden.device)))
+        if all_logits:
+            return self.output(self._final_mix(hidden, completed, pending))
+        parts = []
+        if n_p:
+            parts.append(last_pre)
+        if D:
+            parts.append(torch.arange(rows, rows + D, device=hidden.device))
+        last = torch.cat(parts) if len(parts) > 1 else parts[0]
         return self.output(self._final_mix(hidden[last], completed[last],
                                            None if pending is None else pending[last]))
+
+    def forward_mixed(self, prefill_ids: torch.Tensor, decode_ids: torch.Tensor, *,
+                      prefill_slots: torch.Tensor, decode_slots: torch.Tensor,
+                      decode_pos: torch.Tensor, max_decode_len: int,
+                      cu_prefill: torch.Tensor | None = None) -> torch.Tensor:
+        """``forward_step`` for ``prefill_ids`` [P, Tp]: P new sequences of Tp
+        tokens each (cache slots ``prefill_slots`` [P] int32), plus
+        ``decode_ids`` [D] as in forward_step.  Nothing is read back on the
+        host, so the step is capturable (MixedStepGraph).  ``cu_prefill`` is
+        accepted for compatibility and must be the offsets of that rectangle.
+        Returns [P + D, vocab]."""
+        del cu_prefill
+        P, T = int(prefill_ids.size(0)), int(prefill_ids.size(1))
+        return self.forward_step(prefill_ids=prefill_ids if P else None, prefill_lens=[T] * P,
+                                 prefill_slots=prefill_slots, decode_ids=decode_ids,
+                                 decode_slots=decode_slots, decode_pos=decode_pos,
+                                 max_decode_len=max_decode_len)
 
 
 class MixedStepGraph:

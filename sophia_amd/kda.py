@@ -200,8 +200,15 @@ class SophiaKDA(nn.Module):
         self.recurrent_state.index_fill_(0, idx, 0.0)
         self.conv_state.index_fill_(0, idx, 0.0)
 
-    def cache_snapshot(self, *, device: str, batch_size: int, cache_pos: int | None):
+    def cache_snapshot(self, *, device: str, batch_size: int, cache_pos: int | None,
+                       slots: torch.Tensor | None = None):
+        """Copies of the caches of rows [:batch_size] (attention.py:212-216), or
+        of the cache slots ``slots`` in that order."""
         del cache_pos
+        if slots is not None:
+            idx = slots.to(device=self.recurrent_state.device, dtype=torch.long)
+            return LayerCacheSnapshot(recurrent=self.recurrent_state.index_select(0, idx).to(device),
+                                      conv=self.conv_state.index_select(0, idx).to(device))
         return LayerCacheSnapshot(recurrent=self.recurrent_state[:batch_size].to(device).clone(),
                                   conv=self.conv_state[:batch_size].to(device).clone())
 
@@ -215,8 +222,20 @@ class SophiaKDA(nn.Module):
                 and tuple(snapshot.conv.shape[1:]) != tuple(self.conv_state.shape[1:])):
             raise ValueError("KDA convolution cache shape mismatch")
 
-    def load_cache_snapshot(self, snapshot: LayerCacheSnapshot) -> None:
+    def load_cache_snapshot(self, snapshot: LayerCacheSnapshot, *,
+                            slots: torch.Tensor | None = None) -> None:
+        """attention.py:218-224; with ``slots``, row i of the snapshot goes to
+        cache slot slots[i] and the other slots are left as they are."""
         self.validate_cache_snapshot(snapshot)
+        if slots is not None:
+            idx = slots.to(device=self.recurrent_state.device, dtype=torch.long)
+            if snapshot.recurrent is not None:
+                self.recurrent_state.index_copy_(
+                    0, idx, snapshot.recurrent.to(self.recurrent_state.device, dtype=torch.float32))
+            if snapshot.conv is not None:
+                self.conv_state.index_copy_(
+                    0, idx, snapshot.conv.to(self.conv_state.device, dtype=torch.float32))
+            return
         required = snapshot.batch_size()
         self.ensure_batch_capacity(required)
         if snapshot.recurrent is not None:
@@ -419,17 +438,22 @@ class SophiaKDA(nn.Module):
 
 
     def forward_mixed(self, x: torch.Tensor, n_prefill: int, cu_prefill: torch.Tensor,
-                      prefill_slots: torch.Tensor | None, decode_slots: torch.Tensor | None
-                      ) -> torch.Tensor:
+                      prefill_slots: torch.Tensor | None, decode_slots: torch.Tensor | None, *,
+                      prefill_reads_cache: bool = False,
+                      cu_prefill_host: torch.Tensor | None = None) -> torch.Tensor:
         """One continuous-batching step over packed rows x [N, dim].
 
-        Rows [0, n_prefill) hold new sequences delimited by int32
-        ``cu_prefill`` (device, offsets from row 0); they start from empty
-        caches and leave their final recurrent and conv state in cache slots
-        ``prefill_slots``.  Rows [n_prefill, N) are one decode token each for
-        the sequences in ``decode_slots``, whose caches are read and advanced
-        in place (decode kernels).  One fused projection GEMM and one output
-        epilogue cover all rows.  Returns [N, dim].
+        Rows [0, n_prefill) hold prefill sequences delimited by int32
+        ``cu_prefill`` (device, offsets from row 0, any lengths).  Without
+        ``prefill_reads_cache`` they start from empty caches; with it each
+        continues from the recurrent state and conv history in its slot of
+        ``prefill_slots`` (a new sequence's slot must have been zeroed, e.g.
+        with ``reset_slots``).  Either way they leave their final state and
+        history in those slots.  Rows [n_prefill, N) are one decode token each
+        for the sequences in ``decode_slots``, whose caches are read and
+        advanced in place (decode kernels).  One fused projection GEMM and one
+        output epilogue cover all rows.  ``cu_prefill_host``: host copy of
+        ``cu_prefill`` (plans the prefill scan).  Returns [N, dim].
         """
         _require_gpu(x)
         x2 = x.reshape(-1, self.dim)
@@ -447,7 +471,8 @@ class SophiaKDA(nn.Module):
         conv_out = torch.empty((n, 3 * i), dtype=qkv.dtype, device=qkv.device)
         if n_prefill > 0:
             ops.short_conv_fwd(qkv[:n_prefill], conv_w, cu_prefill, conv_state=conv_state,
-                               state_slots=prefill_slots, read_history=False,
+                               state_slots=prefill_slots,
+                               read_history=bool(prefill_reads_cache) and hist > 0,
                                write_history=hist > 0, out=conv_out[:n_prefill],
                                weight_rounded=True)
         if n_decode > 0:
@@ -461,9 +486,10 @@ class SophiaKDA(nn.Module):
         gate_args = dict(A_log=self.A_log, dt_bias=self.dt_bias, lower_bound=self.lower_bound)
         if n_prefill > 0:
             ops.kda_chunk_fwd(q[:n_prefill], k[:n_prefill], v[:n_prefill], decay[:n_prefill],
-                              beta_logits[:n_prefill], cu_prefill, initial_state=None,
+                              beta_logits[:n_prefill], cu_prefill,
+                              initial_state=self.recurrent_state if prefill_reads_cache else None,
                               final_state=self.recurrent_state, state_slots=prefill_slots,
-                              out=o[:n_prefill], **gate_args)
+                              out=o[:n_prefill], cu_seqlens_cpu=cu_prefill_host, **gate_args)
         if n_decode > 0:
             ops.kda_decode_step(q[n_prefill:], k[n_prefill:], v[n_prefill:], decay[n_prefill:],
                                 beta_logits[n_prefill:], self.recurrent_state,

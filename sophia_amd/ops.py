@@ -653,15 +653,19 @@ def mla_decode_attn(qa: torch.Tensor, latent_cache: torch.Tensor, slots: torch.T
 
 def causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor,
                      max_len: int, *, scale: float | None = None,
+                     cu_seqlens_k: torch.Tensor | None = None,
                      out: torch.Tensor | None = None) -> torch.Tensor:
-    """Causal self-attention within each packed sequence (the no-cache prefill
-    attention of SophiaMLA, ml/runtime/model/attention.py:630-639,
-    ``scaled_dot_product_attention(q, k, v, is_causal=True)``).
+    """Causal self-attention within each packed sequence (the prefill
+    attention of SophiaMLA, ml/runtime/model/attention.py:630-654,
+    ``scaled_dot_product_attention`` with a causal mask).
 
-    q, k, v: [total, heads, 128] bf16 with dense [heads, 128] rows (row
-    strides free); cu_seqlens int32 [n + 1] on the device; ``max_len`` (host
-    int) must bound every sequence length.  Returns [total, heads, 128] bf16
-    (or writes ``out``, which may be a row-strided view)."""
+    q: [rows, heads, 128] bf16, the queries of the sequences delimited by
+    ``cu_seqlens`` (int32, device); k, v: the keys and values, delimited by
+    ``cu_seqlens_k`` (default: the same rows as q).  A sequence with more keys
+    than queries continues after cached tokens: its queries are the last
+    positions of its key range (the tril(keys - queries) mask).  ``max_len``
+    (host int) must bound every sequence's query count.  Returns [rows, heads,
+    128] bf16 (or writes ``out``, which may be a row-strided view)."""
     for t, name in ((q, "q"), (k, "k"), (v, "v")):
         _gpu(t, name)
         if t.dtype != torch.bfloat16:
@@ -672,9 +676,15 @@ def causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqle
     qs = _heads_rows(q, "q", heads, hd)
     ks = _heads_rows(k, "k", heads, hd)
     vs = _heads_rows(v, "v", heads, hd)
-    if int(k.size(0)) != total or int(v.size(0)) != total:
-        raise RuntimeError("q, k and v must have the same number of rows")
+    total_k = int(k.size(0))
+    if int(v.size(0)) != total_k:
+        raise RuntimeError("k and v must have the same number of rows")
     cu = _int32(cu_seqlens, "cu_seqlens", q.device)
+    cuk = _int32(cu_seqlens_k, "cu_seqlens_k", q.device)
+    if cuk is None and total_k != total:
+        raise RuntimeError("q, k and v must have the same number of rows without cu_seqlens_k")
+    if cuk is not None and int(cuk.numel()) != int(cu.numel()):
+        raise RuntimeError("cu_seqlens_k must have as many entries as cu_seqlens")
     y = out if out is not None else torch.empty((total, heads, hd), dtype=q.dtype, device=q.device)
     if y.dtype != torch.bfloat16 or tuple(y.shape) != (total, heads, hd):
         raise RuntimeError(f"out must be bfloat16 [{total}, {heads}, {hd}]")
@@ -682,8 +692,8 @@ def causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqle
     for t, name in ((q, "q"), (k, "k"), (v, "v")):
         _aligned(t, name)
     rc = nat.lib().sophia_causal_attention(
-        nat.ptr(q), qs, nat.ptr(k), ks, nat.ptr(v), vs, nat.ptr(y), os_, nat.ptr(cu),
-        int(cu.numel()) - 1, total, int(max_len), heads, hd,
+        nat.ptr(q), qs, nat.ptr(k), ks, nat.ptr(v), vs, nat.ptr(y), os_, nat.ptr(cu), nat.ptr(cuk),
+        int(cu.numel()) - 1, total, total_k, int(max_len), heads, hd,
         float(hd ** -0.5 if scale is None else scale), nat.DTYPE_BF16, nat.stream_handle(q.device))
     nat.check(rc, "sophia_causal_attention")
     return y

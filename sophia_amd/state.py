@@ -109,6 +109,17 @@ class RuntimeCacheSnapshot:
 
     layers: tuple = ()
 
+    def clone(self) -> "RuntimeCacheSnapshot":
+        return RuntimeCacheSnapshot(layers=tuple(None if layer is None else layer.clone()
+                                                 for layer in self.layers))
+
+    def is_empty(self) -> bool:
+        return all(layer is None or layer.is_empty() for layer in self.layers)
+
+    def batch_size(self) -> int:
+        """Rows of the largest cache tensor over all layers (0 when empty)."""
+        return max((layer.batch_size() for layer in self.layers if layer is not None), default=0)
+
     def to_payload(self) -> dict[str, torch.Tensor]:
         payload: dict[str, torch.Tensor] = {}
         for index, layer in enumerate(self.layers):

@@ -136,11 +136,11 @@ def test_host_side_queries_and_validation():
                                     16, 128, 3, None, 0, None)
     assert rc == nat.SOPHIA_ERR_INVALID and "workspace" in nat.last_error()
     # Causal attention: bf16 and head_dim 128 only.
-    rc = lib.sophia_causal_attention(16, 2048, 32, 2048, 48, 2048, 64, 2048, 80, 2, 100, 64, 16, 128,
-                                     0.08, 0, None)
+    rc = lib.sophia_causal_attention(16, 2048, 32, 2048, 48, 2048, 64, 2048, 80, None, 2, 100, 0, 64,
+                                     16, 128, 0.08, 0, None)
     assert rc == nat.SOPHIA_ERR_INVALID and "bf16" in nat.last_error()
-    rc = lib.sophia_causal_attention(16, 1024, 32, 1024, 48, 1024, 64, 1024, 80, 2, 100, 64, 16, 64,
-                                     0.08, 1, None)
+    rc = lib.sophia_causal_attention(16, 1024, 32, 1024, 48, 1024, 64, 1024, 80, None, 2, 100, 0, 64,
+                                     16, 64, 0.08, 1, None)
     assert rc == nat.SOPHIA_ERR_INVALID and "head_dim" in nat.last_error()
 
 

@@ -334,6 +334,41 @@ def test_causal_attention_matches_reference(lengths, heads):
     assert bool((big[:, 0].float() == 7.0).all()), "wrote outside the output view"
 
 
+@pytest.mark.parametrize("queries,keys,heads", [((1, 77, 200, 64, 5), (1, 300, 200, 1000, 70), 2),
+                                                 ((1024, 3), (1024, 2051), 16), ((0, 128), (40, 129), 1)])
+def test_causal_attention_after_cached_keys_matches_reference(queries, keys, heads):
+    """Queries that continue after cached keys (cu_seqlens_k): sequence s has
+    queries[s] query rows and keys[s] >= queries[s] key rows, and query i sits
+    at position i + keys[s] - queries[s] (the tril(klen - seqlen) mask of
+    ml/runtime/model/attention.py:641-654), against a float32 reference
+    computed per sequence.  Same tolerance as above (bf16 probabilities)."""
+    from sophia_amd import ops
+    dev = _dev()
+    g = torch.Generator(device="cpu").manual_seed(sum(keys) + heads)
+    tq, tk = sum(queries), sum(keys)
+    cu = torch.tensor([0] + list(np.cumsum(queries)), dtype=torch.int32)
+    cuk = torch.tensor([0] + list(np.cumsum(keys)), dtype=torch.int32)
+    q = torch.randn(tq, heads, 128, generator=g).to(dev, torch.bfloat16)
+    k = torch.randn(tk, heads, 128, generator=g).to(dev, torch.bfloat16)
+    v = torch.randn(tk, heads, 128, generator=g).to(dev, torch.bfloat16)
+    scale = 128 ** -0.5
+    y = ops.causal_attention(q, k, v, cu.to(dev), max(queries), scale=scale, cu_seqlens_k=cuk.to(dev))
+    torch.cuda.synchronize()
+    qf, kf, vf = (t.float().cpu() for t in (q, k, v))
+    ref = torch.zeros(tq, heads, 128)
+    for s in range(len(queries)):
+        a, b, ka, kb = int(cu[s]), int(cu[s + 1]), int(cuk[s]), int(cuk[s + 1])
+        nq, nk = b - a, kb - ka
+        if nq == 0:
+            continue
+        sc = torch.einsum("thd,shd->hts", qf[a:b], kf[ka:kb]) * scale
+        allow = torch.ones(nq, nk, dtype=torch.bool).tril(nk - nq)
+        sc = sc.masked_fill(~allow, float("-inf"))
+        ref[a:b] = torch.einsum("hts,shd->thd", torch.softmax(sc, dim=-1), vf[ka:kb])
+    err = float((y.float().cpu() - ref).abs().max()) / float(ref.abs().max())
+    assert err <= 1e-2, err
+
+
 def test_mla_prefill_bf16_kernel_matches_sdpa_path():
     """SophiaMLA.forward in bf16 (HIP causal kernel) against the same module in
     fp32 (torch SDPA) on the same weights and input."""
