@@ -42,10 +42,24 @@ PREFILL_BYTES_PER_TOKEN = HEADS * (4 * DIM * 2 + DIM * 4 + 4)          # 24,640
 # Causal chunk-form flops per token at C = 64: H * (5 C d + 6 d^2).
 PREFILL_FLOPS_PER_TOKEN = HEADS * (5 * 64 * DIM + 6 * DIM * DIM)      # 2,228,224
 METRIC = "KDA prefill tokens/s + % MFMA peak; decode-step µs and HBM GB/s at B=256"
-# HBM bytes per launch measured with rocprofv3 on this workload (FETCH_SIZE and
-# WRITE_SIZE in separate passes; FETCH_SIZE doubled, the factor a plain 1 GiB
-# device copy gives on MI355X).  Re-measured whenever a kernel changes.
-MEASURED_TRAFFIC_BYTES = {"prefill": 794.9e6, "decode": 548.8e6, "short_conv": 321.2e6}
+# HBM bytes per launch come from the rocprofv3 counter summary committed under
+# profiles/ (FETCH_SIZE and WRITE_SIZE in separate passes, calibrated on a plain
+# 1 GiB device copy); the summary carries them in a fenced ```json block with
+# the kernel build they were measured on.  Missing figures are reported as null.
+TRAFFIC_PROFILE = os.path.join(HERE, "profiles", "hbm_traffic_counters.md")
+
+
+def measured_traffic() -> dict:
+    """{"bytes": {workload: bytes per call}, "source": ...} parsed from the
+    counter summary, or empty figures when it is absent."""
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+        block = text.split("```json", 1)[1].split("```", 1)[0]
+        data = json.loads(block)
+        return {"bytes": data.get("traffic_bytes_per_call", {}),
+                "source": f"profiles/hbm_traffic_counters.md ({data.get('measured', 'undated')})"}
+    except (OSError, IndexError, ValueError):
+        return {"bytes": {}, "source": None}
 
 
 def prefill_lengths(seed: int = 0, n: int = 8, lo: int = 256, hi: int = 4096) -> list[int]:
@@ -132,6 +146,131 @@ def cpu_baseline(inputs, lengths, budget_s: float = 10.0):
                       f"{elapsed:.1f} s by the C per-token fp32 recurrence of the reference's "
                       f"CPU path (OpenMP over sequence x head, {cores} threads); "
                       f"os.cpu_count()={os.cpu_count()}"}
+
+
+def _threads(torch) -> dict:
+    return {"os_cpu_count": os.cpu_count(), "affinity_cores": len(os.sched_getaffinity(0)),
+            "torch_threads": torch.get_num_threads()}
+
+
+def _timed(fn, budget_s: float, min_reps: int = 1) -> tuple[int, float]:
+    reps, elapsed = 0, 0.0
+    while elapsed < budget_s or reps < min_reps:
+        t0 = time.perf_counter()
+        fn()
+        elapsed += time.perf_counter() - t0
+        reps += 1
+    return reps, elapsed
+
+
+def cpu_baselines(torch, budget_s: float = 4.0) -> dict:
+    """The reference's CPU path for the other configurations, restated by the
+    oracle and timed on this host (fp32 throughout):
+      config 1: the whole mixer layer (numpy restatement of SophiaKDA.forward,
+                B = 1, T = 512, dim 1536, seed-42 init draws), ms per forward;
+      config 3: one decode step of 256 sequences (C per-token recurrence,
+                OpenMP over sequence x head, plus the conv step), us per step;
+      config 4: the first 8,192 tokens of the 65,536-token sequence (C
+                recurrence, 16 (sequence, head) pairs in parallel), tokens/s."""
+    from oracle import c_oracle
+    from oracle import kda_oracle as ko
+    cores = len(os.sched_getaffinity(0))
+    out = {}
+    # config 1
+    from sophia_amd.config import ModelArgs
+    from sophia_amd.kda import SophiaKDA
+    torch.manual_seed(42)
+    params = {k: v.detach().numpy() for k, v in SophiaKDA(ModelArgs(max_batch_size=1)).state_dict().items()}
+    x = np.random.default_rng(0).standard_normal((1, 512, 1536)).astype(np.float32)
+    reps, el = _timed(lambda: ko.mixer_forward(params, x, num_heads=16), budget_s)
+    out["config1_mixer_layer"] = {
+        "value": round(el / reps * 1e3, 1), "unit": "ms/forward", "cores": cores, "kind": "port",
+        "sample": f"B=1, T=512, dim 1536 forward run {reps} times: numpy restatement of "
+                  f"SophiaKDA.forward in fp32 (BLAS GEMMs on the host's threads, the per-token "
+                  f"recurrence serial)", **_threads(torch)}
+    # config 3
+    rng = np.random.default_rng(3)
+    b, h = 256, 16
+    q = rng.standard_normal((b, h, 128)).astype(np.float32)
+    k = rng.standard_normal((b, h, 128)).astype(np.float32)
+    v = rng.standard_normal((b, h, 128)).astype(np.float32)
+    g = rng.uniform(-5.0, 0.0, (b, h, 128)).astype(np.float32)
+    beta = (1 / (1 + np.exp(-rng.standard_normal((b, h))))).astype(np.float32)
+    s0 = (rng.standard_normal((b, h, 128, 128)) * 0.02).astype(np.float32)
+    cu = np.arange(b + 1, dtype=np.int32)
+    xc = rng.standard_normal((b, 1, 3 * h * 128)).astype(np.float32)
+    wc = (rng.standard_normal((3 * h * 128, 4)) * 0.02).astype(np.float32)
+    hist = rng.standard_normal((b, 3 * h * 128, 3)).astype(np.float32)
+
+    def decode():
+        ko.short_conv(xc, wc, hist)
+        c_oracle.kda_varlen(q, k, v, g, beta, cu, initial_states=s0, use_gate=False,
+                            use_beta_sigmoid=False, nthreads=cores)
+
+    reps, el = _timed(decode, budget_s)
+    out["config3_decode_step"] = {
+        "value": round(el / reps * 1e6, 1), "unit": "us/step", "cores": cores, "kind": "port",
+        "sample": f"B=256 one-token step run {reps} times: C per-token recurrence (OpenMP over 4,096 "
+                  f"sequence x head pairs, {cores} threads) plus the numpy conv step", **_threads(torch)}
+    # config 4
+    t4 = 8192
+    gen = torch.Generator().manual_seed(10)
+    q4 = torch.nn.functional.normalize(torch.randn(t4, h, 128, generator=gen), dim=-1).numpy()
+    k4 = torch.nn.functional.normalize(torch.randn(t4, h, 128, generator=gen), dim=-1).numpy()
+    v4 = torch.randn(t4, h, 128, generator=gen).numpy()
+    g4 = (torch.rand(t4, h, 128, generator=gen) * -4.5 - 0.5).numpy()
+    b4 = torch.sigmoid(torch.randn(t4, h, generator=gen)).numpy()
+    cu4 = np.array([0, t4], dtype=np.int32)
+    reps, el = _timed(lambda: c_oracle.kda_varlen(q4, k4, v4, g4, b4, cu4, use_gate=False,
+                                                  use_beta_sigmoid=False, nthreads=cores), budget_s)
+    out["config4_long_prefill"] = {
+        "value": round(t4 * reps / el, 1), "unit": "tokens/s", "cores": min(cores, h), "kind": "port",
+        "sample": f"first 8,192 tokens of the 65,536-token sequence x 16 heads run {reps} times: C "
+                  f"per-token recurrence, one thread per head (16 pairs)", **_threads(torch)}
+    return out
+
+
+def long_prefill_bench(torch, dev, stream, steps: int, warmup: int, traffic: dict) -> dict:
+    """Config 4: one sequence of 65,536 tokens (1,024 chunks), 16 heads, bf16
+    q/k/v/o, fp32 g ~ U[-5, -0.5] and beta, zero initial state, final state
+    written; timed like the headline prefill."""
+    from sophia_amd import ops
+    total = 65536
+    gen = torch.Generator().manual_seed(10)
+    shape = (total, HEADS, DIM)
+    q = torch.nn.functional.normalize(torch.randn(shape, generator=gen), dim=-1).to(torch.bfloat16).to(dev)
+    k = torch.nn.functional.normalize(torch.randn(shape, generator=gen), dim=-1).to(torch.bfloat16).to(dev)
+    v = torch.randn(shape, generator=gen).to(torch.bfloat16).to(dev)
+    g = (torch.rand(shape, generator=gen) * -4.5 - 0.5).to(dev)
+    beta = torch.sigmoid(torch.randn((total, HEADS), generator=gen)).to(dev)
+    cu_cpu = torch.tensor([0, total], dtype=torch.int32)
+    cu = cu_cpu.to(dev)
+    final = torch.zeros((1, HEADS, DIM, DIM), device=dev)
+    out = torch.empty(shape, dtype=torch.bfloat16, device=dev)
+
+    def call():
+        ops.kda_chunk_fwd(q, k, v, g, beta, cu, use_qk_l2norm=True, use_gate=False,
+                          use_beta_sigmoid=False, final_state=final, out=out, cu_seqlens_cpu=cu_cpu)
+
+    _, per = time_events(torch, call, steps, warmup, stream)
+    eager = float(np.mean(per))
+    graph = graph_ms_per_call(torch, dev, call, max(steps // 2, 3), stream, per_graph=4)
+    ms = min(eager, graph)
+    if not torch.isfinite(out.float()).all():
+        raise RuntimeError("non-finite long-prefill output")
+    gbs = total * PREFILL_BYTES_PER_TOKEN / (ms / 1e3) / 1e9
+    tflops = total * PREFILL_FLOPS_PER_TOKEN / (ms / 1e3) / 1e12
+    return {"workload": "KDA chunk prefill, one sequence of 65,536 tokens (1,024 chunks), 16 heads x 128, "
+                        "bf16 q/k/v/o, fp32 g ~ U[-5,-0.5] / beta / state",
+            "tokens_per_s": round(total / (ms / 1e3), 1), "ms_per_call": round(ms, 4),
+            "ms_eager": round(eager, 4), "ms_graph": round(graph, 4),
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "traffic": traffic["bytes"].get("long_prefill"),
+                         "traffic_source": traffic["source"],
+                         "algorithmic_bytes_per_launch": total * PREFILL_BYTES_PER_TOKEN},
+            "mfma": {"achieved_tflops": round(tflops, 2),
+                     "frac_of_peak": round(tflops / BF16_PEAK_TFLOPS, 4)}}
 
 
 def copy_bandwidth(torch, dev, stream, nbytes: int = 1 << 30) -> float:
@@ -258,7 +397,7 @@ def main(argv=None) -> int:
     ap.add_argument("--tune-gemms", metavar="CSV", default=None,
                     help="time the mixed step's library GEMM candidates and write the "
                          "per-shape selection to CSV (torch TunableOp)")
-    ap.add_argument("--only", choices=["all", "kda", "prefill", "conv", "decode", "copy", "mixed"],
+    ap.add_argument("--only", choices=["all", "kda", "prefill", "conv", "decode", "copy", "mixed", "long"],
                     default="all",
                     help="run one workload only (for kernel profiling; 'kda' = prefill, ShortConv "
                          "and decode without the decoder step); the JSON line then carries that "
@@ -288,6 +427,7 @@ def main(argv=None) -> int:
                           "bytes_written_per_copy": 1 << 30}), flush=True)
         return 0
 
+    traffic = measured_traffic()
     lengths = prefill_lengths()
     total = int(sum(lengths))
     inp = make_prefill_inputs(torch, dev, lengths)
@@ -330,7 +470,7 @@ def main(argv=None) -> int:
                    "kernel_ms_graph": round(graph_ms, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": MEASURED_TRAFFIC_BYTES["prefill"],
+                     "traffic": traffic["bytes"].get("prefill"), "traffic_source": traffic["source"],
                      "kernel": "kda_chunk_intra + kda_chunk_scan (one call)",
                      "algorithmic_bytes_per_launch": total * PREFILL_BYTES_PER_TOKEN},
         "mfma": {"achieved_tflops": round(tflops, 2), "peak_tflops": BF16_PEAK_TFLOPS,
@@ -369,7 +509,7 @@ def main(argv=None) -> int:
                                 "us_graph": round(cgraph * 1e3, 2),
                                 "GBps": round(cbytes / (cms / 1e3) / 1e9, 1),
                                 "algorithmic_bytes": cbytes,
-                                "traffic": MEASURED_TRAFFIC_BYTES["short_conv"]}
+                                "traffic": traffic["bytes"].get("short_conv")}
     del xconv, yconv, conv_state
 
     # Decode step at B = 256.
@@ -405,10 +545,13 @@ def main(argv=None) -> int:
                             "us_per_step_eager": round(eager_ms * 1e3, 2),
                             "us_per_step_graph": round(graph_ms * 1e3, 2),
                             "algorithmic_bytes": dbytes, "steps": dsteps,
-                            "traffic": MEASURED_TRAFFIC_BYTES["decode"],
+                            "traffic": traffic["bytes"].get("decode"),
                             "kernel": "kda_decode_kernel"}
     del dstate
 
+    if args.only in ("all", "kda", "long"):
+        result["long_prefill"] = long_prefill_bench(torch, dev, stream, max(args.steps // 2, 5),
+                                                    max(args.warmup // 2, 2), traffic)
     if args.only in ("all", "mixed"):
         result["mixed_step"] = mixed_step_bench(torch, dev, stream, max(args.steps // 2, 5),
                                                 max(args.warmup // 2, 2),
@@ -417,6 +560,8 @@ def main(argv=None) -> int:
         result["hbm_copy_GBps"] = round(copy_bandwidth(torch, dev, stream), 1)
     if not args.no_cpu and args.only == "all":
         result["cpu_baseline"] = cpu_baseline(inp, lengths)
+        result["cpu_baseline"].update(_threads(torch))
+        result["cpu_baselines_other_configs"] = cpu_baselines(torch)
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)
