@@ -179,6 +179,32 @@ int sophia_kda_decode_step(const void *q, const void *k, const void *v, int64_t 
                            const int32_t *state_slots, int read_state, int batch, int num_heads,
                            int head_dim, void *o, int64_t o_row_stride, void *stream);
 
+/*
+ * One decode step of a KDA layer with its ShortConv: the one-token conv of
+ * the q, k and v channels (CausalDepthwiseConv1d.forward with T == 1 on the
+ * cached history, attention.py:32-60,236-257) followed by the recurrent step
+ * of sophia_kda_decode_step, in one launch.
+ *   x_q, x_k, x_v : [batch, H, 128] pre-conv projection rows (row stride
+ *                   x_row_stride elements, dtype qkv_dtype); the conv output is
+ *                   rounded to that dtype, as the separate ShortConv writes it.
+ *   conv_weight   : [3 * H * 128, kernel_size] fp32 taps (q | k | v channels,
+ *                   rounded to the activation dtype), 16-byte aligned.
+ *   conv_state    : [n_state_slots, 3 * H * 128, kernel_size - 1] fp32 history,
+ *                   the slot of each row shifted by one token in place.
+ *   kernel_size   : 4.
+ * Other arguments as sophia_kda_decode_step; read_state == 0 treats both the
+ * recurrent state and the conv history as zero.  Results are those of
+ * sophia_short_conv_step followed by sophia_kda_decode_step.
+ */
+int sophia_kda_decode_conv_step(const void *x_q, const void *x_k, const void *x_v, int64_t x_row_stride,
+                                int qkv_dtype, const float *conv_weight, float *conv_state, int kernel_size,
+                                const void *g, int64_t g_row_stride, int g_dtype, const void *beta,
+                                int64_t beta_row_stride, int beta_dtype, const float *A_log,
+                                const float *dt_bias, float scale, float lower_bound, unsigned flags,
+                                float *state, int n_state_slots, const int32_t *state_slots, int read_state,
+                                int batch, int num_heads, int head_dim, void *o, int64_t o_row_stride,
+                                void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -56,6 +56,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "sophia_kda_decode_step": (_i32, [_vp, _vp, _vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64, _i32,
                                       _vp, _vp, _f32, _f32, _u32, _vp, _i32, _vp, _i32, _i32, _i32,
                                       _i32, _vp, _i64, _vp]),
+    "sophia_kda_decode_conv_step": (_i32, [_vp, _vp, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _i64, _i32,
+                                           _vp, _i64, _i32, _vp, _vp, _f32, _f32, _u32, _vp, _i32,
+                                           _vp, _i32, _i32, _i32, _i32, _vp, _i64, _vp]),
     "sophia_attn_res_mix": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i32, _vp, _vp,
                                    _f32, _vp, _f32, _vp, _i64, _i64, _i32, _i32, _vp]),
     "sophia_situ_glu": (_i32, [_vp, _i64, _vp, _i64, _i64, _i32, _f32, _f32, _i32, _vp]),

@@ -45,6 +45,11 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
          (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
 }
 
+// x rounded to the given element type and back (identity for fp32).
+__device__ __forceinline__ float as_dtype(float x, int dtype) {
+  return dtype == SOPHIA_DTYPE_BF16 ? bf16_bits_to_f32(f32_to_bf16_bits(x)) : x;
+}
+
 // Loads one element of either dtype as float.
 __device__ __forceinline__ float load_elem(const void *base, int64_t idx, int dtype) {
   if (dtype == SOPHIA_DTYPE_BF16)

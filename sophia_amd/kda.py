@@ -475,7 +475,8 @@ class SophiaKDA(nn.Module):
                                read_history=bool(prefill_reads_cache) and hist > 0,
                                write_history=hist > 0, out=conv_out[:n_prefill],
                                weight_rounded=True)
-        if n_decode > 0:
+        fused_decode = n_decode > 0 and hist == 3
+        if n_decode > 0 and not fused_decode:
             ops.short_conv_step(qkv[n_prefill:], conv_w, conv_state, state_slots=decode_slots,
                                 read_history=True, out=conv_out[n_prefill:], weight_rounded=True)
         q = conv_out[:, :i].unflatten(1, (h, d))
@@ -490,7 +491,12 @@ class SophiaKDA(nn.Module):
                               initial_state=self.recurrent_state if prefill_reads_cache else None,
                               final_state=self.recurrent_state, state_slots=prefill_slots,
                               out=o[:n_prefill], cu_seqlens_cpu=cu_prefill_host, **gate_args)
-        if n_decode > 0:
+        if fused_decode:
+            # ShortConv step and recurrent step of the decode rows in one launch.
+            ops.kda_decode_conv_step(qkv[n_prefill:], conv_w, conv_state, decay[n_prefill:],
+                                     beta_logits[n_prefill:], self.recurrent_state,
+                                     state_slots=decode_slots, out=o[n_prefill:], **gate_args)
+        elif n_decode > 0:
             ops.kda_decode_step(q[n_prefill:], k[n_prefill:], v[n_prefill:], decay[n_prefill:],
                                 beta_logits[n_prefill:], self.recurrent_state,
                                 state_slots=decode_slots, read_state=True, out=o[n_prefill:],

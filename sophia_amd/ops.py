@@ -325,6 +325,69 @@ def kda_decode_step(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.
     return o
 
 
+def kda_decode_conv_step(x_qkv: torch.Tensor, conv_weight: torch.Tensor, conv_state: torch.Tensor,
+                         g: torch.Tensor, beta: torch.Tensor, state: torch.Tensor, *, A_log=None,
+                         dt_bias=None, scale: float | None = None, lower_bound: float = -5.0,
+                         use_qk_l2norm: bool = True, use_gate: bool = True,
+                         use_beta_sigmoid: bool = True, state_slots: torch.Tensor | None = None,
+                         read_state: bool = True, out: torch.Tensor | None = None) -> torch.Tensor:
+    """One decode step of a KDA layer with its ShortConv in one launch:
+    ``short_conv_step`` of the q | k | v channels followed by
+    ``kda_decode_step`` (attention.py:236-257, 330-348).
+
+    x_qkv: [B, 3 * H * 128] pre-conv projection rows (dense rows, row stride
+    free); conv_weight: [3 * H * 128, 4] fp32 taps already rounded to
+    x_qkv.dtype (contiguous); conv_state: fp32 [slots, 3 * H * 128, 3], each
+    row's slot shifted in place; g: [B, H, 128]; beta: [B, H]; state: fp32
+    [slots, H, 128, 128] updated in place.  Returns o [B, H, 128] in
+    x_qkv.dtype."""
+    for t, name in ((x_qkv, "x_qkv"), (g, "g"), (beta, "beta")):
+        _gpu(t, name)
+    device = x_qkv.device
+    batch = int(x_qkv.size(0))
+    heads = int(g.size(1)) if g.dim() == 3 else 0
+    inner = heads * HEAD_DIM
+    xs = _rows(x_qkv, "x_qkv", 3 * inner)
+    gs = _heads_rows(g, "g", heads, HEAD_DIM)
+    bs = _rows(beta, "beta", heads)
+    for t, name in ((g, "g"), (beta, "beta")):
+        _nrows(t, name, batch)
+    if (conv_weight.dtype != torch.float32 or not conv_weight.is_contiguous()
+            or tuple(conv_weight.shape) != (3 * inner, 4) or conv_weight.device != device):
+        raise RuntimeError(f"conv_weight must be contiguous fp32 [{3 * inner}, 4] on {device}")
+    _gpu(conv_state, "conv_state")
+    if (conv_state.dtype != torch.float32 or not conv_state.is_contiguous()
+            or tuple(conv_state.shape[1:]) != (3 * inner, 3)):
+        raise RuntimeError(f"conv_state must be contiguous fp32 [slots, {3 * inner}, 3]")
+    _state(state, "state", heads, device)
+    if int(conv_state.size(0)) != int(state.size(0)):
+        raise RuntimeError("conv_state and state must have the same number of slots")
+    slots = _int32(state_slots, "state_slots", device)
+    _slot_count(slots, batch)
+    if slots is None and int(state.size(0)) < batch:
+        raise RuntimeError("state has fewer slots than the batch")
+    a_log, dtb = _gate_params(use_gate, A_log, dt_bias, heads, device)
+    if scale is None:
+        scale = HEAD_DIM ** -0.5
+    o = out if out is not None else torch.empty((batch, heads, HEAD_DIM), dtype=x_qkv.dtype,
+                                                device=device)
+    os_ = _heads_rows(o, "out", heads, HEAD_DIM)
+    _nrows(o, "out", batch)
+    if o.dtype != x_qkv.dtype:
+        raise RuntimeError("out must have x_qkv's dtype")
+    base = x_qkv.data_ptr()
+    esz = x_qkv.element_size()
+    rc = nat.lib().sophia_kda_decode_conv_step(
+        base, base + inner * esz, base + 2 * inner * esz, xs, nat.dtype_code(x_qkv.dtype),
+        nat.ptr(conv_weight), nat.ptr(conv_state), 4, nat.ptr(g), gs, nat.dtype_code(g.dtype),
+        nat.ptr(beta), bs, nat.dtype_code(beta.dtype), nat.ptr(a_log), nat.ptr(dtb), float(scale),
+        float(lower_bound), _flags(use_qk_l2norm, use_gate, use_beta_sigmoid), nat.ptr(state),
+        int(state.size(0)), nat.ptr(slots), int(bool(read_state)), batch, heads, HEAD_DIM,
+        nat.ptr(o), os_, nat.stream_handle(device))
+    nat.check(rc, "sophia_kda_decode_conv_step")
+    return o
+
+
 # -------------------------------------------- flash-linear-attention signatures
 def _detached(t):
     """Gate parameters enter the kernels as values (the forward-only kernels

@@ -498,3 +498,59 @@ def test_decode_step_config3_batch256():
     assert _rel(_np(state)[rows], s_ref) < 1e-4
     # every row was updated in place
     assert bool((state - s0.to(dev)).abs().amax(dim=(1, 2, 3)).gt(0).all())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_decode_conv_step_matches_separate_launches_and_oracle(dtype):
+    """sophia_kda_decode_conv_step (ShortConv step + recurrent step in one
+    launch) against short_conv_step followed by kda_decode_step: the conv
+    history is bit-identical; outputs and states agree to rounding (the fused
+    kernel runs one work-group of 128 value columns, which sums the column
+    reductions in another order); both against the oracle.  Includes a row
+    whose slot is out of range (output 0, no cache touched)."""
+    from sophia_amd import ops
+    dev = _dev()
+    rng = np.random.default_rng(21)
+    batch, heads = 9, 3
+    inner = heads * 128
+    x = rng.standard_normal((batch, 3 * inner)).astype(np.float32)
+    w = (rng.standard_normal((3 * inner, 4)) * 0.5).astype(np.float32)
+    z = (rng.standard_normal((batch, heads, 128)) * 2.0).astype(np.float32)
+    b = rng.standard_normal((batch, heads)).astype(np.float32)
+    a_log = (rng.standard_normal(heads) * 0.3).astype(np.float32)
+    dtb = ko.inverse_softplus(np.exp(rng.uniform(np.log(1e-3), np.log(1e-1), inner))).astype(np.float32)
+    slots = np.array([4, 0, 9, 2, 7, 1, 8, 3, 11], dtype=np.int32)   # 11 is out of range
+    s0 = (rng.standard_normal((10, heads, 128, 128)) * 0.02).astype(np.float32)
+    c0 = rng.standard_normal((10, 3 * inner, 3)).astype(np.float32)
+    xt = torch.tensor(x).to(dtype).to(dev)
+    wt = torch.tensor(w).to(dtype).float().to(dev)             # taps rounded to the activation dtype
+    kw = dict(A_log=torch.tensor(a_log), dt_bias=torch.tensor(dtb), state_slots=torch.tensor(slots, device=dev))
+    zt, bt = torch.tensor(z, device=dev), torch.tensor(b, device=dev)
+    # separate launches
+    st_a, cs_a = torch.tensor(s0, device=dev), torch.tensor(c0, device=dev)
+    y = ops.short_conv_step(xt, wt, cs_a, state_slots=kw["state_slots"], read_history=True, weight_rounded=True)
+    q, k, v = (y[:, i * inner:(i + 1) * inner].unflatten(1, (heads, 128)) for i in range(3))
+    o_a = ops.kda_decode_step(q, k, v, zt, bt, st_a, **kw)
+    # fused
+    st_b, cs_b = torch.tensor(s0, device=dev), torch.tensor(c0, device=dev)
+    o_b = ops.kda_decode_conv_step(xt, wt, cs_b, zt, bt, st_b, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(cs_a, cs_b), "conv history differs"
+    tol = 1e-4 if dtype == torch.float32 else 1e-2
+    assert _rel(_np(o_b), _np(o_a)) < tol
+    assert _rel(_np(st_b), _np(st_a)) < 1e-5
+    assert np.all(_np(o_b)[8] == 0.0)
+    untouched = [5, 6]
+    assert torch.equal(st_b[untouched], torch.tensor(s0[untouched], device=dev))
+    # oracle: conv step then recurrent step in float64
+    ok = slots < 10
+    xs = _np(xt)[ok]
+    hist = c0[slots[ok]]
+    hist_in = _np(torch.tensor(hist).to(dtype)) if dtype == torch.bfloat16 else hist
+    yr, _ = ko.short_conv(xs[:, None].astype(np.float64), _np(wt).astype(np.float64), hist_in.astype(np.float64))
+    yr = _np(torch.tensor(yr[:, 0]).to(dtype))
+    qr, kr, vr = (yr[:, i * inner:(i + 1) * inner].reshape(-1, heads, 128) for i in range(3))
+    o_ref, s_ref = ko.kda_decode_step(qr, kr, vr, z[ok], b[ok], s0[slots[ok]], A_log=a_log, dt_bias=dtb,
+                                      dtype=np.float64)
+    assert _rel(_np(o_b)[ok], o_ref) < REL_TOL
+    assert _rel(_np(st_b)[slots[ok]], s_ref) < REL_TOL
