@@ -205,6 +205,46 @@ int sophia_kda_decode_conv_step(const void *x_q, const void *x_k, const void *x_
                                 int batch, int num_heads, int head_dim, void *o, int64_t o_row_stride,
                                 void *stream);
 
+/*
+ * Backward of the prefill (training).  Replaces FlashKDA's chunk_kda_train_bwd
+ * followed by l2norm_bwd and fused_beta_sigmoid_bwd, as FlashKDAFunction.
+ * backward calls them (ml/training/pretrain/engine/sm120_concurrent_ffn.py:
+ * 301-373): the gradients of o = KDA(q, k, v, g, beta; h0) and of its final
+ * states with respect to every input, the l2 norms, the gate and the beta
+ * sigmoid included (same flags as sophia_kda_chunk_fwd).
+ *   q, k, v, g, beta, A_log, dt_bias, scale, lower_bound, flags, cu_seqlens,
+ *                     n_seqs, total_tokens, num_heads, head_dim:
+ *                     the forward's inputs, as for sophia_kda_chunk_fwd.
+ *   initial_state   : [n_seqs, H, 128, 128] fp32 per sequence, or NULL (zeros).
+ *   d_out           : [total, H, 128] gradient of o (row stride in elements),
+ *                     dtype SOPHIA_DTYPE_F32 or _BF16.
+ *   d_final_state   : [n_seqs, H, 128, 128] fp32 gradient of the final states,
+ *                     or NULL (zeros).
+ * Outputs, fp32, dense:
+ *   dq, dk, dv, dg  : [total, H, 128]   (dg with respect to the g input: the
+ *                                        decay logits when the gate is applied
+ *                                        in the kernel, else the log-decay)
+ *   dbeta           : [total, H]         (with respect to the beta input)
+ *   d_initial_state : [n_seqs, H, 128, 128] or NULL (not computed)
+ *   dA_log          : [H] or NULL        (only with SOPHIA_KDA_GATE_IN_KERNEL)
+ *   ddt_bias        : [H * 128] or NULL  (only with SOPHIA_KDA_GATE_IN_KERNEL)
+ * workspace: device memory of sophia_kda_chunk_bwd_workspace_size() bytes,
+ * 256-byte aligned.  Arithmetic is fp32 throughout; sums over tokens and value
+ * columns run in a fixed order (results are deterministic).
+ */
+size_t sophia_kda_chunk_bwd_workspace_size(int64_t total_tokens, int n_seqs, int num_heads,
+                                           int head_dim);
+int sophia_kda_chunk_bwd(const void *q, const void *k, const void *v, int64_t qkv_row_stride,
+                         int qkv_dtype, const void *g, int64_t g_row_stride, int g_dtype,
+                         const void *beta, int64_t beta_row_stride, int beta_dtype, const float *A_log,
+                         const float *dt_bias, float scale, float lower_bound, unsigned flags,
+                         const int32_t *cu_seqlens, int n_seqs, int64_t total_tokens, int num_heads,
+                         int head_dim, const float *initial_state, const void *d_out,
+                         int64_t d_out_row_stride, int d_out_dtype, const float *d_final_state, float *dq,
+                         float *dk, float *dv, float *dg, float *dbeta, float *d_initial_state,
+                         float *dA_log, float *ddt_bias, void *workspace, size_t workspace_bytes,
+                         void *stream);
+
 #ifdef __cplusplus
 }
 #endif

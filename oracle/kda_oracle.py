@@ -25,6 +25,11 @@ Parity status of each function (what pins it; see tests/test_oracle_*.py):
   numpy.diag, hand-worked 2x2 step, beta=0 pure decay, orthonormal-key
   write/read, alpha=1/beta=1 projection property.
 * ``kda_varlen``       -- pinned: packed run == each sequence run alone.
+* ``kda_varlen_bwd``   -- pinned: central finite differences of
+  ``kda_varlen`` in float64 for every input (q, k, v, g, beta, the initial
+  state, A_log, dt_bias), with and without the in-kernel norms, gate and
+  beta sigmoid, and torch.autograd through an independent float64 torch
+  restatement of the recurrence.
 * ``rms_norm``         -- pinned: unit RMS after normalisation.
 * ``mixer_forward``    -- pinned by the reference's own module invariants
   (causality, cached decode == full prompt, split prefill == one shot,
@@ -193,6 +198,120 @@ def kda_varlen(q, k, v, g, beta, cu_seqlens, *, initial_states=None, **kw):
     return out, finals
 
 
+def kda_varlen_bwd(q, k, v, g, beta, cu_seqlens, d_out, *, d_final_states=None,
+                   initial_states=None, A_log=None, dt_bias=None, lower_bound=-5.0,
+                   use_qk_l2norm=True, use_gate=True, use_beta_sigmoid=True, scale=None,
+                   dtype=np.float64):
+    """Gradients of ``kda_varlen`` (the packed prefill) by the chain rule.
+
+    This is what FlashKDAFunction.backward returns
+    (ml/training/pretrain/engine/sm120_concurrent_ffn.py:301-373: the
+    chunk_kda_train_bwd call, then l2norm_bwd and fused_beta_sigmoid_bwd),
+    restated per token from the forward recurrence of ``kda_recurrent``:
+    with q^ = scale q/|q|, k^ = k/|k|, alpha = e^g,
+      S~ = Diag(alpha) S_{t-1}, p = k^T S~, u = beta (v - p),
+      S_t = S~ + k^ u^T, o_t = S_t^T q^,
+    the reverse step is
+      dS += q^ do^T; dq^ = S_t do; du = dS^T k^; dv = beta du;
+      dbeta = du . (v - p); dp = -beta du; dk^ = dS u + S~ dp;
+      dS~ = dS + k^ dp^T; dalpha = rowsum(dS~ o S_{t-1}); dS_{t-1} = Diag(alpha) dS~,
+    followed by the backward of the norms, the gate
+    g = lb sigmoid(e^A_log (z + dt_bias)) and the beta sigmoid.
+
+    Shapes as ``kda_varlen``; d_out: [sum_T, H, V]; d_final_states:
+    [N, H, K, V] or None.  Returns a dict of dq, dk, dv, dg, dbeta, dh0
+    (gradients of the inputs as passed, dg of the logits when ``use_gate``),
+    and dA_log [H], ddt_bias [H*K] when ``use_gate``.
+    """
+    q = np.asarray(q, dtype=dtype)
+    k = np.asarray(k, dtype=dtype)
+    v = np.asarray(v, dtype=dtype)
+    g = np.asarray(g, dtype=dtype)
+    beta = np.asarray(beta, dtype=dtype)
+    d_out = np.asarray(d_out, dtype=dtype)
+    total, heads, key_dim = q.shape
+    value_dim = v.shape[-1]
+    if scale is None:
+        scale = key_dim ** -0.5
+    cu = [int(x) for x in np.asarray(cu_seqlens).tolist()]
+    n = len(cu) - 1
+    # forward pieces, all tokens at once
+    if use_qk_l2norm:
+        nq = np.maximum(np.sqrt(np.sum(q * q, axis=-1, keepdims=True)), dtype(1e-12))
+        nk = np.maximum(np.sqrt(np.sum(k * k, axis=-1, keepdims=True)), dtype(1e-12))
+        qh, kh = q / nq * scale, k / nk
+    else:
+        qh, kh = q * scale, k
+    if use_gate:
+        ea = np.exp(np.asarray(A_log, dtype=dtype)).reshape(1, heads, 1)
+        zb = g + np.asarray(dt_bias, dtype=dtype).reshape(1, heads, key_dim)
+        sg = sigmoid(ea * zb)
+        logd = lower_bound * sg
+    else:
+        logd = g
+    alpha = np.exp(logd)
+    bt = sigmoid(beta) if use_beta_sigmoid else beta
+    dqh = np.zeros_like(qh)
+    dkh = np.zeros_like(kh)
+    dalpha = np.zeros_like(alpha)
+    dv = np.zeros_like(v)
+    dbt = np.zeros_like(bt)
+    dh0 = np.zeros((n, heads, key_dim, value_dim), dtype=dtype)
+    for s in range(n):
+        a, b = cu[s], cu[s + 1]
+        S = (np.zeros((heads, key_dim, value_dim), dtype=dtype) if initial_states is None
+             else np.array(initial_states[s], dtype=dtype))
+        states, preds = [S], []
+        for t in range(a, b):
+            St = S * alpha[t][..., None]
+            p = np.einsum("hd,hdv->hv", kh[t], St)
+            S = St + kh[t][..., None] * (bt[t][:, None] * (v[t] - p))[:, None, :]
+            states.append(S)
+            preds.append(p)
+        dS = (np.zeros((heads, key_dim, value_dim), dtype=dtype) if d_final_states is None
+              else np.array(d_final_states[s], dtype=dtype))
+        for i in range(b - a - 1, -1, -1):
+            t = a + i
+            prev, cur, p = states[i], states[i + 1], preds[i]
+            do = d_out[t]
+            dS = dS + qh[t][..., None] * do[:, None, :]
+            dqh[t] = np.einsum("hdv,hv->hd", cur, do)
+            du = np.einsum("hdv,hd->hv", dS, kh[t])
+            vp = v[t] - p
+            u = bt[t][:, None] * vp
+            dv[t] = bt[t][:, None] * du
+            dbt[t] = np.sum(du * vp, axis=-1)
+            dp = -bt[t][:, None] * du
+            st = prev * alpha[t][..., None]
+            dkh[t] = np.einsum("hdv,hv->hd", dS, u) + np.einsum("hdv,hv->hd", st, dp)
+            dst = dS + kh[t][..., None] * dp[:, None, :]
+            dalpha[t] = np.sum(dst * prev, axis=-1)
+            dS = dst * alpha[t][..., None]
+        dh0[s] = dS
+    # norms: y = x / n, dx = (dy - y (y . dy)) / n (n held constant when clamped)
+    if use_qk_l2norm:
+        def norm_bwd(x, nx, dy):
+            y = x / nx
+            unclamped = np.sqrt(np.sum(x * x, axis=-1, keepdims=True)) >= 1e-12
+            proj = np.where(unclamped, y * np.sum(y * dy, axis=-1, keepdims=True), 0.0)
+            return (dy - proj) / nx
+        dq = norm_bwd(q, nq, dqh * scale)
+        dk = norm_bwd(k, nk, dkh)
+    else:
+        dq, dk = dqh * scale, dkh
+    dlogd = dalpha * alpha
+    out = {"dv": dv, "dh0": dh0, "dq": dq, "dk": dk}
+    if use_gate:
+        dz = dlogd * lower_bound * sg * (1.0 - sg) * ea
+        out["dg"] = dz
+        out["ddt_bias"] = dz.sum(axis=0).reshape(heads * key_dim)
+        out["dA_log"] = (dz * zb).sum(axis=(0, 2))
+    else:
+        out["dg"] = dlogd
+    out["dbeta"] = dbt * bt * (1.0 - bt) if use_beta_sigmoid else dbt
+    return out
+
+
 def kda_decode_step(q, k, v, g, beta, state, **kw):
     """One recurrent step for B sequences (the fused_recurrent_kda call at
     attention.py:330-348): q,k: [B, H, K]; v: [B, H, V]; g: [B, H, K];
@@ -270,6 +389,7 @@ __all__ = [
     "kda_gate",
     "kda_recurrent",
     "kda_varlen",
+    "kda_varlen_bwd",
     "l2_normalize",
     "linear",
     "mixer_forward",

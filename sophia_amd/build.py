@@ -20,7 +20,7 @@ LIB_DIR = os.path.join(HERE, "_lib")
 LIB_NAME = "libsophia_kda.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 ARCH = "gfx950"
-SOURCES = ("errors.cpp", "short_conv.hip", "kda_decode.hip", "kda_chunk.hip", "decoder_ops.hip")
+SOURCES = ("errors.cpp", "short_conv.hip", "kda_decode.hip", "kda_chunk.hip", "decoder_ops.hip", "kda_bwd.hip")
 
 # Packed-fp32 VALU ops are switched off for all device code.
 COMMON_FLAGS = [

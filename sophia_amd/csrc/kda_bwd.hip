@@ -1,0 +1,589 @@
+// KDA backward over a packed ragged batch (training), gfx950.
+//
+// Gradients of the prefill (the chunk forward with a zero or given initial
+// state) with respect to q, k, v, g, beta, the initial state, A_log and
+// dt_bias.  Replaces FlashKDA's chunk_kda_train_bwd together with the
+// l2norm_bwd and fused_beta_sigmoid_bwd calls after it, as FlashKDAFunction.
+// backward makes them (ml/training/pretrain/engine/sm120_concurrent_ffn.py:
+// 301-373, the call at 320).
+//
+// Per token t of a sequence (q^ = q/|q| * scale, k^ = k/|k|, alpha = e^g):
+//   S~ = Diag(alpha) S_{t-1},  p = k^T S~,  u = beta (v - p),
+//   S_t = S~ + k^ u^T,         o_t = S_t^T q^
+// and in reverse, with dS the gradient of S_t (dS_T = dht):
+//   dS += q^ do^T;  dq^ = S_t do;  du = dS^T k^;  dv = beta du;
+//   dbeta = du . (v - p);  dp = -beta du;  dk^ = dS u + S~ dp;
+//   dS~ = dS + k^ dp^T;  dalpha = rowsum(dS~ o S_{t-1});  dS_{t-1} = Diag(alpha) dS~.
+//
+// Kernels:
+//  * kda_bwd_prep_kernel, one work-group of 128 threads per (token, head):
+//    q^, k^, the log-decay g (gate applied) and beta (sigmoid applied), fp32.
+//  * kda_bwd_chain_kernel, one work-group of 512 threads per (sequence, head,
+//    32-column value slice): the value columns of the state evolve
+//    independently, so each slice runs the recurrence alone.  It first runs
+//    the sequence forward and keeps the state at every 64-token chunk start
+//    (in the workspace); then, chunk by chunk in reverse, it recomputes the
+//    chunk forward keeping the state every 8 tokens in LDS, and for each
+//    8-token piece in reverse recomputes its states in registers and runs the
+//    reverse steps.  Sums over value columns (dq^, dk^, dalpha) leave as
+//    per-slice partials; dbeta leaves per value column.
+//  * kda_bwd_post_kernel, one work-group of 128 threads per (token, head):
+//    sums the partials and applies the backward of the l2 norms, of the gate
+//    g = lb sigmoid(e^A_log (z + dt_bias)) and of the beta sigmoid.
+//  * kda_bwd_gate_partial_kernel / kda_bwd_gate_final_kernel: dA_log and
+//    ddt_bias, sums over tokens of dz (z + dt_bias) and dz, in a fixed order.
+//
+// Thread t of the chain kernel owns value column j = t % 32 of its slice and
+// state rows 8 (t / 32) .. +7.  A sum over the 128 rows (k^T X for a column)
+// is 8 local terms, a xor-32 shuffle and 8 wavefront partials through LDS (one
+// barrier); a sum over the 32 columns (X z for a row) is a butterfly inside
+// each half-wavefront that leaves the sum of value i in lane i.
+#include <mutex>
+
+#include "common.hpp"
+
+namespace sophia {
+namespace {
+
+constexpr int kD = 128;
+constexpr int kC = 64;           // checkpoint interval (chunk)
+constexpr int kSub = 8;          // sub-checkpoint interval inside a chunk
+constexpr int kNV = 32;          // value columns per work-group
+constexpr int kSlices = kD / kNV;
+constexpr int kChainThreads = 512;
+constexpr int kRows = kD / (kChainThreads / kNV);   // state rows per thread: 8
+constexpr int kGateParts = 64;   // token partitions of the dA_log / ddt_bias sums
+constexpr int kMaxDevices = 64;
+constexpr size_t kChainLds = (static_cast<size_t>(kC / kSub) * kD * kNV + 2 * 8 * kNV) * sizeof(float);
+
+struct BwdArgs {
+  // inputs
+  const void *q, *k, *v;
+  int64_t qkv_stride;
+  int qkv_dtype;
+  const void *g;
+  int64_t g_stride;
+  int g_dtype;
+  const void *beta;
+  int64_t beta_stride;
+  int beta_dtype;
+  const float *A_log, *dt_bias;
+  float scale, lb;
+  unsigned flags;
+  const int32_t *cu;
+  int n_seqs;
+  int64_t total;
+  int num_heads;
+  const float *h0;        // [n_seqs, H, 128, 128] or NULL
+  const void *dout;       // [total, H, 128] rows of do_stride elements
+  int64_t do_stride;
+  int do_dtype;
+  const float *dht;       // [n_seqs, H, 128, 128] or NULL
+  // outputs (fp32)
+  float *dq, *dk, *dv, *dg, *dbeta, *dh0, *dA_log, *ddt_bias;
+  // workspace
+  float *qh, *kh, *gl, *bt;        // prepared q^, k^, log-decay, beta
+  float *ckpt;                     // [chunks, H, 128, 128] chunk-start states
+  float *dqh, *dkh, *dal;          // [kSlices, total, H, 128] partial sums
+  float *dbc;                      // [total, H, 128] dbeta per value column
+  float *gpb, *gpa;                // [kGateParts, H, 128] partial ddt_bias / dA_log
+};
+
+// ---- prep ---------------------------------------------------------------------
+__global__ __launch_bounds__(kD) void kda_bwd_prep_kernel(BwdArgs a) {
+  const int64_t tok = blockIdx.x;
+  const int h = blockIdx.y;
+  const int c = threadIdx.x;
+  __shared__ float s_red[2][2];
+  const int64_t row = tok * a.qkv_stride + static_cast<int64_t>(h) * kD + c;
+  const float qv = load_elem(a.q, row, a.qkv_dtype);
+  const float kv = load_elem(a.k, row, a.qkv_dtype);
+  float z = load_elem(a.g, tok * a.g_stride + static_cast<int64_t>(h) * kD + c, a.g_dtype);
+  float b = load_elem(a.beta, tok * a.beta_stride + h, a.beta_dtype);
+  const float sq = wave_sum(qv * qv), sk = wave_sum(kv * kv);
+  if ((c & 63) == 0) {
+    s_red[c >> 6][0] = sq;
+    s_red[c >> 6][1] = sk;
+  }
+  __syncthreads();
+  float qs = a.scale, ks = 1.f;
+  if (a.flags & SOPHIA_KDA_QK_L2NORM) {
+    qs /= fmaxf(sqrtf(s_red[0][0] + s_red[1][0]), 1e-12f);
+    ks /= fmaxf(sqrtf(s_red[0][1] + s_red[1][1]), 1e-12f);
+  }
+  if (a.flags & SOPHIA_KDA_GATE_IN_KERNEL)
+    z = a.lb / (1.f + expf(-expf(a.A_log[h]) * (z + a.dt_bias[h * kD + c])));
+  const int64_t o = (tok * a.num_heads + h) * kD + c;
+  a.qh[o] = qv * qs;
+  a.kh[o] = kv * ks;
+  a.gl[o] = z;
+  if (c == 0) {
+    if (a.flags & SOPHIA_KDA_BETA_SIGMOID) b = 1.f / (1.f + expf(-b));
+    a.bt[tok * a.num_heads + h] = b;
+  }
+}
+
+// ---- chain --------------------------------------------------------------------
+struct ChainCtx {
+  const BwdArgs *a;
+  int h, col, j, rg, lane, wave;
+  float *s_kred;    // [2][8 waves][32]
+};
+
+// Sum over the 128 state rows of x (one partial per thread, over its 8 rows)
+// for the thread's column.  Consecutive calls alternate between two LDS
+// buffers, so a buffer is rewritten only after every thread has passed the
+// barrier of the call in between (and so has read it).
+__device__ __forceinline__ float row_sum(const ChainCtx &c, float x, int &kb) {
+  x += __shfl_xor(x, 32, 64);
+  float *buf = c.s_kred + kb * 8 * kNV;
+  kb ^= 1;
+  if (c.lane < kNV) buf[c.wave * kNV + c.j] = x;
+  lds_barrier();
+  float s = 0.f;
+#pragma unroll
+  for (int w = 0; w < 8; ++w) s += buf[w * kNV + c.j];
+  return s;
+}
+
+// The inputs of one token for the thread's rows and column.
+struct TokenIn {
+  f4 q[kRows / 4], k[kRows / 4], g[kRows / 4];
+  float v, bt;
+};
+
+__device__ __forceinline__ void load_token(const ChainCtx &c, int64_t tok, TokenIn &in) {
+  const BwdArgs &a = *c.a;
+  const int64_t base = (tok * a.num_heads + c.h) * kD + c.rg * kRows;
+#pragma unroll
+  for (int i = 0; i < kRows / 4; ++i) {
+    in.q[i] = *reinterpret_cast<const f4 *>(a.qh + base + 4 * i);
+    in.k[i] = *reinterpret_cast<const f4 *>(a.kh + base + 4 * i);
+    in.g[i] = *reinterpret_cast<const f4 *>(a.gl + base + 4 * i);
+  }
+  in.v = load_elem(a.v, tok * a.qkv_stride + static_cast<int64_t>(c.h) * kD + c.col, a.qkv_dtype);
+  in.bt = a.bt[tok * a.num_heads + c.h];
+}
+
+__device__ __forceinline__ float tq(const TokenIn &in, int i) { return in.q[i >> 2][i & 3]; }
+__device__ __forceinline__ float tk(const TokenIn &in, int i) { return in.k[i >> 2][i & 3]; }
+__device__ __forceinline__ float talpha(const TokenIn &in, int i) { return expf(in.g[i >> 2][i & 3]); }
+
+// S <- S_t from S_{t-1}; returns p = k^T S~ of the thread's column.
+__device__ __forceinline__ float fwd_step(const ChainCtx &c, const TokenIn &in, float (&S)[kRows], int &kb) {
+  float part = 0.f;
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) {
+    S[i] *= talpha(in, i);
+    part = fmaf(tk(in, i), S[i], part);
+  }
+  const float p = row_sum(c, part, kb);
+  const float u = in.bt * (in.v - p);
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) S[i] = fmaf(tk(in, i), u, S[i]);
+  return p;
+}
+
+// Runs tokens [t0, t0 + n) forward from S, with the next token's inputs
+// loaded while the current one is processed.
+__device__ __forceinline__ void fwd_run(const ChainCtx &c, int64_t t0, int n, float (&S)[kRows], int &kb) {
+  if (n <= 0) return;
+  TokenIn cur, nxt;
+  load_token(c, t0, cur);
+  for (int t = 0; t < n; ++t) {
+    if (t + 1 < n) load_token(c, t0 + t + 1, nxt);
+    fwd_step(c, cur, S, kb);
+    cur = nxt;
+  }
+}
+
+// One butterfly stage over lanes l ^ m: of x[0 .. 2N) keep the half selected
+// by lane bit m and add the partner lane's copy of that half.
+template <int N>
+__device__ __forceinline__ void fold(const float (&x)[2 * N], float (&y)[N], int l, int m) {
+  const bool up = (l & m) != 0;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const float keep = up ? x[N + i] : x[i], send = up ? x[i] : x[N + i];
+    y[i] = keep + __shfl_xor(send, m, 64);
+  }
+}
+
+// Sum over the 32 lanes of a half-wavefront: on return lane i holds the sum
+// over those lanes of x[i].
+__device__ __forceinline__ float col_sum32(const float (&x)[32], int l) {
+  float y16[16], y8[8], y4[4], y2[2], y1[1];
+  fold<16>(x, y16, l, 16);
+  fold<8>(y16, y8, l, 8);
+  fold<4>(y8, y4, l, 4);
+  fold<2>(y4, y2, l, 2);
+  fold<1>(y2, y1, l, 1);
+  return y1[0];
+}
+
+__global__ __launch_bounds__(kChainThreads) void kda_bwd_chain_kernel(BwdArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  float *s_sub = smem;                                     // [kC / kSub][128][32]
+  float *s_kred = s_sub + (kC / kSub) * kD * kNV;           // [2][8][32]
+
+  const int s = blockIdx.x / (a.num_heads * kSlices);
+  const int rem = blockIdx.x % (a.num_heads * kSlices);
+  const int h = rem / kSlices;
+  const int slice = rem % kSlices;
+  if (s >= a.n_seqs) return;
+  ChainCtx c;
+  c.a = &a;
+  c.h = h;
+  c.j = threadIdx.x % kNV;
+  c.col = slice * kNV + c.j;
+  c.rg = threadIdx.x / kNV;
+  c.lane = threadIdx.x & 63;
+  c.wave = threadIdx.x >> 6;
+  c.s_kred = s_kred;
+  const int l32 = threadIdx.x & 31;
+  const int r0 = c.rg * kRows;
+  const int64_t seq_a = iclamp64(a.cu[s], 0, a.total);
+  const int64_t seq_b = iclamp64(a.cu[s + 1], seq_a, a.total);
+  const int len = static_cast<int>(seq_b - seq_a);
+  const int nch = (len + kC - 1) / kC;
+  // Checkpoint slots of this sequence: seq_a / 64 + s + chunk.  For ordered
+  // offsets the sequences' slots do not overlap, and for any offsets they
+  // stay below total / 64 + n_seqs.
+  const int64_t ck0 = seq_a / kC + s;
+  const int64_t state_off = (static_cast<int64_t>(s) * a.num_heads + h) * kD * kD;
+  int kb = 0;
+
+  // ---- pass 1: forward, the state at every chunk start -> workspace
+  float S[kRows];
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) S[i] = a.h0 ? a.h0[state_off + static_cast<int64_t>(r0 + i) * kD + c.col] : 0.f;
+  for (int ch = 0; ch < nch; ++ch) {
+    float *ck = a.ckpt + ((ck0 + ch) * a.num_heads + h) * kD * kD;
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) ck[static_cast<int64_t>(r0 + i) * kD + c.col] = S[i];
+    fwd_run(c, seq_a + static_cast<int64_t>(ch) * kC, min(kC, len - ch * kC), S, kb);
+  }
+  // Each checkpoint is read back below by the thread that wrote it.
+
+  // ---- pass 2: reverse, chunk by chunk
+  float dS[kRows];
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) dS[i] = a.dht ? a.dht[state_off + static_cast<int64_t>(r0 + i) * kD + c.col] : 0.f;
+  for (int ch = nch - 1; ch >= 0; --ch) {
+    const int64_t t0 = seq_a + static_cast<int64_t>(ch) * kC;
+    const int n = min(kC, len - ch * kC);
+    const float *ck = a.ckpt + ((ck0 + ch) * a.num_heads + h) * kD * kD;
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) S[i] = ck[static_cast<int64_t>(r0 + i) * kD + c.col];
+    // sub-checkpoints: the state before tokens 0, 8, 16, ... of the chunk
+    // (each thread reads back only its own entries)
+    const int nsub = (n + kSub - 1) / kSub;
+    for (int sb = 0; sb < nsub; ++sb) {
+#pragma unroll
+      for (int i = 0; i < kRows; ++i) s_sub[(sb * kD + r0 + i) * kNV + c.j] = S[i];
+      if (sb + 1 < nsub) fwd_run(c, t0 + sb * kSub, kSub, S, kb);
+    }
+    for (int sb = nsub - 1; sb >= 0; --sb) {
+      const int64_t p0 = t0 + sb * kSub;
+      const int m = min(kSub, n - sb * kSub);
+      // Sp[t]: the state before token t of the piece (Sp[t + 1] after it);
+      // P[t]: that token's p
+      float Sp[kSub + 1][kRows], P[kSub];
+#pragma unroll
+      for (int i = 0; i < kRows; ++i) Sp[0][i] = s_sub[(sb * kD + r0 + i) * kNV + c.j];
+      {
+        TokenIn cur, nxt;
+        load_token(c, p0, cur);
+#pragma unroll
+        for (int t = 0; t < kSub; ++t) {
+          if (t < m) {
+            if (t + 1 < m) load_token(c, p0 + t + 1, nxt);
+#pragma unroll
+            for (int i = 0; i < kRows; ++i) Sp[t + 1][i] = Sp[t][i];
+            P[t] = fwd_step(c, cur, Sp[t + 1], kb);
+            cur = nxt;
+          }
+        }
+      }
+      TokenIn cur, nxt;
+      load_token(c, p0 + m - 1, cur);
+      float dov = load_elem(a.dout, (p0 + m - 1) * a.do_stride + static_cast<int64_t>(h) * kD + c.col, a.do_dtype);
+#pragma unroll
+      for (int tt = kSub - 1; tt >= 0; --tt) {
+        if (tt < m) {
+          const int64_t tok = p0 + tt;
+          float dov_n = 0.f;
+          if (tt > 0) {
+            load_token(c, tok - 1, nxt);
+            dov_n = load_elem(a.dout, (tok - 1) * a.do_stride + static_cast<int64_t>(h) * kD + c.col, a.do_dtype);
+          }
+          const float vp = cur.v - P[tt];
+          const float u = cur.bt * vp;
+          float x[32];
+          float part = 0.f;
+#pragma unroll
+          for (int i = 0; i < kRows; ++i) {
+            dS[i] = fmaf(tq(cur, i), dov, dS[i]);      // dS_t += q^ do^T
+            x[i] = Sp[tt + 1][i] * dov;                // dq^ partial: S_t do
+            part = fmaf(tk(cur, i), dS[i], part);
+          }
+          const float du = row_sum(c, part, kb);       // dS_t^T k^
+          const float dp = -cur.bt * du;
+#pragma unroll
+          for (int i = 0; i < kRows; ++i) {
+            const float al = talpha(cur, i);
+            const float st = al * Sp[tt][i];                  // S~
+            x[kRows + i] = fmaf(dS[i], u, st * dp);           // dk^ partial
+            const float dst = fmaf(tk(cur, i), dp, dS[i]);    // dS~
+            x[2 * kRows + i] = dst * Sp[tt][i];               // dalpha partial
+            dS[i] = al * dst;                                 // dS_{t-1}
+          }
+#pragma unroll
+          for (int i = 3 * kRows; i < 32; ++i) x[i] = 0.f;
+          const float r = col_sum32(x, l32);
+          if (l32 < 3 * kRows) {
+            const int vec = l32 / kRows, row = r0 + (l32 % kRows);
+            float *dst = vec == 0 ? a.dqh : (vec == 1 ? a.dkh : a.dal);
+            dst[((static_cast<int64_t>(slice) * a.total + tok) * a.num_heads + h) * kD + row] = r;
+          }
+          if (c.rg == 0) {
+            const int64_t o = (tok * a.num_heads + h) * kD + c.col;
+            a.dv[o] = cur.bt * du;
+            a.dbc[o] = du * vp;
+          }
+          cur = nxt;
+          dov = dov_n;
+        }
+      }
+    }
+  }
+  if (a.dh0) {
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) a.dh0[state_off + static_cast<int64_t>(r0 + i) * kD + c.col] = dS[i];
+  }
+}
+
+// ---- post -----------------------------------------------------------------------
+__global__ __launch_bounds__(kD) void kda_bwd_post_kernel(BwdArgs a) {
+  const int64_t tok = blockIdx.x;
+  const int h = blockIdx.y;
+  const int c = threadIdx.x;
+  __shared__ float s_red[2][5];
+  const int64_t o = (tok * a.num_heads + h) * kD + c;
+  float dqh = 0.f, dkh = 0.f, dal = 0.f;
+#pragma unroll
+  for (int sl = 0; sl < kSlices; ++sl) {
+    const int64_t po = ((static_cast<int64_t>(sl) * a.total + tok) * a.num_heads + h) * kD + c;
+    dqh += a.dqh[po];
+    dkh += a.dkh[po];
+    dal += a.dal[po];
+  }
+  const int64_t row = tok * a.qkv_stride + static_cast<int64_t>(h) * kD + c;
+  const float qv = load_elem(a.q, row, a.qkv_dtype);
+  const float kv = load_elem(a.k, row, a.qkv_dtype);
+  const bool l2 = (a.flags & SOPHIA_KDA_QK_L2NORM) != 0;
+  // With the norm, y = x / n (n = max(|x|, eps)) and dx = (dy - y (y . dy)) / n
+  // where |x| >= eps, dx = dy / n where the clamp holds n constant.
+  const float yq = l2 ? a.qh[o] / a.scale : qv;
+  const float yk = a.kh[o];
+  const float dyq = dqh * a.scale;
+  const float r0 = wave_sum(yq * dyq), r1 = wave_sum(yk * dkh), r2 = wave_sum(qv * qv),
+              r3 = wave_sum(kv * kv), r4 = wave_sum(a.dbc[o]);
+  if ((c & 63) == 0) {
+    s_red[c >> 6][0] = r0;
+    s_red[c >> 6][1] = r1;
+    s_red[c >> 6][2] = r2;
+    s_red[c >> 6][3] = r3;
+    s_red[c >> 6][4] = r4;
+  }
+  __syncthreads();
+  float dq = dyq, dk = dkh;
+  if (l2) {
+    const float lq = sqrtf(s_red[0][2] + s_red[1][2]), lk = sqrtf(s_red[0][3] + s_red[1][3]);
+    const float nq = fmaxf(lq, 1e-12f), nk = fmaxf(lk, 1e-12f);
+    dq = (lq < 1e-12f ? dyq : dyq - yq * (s_red[0][0] + s_red[1][0])) / nq;
+    dk = (lk < 1e-12f ? dkh : dkh - yk * (s_red[0][1] + s_red[1][1])) / nk;
+  }
+  a.dq[o] = dq;
+  a.dk[o] = dk;
+  // alpha = e^g: dg = dalpha alpha; through the gate, dz = dg lb s (1 - s) e^A_log
+  float dgv = dal * expf(a.gl[o]);
+  if (a.flags & SOPHIA_KDA_GATE_IN_KERNEL) {
+    const float z = load_elem(a.g, tok * a.g_stride + static_cast<int64_t>(h) * kD + c, a.g_dtype);
+    const float ea = expf(a.A_log[h]);
+    const float sg = 1.f / (1.f + expf(-ea * (z + a.dt_bias[h * kD + c])));
+    dgv = dgv * a.lb * sg * (1.f - sg) * ea;
+  }
+  a.dg[o] = dgv;
+  if (c == 0) {
+    float db = s_red[0][4] + s_red[1][4];
+    if (a.flags & SOPHIA_KDA_BETA_SIGMOID) {
+      const float bt = a.bt[tok * a.num_heads + h];
+      db *= bt * (1.f - bt);
+    }
+    a.dbeta[tok * a.num_heads + h] = db;
+  }
+}
+
+// ---- gate parameters ---------------------------------------------------------------
+// g = lb sigmoid(e^A_log (z + b)): dA_log = sum dz (z + b), ddt_bias = sum dz.
+__global__ __launch_bounds__(kD) void kda_bwd_gate_partial_kernel(BwdArgs a) {
+  const int h = blockIdx.x, part = blockIdx.y, c = threadIdx.x;
+  const int64_t per = (a.total + kGateParts - 1) / kGateParts;
+  const int64_t t_lo = imin64(static_cast<int64_t>(part) * per, a.total);
+  const int64_t t_hi = imin64(t_lo + per, a.total);
+  const float b = a.dt_bias[h * kD + c];
+  float sb = 0.f, sa = 0.f;
+  for (int64_t tok = t_lo; tok < t_hi; ++tok) {
+    const float dz = a.dg[(tok * a.num_heads + h) * kD + c];
+    const float z = load_elem(a.g, tok * a.g_stride + static_cast<int64_t>(h) * kD + c, a.g_dtype);
+    sb += dz;
+    sa = fmaf(dz, z + b, sa);
+  }
+  const int64_t o = (static_cast<int64_t>(part) * a.num_heads + h) * kD + c;
+  a.gpb[o] = sb;
+  a.gpa[o] = sa;
+}
+
+__global__ __launch_bounds__(kD) void kda_bwd_gate_final_kernel(BwdArgs a) {
+  const int h = blockIdx.x, c = threadIdx.x;
+  __shared__ float s_red[2];
+  float sb = 0.f, sa = 0.f;
+  for (int part = 0; part < kGateParts; ++part) {
+    const int64_t o = (static_cast<int64_t>(part) * a.num_heads + h) * kD + c;
+    sb += a.gpb[o];
+    sa += a.gpa[o];
+  }
+  if (a.ddt_bias) a.ddt_bias[h * kD + c] = sb;
+  sa = wave_sum(sa);
+  if ((c & 63) == 0) s_red[c >> 6] = sa;
+  __syncthreads();
+  if (c == 0 && a.dA_log) a.dA_log[h] = s_red[0] + s_red[1];
+}
+
+size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+size_t max_chunks(int64_t total_tokens, int n_seqs) {
+  return static_cast<size_t>(total_tokens / kC) + static_cast<size_t>(n_seqs);
+}
+
+int ensure_chain_lds() {
+  static std::mutex mu;
+  static bool done[kMaxDevices] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(SOPHIA_ERR_HIP, "kda_chunk_bwd: hipGetDevice: %s", hipGetErrorString(e));
+  std::lock_guard<std::mutex> lock(mu);
+  if (dev >= 0 && dev < kMaxDevices && done[dev]) return SOPHIA_OK;
+  e = hipFuncSetAttribute(reinterpret_cast<const void *>(&kda_bwd_chain_kernel),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kChainLds));
+  if (e != hipSuccess)
+    return set_error(SOPHIA_ERR_HIP, "kda_chunk_bwd: cannot set LDS size: %s", hipGetErrorString(e));
+  if (dev >= 0 && dev < kMaxDevices) done[dev] = true;
+  return SOPHIA_OK;
+}
+
+}  // namespace
+}  // namespace sophia
+
+using namespace sophia;
+
+extern "C" size_t sophia_kda_chunk_bwd_workspace_size(int64_t total_tokens, int n_seqs, int num_heads,
+                                                      int head_dim) {
+  if (total_tokens < 0 || n_seqs <= 0 || num_heads <= 0 || head_dim != kD) return 0;
+  const size_t tok = static_cast<size_t>(total_tokens) * num_heads;
+  return 3 * align256(tok * kD * 4) + align256(tok * 4) +
+         align256(max_chunks(total_tokens, n_seqs) * num_heads * kD * kD * 4) +
+         3 * align256(kSlices * tok * kD * 4) + align256(tok * kD * 4) +
+         2 * align256(static_cast<size_t>(kGateParts) * num_heads * kD * 4);
+}
+
+extern "C" int sophia_kda_chunk_bwd(const void *q, const void *k, const void *v, int64_t qkv_row_stride,
+                                    int qkv_dtype, const void *g, int64_t g_row_stride, int g_dtype,
+                                    const void *beta, int64_t beta_row_stride, int beta_dtype,
+                                    const float *A_log, const float *dt_bias, float scale, float lower_bound,
+                                    unsigned flags, const int32_t *cu_seqlens, int n_seqs, int64_t total_tokens,
+                                    int num_heads, int head_dim, const float *initial_state, const void *d_out,
+                                    int64_t d_out_row_stride, int d_out_dtype, const float *d_final_state,
+                                    float *dq, float *dk, float *dv, float *dg, float *dbeta,
+                                    float *d_initial_state, float *dA_log, float *ddt_bias, void *workspace,
+                                    size_t workspace_bytes, void *stream) {
+  SOPHIA_REQUIRE(head_dim == kD, "kda_chunk_bwd: head_dim must be 128 (got %d)", head_dim);
+  SOPHIA_REQUIRE(n_seqs > 0 && num_heads > 0 && num_heads <= 65535 && total_tokens >= 0 &&
+                     total_tokens <= 0x7fffffff,
+                 "kda_chunk_bwd: bad n_seqs / num_heads / total_tokens");
+  SOPHIA_REQUIRE(qkv_dtype == SOPHIA_DTYPE_F32 || qkv_dtype == SOPHIA_DTYPE_BF16, "kda_chunk_bwd: qkv dtype");
+  SOPHIA_REQUIRE(g_dtype == SOPHIA_DTYPE_F32 || g_dtype == SOPHIA_DTYPE_BF16, "kda_chunk_bwd: g dtype");
+  SOPHIA_REQUIRE(beta_dtype == SOPHIA_DTYPE_F32 || beta_dtype == SOPHIA_DTYPE_BF16, "kda_chunk_bwd: beta dtype");
+  SOPHIA_REQUIRE(d_out_dtype == SOPHIA_DTYPE_F32 || d_out_dtype == SOPHIA_DTYPE_BF16,
+                 "kda_chunk_bwd: d_out dtype");
+  SOPHIA_REQUIRE(cu_seqlens && workspace &&
+                     (total_tokens == 0 || (q && k && v && g && beta && d_out && dq && dk && dv && dg && dbeta)),
+                 "kda_chunk_bwd: NULL pointer");
+  const bool gate = (flags & SOPHIA_KDA_GATE_IN_KERNEL) != 0;
+  SOPHIA_REQUIRE(!gate || (A_log && dt_bias), "kda_chunk_bwd: gate in kernel needs A_log and dt_bias");
+  SOPHIA_REQUIRE(gate || (!dA_log && !ddt_bias),
+                 "kda_chunk_bwd: dA_log / ddt_bias exist only with the gate in the kernel");
+  SOPHIA_REQUIRE(qkv_row_stride >= static_cast<int64_t>(num_heads) * kD &&
+                     g_row_stride >= static_cast<int64_t>(num_heads) * kD && beta_row_stride >= num_heads &&
+                     d_out_row_stride >= static_cast<int64_t>(num_heads) * kD,
+                 "kda_chunk_bwd: row stride smaller than a row");
+  SOPHIA_REQUIRE((reinterpret_cast<uintptr_t>(workspace) % 256) == 0,
+                 "kda_chunk_bwd: workspace must be 256-byte aligned");
+  const int64_t blocks = static_cast<int64_t>(n_seqs) * num_heads * kSlices;
+  SOPHIA_REQUIRE(blocks <= 0x7fffffff, "kda_chunk_bwd: grid too large");
+  const size_t need = sophia_kda_chunk_bwd_workspace_size(total_tokens, n_seqs, num_heads, head_dim);
+  if (workspace_bytes < need)
+    return set_error(SOPHIA_ERR_WORKSPACE, "kda_chunk_bwd: workspace %zu bytes < required %zu", workspace_bytes,
+                     need);
+  const size_t tok = static_cast<size_t>(total_tokens) * num_heads;
+  uint8_t *w = static_cast<uint8_t *>(workspace);
+  auto carve = [&w](size_t bytes) {
+    float *p = reinterpret_cast<float *>(w);
+    w += align256(bytes);
+    return p;
+  };
+  BwdArgs a{};
+  a.q = q; a.k = k; a.v = v; a.qkv_stride = qkv_row_stride; a.qkv_dtype = qkv_dtype;
+  a.g = g; a.g_stride = g_row_stride; a.g_dtype = g_dtype;
+  a.beta = beta; a.beta_stride = beta_row_stride; a.beta_dtype = beta_dtype;
+  a.A_log = A_log; a.dt_bias = dt_bias; a.scale = scale; a.lb = lower_bound; a.flags = flags;
+  a.cu = cu_seqlens; a.n_seqs = n_seqs; a.total = total_tokens; a.num_heads = num_heads;
+  a.h0 = initial_state; a.dout = d_out; a.do_stride = d_out_row_stride; a.do_dtype = d_out_dtype;
+  a.dht = d_final_state;
+  a.dq = dq; a.dk = dk; a.dv = dv; a.dg = dg; a.dbeta = dbeta; a.dh0 = d_initial_state;
+  a.dA_log = dA_log; a.ddt_bias = ddt_bias;
+  a.qh = carve(tok * kD * 4);
+  a.kh = carve(tok * kD * 4);
+  a.gl = carve(tok * kD * 4);
+  a.bt = carve(tok * 4);
+  a.ckpt = carve(max_chunks(total_tokens, n_seqs) * num_heads * kD * kD * 4);
+  a.dqh = carve(kSlices * tok * kD * 4);
+  a.dkh = carve(kSlices * tok * kD * 4);
+  a.dal = carve(kSlices * tok * kD * 4);
+  a.dbc = carve(tok * kD * 4);
+  a.gpb = carve(static_cast<size_t>(kGateParts) * num_heads * kD * 4);
+  a.gpa = carve(static_cast<size_t>(kGateParts) * num_heads * kD * 4);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (const int rc = ensure_chain_lds()) return rc;
+  if (total_tokens > 0) {
+    hipLaunchKernelGGL(kda_bwd_prep_kernel, dim3(static_cast<unsigned>(total_tokens), num_heads), dim3(kD), 0, st,
+                       a);
+    if (const int rc = check_launch("kda_bwd_prep")) return rc;
+  }
+  hipLaunchKernelGGL(kda_bwd_chain_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kChainThreads), kChainLds, st,
+                     a);
+  if (const int rc = check_launch("kda_bwd_chain")) return rc;
+  if (total_tokens > 0) {
+    hipLaunchKernelGGL(kda_bwd_post_kernel, dim3(static_cast<unsigned>(total_tokens), num_heads), dim3(kD), 0, st,
+                       a);
+    if (const int rc = check_launch("kda_bwd_post")) return rc;
+  }
+  if (gate && (dA_log || ddt_bias)) {
+    hipLaunchKernelGGL(kda_bwd_gate_partial_kernel, dim3(num_heads, kGateParts), dim3(kD), 0, st, a);
+    if (const int rc = check_launch("kda_bwd_gate_partial")) return rc;
+    hipLaunchKernelGGL(kda_bwd_gate_final_kernel, dim3(num_heads), dim3(kD), 0, st, a);
+    if (const int rc = check_launch("kda_bwd_gate_final")) return rc;
+  }
+  return SOPHIA_OK;
+}

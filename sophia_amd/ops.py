@@ -278,6 +278,87 @@ def kda_chunk_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
     return o
 
 
+def kda_chunk_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
+                  beta: torch.Tensor, cu_seqlens: torch.Tensor, d_out: torch.Tensor, *,
+                  A_log=None, dt_bias=None, scale: float | None = None,
+                  lower_bound: float = -5.0, use_qk_l2norm: bool = True, use_gate: bool = True,
+                  use_beta_sigmoid: bool = True, initial_state: torch.Tensor | None = None,
+                  d_final_state: torch.Tensor | None = None,
+                  cu_seqlens_cpu: torch.Tensor | None = None):
+    """Gradients of ``kda_chunk_fwd`` (no cache slots: one state per sequence).
+
+    The HIP counterpart of FlashKDA's chunk_kda_train_bwd plus l2norm_bwd and
+    fused_beta_sigmoid_bwd (sm120_concurrent_ffn.py:301-373).  Inputs as for
+    kda_chunk_fwd; d_out: [total, H, 128] gradient of o; d_final_state: fp32
+    [N, H, 128, 128] or None.  Returns fp32 (dq, dk, dv, dg, dbeta, dh0,
+    dA_log, ddt_bias): dg with respect to the g input as passed, dh0
+    [N, H, 128, 128], dA_log [H] and ddt_bias [H * 128] (empty without the
+    in-kernel gate).  A host ``cu_seqlens`` (or ``cu_seqlens_cpu``) is checked
+    to rise from 0 to the token count.
+    """
+    for t, name in ((q, "q"), (k, "k"), (v, "v"), (g, "g"), (beta, "beta"), (d_out, "d_out")):
+        _gpu(t, name)
+    device = q.device
+    total, heads = int(q.size(0)), int(q.size(1))
+    qs = _heads_rows(q, "q", heads, HEAD_DIM)
+    if k.stride() != q.stride() or v.stride() != q.stride():
+        raise RuntimeError("q, k and v must share one row layout")
+    _heads_rows(k, "k", heads, HEAD_DIM)
+    _heads_rows(v, "v", heads, HEAD_DIM)
+    if not (q.dtype == k.dtype == v.dtype):
+        raise RuntimeError("q, k and v must share one dtype")
+    for t, name in ((k, "k"), (v, "v"), (g, "g"), (beta, "beta"), (d_out, "d_out")):
+        _nrows(t, name, total)
+    gs = _heads_rows(g, "g", heads, HEAD_DIM)
+    bs = _rows(beta, "beta", heads)
+    ds = _heads_rows(d_out, "d_out", heads, HEAD_DIM)
+    if not isinstance(cu_seqlens, torch.Tensor):
+        raise RuntimeError("cu_seqlens must be a tensor")
+    if cu_seqlens_cpu is None and not cu_seqlens.is_cuda:
+        cu_seqlens_cpu = cu_seqlens
+    cu_host = None if cu_seqlens_cpu is None else torch.as_tensor(cu_seqlens_cpu).to("cpu", torch.int64)
+    cu = _int32(cu_seqlens.to(device=device, dtype=torch.int32).contiguous(), "cu_seqlens", device)
+    n = int(cu.numel()) - 1
+    if n < 1:
+        raise RuntimeError("cu_seqlens must hold at least one sequence")
+    if cu_host is not None and (int(cu_host.numel()) != n + 1 or int(cu_host[0]) != 0
+                                or int(cu_host[-1]) != total
+                                or bool((cu_host[1:] < cu_host[:-1]).any())):
+        raise RuntimeError("cu_seqlens must rise from 0 to the token count")
+    _state(initial_state, "initial_state", heads, device)
+    _state(d_final_state, "d_final_state", heads, device)
+    for t, name in ((initial_state, "initial_state"), (d_final_state, "d_final_state")):
+        if t is not None:
+            _nrows(t, name, n)
+    a_log, dtb = _gate_params(use_gate, A_log, dt_bias, heads, device)
+    if scale is None:
+        scale = HEAD_DIM ** -0.5
+    f32 = dict(dtype=torch.float32, device=device)
+    dq = torch.empty((total, heads, HEAD_DIM), **f32)
+    dk = torch.empty_like(dq)
+    dv = torch.empty_like(dq)
+    dg = torch.empty_like(dq)
+    dbeta = torch.empty((total, heads), **f32)
+    dh0 = torch.empty((n, heads, HEAD_DIM, HEAD_DIM), **f32)
+    da = torch.empty((heads if use_gate else 0,), **f32)
+    dbias = torch.empty((heads * HEAD_DIM if use_gate else 0,), **f32)
+    lib = nat.lib()
+    need = int(lib.sophia_kda_chunk_bwd_workspace_size(total, n, heads, HEAD_DIM))
+    buf, ws_addr, ws_bytes = _workspace(need, device)
+    rc = lib.sophia_kda_chunk_bwd(
+        nat.ptr(q), nat.ptr(k), nat.ptr(v), qs, nat.dtype_code(q.dtype), nat.ptr(g), gs,
+        nat.dtype_code(g.dtype), nat.ptr(beta), bs, nat.dtype_code(beta.dtype), nat.ptr(a_log),
+        nat.ptr(dtb), float(scale), float(lower_bound),
+        _flags(use_qk_l2norm, use_gate, use_beta_sigmoid), nat.ptr(cu), n, total, heads, HEAD_DIM,
+        nat.ptr(initial_state), nat.ptr(d_out), ds, nat.dtype_code(d_out.dtype),
+        nat.ptr(d_final_state), nat.ptr(dq), nat.ptr(dk), nat.ptr(dv), nat.ptr(dg),
+        nat.ptr(dbeta), nat.ptr(dh0), nat.ptr(da) if use_gate else None,
+        nat.ptr(dbias) if use_gate else None, ws_addr, ws_bytes, nat.stream_handle(device))
+    nat.check(rc, "sophia_kda_chunk_bwd")
+    del buf
+    return dq, dk, dv, dg, dbeta, dh0, da, dbias
+
+
 def kda_decode_step(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
                     beta: torch.Tensor, state: torch.Tensor, *, A_log=None, dt_bias=None,
                     scale: float | None = None, lower_bound: float = -5.0,
@@ -440,6 +521,16 @@ def chunk_kda(q, k, v, g, beta, *, scale=None, initial_state=None, output_final_
     def flat(t, width):
         return t.reshape(total, heads, width) if t.dim() == 4 else t.reshape(total, heads)
 
+    scale = float(HEAD_DIM ** -0.5 if scale is None else scale)
+    if torch.is_grad_enabled() and any(
+            isinstance(t, torch.Tensor) and t.requires_grad
+            for t in (q, k, v, g, beta, A_log, dt_bias, initial_state)):
+        o, ht = ChunkKDAFunction.apply(
+            flat(q, HEAD_DIM), flat(k, HEAD_DIM), flat(v, HEAD_DIM), flat(g, HEAD_DIM),
+            beta.reshape(total, heads), A_log, dt_bias, scale, initial_state,
+            bool(output_final_state), bool(use_qk_l2norm_in_kernel), bool(use_gate_in_kernel),
+            bool(use_beta_sigmoid_in_kernel), cu, cu_seqlens_cpu, lb)
+        return o.view(bsz, seqlen, heads, HEAD_DIM), ht
     h0 = None
     if initial_state is not None:
         h0 = initial_state if (initial_state.dtype == torch.float32
@@ -451,10 +542,91 @@ def chunk_kda(q, k, v, g, beta, *, scale=None, initial_state=None, output_final_
     o = torch_ops.kda_chunk_fwd(
         flat(q, HEAD_DIM), flat(k, HEAD_DIM), flat(v, HEAD_DIM), flat(g, HEAD_DIM),
         beta.reshape(total, heads), cu, _detached(A_log), _detached(dt_bias),
-        float(HEAD_DIM ** -0.5 if scale is None else scale), lb, bool(use_qk_l2norm_in_kernel),
+        scale, lb, bool(use_qk_l2norm_in_kernel),
         bool(use_gate_in_kernel), bool(use_beta_sigmoid_in_kernel), h0, ht, False, None,
         cu_seqlens_cpu)
     return o.view(bsz, seqlen, heads, HEAD_DIM), ht
+
+
+def _meta(t):
+    """(shape, dtype) of a tensor input, kept for its gradient; None otherwise."""
+    return (t.shape, t.dtype) if isinstance(t, torch.Tensor) else None
+
+
+def _grad_like(grad: torch.Tensor, meta):
+    """A fp32 kernel gradient in the shape and dtype of the input it belongs to."""
+    if meta is None:
+        return None
+    return grad.view(meta[0]).to(meta[1])
+
+
+class ChunkKDAFunction(torch.autograd.Function):
+    """FlashKDAFunction (ml/training/pretrain/engine/sm120_concurrent_ffn.py:
+    209-373) over the HIP kernels: the forward is the chunk prefill
+    (sophia::kda_chunk_fwd), the backward sophia::kda_chunk_bwd, which folds
+    in the l2norm / beta-sigmoid backward the reference runs after
+    chunk_kda_train_bwd.  Inputs are packed [total, H, 128] rows (beta
+    [total, H]); returns (o, final_state or None).  The backward saves the
+    inputs only and recomputes the states it needs."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, A_log, dt_bias, scale, initial_state, output_final_state,
+                use_qk_l2norm, use_gate, use_beta_sigmoid, cu, cu_seqlens_cpu, lower_bound):
+        total, heads = int(q.size(0)), int(q.size(1))
+        n = int(cu.numel()) - 1
+        h0 = None
+        if initial_state is not None:
+            h0 = initial_state.detach().float().reshape(n, heads, HEAD_DIM, HEAD_DIM).contiguous()
+        a_log = None if A_log is None else A_log.detach()
+        dtb = None if dt_bias is None else dt_bias.detach()
+        ht = torch.empty((n, heads, HEAD_DIM, HEAD_DIM), dtype=torch.float32, device=q.device) \
+            if output_final_state else None
+        o = torch_ops.kda_chunk_fwd(q, k, v, g, beta, cu, a_log, dtb, scale, lower_bound,
+                                    use_qk_l2norm, use_gate, use_beta_sigmoid, h0, ht, False, None,
+                                    cu_seqlens_cpu)
+        ctx.save_for_backward(q, k, v, g, beta, a_log, dtb, h0, cu)
+        ctx.cu_cpu = cu_seqlens_cpu
+        ctx.args = (float(scale), float(lower_bound), bool(use_qk_l2norm), bool(use_gate),
+                    bool(use_beta_sigmoid))
+        ctx.inputs = (_meta(A_log), _meta(dt_bias), _meta(initial_state))
+        ctx.set_materialize_grads(False)
+        return o, ht
+
+    @staticmethod
+    def backward(ctx, do, dht):
+        q, k, v, g, beta, a_log, dtb, h0, cu = ctx.saved_tensors
+        scale, lb, use_l2, use_gate, use_sig = ctx.args
+        A_log, dt_bias, initial_state = ctx.inputs
+        if do is None:
+            do = torch.zeros((q.size(0), q.size(1), HEAD_DIM), dtype=torch.float32, device=q.device)
+        dht = None if dht is None else dht.float().contiguous()
+        dq, dk, dv, dg, db, dh0, da, dbias = torch_ops.kda_chunk_bwd(
+            q, k, v, g, beta, cu, do.contiguous(), a_log, dtb, scale, lb, use_l2, use_gate,
+            use_sig, h0, dht, ctx.cu_cpu)
+        return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg.to(g.dtype), db.to(beta.dtype),
+                _grad_like(da, A_log) if use_gate else None,
+                _grad_like(dbias, dt_bias) if use_gate else None, None,
+                _grad_like(dh0, initial_state), None, None, None, None, None, None, None)
+
+
+def flash_kda(q, k, v, g, beta, A_log, dt_bias, scale=None, initial_state=None,
+              output_final_state=False, use_qk_l2norm_in_kernel=False, use_gate_in_kernel=False,
+              use_beta_sigmoid_in_kernel=False, allow_neg_eigval=False, state_v_first=False,
+              cu_seqlens=None, cu_seqlens_cpu=None, safe_gate=False, lower_bound=None,
+              chunk_size=64, **kwargs):
+    """The reference's flash_kda training entry (sm120_concurrent_ffn.py:375-423):
+    same arguments, differentiable in q, k, v, g, beta, A_log, dt_bias and
+    initial_state.  Returns (o [B, T, H, 128], final_state or None)."""
+    if kwargs:
+        raise TypeError(sorted(kwargs))
+    return chunk_kda(q, k, v, g, beta, scale=scale, initial_state=initial_state,
+                     output_final_state=output_final_state,
+                     use_qk_l2norm_in_kernel=use_qk_l2norm_in_kernel,
+                     use_gate_in_kernel=use_gate_in_kernel,
+                     use_beta_sigmoid_in_kernel=use_beta_sigmoid_in_kernel, safe_gate=safe_gate,
+                     lower_bound=lower_bound, A_log=A_log, dt_bias=dt_bias, cu_seqlens=cu_seqlens,
+                     cu_seqlens_cpu=cu_seqlens_cpu, chunk_size=chunk_size,
+                     allow_neg_eigval=allow_neg_eigval, state_v_first=state_v_first)
 
 
 def fused_recurrent_kda(q, k, v, g, beta, *, A_log=None, dt_bias=None, scale=None,

@@ -12,6 +12,8 @@ checks every argument and launches through the C ABI on the current stream):
   sophia::short_conv_fwd    (x, weight, cu_seqlens, conv_state!, ...) -> y
   sophia::short_conv_step   (x, weight, conv_state!, ...) -> y
   sophia::kda_chunk_fwd     (q, k, v, g, beta, cu_seqlens, ..., final_state!, ...) -> o
+  sophia::kda_chunk_bwd     (q, k, v, g, beta, cu_seqlens, d_out, ...) -> (dq, dk, dv, dg,
+                            dbeta, dh0, dA_log, ddt_bias)
   sophia::kda_decode_step   (q, k, v, g, beta, state!, ...) -> o
   sophia::gated_head_norm   (o, gate, norm_weight, ...) -> y
 """
@@ -80,6 +82,37 @@ def _(q, k, v, g, beta, cu_seqlens, A_log, dt_bias, scale, lower_bound, use_qk_l
     return q.new_empty((q.shape[0], q.shape[1], v.shape[2]))
 
 
+@torch.library.custom_op(f"{_LIB}::kda_chunk_bwd", mutates_args=(), device_types="cuda")
+def kda_chunk_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
+                  beta: torch.Tensor, cu_seqlens: torch.Tensor, d_out: torch.Tensor,
+                  A_log: Optional[torch.Tensor], dt_bias: Optional[torch.Tensor], scale: float,
+                  lower_bound: float, use_qk_l2norm: bool, use_gate: bool, use_beta_sigmoid: bool,
+                  initial_state: Optional[torch.Tensor], d_final_state: Optional[torch.Tensor],
+                  cu_seqlens_cpu: Optional[torch.Tensor]
+                  ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
+                             torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Prefill backward: fp32 gradients of every input (dA_log / ddt_bias empty
+    without the in-kernel gate)."""
+    return ops.kda_chunk_bwd(q, k, v, g, beta, cu_seqlens, d_out, A_log=A_log, dt_bias=dt_bias,
+                             scale=scale, lower_bound=lower_bound, use_qk_l2norm=use_qk_l2norm,
+                             use_gate=use_gate, use_beta_sigmoid=use_beta_sigmoid,
+                             initial_state=initial_state, d_final_state=d_final_state,
+                             cu_seqlens_cpu=cu_seqlens_cpu)
+
+
+@kda_chunk_bwd.register_fake
+def _(q, k, v, g, beta, cu_seqlens, d_out, A_log, dt_bias, scale, lower_bound, use_qk_l2norm,
+      use_gate, use_beta_sigmoid, initial_state, d_final_state, cu_seqlens_cpu):
+    total, heads, dim = q.shape
+    n = cu_seqlens.shape[0] - 1
+    f32 = dict(dtype=torch.float32)
+    return (q.new_empty((total, heads, dim), **f32), q.new_empty((total, heads, dim), **f32),
+            q.new_empty((total, heads, dim), **f32), q.new_empty((total, heads, dim), **f32),
+            q.new_empty((total, heads), **f32), q.new_empty((n, heads, dim, dim), **f32),
+            q.new_empty((heads if use_gate else 0,), **f32),
+            q.new_empty((heads * dim if use_gate else 0,), **f32))
+
+
 @torch.library.custom_op(f"{_LIB}::kda_decode_step", mutates_args=("state",), device_types="cuda")
 def kda_decode_step(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
                     beta: torch.Tensor, state: torch.Tensor, A_log: Optional[torch.Tensor],
@@ -110,5 +143,5 @@ def _(o, gate, norm_weight, heads, head_dim, eps):
     return gate.new_empty((rows, heads * head_dim))
 
 
-__all__ = ["gated_head_norm", "kda_chunk_fwd", "kda_decode_step", "short_conv_fwd",
+__all__ = ["gated_head_norm", "kda_chunk_bwd", "kda_chunk_fwd", "kda_decode_step", "short_conv_fwd",
            "short_conv_step"]

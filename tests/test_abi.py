@@ -142,6 +142,28 @@ def test_host_side_queries_and_validation():
     rc = lib.sophia_causal_attention(16, 1024, 32, 1024, 48, 1024, 64, 1024, 80, None, 2, 100, 0, 64,
                                      16, 64, 0.08, 1, None)
     assert rc == nat.SOPHIA_ERR_INVALID and "head_dim" in nat.last_error()
+    # KDA backward: size query, head_dim, gate-parameter outputs without the
+    # gate, short workspace (all rejected before any launch).
+    bws = lib.sophia_kda_chunk_bwd_workspace_size(1000, 3, 16, 128)
+    assert bws > lib.sophia_kda_chunk_bwd_workspace_size(500, 3, 16, 128) > 0
+    assert lib.sophia_kda_chunk_bwd_workspace_size(1000, 3, 16, 64) == 0
+    assert lib.sophia_kda_chunk_bwd_workspace_size(1000, 0, 16, 128) == 0
+    bwd = lambda *a: lib.sophia_kda_chunk_bwd(*a)  # noqa: E731
+    args = [16, 32, 48, 2048, 1, 64, 2048, 0, 80, 16, 0, None, None, 0.08, -5.0, 0, 96, 3, 1000,
+            16, 128, None, 112, 2048, 1, None, 128, 144, 160, 176, 192, None, None, None, 256,
+            bws, None]
+    a = list(args)
+    a[20] = 64
+    assert bwd(*a) == nat.SOPHIA_ERR_INVALID and "head_dim" in nat.last_error()
+    a = list(args)
+    a[32] = 240
+    assert bwd(*a) == nat.SOPHIA_ERR_INVALID and "dA_log" in nat.last_error()
+    a = list(args)
+    a[35] = bws - 1
+    assert bwd(*a) == nat.SOPHIA_ERR_WORKSPACE
+    a = list(args)
+    a[3] = 2047
+    assert bwd(*a) == nat.SOPHIA_ERR_INVALID and "stride" in nat.last_error()
 
 
 def test_ops_reject_cpu_tensors():
@@ -152,6 +174,8 @@ def test_ops_reject_cpu_tensors():
         ops.kda_chunk_fwd(x, x, x, x, torch.zeros(4, 16), torch.tensor([0, 4], dtype=torch.int32))
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         ops.kda_decode_step(x, x, x, x, torch.zeros(4, 16), torch.zeros(4, 16, 128, 128))
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.kda_chunk_bwd(x, x, x, x, torch.zeros(4, 16), torch.tensor([0, 4], dtype=torch.int32), x)
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         ops.short_conv_fwd(torch.zeros(4, 8), torch.zeros(8, 4),
                            torch.tensor([0, 4], dtype=torch.int32))
