@@ -273,6 +273,35 @@ def long_prefill_bench(torch, dev, stream, steps: int, warmup: int, traffic: dic
                      "frac_of_peak": round(tflops / BF16_PEAK_TFLOPS, 4)}}
 
 
+# Backward bytes per (token, head): q, k, v, do in bf16 and g, beta in fp32 read;
+# dq, dk, dv, dg and dbeta written in fp32.
+BWD_BYTES_PER_TOKEN = HEADS * (4 * DIM * 2 + DIM * 4 + 4 + 4 * DIM * 4 + 4)
+
+
+def backward_bench(torch, dev, stream, inp, steps: int, warmup: int) -> dict:
+    """The KDA backward (sophia_kda_chunk_bwd) over the headline prefill
+    batch: gradients of q, k, v, g, beta and the initial states for a bf16
+    output gradient, with the same flags as the timed prefill."""
+    from sophia_amd import ops
+    total = int(inp["q"].size(0))
+    gen = torch.Generator().manual_seed(12)
+    d_out = torch.randn((total, HEADS, DIM), generator=gen).to(torch.bfloat16).to(dev)
+
+    def call():
+        ops.kda_chunk_bwd(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], inp["cu"], d_out,
+                          use_qk_l2norm=True, use_gate=False, use_beta_sigmoid=False,
+                          cu_seqlens_cpu=inp["cu_cpu"])
+
+    _, per = time_events(torch, call, steps, warmup, stream)
+    ms = float(np.mean(per))
+    gbs = total * BWD_BYTES_PER_TOKEN / (ms / 1e3) / 1e9
+    return {"workload": "KDA backward over the prefill batch (same lengths, flags and inputs), "
+                        "bf16 d_out, fp32 gradients",
+            "tokens_per_s": round(total / (ms / 1e3), 1), "ms_per_call": round(ms, 3),
+            "algorithmic_bytes_per_call": total * BWD_BYTES_PER_TOKEN,
+            "GBps": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def copy_bandwidth(torch, dev, stream, nbytes: int = 1 << 30) -> float:
     """Device-to-device copy rate (GB/s, read + write bytes) of a plain
     torch copy kernel on this GPU: the practical HBM ceiling beside the
@@ -397,7 +426,8 @@ def main(argv=None) -> int:
     ap.add_argument("--tune-gemms", metavar="CSV", default=None,
                     help="time the mixed step's library GEMM candidates and write the "
                          "per-shape selection to CSV (torch TunableOp)")
-    ap.add_argument("--only", choices=["all", "kda", "prefill", "conv", "decode", "copy", "mixed", "long"],
+    ap.add_argument("--only", choices=["all", "kda", "prefill", "conv", "decode", "copy", "mixed", "long",
+                                       "bwd"],
                     default="all",
                     help="run one workload only (for kernel profiling; 'kda' = prefill, ShortConv "
                          "and decode without the decoder step); the JSON line then carries that "
@@ -552,6 +582,9 @@ def main(argv=None) -> int:
     if args.only in ("all", "kda", "long"):
         result["long_prefill"] = long_prefill_bench(torch, dev, stream, max(args.steps // 2, 5),
                                                     max(args.warmup // 2, 2), traffic)
+    if args.only in ("all", "bwd"):
+        result["backward"] = backward_bench(torch, dev, stream, inp, max(args.steps // 4, 3),
+                                            max(args.warmup // 2, 1))
     if args.only in ("all", "mixed"):
         result["mixed_step"] = mixed_step_bench(torch, dev, stream, max(args.steps // 2, 5),
                                                 max(args.warmup // 2, 2),
