@@ -24,6 +24,11 @@
  *                           chunk_size = 64, safe_gate, lower_bound, A_log, dt_bias)
  *   sophia_kda_decode_step  fla.ops.kda.fused_recurrent_kda as called at
  *                           attention.py:330-348 (T == 1 with a cached state)
+ *   sophia_kda_decode_conv_step  the two above in one launch (the conv step of
+ *                           attention.py:236-257 followed by 330-348)
+ *   sophia_kda_chunk_bwd    FlashKDA's chunk_kda_train_bwd with l2norm_bwd and
+ *                           fused_beta_sigmoid_bwd, as FlashKDAFunction.backward
+ *                           calls them (sm120_concurrent_ffn.py:301-373)
  */
 #ifndef SOPHIA_KDA_H
 #define SOPHIA_KDA_H
@@ -49,6 +54,11 @@ extern "C" {
 #define SOPHIA_KDA_QK_L2NORM 1u      /* q,k <- q/|q|, k/|k| (eps 1e-12)        */
 #define SOPHIA_KDA_GATE_IN_KERNEL 2u /* g <- lb*sigmoid(exp(A_log[h])*(g+dt_bias)) */
 #define SOPHIA_KDA_BETA_SIGMOID 4u   /* beta <- sigmoid(beta)                   */
+/* Prefill launch switch: keep one scan chain per sequence.  Without it, a
+ * batch of at most 4 sequences with host offsets whose longest sequence has
+ * at least 128 chunks is scanned segment-parallel (its results then differ
+ * from the single chain by rounding only). */
+#define SOPHIA_KDA_SCAN_NO_SEGMENTS 8u
 
 /* Message of the last failing call on this thread ("" if none). */
 const char *sophia_last_error(void);
@@ -115,10 +125,11 @@ size_t sophia_kda_chunk_workspace_size(int64_t total_tokens, int n_seqs, int num
  *                 not written.
  *   o           : [total_tokens, H, 128] rows of stride o_row_stride, dtype qkv_dtype.
  *   cu_seqlens_host: NULL, or a host copy of cu_seqlens (FlashKDA's
- *                 cu_seqlens_cpu, sm120_concurrent_ffn.py:231).  It only shapes
- *                 the launch (more work-groups per chain for a batch whose
- *                 longest sequence is at least twice the mean, longest
- *                 sequences first); results are identical with or without it.
+ *                 cu_seqlens_cpu, sm120_concurrent_ffn.py:231).  It shapes
+ *                 the launch (longest sequences first, more work-groups per
+ *                 chain for long chains, segments for a few long sequences --
+ *                 see SOPHIA_KDA_SCAN_NO_SEGMENTS); results are identical with
+ *                 or without it, but for the rounding of segmented chains.
  *                 Must be non-decreasing within [0, total_tokens].
  *   workspace   : device scratch of sophia_kda_chunk_workspace_size() bytes,
  *                 256-byte aligned; contents need not be initialised.

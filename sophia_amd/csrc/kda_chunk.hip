@@ -760,6 +760,14 @@ constexpr int kMaxClasses = 4;
 // while the U/O waves finish O and store it.  Each role streams only its own
 // record fragments, through a ring of register buffers of its own.
 constexpr int kScanThreads = 512;
+// What a scan work-group computes.
+//  kModeRun:      the chain's outputs O and its final state.
+//  kModeComposeM: the linear part M of the chain's map S -> M S + B (start
+//                 from S = I, no Ut, no O); fin receives M.
+//  kModeComposeB: its affine part B (start from S = 0, no O); fin receives B.
+constexpr int kModeRun = 0;
+constexpr int kModeComposeM = 1;
+constexpr int kModeComposeB = 2;
 // Ring depths (record buffers in flight): the U/O buffers grow with the
 // number of value-column tiles, so the widest work-group keeps two.
 template <int NT>
@@ -780,16 +788,19 @@ struct SFrags {
 };
 
 // The operands used before the U barrier (-W, Q e^G, Ut) ...
-template <int NT>
+template <int NT, int MODE = kModeRun>
 __device__ __forceinline__ void load_uo_main(UOFrags<NT> &f, const uint8_t *rec, int w, int l, int nt0) {
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
     f.wn[ks] = *reinterpret_cast<const u4 *>(rec + kOffW + ((w * 4 + ks) * 64 + l) * 16);
-    f.qb[ks] = *reinterpret_cast<const u4 *>(rec + kOffQ + ((w * 4 + ks) * 64 + l) * 16);
+    if constexpr (MODE == kModeRun)
+      f.qb[ks] = *reinterpret_cast<const u4 *>(rec + kOffQ + ((w * 4 + ks) * 64 + l) * 16);
   }
+  if constexpr (MODE != kModeComposeM) {
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt)
-    f.ut[nt] = *reinterpret_cast<const u2 *>(rec + kOffU + ((w * 8 + nt0 + nt) * 64 + l) * 8);
+    for (int nt = 0; nt < NT; ++nt)
+      f.ut[nt] = *reinterpret_cast<const u2 *>(rec + kOffU + ((w * 8 + nt0 + nt) * 64 + l) * 8);
+  }
 }
 // ... and A_qk, used after it.
 template <int NT>
@@ -812,13 +823,20 @@ __device__ __forceinline__ void load_s(SFrags &f, const uint8_t *rec, int sw, in
 
 // Makes the wave wait for the loads of a buffer here: an empty asm statement
 // that reads every register of it.
-template <int NT>
+template <int NT, int MODE = kModeRun>
 __device__ __forceinline__ void touch(const UOFrags<NT> &f) {
+  if constexpr (MODE == kModeRun) {
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) asm volatile("" ::"v"(f.wn[ks]), "v"(f.qb[ks]));
-  asm volatile("" ::"v"(f.aq[0]), "v"(f.aq[1]));
+    for (int ks = 0; ks < 4; ++ks) asm volatile("" ::"v"(f.wn[ks]), "v"(f.qb[ks]));
+    asm volatile("" ::"v"(f.aq[0]), "v"(f.aq[1]));
+  } else {
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) asm volatile("" ::"v"(f.ut[nt]));
+    for (int ks = 0; ks < 4; ++ks) asm volatile("" ::"v"(f.wn[ks]));
+  }
+  if constexpr (MODE != kModeComposeM) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) asm volatile("" ::"v"(f.ut[nt]));
+  }
 }
 __device__ __forceinline__ void touch(const SFrags &f) {
   asm volatile("" ::"v"(f.kt[0][0]), "v"(f.kt[0][1]), "v"(f.kt[1][0]), "v"(f.kt[1][1]));
@@ -827,10 +845,22 @@ __device__ __forceinline__ void touch(const SFrags &f) {
 
 struct ScanGeom {
   int h, nt0, nchunks;
-  int64_t seq_a, seq_b;
+  int64_t tok_a, seq_b;
   const uint8_t *rec0;
   size_t rec_stride;
 };
+
+// Work of one scan work-group: a chain of consecutive chunks of one sequence
+// (the whole sequence, or one segment of it).
+struct Chain {
+  int first;          // global number of the chain's first chunk
+  int nchunks;        // chunks in the chain
+  int64_t tok_a;      // first token of the chain
+  int64_t seq_b;      // end of its sequence: rows at or past it go to the scratch rows
+  const float *init;  // [128][128] fp32 state entering the chain, or NULL (zero)
+  float *fin;         // where the state leaving the chain goes, or NULL
+};
+
 
 // One chunk of the U/O role, in two parts around the U barrier (two
 // barriers in all).
@@ -840,7 +870,7 @@ struct ScanGeom {
 // products gives O^T = S^T (Q e^G)^T + U^T A_qk^T with the same fragments.  The
 // O^T C tile puts 4 consecutive value columns of one token row in each lane:
 // one 8-byte (bf16) or 16-byte (fp32) store per tile.
-template <int NT>
+template <int NT, int MODE = kModeRun>
 __device__ __forceinline__ void uo_pre(const UOFrags<NT> &f, f4 (&O)[NT], const uint8_t *sSb, uint8_t *sUb,
                                        int w, int l) {
   lds_barrier();  // S of this chunk is published
@@ -850,17 +880,22 @@ __device__ __forceinline__ void uo_pre(const UOFrags<NT> &f, f4 (&O)[NT], const 
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
       sb[ks] = bits_to_bf8(*reinterpret_cast<const u4 *>(sSb + ((ks * NT + nt) * 64 + l) * 16));
-    const u2 uw = f.ut[nt];
-    f4 u = {__uint_as_float(uw.x << 16), __uint_as_float(uw.x & 0xffff0000u),
-            __uint_as_float(uw.y << 16), __uint_as_float(uw.y & 0xffff0000u)};
+    f4 u = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (MODE != kModeComposeM) {
+      const u2 uw = f.ut[nt];
+      u = f4{__uint_as_float(uw.x << 16), __uint_as_float(uw.x & 0xffff0000u),
+             __uint_as_float(uw.y << 16), __uint_as_float(uw.y & 0xffff0000u)};
+    }
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) u = mfma32(bits_to_bf8(f.wn[ks]), sb[ks], u);
     // U rows 16w.. are half (w & 1) of K-step w / 2 of the U operand.
     *reinterpret_cast<u2 *>(sUb + (((w >> 1) * NT + nt) * 64 + l) * 16 + (w & 1) * 8) = pack4_bf16(u);
-    f4 o = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (MODE == kModeRun) {
+      f4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) o = mfma32(sb[ks], bits_to_bf8(f.qb[ks]), o);
-    O[nt] = o;   // O^T tiles: value columns 16(nt0 + nt) + 4gq + e, token row 16w + lr
+      for (int ks = 0; ks < 4; ++ks) o = mfma32(sb[ks], bits_to_bf8(f.qb[ks]), o);
+      O[nt] = o;   // O^T tiles: value columns 16(nt0 + nt) + 4gq + e, token row 16w + lr
+    }
   }
   lds_barrier();  // U is published
 }
@@ -882,7 +917,7 @@ __device__ __forceinline__ void uo_post(const ScanArgs &p, const ScanGeom &g, co
       O[nt] = mfma32(u1, bits_to_bf8(f.aq[1]), O[nt]);
     }
   }
-  const int64_t tok0 = g.seq_a + static_cast<int64_t>(cc) * kC;
+  const int64_t tok0 = g.tok_a + static_cast<int64_t>(cc) * kC;
   const int r = 16 * w + lr;
   const bool row_ok = static_cast<int64_t>(r) < g.seq_b - tok0;
   const int64_t col = static_cast<int64_t>(g.h) * kD + 16 * g.nt0 + 4 * gq;
@@ -947,10 +982,11 @@ __device__ __forceinline__ void state_update(const SFrags &f, f4 (&S)[2][NT], ui
 // over every path into it, so a prologue that interleaves the loads of two
 // buffers makes every later step wait for its newest buffer too.
 //
-// scan_item: one (sequence s, head h, value-column slice `half`) of the scan
-// on 512 threads, with the S and U exchange buffers at sSb / sUb.
-template <int NVB, int O_DT>
-__device__ __forceinline__ void scan_item(const ScanArgs &p, int s, int first, int h, int half, uint8_t *sSb,
+// scan_item: one chain (a sequence or a segment of one), head h and
+// value-column slice `half` of the scan on 512 threads, with the S and U
+// exchange buffers at sSb / sUb.  MODE selects what the chain computes.
+template <int NVB, int O_DT, int MODE>
+__device__ __forceinline__ void scan_item(const ScanArgs &p, const Chain &c, int h, int half, uint8_t *sSb,
                                           uint8_t *sUb) {
   constexpr int NT = NVB / 16;               // 16-column tiles per work-group
   const int tid = threadIdx.x;
@@ -960,14 +996,13 @@ __device__ __forceinline__ void scan_item(const ScanArgs &p, int s, int first, i
   ScanGeom g;
   g.h = h;
   g.nt0 = half * NT;
-  g.seq_a = iclamp64(p.cu[s], 0, p.total);
-  g.seq_b = iclamp64(p.cu[s + 1], g.seq_a, p.total);
+  g.tok_a = c.tok_a;
+  g.seq_b = c.seq_b;
   // Wave-uniform by construction; readfirstlane makes the compiler see it, so
   // that the per-chunk `live` tests below are scalar branches (a store under a
   // divergent branch makes the compiler drain the ring loads at the join).
-  g.nchunks = __builtin_amdgcn_readfirstlane(
-      static_cast<int>(imin64((g.seq_b - g.seq_a + kC - 1) / kC, p.max_ch - first)));
-  g.rec0 = p.records + (static_cast<size_t>(first) * p.num_heads + h) * kRecBytes;
+  g.nchunks = __builtin_amdgcn_readfirstlane(c.nchunks);
+  g.rec0 = p.records + (static_cast<size_t>(c.first) * p.num_heads + h) * kRecBytes;
   g.rec_stride = static_cast<size_t>(p.num_heads) * kRecBytes;
   const int nchunks = g.nchunks;
   const int last = nchunks - 1;
@@ -981,24 +1016,26 @@ __device__ __forceinline__ void scan_item(const ScanArgs &p, int s, int first, i
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const uint8_t *rec = g.rec0 + min(r, last) * g.rec_stride;
-      load_uo_main<NT>(f[r], rec, w, l, g.nt0);
-      load_uo_aq<NT>(f[r], rec, w, l);
+      load_uo_main<NT, MODE>(f[r], rec, w, l, g.nt0);
+      if constexpr (MODE == kModeRun) load_uo_aq<NT>(f[r], rec, w, l);
       __builtin_amdgcn_sched_barrier(0);  // keep the ring order (see above)
     }
-    touch<NT>(f[0]);
+    touch<NT, MODE>(f[0]);
     for (int cc = 0; cc < nchunks; cc += R) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const bool live = cc + r < nchunks;
         const uint8_t *rec = g.rec0 + min(cc + r + R, last) * g.rec_stride;
         f4 O[NT];
-        if (live) uo_pre<NT>(f[r], O, sSb, sUb, w, l);
+        if (live) uo_pre<NT, MODE>(f[r], O, sSb, sUb, w, l);
         // Refill while the state role works: the loads may wait for memory
         // queue space here, off the critical path.
-        load_uo_main<NT>(f[r], rec, w, l, g.nt0);
-        if (live) uo_post<NT, O_DT>(p, g, f[r], O, sUb, w, l, cc + r);
-        load_uo_aq<NT>(f[r], rec, w, l);
-        touch<NT>(f[(r + 1) % R]);
+        load_uo_main<NT, MODE>(f[r], rec, w, l, g.nt0);
+        if constexpr (MODE == kModeRun) {
+          if (live) uo_post<NT, O_DT>(p, g, f[r], O, sUb, w, l, cc + r);
+          load_uo_aq<NT>(f[r], rec, w, l);
+        }
+        touch<NT, MODE>(f[(r + 1) % R]);
       }
     }
     return;
@@ -1007,20 +1044,19 @@ __device__ __forceinline__ void scan_item(const ScanArgs &p, int s, int first, i
   // ---- state role: S tiles [mi 2][nt NT], rows 32sw + 16mi + 4gq + e,
   // column 16(nt0 + nt) + lr.
   const int sw = wave - 4;
-  const int slot = p.slots ? p.slots[s] : s;
-  const bool has_slot = slot >= 0 && slot < p.n_slots;  // else: zero start, nothing written
-  const int64_t state_off = (static_cast<int64_t>(has_slot ? slot : 0) * p.num_heads + h) * kD * kD;
   f4 S[2][NT];
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       f4 v = {0.f, 0.f, 0.f, 0.f};
-      if (p.h0 && has_slot) {
+      if constexpr (MODE == kModeComposeM) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (32 * sw + 16 * mi + 4 * gq + e == 16 * (g.nt0 + nt) + lr) ? 1.f : 0.f;
+      } else if (c.init) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          v[e] = p.h0[state_off + static_cast<int64_t>(32 * sw + 16 * mi + 4 * gq + e) * kD +
-                      16 * (g.nt0 + nt) + lr];
+          v[e] = c.init[static_cast<int64_t>(32 * sw + 16 * mi + 4 * gq + e) * kD + 16 * (g.nt0 + nt) + lr];
       }
       S[mi][nt] = v;
     }
@@ -1046,16 +1082,30 @@ __device__ __forceinline__ void scan_item(const ScanArgs &p, int s, int first, i
       }
     }
   }
-  if (p.ht && has_slot) {
+  if (c.fin) {
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          p.ht[state_off + static_cast<int64_t>(32 * sw + 16 * mi + 4 * gq + e) * kD + 16 * (g.nt0 + nt) + lr] =
-              S[mi][nt][e];
+          c.fin[static_cast<int64_t>(32 * sw + 16 * mi + 4 * gq + e) * kD + 16 * (g.nt0 + nt) + lr] = S[mi][nt][e];
   }
+}
+
+// The chain of a whole sequence s, with its state slot.
+__device__ __forceinline__ Chain sequence_chain(const ScanArgs &p, int s, int h) {
+  Chain c;
+  c.first = first_chunk(p.cu, p.n_seqs, p.total, s);
+  c.tok_a = iclamp64(p.cu[s], 0, p.total);
+  c.seq_b = iclamp64(p.cu[s + 1], c.tok_a, p.total);
+  c.nchunks = static_cast<int>(imin64((c.seq_b - c.tok_a + kC - 1) / kC, p.max_ch - c.first));
+  const int slot = p.slots ? p.slots[s] : s;
+  const bool has_slot = slot >= 0 && slot < p.n_slots;  // else: zero start, nothing written
+  const int64_t state_off = (static_cast<int64_t>(has_slot ? slot : 0) * p.num_heads + h) * kD * kD;
+  c.init = p.h0 && has_slot ? p.h0 + state_off : nullptr;
+  c.fin = p.ht && has_slot ? p.ht + state_off : nullptr;
+  return c;
 }
 
 template <int O_DT>
@@ -1083,13 +1133,232 @@ __global__ __launch_bounds__(kScanThreads) void kda_chunk_scan_kernel(ScanArgs p
   const int rank = rank_lo + sh / p.num_heads;
   if (rank >= rank_hi || rank >= p.n_seqs) return;
   const int s = rank < kOrderMax ? static_cast<int>((p.order_bits >> (4 * rank)) & 15u) : rank;
-  const int first = first_chunk(p.cu, p.n_seqs, p.total, s);
+  const Chain c = sequence_chain(p, s, h);
   switch (splits) {
-    case 8: scan_item<16, O_DT>(p, s, first, h, half, sSb, sUb); break;
-    case 4: scan_item<32, O_DT>(p, s, first, h, half, sSb, sUb); break;
-    case 2: scan_item<64, O_DT>(p, s, first, h, half, sSb, sUb); break;
-    default: scan_item<128, O_DT>(p, s, first, h, half, sSb, sUb); break;
+    case 8: scan_item<16, O_DT, kModeRun>(p, c, h, half, sSb, sUb); break;
+    case 4: scan_item<32, O_DT, kModeRun>(p, c, h, half, sSb, sUb); break;
+    case 2: scan_item<64, O_DT, kModeRun>(p, c, h, half, sSb, sUb); break;
+    default: scan_item<128, O_DT, kModeRun>(p, c, h, half, sSb, sUb); break;
   }
+}
+
+// ---- segment-parallel scan ----------------------------------------------------
+// A batch of a few long sequences leaves most of the chip idle in the scan
+// above: 16 heads x 8 slices of one sequence are 128 chains of 1,024 chunk
+// steps each for 65,536 tokens.  The chunk step is affine in the state,
+// S1 = M S0 + B with M = Diag(e^{G_C}) - Kbar^T W and B = Kbar^T Ut, so a
+// sequence is cut into segments of kSegChunks chunks, run in three launches:
+//  1. compose: every segment but the last runs its chain twice without
+//     outputs, from S = I without Ut (giving its M) and from S = 0 (giving
+//     its B), into `maps`;
+//  2. prefix: per (sequence, head, 16 value columns), the states entering
+//     segments 1.. in turn, S <- M S + B in fp32, into `sin`;
+//  3. run: every segment runs its chain with outputs from its entering state
+//     (the sequence's initial state for segment 0); the last one writes the
+//     final state.
+// Launches 1 and 3 are chains of kSegChunks steps over many more work-groups.
+// Results differ from the single chain by rounding only (the bf16 operand
+// rounding of the state inside each chain, and the fp32 products of step 2).
+constexpr int kSegChunks = 64;
+constexpr int kSegSeqMax = 4;
+struct SegArgs {
+  ScanArgs p;
+  int n;                               // sequences (<= kSegSeqMax)
+  int run0, run1, run2, run3, run4;    // first segment of sequence s (run4 = all segments)
+  int cmp0, cmp1, cmp2, cmp3, cmp4;    // first composed segment of sequence s
+  int splits;                          // work-groups per (segment, head) and 128 columns
+  float *maps;                         // [segments][H][2][128][128] fp32: M, B
+  float *sin;                          // [segments][H][128][128] fp32: state entering the segment
+};
+
+__device__ __forceinline__ int seq_of(int x, int a1, int a2, int a3, int n) {
+  return (n > 1 && x >= a1) + (n > 2 && x >= a2) + (n > 3 && x >= a3);
+}
+__device__ __forceinline__ int pick(int s, int a0, int a1, int a2, int a3, int a4) {
+  return s == 0 ? a0 : s == 1 ? a1 : s == 2 ? a2 : s == 3 ? a3 : a4;
+}
+
+// Work-group b -> (item, sub): the `subs` work-groups of one item share
+// b mod 8, i.e. one XCD and its L2 (they read the same records).
+__device__ __forceinline__ void seg_item(int b, int subs, int &item, int &sub) {
+  const int group = b / (8 * subs);
+  sub = (b / 8) % subs;
+  item = group * 8 + (b % 8);
+}
+
+__global__ __launch_bounds__(kScanThreads) void kda_chunk_seg_compose_kernel(SegArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t sSb[4 * 8 * 64 * 16];
+  __shared__ __attribute__((aligned(16))) uint8_t sUb[2 * 8 * 64 * 16];
+  const ScanArgs &p = a.p;
+  int item, sub;
+  seg_item(blockIdx.x, 2 * a.splits, item, sub);
+  const int h = item % p.num_heads;
+  const int ci = item / p.num_heads;
+  if (ci >= a.cmp4) return;
+  const int s = seq_of(ci, a.cmp1, a.cmp2, a.cmp3, a.n);
+  const int j = ci - pick(s, a.cmp0, a.cmp1, a.cmp2, a.cmp3, a.cmp4);
+  const bool affine = sub >= a.splits;
+  const int half = sub % a.splits;
+  Chain c = sequence_chain(p, s, h);
+  c.first += j * kSegChunks;
+  c.tok_a += static_cast<int64_t>(j) * kSegChunks * kC;
+  c.nchunks = static_cast<int>(imin64(imin64(kSegChunks, c.nchunks - j * kSegChunks), p.max_ch - c.first));
+  c.init = nullptr;
+  const int seg = pick(s, a.run0, a.run1, a.run2, a.run3, a.run4) + j;
+  c.fin = a.maps + ((static_cast<size_t>(seg) * p.num_heads + h) * 2 + (affine ? 1 : 0)) * kD * kD;
+  switch (a.splits) {
+    case 8:
+      if (affine) scan_item<16, SOPHIA_DTYPE_BF16, kModeComposeB>(p, c, h, half, sSb, sUb);
+      else scan_item<16, SOPHIA_DTYPE_BF16, kModeComposeM>(p, c, h, half, sSb, sUb);
+      break;
+    case 4:
+      if (affine) scan_item<32, SOPHIA_DTYPE_BF16, kModeComposeB>(p, c, h, half, sSb, sUb);
+      else scan_item<32, SOPHIA_DTYPE_BF16, kModeComposeM>(p, c, h, half, sSb, sUb);
+      break;
+    case 2:
+      if (affine) scan_item<64, SOPHIA_DTYPE_BF16, kModeComposeB>(p, c, h, half, sSb, sUb);
+      else scan_item<64, SOPHIA_DTYPE_BF16, kModeComposeM>(p, c, h, half, sSb, sUb);
+      break;
+    default:
+      if (affine) scan_item<128, SOPHIA_DTYPE_BF16, kModeComposeB>(p, c, h, half, sSb, sUb);
+      else scan_item<128, SOPHIA_DTYPE_BF16, kModeComposeM>(p, c, h, half, sSb, sUb);
+      break;
+  }
+}
+
+// One 256-thread work-group per (sequence, head, 16 value columns): thread t
+// owns state row t / 2 and columns 8 (t % 2) .. +7 of the slice.
+__global__ __launch_bounds__(256) void kda_chunk_seg_prefix_kernel(SegArgs a) {
+  __shared__ __attribute__((aligned(16))) float sS[2][kD][16];
+  const ScanArgs &p = a.p;
+  const int slice = blockIdx.x % 8;
+  const int sh = blockIdx.x / 8;
+  const int h = sh % p.num_heads;
+  const int s = sh / p.num_heads;
+  if (s >= a.n) return;
+  const int seg0 = pick(s, a.run0, a.run1, a.run2, a.run3, a.run4);
+  const int nseg = pick(s + 1, a.run0, a.run1, a.run2, a.run3, a.run4) - seg0;
+  if (nseg <= 1) return;
+  const int t = threadIdx.x;
+  const int row = t >> 1, c8 = (t & 1) * 8, col = 16 * slice + c8;
+  const Chain c = sequence_chain(p, s, h);
+  float *first_in = a.sin + (static_cast<size_t>(seg0) * p.num_heads + h) * kD * kD + row * kD + col;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float v = c.init ? c.init[row * kD + col + i] : 0.f;
+    sS[0][row][c8 + i] = v;
+    first_in[i] = v;
+  }
+  __syncthreads();
+  int cur = 0;
+  for (int j = 0; j + 1 < nseg; ++j) {
+    const size_t seg = static_cast<size_t>(seg0 + j);
+    const float *M = a.maps + ((seg * p.num_heads + h) * 2) * kD * kD;
+    const float *B = M + kD * kD;
+    float acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = B[row * kD + col + i];
+    for (int k = 0; k < kD; k += 4) {
+      const f4 m = *reinterpret_cast<const f4 *>(M + row * kD + k);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = fmaf(m[kk], sS[cur][k + kk][c8 + i], acc[i]);
+    }
+    float *dst = a.sin + ((seg + 1) * p.num_heads + h) * kD * kD + row * kD + col;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      sS[cur ^ 1][row][c8 + i] = acc[i];
+      dst[i] = acc[i];
+    }
+    __syncthreads();
+    cur ^= 1;
+  }
+}
+
+template <int O_DT>
+__global__ __launch_bounds__(kScanThreads) void kda_chunk_seg_run_kernel(SegArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t sSb[4 * 8 * 64 * 16];
+  __shared__ __attribute__((aligned(16))) uint8_t sUb[2 * 8 * 64 * 16];
+  const ScanArgs &p = a.p;
+  int item, half;
+  seg_item(blockIdx.x, a.splits, item, half);
+  const int h = item % p.num_heads;
+  const int gi = item / p.num_heads;
+  if (gi >= a.run4) return;
+  const int s = seq_of(gi, a.run1, a.run2, a.run3, a.n);
+  const int seg0 = pick(s, a.run0, a.run1, a.run2, a.run3, a.run4);
+  const int nseg = pick(s + 1, a.run0, a.run1, a.run2, a.run3, a.run4) - seg0;
+  const int j = gi - seg0;
+  Chain c = sequence_chain(p, s, h);
+  if (nseg > 1) {
+    // A segmented sequence's segments all start from `sin` (segment 0's copy
+    // of the initial state was made by the prefix launch, so a final state
+    // that aliases the initial one is written only after it was read).
+    c.first += j * kSegChunks;
+    c.tok_a += static_cast<int64_t>(j) * kSegChunks * kC;
+    c.nchunks = static_cast<int>(imin64(imin64(kSegChunks, c.nchunks - j * kSegChunks), p.max_ch - c.first));
+    c.init = a.sin + (static_cast<size_t>(gi) * p.num_heads + h) * kD * kD;
+    if (j + 1 < nseg) c.fin = nullptr;
+  }
+  switch (a.splits) {
+    case 8: scan_item<16, O_DT, kModeRun>(p, c, h, half, sSb, sUb); break;
+    case 4: scan_item<32, O_DT, kModeRun>(p, c, h, half, sSb, sUb); break;
+    case 2: scan_item<64, O_DT, kModeRun>(p, c, h, half, sSb, sUb); break;
+    default: scan_item<128, O_DT, kModeRun>(p, c, h, half, sSb, sUb); break;
+  }
+}
+
+// Upper bound on the segments of any batch of total_tokens tokens: only a
+// sequence of at least 2 kSegChunks chunks is segmented, so the segments
+// number at most 1.5 (1 + 1 / (2 kSegChunks - 1)) total / (64 kSegChunks).
+inline int64_t max_segments(int64_t total_tokens) {
+  if (total_tokens < static_cast<int64_t>(2 * kSegChunks - 1) * kC + 1) return 0;
+  return 2 * (total_tokens / (static_cast<int64_t>(kSegChunks) * kC)) + 2;
+}
+inline size_t seg_bytes(int64_t total_tokens, int num_heads) {
+  return static_cast<size_t>(max_segments(total_tokens)) * num_heads * 3 * kD * kD * sizeof(float);
+}
+
+struct SegPlan {
+  bool on = false;
+  int run[kSegSeqMax + 1] = {};
+  int cmp[kSegSeqMax + 1] = {};
+  int run_splits = 1, cmp_splits = 1;
+};
+
+// Segments are used for at most kSegSeqMax sequences with host offsets, when
+// their (sequence, head) pairs are too few to fill the chip with 4 slices
+// each and the longest has at least 2 kSegChunks chunks.
+SegPlan plan_segments(const int32_t *cu_host, int n_seqs, int num_heads, int cus, int64_t total,
+                      unsigned flags) {
+  SegPlan pl;
+  if (!cu_host || n_seqs > kSegSeqMax || (flags & SOPHIA_KDA_SCAN_NO_SEGMENTS)) return pl;
+  if (static_cast<int64_t>(n_seqs) * num_heads * 4 > cus) return pl;
+  int64_t chunks[kSegSeqMax] = {}, nmax = 0;
+  for (int i = 0; i < n_seqs; ++i) {
+    const int64_t a = iclamp64(cu_host[i], 0, total);
+    const int64_t b = iclamp64(cu_host[i + 1], a, total);
+    chunks[i] = (b - a + kC - 1) / kC;
+    nmax = chunks[i] > nmax ? chunks[i] : nmax;
+  }
+  if (nmax < 2 * kSegChunks) return pl;
+  for (int i = 0; i < n_seqs; ++i) {
+    const int64_t nseg = chunks[i] >= 2 * kSegChunks ? (chunks[i] + kSegChunks - 1) / kSegChunks : 1;
+    pl.run[i + 1] = pl.run[i] + static_cast<int>(nseg);
+    pl.cmp[i + 1] = pl.cmp[i] + static_cast<int>(nseg - 1);
+  }
+  for (int i = n_seqs + 1; i <= kSegSeqMax; ++i) {
+    pl.run[i] = pl.run[n_seqs];
+    pl.cmp[i] = pl.cmp[n_seqs];
+  }
+  if (pl.run[n_seqs] > max_segments(total)) return pl;  // cannot happen (bound above)
+  const int64_t run_pairs = static_cast<int64_t>(pl.run[n_seqs]) * num_heads;
+  const int64_t cmp_pairs = static_cast<int64_t>(pl.cmp[n_seqs]) * num_heads * 2;
+  while (pl.run_splits < 8 && run_pairs * pl.run_splits * 2 <= cus) pl.run_splits *= 2;
+  while (pl.cmp_splits < 8 && cmp_pairs * pl.cmp_splits * 2 <= cus) pl.cmp_splits *= 2;
+  pl.on = true;
+  return pl;
 }
 
 // Host-side plan of the scan launch.  Every (sequence, head) pair of the
@@ -1207,7 +1476,8 @@ extern "C" size_t sophia_kda_chunk_workspace_size(int64_t total_tokens, int n_se
                                                   int head_dim) {
   if (total_tokens < 0 || n_seqs <= 0 || num_heads <= 0 || head_dim != kD) return 0;
   return kTrashBytes +
-         static_cast<size_t>(max_chunks(total_tokens, n_seqs)) * num_heads * kRecBytes;
+         static_cast<size_t>(max_chunks(total_tokens, n_seqs)) * num_heads * kRecBytes +
+         seg_bytes(total_tokens, num_heads);
 }
 
 namespace {
@@ -1288,11 +1558,42 @@ int chunk_fwd_impl(const void *q, const void *k, const void *v, int64_t qkv_row_
   // The state scan is sequential over the chunks of a sequence: the 128
   // value columns of each (sequence, head) are split over 1, 2, 4 or 8
   // work-groups (plan_scan), so that a small batch still spreads its
-  // critical path over the chip.  The host copy of the offsets only shapes
-  // this plan; results do not depend on it.
+  // critical path over the chip.  The host copy of the offsets shapes this
+  // plan; results do not depend on it, except that a few long sequences are
+  // cut into segments (plan_segments; rounding differences only, and
+  // SOPHIA_KDA_SCAN_NO_SEGMENTS keeps one chain per sequence).
   int device = 0, cus = 256;
   if (hipGetDevice(&device) == hipSuccess)
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) cus = 256;
+  const SegPlan sp = plan_segments(cu_seqlens_host, n_seqs, num_heads, cus, total_tokens, flags);
+  if (sp.on) {
+    float *maps = reinterpret_cast<float *>(records + static_cast<size_t>(max_ch) * num_heads * kRecBytes);
+    float *sin = maps + static_cast<size_t>(max_segments(total_tokens)) * num_heads * 2 * kD * kD;
+    SegArgs a{{cu_seqlens, n_seqs, total_tokens, num_heads, max_ch, records, initial_state, final_state,
+               n_state_slots, state_slots, o, o_row_stride, trash, 0, 1, 0, 0, 0, 0, 0, 0, 0, 0, 0, 1, 1, 1, 1},
+              n_seqs,
+              sp.run[0], sp.run[1], sp.run[2], sp.run[3], sp.run[4],
+              sp.cmp[0], sp.cmp[1], sp.cmp[2], sp.cmp[3], sp.cmp[4],
+              sp.cmp_splits, maps, sin};
+    const int64_t cmp_blocks = (static_cast<int64_t>(sp.cmp[n_seqs]) * num_heads + 7) / 8 * 8 * 2 * sp.cmp_splits;
+    if (cmp_blocks > 0) {
+      hipLaunchKernelGGL(kda_chunk_seg_compose_kernel, dim3(static_cast<unsigned>(cmp_blocks)),
+                         dim3(kScanThreads), 0, st, a);
+      if (const int rc2 = check_launch("kda_chunk_seg_compose")) return rc2;
+      hipLaunchKernelGGL(kda_chunk_seg_prefix_kernel, dim3(static_cast<unsigned>(n_seqs * num_heads * 8)),
+                         dim3(256), 0, st, a);
+      if (const int rc2 = check_launch("kda_chunk_seg_prefix")) return rc2;
+    }
+    a.splits = sp.run_splits;
+    const int64_t run_blocks = (static_cast<int64_t>(sp.run[n_seqs]) * num_heads + 7) / 8 * 8 * sp.run_splits;
+    if (qkv_dtype == SOPHIA_DTYPE_BF16)
+      hipLaunchKernelGGL(kda_chunk_seg_run_kernel<SOPHIA_DTYPE_BF16>, dim3(static_cast<unsigned>(run_blocks)),
+                         dim3(kScanThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL(kda_chunk_seg_run_kernel<SOPHIA_DTYPE_F32>, dim3(static_cast<unsigned>(run_blocks)),
+                         dim3(kScanThreads), 0, st, a);
+    return check_launch("kda_chunk_seg_run");
+  }
   const ScanPlan pl = plan_scan(cu_seqlens_host, n_seqs, num_heads, cus);
   SOPHIA_REQUIRE(pl.blocks > 0 && pl.blocks <= 0x7fffffff, "kda_chunk_fwd: grid too large");
   ScanArgs sa{cu_seqlens, n_seqs, total_tokens, num_heads, max_ch, records,

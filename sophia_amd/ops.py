@@ -199,7 +199,8 @@ def kda_chunk_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
                   final_state: torch.Tensor | None = None,
                   state_slots: torch.Tensor | None = None,
                   out: torch.Tensor | None = None,
-                  cu_seqlens_cpu: torch.Tensor | None = None) -> torch.Tensor:
+                  cu_seqlens_cpu: torch.Tensor | None = None,
+                  scan_segments: bool = True) -> torch.Tensor:
     """Chunk-64 KDA prefill over a packed batch.
 
     q, k, v, g: [total, H, 128] (rows may be strided views of a wider
@@ -208,7 +209,9 @@ def kda_chunk_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
     None, indexed by ``state_slots`` (default: sequence index); they may be
     the same tensor.  ``cu_seqlens_cpu`` (FlashKDA's name; default: cu_seqlens
     itself when it lives on the host) lets the launch be planned from the
-    sequence lengths; results are the same without it.
+    sequence lengths; results are the same without it, but that a few long
+    sequences are then scanned in segments (rounding differences only;
+    ``scan_segments=False`` keeps one chain per sequence).
     Returns o [total, H, 128] in q.dtype.
     """
     for t, name in ((q, "q"), (k, "k"), (v, "v"), (g, "g"), (beta, "beta")):
@@ -269,7 +272,8 @@ def kda_chunk_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
         nat.ptr(q), nat.ptr(k), nat.ptr(v), qs, nat.dtype_code(q.dtype), nat.ptr(g), gs,
         nat.dtype_code(g.dtype), nat.ptr(beta), bs, nat.dtype_code(beta.dtype), nat.ptr(a_log),
         nat.ptr(dtb), float(scale), float(lower_bound),
-        _flags(use_qk_l2norm, use_gate, use_beta_sigmoid), nat.ptr(cu),
+        _flags(use_qk_l2norm, use_gate, use_beta_sigmoid)
+        | (0 if scan_segments else nat.SCAN_NO_SEGMENTS), nat.ptr(cu),
         None if cu_host is None else cu_host.data_ptr(), n, total, heads, HEAD_DIM,
         nat.ptr(initial_state), nat.ptr(final_state), n_slots, nat.ptr(slots), nat.ptr(o), os_,
         ws_addr, ws_bytes, nat.stream_handle(device))
