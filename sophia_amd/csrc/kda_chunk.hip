@@ -1226,13 +1226,21 @@ __global__ __launch_bounds__(kScanThreads) void kda_chunk_seg_compose_kernel(Seg
   }
 }
 
-// One 256-thread work-group per (sequence, head, 16 value columns): thread t
-// owns state row t / 2 and columns 8 (t % 2) .. +7 of the slice.
+// One 256-thread work-group per (sequence, head, 16 value columns).  A step
+// S <- M S + B is 128 x 16 outputs on fp32 MFMA (16x16x4): wavefront w owns
+// rows 32w .. 32w + 31 as two 16 x 16 tiles over 32 k-steps.  M is staged in
+// LDS (rows padded to 132 floats: the 16 rows x 4 k of an A operand fall in
+// distinct banks); the next step's M and B are loaded into registers while
+// this step computes.
+constexpr int kLdM = kD + 4;
 __global__ __launch_bounds__(256) void kda_chunk_seg_prefix_kernel(SegArgs a) {
+  __shared__ __attribute__((aligned(16))) float sM[kD * kLdM];
   __shared__ __attribute__((aligned(16))) float sS[2][kD][16];
   const ScanArgs &p = a.p;
-  const int slice = blockIdx.x % 8;
-  const int sh = blockIdx.x / 8;
+  // The 8 slices of one (sequence, head) share blockIdx mod 8, i.e. one XCD,
+  // whose L2 then serves each map to all of them.
+  int sh, slice;
+  seg_item(blockIdx.x, 8, sh, slice);
   const int h = sh % p.num_heads;
   const int s = sh / p.num_heads;
   if (s >= a.n) return;
@@ -1240,38 +1248,65 @@ __global__ __launch_bounds__(256) void kda_chunk_seg_prefix_kernel(SegArgs a) {
   const int nseg = pick(s + 1, a.run0, a.run1, a.run2, a.run3, a.run4) - seg0;
   if (nseg <= 1) return;
   const int t = threadIdx.x;
-  const int row = t >> 1, c8 = (t & 1) * 8, col = 16 * slice + c8;
+  const int w = t >> 6, l = t & 63, x = l & 15, y = l >> 4;
+  const int col = 16 * slice + x;
   const Chain c = sequence_chain(p, s, h);
-  float *first_in = a.sin + (static_cast<size_t>(seg0) * p.num_heads + h) * kD * kD + row * kD + col;
+  {
+    // the state entering segment 0: thread t copies row t / 2, 8 columns
+    const int row = t >> 1, c8 = (t & 1) * 8;
+    float *first_in = a.sin + (static_cast<size_t>(seg0) * p.num_heads + h) * kD * kD + row * kD + 16 * slice + c8;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float v = c.init ? c.init[row * kD + col + i] : 0.f;
-    sS[0][row][c8 + i] = v;
-    first_in[i] = v;
+    for (int i = 0; i < 8; ++i) {
+      const float v = c.init ? c.init[row * kD + 16 * slice + c8 + i] : 0.f;
+      sS[0][row][c8 + i] = v;
+      first_in[i] = v;
+    }
   }
-  __syncthreads();
+  // M of segment `seg` into registers (piece i: row (t + 256 i) / 32, columns
+  // 4 ((t + 256 i) % 32) .. +3) and the B values of this lane's C tiles.
+  f4 mr[16];
+  f4 br[2];
+  const auto load_map = [&](size_t seg) {
+    const float *M = a.maps + ((seg * p.num_heads + h) * 2) * kD * kD;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int idx = t + 256 * i;
+      mr[i] = *reinterpret_cast<const f4 *>(M + (idx >> 5) * kD + 4 * (idx & 31));
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) br[r][i] = M[kD * kD + (32 * w + 16 * r + 4 * y + i) * kD + col];
+  };
+  load_map(static_cast<size_t>(seg0));
   int cur = 0;
   for (int j = 0; j + 1 < nseg; ++j) {
     const size_t seg = static_cast<size_t>(seg0 + j);
-    const float *M = a.maps + ((seg * p.num_heads + h) * 2) * kD * kD;
-    const float *B = M + kD * kD;
-    float acc[8];
+    __syncthreads();  // every wavefront is done with the previous M and S
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = B[row * kD + col + i];
-    for (int k = 0; k < kD; k += 4) {
-      const f4 m = *reinterpret_cast<const f4 *>(M + row * kD + k);
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] = fmaf(m[kk], sS[cur][k + kk][c8 + i], acc[i]);
+    for (int i = 0; i < 16; ++i) {
+      const int idx = t + 256 * i;
+      *reinterpret_cast<f4 *>(&sM[(idx >> 5) * kLdM + 4 * (idx & 31)]) = mr[i];
     }
-    float *dst = a.sin + ((seg + 1) * p.num_heads + h) * kD * kD + row * kD + col;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      sS[cur ^ 1][row][c8 + i] = acc[i];
-      dst[i] = acc[i];
-    }
+    f4 acc[2] = {br[0], br[1]};
     __syncthreads();
+    // the next map loads while this step computes
+    if (j + 2 < nseg) load_map(seg + 1);
+#pragma unroll 8
+    for (int ks = 0; ks < kD / 4; ++ks) {
+      const float b = sS[cur][4 * ks + y][x];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) acc[r] = mfma_f32x4(sM[(32 * w + 16 * r + x) * kLdM + 4 * ks + y], b, acc[r]);
+    }
+    float *dst = a.sin + ((seg + 1) * p.num_heads + h) * kD * kD;
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = 32 * w + 16 * r + 4 * y + i;
+        sS[cur ^ 1][row][x] = acc[r][i];
+        dst[row * kD + col] = acc[r][i];
+      }
     cur ^= 1;
   }
 }
@@ -1580,7 +1615,7 @@ int chunk_fwd_impl(const void *q, const void *k, const void *v, int64_t qkv_row_
       hipLaunchKernelGGL(kda_chunk_seg_compose_kernel, dim3(static_cast<unsigned>(cmp_blocks)),
                          dim3(kScanThreads), 0, st, a);
       if (const int rc2 = check_launch("kda_chunk_seg_compose")) return rc2;
-      hipLaunchKernelGGL(kda_chunk_seg_prefix_kernel, dim3(static_cast<unsigned>(n_seqs * num_heads * 8)),
+      hipLaunchKernelGGL(kda_chunk_seg_prefix_kernel, dim3(static_cast<unsigned>((n_seqs * num_heads + 7) / 8 * 64)),
                          dim3(256), 0, st, a);
       if (const int rc2 = check_launch("kda_chunk_seg_prefix")) return rc2;
     }
