@@ -17,7 +17,8 @@
 //
 // Kernels:
 //  * kda_bwd_prep_kernel, one work-group of 128 threads per (token, head):
-//    q^, k^, the log-decay g (gate applied) and beta (sigmoid applied), fp32.
+//    q^, k^, the decay alpha = e^g (gate applied) and beta (sigmoid applied),
+//    fp32.
 //  * kda_bwd_chain_kernel, one work-group of 512 threads per (sequence, head,
 //    32-column value slice): the value columns of the state evolve
 //    independently, so each slice runs the recurrence alone.  It first runs
@@ -25,8 +26,11 @@
 //    (in the workspace); then, chunk by chunk in reverse, it recomputes the
 //    chunk forward keeping the state every 8 tokens in LDS, and for each
 //    8-token piece in reverse recomputes its states in registers and runs the
-//    reverse steps.  Sums over value columns (dq^, dk^, dalpha) leave as
-//    per-slice partials; dbeta leaves per value column.
+//    reverse steps.  Every 8-token piece it walks is staged in LDS by the
+//    whole work-group, the next piece's loads in flight while the current one
+//    is processed (one-token-ahead register loads left every step waiting on
+//    memory).  Sums over value columns (dq^, dk^, dalpha) leave as per-slice
+//    partials; dbeta leaves per value column.
 //  * kda_bwd_post_kernel, one work-group of 128 threads per (token, head):
 //    sums the partials and applies the backward of the l2 norms, of the gate
 //    g = lb sigmoid(e^A_log (z + dt_bias)) and of the beta sigmoid.
@@ -54,7 +58,7 @@ constexpr int kChainThreads = 512;
 constexpr int kRows = kD / (kChainThreads / kNV);   // state rows per thread: 8
 constexpr int kGateParts = 64;   // token partitions of the dA_log / ddt_bias sums
 constexpr int kMaxDevices = 64;
-constexpr size_t kChainLds = (static_cast<size_t>(kC / kSub) * kD * kNV + 2 * 8 * kNV) * sizeof(float);
+constexpr size_t kChainLdsFloats = static_cast<size_t>(kC / kSub) * kD * kNV + 2 * 8 * kNV;
 
 struct BwdArgs {
   // inputs
@@ -82,7 +86,7 @@ struct BwdArgs {
   // outputs (fp32)
   float *dq, *dk, *dv, *dg, *dbeta, *dh0, *dA_log, *ddt_bias;
   // workspace
-  float *qh, *kh, *gl, *bt;        // prepared q^, k^, log-decay, beta
+  float *qh, *kh, *gl, *bt;        // prepared q^, k^, alpha = e^g, beta
   float *ckpt;                     // [chunks, H, 128, 128] chunk-start states
   float *dqh, *dkh, *dal;          // [kSlices, total, H, 128] partial sums
   float *dbc;                      // [total, H, 128] dbeta per value column
@@ -116,7 +120,7 @@ __global__ __launch_bounds__(kD) void kda_bwd_prep_kernel(BwdArgs a) {
   const int64_t o = (tok * a.num_heads + h) * kD + c;
   a.qh[o] = qv * qs;
   a.kh[o] = kv * ks;
-  a.gl[o] = z;
+  a.gl[o] = expf(z);
   if (c == 0) {
     if (a.flags & SOPHIA_KDA_BETA_SIGMOID) b = 1.f / (1.f + expf(-b));
     a.bt[tok * a.num_heads + h] = b;
@@ -124,6 +128,16 @@ __global__ __launch_bounds__(kD) void kda_bwd_prep_kernel(BwdArgs a) {
 }
 
 // ---- chain --------------------------------------------------------------------
+// The inputs of one 8-token piece, staged in LDS for the whole work-group
+// (rows of q^, k^, alpha; the slice's 32 columns of v and of do; beta).
+struct Piece {
+  float q[kSub][kD], k[kSub][kD], al[kSub][kD];
+  float v[kSub][kNV], dout[kSub][kNV];
+  float bt[kSub];
+};
+
+constexpr size_t kChainLds = kChainLdsFloats * sizeof(float) + 2 * sizeof(Piece);
+
 struct ChainCtx {
   const BwdArgs *a;
   int h, col, j, rg, lane, wave;
@@ -148,26 +162,25 @@ __device__ __forceinline__ float row_sum(const ChainCtx &c, float x, int &kb) {
 
 // The inputs of one token for the thread's rows and column.
 struct TokenIn {
-  f4 q[kRows / 4], k[kRows / 4], g[kRows / 4];
-  float v, bt;
+  f4 q[kRows / 4], k[kRows / 4], al[kRows / 4];
+  float v, bt, dout;
 };
 
-__device__ __forceinline__ void load_token(const ChainCtx &c, int64_t tok, TokenIn &in) {
-  const BwdArgs &a = *c.a;
-  const int64_t base = (tok * a.num_heads + c.h) * kD + c.rg * kRows;
+__device__ __forceinline__ void token_from(const ChainCtx &c, const Piece &pc, int t, TokenIn &in) {
 #pragma unroll
   for (int i = 0; i < kRows / 4; ++i) {
-    in.q[i] = *reinterpret_cast<const f4 *>(a.qh + base + 4 * i);
-    in.k[i] = *reinterpret_cast<const f4 *>(a.kh + base + 4 * i);
-    in.g[i] = *reinterpret_cast<const f4 *>(a.gl + base + 4 * i);
+    in.q[i] = *reinterpret_cast<const f4 *>(&pc.q[t][c.rg * kRows + 4 * i]);
+    in.k[i] = *reinterpret_cast<const f4 *>(&pc.k[t][c.rg * kRows + 4 * i]);
+    in.al[i] = *reinterpret_cast<const f4 *>(&pc.al[t][c.rg * kRows + 4 * i]);
   }
-  in.v = load_elem(a.v, tok * a.qkv_stride + static_cast<int64_t>(c.h) * kD + c.col, a.qkv_dtype);
-  in.bt = a.bt[tok * a.num_heads + c.h];
+  in.v = pc.v[t][c.j];
+  in.dout = pc.dout[t][c.j];
+  in.bt = pc.bt[t];
 }
 
 __device__ __forceinline__ float tq(const TokenIn &in, int i) { return in.q[i >> 2][i & 3]; }
 __device__ __forceinline__ float tk(const TokenIn &in, int i) { return in.k[i >> 2][i & 3]; }
-__device__ __forceinline__ float talpha(const TokenIn &in, int i) { return expf(in.g[i >> 2][i & 3]); }
+__device__ __forceinline__ float talpha(const TokenIn &in, int i) { return in.al[i >> 2][i & 3]; }
 
 // S <- S_t from S_{t-1}; returns p = k^T S~ of the thread's column.
 __device__ __forceinline__ float fwd_step(const ChainCtx &c, const TokenIn &in, float (&S)[kRows], int &kb) {
@@ -182,19 +195,6 @@ __device__ __forceinline__ float fwd_step(const ChainCtx &c, const TokenIn &in, 
 #pragma unroll
   for (int i = 0; i < kRows; ++i) S[i] = fmaf(tk(in, i), u, S[i]);
   return p;
-}
-
-// Runs tokens [t0, t0 + n) forward from S, with the next token's inputs
-// loaded while the current one is processed.
-__device__ __forceinline__ void fwd_run(const ChainCtx &c, int64_t t0, int n, float (&S)[kRows], int &kb) {
-  if (n <= 0) return;
-  TokenIn cur, nxt;
-  load_token(c, t0, cur);
-  for (int t = 0; t < n; ++t) {
-    if (t + 1 < n) load_token(c, t0 + t + 1, nxt);
-    fwd_step(c, cur, S, kb);
-    cur = nxt;
-  }
 }
 
 // One butterfly stage over lanes l ^ m: of x[0 .. 2N) keep the half selected
@@ -221,10 +221,87 @@ __device__ __forceinline__ float col_sum32(const float (&x)[32], int l) {
   return y1[0];
 }
 
+// Where the chain kernel is in its walk over the sequence: phase 0 runs the
+// chunks forward (piece p of chunk ch), phase 1 recomputes pieces 0 ..
+// np - 2 of chunk ch to their sub-checkpoints, phase 2 takes the pieces of
+// chunk ch in reverse (recompute, then the reverse steps).
+struct Visit {
+  int phase, ch, p;
+};
+
+__device__ __forceinline__ int pieces_of(int len, int ch) {
+  return (min(kC, len - ch * kC) + kSub - 1) / kSub;
+}
+
+// Phase 1 of chunk ch if it has pieces to recompute, else straight to phase 2.
+__device__ __forceinline__ Visit reverse_entry(int len, int ch) {
+  const int np = pieces_of(len, ch);
+  return np >= 2 ? Visit{1, ch, 0} : Visit{2, ch, np - 1};
+}
+
+// The visit after v; phase 3 = done.
+__device__ __forceinline__ Visit next_visit(const Visit &v, int len, int nch) {
+  const int np = pieces_of(len, v.ch);
+  if (v.phase == 0) {
+    if (v.p + 1 < np) return Visit{0, v.ch, v.p + 1};
+    if (v.ch + 1 < nch) return Visit{0, v.ch + 1, 0};
+    return reverse_entry(len, nch - 1);
+  }
+  if (v.phase == 1) return v.p + 1 <= np - 2 ? Visit{1, v.ch, v.p + 1} : Visit{2, v.ch, np - 1};
+  if (v.p > 0) return Visit{2, v.ch, v.p - 1};
+  if (v.ch > 0) return reverse_entry(len, v.ch - 1);
+  return Visit{3, 0, 0};
+}
+
+// The loads of one piece (tokens [tok0, tok0 + m)) into the LDS piece at
+// `dst` (byte address of its q field): the rows of q^, k^ and alpha go
+// straight to LDS, 1 KiB (two token rows) per wavefront instruction, lane l
+// writing bytes 16 l .. 16 l + 15 of its block; v, do and beta come into
+// registers and are stored by piece_store.  Rows past m re-read row m - 1.
+struct PieceRegs {
+  float s[2];
+};
+
+__device__ __forceinline__ void piece_load(const BwdArgs &a, int h, int col0, int64_t tok0, int m, uint8_t *dst,
+                                           PieceRegs &r) {
+  const int t = threadIdx.x;
+  const int w = t >> 6, l = t & 63;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int blk = w + 8 * u;             // 12 blocks: 3 arrays x 4 token pairs
+    if (blk < 3 * kSub / 2) {
+      const int arr = blk / (kSub / 2), pair = blk % (kSub / 2);
+      const int tok = min(2 * pair + (l >> 5), m - 1);
+      const float *src = (arr == 0 ? a.qh : (arr == 1 ? a.kh : a.gl)) +
+                         ((tok0 + tok) * a.num_heads + h) * kD + 4 * (l & 31);
+      __builtin_amdgcn_global_load_lds(src, dst + arr * (kSub * kD * 4) + pair * 1024, 16, 0, 0);
+    }
+  }
+  const int which = t >> 8, rem = t & 255, tok = rem >> 5, cj = rem & 31;
+  float val = 0.f;
+  if (tok < m) {
+    if (which == 0)
+      val = load_elem(a.v, (tok0 + tok) * a.qkv_stride + static_cast<int64_t>(h) * kD + col0 + cj, a.qkv_dtype);
+    else
+      val = load_elem(a.dout, (tok0 + tok) * a.do_stride + static_cast<int64_t>(h) * kD + col0 + cj, a.do_dtype);
+  }
+  r.s[0] = val;
+  r.s[1] = (t < kSub && t < m) ? a.bt[(tok0 + t) * a.num_heads + h] : 0.f;
+}
+
+__device__ __forceinline__ void piece_store(Piece &pc, const PieceRegs &r) {
+  const int t = threadIdx.x;
+  const int which = t >> 8, rem = t & 255, tok = rem >> 5, cj = rem & 31;
+  (which == 0 ? pc.v : pc.dout)[tok][cj] = r.s[0];
+  if (t < kSub) pc.bt[t] = r.s[1];
+}
+
 __global__ __launch_bounds__(kChainThreads) void kda_bwd_chain_kernel(BwdArgs a) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
   float *s_sub = smem;                                     // [kC / kSub][128][32]
   float *s_kred = s_sub + (kC / kSub) * kD * kNV;           // [2][8][32]
+  Piece *s_pc = reinterpret_cast<Piece *>(s_kred + 2 * 8 * kNV);   // [2]
+  uint8_t *s_pc_bytes = reinterpret_cast<uint8_t *>(smem) + kChainLdsFloats * sizeof(float);
 
   const int s = blockIdx.x / (a.num_heads * kSlices);
   const int rem = blockIdx.x % (a.num_heads * kSlices);
@@ -242,6 +319,7 @@ __global__ __launch_bounds__(kChainThreads) void kda_bwd_chain_kernel(BwdArgs a)
   c.s_kred = s_kred;
   const int l32 = threadIdx.x & 31;
   const int r0 = c.rg * kRows;
+  const int col0 = slice * kNV;
   const int64_t seq_a = iclamp64(a.cu[s], 0, a.total);
   const int64_t seq_b = iclamp64(a.cu[s + 1], seq_a, a.total);
   const int len = static_cast<int>(seq_b - seq_a);
@@ -253,108 +331,140 @@ __global__ __launch_bounds__(kChainThreads) void kda_bwd_chain_kernel(BwdArgs a)
   const int64_t state_off = (static_cast<int64_t>(s) * a.num_heads + h) * kD * kD;
   int kb = 0;
 
-  // ---- pass 1: forward, the state at every chunk start -> workspace
-  float S[kRows];
+  float S[kRows], dS[kRows];
 #pragma unroll
-  for (int i = 0; i < kRows; ++i) S[i] = a.h0 ? a.h0[state_off + static_cast<int64_t>(r0 + i) * kD + c.col] : 0.f;
-  for (int ch = 0; ch < nch; ++ch) {
-    float *ck = a.ckpt + ((ck0 + ch) * a.num_heads + h) * kD * kD;
-#pragma unroll
-    for (int i = 0; i < kRows; ++i) ck[static_cast<int64_t>(r0 + i) * kD + c.col] = S[i];
-    fwd_run(c, seq_a + static_cast<int64_t>(ch) * kC, min(kC, len - ch * kC), S, kb);
+  for (int i = 0; i < kRows; ++i) {
+    S[i] = a.h0 ? a.h0[state_off + static_cast<int64_t>(r0 + i) * kD + c.col] : 0.f;
+    dS[i] = a.dht ? a.dht[state_off + static_cast<int64_t>(r0 + i) * kD + c.col] : 0.f;
   }
-  // Each checkpoint is read back below by the thread that wrote it.
+  const auto ckpt = [&](int ch) { return a.ckpt + ((ck0 + ch) * a.num_heads + h) * kD * kD; };
+  const auto tok_of = [&](const Visit &v) { return seq_a + static_cast<int64_t>(v.ch) * kC + v.p * kSub; };
+  const auto count_of = [&](const Visit &v) { return min(kSub, min(kC, len - v.ch * kC) - v.p * kSub); };
 
-  // ---- pass 2: reverse, chunk by chunk
-  float dS[kRows];
-#pragma unroll
-  for (int i = 0; i < kRows; ++i) dS[i] = a.dht ? a.dht[state_off + static_cast<int64_t>(r0 + i) * kD + c.col] : 0.f;
-  for (int ch = nch - 1; ch >= 0; --ch) {
-    const int64_t t0 = seq_a + static_cast<int64_t>(ch) * kC;
-    const int n = min(kC, len - ch * kC);
-    const float *ck = a.ckpt + ((ck0 + ch) * a.num_heads + h) * kD * kD;
-#pragma unroll
-    for (int i = 0; i < kRows; ++i) S[i] = ck[static_cast<int64_t>(r0 + i) * kD + c.col];
-    // sub-checkpoints: the state before tokens 0, 8, 16, ... of the chunk
-    // (each thread reads back only its own entries)
-    const int nsub = (n + kSub - 1) / kSub;
-    for (int sb = 0; sb < nsub; ++sb) {
-#pragma unroll
-      for (int i = 0; i < kRows; ++i) s_sub[(sb * kD + r0 + i) * kNV + c.j] = S[i];
-      if (sb + 1 < nsub) fwd_run(c, t0 + sb * kSub, kSub, S, kb);
+  if (nch > 0) {
+    Visit v{0, 0, 0};
+    int cb = 0;
+    {
+      PieceRegs r;
+      piece_load(a, h, col0, tok_of(v), count_of(v), s_pc_bytes, r);
+      piece_store(s_pc[0], r);
     }
-    for (int sb = nsub - 1; sb >= 0; --sb) {
-      const int64_t p0 = t0 + sb * kSub;
-      const int m = min(kSub, n - sb * kSub);
-      // Sp[t]: the state before token t of the piece (Sp[t + 1] after it);
-      // P[t]: that token's p
-      float Sp[kSub + 1][kRows], P[kSub];
+    __syncthreads();
+    while (true) {
+      const Visit nv = next_visit(v, len, nch);
+      const bool more = nv.phase < 3;
+      PieceRegs r;
+      if (more) piece_load(a, h, col0, tok_of(nv), count_of(nv), s_pc_bytes + (cb ^ 1) * sizeof(Piece), r);
+      const Piece &pc = s_pc[cb];
+      const int m = count_of(v);
+      const int np = pieces_of(len, v.ch);
+      if (v.phase == 0) {
+        // Each checkpoint is read back later by the thread that wrote it.
+        if (v.p == 0) {
 #pragma unroll
-      for (int i = 0; i < kRows; ++i) Sp[0][i] = s_sub[(sb * kD + r0 + i) * kNV + c.j];
-      {
-        TokenIn cur, nxt;
-        load_token(c, p0, cur);
+          for (int i = 0; i < kRows; ++i) ckpt(v.ch)[static_cast<int64_t>(r0 + i) * kD + c.col] = S[i];
+        }
+#pragma unroll 1
+        for (int t = 0; t < m; ++t) {
+          TokenIn in;
+          token_from(c, pc, t, in);
+          fwd_step(c, in, S, kb);
+        }
+      } else if (v.phase == 1) {
+        // sub-checkpoints: the state before pieces 0, 1, ... of the chunk
+        // (each thread reads back only its own entries)
+        if (v.p == 0) {
+#pragma unroll
+          for (int i = 0; i < kRows; ++i) S[i] = ckpt(v.ch)[static_cast<int64_t>(r0 + i) * kD + c.col];
+        }
+#pragma unroll
+        for (int i = 0; i < kRows; ++i) s_sub[(v.p * kD + r0 + i) * kNV + c.j] = S[i];
+#pragma unroll 1
+        for (int t = 0; t < m; ++t) {
+          TokenIn in;
+          token_from(c, pc, t, in);
+          fwd_step(c, in, S, kb);
+        }
+        if (v.p + 1 == np - 1) {
+#pragma unroll
+          for (int i = 0; i < kRows; ++i) s_sub[((v.p + 1) * kD + r0 + i) * kNV + c.j] = S[i];
+        }
+      } else {
+        if (np == 1) {
+#pragma unroll
+          for (int i = 0; i < kRows; ++i)
+            s_sub[(r0 + i) * kNV + c.j] = ckpt(v.ch)[static_cast<int64_t>(r0 + i) * kD + c.col];
+        }
+        const int64_t p0 = tok_of(v);
+        // Sp[t]: the state before token t of the piece; P[t]: that token's p.
+        // (S, dead in this phase, carries the recompute.)
+        float Sp[kSub][kRows], P[kSub];
+#pragma unroll
+        for (int i = 0; i < kRows; ++i) S[i] = s_sub[(v.p * kD + r0 + i) * kNV + c.j];
 #pragma unroll
         for (int t = 0; t < kSub; ++t) {
           if (t < m) {
-            if (t + 1 < m) load_token(c, p0 + t + 1, nxt);
+            TokenIn in;
+            token_from(c, pc, t, in);
 #pragma unroll
-            for (int i = 0; i < kRows; ++i) Sp[t + 1][i] = Sp[t][i];
-            P[t] = fwd_step(c, cur, Sp[t + 1], kb);
-            cur = nxt;
+            for (int i = 0; i < kRows; ++i) Sp[t][i] = S[i];
+            P[t] = fwd_step(c, in, S, kb);
           }
+          // one token's LDS reads at a time: hoisting all of them would
+          // need more registers than the wavefront has
+          __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int tt = kSub - 1; tt >= 0; --tt) {
+          if (tt < m) {
+            const int64_t tok = p0 + tt;
+            TokenIn cur;
+            token_from(c, pc, tt, cur);
+            const float dov = cur.dout;
+            const float vp = cur.v - P[tt];
+            const float u = cur.bt * vp;
+            float x[32];
+            float part = 0.f;
+#pragma unroll
+            for (int i = 0; i < kRows; ++i) {
+              dS[i] = fmaf(tq(cur, i), dov, dS[i]);      // dS_t += q^ do^T
+              const float st_i = fmaf(tk(cur, i), u, talpha(cur, i) * Sp[tt][i]);   // S_t
+              x[i] = st_i * dov;                         // dq^ partial: S_t do
+              part = fmaf(tk(cur, i), dS[i], part);
+            }
+            const float du = row_sum(c, part, kb);       // dS_t^T k^
+            const float dp = -cur.bt * du;
+#pragma unroll
+            for (int i = 0; i < kRows; ++i) {
+              const float al = talpha(cur, i);
+              const float st = al * Sp[tt][i];                  // S~
+              x[kRows + i] = fmaf(dS[i], u, st * dp);           // dk^ partial
+              const float dst = fmaf(tk(cur, i), dp, dS[i]);    // dS~
+              x[2 * kRows + i] = dst * Sp[tt][i];               // dalpha partial
+              dS[i] = al * dst;                                 // dS_{t-1}
+            }
+#pragma unroll
+            for (int i = 3 * kRows; i < 32; ++i) x[i] = 0.f;
+            const float rsum = col_sum32(x, l32);
+            if (l32 < 3 * kRows) {
+              const int vec = l32 / kRows, row = r0 + (l32 % kRows);
+              float *dst = vec == 0 ? a.dqh : (vec == 1 ? a.dkh : a.dal);
+              dst[((static_cast<int64_t>(slice) * a.total + tok) * a.num_heads + h) * kD + row] = rsum;
+            }
+            if (c.rg == 0) {
+              const int64_t o = (tok * a.num_heads + h) * kD + c.col;
+              a.dv[o] = cur.bt * du;
+              a.dbc[o] = du * vp;
+            }
+          }
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
-      TokenIn cur, nxt;
-      load_token(c, p0 + m - 1, cur);
-      float dov = load_elem(a.dout, (p0 + m - 1) * a.do_stride + static_cast<int64_t>(h) * kD + c.col, a.do_dtype);
-#pragma unroll
-      for (int tt = kSub - 1; tt >= 0; --tt) {
-        if (tt < m) {
-          const int64_t tok = p0 + tt;
-          float dov_n = 0.f;
-          if (tt > 0) {
-            load_token(c, tok - 1, nxt);
-            dov_n = load_elem(a.dout, (tok - 1) * a.do_stride + static_cast<int64_t>(h) * kD + c.col, a.do_dtype);
-          }
-          const float vp = cur.v - P[tt];
-          const float u = cur.bt * vp;
-          float x[32];
-          float part = 0.f;
-#pragma unroll
-          for (int i = 0; i < kRows; ++i) {
-            dS[i] = fmaf(tq(cur, i), dov, dS[i]);      // dS_t += q^ do^T
-            x[i] = Sp[tt + 1][i] * dov;                // dq^ partial: S_t do
-            part = fmaf(tk(cur, i), dS[i], part);
-          }
-          const float du = row_sum(c, part, kb);       // dS_t^T k^
-          const float dp = -cur.bt * du;
-#pragma unroll
-          for (int i = 0; i < kRows; ++i) {
-            const float al = talpha(cur, i);
-            const float st = al * Sp[tt][i];                  // S~
-            x[kRows + i] = fmaf(dS[i], u, st * dp);           // dk^ partial
-            const float dst = fmaf(tk(cur, i), dp, dS[i]);    // dS~
-            x[2 * kRows + i] = dst * Sp[tt][i];               // dalpha partial
-            dS[i] = al * dst;                                 // dS_{t-1}
-          }
-#pragma unroll
-          for (int i = 3 * kRows; i < 32; ++i) x[i] = 0.f;
-          const float r = col_sum32(x, l32);
-          if (l32 < 3 * kRows) {
-            const int vec = l32 / kRows, row = r0 + (l32 % kRows);
-            float *dst = vec == 0 ? a.dqh : (vec == 1 ? a.dkh : a.dal);
-            dst[((static_cast<int64_t>(slice) * a.total + tok) * a.num_heads + h) * kD + row] = r;
-          }
-          if (c.rg == 0) {
-            const int64_t o = (tok * a.num_heads + h) * kD + c.col;
-            a.dv[o] = cur.bt * du;
-            a.dbc[o] = du * vp;
-          }
-          cur = nxt;
-          dov = dov_n;
-        }
-      }
+      if (!more) break;
+      piece_store(s_pc[cb ^ 1], r);
+      __syncthreads();  // the next piece is in LDS; this one is no longer read
+      cb ^= 1;
+      v = nv;
     }
   }
   if (a.dh0) {
@@ -407,7 +517,7 @@ __global__ __launch_bounds__(kD) void kda_bwd_post_kernel(BwdArgs a) {
   a.dq[o] = dq;
   a.dk[o] = dk;
   // alpha = e^g: dg = dalpha alpha; through the gate, dz = dg lb s (1 - s) e^A_log
-  float dgv = dal * expf(a.gl[o]);
+  float dgv = dal * a.gl[o];
   if (a.flags & SOPHIA_KDA_GATE_IN_KERNEL) {
     const float z = load_elem(a.g, tok * a.g_stride + static_cast<int64_t>(h) * kD + c, a.g_dtype);
     const float ea = expf(a.A_log[h]);
