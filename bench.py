@@ -276,9 +276,15 @@ def long_prefill_bench(torch, dev, stream, steps: int, warmup: int, traffic: dic
 # Backward bytes per (token, head): q, k, v, do in bf16 and g, beta in fp32 read;
 # dq, dk, dv, dg and dbeta written in fp32.
 BWD_BYTES_PER_TOKEN = HEADS * (4 * DIM * 2 + DIM * 4 + 4 + 4 * DIM * 4 + 4)
+# Backward flops per token in the recurrent form: one forward step (decay d^2,
+# k^T S~ 2d^2, rank-1 update 2d^2) and the reverse step (q do^T 2d^2, S_t do
+# 2d^2, dS^T k 2d^2, dS u + S~ dp 4d^2, dS~ 2d^2, dalpha 2d^2, Diag(alpha) dS~
+# d^2): 20 d^2 per head.
+BWD_FLOPS_PER_TOKEN = HEADS * 20 * DIM * DIM
+FP32_PEAK_TFLOPS = 157.3
 
 
-def backward_bench(torch, dev, stream, inp, steps: int, warmup: int) -> dict:
+def backward_bench(torch, dev, stream, inp, steps: int, warmup: int, with_cpu: bool = False) -> dict:
     """The KDA backward (sophia_kda_chunk_bwd) over the headline prefill
     batch: gradients of q, k, v, g, beta and the initial states for a bf16
     output gradient, with the same flags as the timed prefill."""
@@ -295,11 +301,37 @@ def backward_bench(torch, dev, stream, inp, steps: int, warmup: int) -> dict:
     _, per = time_events(torch, call, steps, warmup, stream)
     ms = float(np.mean(per))
     gbs = total * BWD_BYTES_PER_TOKEN / (ms / 1e3) / 1e9
-    return {"workload": "KDA backward over the prefill batch (same lengths, flags and inputs), "
-                        "bf16 d_out, fp32 gradients",
-            "tokens_per_s": round(total / (ms / 1e3), 1), "ms_per_call": round(ms, 3),
-            "algorithmic_bytes_per_call": total * BWD_BYTES_PER_TOKEN,
-            "GBps": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+    tflops = total * BWD_FLOPS_PER_TOKEN / (ms / 1e3) / 1e12
+    out = {"workload": "KDA backward over the prefill batch (same lengths, flags and inputs), "
+                       "bf16 d_out, fp32 gradients",
+           "tokens_per_s": round(total / (ms / 1e3), 1), "ms_per_call": round(ms, 3),
+           "roofline": {"bound": "fp32 VALU (sequential chain)", "achieved": round(tflops, 2),
+                        "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                        "frac": round(tflops / FP32_PEAK_TFLOPS, 4),
+                        "flops_per_token": BWD_FLOPS_PER_TOKEN},
+           "algorithmic_bytes_per_call": total * BWD_BYTES_PER_TOKEN,
+           "GBps": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+    if with_cpu:
+        out["cpu_baseline"] = backward_cpu_baseline(torch, inp, d_out)
+    return out
+
+
+def backward_cpu_baseline(torch, inp, d_out, budget_s: float = 6.0) -> dict:
+    """The oracle's C restatement of the backward (oracle/kda_ref.c: the
+    chain rule through the reference's per-token recurrence, fp32, OpenMP
+    over sequence x head) over the same batch on this host's cores."""
+    from oracle import c_oracle
+    cores = len(os.sched_getaffinity(0))
+    args = [inp[n].float().cpu().numpy() for n in ("q", "k", "v", "g", "beta")]
+    cu = inp["cu_cpu"].numpy()
+    do = d_out.float().cpu().numpy()
+    total = int(cu[-1])
+    reps, el = _timed(lambda: c_oracle.kda_varlen_bwd(*args, cu, do, use_qk_l2norm=True, use_gate=False,
+                                                      use_beta_sigmoid=False, nthreads=cores), budget_s)
+    return {"value": round(total * reps / el, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"whole workload ({total} tokens x 16 heads) run {reps} times by the C backward "
+                      f"of the per-token recurrence (OpenMP over sequence x head, {cores} threads)",
+            **_threads(torch)}
 
 
 def copy_bandwidth(torch, dev, stream, nbytes: int = 1 << 30) -> float:
@@ -584,7 +616,7 @@ def main(argv=None) -> int:
                                                     max(args.warmup // 2, 2), traffic)
     if args.only in ("all", "bwd"):
         result["backward"] = backward_bench(torch, dev, stream, inp, max(args.steps // 4, 3),
-                                            max(args.warmup // 2, 1))
+                                            max(args.warmup // 2, 1), with_cpu=not args.no_cpu)
     if args.only in ("all", "mixed"):
         result["mixed_step"] = mixed_step_bench(torch, dev, stream, max(args.steps // 2, 5),
                                                 max(args.warmup // 2, 2),

@@ -113,6 +113,190 @@ int oracle_kda_varlen_f32(const float *q, const float *k, const float *v, const 
   return bad ? -2 : 0;
 }
 
+/*
+ * Gradients of oracle_kda_varlen_f32 (the chain rule through the per-token
+ * recurrence; what FlashKDAFunction.backward returns,
+ * ml/training/pretrain/engine/sm120_concurrent_ffn.py:301-373).  Per
+ * (sequence, head): the state at every 64-token chunk start is kept, and each
+ * chunk is recomputed with all its states before its reverse steps.
+ *   d_out: [T, H, V]; d_ht: [N, H, K, V] or NULL.
+ *   dq, dk, dg: [T, H, K]; dv: [T, H, V]; dbeta: [T, H]; dh0: [N, H, K, V];
+ *   dA_part: [N, H] and dbias_part: [N, H, K] (per-sequence sums, with the gate).
+ */
+int oracle_kda_varlen_bwd_f32(const float *q, const float *k, const float *v, const float *g,
+                              const float *beta, const float *A_log, const float *dt_bias,
+                              float lower_bound, float scale, int flags, const int32_t *cu_seqlens,
+                              int n_seqs, int H, int K, int V, const float *h0, const float *d_out,
+                              const float *d_ht, float *dq, float *dk, float *dv, float *dg,
+                              float *dbeta, float *dh0, float *dA_part, float *dbias_part,
+                              int nthreads) {
+  if (K <= 0 || V <= 0 || H <= 0 || n_seqs < 0) return -1;
+#ifdef _OPENMP
+  if (nthreads > 0) omp_set_num_threads(nthreads);
+#else
+  (void)nthreads;
+#endif
+  const int C = 64;
+  const size_t KV = (size_t)K * V;
+  const long pairs = (long)n_seqs * H;
+  int bad = 0;
+#pragma omp parallel for schedule(dynamic, 1)
+  for (long pr = 0; pr < pairs; ++pr) {
+    const int s = (int)(pr / H), h = (int)(pr % H);
+    const int t0 = cu_seqlens[s], T = cu_seqlens[s + 1] - cu_seqlens[s];
+    const int nch = (T + C - 1) / C;
+    float *ck = (float *)malloc(sizeof(float) * KV * (size_t)(nch > 0 ? nch : 1));
+    float *st = (float *)malloc(sizeof(float) * KV * (size_t)(C + 1));
+    float *dS = (float *)malloc(sizeof(float) * KV);
+    float *qn = (float *)malloc(sizeof(float) * (size_t)K * (T > 0 ? T : 1));
+    float *kn = (float *)malloc(sizeof(float) * (size_t)K * (T > 0 ? T : 1));
+    float *al = (float *)malloc(sizeof(float) * (size_t)K * (T > 0 ? T : 1));
+    float *bt = (float *)malloc(sizeof(float) * (size_t)(T > 0 ? T : 1));
+    float *p = (float *)malloc(sizeof(float) * (size_t)V);
+    float *u = (float *)malloc(sizeof(float) * (size_t)V);
+    float *du = (float *)malloc(sizeof(float) * (size_t)V);
+    float *dqh = (float *)malloc(sizeof(float) * (size_t)K);
+    float *dkh = (float *)malloc(sizeof(float) * (size_t)K);
+    float *dal = (float *)malloc(sizeof(float) * (size_t)K);
+    if (!ck || !st || !dS || !qn || !kn || !al || !bt || !p || !u || !du || !dqh || !dkh || !dal) {
+#pragma omp atomic write
+      bad = 1;
+      free(ck); free(st); free(dS); free(qn); free(kn); free(al); free(bt); free(p); free(u); free(du);
+      free(dqh); free(dkh); free(dal);
+      continue;
+    }
+    const float head_scale = A_log ? expf(A_log[h]) : 1.0f;
+    /* prepared inputs */
+    for (int t = 0; t < T; ++t) {
+      const size_t r = ((size_t)(t0 + t) * H + h) * K;
+      float qs = scale, ks = 1.0f;
+      if (flags & ORACLE_QK_L2NORM) {
+        float sq = 0.f, sk = 0.f;
+        for (int i = 0; i < K; ++i) { sq += q[r + i] * q[r + i]; sk += k[r + i] * k[r + i]; }
+        qs = scale / fmaxf(sqrtf(sq), 1e-12f);
+        ks = 1.0f / fmaxf(sqrtf(sk), 1e-12f);
+      }
+      for (int i = 0; i < K; ++i) {
+        qn[(size_t)t * K + i] = q[r + i] * qs;
+        kn[(size_t)t * K + i] = k[r + i] * ks;
+        float gl = g[r + i];
+        if (flags & ORACLE_GATE) gl = lower_bound * sigmoidf_ref(head_scale * (gl + dt_bias[h * K + i]));
+        al[(size_t)t * K + i] = expf(gl);
+      }
+      float b = beta[(size_t)(t0 + t) * H + h];
+      if (flags & ORACLE_BETA_SIGMOID) b = sigmoidf_ref(b);
+      bt[t] = b;
+    }
+    /* one forward step: S (K x V) from its predecessor, p and u of the token */
+#define FWD_STEP(Sin, Sout, t)                                                        \
+    do {                                                                              \
+      for (int j = 0; j < V; ++j) p[j] = 0.f;                                         \
+      for (int i = 0; i < K; ++i) {                                                   \
+        const float a_ = al[(size_t)(t) * K + i], k_ = kn[(size_t)(t) * K + i];       \
+        for (int j = 0; j < V; ++j) {                                                 \
+          const float x_ = (Sin)[(size_t)i * V + j] * a_;                             \
+          (Sout)[(size_t)i * V + j] = x_;                                             \
+          p[j] += k_ * x_;                                                            \
+        }                                                                             \
+      }                                                                               \
+      const float *vt_ = v + ((size_t)(t0 + (t)) * H + h) * V;                        \
+      for (int j = 0; j < V; ++j) u[j] = bt[t] * (vt_[j] - p[j]);                     \
+      for (int i = 0; i < K; ++i) {                                                   \
+        const float k_ = kn[(size_t)(t) * K + i];                                     \
+        for (int j = 0; j < V; ++j) (Sout)[(size_t)i * V + j] += k_ * u[j];           \
+      }                                                                               \
+    } while (0)
+    /* forward: chunk-start states */
+    const size_t soff = ((size_t)s * H + h) * KV;
+    if (h0) memcpy(st, h0 + soff, sizeof(float) * KV); else memset(st, 0, sizeof(float) * KV);
+    for (int c = 0; c < nch; ++c) {
+      memcpy(ck + (size_t)c * KV, st, sizeof(float) * KV);
+      const int n = T - c * C < C ? T - c * C : C;
+      for (int t = 0; t < n; ++t) FWD_STEP(st, st, c * C + t);
+    }
+    if (d_ht) memcpy(dS, d_ht + soff, sizeof(float) * KV); else memset(dS, 0, sizeof(float) * KV);
+    for (int c = nch - 1; c >= 0; --c) {
+      const int n = T - c * C < C ? T - c * C : C;
+      memcpy(st, ck + (size_t)c * KV, sizeof(float) * KV);
+      for (int t = 0; t < n; ++t) FWD_STEP(st + (size_t)t * KV, st + (size_t)(t + 1) * KV, c * C + t);
+      for (int tt = n - 1; tt >= 0; --tt) {
+        const int t = c * C + tt;
+        const float *Sprev = st + (size_t)tt * KV, *Scur = st + (size_t)(tt + 1) * KV;
+        const float *dot = d_out + ((size_t)(t0 + t) * H + h) * V;
+        const float *vt = v + ((size_t)(t0 + t) * H + h) * V;
+        const float b = bt[t];
+        /* p and u of this token again */
+        for (int j = 0; j < V; ++j) p[j] = 0.f;
+        for (int i = 0; i < K; ++i)
+          for (int j = 0; j < V; ++j) p[j] += kn[(size_t)t * K + i] * al[(size_t)t * K + i] * Sprev[(size_t)i * V + j];
+        for (int j = 0; j < V; ++j) { u[j] = b * (vt[j] - p[j]); du[j] = 0.f; }
+        for (int i = 0; i < K; ++i) {
+          const float qi = qn[(size_t)t * K + i], ki = kn[(size_t)t * K + i];
+          float acc = 0.f;
+          for (int j = 0; j < V; ++j) {
+            dS[(size_t)i * V + j] += qi * dot[j];
+            acc += Scur[(size_t)i * V + j] * dot[j];
+            du[j] += ki * dS[(size_t)i * V + j];
+          }
+          dqh[i] = acc;
+        }
+        float db = 0.f;
+        float *dvt = dv + ((size_t)(t0 + t) * H + h) * V;
+        for (int j = 0; j < V; ++j) {
+          dvt[j] = b * du[j];
+          db += du[j] * (vt[j] - p[j]);
+        }
+        for (int i = 0; i < K; ++i) {
+          const float ai = al[(size_t)t * K + i], ki = kn[(size_t)t * K + i];
+          float a1 = 0.f, a2 = 0.f;
+          for (int j = 0; j < V; ++j) {
+            const float dp = -b * du[j];
+            const float sprev = Sprev[(size_t)i * V + j];
+            const float dsij = dS[(size_t)i * V + j];
+            a1 += dsij * u[j] + ai * sprev * dp;
+            const float dst = dsij + ki * dp;
+            a2 += dst * sprev;
+            dS[(size_t)i * V + j] = ai * dst;
+          }
+          dkh[i] = a1;
+          dal[i] = a2;
+        }
+        /* input gradients of the token */
+        const size_t r = ((size_t)(t0 + t) * H + h) * K;
+        if (flags & ORACLE_QK_L2NORM) {
+          float sq = 0.f, sk = 0.f, yq = 0.f, yk = 0.f;
+          for (int i = 0; i < K; ++i) { sq += q[r + i] * q[r + i]; sk += k[r + i] * k[r + i]; }
+          const float nq = fmaxf(sqrtf(sq), 1e-12f), nk = fmaxf(sqrtf(sk), 1e-12f);
+          for (int i = 0; i < K; ++i) { yq += q[r + i] / nq * dqh[i] * scale; yk += k[r + i] / nk * dkh[i]; }
+          for (int i = 0; i < K; ++i) {
+            dq[r + i] = (dqh[i] * scale - (sqrtf(sq) >= 1e-12f ? q[r + i] / nq * yq : 0.f)) / nq;
+            dk[r + i] = (dkh[i] - (sqrtf(sk) >= 1e-12f ? k[r + i] / nk * yk : 0.f)) / nk;
+          }
+        } else {
+          for (int i = 0; i < K; ++i) { dq[r + i] = dqh[i] * scale; dk[r + i] = dkh[i]; }
+        }
+        for (int i = 0; i < K; ++i) {
+          float dgv = dal[i] * al[(size_t)t * K + i];
+          if (flags & ORACLE_GATE) {
+            const float zb = g[r + i] + dt_bias[h * K + i];
+            const float sg = sigmoidf_ref(head_scale * zb);
+            dgv *= lower_bound * sg * (1.f - sg) * head_scale;
+            if (dbias_part) dbias_part[((size_t)s * H + h) * K + i] += dgv;
+            if (dA_part) dA_part[(size_t)s * H + h] += dgv * zb;
+          }
+          dg[r + i] = dgv;
+        }
+        dbeta[(size_t)(t0 + t) * H + h] = (flags & ORACLE_BETA_SIGMOID) ? db * b * (1.f - b) : db;
+      }
+    }
+#undef FWD_STEP
+    if (dh0) memcpy(dh0 + soff, dS, sizeof(float) * KV);
+    free(ck); free(st); free(dS); free(qn); free(kn); free(al); free(bt); free(p); free(u); free(du);
+    free(dqh); free(dkh); free(dal);
+  }
+  return bad ? -2 : 0;
+}
+
 int oracle_max_threads(void) {
 #ifdef _OPENMP
   return omp_get_max_threads();

@@ -115,3 +115,32 @@ def test_dropped_final_state_term_is_caught():
     val[0] = keep
     fd0 = (up - down) / (2 * eps)
     assert abs(bad.reshape(-1)[0] - fd0) > 1e-3
+
+
+def test_c_backward_matches_numpy_backward():
+    """The C restatement of the backward (the CPU baseline of bench.py's
+    backward leg) equals the numpy float64 backward to fp32 rounding."""
+    from oracle import c_oracle
+    rng = np.random.default_rng(51)
+    cu = [0, 20, 20, 75, 100]
+    heads, kd, vd = 2, 16, 24
+    total = cu[-1]
+    for gated in (True, False):
+        q = rng.standard_normal((total, heads, kd))
+        k = rng.standard_normal((total, heads, kd))
+        v = rng.standard_normal((total, heads, vd))
+        g = rng.standard_normal((total, heads, kd)) if gated else -rng.uniform(0, 1, (total, heads, kd))
+        beta = rng.standard_normal((total, heads)) if gated else rng.uniform(0, 1, (total, heads))
+        a_log = rng.uniform(-1, 1, heads)
+        dt_bias = rng.standard_normal(heads * kd) * 0.5
+        h0 = rng.standard_normal((4, heads, kd, vd)) * 0.3
+        d_out = rng.standard_normal((total, heads, vd))
+        d_fin = rng.standard_normal((4, heads, kd, vd)) * 0.3
+        kw = dict(use_qk_l2norm=gated, use_gate=gated, use_beta_sigmoid=gated, A_log=a_log,
+                  dt_bias=dt_bias, initial_states=h0, d_final_states=d_fin)
+        want = ko.kda_varlen_bwd(q, k, v, g, beta, cu, d_out, **kw)
+        got = c_oracle.kda_varlen_bwd(q, k, v, g, beta, cu, d_out, **kw)
+        assert set(got) == set(want)
+        for name in want:
+            err = np.max(np.abs(got[name] - want[name])) / max(np.max(np.abs(want[name])), 1e-30)
+            assert err < 1e-4, f"gated={gated} {name}: {err:.2e}"
