@@ -22,15 +22,14 @@
 //  * kda_bwd_chain_kernel, one work-group of 512 threads per (sequence, head,
 //    32-column value slice): the value columns of the state evolve
 //    independently, so each slice runs the recurrence alone.  It first runs
-//    the sequence forward and keeps the state at every 64-token chunk start
-//    (in the workspace); then, chunk by chunk in reverse, it recomputes the
-//    chunk forward keeping the state every 8 tokens in LDS, and for each
-//    8-token piece in reverse recomputes its states in registers and runs the
-//    reverse steps.  Every 8-token piece it walks is staged in LDS by the
-//    whole work-group, the next piece's loads in flight while the current one
-//    is processed (one-token-ahead register loads left every step waiting on
-//    memory).  Sums over value columns (dq^, dk^, dalpha) leave as per-slice
-//    partials; dbeta leaves per value column.
+//    the sequence forward and keeps the state at every 8-token piece start in
+//    the workspace (64 KiB per piece and head); then it takes the pieces in
+//    reverse, recomputes each piece's 8 states in registers from its
+//    checkpoint and runs the reverse steps: two passes over the tokens plus
+//    the recompute.  Every piece it walks is staged in LDS by the whole
+//    work-group, the next piece's loads in flight while the current one is
+//    processed.  Sums over value columns (dq^, dk^, dalpha) leave as
+//    per-slice partials; dbeta leaves per value column.
 //  * kda_bwd_post_kernel, one work-group of 128 threads per (token, head):
 //    sums the partials and applies the backward of the l2 norms, of the gate
 //    g = lb sigmoid(e^A_log (z + dt_bias)) and of the beta sigmoid.
@@ -50,15 +49,14 @@ namespace sophia {
 namespace {
 
 constexpr int kD = 128;
-constexpr int kC = 64;           // checkpoint interval (chunk)
-constexpr int kSub = 8;          // sub-checkpoint interval inside a chunk
+constexpr int kSub = 8;          // checkpoint interval: one piece of tokens
 constexpr int kNV = 32;          // value columns per work-group
 constexpr int kSlices = kD / kNV;
 constexpr int kChainThreads = 512;
 constexpr int kRows = kD / (kChainThreads / kNV);   // state rows per thread: 8
 constexpr int kGateParts = 64;   // token partitions of the dA_log / ddt_bias sums
 constexpr int kMaxDevices = 64;
-constexpr size_t kChainLdsFloats = static_cast<size_t>(kC / kSub) * kD * kNV + 2 * 8 * kNV;
+constexpr size_t kChainLdsFloats = 2 * 8 * kNV;
 
 struct BwdArgs {
   // inputs
@@ -87,7 +85,7 @@ struct BwdArgs {
   float *dq, *dk, *dv, *dg, *dbeta, *dh0, *dA_log, *ddt_bias;
   // workspace
   float *qh, *kh, *gl, *bt;        // prepared q^, k^, alpha = e^g, beta
-  float *ckpt;                     // [chunks, H, 128, 128] chunk-start states
+  float *ckpt;                     // [pieces, H, 128, 128] states at every 8-token piece start
   float *dqh, *dkh, *dal;          // [kSlices, total, H, 128] partial sums
   float *dbc;                      // [total, H, 128] dbeta per value column
   float *gpb, *gpa;                // [kGateParts, H, 128] partial ddt_bias / dA_log
@@ -221,38 +219,6 @@ __device__ __forceinline__ float col_sum32(const float (&x)[32], int l) {
   return y1[0];
 }
 
-// Where the chain kernel is in its walk over the sequence: phase 0 runs the
-// chunks forward (piece p of chunk ch), phase 1 recomputes pieces 0 ..
-// np - 2 of chunk ch to their sub-checkpoints, phase 2 takes the pieces of
-// chunk ch in reverse (recompute, then the reverse steps).
-struct Visit {
-  int phase, ch, p;
-};
-
-__device__ __forceinline__ int pieces_of(int len, int ch) {
-  return (min(kC, len - ch * kC) + kSub - 1) / kSub;
-}
-
-// Phase 1 of chunk ch if it has pieces to recompute, else straight to phase 2.
-__device__ __forceinline__ Visit reverse_entry(int len, int ch) {
-  const int np = pieces_of(len, ch);
-  return np >= 2 ? Visit{1, ch, 0} : Visit{2, ch, np - 1};
-}
-
-// The visit after v; phase 3 = done.
-__device__ __forceinline__ Visit next_visit(const Visit &v, int len, int nch) {
-  const int np = pieces_of(len, v.ch);
-  if (v.phase == 0) {
-    if (v.p + 1 < np) return Visit{0, v.ch, v.p + 1};
-    if (v.ch + 1 < nch) return Visit{0, v.ch + 1, 0};
-    return reverse_entry(len, nch - 1);
-  }
-  if (v.phase == 1) return v.p + 1 <= np - 2 ? Visit{1, v.ch, v.p + 1} : Visit{2, v.ch, np - 1};
-  if (v.p > 0) return Visit{2, v.ch, v.p - 1};
-  if (v.ch > 0) return reverse_entry(len, v.ch - 1);
-  return Visit{3, 0, 0};
-}
-
 // The loads of one piece (tokens [tok0, tok0 + m)) into the LDS piece at
 // `dst` (byte address of its q field): the rows of q^, k^ and alpha go
 // straight to LDS, 1 KiB (two token rows) per wavefront instruction, lane l
@@ -298,9 +264,8 @@ __device__ __forceinline__ void piece_store(Piece &pc, const PieceRegs &r) {
 
 __global__ __launch_bounds__(kChainThreads) void kda_bwd_chain_kernel(BwdArgs a) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
-  float *s_sub = smem;                                     // [kC / kSub][128][32]
-  float *s_kred = s_sub + (kC / kSub) * kD * kNV;           // [2][8][32]
-  Piece *s_pc = reinterpret_cast<Piece *>(s_kred + 2 * 8 * kNV);   // [2]
+  float *s_kred = smem;                                              // [2][8][32]
+  Piece *s_pc = reinterpret_cast<Piece *>(s_kred + 2 * 8 * kNV);     // [2]
   uint8_t *s_pc_bytes = reinterpret_cast<uint8_t *>(smem) + kChainLdsFloats * sizeof(float);
 
   const int s = blockIdx.x / (a.num_heads * kSlices);
@@ -323,11 +288,11 @@ __global__ __launch_bounds__(kChainThreads) void kda_bwd_chain_kernel(BwdArgs a)
   const int64_t seq_a = iclamp64(a.cu[s], 0, a.total);
   const int64_t seq_b = iclamp64(a.cu[s + 1], seq_a, a.total);
   const int len = static_cast<int>(seq_b - seq_a);
-  const int nch = (len + kC - 1) / kC;
-  // Checkpoint slots of this sequence: seq_a / 64 + s + chunk.  For ordered
+  const int np = (len + kSub - 1) / kSub;   // 8-token pieces
+  // Checkpoint slots of this sequence: seq_a / 8 + s + piece.  For ordered
   // offsets the sequences' slots do not overlap, and for any offsets they
-  // stay below total / 64 + n_seqs.
-  const int64_t ck0 = seq_a / kC + s;
+  // stay below total / 8 + n_seqs.
+  const int64_t ck0 = seq_a / kSub + s;
   const int64_t state_off = (static_cast<int64_t>(s) * a.num_heads + h) * kD * kD;
   int kb = 0;
 
@@ -337,70 +302,51 @@ __global__ __launch_bounds__(kChainThreads) void kda_bwd_chain_kernel(BwdArgs a)
     S[i] = a.h0 ? a.h0[state_off + static_cast<int64_t>(r0 + i) * kD + c.col] : 0.f;
     dS[i] = a.dht ? a.dht[state_off + static_cast<int64_t>(r0 + i) * kD + c.col] : 0.f;
   }
-  const auto ckpt = [&](int ch) { return a.ckpt + ((ck0 + ch) * a.num_heads + h) * kD * kD; };
-  const auto tok_of = [&](const Visit &v) { return seq_a + static_cast<int64_t>(v.ch) * kC + v.p * kSub; };
-  const auto count_of = [&](const Visit &v) { return min(kSub, min(kC, len - v.ch * kC) - v.p * kSub); };
+  // The state before piece p (rows r0.., column col of this thread): written
+  // by the forward walk, read back by the same thread in the reverse walk.
+  const auto ckpt = [&](int p, int i) -> float & {
+    return a.ckpt[((ck0 + p) * a.num_heads + h) * kD * kD + static_cast<int64_t>(r0 + i) * kD + c.col];
+  };
+  const auto count_of = [&](int p) { return min(kSub, len - p * kSub); };
 
-  if (nch > 0) {
-    Visit v{0, 0, 0};
+  if (np > 0) {
+    // Walk: pieces 0 .. np - 1 forward (v = p), then np - 1 .. 0 in reverse
+    // (v = 2 np - 1 - p); each piece's inputs staged in LDS one visit ahead.
+    const int nvis = 2 * np;
+    const auto piece_of = [&](int vis) { return vis < np ? vis : 2 * np - 1 - vis; };
     int cb = 0;
     {
       PieceRegs r;
-      piece_load(a, h, col0, tok_of(v), count_of(v), s_pc_bytes, r);
+      piece_load(a, h, col0, seq_a, count_of(0), s_pc_bytes, r);
       piece_store(s_pc[0], r);
     }
     __syncthreads();
-    while (true) {
-      const Visit nv = next_visit(v, len, nch);
-      const bool more = nv.phase < 3;
+    for (int vis = 0; vis < nvis; ++vis) {
+      const int p = piece_of(vis);
+      const bool more = vis + 1 < nvis;
       PieceRegs r;
-      if (more) piece_load(a, h, col0, tok_of(nv), count_of(nv), s_pc_bytes + (cb ^ 1) * sizeof(Piece), r);
+      if (more) {
+        const int pn = piece_of(vis + 1);
+        piece_load(a, h, col0, seq_a + static_cast<int64_t>(pn) * kSub, count_of(pn),
+                   s_pc_bytes + (cb ^ 1) * sizeof(Piece), r);
+      }
       const Piece &pc = s_pc[cb];
-      const int m = count_of(v);
-      const int np = pieces_of(len, v.ch);
-      if (v.phase == 0) {
-        // Each checkpoint is read back later by the thread that wrote it.
-        if (v.p == 0) {
+      const int m = count_of(p);
+      if (vis < np) {
 #pragma unroll
-          for (int i = 0; i < kRows; ++i) ckpt(v.ch)[static_cast<int64_t>(r0 + i) * kD + c.col] = S[i];
-        }
+        for (int i = 0; i < kRows; ++i) ckpt(p, i) = S[i];
 #pragma unroll 1
         for (int t = 0; t < m; ++t) {
           TokenIn in;
           token_from(c, pc, t, in);
           fwd_step(c, in, S, kb);
-        }
-      } else if (v.phase == 1) {
-        // sub-checkpoints: the state before pieces 0, 1, ... of the chunk
-        // (each thread reads back only its own entries)
-        if (v.p == 0) {
-#pragma unroll
-          for (int i = 0; i < kRows; ++i) S[i] = ckpt(v.ch)[static_cast<int64_t>(r0 + i) * kD + c.col];
-        }
-#pragma unroll
-        for (int i = 0; i < kRows; ++i) s_sub[(v.p * kD + r0 + i) * kNV + c.j] = S[i];
-#pragma unroll 1
-        for (int t = 0; t < m; ++t) {
-          TokenIn in;
-          token_from(c, pc, t, in);
-          fwd_step(c, in, S, kb);
-        }
-        if (v.p + 1 == np - 1) {
-#pragma unroll
-          for (int i = 0; i < kRows; ++i) s_sub[((v.p + 1) * kD + r0 + i) * kNV + c.j] = S[i];
         }
       } else {
-        if (np == 1) {
-#pragma unroll
-          for (int i = 0; i < kRows; ++i)
-            s_sub[(r0 + i) * kNV + c.j] = ckpt(v.ch)[static_cast<int64_t>(r0 + i) * kD + c.col];
-        }
-        const int64_t p0 = tok_of(v);
+        const int64_t p0 = seq_a + static_cast<int64_t>(p) * kSub;
         // Sp[t]: the state before token t of the piece; P[t]: that token's p.
-        // (S, dead in this phase, carries the recompute.)
         float Sp[kSub][kRows], P[kSub];
 #pragma unroll
-        for (int i = 0; i < kRows; ++i) S[i] = s_sub[(v.p * kD + r0 + i) * kNV + c.j];
+        for (int i = 0; i < kRows; ++i) S[i] = ckpt(p, i);
 #pragma unroll
         for (int t = 0; t < kSub; ++t) {
           if (t < m) {
@@ -464,7 +410,6 @@ __global__ __launch_bounds__(kChainThreads) void kda_bwd_chain_kernel(BwdArgs a)
       piece_store(s_pc[cb ^ 1], r);
       __syncthreads();  // the next piece is in LDS; this one is no longer read
       cb ^= 1;
-      v = nv;
     }
   }
   if (a.dh0) {
@@ -573,8 +518,8 @@ __global__ __launch_bounds__(kD) void kda_bwd_gate_final_kernel(BwdArgs a) {
 
 size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
-size_t max_chunks(int64_t total_tokens, int n_seqs) {
-  return static_cast<size_t>(total_tokens / kC) + static_cast<size_t>(n_seqs);
+size_t max_pieces(int64_t total_tokens, int n_seqs) {
+  return static_cast<size_t>(total_tokens / kSub) + static_cast<size_t>(n_seqs);
 }
 
 int ensure_chain_lds() {
@@ -603,7 +548,7 @@ extern "C" size_t sophia_kda_chunk_bwd_workspace_size(int64_t total_tokens, int 
   if (total_tokens < 0 || n_seqs <= 0 || num_heads <= 0 || head_dim != kD) return 0;
   const size_t tok = static_cast<size_t>(total_tokens) * num_heads;
   return 3 * align256(tok * kD * 4) + align256(tok * 4) +
-         align256(max_chunks(total_tokens, n_seqs) * num_heads * kD * kD * 4) +
+         align256(max_pieces(total_tokens, n_seqs) * num_heads * kD * kD * 4) +
          3 * align256(kSlices * tok * kD * 4) + align256(tok * kD * 4) +
          2 * align256(static_cast<size_t>(kGateParts) * num_heads * kD * 4);
 }
@@ -667,7 +612,7 @@ extern "C" int sophia_kda_chunk_bwd(const void *q, const void *k, const void *v,
   a.kh = carve(tok * kD * 4);
   a.gl = carve(tok * kD * 4);
   a.bt = carve(tok * 4);
-  a.ckpt = carve(max_chunks(total_tokens, n_seqs) * num_heads * kD * kD * 4);
+  a.ckpt = carve(max_pieces(total_tokens, n_seqs) * num_heads * kD * kD * 4);
   a.dqh = carve(kSlices * tok * kD * 4);
   a.dkh = carve(kSlices * tok * kD * 4);
   a.dal = carve(kSlices * tok * kD * 4);
