@@ -88,6 +88,7 @@ struct BwdArgs {
   float *ckpt;                     // [pieces, H, 128, 128] states at every 8-token piece start
   float *dqh, *dkh, *dal;          // [kSlices, total, H, 128] partial sums
   float *dbc;                      // [total, H, 128] dbeta per value column
+  float *pv;                       // [total, H, 128] p = k^T S~ of every token (forward walk)
   float *gpb, *gpa;                // [kGateParts, H, 128] partial ddt_bias / dA_log
 };
 
@@ -130,7 +131,7 @@ __global__ __launch_bounds__(kD) void kda_bwd_prep_kernel(BwdArgs a) {
 // (rows of q^, k^, alpha; the slice's 32 columns of v and of do; beta).
 struct Piece {
   float q[kSub][kD], k[kSub][kD], al[kSub][kD];
-  float v[kSub][kNV], dout[kSub][kNV];
+  float v[kSub][kNV], dout[kSub][kNV], p[kSub][kNV];
   float bt[kSub];
 };
 
@@ -228,8 +229,9 @@ struct PieceRegs {
   float s[2];
 };
 
+// with_p: also the slice's p values of the piece (written by the forward walk).
 __device__ __forceinline__ void piece_load(const BwdArgs &a, int h, int col0, int64_t tok0, int m, uint8_t *dst,
-                                           PieceRegs &r) {
+                                           bool with_p, PieceRegs &r) {
   const int t = threadIdx.x;
   const int w = t >> 6, l = t & 63;
 #pragma unroll
@@ -252,14 +254,24 @@ __device__ __forceinline__ void piece_load(const BwdArgs &a, int h, int col0, in
       val = load_elem(a.dout, (tok0 + tok) * a.do_stride + static_cast<int64_t>(h) * kD + col0 + cj, a.do_dtype);
   }
   r.s[0] = val;
-  r.s[1] = (t < kSub && t < m) ? a.bt[(tok0 + t) * a.num_heads + h] : 0.f;
+  // threads 0 .. 255: p (8 tokens x 32 columns); 256 .. 263: beta
+  float v1 = 0.f;
+  if (which == 0) {
+    if (with_p && tok < m) v1 = a.pv[((tok0 + tok) * a.num_heads + h) * kD + col0 + cj];
+  } else if (rem < kSub && rem < m) {
+    v1 = a.bt[(tok0 + rem) * a.num_heads + h];
+  }
+  r.s[1] = v1;
 }
 
 __device__ __forceinline__ void piece_store(Piece &pc, const PieceRegs &r) {
   const int t = threadIdx.x;
   const int which = t >> 8, rem = t & 255, tok = rem >> 5, cj = rem & 31;
   (which == 0 ? pc.v : pc.dout)[tok][cj] = r.s[0];
-  if (t < kSub) pc.bt[t] = r.s[1];
+  if (which == 0)
+    pc.p[tok][cj] = r.s[1];
+  else if (rem < kSub)
+    pc.bt[rem] = r.s[1];
 }
 
 __global__ __launch_bounds__(kChainThreads) void kda_bwd_chain_kernel(BwdArgs a) {
@@ -317,34 +329,44 @@ __global__ __launch_bounds__(kChainThreads) void kda_bwd_chain_kernel(BwdArgs a)
     int cb = 0;
     {
       PieceRegs r;
-      piece_load(a, h, col0, seq_a, count_of(0), s_pc_bytes, r);
+      piece_load(a, h, col0, seq_a, count_of(0), s_pc_bytes, false, r);
       piece_store(s_pc[0], r);
     }
     __syncthreads();
     for (int vis = 0; vis < nvis; ++vis) {
       const int p = piece_of(vis);
       const bool more = vis + 1 < nvis;
+      // The last forward visit is followed by the reverse visit of the same
+      // piece: that piece stays in its buffer, its p values written there.
+      const bool same_next = vis == np - 1;
       PieceRegs r;
-      if (more) {
+      if (more && !same_next) {
         const int pn = piece_of(vis + 1);
         piece_load(a, h, col0, seq_a + static_cast<int64_t>(pn) * kSub, count_of(pn),
-                   s_pc_bytes + (cb ^ 1) * sizeof(Piece), r);
+                   s_pc_bytes + (cb ^ 1) * sizeof(Piece), vis + 1 >= np, r);
       }
-      const Piece &pc = s_pc[cb];
+      Piece &pc = s_pc[cb];
       const int m = count_of(p);
       if (vis < np) {
 #pragma unroll
         for (int i = 0; i < kRows; ++i) ckpt(p, i) = S[i];
+        const int64_t p0 = seq_a + static_cast<int64_t>(p) * kSub;
 #pragma unroll 1
         for (int t = 0; t < m; ++t) {
           TokenIn in;
           token_from(c, pc, t, in);
-          fwd_step(c, in, S, kb);
+          const float pt = fwd_step(c, in, S, kb);
+          if (c.rg == 0) {
+            a.pv[((p0 + t) * a.num_heads + h) * kD + c.col] = pt;
+            pc.p[t][c.j] = pt;
+          }
         }
       } else {
         const int64_t p0 = seq_a + static_cast<int64_t>(p) * kSub;
-        // Sp[t]: the state before token t of the piece; P[t]: that token's p.
-        float Sp[kSub][kRows], P[kSub];
+        // Sp[t]: the state before token t of the piece, recomputed from the
+        // checkpoint with the p values of the forward walk (so without the
+        // cross-row sum: no barrier).
+        float Sp[kSub][kRows];
 #pragma unroll
         for (int i = 0; i < kRows; ++i) S[i] = ckpt(p, i);
 #pragma unroll
@@ -352,9 +374,12 @@ __global__ __launch_bounds__(kChainThreads) void kda_bwd_chain_kernel(BwdArgs a)
           if (t < m) {
             TokenIn in;
             token_from(c, pc, t, in);
+            const float u = in.bt * (in.v - pc.p[t][c.j]);
 #pragma unroll
-            for (int i = 0; i < kRows; ++i) Sp[t][i] = S[i];
-            P[t] = fwd_step(c, in, S, kb);
+            for (int i = 0; i < kRows; ++i) {
+              Sp[t][i] = S[i];
+              S[i] = fmaf(tk(in, i), u, S[i] * talpha(in, i));
+            }
           }
           // one token's LDS reads at a time: hoisting all of them would
           // need more registers than the wavefront has
@@ -367,7 +392,7 @@ __global__ __launch_bounds__(kChainThreads) void kda_bwd_chain_kernel(BwdArgs a)
             TokenIn cur;
             token_from(c, pc, tt, cur);
             const float dov = cur.dout;
-            const float vp = cur.v - P[tt];
+            const float vp = cur.v - pc.p[tt][c.j];
             const float u = cur.bt * vp;
             float x[32];
             float part = 0.f;
@@ -407,9 +432,13 @@ __global__ __launch_bounds__(kChainThreads) void kda_bwd_chain_kernel(BwdArgs a)
         }
       }
       if (!more) break;
-      piece_store(s_pc[cb ^ 1], r);
-      __syncthreads();  // the next piece is in LDS; this one is no longer read
-      cb ^= 1;
+      if (same_next) {
+        __syncthreads();  // this piece's p values are in LDS
+      } else {
+        piece_store(s_pc[cb ^ 1], r);
+        __syncthreads();  // the next piece is in LDS; this one is no longer read
+        cb ^= 1;
+      }
     }
   }
   if (a.dh0) {
@@ -549,7 +578,7 @@ extern "C" size_t sophia_kda_chunk_bwd_workspace_size(int64_t total_tokens, int 
   const size_t tok = static_cast<size_t>(total_tokens) * num_heads;
   return 3 * align256(tok * kD * 4) + align256(tok * 4) +
          align256(max_pieces(total_tokens, n_seqs) * num_heads * kD * kD * 4) +
-         3 * align256(kSlices * tok * kD * 4) + align256(tok * kD * 4) +
+         3 * align256(kSlices * tok * kD * 4) + 2 * align256(tok * kD * 4) +
          2 * align256(static_cast<size_t>(kGateParts) * num_heads * kD * 4);
 }
 
@@ -617,6 +646,7 @@ extern "C" int sophia_kda_chunk_bwd(const void *q, const void *k, const void *v,
   a.dkh = carve(kSlices * tok * kD * 4);
   a.dal = carve(kSlices * tok * kD * 4);
   a.dbc = carve(tok * kD * 4);
+  a.pv = carve(tok * kD * 4);
   a.gpb = carve(static_cast<size_t>(kGateParts) * num_heads * kD * 4);
   a.gpa = carve(static_cast<size_t>(kGateParts) * num_heads * kD * 4);
   hipStream_t st = static_cast<hipStream_t>(stream);
