@@ -143,12 +143,29 @@ struct ChainCtx {
   float *s_kred;    // [2][8 waves][32]
 };
 
+// Lane exchanges without the LDS crossbar: the value of lane l ^ 16 (or
+// l ^ 32) through gfx950's row swaps (v_permlane16_swap / v_permlane32_swap
+// with both operands the same register: each lane then finds its partner's
+// value in one of the two results), and DPP within 16-lane rows.
+__device__ __forceinline__ float xor16(float v, int l) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((l & 16) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float xor32(float v, int l) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((l & 32) ? r[0] : r[1]);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
 // Sum over the 128 state rows of x (one partial per thread, over its 8 rows)
 // for the thread's column.  Consecutive calls alternate between two LDS
 // buffers, so a buffer is rewritten only after every thread has passed the
 // barrier of the call in between (and so has read it).
 __device__ __forceinline__ float row_sum(const ChainCtx &c, float x, int &kb) {
-  x += __shfl_xor(x, 32, 64);
+  x += xor32(x, c.lane);
   float *buf = c.s_kred + kb * 8 * kNV;
   kb ^= 1;
   if (c.lane < kNV) buf[c.wave * kNV + c.j] = x;
@@ -196,15 +213,26 @@ __device__ __forceinline__ float fwd_step(const ChainCtx &c, const TokenIn &in, 
   return p;
 }
 
-// One butterfly stage over lanes l ^ m: of x[0 .. 2N) keep the half selected
-// by lane bit m and add the partner lane's copy of that half.
-template <int N>
-__device__ __forceinline__ void fold(const float (&x)[2 * N], float (&y)[N], int l, int m) {
-  const bool up = (l & m) != 0;
+// One butterfly stage: of x[0 .. 2N) keep the half selected by lane bit m and
+// add the partner lane's copy of that half.  The partner differs in bit m
+// and in lower bits only: lane ^ 16 (row swap), the mirrored lane of the
+// 16-lane row (lane ^ 15, DPP row_mirror), of the 8-lane half-row (lane ^ 7,
+// row_half_mirror), lane ^ 2 and lane ^ 1 (quad_perm).  Partners hold the
+// same half before the stage, so the halves exchange cleanly, and the
+// partner masks 16, 15, 7, 2, 1 together reach all 32 lanes.
+template <int N, int M>
+__device__ __forceinline__ void fold(const float (&x)[2 * N], float (&y)[N], int l) {
+  const bool up = (l & M) != 0;
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     const float keep = up ? x[N + i] : x[i], send = up ? x[i] : x[N + i];
-    y[i] = keep + __shfl_xor(send, m, 64);
+    float got;
+    if constexpr (M == 16) got = xor16(send, l);
+    else if constexpr (M == 8) got = dpp<0x140>(send);     // row_mirror
+    else if constexpr (M == 4) got = dpp<0x141>(send);     // row_half_mirror
+    else if constexpr (M == 2) got = dpp<0x4E>(send);      // quad_perm 2,3,0,1
+    else got = dpp<0xB1>(send);                            // quad_perm 1,0,3,2
+    y[i] = keep + got;
   }
 }
 
@@ -212,11 +240,11 @@ __device__ __forceinline__ void fold(const float (&x)[2 * N], float (&y)[N], int
 // over those lanes of x[i].
 __device__ __forceinline__ float col_sum32(const float (&x)[32], int l) {
   float y16[16], y8[8], y4[4], y2[2], y1[1];
-  fold<16>(x, y16, l, 16);
-  fold<8>(y16, y8, l, 8);
-  fold<4>(y8, y4, l, 4);
-  fold<2>(y4, y2, l, 2);
-  fold<1>(y2, y1, l, 1);
+  fold<16, 16>(x, y16, l);
+  fold<8, 8>(y16, y8, l);
+  fold<4, 4>(y8, y4, l);
+  fold<2, 2>(y4, y2, l);
+  fold<1, 1>(y2, y1, l);
   return y1[0];
 }
 
