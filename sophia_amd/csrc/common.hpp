@@ -130,6 +130,18 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// The value of lane l ^ 16 (or l ^ 32) without the LDS crossbar: gfx950's
+// row swaps (v_permlane16_swap / v_permlane32_swap) with both operands the
+// same register leave each lane's partner value in one of the two results.
+__device__ __forceinline__ float lane_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float lane_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
+
 // Butterfly sum over the whole 64-lane wavefront.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -143,18 +143,8 @@ struct ChainCtx {
   float *s_kred;    // [2][8 waves][32]
 };
 
-// Lane exchanges without the LDS crossbar: the value of lane l ^ 16 (or
-// l ^ 32) through gfx950's row swaps (v_permlane16_swap / v_permlane32_swap
-// with both operands the same register: each lane then finds its partner's
-// value in one of the two results), and DPP within 16-lane rows.
-__device__ __forceinline__ float xor16(float v, int l) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float((l & 16) ? r[0] : r[1]);
-}
-__device__ __forceinline__ float xor32(float v, int l) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float((l & 32) ? r[0] : r[1]);
-}
+// DPP within 16-lane rows (the exchanges across rows are lane_xor16 /
+// lane_xor32, gfx950's row swaps).
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
@@ -165,7 +155,7 @@ __device__ __forceinline__ float dpp(float v) {
 // buffers, so a buffer is rewritten only after every thread has passed the
 // barrier of the call in between (and so has read it).
 __device__ __forceinline__ float row_sum(const ChainCtx &c, float x, int &kb) {
-  x += xor32(x, c.lane);
+  x += lane_xor32(x);
   float *buf = c.s_kred + kb * 8 * kNV;
   kb ^= 1;
   if (c.lane < kNV) buf[c.wave * kNV + c.j] = x;
@@ -227,7 +217,7 @@ __device__ __forceinline__ void fold(const float (&x)[2 * N], float (&y)[N], int
   for (int i = 0; i < N; ++i) {
     const float keep = up ? x[N + i] : x[i], send = up ? x[i] : x[N + i];
     float got;
-    if constexpr (M == 16) got = xor16(send, l);
+    if constexpr (M == 16) got = lane_xor16(send);
     else if constexpr (M == 8) got = dpp<0x140>(send);     // row_mirror
     else if constexpr (M == 4) got = dpp<0x141>(send);     // row_half_mirror
     else if constexpr (M == 2) got = dpp<0x4E>(send);      // quad_perm 2,3,0,1
