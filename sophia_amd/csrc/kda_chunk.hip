@@ -152,10 +152,14 @@ __device__ __forceinline__ int first_chunk(const int32_t *cu, int n, int64_t tot
 }
 
 // ---- intra-chunk kernel ----------------------------------------------------
-// Record writes use non-temporal stores: the records are read back only by the
-// scan kernel, which then runs 99 -> 85 us on the 8-sequence benchmark batch
-// (and this kernel 119 -> 116 us).  The inputs are read once, also with the
-// non-temporal hint (~1 %).
+// The inputs are read once, with the non-temporal hint, so that they do not
+// take the place of the records in the last-level cache (MALL, 256 MB): the
+// records are written with ordinary stores and the scan reads them back from
+// it where they are still there.  Work-groups take the chunks last first, so
+// the first chunks of every sequence, which the scan reads first, are the most
+// recently written.  On the 8-sequence benchmark batch (236 MB of records)
+// the scan that follows runs 87 -> 71 us against non-temporal record stores in
+// chunk order; ordinary input loads instead push it to 95 us.
 // LDS regions (bytes).  Lifetimes (steps below) let regions A and B be reused.
 //  E: e^{sub-block totals}          float [128][4]           steps 3-8
 //  A: key-side rows KD (6 copies)   bf16  [96][136]           steps 4-5
@@ -306,7 +310,7 @@ __device__ __forceinline__ void intra_scaled_operands(
     for (int i = 0; i < 8; ++i)
       sKb[sb.b[i & 3] + 64 * (32 * ks + 16 * (i >> 2))] = f32_to_bf16_bits(kbar[i]);
     // Q e^G goes straight to the workspace in A-operand order (mb = W).
-    __builtin_nontemporal_store(bf8_to_bits(pack8(qe)), reinterpret_cast<u4 *>(rec + kOffQ + ((W * 4 + ks) * 64 + l) * 16));
+    *reinterpret_cast<u4 *>(rec + kOffQ + ((W * 4 + ks) * 64 + l) * 16) = bf8_to_bits(pack8(qe));
     // Key-side rows of this block for the later query blocks, row-major bf16.
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
@@ -508,7 +512,7 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
       const int r0 = 32 * ks + 4 * gq;
       const u2 lo = *reinterpret_cast<const u2 *>(&sKb[swz(ch, r0)]);
       const u2 hi = *reinterpret_cast<const u2 *>(&sKb[swz(ch, r0 + 16)]);
-      __builtin_nontemporal_store(u4{lo.x, lo.y, hi.x, hi.y}, reinterpret_cast<u4 *>(rec + kOffKt + ((mb * 2 + ks) * 64 + l) * 16));
+      *reinterpret_cast<u4 *>(rec + kOffKt + ((mb * 2 + ks) * 64 + l) * 16) = u4{lo.x, lo.y, hi.x, hi.y};
     }
   }
   lds_barrier();
@@ -673,7 +677,7 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
   //         16nb + lr, k = channels perm_k(w, gq, .)) to the workspace; e^{G_C}.
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt)
-    __builtin_nontemporal_store(pack4_bf16(accU[nt]), reinterpret_cast<u2 *>(rec + kOffU + ((w * 8 + nt) * 64 + l) * 8));
+    *reinterpret_cast<u2 *>(rec + kOffU + ((w * 8 + nt) * 64 + l) * 8) = pack4_bf16(accU[nt]);
 #pragma unroll
   for (int nb = 0; nb < 4; ++nb) {
     float t[8];
@@ -682,7 +686,7 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
       t[e] = -accW[0][nb][e];
       t[4 + e] = -accW[1][nb][e];
     }
-    __builtin_nontemporal_store(bf8_to_bits(pack8(t)), reinterpret_cast<u4 *>(rec + kOffW + ((nb * 4 + w) * 64 + l) * 16));
+    *reinterpret_cast<u4 *>(rec + kOffW + ((nb * 4 + w) * 64 + l) * 16) = bf8_to_bits(pack8(t));
   }
   if (tid < kD) {
     const f4 E = *reinterpret_cast<const f4 *>(&s_E[tid * 4]);
@@ -696,7 +700,7 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
     const uint16_t *src = &sQK[(16 * w + lr) * kLdQK + 32 * ks + 4 * gq];
     const u2 lo = *reinterpret_cast<const u2 *>(src);
     const u2 hi = *reinterpret_cast<const u2 *>(src + 16);
-    __builtin_nontemporal_store(u4{lo.x, lo.y, hi.x, hi.y}, reinterpret_cast<u4 *>(rec + kOffA + ((w * 2 + ks) * 64 + l) * 16));
+    *reinterpret_cast<u4 *>(rec + kOffA + ((w * 2 + ks) * 64 + l) * 16) = u4{lo.x, lo.y, hi.x, hi.y};
   }
 }
 
@@ -705,10 +709,10 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   // Head-fastest order: the heads of one chunk run together and read the
   // same token rows (measured 3-10 % faster than chunk-fastest; the scan that
-  // follows also reads the records faster).
+  // follows also reads the records faster).  Chunks run last first (see above).
   const int h = static_cast<int>(blockIdx.x % static_cast<unsigned>(p.num_heads));
-  const int c = static_cast<int>(blockIdx.x / static_cast<unsigned>(p.num_heads));
-  if (c >= p.max_ch) return;
+  const int c = static_cast<int>(p.max_ch - 1) - static_cast<int>(blockIdx.x / static_cast<unsigned>(p.num_heads));
+  if (c < 0) return;
   int s, first;
   chunk_of(p.cu, p.n_seqs, p.total, c, s, first);
   if (s >= p.n_seqs) return;  // past the last chunk (uniform over the work-group)
