@@ -498,13 +498,31 @@ def chunk_kda(q, k, v, g, beta, *, scale=None, initial_state=None, output_final_
     (o [B, T, H, 128] in q.dtype, final_state fp32 [N, H, 128, 128] or None).
     The log-decay must stay in [-5, 0]: the gate computed in the kernel always
     does; a precomputed g needs ``safe_gate`` with ``lower_bound >= -5``.
+    As in FlashKDAFunction.forward (sm120_concurrent_ffn.py:240-244),
+    ``allow_neg_eigval`` makes the in-kernel beta sigmoid 2 sigmoid(beta)
+    (beta in [0, 2]: the eigenvalues of I - beta k k^T reach -1) and does
+    nothing without ``use_beta_sigmoid_in_kernel``; ``state_v_first`` takes and
+    returns states as [N, H, V, K] (the transpose of the kernels' [K, V]).
     """
     if kwargs:
         raise TypeError(f"unexpected arguments: {sorted(kwargs)}")
     if int(chunk_size) != CHUNK_SIZE:
         raise RuntimeError("sophia_amd chunk_kda supports chunk_size=64 only")
-    if allow_neg_eigval or state_v_first:
-        raise RuntimeError("allow_neg_eigval / state_v_first are not supported")
+    if allow_neg_eigval and use_beta_sigmoid_in_kernel:
+        # 2 sigmoid(beta) on the device, ahead of the kernels (autograd carries
+        # its derivative); the kernels then take beta as given.
+        beta = 2.0 * torch.sigmoid(beta.float())
+        use_beta_sigmoid_in_kernel = False
+    if state_v_first:
+        o, ht = chunk_kda(q, k, v, g, beta, scale=scale,
+                          initial_state=None if initial_state is None else initial_state.transpose(-1, -2),
+                          output_final_state=output_final_state,
+                          use_qk_l2norm_in_kernel=use_qk_l2norm_in_kernel,
+                          use_gate_in_kernel=use_gate_in_kernel,
+                          use_beta_sigmoid_in_kernel=use_beta_sigmoid_in_kernel, safe_gate=safe_gate,
+                          lower_bound=lower_bound, A_log=A_log, dt_bias=dt_bias, cu_seqlens=cu_seqlens,
+                          cu_seqlens_cpu=cu_seqlens_cpu, chunk_size=chunk_size)
+        return o, (None if ht is None else ht.transpose(-1, -2))
     lb = -5.0 if lower_bound is None else float(lower_bound)
     if not use_gate_in_kernel and not safe_gate:
         raise RuntimeError("a precomputed gate needs safe_gate=True (log-decay in [lower_bound, 0])")

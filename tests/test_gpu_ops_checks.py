@@ -162,3 +162,67 @@ def test_kda_chunk_fwd_host_cu_seqlens_matches_oracle():
     o = ops.kda_chunk_fwd(q, k, v, g, beta, torch.tensor(cu_np), final_state=st, **kw)
     o_ref, h_ref = c_oracle.kda_varlen(_np(q), _np(k), _np(v), _np(g), _np(beta), cu_np, **kw)
     assert _rel(_np(o), o_ref) < REL_TOL and _rel(_np(st), h_ref) < REL_TOL
+
+
+def test_chunk_kda_allow_neg_eigval_matches_oracle():
+    """allow_neg_eigval with the beta sigmoid in the kernel: beta = 2 sigmoid(b)
+    (sm120_concurrent_ffn.py:240-244).  Forward against the fp32 C oracle given
+    that beta; the gradient of the raw b against the float64 oracle backward
+    times 2 s (1 - s)."""
+    from sophia_amd import ops
+    dev = _dev()
+    rng = np.random.default_rng(41)
+    lens = [130, 70]
+    cu_np = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    total, heads = int(cu_np[-1]), 2
+    f32 = lambda a: torch.tensor(a, dtype=torch.float32, device=dev)
+    q, k, v = (f32(rng.standard_normal((1, total, heads, 128))) for _ in range(3))
+    g = f32(rng.uniform(-1.0, 0.0, (1, total, heads, 128)))
+    b = f32(rng.standard_normal((1, total, heads)) * 1.5).requires_grad_(True)
+    cu_cpu = torch.tensor(cu_np)
+    o, ht = ops.chunk_kda(q, k, v, g, b, output_final_state=True, use_qk_l2norm_in_kernel=True,
+                          use_beta_sigmoid_in_kernel=True, allow_neg_eigval=True, safe_gate=True,
+                          lower_bound=-5.0, cu_seqlens=cu_cpu.to(dev), cu_seqlens_cpu=cu_cpu)
+    beta_eff = 2.0 / (1.0 + np.exp(-_np(b)[0].astype(np.float64)))
+    assert beta_eff.max() > 1.5      # the case reaches negative eigenvalues of I - beta k k^T
+    o_ref, h_ref = c_oracle.kda_varlen(_np(q)[0], _np(k)[0], _np(v)[0], _np(g)[0], beta_eff, cu_np,
+                                       use_qk_l2norm=True, use_gate=False, use_beta_sigmoid=False)
+    assert _rel(_np(o)[0], o_ref) < REL_TOL
+    assert _rel(_np(ht), h_ref) < REL_TOL
+    w = torch.tensor(rng.standard_normal((1, total, heads, 128)), dtype=torch.float32, device=dev)
+    (o * w).sum().backward()
+    ref = ko.kda_varlen_bwd(_np(q)[0], _np(k)[0], _np(v)[0], _np(g)[0], beta_eff, cu_np, _np(w)[0],
+                            use_qk_l2norm=True, use_gate=False, use_beta_sigmoid=False)
+    s = beta_eff / 2.0
+    db_ref = ref["dbeta"] * 2.0 * s * (1.0 - s)
+    assert _rel(_np(b.grad)[0], db_ref) < 1e-4
+
+
+def test_chunk_kda_state_v_first_is_the_transposed_state():
+    """state_v_first: states in and out as [N, H, V, K].  Bit-equal to the
+    default layout with the states transposed, forward and initial-state
+    gradient."""
+    from sophia_amd import ops
+    dev = _dev()
+    rng = np.random.default_rng(42)
+    lens = [100, 37]
+    cu_np = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    total, heads, n = int(cu_np[-1]), 2, len(lens)
+    f32 = lambda a: torch.tensor(a, dtype=torch.float32, device=dev)
+    q, k, v = (f32(rng.standard_normal((1, total, heads, 128))) for _ in range(3))
+    g = f32(rng.uniform(-2.0, 0.0, (1, total, heads, 128)))
+    b = f32(rng.uniform(0.0, 1.0, (1, total, heads)))
+    h0 = f32(rng.standard_normal((n, heads, 128, 128)) * 0.1)
+    cu_cpu = torch.tensor(cu_np)
+    kw = dict(output_final_state=True, use_qk_l2norm_in_kernel=True, safe_gate=True, lower_bound=-5.0,
+              cu_seqlens=cu_cpu.to(dev), cu_seqlens_cpu=cu_cpu)
+    o1, h1 = ops.chunk_kda(q, k, v, g, b, initial_state=h0, **kw)
+    o2, h2 = ops.chunk_kda(q, k, v, g, b, initial_state=h0.transpose(-1, -2).contiguous(),
+                           state_v_first=True, **kw)
+    assert torch.equal(o1, o2) and torch.equal(h1, h2.transpose(-1, -2))
+    a1 = h0.clone().requires_grad_(True)
+    a2 = h0.transpose(-1, -2).contiguous().requires_grad_(True)
+    w = f32(rng.standard_normal((1, total, heads, 128)))
+    (ops.chunk_kda(q, k, v, g, b, initial_state=a1, **kw)[0] * w).sum().backward()
+    (ops.chunk_kda(q, k, v, g, b, initial_state=a2, state_v_first=True, **kw)[0] * w).sum().backward()
+    assert torch.equal(a1.grad, a2.grad.transpose(-1, -2))
