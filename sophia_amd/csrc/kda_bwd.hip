@@ -28,8 +28,8 @@
 //    checkpoint and runs the reverse steps: two passes over the tokens plus
 //    the recompute.  Every piece it walks is staged in LDS by the whole
 //    work-group, the next piece's loads in flight while the current one is
-//    processed.  Sums over value columns (dq^, dk^, dalpha) leave as
-//    per-slice partials; dbeta leaves per value column.
+//    processed.  Sums over value columns (dq^, dk^, dalpha, and dbeta in the
+//    same column reduction) leave as per-slice partials.
 //  * kda_bwd_post_kernel, one work-group of 128 threads per (token, head):
 //    sums the partials and applies the backward of the l2 norms, of the gate
 //    g = lb sigmoid(e^A_log (z + dt_bias)) and of the beta sigmoid.
@@ -87,7 +87,7 @@ struct BwdArgs {
   float *qh, *kh, *gl, *bt;        // prepared q^, k^, alpha = e^g, beta
   float *ckpt;                     // [pieces, H, 128, 128] states at every 8-token piece start
   float *dqh, *dkh, *dal;          // [kSlices, total, H, 128] partial sums
-  float *dbc;                      // [total, H, 128] dbeta per value column
+  float *dbp;                      // [kSlices, total, H] dbeta summed over a slice's columns
   float *pv;                       // [total, H, 128] p = k^T S~ of every token (forward walk)
   float *gpb, *gpa;                // [kGateParts, H, 128] partial ddt_bias / dA_log
 };
@@ -432,8 +432,9 @@ __global__ __launch_bounds__(kChainThreads) void kda_bwd_chain_kernel(BwdArgs a)
               x[2 * kRows + i] = dst * Sp[tt][i];               // dalpha partial
               dS[i] = al * dst;                                 // dS_{t-1}
             }
+            x[3 * kRows] = du * vp;                             // dbeta term of this column
 #pragma unroll
-            for (int i = 3 * kRows; i < 32; ++i) x[i] = 0.f;
+            for (int i = 3 * kRows + 1; i < 32; ++i) x[i] = 0.f;
             const float rsum = col_sum32(x, l32);
             if (l32 < 3 * kRows) {
               const int vec = l32 / kRows, row = r0 + (l32 % kRows);
@@ -441,9 +442,8 @@ __global__ __launch_bounds__(kChainThreads) void kda_bwd_chain_kernel(BwdArgs a)
               dst[((static_cast<int64_t>(slice) * a.total + tok) * a.num_heads + h) * kD + row] = rsum;
             }
             if (c.rg == 0) {
-              const int64_t o = (tok * a.num_heads + h) * kD + c.col;
-              a.dv[o] = cur.bt * du;
-              a.dbc[o] = du * vp;
+              a.dv[(tok * a.num_heads + h) * kD + c.col] = cur.bt * du;
+              if (l32 == 3 * kRows) a.dbp[(static_cast<int64_t>(slice) * a.total + tok) * a.num_heads + h] = rsum;
             }
           }
           __builtin_amdgcn_sched_barrier(0);
@@ -470,7 +470,7 @@ __global__ __launch_bounds__(kD) void kda_bwd_post_kernel(BwdArgs a) {
   const int64_t tok = blockIdx.x;
   const int h = blockIdx.y;
   const int c = threadIdx.x;
-  __shared__ float s_red[2][5];
+  __shared__ float s_red[2][4];
   const int64_t o = (tok * a.num_heads + h) * kD + c;
   float dqh = 0.f, dkh = 0.f, dal = 0.f;
 #pragma unroll
@@ -485,26 +485,25 @@ __global__ __launch_bounds__(kD) void kda_bwd_post_kernel(BwdArgs a) {
   const float kv = load_elem(a.k, row, a.qkv_dtype);
   const bool l2 = (a.flags & SOPHIA_KDA_QK_L2NORM) != 0;
   // With the norm, y = x / n (n = max(|x|, eps)) and dx = (dy - y (y . dy)) / n
-  // where |x| >= eps, dx = dy / n where the clamp holds n constant.
-  const float yq = l2 ? a.qh[o] / a.scale : qv;
-  const float yk = a.kh[o];
+  // where |x| >= eps, dx = dy / n where the clamp holds n constant; y . dy is
+  // formed as (x . dy) / n, so y is not read back.
   const float dyq = dqh * a.scale;
-  const float r0 = wave_sum(yq * dyq), r1 = wave_sum(yk * dkh), r2 = wave_sum(qv * qv),
-              r3 = wave_sum(kv * kv), r4 = wave_sum(a.dbc[o]);
+  const float r0 = wave_sum(qv * dyq), r1 = wave_sum(kv * dkh), r2 = wave_sum(qv * qv),
+              r3 = wave_sum(kv * kv);
   if ((c & 63) == 0) {
     s_red[c >> 6][0] = r0;
     s_red[c >> 6][1] = r1;
     s_red[c >> 6][2] = r2;
     s_red[c >> 6][3] = r3;
-    s_red[c >> 6][4] = r4;
   }
   __syncthreads();
   float dq = dyq, dk = dkh;
   if (l2) {
     const float lq = sqrtf(s_red[0][2] + s_red[1][2]), lk = sqrtf(s_red[0][3] + s_red[1][3]);
     const float nq = fmaxf(lq, 1e-12f), nk = fmaxf(lk, 1e-12f);
-    dq = (lq < 1e-12f ? dyq : dyq - yq * (s_red[0][0] + s_red[1][0])) / nq;
-    dk = (lk < 1e-12f ? dkh : dkh - yk * (s_red[0][1] + s_red[1][1])) / nk;
+    const float yq = qv / nq, yk = kv / nk;
+    dq = (lq < 1e-12f ? dyq : dyq - yq * ((s_red[0][0] + s_red[1][0]) / nq)) / nq;
+    dk = (lk < 1e-12f ? dkh : dkh - yk * ((s_red[0][1] + s_red[1][1]) / nk)) / nk;
   }
   a.dq[o] = dq;
   a.dk[o] = dk;
@@ -518,7 +517,9 @@ __global__ __launch_bounds__(kD) void kda_bwd_post_kernel(BwdArgs a) {
   }
   a.dg[o] = dgv;
   if (c == 0) {
-    float db = s_red[0][4] + s_red[1][4];
+    float db = 0.f;
+#pragma unroll
+    for (int sl = 0; sl < kSlices; ++sl) db += a.dbp[(static_cast<int64_t>(sl) * a.total + tok) * a.num_heads + h];
     if (a.flags & SOPHIA_KDA_BETA_SIGMOID) {
       const float bt = a.bt[tok * a.num_heads + h];
       db *= bt * (1.f - bt);
@@ -596,7 +597,7 @@ extern "C" size_t sophia_kda_chunk_bwd_workspace_size(int64_t total_tokens, int 
   const size_t tok = static_cast<size_t>(total_tokens) * num_heads;
   return 3 * align256(tok * kD * 4) + align256(tok * 4) +
          align256(max_pieces(total_tokens, n_seqs) * num_heads * kD * kD * 4) +
-         3 * align256(kSlices * tok * kD * 4) + 2 * align256(tok * kD * 4) +
+         3 * align256(kSlices * tok * kD * 4) + align256(kSlices * tok * 4) + align256(tok * kD * 4) +
          2 * align256(static_cast<size_t>(kGateParts) * num_heads * kD * 4);
 }
 
@@ -663,7 +664,7 @@ extern "C" int sophia_kda_chunk_bwd(const void *q, const void *k, const void *v,
   a.dqh = carve(kSlices * tok * kD * 4);
   a.dkh = carve(kSlices * tok * kD * 4);
   a.dal = carve(kSlices * tok * kD * 4);
-  a.dbc = carve(tok * kD * 4);
+  a.dbp = carve(kSlices * tok * 4);
   a.pv = carve(tok * kD * 4);
   a.gpb = carve(static_cast<size_t>(kGateParts) * num_heads * kD * 4);
   a.gpa = carve(static_cast<size_t>(kGateParts) * num_heads * kD * 4);
