@@ -21,8 +21,11 @@ Kg = K e^G, Kn = K e^-G, Qg = Q e^G, Kbar = K e^(Gamma - G):
             dA_kk = tril_strict(-T^T dT T^T), then the products back to Q, K, V,
             beta and G, and dg = reverse cumsum of dG plus dGamma on every row.
 
-The exponentials are formed over a whole chunk here (float64 holds e^320); the
-kernels factor them per 16-token sub-block exactly as the forward does.
+``chunk_backward`` forms the exponentials over a whole chunk (float64 holds
+e^320).  ``chunk_backward_factored`` is the form fp32 kernels need: the
+products through A_qk and A_kk take the forward's per-16-token sub-block
+factors (``decay_products_factored``), so no factor exceeds e^80, and every
+other exponential it forms is at most 1.
 """
 
 from __future__ import annotations
@@ -50,7 +53,8 @@ def chunk_forward(qn, kn, v, g, beta, s0):
     rows = np.arange(CHUNK)
     strict = rows[:, None] > rows[None, :]
     incl = rows[:, None] >= rows[None, :]
-    A_kk = np.where(strict, beta[:, None] * (Kg @ Kn.T), 0.0)
+    P = np.where(strict, Kg @ Kn.T, 0.0)
+    A_kk = beta[:, None] * P
     A_qk = np.where(incl, Qg @ Kn.T, 0.0)
     T = np.linalg.inv(np.eye(CHUNK) + A_kk)
     Xw = beta[:, None] * Kg
@@ -61,7 +65,7 @@ def chunk_forward(qn, kn, v, g, beta, s0):
     o = Qg @ s0 + A_qk @ U
     s1 = np.exp(gam)[:, None] * s0 + Kbar.T @ U
     ctx = dict(c=c, qn=qn, kn=kn, v=v, beta=beta, G=G, gam=gam, Kg=Kg, Kn=Kn, Qg=Qg, Kbar=Kbar,
-               A_qk=A_qk, T=T, Xw=Xw, Xu=Xu, W=W, U=U, s0=s0, strict=strict, incl=incl)
+               A_qk=A_qk, P=P, T=T, Xw=Xw, Xu=Xu, W=W, U=U, s0=s0, strict=strict, incl=incl)
     return o[:c], s1, ctx
 
 
@@ -143,3 +147,99 @@ def kda_chunked_bwd(qn, kn, v, g, beta, s0, do, ds_final=None):
         for arr, part in zip(out, (dq_c, dk_c, dv_c, dg_c, db_c)):
             arr[start:stop] = part
     return (*out, ds)
+
+
+SUB = 16
+
+
+def _factors(G):
+    """Sub-block reference points of chunk_model.py: ref[s] = G[16 s - 1]
+    (ref[0] = 0), and the per-row factors a = e^(G - ref[blk]) <= 1,
+    bq = e^(ref[blk] - G) <= e^80, d = e^(ref[blk + 1] - G) <= 1."""
+    key_dim = G.shape[1]
+    ref = np.zeros((5, key_dim))
+    for s in range(1, 5):
+        ref[s] = G[SUB * s - 1]
+    blk = np.arange(CHUNK) // SUB
+    a = np.exp(G - ref[blk])
+    bq = np.exp(ref[blk] - G)
+    d = np.exp(ref[blk + 1] - G)
+    return ref, a, bq, d
+
+
+def decay_products_factored(ctx, dA_qk, dP):
+    """The gradient products through A_qk = tril(Qg Kn^T) and P = Kg Kn^T (the
+    unmasked A_kk / beta) with no factor above e^80, as fp32 kernels form them.
+
+    For r in sub-block i and j in sub-block b <= i,
+    e^(G_r - G_j) = a_r f_ib d_j with f_ib = e^(ref_i - ref_(b+1)) <= 1 (b < i),
+    and a_r bq_j on the diagonal blocks.  Returns (dq_e, dk_e, dG_e): the
+    contributions of dA_qk and dP to dq, dk and dG, equal to
+    dQg += dA_qk Kn, dKg += dP Kn, dKn = dA_qk^T Qg + dP^T Kg taken through
+    Qg = Q e^G, Kg = K e^G, Kn = K e^-G."""
+    qn, kn, G = ctx["qn"], ctx["kn"], ctx["G"]
+    ref, a, bq, d = _factors(G)
+    QS, KS = qn * a, kn * a             # <= |q|, |k|
+    KB, KD = kn * bq, kn * d            # KB only on diagonal blocks
+    dq_p = np.zeros_like(qn)            # sum_j dA_qk[r, j] k_j e^(G_r - G_j)
+    dkg_p = np.zeros_like(kn)           # sum_j dP[r, j] k_j e^(G_r - G_j)
+    dkq = np.zeros_like(kn)             # sum_r dA_qk[r, j] q_r e^(G_r - G_j)
+    dkk = np.zeros_like(kn)             # sum_r dP[r, j] k_r e^(G_r - G_j)
+    for i in range(4):
+        ri = slice(SUB * i, SUB * i + SUB)
+        for b in range(i + 1):
+            rb = slice(SUB * b, SUB * b + SUB)
+            Aq, Ak = dA_qk[ri, rb], dP[ri, rb]
+            if b == i:
+                dq_p[ri] += a[ri] * (Aq @ KB[rb])
+                dkg_p[ri] += a[ri] * (Ak @ KB[rb])
+                dkq[rb] += bq[rb] * (Aq.T @ QS[ri])
+                dkk[rb] += bq[rb] * (Ak.T @ KS[ri])
+            else:
+                f = np.exp(ref[i] - ref[b + 1])[None, :]
+                dq_p[ri] += a[ri] * f * (Aq @ KD[rb])
+                dkg_p[ri] += a[ri] * f * (Ak @ KD[rb])
+                dkq[rb] += d[rb] * f * (Aq.T @ QS[ri])
+                dkk[rb] += d[rb] * f * (Ak.T @ KS[ri])
+    dq_e = dq_p
+    dk_e = dkg_p + dkq + dkk
+    dG_e = qn * dq_p + kn * dkg_p - kn * (dkq + dkk)
+    return dq_e, dk_e, dG_e
+
+
+def chunk_backward_factored(ctx, do, ds1):
+    """chunk_backward with the A_qk / A_kk products through the sub-block
+    factors (decay_products_factored) instead of e^G and e^-G over the chunk;
+    every other exponential it forms is at most 1."""
+    c = ctx["c"]
+    do = _pad(np.asarray(do, dtype=np.float64), CHUNK - c)
+    s0, U, T, W = ctx["s0"], ctx["U"], ctx["T"], ctx["W"]
+    beta, v, kn = ctx["beta"], ctx["v"], ctx["kn"]
+    Kg, Qg, Kbar, A_qk = ctx["Kg"], ctx["Qg"], ctx["Kbar"], ctx["A_qk"]
+    G, gam = ctx["G"], ctx["gam"]
+    dU = A_qk.T @ do + Kbar @ ds1
+    ds0 = np.exp(gam)[:, None] * ds1 + Qg.T @ do - W.T @ dU
+    dA_qk = np.where(ctx["incl"], do @ U.T, 0.0)
+    dQg = do @ s0.T
+    dW = -dU @ s0.T
+    dKbar = U @ ds1.T
+    dgam = np.sum(ds1 * s0, axis=1) * np.exp(gam)
+    dT = dW @ ctx["Xw"].T + dU @ ctx["Xu"].T
+    dXw = T.T @ dW
+    dXu = T.T @ dU
+    dv = beta[:, None] * dXu
+    dbeta = np.sum(dXu * v, axis=1) + np.sum(dXw * Kg, axis=1)
+    dA_kk = np.where(ctx["strict"], -T.T @ dT @ T.T, 0.0)
+    A_kk_over_beta = ctx["P"]
+    # A_kk = Diag(beta) P (strict): dbeta from P = A_kk / beta without dividing
+    dbeta += np.sum(dA_kk * A_kk_over_beta, axis=1)
+    dP = beta[:, None] * dA_kk
+    dq_e, dk_e, dG_e = decay_products_factored(ctx, dA_qk, dP)
+    eG = np.exp(G)                      # <= 1
+    dKg = beta[:, None] * dXw
+    dqn = dQg * eG + dq_e
+    dkn = dKg * eG + dKbar * np.exp(gam[None, :] - G) + dk_e
+    dG = dKg * Kg + dQg * Qg - dKbar * Kbar + dG_e
+    dgam = dgam + np.sum(dKbar * Kbar, axis=0)
+    dg = np.cumsum(dG[::-1], axis=0)[::-1] + dgam[None, :]
+    return dqn[:c], dkn[:c], dv[:c], dg[:c], dbeta[:c], ds0

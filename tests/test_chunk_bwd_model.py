@@ -69,3 +69,36 @@ def test_reverse_chunk_scan_step_needs_no_state():
     ctx2 = dict(ctx, s0=np.full_like(s0, np.nan))        # the state must not be read
     ds0 = cbm.chunk_dstate(ctx2, do, dsf)
     assert _rel(ds0, ds0_full) < 1e-12
+
+
+@pytest.mark.parametrize("g_lo,seed", [(-5.0, 21), (-1e-3, 22), (-0.5, 23)])
+def test_factored_decay_products_equal_the_chunk_backward(g_lo, seed):
+    """The sub-block-factored products (no factor above e^80) give the same
+    chunk gradients as the whole-chunk exponentials, for a full and a partial
+    chunk, including the strongest decay (cumulative log-decay -320)."""
+    for c in (64, 37):
+        qn, kn, v, g, beta, s0, do, dsf = _case(c, 16, 8, seed, g_lo=g_lo, g_hi=0.0)
+        _, _, ctx = cbm.chunk_forward(qn, kn, v, g, beta, s0)
+        ref = cbm.chunk_backward(ctx, do, dsf)
+        got = cbm.chunk_backward_factored(ctx, do, dsf)
+        for a, b in zip(got, ref):
+            assert _rel(a, b) < 1e-10
+
+
+def test_factored_decay_products_are_fp32_safe():
+    """In float32 the factored products stay finite at the strongest decay and
+    match float64 to fp32 rounding (the whole-chunk e^-G would overflow)."""
+    qn, kn, v, g, beta, s0, do, dsf = _case(64, 16, 8, 31, g_lo=-5.0, g_hi=-4.0)
+    _, _, ctx = cbm.chunk_forward(qn, kn, v, g, beta, s0)
+    rng = np.random.default_rng(32)
+    rows = np.arange(64)
+    dA_qk = np.where(rows[:, None] >= rows[None, :], rng.standard_normal((64, 64)), 0.0)
+    dP = np.where(rows[:, None] > rows[None, :], rng.standard_normal((64, 64)), 0.0)
+    ref = cbm.decay_products_factored(ctx, dA_qk, dP)
+    ctx32 = {key: ctx[key].astype(np.float32) for key in ("qn", "kn", "G")}
+    with np.errstate(over="raise", invalid="raise"):
+        got = cbm.decay_products_factored(ctx32, dA_qk.astype(np.float32), dP.astype(np.float32))
+    assert np.exp(-ctx["G"].min()) > np.finfo(np.float32).max   # e^-G alone overflows fp32
+    for a, b in zip(got, ref):
+        assert np.all(np.isfinite(a))
+        assert _rel(a, b) < 1e-4
