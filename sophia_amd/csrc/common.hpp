@@ -39,10 +39,13 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   __bf16 h = static_cast<__bf16>(f);  // round to nearest even (v_cvt_pk_bf16_f32 on gfx950)
   return __builtin_bit_cast(uint16_t, h);
 }
-// Packs two floats into one dword of bf16 (lo in bits 0..15).
+// Packs two floats into one dword of bf16 (lo in bits 0..15), round to
+// nearest even: one v_cvt_pk_bf16_f32 (a two-element vector conversion; two
+// scalar ones would cost two conversions, a shift and an or).
+typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return static_cast<uint32_t>(f32_to_bf16_bits(lo)) |
-         (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
+  const bf2 v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 // x rounded to the given element type and back (identity for fp32).

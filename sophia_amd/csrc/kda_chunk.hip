@@ -40,6 +40,7 @@ namespace {
 constexpr int kD = 128;   // key / value head dim
 constexpr int kC = 64;    // chunk length
 constexpr int kThreads = 256;
+constexpr float kLog2e = 1.4426950408889634f;
 
 // ---- workspace record, per (chunk, head) ----------------------------------
 constexpr size_t kFrag = 64 * 16;                  // one A fragment: 64 lanes x 8 bf16
@@ -282,8 +283,8 @@ __device__ __forceinline__ void intra_scaled_operands(
     for (int i = 0; i < 8; ++i) {
       const int e = 8 * ks + i;
       const f4 E = *reinterpret_cast<const f4 *>(&s_E[perm_k(ks, gq, i) * 4]);
-      const float a = __expf(gv[e]);
-      const float b = __expf(-gv[e]);
+      const float a = __builtin_amdgcn_exp2f(gv[e]);
+      const float b = __builtin_amdgcn_exp2f(-gv[e]);
       float eref = 1.f, etl = 1.f;
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
@@ -437,7 +438,9 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
     if (p.flags & SOPHIA_KDA_BETA_SIGMOID) bt = fast_sigmoid(bt);
     bt *= vmask;
     if constexpr (GATE) hs = __expf(hs);
-    const float glb = GATE ? p.lb * vmask : vmask;
+    // Log-decays are kept in base 2 (times log2 e) from here on, so that each
+    // exponential below is one v_exp_f32.
+    const float glb = (GATE ? p.lb * vmask : vmask) * kLog2e;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const f4 a = rq[i].get(), b = rk[i].get(), cc = rv[i].get(), d = rg[i].get();
@@ -479,12 +482,12 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
     }
   }
 
-  // ---- 3. within-sub-block cumulative log-decay; E[ch][i] = e^{tot_i}
+  // ---- 3. within-sub-block cumulative log-decay (base 2); E[ch][i] = e^{tot_i}
 #pragma unroll
   for (int e = 0; e < 32; ++e) gv[e] = row_scan16(gv[e]);
   if (lr == 15) {
 #pragma unroll
-    for (int e = 0; e < 32; ++e) s_E[perm_k(e >> 3, gq, e & 7) * 4 + w] = __expf(gv[e]);
+    for (int e = 0; e < 32; ++e) s_E[perm_k(e >> 3, gq, e & 7) * 4 + w] = __builtin_amdgcn_exp2f(gv[e]);
   }
   lds_barrier();
 
@@ -694,9 +697,12 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
   }
 
   // ---- 10. A_qk fragments from LDS to the workspace
-  // A_qk: m = chunk rows 16w + lr, k = chunk rows perm_k(ks, gq, .)
+  // A_qk: m = chunk rows 16w + lr, k = chunk rows perm_k(ks, gq, .).  The
+  // fragments of K-step 1 for rows 0..31 are zero (A_qk is lower
+  // triangular): they are neither written nor read.
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
+    if (ks == 1 && w < 2) break;
     const uint16_t *src = &sQK[(16 * w + lr) * kLdQK + 32 * ks + 4 * gq];
     const u2 lo = *reinterpret_cast<const u2 *>(src);
     const u2 hi = *reinterpret_cast<const u2 *>(src + 16);
@@ -806,12 +812,13 @@ __device__ __forceinline__ void load_uo_main(UOFrags<NT> &f, const uint8_t *rec,
       f.ut[nt] = *reinterpret_cast<const u2 *>(rec + kOffU + ((w * 8 + nt0 + nt) * 64 + l) * 8);
   }
 }
-// ... and A_qk, used after it.
+// ... and A_qk, used after it.  Rows 0..31 (w < 2) use K-step 0 only: their
+// K-step-1 fragment is not in the record, so that load re-reads K-step 0
+// (same lines, unused) instead of sitting under a branch.
 template <int NT>
 __device__ __forceinline__ void load_uo_aq(UOFrags<NT> &f, const uint8_t *rec, int w, int l) {
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks)
-    f.aq[ks] = *reinterpret_cast<const u4 *>(rec + kOffA + ((w * 2 + ks) * 64 + l) * 16);
+  f.aq[0] = *reinterpret_cast<const u4 *>(rec + kOffA + ((w * 2) * 64 + l) * 16);
+  f.aq[1] = *reinterpret_cast<const u4 *>(rec + kOffA + ((w * 2 + (w >= 2 ? 1 : 0)) * 64 + l) * 16);
 }
 
 __device__ __forceinline__ void load_s(SFrags &f, const uint8_t *rec, int sw, int l, int gq) {
