@@ -293,22 +293,27 @@ def backward_bench(torch, dev, stream, inp, steps: int, warmup: int, with_cpu: b
     gen = torch.Generator().manual_seed(12)
     d_out = torch.randn((total, HEADS, DIM), generator=gen).to(torch.bfloat16).to(dev)
 
-    def call():
+    def call(recurrent=False):
         ops.kda_chunk_bwd(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], inp["cu"], d_out,
                           use_qk_l2norm=True, use_gate=False, use_beta_sigmoid=False,
-                          cu_seqlens_cpu=inp["cu_cpu"])
+                          cu_seqlens_cpu=inp["cu_cpu"], recurrent=recurrent)
 
     _, per = time_events(torch, call, steps, warmup, stream)
     ms = float(np.mean(per))
+    _, per_rec = time_events(torch, lambda: call(True), max(steps // 2, 2), 1, stream)
     gbs = total * BWD_BYTES_PER_TOKEN / (ms / 1e3) / 1e9
     tflops = total * BWD_FLOPS_PER_TOKEN / (ms / 1e3) / 1e12
     out = {"workload": "KDA backward over the prefill batch (same lengths, flags and inputs), "
                        "bf16 d_out, fp32 gradients",
+           "form": "chunk (records, forward-state and reverse chunk scans on bf16 MFMA operands, "
+                   "per-chunk gradients on fp32 MFMA)",
            "tokens_per_s": round(total / (ms / 1e3), 1), "ms_per_call": round(ms, 3),
-           "roofline": {"bound": "fp32 VALU (sequential chain)", "achieved": round(tflops, 2),
+           "recurrent_form_ms_per_call": round(float(np.mean(per_rec)), 3),
+           "roofline": {"bound": "fp32 MFMA / latency", "achieved": round(tflops, 2),
                         "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
                         "frac": round(tflops / FP32_PEAK_TFLOPS, 4),
-                        "flops_per_token": BWD_FLOPS_PER_TOKEN},
+                        "flops_per_token": BWD_FLOPS_PER_TOKEN,
+                        "flops_convention": "the per-token recurrent form's 20 d^2 per head"},
            "algorithmic_bytes_per_call": total * BWD_BYTES_PER_TOKEN,
            "GBps": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
     if with_cpu:

@@ -59,6 +59,10 @@ extern "C" {
  * at least 128 chunks is scanned segment-parallel (its results then differ
  * from the single chain by rounding only). */
 #define SOPHIA_KDA_SCAN_NO_SEGMENTS 8u
+/* Backward switch (sophia_kda_chunk_bwd): the per-token recurrent form in
+ * fp32 arithmetic instead of the chunk form on bf16 MFMA operands (fp32
+ * accumulation and state, the forward's arithmetic). */
+#define SOPHIA_KDA_BWD_RECURRENT 16u
 
 /* Message of the last failing call on this thread ("" if none). */
 const char *sophia_last_error(void);

@@ -31,6 +31,7 @@ QK_L2NORM = 1
 GATE_IN_KERNEL = 2
 BETA_SIGMOID = 4
 SCAN_NO_SEGMENTS = 8
+BWD_RECURRENT = 16
 
 # Every symbol of include/sophia_kda.h and include/sophia_decoder.h, with its
 # ctypes signature.

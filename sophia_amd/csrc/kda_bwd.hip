@@ -44,6 +44,7 @@
 #include <mutex>
 
 #include "common.hpp"
+#include "kda_chunk_bwd.hpp"
 
 namespace sophia {
 namespace {
@@ -85,6 +86,9 @@ struct BwdArgs {
   float *dq, *dk, *dv, *dg, *dbeta, *dh0, *dA_log, *ddt_bias;
   // workspace
   float *qh, *kh, *gl, *bt;        // prepared q^, k^, alpha = e^g, beta
+  float *glg;                      // prepared log-decay g (chunk form only), or NULL
+  int parts;                       // partial sums per gradient: kSlices (recurrent) or 1 (chunk form)
+  int dg_given;                    // dal holds the gradient of g itself (chunk form), not of alpha
   float *ckpt;                     // [pieces, H, 128, 128] states at every 8-token piece start
   float *dqh, *dkh, *dal;          // [kSlices, total, H, 128] partial sums
   float *dbp;                      // [kSlices, total, H] dbeta summed over a slice's columns
@@ -120,6 +124,7 @@ __global__ __launch_bounds__(kD) void kda_bwd_prep_kernel(BwdArgs a) {
   a.qh[o] = qv * qs;
   a.kh[o] = kv * ks;
   a.gl[o] = expf(z);
+  if (a.glg) a.glg[o] = z;
   if (c == 0) {
     if (a.flags & SOPHIA_KDA_BETA_SIGMOID) b = 1.f / (1.f + expf(-b));
     a.bt[tok * a.num_heads + h] = b;
@@ -473,8 +478,7 @@ __global__ __launch_bounds__(kD) void kda_bwd_post_kernel(BwdArgs a) {
   __shared__ float s_red[2][4];
   const int64_t o = (tok * a.num_heads + h) * kD + c;
   float dqh = 0.f, dkh = 0.f, dal = 0.f;
-#pragma unroll
-  for (int sl = 0; sl < kSlices; ++sl) {
+  for (int sl = 0; sl < a.parts; ++sl) {
     const int64_t po = ((static_cast<int64_t>(sl) * a.total + tok) * a.num_heads + h) * kD + c;
     dqh += a.dqh[po];
     dkh += a.dkh[po];
@@ -507,8 +511,9 @@ __global__ __launch_bounds__(kD) void kda_bwd_post_kernel(BwdArgs a) {
   }
   a.dq[o] = dq;
   a.dk[o] = dk;
-  // alpha = e^g: dg = dalpha alpha; through the gate, dz = dg lb s (1 - s) e^A_log
-  float dgv = dal * a.gl[o];
+  // alpha = e^g: dg = dalpha alpha (the chunk form gives dg itself); through
+  // the gate, dz = dg lb s (1 - s) e^A_log
+  float dgv = a.dg_given ? dal : dal * a.gl[o];
   if (a.flags & SOPHIA_KDA_GATE_IN_KERNEL) {
     const float z = load_elem(a.g, tok * a.g_stride + static_cast<int64_t>(h) * kD + c, a.g_dtype);
     const float ea = expf(a.A_log[h]);
@@ -518,8 +523,7 @@ __global__ __launch_bounds__(kD) void kda_bwd_post_kernel(BwdArgs a) {
   a.dg[o] = dgv;
   if (c == 0) {
     float db = 0.f;
-#pragma unroll
-    for (int sl = 0; sl < kSlices; ++sl) db += a.dbp[(static_cast<int64_t>(sl) * a.total + tok) * a.num_heads + h];
+    for (int sl = 0; sl < a.parts; ++sl) db += a.dbp[(static_cast<int64_t>(sl) * a.total + tok) * a.num_heads + h];
     if (a.flags & SOPHIA_KDA_BETA_SIGMOID) {
       const float bt = a.bt[tok * a.num_heads + h];
       db *= bt * (1.f - bt);
@@ -591,14 +595,28 @@ int ensure_chain_lds() {
 
 using namespace sophia;
 
+// Workspace: the prepared inputs and the gate partials (both forms), then
+// either form's own part.
+namespace {
+size_t bwd_common_bytes(size_t tok, int num_heads) {
+  return 3 * align256(tok * kD * 4) + align256(tok * 4) + 2 * align256(static_cast<size_t>(kGateParts) * num_heads * kD * 4);
+}
+size_t bwd_recurrent_bytes(int64_t total_tokens, int n_seqs, int num_heads, size_t tok) {
+  return align256(max_pieces(total_tokens, n_seqs) * num_heads * kD * kD * 4) + 3 * align256(kSlices * tok * kD * 4) +
+         align256(kSlices * tok * 4) + align256(tok * kD * 4);
+}
+size_t bwd_chunk_bytes(int64_t total_tokens, int n_seqs, int num_heads, size_t tok) {
+  return 4 * align256(tok * kD * 4) + align256(tok * 4) + align256(chunk_bwd_scratch_bytes(total_tokens, n_seqs, num_heads));
+}
+}  // namespace
+
 extern "C" size_t sophia_kda_chunk_bwd_workspace_size(int64_t total_tokens, int n_seqs, int num_heads,
                                                       int head_dim) {
   if (total_tokens < 0 || n_seqs <= 0 || num_heads <= 0 || head_dim != kD) return 0;
   const size_t tok = static_cast<size_t>(total_tokens) * num_heads;
-  return 3 * align256(tok * kD * 4) + align256(tok * 4) +
-         align256(max_pieces(total_tokens, n_seqs) * num_heads * kD * kD * 4) +
-         3 * align256(kSlices * tok * kD * 4) + align256(kSlices * tok * 4) + align256(tok * kD * 4) +
-         2 * align256(static_cast<size_t>(kGateParts) * num_heads * kD * 4);
+  const size_t rec = bwd_recurrent_bytes(total_tokens, n_seqs, num_heads, tok);
+  const size_t chk = bwd_chunk_bytes(total_tokens, n_seqs, num_heads, tok);
+  return bwd_common_bytes(tok, num_heads) + (rec > chk ? rec : chk);
 }
 
 extern "C" int sophia_kda_chunk_bwd(const void *q, const void *k, const void *v, int64_t qkv_row_stride,
@@ -660,24 +678,60 @@ extern "C" int sophia_kda_chunk_bwd(const void *q, const void *k, const void *v,
   a.kh = carve(tok * kD * 4);
   a.gl = carve(tok * kD * 4);
   a.bt = carve(tok * 4);
-  a.ckpt = carve(max_pieces(total_tokens, n_seqs) * num_heads * kD * kD * 4);
-  a.dqh = carve(kSlices * tok * kD * 4);
-  a.dkh = carve(kSlices * tok * kD * 4);
-  a.dal = carve(kSlices * tok * kD * 4);
-  a.dbp = carve(kSlices * tok * 4);
-  a.pv = carve(tok * kD * 4);
   a.gpb = carve(static_cast<size_t>(kGateParts) * num_heads * kD * 4);
   a.gpa = carve(static_cast<size_t>(kGateParts) * num_heads * kD * 4);
+  const bool recurrent = (flags & SOPHIA_KDA_BWD_RECURRENT) != 0;
+  if (!recurrent && total_tokens > 0) {
+    // the chunk form reads rows of q, k, v and d_out four elements at a time
+    const auto aligned = [](const void *ptr, int dtype) {
+      return reinterpret_cast<uintptr_t>(ptr) % (dtype == SOPHIA_DTYPE_BF16 ? 8 : 16) == 0;
+    };
+    SOPHIA_REQUIRE(qkv_row_stride % 4 == 0 && g_row_stride % 4 == 0 && d_out_row_stride % 4 == 0,
+                   "kda_chunk_bwd: q/k/v/g/d_out row strides must be multiples of 4 elements");
+    SOPHIA_REQUIRE(aligned(q, qkv_dtype) && aligned(k, qkv_dtype) && aligned(v, qkv_dtype) &&
+                       aligned(g, g_dtype) && aligned(d_out, d_out_dtype),
+                   "kda_chunk_bwd: q/k/v/g/d_out must be aligned to 4 elements");
+  }
+  void *scratch = nullptr;
+  if (recurrent) {
+    a.ckpt = carve(max_pieces(total_tokens, n_seqs) * num_heads * kD * kD * 4);
+    a.dqh = carve(kSlices * tok * kD * 4);
+    a.dkh = carve(kSlices * tok * kD * 4);
+    a.dal = carve(kSlices * tok * kD * 4);
+    a.dbp = carve(kSlices * tok * 4);
+    a.pv = carve(tok * kD * 4);
+    a.parts = kSlices;
+    a.dg_given = 0;
+  } else {
+    a.glg = carve(tok * kD * 4);
+    a.dqh = carve(tok * kD * 4);
+    a.dkh = carve(tok * kD * 4);
+    a.dal = carve(tok * kD * 4);
+    a.dbp = carve(tok * 4);
+    scratch = carve(chunk_bwd_scratch_bytes(total_tokens, n_seqs, num_heads));
+    a.parts = 1;
+    a.dg_given = 1;
+  }
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (const int rc = ensure_chain_lds()) return rc;
   if (total_tokens > 0) {
     hipLaunchKernelGGL(kda_bwd_prep_kernel, dim3(static_cast<unsigned>(total_tokens), num_heads), dim3(kD), 0, st,
                        a);
     if (const int rc = check_launch("kda_bwd_prep")) return rc;
   }
-  hipLaunchKernelGGL(kda_bwd_chain_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kChainThreads), kChainLds, st,
-                     a);
-  if (const int rc = check_launch("kda_bwd_chain")) return rc;
+  if (recurrent) {
+    if (const int rc = ensure_chain_lds()) return rc;
+    hipLaunchKernelGGL(kda_bwd_chain_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kChainThreads), kChainLds, st,
+                       a);
+    if (const int rc = check_launch("kda_bwd_chain")) return rc;
+  } else {
+    // The chunk form (records, forward states, reverse chunk scan, per-chunk
+    // gradients on MFMA): d q^, d k^, d g, d beta of every token, dv, dh0.
+    ChunkBwdIO io{q, k, v, qkv_row_stride, qkv_dtype, g, g_row_stride, g_dtype, beta, beta_row_stride,
+                  beta_dtype, A_log, dt_bias, scale, lower_bound, flags, cu_seqlens, n_seqs, total_tokens,
+                  num_heads, initial_state, d_out, d_out_row_stride, d_out_dtype, d_final_state,
+                  a.qh, a.kh, a.glg, a.bt, a.dqh, a.dkh, a.dal, a.dbp, dv, d_initial_state};
+    if (const int rc = chunk_bwd_run(io, scratch, st)) return rc;
+  }
   if (total_tokens > 0) {
     hipLaunchKernelGGL(kda_bwd_post_kernel, dim3(static_cast<unsigned>(total_tokens), num_heads), dim3(kD), 0, st,
                        a);

@@ -33,6 +33,7 @@
 #include <mutex>
 
 #include "common.hpp"
+#include "kda_chunk_bwd.hpp"
 
 namespace sophia {
 namespace {
@@ -51,6 +52,20 @@ constexpr size_t kOffA = kOffKt + 16 * kFrag;      // A_qk    [mb 4][ks 2]
 constexpr size_t kOffU = kOffA + 8 * kFrag;        // Ut      [mb 4][nt 8][lane 64][4 bf16]
 constexpr size_t kOffG = kOffU + 32 * 64 * 8;      // e^{G_C} [128] fp32
 constexpr size_t kRecBytes = kOffG + kD * 4;       // 74240
+
+// ---- backward record, per (chunk, head) (the backward's instantiation of
+// the intra kernel writes it beside the forward record) -------------------
+//  Kbar   A operand, m = chunk rows 16mb + lr, k = channels perm_k   [mb 4][ks 4]
+//  Qg^T   A operand, m = channels 16mb + lr, k = chunk rows perm_k [mb 8][ks 2]
+//  -W^T   A operand, m = channels, k = chunk rows perm_k           [mb 8][ks 2]
+//  A_qk^T A operand, m = chunk rows j 16mb + lr, k = rows i perm_k [mb 4][ks 2]
+//  dO     B operand, k = chunk rows perm_k, n = value cols 16nt+lr [ks 2][nt 8]
+constexpr size_t kBOffKbar = 0;
+constexpr size_t kBOffQt = kBOffKbar + 16 * kFrag;
+constexpr size_t kBOffWt = kBOffQt + 16 * kFrag;
+constexpr size_t kBOffAt = kBOffWt + 16 * kFrag;
+constexpr size_t kBOffDo = kBOffAt + 8 * kFrag;
+constexpr size_t kBwdRecBytes = kBOffDo + 16 * kFrag;   // 73728
 
 inline int64_t max_chunks(int64_t total, int n) { return total / kC + n; }
 // Scratch rows for the stores of chunk rows past the end of a sequence
@@ -178,6 +193,10 @@ constexpr size_t kSmB = kSmA + 96 * kLdKD * 2;
 constexpr size_t kSmC = kSmB + 64 * kLdKD * 2;
 constexpr size_t kSmD = kSmC + 64 * kLdT * 4;
 constexpr size_t kSmIntra = kSmD + 64 * kLdQK * 2;           // 73216
+// Backward instantiations: Q e^G and dO, transposed ([128][64] bf16, swizzled).
+constexpr size_t kSmF = kSmIntra;
+constexpr size_t kSmG = kSmF + 128 * 64 * 2;
+constexpr size_t kSmIntraBwd = kSmG + 128 * 64 * 2;
 static_assert(128 * 64 * 2 <= 96 * kLdKD * 2, "region A holds a swizzled [128][64] bf16 tile");
 static_assert(128 * 64 * 2 <= 64 * kLdKD * 2, "region B holds a swizzled [128][64] bf16 tile");
 static_assert(128 * 64 * 2 <= 64 * kLdT * 4, "region C holds a swizzled [128][64] bf16 tile");
@@ -216,6 +235,13 @@ struct IntraArgs {
   int64_t max_ch;
   uint8_t *records;
   int qkv_lines;  // bf16 q/k/v with 16-byte aligned rows: load whole lines through LDS
+  // Backward instantiations only: the backward record, T = (I + A_kk)^-1 and
+  // P = A_kk / beta (fp32 [64][64] per (chunk, head)), and the output gradient.
+  uint8_t *brec;
+  float *tmat, *pmat;
+  const void *dout;
+  int64_t do_stride;
+  int do_dtype;
 };
 
 __device__ __forceinline__ float fast_sigmoid(float x) {
@@ -271,11 +297,12 @@ __device__ __forceinline__ SwzBases swz_bases(int gq, int row) {
 // eref = e^{ref_W} = prod_{i<W} E_i, etail = e^{G_C - ref_{W+1}} = prod_{i>W} E_i.
 // All products are of factors <= 1, so they can only underflow where the true
 // value is below 2^-126.
-template <int W>
+template <int W, bool BWD>
 __device__ __forceinline__ void intra_scaled_operands(
     const float (&qv)[32], const float (&kv)[32], const float (&gv)[32], float bt,
     const float *s_E, uint16_t *sKD, uint16_t *sKb, uint8_t *rec, const SwzBases &sb, int l,
-    int lr, int gq, bf8 (&QSf)[4], bf8 (&KSf)[4], u4 (&kt_bits)[4], f4 &aqk_d, f4 &akk_d) {
+    int lr, int gq, bf8 (&QSf)[4], bf8 (&KSf)[4], u4 (&kt_bits)[4], f4 &aqk_d, f4 &akk_d,
+    uint8_t *brec, uint16_t *sQt) {
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
     float qa[8], ka[8], kb[8], kd[8], kd1[8], kd2[8], kbar[8], qe[8], kt[8];
@@ -312,6 +339,13 @@ __device__ __forceinline__ void intra_scaled_operands(
       sKb[sb.b[i & 3] + 64 * (32 * ks + 16 * (i >> 2))] = f32_to_bf16_bits(kbar[i]);
     // Q e^G goes straight to the workspace in A-operand order (mb = W).
     *reinterpret_cast<u4 *>(rec + kOffQ + ((W * 4 + ks) * 64 + l) * 16) = bf8_to_bits(pack8(qe));
+    if constexpr (BWD) {
+      // Kbar in A-operand order (m = rows); Q e^G transposed for Qg^T.
+      *reinterpret_cast<u4 *>(brec + kBOffKbar + ((W * 4 + ks) * 64 + l) * 16) = bf8_to_bits(pack8(kbar));
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        sQt[sb.b[i & 3] + 64 * (32 * ks + 16 * (i >> 2))] = f32_to_bf16_bits(qe[i]);
+    }
     // Key-side rows of this block for the later query blocks, row-major bf16.
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
@@ -334,9 +368,16 @@ __device__ __forceinline__ void intra_scaled_operands(
 // wavefronts) with kSmIntra bytes of LDS at smem; writes the record at rec.
 // Every barrier inside is a work-group barrier: a work-group running two
 // items at once runs them in lock step.
-template <int QKV_DT, int G_DT, bool GATE>
+// BWD: the backward's instantiation, which also writes the backward record,
+// T and P of the item (IntraArgs::brec / tmat / pmat) and needs kSmIntraBwd
+// bytes of LDS.
+template <int QKV_DT, int G_DT, bool GATE, bool BWD = false>
 __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int first, int h, uint8_t *smem,
                                            int tid, uint8_t *rec) {
+  const size_t item = static_cast<size_t>(c) * p.num_heads + h;
+  uint8_t *brec = BWD ? p.brec + item * kBwdRecBytes : nullptr;
+  uint16_t *sQt = reinterpret_cast<uint16_t *>(smem + kSmF);
+  uint16_t *sDo = reinterpret_cast<uint16_t *>(smem + kSmG);
   float *s_E = reinterpret_cast<float *>(smem + kSmE);
   uint16_t *sKD = reinterpret_cast<uint16_t *>(smem + kSmA);
   uint16_t *sKt = reinterpret_cast<uint16_t *>(smem + kSmA);
@@ -456,6 +497,17 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
         sV[sb.b[j] + 64 * (32 * (i >> 1) + 16 * (i & 1))] = f32_to_bf16_bits(bt * cc[j]);  // beta V^T
       }
     }
+    if constexpr (BWD) {
+      // dO of this row, transposed (rows past the sequence end are zero).
+      const int64_t drow = ltok * p.do_stride + static_cast<int64_t>(h) * kD;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const f4 d = load4(p.dout, drow + 32 * (i >> 1) + 16 * (i & 1) + 4 * gq, p.do_dtype);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          sDo[sb.b[j] + 64 * (32 * (i >> 1) + 16 * (i & 1))] = f32_to_bf16_bits(vmask * d[j]);
+      }
+    }
   }
 
   // ---- 2. l2 norms (a row is spread over the 4 lane groups)
@@ -496,10 +548,10 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
   u4 kt_bits[4];                // beta K e^G, bf16, operand order
   f4 aqk_d = {0.f, 0.f, 0.f, 0.f}, akk_d = aqk_d;
   switch (w) {
-    case 0: intra_scaled_operands<0>(qv, kv, gv, bt, s_E, sKD, sKb, rec, sb, l, lr, gq, QSf, KSf, kt_bits, aqk_d, akk_d); break;
-    case 1: intra_scaled_operands<1>(qv, kv, gv, bt, s_E, sKD, sKb, rec, sb, l, lr, gq, QSf, KSf, kt_bits, aqk_d, akk_d); break;
-    case 2: intra_scaled_operands<2>(qv, kv, gv, bt, s_E, sKD, sKb, rec, sb, l, lr, gq, QSf, KSf, kt_bits, aqk_d, akk_d); break;
-    default: intra_scaled_operands<3>(qv, kv, gv, bt, s_E, sKD, sKb, rec, sb, l, lr, gq, QSf, KSf, kt_bits, aqk_d, akk_d); break;
+    case 0: intra_scaled_operands<0, BWD>(qv, kv, gv, bt, s_E, sKD, sKb, rec, sb, l, lr, gq, QSf, KSf, kt_bits, aqk_d, akk_d, brec, sQt); break;
+    case 1: intra_scaled_operands<1, BWD>(qv, kv, gv, bt, s_E, sKD, sKb, rec, sb, l, lr, gq, QSf, KSf, kt_bits, aqk_d, akk_d, brec, sQt); break;
+    case 2: intra_scaled_operands<2, BWD>(qv, kv, gv, bt, s_E, sKD, sKb, rec, sb, l, lr, gq, QSf, KSf, kt_bits, aqk_d, akk_d, brec, sQt); break;
+    default: intra_scaled_operands<3, BWD>(qv, kv, gv, bt, s_E, sKD, sKb, rec, sb, l, lr, gq, QSf, KSf, kt_bits, aqk_d, akk_d, brec, sQt); break;
   }
   lds_barrier();
 
@@ -516,6 +568,15 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
       const u2 lo = *reinterpret_cast<const u2 *>(&sKb[swz(ch, r0)]);
       const u2 hi = *reinterpret_cast<const u2 *>(&sKb[swz(ch, r0 + 16)]);
       *reinterpret_cast<u4 *>(rec + kOffKt + ((mb * 2 + ks) * 64 + l) * 16) = u4{lo.x, lo.y, hi.x, hi.y};
+      if constexpr (BWD) {
+        const u2 qlo = *reinterpret_cast<const u2 *>(&sQt[swz(ch, r0)]);
+        const u2 qhi = *reinterpret_cast<const u2 *>(&sQt[swz(ch, r0 + 16)]);
+        *reinterpret_cast<u4 *>(brec + kBOffQt + ((mb * 2 + ks) * 64 + l) * 16) = u4{qlo.x, qlo.y, qhi.x, qhi.y};
+        // dO B operand of value-column tile nt = mb (k = the same chunk rows).
+        const u2 dlo = *reinterpret_cast<const u2 *>(&sDo[swz(ch, r0)]);
+        const u2 dhi = *reinterpret_cast<const u2 *>(&sDo[swz(ch, r0 + 16)]);
+        *reinterpret_cast<u4 *>(brec + kBOffDo + ((ks * 8 + mb) * 64 + l) * 16) = u4{dlo.x, dlo.y, dhi.x, dhi.y};
+      }
     }
   }
   lds_barrier();
@@ -550,6 +611,7 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
         const int r = 16 * w + 4 * gq + e;
         sQK[r * kLdQK + col] = f32_to_bf16_bits(col <= r ? aqk[e] : 0.f);
         sT[r * kLdT + col] = col < r ? akk[e] * brow[e] : 0.f;
+        if constexpr (BWD) p.pmat[item * (kC * kC) + r * kC + col] = col < r ? akk[e] : 0.f;
       }
     }
   }
@@ -674,6 +736,33 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
         for (int mi = 0; mi < 2; ++mi) accW[mi][nb] = mfma32(kta[mi][ks], tb, accW[mi][nb]);
       }
     }
+    if constexpr (BWD) {
+      // W itself (the same fragments with the operands swapped): C tiles of
+      // rows 16nb + 4gq + e and channel 16(2w + mi) + lr.  The tiles of row
+      // blocks 2ks and 2ks + 1 are the two halves of the -W^T A operand of
+      // K-step ks (k = chunk rows perm_k(ks, gq, .)).
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi) {
+        f4 wt[4];
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) {
+          wt[nb] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < (nb < 2 ? 1 : 2); ++ks)
+            wt[nb] = mfma32(t_frag(16 * nb + lr, 32 * ks + 8 * gq), kta[mi][ks], wt[nb]);
+        }
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          float t[8];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            t[e] = -wt[2 * ks][e];
+            t[4 + e] = -wt[2 * ks + 1][e];
+          }
+          *reinterpret_cast<u4 *>(brec + kBOffWt + (((2 * w + mi) * 2 + ks) * 64 + l) * 16) = bf8_to_bits(pack8(t));
+        }
+      }
+    }
   }
 
   // ---- 9. Ut in C-tile order and -W as A-operand fragments (m = chunk rows
@@ -694,6 +783,26 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
   if (tid < kD) {
     const f4 E = *reinterpret_cast<const f4 *>(&s_E[tid * 4]);
     reinterpret_cast<float *>(rec + kOffG)[tid] = E[0] * E[1] * E[2] * E[3];
+  }
+  if constexpr (BWD) {
+    // T (fp32, row-major [64][64]): thread t copies row t / 4, 16 columns.
+    const int r = tid >> 2, c0 = 16 * (tid & 3);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<f4 *>(&p.tmat[item * (kC * kC) + r * kC + c0 + 4 * i]) =
+          *reinterpret_cast<const f4 *>(&sT[r * kLdT + c0 + 4 * i]);
+    // A_qk^T fragments: m = chunk rows j = 16w + lr, k = rows i perm_k(ks, gq, .).
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      uint32_t wd[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const uint32_t a = sQK[perm_k(ks, gq, e) * kLdQK + 16 * w + lr];
+        const uint32_t b = sQK[perm_k(ks, gq, e + 1) * kLdQK + 16 * w + lr];
+        wd[e >> 1] = a | (b << 16);
+      }
+      *reinterpret_cast<u4 *>(brec + kBOffAt + ((w * 2 + ks) * 64 + l) * 16) = u4{wd[0], wd[1], wd[2], wd[3]};
+    }
   }
 
   // ---- 10. A_qk fragments from LDS to the workspace
@@ -724,6 +833,21 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
   if (s >= p.n_seqs) return;  // past the last chunk (uniform over the work-group)
   intra_item<QKV_DT, G_DT, GATE>(p, c, s, first, h, smem, threadIdx.x,
                                  p.records + (static_cast<size_t>(c) * p.num_heads + h) * kRecBytes);
+}
+
+// The backward's instantiation: the same item, plus the backward record, T
+// and P (one work-group per CU: kSmIntraBwd bytes of LDS).
+template <int QKV_DT, int G_DT, bool GATE>
+__global__ __launch_bounds__(kThreads, 1) void kda_chunk_intra_bwd_kernel(IntraArgs p) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int h = static_cast<int>(blockIdx.x % static_cast<unsigned>(p.num_heads));
+  const int c = static_cast<int>(p.max_ch - 1) - static_cast<int>(blockIdx.x / static_cast<unsigned>(p.num_heads));
+  if (c < 0) return;
+  int s, first;
+  chunk_of(p.cu, p.n_seqs, p.total, c, s, first);
+  if (s >= p.n_seqs) return;
+  intra_item<QKV_DT, G_DT, GATE, true>(p, c, s, first, h, smem, threadIdx.x,
+                                       p.records + (static_cast<size_t>(c) * p.num_heads + h) * kRecBytes);
 }
 
 // ---- scan kernel -------------------------------------------------------------
@@ -1355,6 +1479,638 @@ __global__ __launch_bounds__(kScanThreads) void kda_chunk_seg_run_kernel(SegArgs
   }
 }
 
+// ---- backward: forward states, reverse chunk scan, per-chunk gradients --------
+// The chunk form of the backward (FlashKDA's chunk_kda_train_bwd, as
+// FlashKDAFunction.backward calls it, ml/training/pretrain/engine/
+// sm120_concurrent_ffn.py:301-373).  Per chunk, with S0 the state entering it
+// and dS1 the gradient of the state leaving it:
+//   dU  = A_qk^T dO + Kbar dS1
+//   dS0 = Diag(e^Gamma) dS1 + Qg^T dO - W^T dU        (the reverse chunk scan)
+// and once S0, U, dS1 and dU of every chunk are known, its gradients need
+// nothing from the other chunks:
+//   dQg = dO S0^T, dW = -dU S0^T, dKbar = U dS1^T, dA_qk = tril(dO U^T),
+//   dT = dW Xw^T + dU Xu^T (Xw = beta Kg, Xu = beta V), dXw = T^T dW,
+//   dXu = T^T dU, dA_kk = tril_strict(-T^T dT T^T), then back through
+//   A_kk = Diag(beta) P and A_qk with the sub-block factors, and dg = the
+//   reverse cumulative sum of dG plus dGamma on every row.
+// Three kernels after the backward's instantiation of the intra kernel:
+//  * kda_bwd_states_kernel: the forward scan keeping S0 and U of every chunk;
+//  * kda_bwd_rscan_kernel: the reverse scan, same two roles as the forward
+//    one: four wavefronts form dU (rows 16w..), four hold dS in fp32 MFMA
+//    accumulators; it keeps dS1 and dU of every chunk and leaves dh0;
+//  * kda_bwd_grad_kernel: one work-group per (chunk, head), every product on
+//    fp32 MFMA through generic fragment loaders.
+struct BwdChunkArgs {
+  ScanArgs p;                  // offsets, sizes, forward records, h0
+  const uint8_t *brec;         // backward records
+  const float *tmat, *pmat;    // [max_ch][H][64][64]
+  float *s0, *u, *ds1, *du;    // [max_ch][H][128][128], [max_ch][H][64][128]
+  const float *dht;            // [n_seqs][H][128][128] or NULL
+  float *dh0;                  // [n_seqs][H][128][128] or NULL
+  int splits;                  // work-groups (value-column slices) per (sequence, head): 2, 4 or 8
+  const float *qh, *kh, *glog, *bt;   // prepared q^, k^, log-decay [total][H][128], beta [total][H]
+  const void *v;
+  int64_t v_stride;
+  int v_dtype;
+  const void *dout;
+  int64_t do_stride;
+  int do_dtype;
+  float *dqh, *dkh, *dgl, *dbp, *dv;  // gradients of q^, k^, the log-decay, beta, v
+};
+
+// One (sequence, head, NVB value columns) of the forward scan that keeps S0
+// and U of every chunk (the steps of scan_item without O, the records read at
+// each chunk).
+template <int NVB>
+__device__ __forceinline__ void fstate_item(const BwdChunkArgs &a, const Chain &c, int h, int half, uint8_t *sSb,
+                                            uint8_t *sUb) {
+  constexpr int NT = NVB / 16;
+  const ScanArgs &p = a.p;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l = tid & 63, lr = l & 15, gq = l >> 4;
+  const int nt0 = half * NT;
+  const int nchunks = __builtin_amdgcn_readfirstlane(c.nchunks);
+  const size_t H = static_cast<size_t>(p.num_heads);
+  const size_t item0 = static_cast<size_t>(c.first) * H + h;
+  if (wave < 4) {
+    const int w = wave;
+    for (int cc = 0; cc < nchunks; ++cc) {
+      const size_t it = item0 + static_cast<size_t>(cc) * H;
+      const uint8_t *rec = p.records + it * kRecBytes;
+      u4 wn[4];
+      u2 ut[NT];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) wn[ks] = *reinterpret_cast<const u4 *>(rec + kOffW + ((w * 4 + ks) * 64 + l) * 16);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) ut[nt] = *reinterpret_cast<const u2 *>(rec + kOffU + ((w * 8 + nt0 + nt) * 64 + l) * 8);
+      float *uo = a.u + it * (kC * kD);
+      lds_barrier();  // S of this chunk is published
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        f4 u = f4{__uint_as_float(ut[nt].x << 16), __uint_as_float(ut[nt].x & 0xffff0000u),
+                  __uint_as_float(ut[nt].y << 16), __uint_as_float(ut[nt].y & 0xffff0000u)};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+          u = mfma32(bits_to_bf8(wn[ks]), bits_to_bf8(*reinterpret_cast<const u4 *>(sSb + ((ks * NT + nt) * 64 + l) * 16)), u);
+        *reinterpret_cast<u2 *>(sUb + (((w >> 1) * NT + nt) * 64 + l) * 16 + (w & 1) * 8) = pack4_bf16(u);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) uo[(16 * w + 4 * gq + e) * kD + 16 * (nt0 + nt) + lr] = u[e];
+      }
+      lds_barrier();  // U is published
+    }
+    return;
+  }
+  const int sw = wave - 4;
+  f4 S[2][NT];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        S[mi][nt][e] = c.init ? c.init[(32 * sw + 16 * mi + 4 * gq + e) * kD + 16 * (nt0 + nt) + lr] : 0.f;
+  if (nchunks > 0) publish_state<NT>(S, sSb, sw, l);
+  for (int cc = 0; cc < nchunks; ++cc) {
+    const size_t it = item0 + static_cast<size_t>(cc) * H;
+    const uint8_t *rec = p.records + it * kRecBytes;
+    SFrags f;
+    load_s(f, rec, sw, l, gq);
+    float *so = a.s0 + it * (kD * kD);
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) so[(32 * sw + 16 * mi + 4 * gq + e) * kD + 16 * (nt0 + nt) + lr] = S[mi][nt][e];
+    lds_barrier();  // S published (the U role forms U)
+    state_update<NT>(f, S, sSb, sUb, sw, l);  // waits for U, updates S, publishes it
+  }
+}
+
+__global__ __launch_bounds__(kScanThreads) void kda_bwd_states_kernel(BwdChunkArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t sSb[4 * 8 * 64 * 16];
+  __shared__ __attribute__((aligned(16))) uint8_t sUb[2 * 8 * 64 * 16];
+  const ScanArgs &p = a.p;
+  int item, half;
+  seg_item(blockIdx.x, a.splits, item, half);
+  const int h = item % p.num_heads;
+  const int s = item / p.num_heads;
+  if (s >= p.n_seqs) return;
+  const Chain c = sequence_chain(p, s, h);
+  switch (a.splits) {
+    case 8: fstate_item<16>(a, c, h, half, sSb, sUb); break;
+    case 4: fstate_item<32>(a, c, h, half, sSb, sUb); break;
+    default: fstate_item<64>(a, c, h, half, sSb, sUb); break;
+  }
+}
+
+// One (sequence, head, NVB value columns) of the reverse scan on 512 threads;
+// the chunks of the sequence in reverse order.  Barriers pair as in
+// scan_item: per chunk, dS published -> the dU role forms and publishes dU ->
+// the state role updates dS and publishes it for the chunk before.
+template <int NVB>
+__device__ __forceinline__ void rscan_item(const BwdChunkArgs &a, const Chain &c, int s, int h, int half,
+                                           uint8_t *sSb, uint8_t *sUb) {
+  constexpr int NT = NVB / 16;
+  const ScanArgs &p = a.p;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l = tid & 63, lr = l & 15, gq = l >> 4;
+  const int nt0 = half * NT;
+  const int nchunks = __builtin_amdgcn_readfirstlane(c.nchunks);
+  const size_t H = static_cast<size_t>(p.num_heads);
+  const size_t item0 = static_cast<size_t>(c.first) * H + h;
+  if (wave < 4) {
+    const int w = wave;
+    for (int cc = nchunks - 1; cc >= 0; --cc) {
+      const size_t it = item0 + static_cast<size_t>(cc) * H;
+      const uint8_t *br = a.brec + it * kBwdRecBytes;
+      u4 at[2], kb[4], dob[2][NT];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) at[ks] = *reinterpret_cast<const u4 *>(br + kBOffAt + ((w * 2 + ks) * 64 + l) * 16);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) kb[ks] = *reinterpret_cast<const u4 *>(br + kBOffKbar + ((w * 4 + ks) * 64 + l) * 16);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          dob[ks][nt] = *reinterpret_cast<const u4 *>(br + kBOffDo + ((ks * 8 + nt0 + nt) * 64 + l) * 16);
+      float *duo = a.du + it * (kC * kD);
+      lds_barrier();  // dS1 of this chunk is published
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        f4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) d = mfma32(bits_to_bf8(at[ks]), bits_to_bf8(dob[ks][nt]), d);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+          d = mfma32(bits_to_bf8(kb[ks]), bits_to_bf8(*reinterpret_cast<const u4 *>(sSb + ((ks * NT + nt) * 64 + l) * 16)), d);
+        *reinterpret_cast<u2 *>(sUb + (((w >> 1) * NT + nt) * 64 + l) * 16 + (w & 1) * 8) = pack4_bf16(d);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) duo[(16 * w + 4 * gq + e) * kD + 16 * (nt0 + nt) + lr] = d[e];
+      }
+      lds_barrier();  // dU is published
+    }
+    return;
+  }
+  // state role: dS rows 32sw + 16mi + 4gq + e, column 16(nt0 + nt) + lr
+  const int sw = wave - 4;
+  const size_t sq = (static_cast<size_t>(s) * H + h) * kD * kD;
+  f4 S[2][NT];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        S[mi][nt][e] = a.dht ? a.dht[sq + (32 * sw + 16 * mi + 4 * gq + e) * kD + 16 * (nt0 + nt) + lr] : 0.f;
+  if (nchunks > 0) publish_state<NT>(S, sSb, sw, l);
+  for (int cc = nchunks - 1; cc >= 0; --cc) {
+    const size_t it = item0 + static_cast<size_t>(cc) * H;
+    const uint8_t *br = a.brec + it * kBwdRecBytes;
+    const float *gam = reinterpret_cast<const float *>(p.records + it * kRecBytes + kOffG);
+    u4 qt[2][2], wt[2][2], dob[2][NT];
+    f4 gm[2];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        qt[mi][ks] = *reinterpret_cast<const u4 *>(br + kBOffQt + (((2 * sw + mi) * 2 + ks) * 64 + l) * 16);
+        wt[mi][ks] = *reinterpret_cast<const u4 *>(br + kBOffWt + (((2 * sw + mi) * 2 + ks) * 64 + l) * 16);
+      }
+      gm[mi] = *reinterpret_cast<const f4 *>(&gam[32 * sw + 16 * mi + 4 * gq]);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+        dob[ks][nt] = *reinterpret_cast<const u4 *>(br + kBOffDo + ((ks * 8 + nt0 + nt) * 64 + l) * 16);
+    float *so = a.ds1 + it * (kD * kD);
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) so[(32 * sw + 16 * mi + 4 * gq + e) * kD + 16 * (nt0 + nt) + lr] = S[mi][nt][e];
+    lds_barrier();  // dS1 published (the dU role forms dU)
+    lds_barrier();  // dU published
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      bf8 ub[2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) ub[ks] = bits_to_bf8(*reinterpret_cast<const u4 *>(sUb + ((ks * NT + nt) * 64 + l) * 16));
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi) {
+        f4 v = S[mi][nt] * gm[mi];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) v = mfma32(bits_to_bf8(qt[mi][ks]), bits_to_bf8(dob[ks][nt]), v);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) v = mfma32(bits_to_bf8(wt[mi][ks]), ub[ks], v);
+        S[mi][nt] = v;
+      }
+    }
+    publish_state<NT>(S, sSb, sw, l);
+  }
+  if (a.dh0) {
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          a.dh0[sq + (32 * sw + 16 * mi + 4 * gq + e) * kD + 16 * (nt0 + nt) + lr] = S[mi][nt][e];
+  }
+}
+
+__global__ __launch_bounds__(kScanThreads) void kda_bwd_rscan_kernel(BwdChunkArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t sSb[4 * 8 * 64 * 16];
+  __shared__ __attribute__((aligned(16))) uint8_t sUb[2 * 8 * 64 * 16];
+  const ScanArgs &p = a.p;
+  int item, half;
+  seg_item(blockIdx.x, a.splits, item, half);
+  const int h = item % p.num_heads;
+  const int s = item / p.num_heads;
+  if (s >= p.n_seqs) return;
+  const Chain c = sequence_chain(p, s, h);
+  switch (a.splits) {
+    case 8: rscan_item<16>(a, c, s, h, half, sSb, sUb); break;
+    case 4: rscan_item<32>(a, c, s, h, half, sSb, sUb); break;
+    default: rscan_item<64>(a, c, s, h, half, sSb, sUb); break;
+  }
+}
+
+// 16 x 16 C tile (+)= A (16 x 32 ks) B (32 ks x 16) over the K-steps k0,
+// k0 + 32, .. (mma8): fa(m, kb, x) fills x[i] = A[m][kb + i] and
+// fb(kb, n, x) fills x[i] = B[kb + i][n] for the lane's m = n = lr and
+// kb = k0 + 32 s + 8 gq (the operand layout of v_mfma_f32_16x16x32_bf16).
+// acc += x . y over the lane group's 8 k values (x[i] = A[m][kb + i],
+// y[i] = B[kb + i][n]) on fp32 MFMA: eight 16x16x4 steps, the k slot of lane
+// group g in step i being 8 g + i.  (bf16 operands here leave dg, and the
+// per-head sums dA_log / ddt_bias over it, 10-40x further from the float64
+// reference: dg is a reverse cumulative sum of terms that cancel.)
+__device__ __forceinline__ f4 mma8(const float (&x)[8], const float (&y)[8], f4 acc) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc = mfma_f32x4(x[i], y[i], acc);
+  return acc;
+}
+template <class FA, class FB>
+__device__ __forceinline__ f4 mma_tile(f4 acc, int k0, int ksteps, int lr, int gq, FA fa, FB fb) {
+  for (int st = 0; st < ksteps; ++st) {
+    const int kb = k0 + 32 * st + 8 * gq;
+    float x[8], y[8];
+    fa(lr, kb, x);
+    fb(kb, lr, y);
+    acc = mma8(x, y, acc);
+  }
+  return acc;
+}
+
+__device__ __forceinline__ void load8f(const float *src, float (&x)[8]) {
+  const f4 a = *reinterpret_cast<const f4 *>(src), b = *reinterpret_cast<const f4 *>(src + 4);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[i] = a[i];
+    x[4 + i] = b[i];
+  }
+}
+
+constexpr int kLdG = 132;   // fp32 row strides of the gradient kernel's LDS tiles
+constexpr int kLdS = 68;
+constexpr size_t kGradLdsFloats = 2 * 64 * kLdG + 4 * 64 * kLdS + 64 + 128 + 4 * 128;
+
+// One (chunk, head) of the per-chunk gradients on 256 threads: wavefront w
+// owns output rows 16w .. 16w + 15 of every 64-row product.  The gradients
+// of q^, k^ and G of the lane's C-tile positions (rows 16w + 4gq + e,
+// channel 16nt + lr) accumulate in registers.
+__global__ __launch_bounds__(256) void kda_bwd_grad_kernel(BwdChunkArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float gsm[];
+  float *sG = gsm;                      // [64][kLdG] G (natural log), later dG
+  float *sDW = sG + 64 * kLdG;          // [64][kLdG] dW
+  float *sT = sDW + 64 * kLdG;          // [64][kLdS] T
+  float *sP = sT + 64 * kLdS;           // [64][kLdS] P, later dP
+  float *sDA = sP + 64 * kLdS;          // [64][kLdS] dA_qk
+  float *sDT = sDA + 64 * kLdS;         // [64][kLdS] dT, later dT T^T
+  float *sBt = sDT + 64 * kLdS;         // [64] beta
+  float *sDg0 = sBt + 64;               // [128] e^Gamma sum_v dS1 S0
+  float *sDgW = sDg0 + 128;             // [4][128] per-wavefront sums of dKbar Kbar
+  const ScanArgs &p = a.p;
+  const int H = p.num_heads;
+  const int h = static_cast<int>(blockIdx.x % static_cast<unsigned>(H));
+  const int cidx = static_cast<int>(blockIdx.x / static_cast<unsigned>(H));
+  if (cidx >= p.max_ch) return;
+  int s, first;
+  chunk_of(p.cu, p.n_seqs, p.total, cidx, s, first);
+  if (s >= p.n_seqs) return;
+  const int64_t seq_a = iclamp64(p.cu[s], 0, p.total);
+  const int64_t seq_b = iclamp64(p.cu[s + 1], seq_a, p.total);
+  const int64_t tok0 = seq_a + static_cast<int64_t>(cidx - first) * kC;
+  const int len = static_cast<int>(imin64(kC, seq_b - tok0));
+  const size_t it = static_cast<size_t>(cidx) * H + h;
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l = tid & 63, lr = l & 15, gq = l >> 4;
+  const int rb = 16 * w;
+  const auto tok_off = [&](int r) { return (tok0 + r) * static_cast<int64_t>(H) + h; };
+  const auto qh_at = [&](int r, int c) { return r < len ? a.qh[tok_off(r) * kD + c] : 0.f; };
+  const auto kh_at = [&](int r, int c) { return r < len ? a.kh[tok_off(r) * kD + c] : 0.f; };
+  const float *S0 = a.s0 + it * (kD * kD);
+  const float *dS1 = a.ds1 + it * (kD * kD);
+  const float *Um = a.u + it * (kC * kD);
+  const float *dUm = a.du + it * (kC * kD);
+
+  // ---- 1. G = cumulative log-decay of the chunk rows; T, P, beta
+  if (tid < kD) {
+    float acc = 0.f;
+    for (int r = 0; r < kC; ++r) {
+      acc += r < len ? a.glog[tok_off(r) * kD + tid] : 0.f;
+      sG[r * kLdG + tid] = acc;
+    }
+  } else {
+    const int t = tid - kD;
+    for (int i = t; i < kC * kC / 4; i += kD) {
+      const int r = (4 * i) / kC, c = (4 * i) % kC;
+      *reinterpret_cast<f4 *>(&sT[r * kLdS + c]) = *reinterpret_cast<const f4 *>(&a.tmat[it * (kC * kC) + 4 * i]);
+      *reinterpret_cast<f4 *>(&sP[r * kLdS + c]) = *reinterpret_cast<const f4 *>(&a.pmat[it * (kC * kC) + 4 * i]);
+    }
+    if (t < kC) sBt[t] = t < len ? a.bt[tok_off(t)] : 0.f;
+  }
+  lds_barrier();
+  const auto Gat = [&](int r, int c) { return sG[r * kLdG + c]; };
+  const auto ref = [&](int blk, int c) { return blk == 0 ? 0.f : sG[(16 * blk - 1) * kLdG + c]; };
+  {
+    // dGamma from the state: e^Gamma_c sum_v dS1[c][v] S0[c][v]
+    const int c = tid >> 1, v0 = (tid & 1) * 64;
+    float acc = 0.f;
+    for (int i = 0; i < 64; i += 4) {
+      const f4 x = *reinterpret_cast<const f4 *>(&dS1[c * kD + v0 + i]);
+      const f4 y = *reinterpret_cast<const f4 *>(&S0[c * kD + v0 + i]);
+      acc += x[0] * y[0] + x[1] * y[1] + x[2] * y[2] + x[3] * y[3];
+    }
+    acc += __shfl_xor(acc, 1, 64);
+    if ((tid & 1) == 0) sDg0[c] = acc * __expf(Gat(kC - 1, c));
+  }
+  const auto dO_rows = [&](int m, int kb, float (&x)[8]) {
+    const int r = rb + m;
+    if (r < len) {
+      const int64_t o = (tok0 + r) * a.do_stride + static_cast<int64_t>(h) * kD + kb;
+      const f4 u0 = load4(a.dout, o, a.do_dtype), u1 = load4(a.dout, o + 4, a.do_dtype);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x[i] = u0[i];
+        x[4 + i] = u1[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[i] = 0.f;
+    }
+  };
+  const f4 zero = {0.f, 0.f, 0.f, 0.f};
+  f4 aq[8], ak[8], aG[8];
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) aq[nt] = ak[nt] = aG[nt] = zero;
+  float dbr[4] = {0.f, 0.f, 0.f, 0.f};
+
+  // ---- 2. dQg = dO S0^T, dKbar = U dS1^T (into the accumulators), dW = -dU S0^T
+  for (int nt = 0; nt < 8; ++nt) {
+    const f4 dq = mma_tile(zero, 0, 4, lr, gq, dO_rows,
+                           [&](int kb, int n, float (&x)[8]) { load8f(S0 + (16 * nt + n) * kD + kb, x); });
+    const f4 dkb = mma_tile(zero, 0, 4, lr, gq, [&](int m, int kb, float (&x)[8]) { load8f(Um + (rb + m) * kD + kb, x); },
+                            [&](int kb, int n, float (&x)[8]) { load8f(dS1 + (16 * nt + n) * kD + kb, x); });
+    const f4 dw = mma_tile(zero, 0, 4, lr, gq, [&](int m, int kb, float (&x)[8]) { load8f(dUm + (rb + m) * kD + kb, x); },
+                           [&](int kb, int n, float (&x)[8]) { load8f(S0 + (16 * nt + n) * kD + kb, x); });
+    const int c = 16 * nt + lr;
+    const float gam = Gat(kC - 1, c);
+    float part = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int r = rb + 4 * gq + e;
+      const float eg = __expf(Gat(r, c));
+      aq[nt][e] = dq[e] * eg;
+      aG[nt][e] = dq[e] * qh_at(r, c) * eg;
+      const float f = __expf(gam - Gat(r, c));
+      const float kbar = kh_at(r, c) * f;
+      ak[nt][e] = dkb[e] * f;
+      aG[nt][e] -= dkb[e] * kbar;
+      part += dkb[e] * kbar;
+      sDW[r * kLdG + c] = -dw[e];
+    }
+    part += __shfl_xor(part, 16, 64);
+    part += __shfl_xor(part, 32, 64);
+    if (gq == 0) sDgW[w * kD + c] = part;
+  }
+  // ---- 3. dA_qk = tril(dO U^T)
+#pragma unroll
+  for (int ib = 0; ib < 4; ++ib) {
+    f4 acc = zero;
+    if (ib <= w)
+      acc = mma_tile(zero, 0, 4, lr, gq, dO_rows,
+                     [&](int kb, int n, float (&x)[8]) { load8f(Um + (16 * ib + n) * kD + kb, x); });
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int r = rb + 4 * gq + e, j = 16 * ib + lr;
+      sDA[r * kLdS + j] = j <= r ? acc[e] : 0.f;
+    }
+  }
+  lds_barrier();
+
+  // ---- 4. dT = dW Xw^T + dU Xu^T (strictly lower part)
+#pragma unroll
+  for (int ib = 0; ib < 4; ++ib) {
+    f4 acc = zero;
+    if (ib <= w) {
+      acc = mma_tile(acc, 0, 4, lr, gq, [&](int m, int kb, float (&x)[8]) { load8f(sDW + (rb + m) * kLdG + kb, x); },
+                     [&](int kb, int n, float (&x)[8]) {
+                       const int j = 16 * ib + n;
+#pragma unroll
+                       for (int i = 0; i < 8; ++i) x[i] = sBt[j] * kh_at(j, kb + i) * __expf(Gat(j, kb + i));
+                     });
+      acc = mma_tile(acc, 0, 4, lr, gq, [&](int m, int kb, float (&x)[8]) { load8f(dUm + (rb + m) * kD + kb, x); },
+                     [&](int kb, int n, float (&x)[8]) {
+                       const int j = 16 * ib + n;
+                       if (j < len) {
+                         const int64_t o = (tok0 + j) * a.v_stride + static_cast<int64_t>(h) * kD + kb;
+                         const f4 u0 = load4(a.v, o, a.v_dtype), u1 = load4(a.v, o + 4, a.v_dtype);
+#pragma unroll
+                         for (int i = 0; i < 4; ++i) {
+                           x[i] = sBt[j] * u0[i];
+                           x[4 + i] = sBt[j] * u1[i];
+                         }
+                       } else {
+#pragma unroll
+                         for (int i = 0; i < 8; ++i) x[i] = 0.f;
+                       }
+                     });
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int r = rb + 4 * gq + e, j = 16 * ib + lr;
+      sDT[r * kLdS + j] = j < r ? acc[e] : 0.f;
+    }
+  }
+  lds_barrier();
+
+  // ---- 5. dXw = T^T dW, dXu = T^T dU (rows j of this wavefront); dv, and
+  //         beta's terms sum_c dXw Kg + sum_v dXu v.
+  const auto tT = [&](int m, int kb, float (&x)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = sT[(kb + i) * kLdS + rb + m];
+  };
+  for (int nt = 0; nt < 8; ++nt) {
+    const f4 dxw = mma_tile(zero, 0, 2, lr, gq, tT, [&](int kb, int n, float (&x)[8]) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[i] = sDW[(kb + i) * kLdG + 16 * nt + n];
+    });
+    const f4 dxu = mma_tile(zero, 0, 2, lr, gq, tT, [&](int kb, int n, float (&x)[8]) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[i] = dUm[(kb + i) * kD + 16 * nt + n];
+    });
+    const int c = 16 * nt + lr;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int r = rb + 4 * gq + e;
+      const float eg = __expf(Gat(r, c));
+      const float kg = kh_at(r, c) * eg;
+      const float bt = sBt[r];
+      ak[nt][e] += bt * dxw[e] * eg;
+      aG[nt][e] += bt * dxw[e] * kg;
+      dbr[e] += dxw[e] * kg;
+      if (r < len) {
+        const int64_t o = tok_off(r) * kD + c;
+        a.dv[o] = bt * dxu[e];
+        dbr[e] += dxu[e] * load_elem(a.v, (tok0 + r) * a.v_stride + static_cast<int64_t>(h) * kD + c, a.v_dtype);
+      }
+    }
+  }
+
+  // ---- 6. dA_kk = tril_strict(-T^T (dT T^T)); beta's term sum_j dA_kk P; dP = beta dA_kk
+  {
+    f4 xt[4];
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) {
+      xt[ib] = zero;
+      if (ib <= w)
+        xt[ib] = mma_tile(zero, 0, 2, lr, gq, [&](int m, int kb, float (&x)[8]) { load8f(sDT + (rb + m) * kLdS + kb, x); },
+                          [&](int kb, int n, float (&x)[8]) { load8f(sT + (16 * ib + n) * kLdS + kb, x); });
+    }
+    lds_barrier();  // dT is read
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sDT[(rb + 4 * gq + e) * kLdS + 16 * ib + lr] = xt[ib][e];
+    lds_barrier();
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) {
+      f4 acc = zero;
+      if (ib <= w)
+        acc = mma_tile(zero, 0, 2, lr, gq, tT, [&](int kb, int n, float (&x)[8]) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) x[i] = sDT[(kb + i) * kLdS + 16 * ib + n];
+        });
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = rb + 4 * gq + e, j = 16 * ib + lr;
+        const float dA = j < r ? -acc[e] : 0.f;
+        dbr[e] += dA * sP[r * kLdS + j];
+        sP[r * kLdS + j] = sBt[r] * dA;
+      }
+    }
+  }
+  lds_barrier();
+
+  // ---- 7. the products through A_qk and P with the sub-block factors: for
+  //         rows r of block w, e^{G_r - G_j} = e^{G_r - ref_w} e^{ref_w - G_j}
+  //         (the first <= 1, the second <= 1 for j before block w and <= e^80
+  //         inside it); for key rows j of block w and r >= 16w,
+  //         e^{G_r - G_j} = e^{G_r - ref_w} e^{ref_w - G_j} as well.
+  {
+    const int kq = (16 * (w + 1) + 31) / 32;
+    const int jmax = 16 * (w + 1);
+    const int ks0 = (16 * w) / 32;
+    for (int nt = 0; nt < 8; ++nt) {
+      const int c = 16 * nt + lr;
+      f4 c1 = zero, c2 = zero, c3 = zero, c4 = zero;
+      for (int st = 0; st < kq; ++st) {
+        const int kb = 32 * st + 8 * gq;
+        float xa[8], xp[8], y[8];
+        load8f(sDA + (rb + lr) * kLdS + kb, xa);
+        load8f(sP + (rb + lr) * kLdS + kb, xp);
+        const float rw = ref(w, c);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int j = kb + i;
+          y[i] = j < jmax ? kh_at(j, c) * __expf(rw - Gat(j, c)) : 0.f;
+        }
+        c1 = mma8(xa, y, c1);
+        c2 = mma8(xp, y, c2);
+      }
+      for (int st = ks0; st < 2; ++st) {
+        const int kb = 32 * st + 8 * gq;
+        float xa[8], xp[8], yq[8], yk[8];
+        const float rw = ref(w, c);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int r = kb + i;
+          xa[i] = sDA[r * kLdS + rb + lr];
+          xp[i] = sP[r * kLdS + rb + lr];
+          const float f = r >= 16 * w ? __expf(Gat(r, c) - rw) : 0.f;
+          yq[i] = qh_at(r, c) * f;
+          yk[i] = kh_at(r, c) * f;
+        }
+        c3 = mma8(xa, yq, c3);
+        c4 = mma8(xp, yk, c4);
+      }
+      const float rw = ref(w, c);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = rb + 4 * gq + e;
+        const float af = __expf(Gat(r, c) - rw);
+        const float bq = __expf(rw - Gat(r, c));
+        const float dqp = af * c1[e], dkgp = af * c2[e], dkr = bq * (c3[e] + c4[e]);
+        const float qv = qh_at(r, c), kv = kh_at(r, c);
+        aq[nt][e] += dqp;
+        ak[nt][e] += dkgp + dkr;
+        aG[nt][e] += qv * dqp + kv * dkgp - kv * dkr;
+      }
+    }
+  }
+
+  // ---- 8. outputs: dq^, dk^, dbeta; dg = reverse cumulative sum of dG + dGamma
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int r = rb + 4 * gq + e, c = 16 * nt + lr;
+      if (r < len) {
+        a.dqh[tok_off(r) * kD + c] = aq[nt][e];
+        a.dkh[tok_off(r) * kD + c] = ak[nt][e];
+      }
+    }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float x = dbr[e];
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) x += __shfl_xor(x, off, 64);
+    const int r = rb + 4 * gq + e;
+    if (lr == 0 && r < len) a.dbp[tok_off(r)] = x;
+  }
+  // sG (every read of G is done once all wavefronts pass this barrier) takes dG.
+  lds_barrier();
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sG[(rb + 4 * gq + e) * kLdG + 16 * nt + lr] = aG[nt][e];
+  lds_barrier();
+  if (tid < kD) {
+    const float dgam = sDg0[tid] + ((sDgW[tid] + sDgW[kD + tid]) + (sDgW[2 * kD + tid] + sDgW[3 * kD + tid]));
+    float acc = 0.f;
+    for (int r = kC - 1; r >= 0; --r) {
+      acc += sG[r * kLdG + tid];
+      if (r < len) a.dgl[tok_off(r) * kD + tid] = acc + dgam;
+    }
+  }
+}
+
 // Upper bound on the segments of any batch of total_tokens tokens: only a
 // sequence of at least 2 kSegChunks chunks is segmented, so the segments
 // number at most 1.5 (1 + 1 / (2 kSegChunks - 1)) total / (64 kSegChunks).
@@ -1483,22 +2239,31 @@ ScanPlan plan_scan(const int32_t *cu_host, int n_seqs, int num_heads, int cus) {
 // Dynamic LDS above the default limit is enabled once per (kernel, device),
 // under a lock: launches may come from several host threads and devices.
 constexpr int kMaxDevices = 64;
-template <int QKV_DT, int G_DT, bool GATE>
-int ensure_intra_lds() {
+// Sets a kernel's dynamic LDS limit once per device (KEY names the kernel).
+template <class KEY>
+int ensure_lds(const void *fn, size_t bytes) {
   static std::mutex mu;
   static bool done[kMaxDevices] = {};
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess)
-    return set_error(SOPHIA_ERR_HIP, "kda_chunk_fwd: hipGetDevice: %s", hipGetErrorString(e));
+    return set_error(SOPHIA_ERR_HIP, "kda_chunk: hipGetDevice: %s", hipGetErrorString(e));
   std::lock_guard<std::mutex> lock(mu);
   if (dev >= 0 && dev < kMaxDevices && done[dev]) return SOPHIA_OK;
-  e = hipFuncSetAttribute(reinterpret_cast<const void *>(&kda_chunk_intra_kernel<QKV_DT, G_DT, GATE>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kSmIntra));
+  e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
   if (e != hipSuccess)
-    return set_error(SOPHIA_ERR_HIP, "kda_chunk_fwd: cannot set LDS size: %s", hipGetErrorString(e));
+    return set_error(SOPHIA_ERR_HIP, "kda_chunk: cannot set LDS size: %s", hipGetErrorString(e));
   if (dev >= 0 && dev < kMaxDevices) done[dev] = true;
   return SOPHIA_OK;
+}
+template <int QKV_DT, int G_DT, bool GATE, bool BWD>
+struct IntraKey {};
+struct GradKey {};
+
+template <int QKV_DT, int G_DT, bool GATE>
+int ensure_intra_lds() {
+  return ensure_lds<IntraKey<QKV_DT, G_DT, GATE, false>>(
+      reinterpret_cast<const void *>(&kda_chunk_intra_kernel<QKV_DT, G_DT, GATE>), kSmIntra);
 }
 
 template <int QKV_DT, int G_DT, bool GATE>
@@ -1508,12 +2273,113 @@ int launch_intra(dim3 grid, hipStream_t st, const IntraArgs &ia) {
   return check_launch("kda_chunk_intra");
 }
 
+template <int QKV_DT, int G_DT, bool GATE>
+int launch_intra_bwd(dim3 grid, hipStream_t st, const IntraArgs &ia) {
+  if (const int rc = ensure_lds<IntraKey<QKV_DT, G_DT, GATE, true>>(
+          reinterpret_cast<const void *>(&kda_chunk_intra_bwd_kernel<QKV_DT, G_DT, GATE>), kSmIntraBwd))
+    return rc;
+  hipLaunchKernelGGL((kda_chunk_intra_bwd_kernel<QKV_DT, G_DT, GATE>), grid, dim3(kThreads), kSmIntraBwd, st, ia);
+  return check_launch("kda_chunk_intra_bwd");
+}
+
 template <int O_DT>
 void launch_scan(dim3 grid, hipStream_t st, const ScanArgs &sa) {
   hipLaunchKernelGGL((kda_chunk_scan_kernel<O_DT>), grid, dim3(kScanThreads), 0, st, sa);
 }
 
+inline size_t align256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
+
 }  // namespace
+
+// Scratch of the chunk-form backward, per (chunk, head): the forward and the
+// backward record, T and P, S0 and dS1, U and dU.
+size_t chunk_bwd_scratch_bytes(int64_t total_tokens, int n_seqs, int num_heads) {
+  const size_t items = static_cast<size_t>(max_chunks(total_tokens, n_seqs)) * num_heads;
+  return align256(kTrashBytes) + align256(items * kRecBytes) + align256(items * kBwdRecBytes) +
+         2 * align256(items * kC * kC * 4) + 2 * align256(items * kD * kD * 4) + 2 * align256(items * kC * kD * 4);
+}
+
+int chunk_bwd_run(const ChunkBwdIO &io, void *scratch, hipStream_t st) {
+  const int H = io.num_heads;
+  const int64_t max_ch = max_chunks(io.total, io.n_seqs);
+  if (max_ch <= 0) return SOPHIA_OK;
+  SOPHIA_REQUIRE(max_ch * H <= 0x7fffffff, "kda_chunk_bwd: grid too large");
+  const size_t items = static_cast<size_t>(max_ch) * H;
+  uint8_t *w = static_cast<uint8_t *>(scratch);
+  const auto carve = [&w](size_t bytes) {
+    uint8_t *p = w;
+    w += align256(bytes);
+    return p;
+  };
+  void *trash = carve(kTrashBytes);
+  uint8_t *records = carve(items * kRecBytes);
+  uint8_t *brec = carve(items * kBwdRecBytes);
+  float *tmat = reinterpret_cast<float *>(carve(items * kC * kC * 4));
+  float *pmat = reinterpret_cast<float *>(carve(items * kC * kC * 4));
+  float *s0 = reinterpret_cast<float *>(carve(items * kD * kD * 4));
+  float *ds1 = reinterpret_cast<float *>(carve(items * kD * kD * 4));
+  float *u = reinterpret_cast<float *>(carve(items * kC * kD * 4));
+  float *du = reinterpret_cast<float *>(carve(items * kC * kD * 4));
+
+  // 1. records (forward and backward), T and P
+  if (io.total > 0) {
+    const auto a16 = [](const void *ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; };
+    const int lines = io.qkv_dtype == SOPHIA_DTYPE_BF16 && io.qkv_stride % 8 == 0 && a16(io.q) && a16(io.k) &&
+                      a16(io.v);
+    IntraArgs ia{io.q, io.k, io.v, io.qkv_stride, io.qkv_dtype, io.g, io.g_stride, io.g_dtype, io.beta,
+                 io.beta_stride, io.beta_dtype, io.A_log, io.dt_bias, io.scale, io.lb, io.flags,
+                 io.cu, io.n_seqs, io.total, H, max_ch, records, lines,
+                 brec, tmat, pmat, io.dout, io.do_stride, io.do_dtype};
+    const dim3 grid(static_cast<unsigned>(items));
+    const bool gate = (io.flags & SOPHIA_KDA_GATE_IN_KERNEL) != 0;
+    const int key = (io.qkv_dtype == SOPHIA_DTYPE_BF16) * 4 + (io.g_dtype == SOPHIA_DTYPE_BF16) * 2 + gate;
+    constexpr int F = SOPHIA_DTYPE_F32, B = SOPHIA_DTYPE_BF16;
+    int rc = SOPHIA_OK;
+    switch (key) {
+      case 0: rc = launch_intra_bwd<F, F, false>(grid, st, ia); break;
+      case 1: rc = launch_intra_bwd<F, F, true>(grid, st, ia); break;
+      case 2: rc = launch_intra_bwd<F, B, false>(grid, st, ia); break;
+      case 3: rc = launch_intra_bwd<F, B, true>(grid, st, ia); break;
+      case 4: rc = launch_intra_bwd<B, F, false>(grid, st, ia); break;
+      case 5: rc = launch_intra_bwd<B, F, true>(grid, st, ia); break;
+      case 6: rc = launch_intra_bwd<B, B, false>(grid, st, ia); break;
+      default: rc = launch_intra_bwd<B, B, true>(grid, st, ia); break;
+    }
+    if (rc) return rc;
+  }
+  // 2-3. forward states and the reverse scan: `splits` slices of the value
+  // columns per (sequence, head), as many as keep every work-group resident.
+  int device = 0, cus = 256;
+  if (hipGetDevice(&device) == hipSuccess)
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) cus = 256;
+  const int64_t pairs = static_cast<int64_t>(io.n_seqs) * H;
+  // (at least 2: a 128-column slice does not fit these kernels' registers)
+  int splits = 2;
+  while (splits < 8 && pairs * splits * 2 <= cus) splits *= 2;
+  const int64_t sblocks = (pairs + 7) / 8 * 8 * splits;
+  SOPHIA_REQUIRE(sblocks <= 0x7fffffff, "kda_chunk_bwd: grid too large");
+  BwdChunkArgs a{};
+  a.p = ScanArgs{io.cu, io.n_seqs, io.total, H, max_ch, records, io.h0, nullptr, io.n_seqs, nullptr, nullptr, 0,
+                 trash, 0xfedcba9876543210ull, 1, 0, 0, 0, 0, 0, 0, 0, 0, 0, 1, 1, 1, 1};
+  a.brec = brec; a.tmat = tmat; a.pmat = pmat;
+  a.s0 = s0; a.u = u; a.ds1 = ds1; a.du = du;
+  a.dht = io.dht; a.dh0 = io.dh0; a.splits = splits;
+  a.qh = io.qh; a.kh = io.kh; a.glog = io.glog; a.bt = io.bt;
+  a.v = io.v; a.v_stride = io.qkv_stride; a.v_dtype = io.qkv_dtype;
+  a.dout = io.dout; a.do_stride = io.do_stride; a.do_dtype = io.do_dtype;
+  a.dqh = io.dqh; a.dkh = io.dkh; a.dgl = io.dgl; a.dbp = io.dbp; a.dv = io.dv;
+  hipLaunchKernelGGL(kda_bwd_states_kernel, dim3(static_cast<unsigned>(sblocks)), dim3(kScanThreads), 0, st, a);
+  if (const int rc = check_launch("kda_bwd_states")) return rc;
+  hipLaunchKernelGGL(kda_bwd_rscan_kernel, dim3(static_cast<unsigned>(sblocks)), dim3(kScanThreads), 0, st, a);
+  if (const int rc = check_launch("kda_bwd_rscan")) return rc;
+  // 4. per-chunk gradients
+  if (io.total == 0) return SOPHIA_OK;
+  const size_t glds = kGradLdsFloats * sizeof(float);
+  if (const int rc = ensure_lds<GradKey>(reinterpret_cast<const void *>(&kda_bwd_grad_kernel), glds)) return rc;
+  hipLaunchKernelGGL(kda_bwd_grad_kernel, dim3(static_cast<unsigned>(items)), dim3(256), glds, st, a);
+  return check_launch("kda_bwd_grad");
+}
+
 }  // namespace sophia
 
 using namespace sophia;

@@ -288,7 +288,7 @@ def kda_chunk_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
                   lower_bound: float = -5.0, use_qk_l2norm: bool = True, use_gate: bool = True,
                   use_beta_sigmoid: bool = True, initial_state: torch.Tensor | None = None,
                   d_final_state: torch.Tensor | None = None,
-                  cu_seqlens_cpu: torch.Tensor | None = None):
+                  cu_seqlens_cpu: torch.Tensor | None = None, recurrent: bool = False):
     """Gradients of ``kda_chunk_fwd`` (no cache slots: one state per sequence).
 
     The HIP counterpart of FlashKDA's chunk_kda_train_bwd plus l2norm_bwd and
@@ -298,7 +298,9 @@ def kda_chunk_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
     dA_log, ddt_bias): dg with respect to the g input as passed, dh0
     [N, H, 128, 128], dA_log [H] and ddt_bias [H * 128] (empty without the
     in-kernel gate).  A host ``cu_seqlens`` (or ``cu_seqlens_cpu``) is checked
-    to rise from 0 to the token count.
+    to rise from 0 to the token count.  The chunk form runs by default (bf16
+    MFMA operands, fp32 accumulation and state, the forward's arithmetic);
+    ``recurrent=True`` runs the per-token recurrence in fp32 instead.
     """
     for t, name in ((q, "q"), (k, "k"), (v, "v"), (g, "g"), (beta, "beta"), (d_out, "d_out")):
         _gpu(t, name)
@@ -353,7 +355,8 @@ def kda_chunk_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
         nat.ptr(q), nat.ptr(k), nat.ptr(v), qs, nat.dtype_code(q.dtype), nat.ptr(g), gs,
         nat.dtype_code(g.dtype), nat.ptr(beta), bs, nat.dtype_code(beta.dtype), nat.ptr(a_log),
         nat.ptr(dtb), float(scale), float(lower_bound),
-        _flags(use_qk_l2norm, use_gate, use_beta_sigmoid), nat.ptr(cu), n, total, heads, HEAD_DIM,
+        _flags(use_qk_l2norm, use_gate, use_beta_sigmoid) | (nat.BWD_RECURRENT if recurrent else 0),
+        nat.ptr(cu), n, total, heads, HEAD_DIM,
         nat.ptr(initial_state), nat.ptr(d_out), ds, nat.dtype_code(d_out.dtype),
         nat.ptr(d_final_state), nat.ptr(dq), nat.ptr(dk), nat.ptr(dv), nat.ptr(dg),
         nat.ptr(dbeta), nat.ptr(dh0), nat.ptr(da) if use_gate else None,

@@ -195,7 +195,9 @@ def test_chunk_kda_allow_neg_eigval_matches_oracle():
                             use_qk_l2norm=True, use_gate=False, use_beta_sigmoid=False)
     s = beta_eff / 2.0
     db_ref = ref["dbeta"] * 2.0 * s * (1.0 - s)
-    assert _rel(_np(b.grad)[0], db_ref) < 1e-4
+    # the autograd path runs the chunk form of the backward (bf16 MFMA
+    # operands in its chunk scans): the bound of test_gpu_kda_bwd's chunk tests
+    assert _rel(_np(b.grad)[0], db_ref) < 1.5e-2
 
 
 def test_chunk_kda_state_v_first_is_the_transposed_state():
