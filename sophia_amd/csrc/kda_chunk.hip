@@ -1740,10 +1740,6 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_rscan_kernel(BwdChunkArg
   }
 }
 
-// 16 x 16 C tile (+)= A (16 x 32 ks) B (32 ks x 16) over the K-steps k0,
-// k0 + 32, .. (mma8): fa(m, kb, x) fills x[i] = A[m][kb + i] and
-// fb(kb, n, x) fills x[i] = B[kb + i][n] for the lane's m = n = lr and
-// kb = k0 + 32 s + 8 gq (the operand layout of v_mfma_f32_16x16x32_bf16).
 // acc += x . y over the lane group's 8 k values (x[i] = A[m][kb + i],
 // y[i] = B[kb + i][n]) on fp32 MFMA: eight 16x16x4 steps, the k slot of lane
 // group g in step i being 8 g + i.  (bf16 operands here leave dg, and the
@@ -1752,17 +1748,6 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_rscan_kernel(BwdChunkArg
 __device__ __forceinline__ f4 mma8(const float (&x)[8], const float (&y)[8], f4 acc) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc = mfma_f32x4(x[i], y[i], acc);
-  return acc;
-}
-template <class FA, class FB>
-__device__ __forceinline__ f4 mma_tile(f4 acc, int k0, int ksteps, int lr, int gq, FA fa, FB fb) {
-  for (int st = 0; st < ksteps; ++st) {
-    const int kb = k0 + 32 * st + 8 * gq;
-    float x[8], y[8];
-    fa(lr, kb, x);
-    fb(kb, lr, y);
-    acc = mma8(x, y, acc);
-  }
   return acc;
 }
 
@@ -1777,23 +1762,47 @@ __device__ __forceinline__ void load8f(const float *src, float (&x)[8]) {
 
 constexpr int kLdG = 132;   // fp32 row strides of the gradient kernel's LDS tiles
 constexpr int kLdS = 68;
-constexpr size_t kGradLdsFloats = 2 * 64 * kLdG + 4 * 64 * kLdS + 64 + 128 + 4 * 128;
+constexpr int kLdQ = 18;    // q^ column block: rows 8 apart land 16 banks apart
+constexpr int kGradThreads = 512;
+constexpr size_t kGradLdsFloats =
+    3 * 64 * kLdG + 2 * 64 * kLdS + 2 * 16 * kLdG + 64 * kLdQ + 64 + 128 + 4 * 128 + 2 * 64;
 
-// One (chunk, head) of the per-chunk gradients on 256 threads: wavefront w
-// owns output rows 16w .. 16w + 15 of every 64-row product.  The gradients
-// of q^, k^ and G of the lane's C-tile positions (rows 16w + 4gq + e,
-// channel 16nt + lr) accumulate in registers.
-__global__ __launch_bounds__(256) void kda_bwd_grad_kernel(BwdChunkArgs a) {
+// One (chunk, head) of the per-chunk gradients on 512 threads: wavefronts w
+// and w + 4 (one pair per SIMD) share the chunk rows 16w .. 16w + 15 of every
+// product whose rows are chunk rows.
+//
+// Since U = T (Xu - Xw S0), the gradient of T, dT = dW Xw^T + dU Xu^T with
+// dW = -dU S0^T, equals dU (T^{-1} U)^T, so that
+//   dA_kk = tril_strict(-T^T dT T^T) = tril_strict(-T^T tril_strict(dU U^T)),
+//   dXw = T^T dW = -dXu S0^T with dXu = T^T dU:
+// neither dW nor dT is formed.
+//
+// LDS holds G, k^ and dU (then dXu, then phase II's exchange) as [64][128]
+// tiles and two [64][64] tiles that each keep a lower-triangular matrix in
+// place and a strictly lower one transposed into the upper triangle: T with
+// P (later dP), and dA_qk with dU U^T.  Step 2 gives the pair the key blocks
+// of dA_qk and dU U^T by parity; step 3 the column blocks of dXu.  Phase II
+// walks the 16-channel column blocks with the pair in two roles: the state
+// wavefront (u = 0) forms dQg = dO S0^T and dXw = -dXu S0^T of block i from
+// one pass over 16 rows of S0, while the chunk wavefront (u = 1) forms
+// dKbar = U dS1^T and the products through A_qk and P of block i and
+// finishes block i - 1 (dq^, dk^, dG into G's dead columns) from the state
+// wavefront's results.  The state matrices stream through a [32][128] block
+// prefetched into registers one block ahead; every tile issues the loads of
+// all its K-steps before its first product.
+__global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs a) {
   extern __shared__ __attribute__((aligned(16))) float gsm[];
-  float *sG = gsm;                      // [64][kLdG] G (natural log), later dG
-  float *sDW = sG + 64 * kLdG;          // [64][kLdG] dW
-  float *sT = sDW + 64 * kLdG;          // [64][kLdS] T
-  float *sP = sT + 64 * kLdS;           // [64][kLdS] P, later dP
-  float *sDA = sP + 64 * kLdS;          // [64][kLdS] dA_qk
-  float *sDT = sDA + 64 * kLdS;         // [64][kLdS] dT, later dT T^T
-  float *sBt = sDT + 64 * kLdS;         // [64] beta
-  float *sDg0 = sBt + 64;               // [128] e^Gamma sum_v dS1 S0
-  float *sDgW = sDg0 + 128;             // [4][128] per-wavefront sums of dKbar Kbar
+  float *sG = gsm;                  // [64][kLdG] G (natural log); dG column blocks as phase II ends them
+  float *sKh = sG + 64 * kLdG;      // [64][kLdG] k^
+  float *sDX = sKh + 64 * kLdG;     // [64][kLdG] dU, then dXu; phase II [2][4][64][8] exchange
+  float *sTP = sDX + 64 * kLdG;     // [64][kLdS] T[r][j] (j <= r) at [r][j]; P / dP [r][j] (j < r) at [j][r]
+  float *sAT = sTP + 64 * kLdS;     // [64][kLdS] dA_qk (j <= r) at [r][j]; (dU U^T)[r][j] (j < r) at [j][r]
+  float *sSl = sAT + 64 * kLdS;     // [32][kLdG] rows 16i .. of S0 (0..15) and dS1 (16..31)
+  float *sQb = sSl + 2 * 16 * kLdG; // [64][kLdQ] q^ columns 16i .. 16i + 15
+  float *sBt = sQb + 64 * kLdQ;     // [64] beta
+  float *sDg0 = sBt + 64;           // [128] e^Gamma sum_v dS1 S0
+  float *sDgW = sDg0 + 128;         // [4][128] per-row-block sums of dKbar Kbar
+  float *sDb = sDgW + 4 * 128;      // [2][64] dbeta of each wavefront of a pair
   const ScanArgs &p = a.p;
   const int H = p.num_heads;
   const int h = static_cast<int>(blockIdx.x % static_cast<unsigned>(H));
@@ -1808,306 +1817,428 @@ __global__ __launch_bounds__(256) void kda_bwd_grad_kernel(BwdChunkArgs a) {
   const int len = static_cast<int>(imin64(kC, seq_b - tok0));
   const size_t it = static_cast<size_t>(cidx) * H + h;
   const int tid = threadIdx.x;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int w = wave & 3, u = wave >> 2;
   const int l = tid & 63, lr = l & 15, gq = l >> 4;
   const int rb = 16 * w;
+  const int st0 = w >> 1;   // T^T[m][k] = T[k][m] vanishes for k < m: row blocks 2, 3 skip K-step 0
   const auto tok_off = [&](int r) { return (tok0 + r) * static_cast<int64_t>(H) + h; };
-  const auto qh_at = [&](int r, int c) { return r < len ? a.qh[tok_off(r) * kD + c] : 0.f; };
-  const auto kh_at = [&](int r, int c) { return r < len ? a.kh[tok_off(r) * kD + c] : 0.f; };
+  const int64_t vrow = static_cast<int64_t>(h) * kD;
   const float *S0 = a.s0 + it * (kD * kD);
   const float *dS1 = a.ds1 + it * (kD * kD);
   const float *Um = a.u + it * (kC * kD);
   const float *dUm = a.du + it * (kC * kD);
-
-  // ---- 1. G = cumulative log-decay of the chunk rows; T, P, beta
-  if (tid < kD) {
-    float acc = 0.f;
-    for (int r = 0; r < kC; ++r) {
-      acc += r < len ? a.glog[tok_off(r) * kD + tid] : 0.f;
-      sG[r * kLdG + tid] = acc;
-    }
-  } else {
-    const int t = tid - kD;
-    for (int i = t; i < kC * kC / 4; i += kD) {
-      const int r = (4 * i) / kC, c = (4 * i) % kC;
-      *reinterpret_cast<f4 *>(&sT[r * kLdS + c]) = *reinterpret_cast<const f4 *>(&a.tmat[it * (kC * kC) + 4 * i]);
-      *reinterpret_cast<f4 *>(&sP[r * kLdS + c]) = *reinterpret_cast<const f4 *>(&a.pmat[it * (kC * kC) + 4 * i]);
-    }
-    if (t < kC) sBt[t] = t < len ? a.bt[tok_off(t)] : 0.f;
-  }
-  lds_barrier();
+  const f4 z4 = {0.f, 0.f, 0.f, 0.f};
   const auto Gat = [&](int r, int c) { return sG[r * kLdG + c]; };
-  const auto ref = [&](int blk, int c) { return blk == 0 ? 0.f : sG[(16 * blk - 1) * kLdG + c]; };
-  {
-    // dGamma from the state: e^Gamma_c sum_v dS1[c][v] S0[c][v]
-    const int c = tid >> 1, v0 = (tid & 1) * 64;
-    float acc = 0.f;
-    for (int i = 0; i < 64; i += 4) {
-      const f4 x = *reinterpret_cast<const f4 *>(&dS1[c * kD + v0 + i]);
-      const f4 y = *reinterpret_cast<const f4 *>(&S0[c * kD + v0 + i]);
-      acc += x[0] * y[0] + x[1] * y[1] + x[2] * y[2] + x[3] * y[3];
-    }
-    acc += __shfl_xor(acc, 1, 64);
-    if ((tid & 1) == 0) sDg0[c] = acc * __expf(Gat(kC - 1, c));
-  }
-  const auto dO_rows = [&](int m, int kb, float (&x)[8]) {
-    const int r = rb + m;
+  const auto Kat = [&](int r, int c) { return sKh[r * kLdG + c]; };
+  // Thread tid's share of a 32-row block of a [.][128] matrix: rows (tid >> 5)
+  // and (tid >> 5) + 16, columns 4 (tid & 31) .. + 3.
+  const int blk_r = tid >> 5, blk_c = 4 * (tid & 31);
+
+  // ---- 1. log-decay, k^ and dU rows (zero past len), T and P, beta; the dO
+  //         rows of this row block; the U rows of the first key block
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = blk_r + 16 * q;
+    f4 gv = z4, kv = z4, dv = z4;
     if (r < len) {
-      const int64_t o = (tok0 + r) * a.do_stride + static_cast<int64_t>(h) * kD + kb;
-      const f4 u0 = load4(a.dout, o, a.do_dtype), u1 = load4(a.dout, o + 4, a.do_dtype);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        x[i] = u0[i];
-        x[4 + i] = u1[i];
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) x[i] = 0.f;
+      gv = *reinterpret_cast<const f4 *>(&a.glog[tok_off(r) * kD + blk_c]);
+      kv = *reinterpret_cast<const f4 *>(&a.kh[tok_off(r) * kD + blk_c]);
+      dv = *reinterpret_cast<const f4 *>(&dUm[r * kD + blk_c]);
     }
-  };
-  const f4 zero = {0.f, 0.f, 0.f, 0.f};
-  f4 aq[8], ak[8], aG[8];
-#pragma unroll
-  for (int nt = 0; nt < 8; ++nt) aq[nt] = ak[nt] = aG[nt] = zero;
-  float dbr[4] = {0.f, 0.f, 0.f, 0.f};
-
-  // ---- 2. dQg = dO S0^T, dKbar = U dS1^T (into the accumulators), dW = -dU S0^T
-  for (int nt = 0; nt < 8; ++nt) {
-    const f4 dq = mma_tile(zero, 0, 4, lr, gq, dO_rows,
-                           [&](int kb, int n, float (&x)[8]) { load8f(S0 + (16 * nt + n) * kD + kb, x); });
-    const f4 dkb = mma_tile(zero, 0, 4, lr, gq, [&](int m, int kb, float (&x)[8]) { load8f(Um + (rb + m) * kD + kb, x); },
-                            [&](int kb, int n, float (&x)[8]) { load8f(dS1 + (16 * nt + n) * kD + kb, x); });
-    const f4 dw = mma_tile(zero, 0, 4, lr, gq, [&](int m, int kb, float (&x)[8]) { load8f(dUm + (rb + m) * kD + kb, x); },
-                           [&](int kb, int n, float (&x)[8]) { load8f(S0 + (16 * nt + n) * kD + kb, x); });
-    const int c = 16 * nt + lr;
-    const float gam = Gat(kC - 1, c);
-    float part = 0.f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int r = rb + 4 * gq + e;
-      const float eg = __expf(Gat(r, c));
-      aq[nt][e] = dq[e] * eg;
-      aG[nt][e] = dq[e] * qh_at(r, c) * eg;
-      const float f = __expf(gam - Gat(r, c));
-      const float kbar = kh_at(r, c) * f;
-      ak[nt][e] = dkb[e] * f;
-      aG[nt][e] -= dkb[e] * kbar;
-      part += dkb[e] * kbar;
-      sDW[r * kLdG + c] = -dw[e];
-    }
-    part += __shfl_xor(part, 16, 64);
-    part += __shfl_xor(part, 32, 64);
-    if (gq == 0) sDgW[w * kD + c] = part;
+    *reinterpret_cast<f4 *>(&sG[r * kLdG + blk_c]) = gv;
+    *reinterpret_cast<f4 *>(&sKh[r * kLdG + blk_c]) = kv;
+    *reinterpret_cast<f4 *>(&sDX[r * kLdG + blk_c]) = dv;
   }
-  // ---- 3. dA_qk = tril(dO U^T)
-#pragma unroll
-  for (int ib = 0; ib < 4; ++ib) {
-    f4 acc = zero;
-    if (ib <= w)
-      acc = mma_tile(zero, 0, 4, lr, gq, dO_rows,
-                     [&](int kb, int n, float (&x)[8]) { load8f(Um + (16 * ib + n) * kD + kb, x); });
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int r = rb + 4 * gq + e, j = 16 * ib + lr;
-      sDA[r * kLdS + j] = j <= r ? acc[e] : 0.f;
-    }
-  }
-  lds_barrier();
-
-  // ---- 4. dT = dW Xw^T + dU Xu^T (strictly lower part)
-#pragma unroll
-  for (int ib = 0; ib < 4; ++ib) {
-    f4 acc = zero;
-    if (ib <= w) {
-      acc = mma_tile(acc, 0, 4, lr, gq, [&](int m, int kb, float (&x)[8]) { load8f(sDW + (rb + m) * kLdG + kb, x); },
-                     [&](int kb, int n, float (&x)[8]) {
-                       const int j = 16 * ib + n;
-#pragma unroll
-                       for (int i = 0; i < 8; ++i) x[i] = sBt[j] * kh_at(j, kb + i) * __expf(Gat(j, kb + i));
-                     });
-      acc = mma_tile(acc, 0, 4, lr, gq, [&](int m, int kb, float (&x)[8]) { load8f(dUm + (rb + m) * kD + kb, x); },
-                     [&](int kb, int n, float (&x)[8]) {
-                       const int j = 16 * ib + n;
-                       if (j < len) {
-                         const int64_t o = (tok0 + j) * a.v_stride + static_cast<int64_t>(h) * kD + kb;
-                         const f4 u0 = load4(a.v, o, a.v_dtype), u1 = load4(a.v, o + 4, a.v_dtype);
-#pragma unroll
-                         for (int i = 0; i < 4; ++i) {
-                           x[i] = sBt[j] * u0[i];
-                           x[4 + i] = sBt[j] * u1[i];
-                         }
-                       } else {
-#pragma unroll
-                         for (int i = 0; i < 8; ++i) x[i] = 0.f;
-                       }
-                     });
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int r = rb + 4 * gq + e, j = 16 * ib + lr;
-      sDT[r * kLdS + j] = j < r ? acc[e] : 0.f;
-    }
-  }
-  lds_barrier();
-
-  // ---- 5. dXw = T^T dW, dXu = T^T dU (rows j of this wavefront); dv, and
-  //         beta's terms sum_c dXw Kg + sum_v dXu v.
-  const auto tT = [&](int m, int kb, float (&x)[8]) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) x[i] = sT[(kb + i) * kLdS + rb + m];
-  };
-  for (int nt = 0; nt < 8; ++nt) {
-    const f4 dxw = mma_tile(zero, 0, 2, lr, gq, tT, [&](int kb, int n, float (&x)[8]) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) x[i] = sDW[(kb + i) * kLdG + 16 * nt + n];
-    });
-    const f4 dxu = mma_tile(zero, 0, 2, lr, gq, tT, [&](int kb, int n, float (&x)[8]) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) x[i] = dUm[(kb + i) * kD + 16 * nt + n];
-    });
-    const int c = 16 * nt + lr;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int r = rb + 4 * gq + e;
-      const float eg = __expf(Gat(r, c));
-      const float kg = kh_at(r, c) * eg;
-      const float bt = sBt[r];
-      ak[nt][e] += bt * dxw[e] * eg;
-      aG[nt][e] += bt * dxw[e] * kg;
-      dbr[e] += dxw[e] * kg;
-      if (r < len) {
-        const int64_t o = tok_off(r) * kD + c;
-        a.dv[o] = bt * dxu[e];
-        dbr[e] += dxu[e] * load_elem(a.v, (tok0 + r) * a.v_stride + static_cast<int64_t>(h) * kD + c, a.v_dtype);
-      }
-    }
-  }
-
-  // ---- 6. dA_kk = tril_strict(-T^T (dT T^T)); beta's term sum_j dA_kk P; dP = beta dA_kk
   {
-    f4 xt[4];
+    const float *tm = a.tmat + it * (kC * kC), *pm = a.pmat + it * (kC * kC);
 #pragma unroll
-    for (int ib = 0; ib < 4; ++ib) {
-      xt[ib] = zero;
-      if (ib <= w)
-        xt[ib] = mma_tile(zero, 0, 2, lr, gq, [&](int m, int kb, float (&x)[8]) { load8f(sDT + (rb + m) * kLdS + kb, x); },
-                          [&](int kb, int n, float (&x)[8]) { load8f(sT + (16 * ib + n) * kLdS + kb, x); });
-    }
-    lds_barrier();  // dT is read
-#pragma unroll
-    for (int ib = 0; ib < 4; ++ib)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sDT[(rb + 4 * gq + e) * kLdS + 16 * ib + lr] = xt[ib][e];
-    lds_barrier();
-#pragma unroll
-    for (int ib = 0; ib < 4; ++ib) {
-      f4 acc = zero;
-      if (ib <= w)
-        acc = mma_tile(zero, 0, 2, lr, gq, tT, [&](int kb, int n, float (&x)[8]) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) x[i] = sDT[(kb + i) * kLdS + 16 * ib + n];
-        });
+    for (int q = 0; q < 2; ++q) {
+      const int i = tid + kGradThreads * q, r = i >> 4, c = 4 * (i & 15);
+      const f4 tv = *reinterpret_cast<const f4 *>(&tm[4 * i]);
+      const f4 pv = *reinterpret_cast<const f4 *>(&pm[4 * i]);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int r = rb + 4 * gq + e, j = 16 * ib + lr;
-        const float dA = j < r ? -acc[e] : 0.f;
-        dbr[e] += dA * sP[r * kLdS + j];
-        sP[r * kLdS + j] = sBt[r] * dA;
+        const int j = c + e;
+        if (j <= r) sTP[r * kLdS + j] = tv[e];
+        if (j < r) sTP[j * kLdS + r] = pv[e];
       }
     }
   }
-  lds_barrier();
-
-  // ---- 7. the products through A_qk and P with the sub-block factors: for
-  //         rows r of block w, e^{G_r - G_j} = e^{G_r - ref_w} e^{ref_w - G_j}
-  //         (the first <= 1, the second <= 1 for j before block w and <= e^80
-  //         inside it); for key rows j of block w and r >= 16w,
-  //         e^{G_r - G_j} = e^{G_r - ref_w} e^{ref_w - G_j} as well.
+  if (tid < kC) sBt[tid] = tid < len ? a.bt[tok_off(tid)] : 0.f;
+  float xo[4][8];
   {
-    const int kq = (16 * (w + 1) + 31) / 32;
-    const int jmax = 16 * (w + 1);
-    const int ks0 = (16 * w) / 32;
-    for (int nt = 0; nt < 8; ++nt) {
-      const int c = 16 * nt + lr;
-      f4 c1 = zero, c2 = zero, c3 = zero, c4 = zero;
-      for (int st = 0; st < kq; ++st) {
-        const int kb = 32 * st + 8 * gq;
-        float xa[8], xp[8], y[8];
-        load8f(sDA + (rb + lr) * kLdS + kb, xa);
-        load8f(sP + (rb + lr) * kLdS + kb, xp);
-        const float rw = ref(w, c);
+    const int r = rb + lr;
+    const int64_t oo = (tok0 + r) * a.do_stride + vrow;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int j = kb + i;
-          y[i] = j < jmax ? kh_at(j, c) * __expf(rw - Gat(j, c)) : 0.f;
-        }
-        c1 = mma8(xa, y, c1);
-        c2 = mma8(xp, y, c2);
-      }
-      for (int st = ks0; st < 2; ++st) {
-        const int kb = 32 * st + 8 * gq;
-        float xa[8], xp[8], yq[8], yk[8];
-        const float rw = ref(w, c);
+    for (int st = 0; st < 4; ++st) {
+      const int kb = 32 * st + 8 * gq;
+      if (r < len) {
+        const f4 u0 = load4(a.dout, oo + kb, a.do_dtype), u1 = load4(a.dout, oo + kb + 4, a.do_dtype);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int r = kb + i;
-          xa[i] = sDA[r * kLdS + rb + lr];
-          xp[i] = sP[r * kLdS + rb + lr];
-          const float f = r >= 16 * w ? __expf(Gat(r, c) - rw) : 0.f;
-          yq[i] = qh_at(r, c) * f;
-          yk[i] = kh_at(r, c) * f;
+        for (int i = 0; i < 4; ++i) {
+          xo[st][i] = u0[i];
+          xo[st][4 + i] = u1[i];
         }
-        c3 = mma8(xa, yq, c3);
-        c4 = mma8(xp, yk, c4);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xo[st][i] = 0.f;
       }
-      const float rw = ref(w, c);
+    }
+  }
+  // U rows of key block ib (rows past len are finite and meet zero dO / dU rows)
+  float un[4][8];
+  const auto fetch_keys = [&](int ib) {
+#pragma unroll
+    for (int st = 0; st < 4; ++st) load8f(Um + (16 * ib + lr) * kD + 32 * st + 8 * gq, un[st]);
+  };
+  if (u <= w) fetch_keys(u);
+  // v at the positions of this wavefront's dXu tiles (rows 16w + 4gq + e, columns 16 (u + 2k) + lr)
+  float vown[4][4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int r = rb + 4 * gq + e;
+      vown[k][e] = r < len ? load_elem(a.v, (tok0 + r) * a.v_stride + vrow + 16 * (u + 2 * k) + lr, a.v_dtype) : 0.f;
+    }
+  lds_barrier();
+  // G = cumulative log-decay: each half of threads 0..255 scans 32 rows of a
+  // channel, then rows 32.. add the total of rows 0..31.
+  if (tid < 256) {
+    const int c = tid & 127, r0 = (tid >> 7) * 32;
+    float acc = 0.f;
+#pragma unroll 8
+    for (int r = r0; r < r0 + 32; ++r) {
+      acc += sG[r * kLdG + c];
+      sG[r * kLdG + c] = acc;
+    }
+  }
+  lds_barrier();
+  if (tid >= 128 && tid < 256) {
+    const int c = tid - 128;
+    const float base = sG[31 * kLdG + c];
+#pragma unroll 8
+    for (int r = 32; r < 64; ++r) sG[r * kLdG + c] += base;
+  }
+
+  // ---- 2. per key block ib <= w with ib = u (mod 2): dA_qk = tril(dO U^T)
+  //         and the strictly lower part of dU U^T
+  {
+    float xd[4][8];   // dU rows of this row block
+#pragma unroll
+    for (int st = 0; st < 4; ++st) load8f(sDX + (rb + lr) * kLdG + 32 * st + 8 * gq, xd[st]);
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2) {
+      const int ib = u + 2 * k2;
+      if (ib > w) continue;
+      f4 aq = z4, ay = z4;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        aq = mma8(xo[st], un[st], aq);
+        ay = mma8(xd[st], un[st], ay);
+      }
+      if (k2 == 0 && ib + 2 <= w) fetch_keys(ib + 2);
+      const int j = 16 * ib + lr;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int r = rb + 4 * gq + e;
-        const float af = __expf(Gat(r, c) - rw);
-        const float bq = __expf(rw - Gat(r, c));
-        const float dqp = af * c1[e], dkgp = af * c2[e], dkr = bq * (c3[e] + c4[e]);
-        const float qv = qh_at(r, c), kv = kh_at(r, c);
-        aq[nt][e] += dqp;
-        ak[nt][e] += dkgp + dkr;
-        aG[nt][e] += qv * dqp + kv * dkgp - kv * dkr;
+        if (j <= r) sAT[r * kLdS + j] = aq[e];
+        if (j < r) sAT[j * kLdS + r] = ay[e];
       }
     }
   }
-
-  // ---- 8. outputs: dq^, dk^, dbeta; dg = reverse cumulative sum of dG + dGamma
+  // phase II's first blocks: rows 0..15 of S0 and dS1 and q^ columns 0..15
+  f4 pre[2], qpre = z4;
+  const int q_r = tid >> 2, q_c = 4 * (tid & 3);
+  const auto fetch2 = [&](int nt) {
 #pragma unroll
-  for (int nt = 0; nt < 8; ++nt)
+    for (int q = 0; q < 2; ++q)
+      pre[q] = *reinterpret_cast<const f4 *>((q == 0 ? S0 : dS1) + (16 * nt + blk_r) * kD + blk_c);
+    if (tid < 256 && q_r < len) qpre = *reinterpret_cast<const f4 *>(&a.qh[tok_off(q_r) * kD + 16 * nt + q_c]);
+  };
+  fetch2(0);
+
+  // ---- 3. dXu = T^T dU (rows of this row block, column blocks u + 2k); dv;
+  //         beta's term sum_v dXu v
+  float ta[2][8];   // T^T rows of this row block
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+    const int kb = 32 * st + 8 * gq, m = rb + lr;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ta[st][i] = m <= kb + i ? sTP[(kb + i) * kLdS + m] : 0.f;
+  }
+  float dbr[4] = {0.f, 0.f, 0.f, 0.f};
+  f4 dxu[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int c = 16 * (u + 2 * k) + lr;
+    dxu[k] = z4;
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      if (st < st0) continue;
+      const int kb = 32 * st + 8 * gq;
+      float y[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) y[i] = sDX[(kb + i) * kLdG + c];
+      dxu[k] = mma8(ta[st], y, dxu[k]);
+    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int r = rb + 4 * gq + e, c = 16 * nt + lr;
-      if (r < len) {
-        a.dqh[tok_off(r) * kD + c] = aq[nt][e];
-        a.dkh[tok_off(r) * kD + c] = ak[nt][e];
+      const int r = rb + 4 * gq + e;
+      const float bt = sBt[r];
+      dbr[e] += dxu[k][e] * vown[k][e];
+      if (r < len) a.dv[tok_off(r) * kD + c] = bt * dxu[k][e];
+    }
+  }
+  lds_barrier();   // dU is read; dA_qk and dU U^T are complete
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sDX[(rb + 4 * gq + e) * kLdG + 16 * (u + 2 * k) + lr] = dxu[k][e];
+
+  // ---- 4. dA_kk = tril_strict(-T^T Y), Y = tril_strict(dU U^T), for key
+  //         blocks ib = u (mod 2); beta's term sum_j dA_kk P; dP = beta dA_kk
+#pragma unroll
+  for (int k2 = 0; k2 < 2; ++k2) {
+    const int ib = u + 2 * k2;
+    if (ib > w) continue;
+    // B[k][n] = Y[k][16 ib + n] (16 ib + n < k) at [16 ib + n][k]
+    const int n = 16 * ib + lr;
+    f4 acc = z4;
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      if (st < st0) continue;
+      const int kb = 32 * st + 8 * gq;
+      float y[8];
+      load8f(sAT + n * kLdS + kb, y);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (kb + i <= n) y[i] = 0.f;
+      acc = mma8(ta[st], y, acc);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int r = rb + 4 * gq + e;
+      if (n < r) {
+        const float dA = -acc[e];
+        dbr[e] += dA * sTP[n * kLdS + r];
+        sTP[n * kLdS + r] = sBt[r] * dA;
       }
     }
+  }
+  lds_barrier();   // dXu and dP are complete
+
+  // ---- 5. (phase II) column blocks i = 0..7.  For rows r of block w the
+  //         products through A_qk and P split e^{G_r - G_j} =
+  //         e^{G_r - ref_w} e^{ref_w - G_j} (the first <= 1, the second <= 1
+  //         for j before block w and <= e^80 inside it), and so do key rows j
+  //         of block w with r >= 16w.  Keys j < 16 (w + 1) take the K-steps
+  //         below kq, queries r >= 16 w those from st0.
+  const auto stash2 = [&]() {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) *reinterpret_cast<f4 *>(sSl + (blk_r + 16 * q) * kLdG + blk_c) = pre[q];
+    if (tid < 256) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sQb[q_r * kLdQ + q_c + e] = qpre[e];
+    }
+  };
+  float *sX = sDX;
+  if (u == 0) {
+    // state wavefronts: dXu rows of this row block
+    float xdu[4][8];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) load8f(sDX + (rb + lr) * kLdG + 32 * st + 8 * gq, xdu[st]);
+    lds_barrier();   // dXu is read: its tile takes the exchange
+    for (int i = 0; i <= 8; ++i) {
+      if (i < 8) stash2();
+      if (i < 7) fetch2(i + 1);
+      lds_barrier();
+      if (i < 8) {
+        const int c = 16 * i + lr;
+        f4 dq = z4, dxw = z4;
+        float s0[4][8];
+#pragma unroll
+        for (int st = 0; st < 4; ++st) load8f(sSl + lr * kLdG + 32 * st + 8 * gq, s0[st]);
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          dq = mma8(xo[st], s0[st], dq);
+          dxw = mma8(xdu[st], s0[st], dxw);
+        }
+        if (w == 0) {
+          float sdot = 0.f;
+#pragma unroll
+          for (int st = 0; st < 4; ++st) {
+            float s1[8];
+            load8f(sSl + (16 + lr) * kLdG + 32 * st + 8 * gq, s1);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) sdot += s0[st][k] * s1[k];
+          }
+          sdot += lane_xor16(sdot);
+          sdot += lane_xor32(sdot);
+          if (gq == 0) sDg0[c] = sdot * __expf(Gat(kC - 1, c));
+        }
+        f4 xq, xw;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          xq[e] = dq[e] * __expf(Gat(rb + 4 * gq + e, c));   // through Qg = q^ e^G
+          xw[e] = -dxw[e];
+        }
+        float *x = sX + (((i & 1) * 4 + w) * 64 + l) * 8;
+        *reinterpret_cast<f4 *>(x) = xq;
+        *reinterpret_cast<f4 *>(x + 4) = xw;
+      }
+      lds_barrier();   // the blocks and the exchange are read
+    }
+  } else {
+    // chunk wavefronts: U rows and dA_qk rows / columns of this row block
+    const int jmax = 16 * (w + 1);
+    const int kq = w < 2 ? 1 : 2;
+    const int m = rb + lr;
+    float xu[4][8], xa[2][8], xat[2][8];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      if (m < len) {
+        load8f(Um + m * kD + 32 * st + 8 * gq, xu[st]);
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) xu[st][k] = 0.f;
+      }
+    }
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const int kb = 32 * st + 8 * gq;
+      load8f(sAT + m * kLdS + kb, xa[st]);    // dA_qk[m][k], k <= m
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int kk = kb + k;
+        if (kk > m) xa[st][k] = 0.f;
+        xat[st][k] = kk >= m ? sAT[kk * kLdS + m] : 0.f;  // dA_qk[k][m]
+      }
+    }
+    lds_barrier();   // matches the state wavefronts' barrier
+    // products of the block in flight, finished one block later
+    f4 hk = z4, h1 = z4, h2 = z4, h34 = z4;
+    float hq[4] = {0.f, 0.f, 0.f, 0.f}, hr = 0.f, hgam = 0.f;
+    for (int i = 0; i <= 8; ++i) {
+      if (i < 8) stash2();
+      if (i < 7) fetch2(i + 1);
+      lds_barrier();
+      if (i >= 1) {
+        // finish block i - 1
+        const int c = 16 * (i - 1) + lr;
+        const float *x = sX + ((((i - 1) & 1) * 4 + w) * 64 + l) * 8;
+        const f4 xq = *reinterpret_cast<const f4 *>(x), xw = *reinterpret_cast<const f4 *>(x + 4);
+        float part = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = rb + 4 * gq + e;
+          const float g = Gat(r, c);
+          const float eg = __expf(g), f = __expf(hgam - g), af = __expf(g - hr), bq = __expf(hr - g);
+          const float kv = Kat(r, c), bt = sBt[r];
+          const float dkbar = hk[e] * f;                    // through Kbar = k^ e^{Gamma - G}
+          const float dkg = bt * xw[e] * eg + af * h2[e];   // through Kg = k^ e^G
+          const float dkr = bq * h34[e];                    // through the k^ e^{-G} factor
+          const float dqv = xq[e] + af * h1[e];
+          part += dkbar * kv;
+          dbr[e] += xw[e] * kv * eg;
+          sG[r * kLdG + c] = hq[e] * dqv + kv * (dkg - dkbar - dkr);   // dG
+          if (r < len) {
+            a.dqh[tok_off(r) * kD + c] = dqv;
+            a.dkh[tok_off(r) * kD + c] = dkbar + dkg + dkr;
+          }
+        }
+        part += lane_xor16(part);
+        part += lane_xor32(part);
+        if (gq == 0) sDgW[w * kD + c] = part;
+      }
+      if (i < 8) {
+        const int c = 16 * i + lr;
+        const float rwc = w == 0 ? 0.f : Gat(rb - 1, c);
+        f4 dkb = z4;
+        {
+          float s1[4][8];
+#pragma unroll
+          for (int st = 0; st < 4; ++st) load8f(sSl + (16 + lr) * kLdG + 32 * st + 8 * gq, s1[st]);
+#pragma unroll
+          for (int st = 0; st < 4; ++st) dkb = mma8(xu[st], s1[st], dkb);
+        }
+        f4 c1 = z4, c2 = z4, c34 = z4;
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+          const int kb = 32 * st + 8 * gq;
+          float xp[8], xpt[8];   // dP[m][k] (k < m), dP[k][m] (k > m)
+          load8f(sTP + m * kLdS + kb, xpt);
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            const int kk = kb + k;
+            if (kk <= m) xpt[k] = 0.f;
+            xp[k] = kk < m ? sTP[kk * kLdS + m] : 0.f;
+          }
+          if (st < kq) {
+            float y[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+              const int j = kb + k;
+              y[k] = j < jmax ? Kat(j, c) * __expf(rwc - Gat(j, c)) : 0.f;
+            }
+            c1 = mma8(xa[st], y, c1);
+            c2 = mma8(xp, y, c2);
+          }
+          if (st >= st0) {
+            float yq[8], yk[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+              const int r = kb + k;
+              const float f = r >= rb ? __expf(Gat(r, c) - rwc) : 0.f;
+              yq[k] = sQb[r * kLdQ + lr] * f;
+              yk[k] = Kat(r, c) * f;
+            }
+            c34 = mma8(xat[st], yq, c34);
+            c34 = mma8(xpt, yk, c34);
+          }
+        }
+        hk = dkb;
+        h1 = c1;
+        h2 = c2;
+        h34 = c34;
+        hr = rwc;
+        hgam = Gat(kC - 1, c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) hq[e] = sQb[(rb + 4 * gq + e) * kLdQ + lr];
+      }
+      lds_barrier();   // the blocks, the exchange and G's columns 16 (i - 1) .. are read
+    }
+  }
+
+  // ---- 6. dbeta; dg = reverse cumulative sum of dG + dGamma
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     float x = dbr[e];
 #pragma unroll
     for (int off = 1; off < 16; off <<= 1) x += __shfl_xor(x, off, 64);
-    const int r = rb + 4 * gq + e;
-    if (lr == 0 && r < len) a.dbp[tok_off(r)] = x;
+    if (lr == 0) sDb[u * 64 + rb + 4 * gq + e] = x;
   }
-  // sG (every read of G is done once all wavefronts pass this barrier) takes dG.
-  lds_barrier();
-#pragma unroll
-  for (int nt = 0; nt < 8; ++nt)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) sG[(rb + 4 * gq + e) * kLdG + 16 * nt + lr] = aG[nt][e];
-  lds_barrier();
-  if (tid < kD) {
-    const float dgam = sDg0[tid] + ((sDgW[tid] + sDgW[kD + tid]) + (sDgW[2 * kD + tid] + sDgW[3 * kD + tid]));
+  // Suffix sums within each half of the rows, then rows 0..31 add the total of 32..63.
+  const int c = tid & 127, half = (tid >> 7) & 1;
+  if (tid < 256) {
     float acc = 0.f;
-    for (int r = kC - 1; r >= 0; --r) {
-      acc += sG[r * kLdG + tid];
-      if (r < len) a.dgl[tok_off(r) * kD + tid] = acc + dgam;
+#pragma unroll 8
+    for (int r = 32 * half + 31; r >= 32 * half; --r) {
+      acc += sG[r * kLdG + c];
+      sG[r * kLdG + c] = acc;
     }
+  }
+  lds_barrier();
+  if (tid < 256) {
+    const float dgam = sDg0[c] + ((sDgW[c] + sDgW[kD + c]) + (sDgW[2 * kD + c] + sDgW[3 * kD + c])) +
+                       (half == 0 ? sG[32 * kLdG + c] : 0.f);
+#pragma unroll 8
+    for (int r = 32 * half; r < 32 * half + 32; ++r)
+      if (r < len) a.dgl[tok_off(r) * kD + c] = sG[r * kLdG + c] + dgam;
+  } else if (tid < 256 + kC) {
+    const int r = tid - 256;
+    if (r < len) a.dbp[tok_off(r)] = sDb[r] + sDb[64 + r];
   }
 }
 
@@ -2376,7 +2507,7 @@ int chunk_bwd_run(const ChunkBwdIO &io, void *scratch, hipStream_t st) {
   if (io.total == 0) return SOPHIA_OK;
   const size_t glds = kGradLdsFloats * sizeof(float);
   if (const int rc = ensure_lds<GradKey>(reinterpret_cast<const void *>(&kda_bwd_grad_kernel), glds)) return rc;
-  hipLaunchKernelGGL(kda_bwd_grad_kernel, dim3(static_cast<unsigned>(items)), dim3(256), glds, st, a);
+  hipLaunchKernelGGL(kda_bwd_grad_kernel, dim3(static_cast<unsigned>(items)), dim3(kGradThreads), glds, st, a);
   return check_launch("kda_bwd_grad");
 }
 
