@@ -15,7 +15,13 @@
 //   dbeta = du . (v - p);  dp = -beta du;  dk^ = dS u + S~ dp;
 //   dS~ = dS + k^ dp^T;  dalpha = rowsum(dS~ o S_{t-1});  dS_{t-1} = Diag(alpha) dS~.
 //
-// Kernels:
+// Two forms.  The default, the chunk form, is kda_chunk.hip's chunk_bwd_run
+// (backward records, forward-state and reverse chunk scans, per-chunk
+// gradients on MFMA, the norms', gate's and sigmoid's backward inside the
+// last kernel) followed by the gate-parameter sums below.  The recurrent
+// form (SOPHIA_KDA_BWD_RECURRENT) runs the per-token recurrence in fp32:
+//
+// Kernels of the recurrent form:
 //  * kda_bwd_prep_kernel, one work-group of 128 threads per (token, head):
 //    q^, k^, the decay alpha = e^g (gate applied) and beta (sigmoid applied),
 //    fp32.
@@ -33,8 +39,9 @@
 //  * kda_bwd_post_kernel, one work-group of 128 threads per (token, head):
 //    sums the partials and applies the backward of the l2 norms, of the gate
 //    g = lb sigmoid(e^A_log (z + dt_bias)) and of the beta sigmoid.
-//  * kda_bwd_gate_partial_kernel / kda_bwd_gate_final_kernel: dA_log and
-//    ddt_bias, sums over tokens of dz (z + dt_bias) and dz, in a fixed order.
+//  * kda_bwd_gate_partial_kernel / kda_bwd_gate_final_kernel (both forms):
+//    dA_log and ddt_bias, sums over tokens of dz (z + dt_bias) and dz, in a
+//    fixed order.
 //
 // Thread t of the chain kernel owns value column j = t % 32 of its slice and
 // state rows 8 (t / 32) .. +7.  A sum over the 128 rows (k^T X for a column)
@@ -86,9 +93,6 @@ struct BwdArgs {
   float *dq, *dk, *dv, *dg, *dbeta, *dh0, *dA_log, *ddt_bias;
   // workspace
   float *qh, *kh, *gl, *bt;        // prepared q^, k^, alpha = e^g, beta
-  float *glg;                      // prepared log-decay g (chunk form only), or NULL
-  int parts;                       // partial sums per gradient: kSlices (recurrent) or 1 (chunk form)
-  int dg_given;                    // dal holds the gradient of g itself (chunk form), not of alpha
   float *ckpt;                     // [pieces, H, 128, 128] states at every 8-token piece start
   float *dqh, *dkh, *dal;          // [kSlices, total, H, 128] partial sums
   float *dbp;                      // [kSlices, total, H] dbeta summed over a slice's columns
@@ -124,7 +128,6 @@ __global__ __launch_bounds__(kD) void kda_bwd_prep_kernel(BwdArgs a) {
   a.qh[o] = qv * qs;
   a.kh[o] = kv * ks;
   a.gl[o] = expf(z);
-  if (a.glg) a.glg[o] = z;
   if (c == 0) {
     if (a.flags & SOPHIA_KDA_BETA_SIGMOID) b = 1.f / (1.f + expf(-b));
     a.bt[tok * a.num_heads + h] = b;
@@ -478,7 +481,7 @@ __global__ __launch_bounds__(kD) void kda_bwd_post_kernel(BwdArgs a) {
   __shared__ float s_red[2][4];
   const int64_t o = (tok * a.num_heads + h) * kD + c;
   float dqh = 0.f, dkh = 0.f, dal = 0.f;
-  for (int sl = 0; sl < a.parts; ++sl) {
+  for (int sl = 0; sl < kSlices; ++sl) {
     const int64_t po = ((static_cast<int64_t>(sl) * a.total + tok) * a.num_heads + h) * kD + c;
     dqh += a.dqh[po];
     dkh += a.dkh[po];
@@ -511,9 +514,8 @@ __global__ __launch_bounds__(kD) void kda_bwd_post_kernel(BwdArgs a) {
   }
   a.dq[o] = dq;
   a.dk[o] = dk;
-  // alpha = e^g: dg = dalpha alpha (the chunk form gives dg itself); through
-  // the gate, dz = dg lb s (1 - s) e^A_log
-  float dgv = a.dg_given ? dal : dal * a.gl[o];
+  // alpha = e^g: dg = dalpha alpha; through the gate, dz = dg lb s (1 - s) e^A_log
+  float dgv = dal * a.gl[o];
   if (a.flags & SOPHIA_KDA_GATE_IN_KERNEL) {
     const float z = load_elem(a.g, tok * a.g_stride + static_cast<int64_t>(h) * kD + c, a.g_dtype);
     const float ea = expf(a.A_log[h]);
@@ -523,7 +525,7 @@ __global__ __launch_bounds__(kD) void kda_bwd_post_kernel(BwdArgs a) {
   a.dg[o] = dgv;
   if (c == 0) {
     float db = 0.f;
-    for (int sl = 0; sl < a.parts; ++sl) db += a.dbp[(static_cast<int64_t>(sl) * a.total + tok) * a.num_heads + h];
+    for (int sl = 0; sl < kSlices; ++sl) db += a.dbp[(static_cast<int64_t>(sl) * a.total + tok) * a.num_heads + h];
     if (a.flags & SOPHIA_KDA_BETA_SIGMOID) {
       const float bt = a.bt[tok * a.num_heads + h];
       db *= bt * (1.f - bt);
@@ -595,8 +597,8 @@ int ensure_chain_lds() {
 
 using namespace sophia;
 
-// Workspace: the prepared inputs and the gate partials (both forms), then
-// either form's own part.
+// Workspace: the prepared inputs (recurrent form) and the gate partials (both
+// forms), then either form's own part.
 namespace {
 size_t bwd_common_bytes(size_t tok, int num_heads) {
   return 3 * align256(tok * kD * 4) + align256(tok * 4) + 2 * align256(static_cast<size_t>(kGateParts) * num_heads * kD * 4);
@@ -605,8 +607,8 @@ size_t bwd_recurrent_bytes(int64_t total_tokens, int n_seqs, int num_heads, size
   return align256(max_pieces(total_tokens, n_seqs) * num_heads * kD * kD * 4) + 3 * align256(kSlices * tok * kD * 4) +
          align256(kSlices * tok * 4) + align256(tok * kD * 4);
 }
-size_t bwd_chunk_bytes(int64_t total_tokens, int n_seqs, int num_heads, size_t tok) {
-  return 4 * align256(tok * kD * 4) + align256(tok * 4) + align256(chunk_bwd_scratch_bytes(total_tokens, n_seqs, num_heads));
+size_t bwd_chunk_bytes(int64_t total_tokens, int n_seqs, int num_heads, size_t) {
+  return align256(chunk_bwd_scratch_bytes(total_tokens, n_seqs, num_heads));
 }
 }  // namespace
 
@@ -700,20 +702,11 @@ extern "C" int sophia_kda_chunk_bwd(const void *q, const void *k, const void *v,
     a.dal = carve(kSlices * tok * kD * 4);
     a.dbp = carve(kSlices * tok * 4);
     a.pv = carve(tok * kD * 4);
-    a.parts = kSlices;
-    a.dg_given = 0;
   } else {
-    a.glg = carve(tok * kD * 4);
-    a.dqh = carve(tok * kD * 4);
-    a.dkh = carve(tok * kD * 4);
-    a.dal = carve(tok * kD * 4);
-    a.dbp = carve(tok * 4);
     scratch = carve(chunk_bwd_scratch_bytes(total_tokens, n_seqs, num_heads));
-    a.parts = 1;
-    a.dg_given = 1;
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (total_tokens > 0) {
+  if (recurrent && total_tokens > 0) {
     hipLaunchKernelGGL(kda_bwd_prep_kernel, dim3(static_cast<unsigned>(total_tokens), num_heads), dim3(kD), 0, st,
                        a);
     if (const int rc = check_launch("kda_bwd_prep")) return rc;
@@ -725,14 +718,15 @@ extern "C" int sophia_kda_chunk_bwd(const void *q, const void *k, const void *v,
     if (const int rc = check_launch("kda_bwd_chain")) return rc;
   } else {
     // The chunk form (records, forward states, reverse chunk scan, per-chunk
-    // gradients on MFMA): d q^, d k^, d g, d beta of every token, dv, dh0.
+    // gradients on MFMA, the norms', gate's and sigmoid's backward included):
+    // dq, dk, dv, dg, dbeta of every token and dh0.
     ChunkBwdIO io{q, k, v, qkv_row_stride, qkv_dtype, g, g_row_stride, g_dtype, beta, beta_row_stride,
                   beta_dtype, A_log, dt_bias, scale, lower_bound, flags, cu_seqlens, n_seqs, total_tokens,
                   num_heads, initial_state, d_out, d_out_row_stride, d_out_dtype, d_final_state,
-                  a.qh, a.kh, a.glg, a.bt, a.dqh, a.dkh, a.dal, a.dbp, dv, d_initial_state};
+                  dq, dk, dg, dbeta, dv, d_initial_state};
     if (const int rc = chunk_bwd_run(io, scratch, st)) return rc;
   }
-  if (total_tokens > 0) {
+  if (recurrent && total_tokens > 0) {
     hipLaunchKernelGGL(kda_bwd_post_kernel, dim3(static_cast<unsigned>(total_tokens), num_heads), dim3(kD), 0, st,
                        a);
     if (const int rc = check_launch("kda_bwd_post")) return rc;

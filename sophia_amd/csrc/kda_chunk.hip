@@ -1508,14 +1508,22 @@ struct BwdChunkArgs {
   const float *dht;            // [n_seqs][H][128][128] or NULL
   float *dh0;                  // [n_seqs][H][128][128] or NULL
   int splits;                  // work-groups (value-column slices) per (sequence, head): 2, 4 or 8
-  const float *qh, *kh, *glog, *bt;   // prepared q^, k^, log-decay [total][H][128], beta [total][H]
-  const void *v;
+  const void *q, *k, *v;       // the forward's inputs (rows of v_stride elements of v_dtype)
   int64_t v_stride;
   int v_dtype;
+  const void *g;
+  int64_t g_stride;
+  int g_dtype;
+  const void *beta;
+  int64_t beta_stride;
+  int beta_dtype;
+  const float *A_log, *dt_bias;
+  float scale, lb;
+  unsigned flags;
   const void *dout;
   int64_t do_stride;
   int do_dtype;
-  float *dqh, *dkh, *dgl, *dbp, *dv;  // gradients of q^, k^, the log-decay, beta, v
+  float *dq, *dk, *dg, *dbeta, *dv;   // gradients of q, k, g, beta, v (fp32)
 };
 
 // One (sequence, head, NVB value columns) of the forward scan that keeps S0
@@ -1765,7 +1773,7 @@ constexpr int kLdS = 68;
 constexpr int kLdQ = 18;    // q^ column block: rows 8 apart land 16 banks apart
 constexpr int kGradThreads = 512;
 constexpr size_t kGradLdsFloats =
-    3 * 64 * kLdG + 2 * 64 * kLdS + 2 * 16 * kLdG + 64 * kLdQ + 64 + 128 + 4 * 128 + 2 * 64;
+    3 * 64 * kLdG + 2 * 64 * kLdS + 2 * 16 * kLdG + 64 * kLdQ + 64 + 128 + 4 * 128 + 2 * 64 + 4 * 64;
 
 // One (chunk, head) of the per-chunk gradients on 512 threads: wavefronts w
 // and w + 4 (one pair per SIMD) share the chunk rows 16w .. 16w + 15 of every
@@ -1803,6 +1811,13 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
   float *sDg0 = sBt + 64;           // [128] e^Gamma sum_v dS1 S0
   float *sDgW = sDg0 + 128;         // [4][128] per-row-block sums of dKbar Kbar
   float *sDb = sDgW + 4 * 128;      // [2][64] dbeta of each wavefront of a pair
+  float *sRq = sDb + 2 * 64;        // [64] q^ = q sRq (scale / |q| with the l2 norm)
+  float *sRk = sRq + 64;            // [64] k^ = k sRk
+  float *sIq = sRk + 64;            // [64] 1 / |q|^2 where the l2 norm's backward has the rank-1 term, else 0
+  float *sIk = sIq + 64;            // [64] the same flag for k (1 or 0)
+  // dq^ sRq of every row (phase II): rows 0..31 in the dA_qk tile (read
+  // into registers by then), rows 32..63 behind the exchange
+  const auto dQrow = [&](int r) { return r < 32 ? sAT + r * kLdG : sDX + 4096 + (r - 32) * kLdG; };
   const ScanArgs &p = a.p;
   const int H = p.num_heads;
   const int h = static_cast<int>(blockIdx.x % static_cast<unsigned>(H));
@@ -1835,19 +1850,44 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
   // and (tid >> 5) + 16, columns 4 (tid & 31) .. + 3.
   const int blk_r = tid >> 5, blk_c = 4 * (tid & 31);
 
-  // ---- 1. log-decay, k^ and dU rows (zero past len), T and P, beta; the dO
-  //         rows of this row block; the U rows of the first key block
+  // ---- 1. the log-decay (the gate applied), k^ (the norms of q and k) and
+  //         dU rows (zero past len), T and P, beta; the dO rows of this row
+  //         block; the U rows of the first key block
+  const bool l2 = (a.flags & SOPHIA_KDA_QK_L2NORM) != 0;
+  const bool gate = (a.flags & SOPHIA_KDA_GATE_IN_KERNEL) != 0;
+  const float ea = gate ? __expf(a.A_log[h]) : 0.f;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int r = blk_r + 16 * q;
-    f4 gv = z4, kv = z4, dv = z4;
+    f4 gv = z4, kv = z4, qv = z4, dv = z4;
     if (r < len) {
-      gv = *reinterpret_cast<const f4 *>(&a.glog[tok_off(r) * kD + blk_c]);
-      kv = *reinterpret_cast<const f4 *>(&a.kh[tok_off(r) * kD + blk_c]);
+      const int64_t ro = (tok0 + r) * a.v_stride + vrow + blk_c;
+      qv = load4(a.q, ro, a.v_dtype);
+      kv = load4(a.k, ro, a.v_dtype);
+      gv = load4(a.g, (tok0 + r) * a.g_stride + vrow + blk_c, a.g_dtype);
+      if (gate) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) gv[e] = kda_log_decay(gv[e], ea, a.dt_bias[h * kD + blk_c + e], a.lb);
+      }
       dv = *reinterpret_cast<const f4 *>(&dUm[r * kD + blk_c]);
     }
+    float sq = qv[0] * qv[0] + qv[1] * qv[1] + qv[2] * qv[2] + qv[3] * qv[3];
+    float sk = kv[0] * kv[0] + kv[1] * kv[1] + kv[2] * kv[2] + kv[3] * kv[3];
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) {   // the 32 threads of row r
+      sq += __shfl_xor(sq, off, 64);
+      sk += __shfl_xor(sk, off, 64);
+    }
+    const float lq = sqrtf(sq), lk = sqrtf(sk);
+    const float rk = l2 ? 1.f / fmaxf(lk, 1e-12f) : 1.f;
+    if ((tid & 31) == 0) {
+      sRq[r] = l2 ? a.scale / fmaxf(lq, 1e-12f) : a.scale;
+      sRk[r] = rk;
+      sIq[r] = l2 && lq >= 1e-12f ? 1.f / (lq * lq) : 0.f;
+      sIk[r] = l2 && lk >= 1e-12f ? 1.f : 0.f;
+    }
     *reinterpret_cast<f4 *>(&sG[r * kLdG + blk_c]) = gv;
-    *reinterpret_cast<f4 *>(&sKh[r * kLdG + blk_c]) = kv;
+    *reinterpret_cast<f4 *>(&sKh[r * kLdG + blk_c]) = kv * rk;
     *reinterpret_cast<f4 *>(&sDX[r * kLdG + blk_c]) = dv;
   }
   {
@@ -1865,7 +1905,14 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
       }
     }
   }
-  if (tid < kC) sBt[tid] = tid < len ? a.bt[tok_off(tid)] : 0.f;
+  if (tid < kC) {
+    float b = 0.f;
+    if (tid < len) {
+      b = load_elem(a.beta, (tok0 + tid) * a.beta_stride + h, a.beta_dtype);
+      if (a.flags & SOPHIA_KDA_BETA_SIGMOID) b = sigmoid_f(b);
+    }
+    sBt[tid] = b;
+  }
   float xo[4][8];
   {
     const int r = rb + lr;
@@ -1955,7 +2002,7 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
 #pragma unroll
     for (int q = 0; q < 2; ++q)
       pre[q] = *reinterpret_cast<const f4 *>((q == 0 ? S0 : dS1) + (16 * nt + blk_r) * kD + blk_c);
-    if (tid < 256 && q_r < len) qpre = *reinterpret_cast<const f4 *>(&a.qh[tok_off(q_r) * kD + 16 * nt + q_c]);
+    if (tid < 256 && q_r < len) qpre = load4(a.q, (tok0 + q_r) * a.v_stride + vrow + 16 * nt + q_c, a.v_dtype);
   };
   fetch2(0);
 
@@ -2039,8 +2086,9 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
 #pragma unroll
     for (int q = 0; q < 2; ++q) *reinterpret_cast<f4 *>(sSl + (blk_r + 16 * q) * kLdG + blk_c) = pre[q];
     if (tid < 256) {
+      const float rq = sRq[q_r];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) sQb[q_r * kLdQ + q_c + e] = qpre[e];
+      for (int e = 0; e < 4; ++e) sQb[q_r * kLdQ + q_c + e] = qpre[e] * rq;
     }
   };
   float *sX = sDX;
@@ -2140,13 +2188,12 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
           const float dkg = bt * xw[e] * eg + af * h2[e];   // through Kg = k^ e^G
           const float dkr = bq * h34[e];                    // through the k^ e^{-G} factor
           const float dqv = xq[e] + af * h1[e];
+          const float dkv = dkbar + dkg + dkr;
           part += dkbar * kv;
           dbr[e] += xw[e] * kv * eg;
           sG[r * kLdG + c] = hq[e] * dqv + kv * (dkg - dkbar - dkr);   // dG
-          if (r < len) {
-            a.dqh[tok_off(r) * kD + c] = dqv;
-            a.dkh[tok_off(r) * kD + c] = dkbar + dkg + dkr;
-          }
+          dQrow(r)[c] = dqv * sRq[r];
+          sKh[r * kLdG + c] = dkv;   // k^'s column block i - 1 is read by now
         }
         part += lane_xor16(part);
         part += lane_xor32(part);
@@ -2219,26 +2266,83 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
     for (int off = 1; off < 16; off <<= 1) x += __shfl_xor(x, off, 64);
     if (lr == 0) sDb[u * 64 + rb + 4 * gq + e] = x;
   }
-  // Suffix sums within each half of the rows, then rows 0..31 add the total of 32..63.
-  const int c = tid & 127, half = (tid >> 7) & 1;
-  if (tid < 256) {
+  // Suffix sums within each quarter of the rows (16 rows, a channel per
+  // thread); the rows of a quarter then add the totals of the quarters after it.
+  {
+    const int c = tid & 127, r0 = (tid >> 7) * 16;
     float acc = 0.f;
 #pragma unroll 8
-    for (int r = 32 * half + 31; r >= 32 * half; --r) {
+    for (int r = r0 + 15; r >= r0; --r) {
       acc += sG[r * kLdG + c];
       sG[r * kLdG + c] = acc;
     }
   }
   lds_barrier();
-  if (tid < 256) {
-    const float dgam = sDg0[c] + ((sDgW[c] + sDgW[kD + c]) + (sDgW[2 * kD + c] + sDgW[3 * kD + c])) +
-                       (half == 0 ? sG[32 * kLdG + c] : 0.f);
-#pragma unroll 8
-    for (int r = 32 * half; r < 32 * half + 32; ++r)
-      if (r < len) a.dgl[tok_off(r) * kD + c] = sG[r * kLdG + c] + dgam;
-  } else if (tid < 256 + kC) {
+  if (tid >= 256 && tid < 256 + kC) {
     const int r = tid - 256;
-    if (r < len) a.dbp[tok_off(r)] = sDb[r] + sDb[64 + r];
+    if (r < len) {
+      float db = sDb[r] + sDb[64 + r];
+      if (a.flags & SOPHIA_KDA_BETA_SIGMOID) db *= sBt[r] * (1.f - sBt[r]);
+      a.dbeta[tok_off(r)] = db;
+    }
+  }
+  // dg, dq and dk rows.  dg of the log-decay is the suffix sum plus dGamma;
+  // through the gate g = lb sigmoid(e^A_log (z + dt_bias)), dz = dg lb s (1 - s) e^A_log.
+  // The l2 norms' backward: dq = dq^ sRq - q (q^ . dq^) / |q|^2 and
+  // dk = (dk^ - k^ (k^ . dk^)) / |k| = dk^ sRk - k sRk^2 (k^ . dk^), with
+  // q^ . dq^ = q . (dq^ sRq) and k^ . dk^ = sRk (k . dk^): sums over the 32
+  // threads of a row.
+  {
+    f4 gbias = z4;
+    if (gate) gbias = *reinterpret_cast<const f4 *>(&a.dt_bias[h * kD + blk_c]);
+    f4 dgam, tail[4];
+    tail[3] = z4;
+#pragma unroll
+    for (int q = 2; q >= 0; --q) tail[q] = tail[q + 1] + *reinterpret_cast<const f4 *>(&sG[16 * (q + 1) * kLdG + blk_c]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int cc = blk_c + e;
+      dgam[e] = sDg0[cc] + ((sDgW[cc] + sDgW[kD + cc]) + (sDgW[2 * kD + cc] + sDgW[3 * kD + cc]));
+    }
+    f4 zv[4], qv[4], kv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int r = blk_r + 16 * q;
+      zv[q] = qv[q] = kv[q] = z4;
+      if (r < len) {
+        const int64_t ro = (tok0 + r) * a.v_stride + vrow + blk_c;
+        qv[q] = load4(a.q, ro, a.v_dtype);
+        kv[q] = load4(a.k, ro, a.v_dtype);
+        if (gate) zv[q] = load4(a.g, (tok0 + r) * a.g_stride + vrow + blk_c, a.g_dtype);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int r = blk_r + 16 * q;
+      const f4 dqs = *reinterpret_cast<const f4 *>(dQrow(r) + blk_c);
+      const f4 dks = *reinterpret_cast<const f4 *>(&sKh[r * kLdG + blk_c]);
+      float sq = qv[q][0] * dqs[0] + qv[q][1] * dqs[1] + qv[q][2] * dqs[2] + qv[q][3] * dqs[3];
+      float sk = kv[q][0] * dks[0] + kv[q][1] * dks[1] + kv[q][2] * dks[2] + kv[q][3] * dks[3];
+#pragma unroll
+      for (int off = 1; off < 32; off <<= 1) {
+        sq += __shfl_xor(sq, off, 64);
+        sk += __shfl_xor(sk, off, 64);
+      }
+      if (r >= len) continue;
+      const float rk = sRk[r];
+      f4 d = *reinterpret_cast<const f4 *>(&sG[r * kLdG + blk_c]) + dgam + tail[q];
+      if (gate) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float sg = sigmoid_f(ea * (zv[q][e] + gbias[e]));
+          d[e] *= a.lb * sg * (1.f - sg) * ea;
+        }
+      }
+      const int64_t o = tok_off(r) * kD + blk_c;
+      *reinterpret_cast<f4 *>(&a.dg[o]) = d;
+      *reinterpret_cast<f4 *>(&a.dq[o]) = dqs - qv[q] * (sIq[r] * sq);
+      *reinterpret_cast<f4 *>(&a.dk[o]) = dks * rk - kv[q] * (sIk[r] * rk * rk * rk * sk);
+    }
   }
 }
 
@@ -2495,10 +2599,12 @@ int chunk_bwd_run(const ChunkBwdIO &io, void *scratch, hipStream_t st) {
   a.brec = brec; a.tmat = tmat; a.pmat = pmat;
   a.s0 = s0; a.u = u; a.ds1 = ds1; a.du = du;
   a.dht = io.dht; a.dh0 = io.dh0; a.splits = splits;
-  a.qh = io.qh; a.kh = io.kh; a.glog = io.glog; a.bt = io.bt;
-  a.v = io.v; a.v_stride = io.qkv_stride; a.v_dtype = io.qkv_dtype;
+  a.q = io.q; a.k = io.k; a.v = io.v; a.v_stride = io.qkv_stride; a.v_dtype = io.qkv_dtype;
+  a.g = io.g; a.g_stride = io.g_stride; a.g_dtype = io.g_dtype;
+  a.beta = io.beta; a.beta_stride = io.beta_stride; a.beta_dtype = io.beta_dtype;
+  a.A_log = io.A_log; a.dt_bias = io.dt_bias; a.scale = io.scale; a.lb = io.lb; a.flags = io.flags;
   a.dout = io.dout; a.do_stride = io.do_stride; a.do_dtype = io.do_dtype;
-  a.dqh = io.dqh; a.dkh = io.dkh; a.dgl = io.dgl; a.dbp = io.dbp; a.dv = io.dv;
+  a.dq = io.dq; a.dk = io.dk; a.dg = io.dg; a.dbeta = io.dbeta; a.dv = io.dv;
   hipLaunchKernelGGL(kda_bwd_states_kernel, dim3(static_cast<unsigned>(sblocks)), dim3(kScanThreads), 0, st, a);
   if (const int rc = check_launch("kda_bwd_states")) return rc;
   hipLaunchKernelGGL(kda_bwd_rscan_kernel, dim3(static_cast<unsigned>(sblocks)), dim3(kScanThreads), 0, st, a);

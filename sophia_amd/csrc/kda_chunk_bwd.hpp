@@ -1,6 +1,6 @@
-// Chunk-form backward stages of kda_chunk.hip, called by the backward entry
-// point in kda_bwd.hip (sophia_kda_chunk_bwd) between its prep and post
-// kernels.  Internal to the library: no C ABI.
+// Chunk-form backward of kda_chunk.hip, called by the backward entry point in
+// kda_bwd.hip (sophia_kda_chunk_bwd), which adds dA_log and ddt_bias from the
+// gradient of g.  Internal to the library: no C ABI.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -33,12 +33,10 @@ struct ChunkBwdIO {
   int64_t do_stride;
   int do_dtype;
   const float *dht;         // [n_seqs][H][128][128] or NULL
-  // prepared inputs (the backward's prep kernel): q^, k^, the log-decay after
-  // the gate [total][H][128], beta after the sigmoid [total][H]
-  const float *qh, *kh, *glog, *bt;
-  // outputs: gradients of q^, k^, the log-decay [total][H][128], of beta
-  // [total][H], of v [total][H][128], of the initial states (or NULL)
-  float *dqh, *dkh, *dgl, *dbp, *dv, *dh0;
+  // outputs: gradients of q, k, g (the gate's input, or the log-decay
+  // itself without the gate in the kernel), v [total][H][128], of beta
+  // [total][H] (all fp32) and of the initial states (or NULL)
+  float *dq, *dk, *dg, *dbeta, *dv, *dh0;
 };
 
 // Scratch bytes chunk_bwd_run needs (256-byte aligned start).
