@@ -1488,18 +1488,21 @@ __global__ __launch_bounds__(kScanThreads) void kda_chunk_seg_run_kernel(SegArgs
 //   dS0 = Diag(e^Gamma) dS1 + Qg^T dO - W^T dU        (the reverse chunk scan)
 // and once S0, U, dS1 and dU of every chunk are known, its gradients need
 // nothing from the other chunks:
-//   dQg = dO S0^T, dW = -dU S0^T, dKbar = U dS1^T, dA_qk = tril(dO U^T),
-//   dT = dW Xw^T + dU Xu^T (Xw = beta Kg, Xu = beta V), dXw = T^T dW,
-//   dXu = T^T dU, dA_kk = tril_strict(-T^T dT T^T), then back through
-//   A_kk = Diag(beta) P and A_qk with the sub-block factors, and dg = the
-//   reverse cumulative sum of dG plus dGamma on every row.
+//   dQg = dO S0^T, dKbar = U dS1^T, dA_qk = tril(dO U^T), dXu = T^T dU,
+//   dXw = T^T dW = -dXu S0^T (dW = -dU S0^T),
+//   dA_kk = tril_strict(-T^T dT T^T) = tril_strict(-T^T tril_strict(dU U^T))
+//   (dT = dW Xw^T + dU Xu^T = dU (T^-1 U)^T, Xw = beta Kg, Xu = beta V),
+//   then back through A_kk = Diag(beta) P and A_qk with the sub-block
+//   factors, and dg = the reverse cumulative sum of dG plus dGamma on every
+//   row; the l2 norms', the gate's and the beta sigmoid's backward follow.
 // Three kernels after the backward's instantiation of the intra kernel:
 //  * kda_bwd_states_kernel: the forward scan keeping S0 and U of every chunk;
 //  * kda_bwd_rscan_kernel: the reverse scan, same two roles as the forward
 //    one: four wavefronts form dU (rows 16w..), four hold dS in fp32 MFMA
 //    accumulators; it keeps dS1 and dU of every chunk and leaves dh0;
-//  * kda_bwd_grad_kernel: one work-group per (chunk, head), every product on
-//    fp32 MFMA through generic fragment loaders.
+//  * kda_bwd_grad_kernel: one work-group of 512 threads per (chunk, head),
+//    every product on fp32 MFMA; it reads the raw q, k, g, beta and writes
+//    the final dq, dk, dv, dg, dbeta.
 struct BwdChunkArgs {
   ScanArgs p;                  // offsets, sizes, forward records, h0
   const uint8_t *brec;         // backward records
@@ -1995,16 +1998,19 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
       }
     }
   }
-  // phase II's first blocks: rows 0..15 of S0 and dS1 and q^ columns 0..15
+  // The blocks of phase II's step i (i = -1 .. 7): rows 16 (i + 1) .. of S0
+  // for the state wavefronts, rows 16 i .. of dS1 and q^'s columns 16 i ..
+  // for the chunk wavefronts.
   f4 pre[2], qpre = z4;
   const int q_r = tid >> 2, q_c = 4 * (tid & 3);
-  const auto fetch2 = [&](int nt) {
-#pragma unroll
-    for (int q = 0; q < 2; ++q)
-      pre[q] = *reinterpret_cast<const f4 *>((q == 0 ? S0 : dS1) + (16 * nt + blk_r) * kD + blk_c);
-    if (tid < 256 && q_r < len) qpre = load4(a.q, (tok0 + q_r) * a.v_stride + vrow + 16 * nt + q_c, a.v_dtype);
+  const auto fetch2 = [&](int i) {
+    if (i < 7) pre[0] = *reinterpret_cast<const f4 *>(S0 + (16 * (i + 1) + blk_r) * kD + blk_c);
+    if (i >= 0) {
+      pre[1] = *reinterpret_cast<const f4 *>(dS1 + (16 * i + blk_r) * kD + blk_c);
+      if (tid < 256 && q_r < len) qpre = load4(a.q, (tok0 + q_r) * a.v_stride + vrow + 16 * i + q_c, a.v_dtype);
+    }
   };
-  fetch2(0);
+  fetch2(-1);
 
   // ---- 3. dXu = T^T dU (rows of this row block, column blocks u + 2k); dv;
   //         beta's term sum_v dXu v
@@ -2076,19 +2082,23 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
   }
   lds_barrier();   // dXu and dP are complete
 
-  // ---- 5. (phase II) column blocks i = 0..7.  For rows r of block w the
-  //         products through A_qk and P split e^{G_r - G_j} =
+  // ---- 5. (phase II) column blocks: in step i the state wavefronts form
+  //         block i + 1 and the chunk wavefronts block i, finishing it from
+  //         the state wavefronts' results of step i - 1.  For rows r of
+  //         block w the products through A_qk and P split e^{G_r - G_j} =
   //         e^{G_r - ref_w} e^{ref_w - G_j} (the first <= 1, the second <= 1
   //         for j before block w and <= e^80 inside it), and so do key rows j
   //         of block w with r >= 16w.  Keys j < 16 (w + 1) take the K-steps
   //         below kq, queries r >= 16 w those from st0.
-  const auto stash2 = [&]() {
+  const auto stash2 = [&](int i) {
+    if (i < 7) *reinterpret_cast<f4 *>(sSl + blk_r * kLdG + blk_c) = pre[0];
+    if (i >= 0) {
+      *reinterpret_cast<f4 *>(sSl + (16 + blk_r) * kLdG + blk_c) = pre[1];
+      if (tid < 256) {
+        const float rq = sRq[q_r];
 #pragma unroll
-    for (int q = 0; q < 2; ++q) *reinterpret_cast<f4 *>(sSl + (blk_r + 16 * q) * kLdG + blk_c) = pre[q];
-    if (tid < 256) {
-      const float rq = sRq[q_r];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sQb[q_r * kLdQ + q_c + e] = qpre[e] * rq;
+        for (int e = 0; e < 4; ++e) sQb[q_r * kLdQ + q_c + e] = qpre[e] * rq;
+      }
     }
   };
   float *sX = sDX;
@@ -2098,33 +2108,21 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
 #pragma unroll
     for (int st = 0; st < 4; ++st) load8f(sDX + (rb + lr) * kLdG + 32 * st + 8 * gq, xdu[st]);
     lds_barrier();   // dXu is read: its tile takes the exchange
-    for (int i = 0; i <= 8; ++i) {
-      if (i < 8) stash2();
+    float s0p[4][8];   // the previous block's S0 rows (wavefront 0: e^Gamma sum_v dS1 S0)
+    for (int i = -1; i < 8; ++i) {
+      stash2(i);
       if (i < 7) fetch2(i + 1);
       lds_barrier();
-      if (i < 8) {
-        const int c = 16 * i + lr;
-        f4 dq = z4, dxw = z4;
-        float s0[4][8];
+      float s0[4][8];
+      if (i < 7) {
+        const int nb = i + 1, c = 16 * nb + lr;
 #pragma unroll
         for (int st = 0; st < 4; ++st) load8f(sSl + lr * kLdG + 32 * st + 8 * gq, s0[st]);
+        f4 dq = z4, dxw = z4;
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
           dq = mma8(xo[st], s0[st], dq);
           dxw = mma8(xdu[st], s0[st], dxw);
-        }
-        if (w == 0) {
-          float sdot = 0.f;
-#pragma unroll
-          for (int st = 0; st < 4; ++st) {
-            float s1[8];
-            load8f(sSl + (16 + lr) * kLdG + 32 * st + 8 * gq, s1);
-#pragma unroll
-            for (int k = 0; k < 8; ++k) sdot += s0[st][k] * s1[k];
-          }
-          sdot += lane_xor16(sdot);
-          sdot += lane_xor32(sdot);
-          if (gq == 0) sDg0[c] = sdot * __expf(Gat(kC - 1, c));
         }
         f4 xq, xw;
 #pragma unroll
@@ -2132,9 +2130,29 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
           xq[e] = dq[e] * __expf(Gat(rb + 4 * gq + e, c));   // through Qg = q^ e^G
           xw[e] = -dxw[e];
         }
-        float *x = sX + (((i & 1) * 4 + w) * 64 + l) * 8;
+        float *x = sX + (((nb & 1) * 4 + w) * 64 + l) * 8;
         *reinterpret_cast<f4 *>(x) = xq;
         *reinterpret_cast<f4 *>(x + 4) = xw;
+      }
+      if (w == 0 && i >= 0) {
+        const int c = 16 * i + lr;
+        float sdot = 0.f;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          float s1[8];
+          load8f(sSl + (16 + lr) * kLdG + 32 * st + 8 * gq, s1);
+#pragma unroll
+          for (int k = 0; k < 8; ++k) sdot += s0p[st][k] * s1[k];
+        }
+        sdot += lane_xor16(sdot);
+        sdot += lane_xor32(sdot);
+        if (gq == 0) sDg0[c] = sdot * __expf(Gat(kC - 1, c));
+      }
+      if (i < 7) {
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+#pragma unroll
+          for (int k = 0; k < 8; ++k) s0p[st][k] = s0[st][k];
       }
       lds_barrier();   // the blocks and the exchange are read
     }
@@ -2165,43 +2183,25 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
       }
     }
     lds_barrier();   // matches the state wavefronts' barrier
-    // products of the block in flight, finished one block later
-    f4 hk = z4, h1 = z4, h2 = z4, h34 = z4;
-    float hq[4] = {0.f, 0.f, 0.f, 0.f}, hr = 0.f, hgam = 0.f;
-    for (int i = 0; i <= 8; ++i) {
-      if (i < 8) stash2();
-      if (i < 7) fetch2(i + 1);
-      lds_barrier();
+    // dG and dk^ of the previous block, written over G's and k^'s columns
+    // once every wavefront has read them (after the next barrier)
+    float pg[4] = {0.f, 0.f, 0.f, 0.f}, pk[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int i = -1; i < 8; ++i) {
       if (i >= 1) {
-        // finish block i - 1
-        const int c = 16 * (i - 1) + lr;
-        const float *x = sX + ((((i - 1) & 1) * 4 + w) * 64 + l) * 8;
-        const f4 xq = *reinterpret_cast<const f4 *>(x), xw = *reinterpret_cast<const f4 *>(x + 4);
-        float part = 0.f;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int r = rb + 4 * gq + e;
-          const float g = Gat(r, c);
-          const float eg = __expf(g), f = __expf(hgam - g), af = __expf(g - hr), bq = __expf(hr - g);
-          const float kv = Kat(r, c), bt = sBt[r];
-          const float dkbar = hk[e] * f;                    // through Kbar = k^ e^{Gamma - G}
-          const float dkg = bt * xw[e] * eg + af * h2[e];   // through Kg = k^ e^G
-          const float dkr = bq * h34[e];                    // through the k^ e^{-G} factor
-          const float dqv = xq[e] + af * h1[e];
-          const float dkv = dkbar + dkg + dkr;
-          part += dkbar * kv;
-          dbr[e] += xw[e] * kv * eg;
-          sG[r * kLdG + c] = hq[e] * dqv + kv * (dkg - dkbar - dkr);   // dG
-          dQrow(r)[c] = dqv * sRq[r];
-          sKh[r * kLdG + c] = dkv;   // k^'s column block i - 1 is read by now
+          const int r = rb + 4 * gq + e, c = 16 * (i - 1) + lr;
+          sG[r * kLdG + c] = pg[e];
+          sKh[r * kLdG + c] = pk[e];
         }
-        part += lane_xor16(part);
-        part += lane_xor32(part);
-        if (gq == 0) sDgW[w * kD + c] = part;
       }
-      if (i < 8) {
+      stash2(i);
+      if (i < 7) fetch2(i + 1);
+      lds_barrier();
+      if (i >= 0) {
         const int c = 16 * i + lr;
         const float rwc = w == 0 ? 0.f : Gat(rb - 1, c);
+        const float gam = Gat(kC - 1, c);
         f4 dkb = z4;
         {
           float s1[4][8];
@@ -2245,18 +2245,40 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
             c34 = mma8(xpt, yk, c34);
           }
         }
-        hk = dkb;
-        h1 = c1;
-        h2 = c2;
-        h34 = c34;
-        hr = rwc;
-        hgam = Gat(kC - 1, c);
+        // finish block i with the state wavefronts' dQg e^G and dXw
+        const float *x = sX + (((i & 1) * 4 + w) * 64 + l) * 8;
+        const f4 xq = *reinterpret_cast<const f4 *>(x), xw = *reinterpret_cast<const f4 *>(x + 4);
+        float part = 0.f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) hq[e] = sQb[(rb + 4 * gq + e) * kLdQ + lr];
+        for (int e = 0; e < 4; ++e) {
+          const int r = rb + 4 * gq + e;
+          const float g = Gat(r, c);
+          const float eg = __expf(g), f = __expf(gam - g), af = __expf(g - rwc), bq = __expf(rwc - g);
+          const float kv = Kat(r, c), qv = sQb[r * kLdQ + lr], bt = sBt[r];
+          const float dkbar = dkb[e] * f;                   // through Kbar = k^ e^{Gamma - G}
+          const float dkg = bt * xw[e] * eg + af * c2[e];   // through Kg = k^ e^G
+          const float dkr = bq * c34[e];                    // through the k^ e^{-G} factor
+          const float dqv = xq[e] + af * c1[e];
+          part += dkbar * kv;
+          dbr[e] += xw[e] * kv * eg;
+          pg[e] = qv * dqv + kv * (dkg - dkbar - dkr);      // dG
+          pk[e] = dkbar + dkg + dkr;                        // dk^
+          dQrow(r)[c] = dqv * sRq[r];
+        }
+        part += lane_xor16(part);
+        part += lane_xor32(part);
+        if (gq == 0) sDgW[w * kD + c] = part;
       }
-      lds_barrier();   // the blocks, the exchange and G's columns 16 (i - 1) .. are read
+      lds_barrier();   // the blocks, the exchange and G's and k^'s columns 16 i .. are read
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int r = rb + 4 * gq + e, c = 16 * 7 + lr;
+      sG[r * kLdG + c] = pg[e];
+      sKh[r * kLdG + c] = pk[e];
     }
   }
+  lds_barrier();   // dG and dk^ are complete
 
   // ---- 6. dbeta; dg = reverse cumulative sum of dG + dGamma
 #pragma unroll

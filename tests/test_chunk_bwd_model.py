@@ -102,3 +102,27 @@ def test_factored_decay_products_are_fp32_safe():
     for a, b in zip(got, ref):
         assert np.all(np.isfinite(a))
         assert _rel(a, b) < 1e-4
+
+
+@pytest.mark.parametrize("total,seed,g_lo", [(64, 11, -5.0), (45, 12, -0.5), (64, 13, -0.05)])
+def test_gradient_kernel_identities(total, seed, g_lo):
+    """The per-chunk gradient kernel forms neither dW nor dT: since
+    U = T (Xu - Xw S0), dT = dW Xw^T + dU Xu^T = dU (T^-1 U)^T, so
+    tril_strict(-T^T dT T^T) = tril_strict(-T^T Y) with Y the strictly lower
+    part of dU U^T (the only part the strict result reads), and
+    T^T dW = -(T^T dU) S0^T.  The plausible slips (U dU^T for dU U^T, T for
+    T^T) break the equality."""
+    qn, kn, v, g, beta, s0, do, dsf = _case(total, 32, 24, seed, g_lo=g_lo)
+    o, s1, ctx = cbm.chunk_forward(qn, kn, v, g, beta, s0)
+    do = cbm._pad(do, cbm.CHUNK - total)
+    dU = ctx["A_qk"].T @ do + ctx["Kbar"] @ dsf
+    T, U, strict = ctx["T"], ctx["U"], ctx["strict"]
+    dW = -dU @ s0.T
+    dT = dW @ ctx["Xw"].T + dU @ ctx["Xu"].T
+    want = np.where(strict, -T.T @ dT @ T.T, 0.0)
+    got = np.where(strict, -T.T @ np.where(strict, dU @ U.T, 0.0), 0.0)
+    assert _rel(got, want) < 1e-11
+    assert _rel(-(T.T @ dU) @ s0.T, T.T @ dW) < 1e-11
+    for bad in (np.where(strict, -T.T @ np.where(strict, U @ dU.T, 0.0), 0.0),
+                np.where(strict, -T @ np.where(strict, dU @ U.T, 0.0), 0.0)):
+        assert _rel(bad, want) > 1e-3
