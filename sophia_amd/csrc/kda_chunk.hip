@@ -337,8 +337,9 @@ __device__ __forceinline__ void intra_scaled_operands(
 #pragma unroll
     for (int i = 0; i < 8; ++i)
       sKb[sb.b[i & 3] + 64 * (32 * ks + 16 * (i >> 2))] = f32_to_bf16_bits(kbar[i]);
-    // Q e^G goes straight to the workspace in A-operand order (mb = W).
-    *reinterpret_cast<u4 *>(rec + kOffQ + ((W * 4 + ks) * 64 + l) * 16) = bf8_to_bits(pack8(qe));
+    // Q e^G goes straight to the workspace in A-operand order (mb = W); the
+    // backward's forward-state scan forms no O and reads no Q e^G.
+    if constexpr (!BWD) *reinterpret_cast<u4 *>(rec + kOffQ + ((W * 4 + ks) * 64 + l) * 16) = bf8_to_bits(pack8(qe));
     if constexpr (BWD) {
       // Kbar in A-operand order (m = rows); Q e^G transposed for Qg^T.
       *reinterpret_cast<u4 *>(brec + kBOffKbar + ((W * 4 + ks) * 64 + l) * 16) = bf8_to_bits(pack8(kbar));
@@ -805,10 +806,12 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
     }
   }
 
-  // ---- 10. A_qk fragments from LDS to the workspace
+  // ---- 10. A_qk fragments from LDS to the workspace (not for the backward's
+  // forward-state scan, which forms no O)
   // A_qk: m = chunk rows 16w + lr, k = chunk rows perm_k(ks, gq, .).  The
   // fragments of K-step 1 for rows 0..31 are zero (A_qk is lower
   // triangular): they are neither written nor read.
+  if constexpr (BWD) return;
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
     if (ks == 1 && w < 2) break;
@@ -1599,6 +1602,31 @@ __device__ __forceinline__ void fstate_item(const BwdChunkArgs &a, const Chain &
   }
 }
 
+// Sequence whose chains the work-groups of rank `rank` run in the backward's
+// two scans: for a batch of at most kOrderMax sequences the longest first
+// (most chunks; ties by index), so that the work-groups of a second round
+// hold the short chains; `rank` itself for larger batches.  Lane i ranks
+// sequence i against the others (one load per lane, a shuffle per sequence).
+__device__ __forceinline__ int longest_first(const ScanArgs &p, int rank) {
+  const int n = p.n_seqs;
+  if (n > kOrderMax) return rank;
+  const int lane = threadIdx.x & 63;
+  int64_t ch = -1;
+  if (lane < n) {
+    const int64_t a0 = iclamp64(p.cu[lane], 0, p.total);
+    const int64_t b0 = iclamp64(p.cu[lane + 1], a0, p.total);
+    ch = (b0 - a0 + kC - 1) / kC;
+  }
+  const int c32 = static_cast<int>(ch);
+  int r = 0;
+  for (int j = 0; j < n; ++j) {
+    const int cj = __shfl(c32, j, 64);
+    r += (cj > c32 || (cj == c32 && j < lane)) ? 1 : 0;
+  }
+  const unsigned long long hit = __ballot(lane < n && r == rank);
+  return hit ? __builtin_ctzll(hit) : rank;
+}
+
 __global__ __launch_bounds__(kScanThreads) void kda_bwd_states_kernel(BwdChunkArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t sSb[4 * 8 * 64 * 16];
   __shared__ __attribute__((aligned(16))) uint8_t sUb[2 * 8 * 64 * 16];
@@ -1606,8 +1634,8 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_states_kernel(BwdChunkAr
   int item, half;
   seg_item(blockIdx.x, a.splits, item, half);
   const int h = item % p.num_heads;
-  const int s = item / p.num_heads;
-  if (s >= p.n_seqs) return;
+  if (item / p.num_heads >= p.n_seqs) return;
+  const int s = longest_first(p, item / p.num_heads);
   const Chain c = sequence_chain(p, s, h);
   switch (a.splits) {
     case 8: fstate_item<16>(a, c, h, half, sSb, sUb); break;
@@ -1741,8 +1769,8 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_rscan_kernel(BwdChunkArg
   int item, half;
   seg_item(blockIdx.x, a.splits, item, half);
   const int h = item % p.num_heads;
-  const int s = item / p.num_heads;
-  if (s >= p.n_seqs) return;
+  if (item / p.num_heads >= p.n_seqs) return;
+  const int s = longest_first(p, item / p.num_heads);
   const Chain c = sequence_chain(p, s, h);
   switch (a.splits) {
     case 8: rscan_item<16>(a, c, s, h, half, sSb, sUb); break;
@@ -2610,9 +2638,14 @@ int chunk_bwd_run(const ChunkBwdIO &io, void *scratch, hipStream_t st) {
   if (hipGetDevice(&device) == hipSuccess)
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) cus = 256;
   const int64_t pairs = static_cast<int64_t>(io.n_seqs) * H;
-  // (at least 2: a 128-column slice does not fit these kernels' registers)
+  // (at least 2: a 128-column slice does not fit these kernels' registers).
+  // With the chains taken longest first (at most kOrderMax sequences) two
+  // rounds of work-groups pay: thinner slices store less per chunk step, and
+  // the second round holds the short chains (benchmark batch: 2 slices
+  // 258.7 + 147.3 us, 4 slices 156.1 + 107.1 us, 8 slices 205.7 + 142.5 us).
   int splits = 2;
-  while (splits < 8 && pairs * splits * 2 <= cus) splits *= 2;
+  const int64_t room = io.n_seqs <= kOrderMax ? 2 * static_cast<int64_t>(cus) : cus;
+  while (splits < 8 && pairs * splits * 2 <= room) splits *= 2;
   const int64_t sblocks = (pairs + 7) / 8 * 8 * splits;
   SOPHIA_REQUIRE(sblocks <= 0x7fffffff, "kda_chunk_bwd: grid too large");
   BwdChunkArgs a{};

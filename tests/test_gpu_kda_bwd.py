@@ -282,3 +282,26 @@ def test_chunk_bwd_matches_recurrent_at_size():
     want = _hip(inp, cu, d_out, d_final, flags, recurrent=True)
     got = _hip(inp, cu, d_out, d_final, flags, recurrent=False)
     _compare(got, want, "chunk vs recurrent", TOL_CHUNK)
+
+
+def test_chunk_bwd_sequence_order_is_immaterial():
+    """The backward's two chunk scans take the chains longest first (for up to
+    16 sequences) and, with that order, thinner value-column slices over two
+    rounds of work-groups.  The same sequences packed in the reverse order
+    must give each token and each sequence bit-identical gradients: every
+    chain's arithmetic depends only on its own sequence."""
+    lens = [70, 900, 0, 1500, 257, 64, 1]
+    heads = 4
+    cu = [0] + list(np.cumsum(lens))
+    inp, d_out, d_final, flags = _inputs(cu, heads, seed=21, gated=False, dtype=torch.bfloat16)
+    got = _hip(inp, cu, d_out, d_final, flags, recurrent=False)
+    order = list(range(len(lens)))[::-1]
+    rows = [np.arange(cu[i], cu[i + 1]) for i in order]
+    perm = np.concatenate(rows)
+    cu_r = [0] + list(np.cumsum([lens[i] for i in order]))
+    inp_r = {k: (None if t is None else (t[perm] if k not in ("h0",) else t[order]))
+             for k, t in inp.items()}
+    got_r = _hip(inp_r, cu_r, d_out[perm], d_final[order], flags, recurrent=False)
+    for name in ("q", "k", "v", "g", "beta"):
+        assert np.array_equal(got[name][perm], got_r[name]), f"d{name} differs with the order"
+    assert np.array_equal(got["h0"][order], got_r["h0"]), "dh0 differs with the order"
