@@ -305,3 +305,42 @@ def test_chunk_bwd_sequence_order_is_immaterial():
     for name in ("q", "k", "v", "g", "beta"):
         assert np.array_equal(got[name][perm], got_r[name]), f"d{name} differs with the order"
     assert np.array_equal(got["h0"][order], got_r["h0"]), "dh0 differs with the order"
+
+
+def test_chunk_bwd_long_slow_decay_sequence():
+    """One 16,384-token sequence (256 chunk steps in each scan), 4 heads,
+    with the gate of a freshly initialised mixer in the kernel (A_log = 0,
+    dt_bias = inverse_softplus(dt), dt log-uniform in [1e-3, 1e-1], decay
+    logits z ~ N(0, 0.5^2); ml/runtime/model/attention.py:101-106): the state
+    and its gradient keep most of their memory across the whole chain, so a
+    per-chunk rounding in either scan would accumulate.  Chunk form against
+    the fp32 recurrent form, dA_log and ddt_bias (sums over all tokens)
+    included."""
+    gen = torch.Generator().manual_seed(61)
+    total, heads = 16384, 4
+    lo, hi = np.log(1e-3), np.log(1e-1)
+    dt = torch.exp(torch.rand(heads * D, generator=gen) * (hi - lo) + lo).clamp_min(1e-4)
+    inp = {
+        "q": torch.randn(total, heads, D, generator=gen).to(torch.bfloat16),
+        "k": torch.randn(total, heads, D, generator=gen).to(torch.bfloat16),
+        "v": torch.randn(total, heads, D, generator=gen).to(torch.bfloat16),
+        "g": torch.randn(total, heads, D, generator=gen) * 0.5,
+        "beta": torch.randn(total, heads, generator=gen),
+        "A_log": torch.zeros(heads),
+        "dt_bias": dt + torch.log(-torch.expm1(-dt)),
+        "h0": torch.randn(1, heads, D, D, generator=gen) * 0.05,
+    }
+    g_np = ko.kda_gate(inp["g"].numpy(), inp["A_log"].numpy(), inp["dt_bias"].numpy(), -5.0)
+    assert float(np.median(g_np)) > -0.6  # the long-memory regime
+    d_out = torch.randn(total, heads, D, generator=gen).to(torch.bfloat16)
+    d_final = torch.randn(1, heads, D, D, generator=gen) * 0.05
+    flags = dict(use_qk_l2norm=True, use_gate=True, use_beta_sigmoid=True)
+    cu = [0, total]
+    want = _hip(inp, cu, d_out, d_final, flags, recurrent=True)
+    got = _hip(inp, cu, d_out, d_final, flags, recurrent=False)
+    _compare(got, want, "chunk vs recurrent, 16 k slow-decay tokens", TOL_CHUNK)
+    # the first 1,024 tokens, whose gradients come through the whole reverse chain
+    for name in ("q", "k", "v", "g"):
+        err = _rel(got[name][:1024], want[name][:1024])
+        print(f"first 1,024 tokens d{name}: rel err {err:.2e}", flush=True)
+        assert err <= TOL_CHUNK
