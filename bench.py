@@ -306,10 +306,11 @@ def backward_bench(torch, dev, stream, inp, steps: int, warmup: int, with_cpu: b
     out = {"workload": "KDA backward over the prefill batch (same lengths, flags and inputs), "
                        "bf16 d_out, fp32 gradients",
            "form": "chunk (records, forward-state and reverse chunk scans on bf16 MFMA operands, "
-                   "per-chunk gradients on fp32 MFMA with the norm, gate and sigmoid backward fused)",
+                   "per-chunk gradients as split-bf16 MFMA products (hi*hi + hi*lo + lo*hi, fp32 "
+                   "accumulation) with the norm, gate and sigmoid backward fused)",
            "tokens_per_s": round(total / (ms / 1e3), 1), "ms_per_call": round(ms, 3),
            "recurrent_form_ms_per_call": round(float(np.mean(per_rec)), 3),
-           "roofline": {"bound": "memory latency / fp32 MFMA", "achieved": round(tflops, 2),
+           "roofline": {"bound": "memory latency / MFMA (fp32 peak as the yardstick)", "achieved": round(tflops, 2),
                         "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
                         "frac": round(tflops / FP32_PEAK_TFLOPS, 4),
                         "flops_per_token": BWD_FLOPS_PER_TOKEN,

@@ -1504,8 +1504,9 @@ __global__ __launch_bounds__(kScanThreads) void kda_chunk_seg_run_kernel(SegArgs
 //    one: four wavefronts form dU (rows 16w..), four hold dS in fp32 MFMA
 //    accumulators; it keeps dS1 and dU of every chunk and leaves dh0;
 //  * kda_bwd_grad_kernel: one work-group of 512 threads per (chunk, head),
-//    every product on fp32 MFMA; it reads the raw q, k, g, beta and writes
-//    the final dq, dk, dv, dg, dbeta.
+//    every product as a split bf16 product (about 16 mantissa bits, fp32
+//    accumulation); it reads the raw q, k, g, beta and writes the final dq,
+//    dk, dv, dg, dbeta.
 struct BwdChunkArgs {
   ScanArgs p;                  // offsets, sizes, forward records, h0
   const uint8_t *brec;         // backward records
@@ -1784,10 +1785,28 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_rscan_kernel(BwdChunkArg
 // group g in step i being 8 g + i.  (bf16 operands here leave dg, and the
 // per-head sums dA_log / ddt_bias over it, 10-40x further from the float64
 // reference: dg is a reverse cumulative sum of terms that cancel.)
-__device__ __forceinline__ f4 mma8(const float (&x)[8], const float (&y)[8], f4 acc) {
+// Split products: x = hi + lo with hi = bf16(x) and lo = bf16(x - hi) keeps
+// ~16 mantissa bits, and hi.hi + hi.lo + lo.hi (lo.lo, below 2^-16 of the
+// product, dropped) on bf16 MFMAs with fp32 accumulation takes three 16x16x32
+// MFMAs where fp32 operands take eight 16x16x4 ones (step i of lane group g
+// covering k = 8g + i).  Lane group g holds k = 8g .. 8g + 7 of a 16x16x32
+// operand, so the same eight values per lane form the fragment in either.
+struct Sp8 {
+  bf8 hi, lo;
+};
+__device__ __forceinline__ Sp8 split8(const float (&x)[8]) {
+  Sp8 s;
+  s.hi = pack8(x);
+  float r[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) acc = mfma_f32x4(x[i], y[i], acc);
-  return acc;
+  for (int i = 0; i < 8; ++i) r[i] = x[i] - static_cast<float>(s.hi[i]);
+  s.lo = pack8(r);
+  return s;
+}
+__device__ __forceinline__ f4 mma3(const Sp8 &x, const Sp8 &y, f4 acc) {
+  acc = mfma32(x.lo, y.hi, acc);
+  acc = mfma32(x.hi, y.lo, acc);
+  return mfma32(x.hi, y.hi, acc);
 }
 
 __device__ __forceinline__ void load8f(const float *src, float (&x)[8]) {
@@ -1964,6 +1983,9 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
       }
     }
   }
+  Sp8 xos[4];   // the dO rows, split (see mma3)
+#pragma unroll
+  for (int st = 0; st < 4; ++st) xos[st] = split8(xo[st]);
   // U rows of key block ib (rows past len are finite and meet zero dO / dU rows)
   float un[4][8];
   const auto fetch_keys = [&](int ib) {
@@ -2003,9 +2025,13 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
   // ---- 2. per key block ib <= w with ib = u (mod 2): dA_qk = tril(dO U^T)
   //         and the strictly lower part of dU U^T
   {
-    float xd[4][8];   // dU rows of this row block
+    Sp8 xds[4];   // dU rows of this row block, split
 #pragma unroll
-    for (int st = 0; st < 4; ++st) load8f(sDX + (rb + lr) * kLdG + 32 * st + 8 * gq, xd[st]);
+    for (int st = 0; st < 4; ++st) {
+      float xd[8];
+      load8f(sDX + (rb + lr) * kLdG + 32 * st + 8 * gq, xd);
+      xds[st] = split8(xd);
+    }
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2) {
       const int ib = u + 2 * k2;
@@ -2013,8 +2039,9 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
       f4 aq = z4, ay = z4;
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
-        aq = mma8(xo[st], un[st], aq);
-        ay = mma8(xd[st], un[st], ay);
+        const Sp8 us = split8(un[st]);
+        aq = mma3(xos[st], us, aq);
+        ay = mma3(xds[st], us, ay);
       }
       if (k2 == 0 && ib + 2 <= w) fetch_keys(ib + 2);
       const int j = 16 * ib + lr;
@@ -2049,6 +2076,9 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
 #pragma unroll
     for (int i = 0; i < 8; ++i) ta[st][i] = m <= kb + i ? sTP[(kb + i) * kLdS + m] : 0.f;
   }
+  Sp8 tas[2];
+#pragma unroll
+  for (int st = 0; st < 2; ++st) tas[st] = split8(ta[st]);
   float dbr[4] = {0.f, 0.f, 0.f, 0.f};
   f4 dxu[4];
 #pragma unroll
@@ -2062,7 +2092,7 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
       float y[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) y[i] = sDX[(kb + i) * kLdG + c];
-      dxu[k] = mma8(ta[st], y, dxu[k]);
+      dxu[k] = mma3(tas[st], split8(y), dxu[k]);
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -2096,7 +2126,7 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
 #pragma unroll
       for (int i = 0; i < 8; ++i)
         if (kb + i <= n) y[i] = 0.f;
-      acc = mma8(ta[st], y, acc);
+      acc = mma3(tas[st], split8(y), acc);
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -2132,9 +2162,13 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
   float *sX = sDX;
   if (u == 0) {
     // state wavefronts: dXu rows of this row block
-    float xdu[4][8];
+    Sp8 xdus[4];
 #pragma unroll
-    for (int st = 0; st < 4; ++st) load8f(sDX + (rb + lr) * kLdG + 32 * st + 8 * gq, xdu[st]);
+    for (int st = 0; st < 4; ++st) {
+      float xdu[8];
+      load8f(sDX + (rb + lr) * kLdG + 32 * st + 8 * gq, xdu);
+      xdus[st] = split8(xdu);
+    }
     lds_barrier();   // dXu is read: its tile takes the exchange
     float s0p[4][8];   // the previous block's S0 rows (wavefront 0: e^Gamma sum_v dS1 S0)
     for (int i = -1; i < 8; ++i) {
@@ -2149,8 +2183,9 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
         f4 dq = z4, dxw = z4;
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
-          dq = mma8(xo[st], s0[st], dq);
-          dxw = mma8(xdu[st], s0[st], dxw);
+          const Sp8 ss = split8(s0[st]);
+          dq = mma3(xos[st], ss, dq);
+          dxw = mma3(xdus[st], ss, dxw);
         }
         f4 xq, xw;
 #pragma unroll
@@ -2210,6 +2245,14 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
         xat[st][k] = kk >= m ? sAT[kk * kLdS + m] : 0.f;  // dA_qk[k][m]
       }
     }
+    Sp8 xus[4], xas[2], xats[2];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) xus[st] = split8(xu[st]);
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      xas[st] = split8(xa[st]);
+      xats[st] = split8(xat[st]);
+    }
     lds_barrier();   // matches the state wavefronts' barrier
     // dG and dk^ of the previous block, written over G's and k^'s columns
     // once every wavefront has read them (after the next barrier)
@@ -2236,7 +2279,7 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
 #pragma unroll
           for (int st = 0; st < 4; ++st) load8f(sSl + (16 + lr) * kLdG + 32 * st + 8 * gq, s1[st]);
 #pragma unroll
-          for (int st = 0; st < 4; ++st) dkb = mma8(xu[st], s1[st], dkb);
+          for (int st = 0; st < 4; ++st) dkb = mma3(xus[st], split8(s1[st]), dkb);
         }
         f4 c1 = z4, c2 = z4, c34 = z4;
 #pragma unroll
@@ -2257,8 +2300,9 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
               const int j = kb + k;
               y[k] = j < jmax ? Kat(j, c) * __expf(rwc - Gat(j, c)) : 0.f;
             }
-            c1 = mma8(xa[st], y, c1);
-            c2 = mma8(xp, y, c2);
+            const Sp8 ys = split8(y);
+            c1 = mma3(xas[st], ys, c1);
+            c2 = mma3(split8(xp), ys, c2);
           }
           if (st >= st0) {
             float yq[8], yk[8];
@@ -2269,8 +2313,8 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
               yq[k] = sQb[r * kLdQ + lr] * f;
               yk[k] = Kat(r, c) * f;
             }
-            c34 = mma8(xat[st], yq, c34);
-            c34 = mma8(xpt, yk, c34);
+            c34 = mma3(xats[st], split8(yq), c34);
+            c34 = mma3(split8(xpt), split8(yk), c34);
           }
         }
         // finish block i with the state wavefronts' dQg e^G and dXw
