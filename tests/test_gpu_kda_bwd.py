@@ -249,6 +249,21 @@ def test_chunk_bwd_matches_torch_autograd_restatement():
     _compare(got, ref, "chunk vs torch autograd", TOL_CHUNK)
 
 
+def test_chunk_bwd_more_sequences_than_the_ranked_plan():
+    """20 sequences: past the 16 that the two chunk scans rank longest first on
+    the device, they take the chains in packing order.  Empty, one-token and
+    multi-chunk sequences mixed, against the oracle."""
+    rng = np.random.default_rng(71)
+    lens = rng.integers(0, 200, size=20)
+    lens[[3, 11]] = 0
+    lens[7] = 1
+    lens[15] = 260
+    cu = [0] + np.cumsum(lens).tolist()
+    inp, d_out, d_final, flags = _inputs(cu, 2, seed=71, gated=True, dtype=torch.bfloat16)
+    _compare(_hip(inp, cu, d_out, d_final, flags, recurrent=False),
+             _oracle(inp, cu, d_out, d_final, flags), "chunk 20 sequences", TOL_CHUNK)
+
+
 def test_chunk_bwd_slow_decay_and_one_token_sequences():
     """Log-decays near 0 (long memory: the reverse scan carries dS through
     every chunk nearly undamped), beta = 0 rows, and sequences of 1 and 64
