@@ -69,6 +69,8 @@ class SlotAllocator:
 
     def release(self, slots) -> None:
         values = [int(s) for s in (slots.tolist() if isinstance(slots, torch.Tensor) else slots)]
+        if len(set(values)) != len(values):
+            raise ValueError(f"slots released twice in one call: {sorted(values)}")
         for s in values:
             if s not in self._held:
                 raise ValueError(f"slot {s} is not held")

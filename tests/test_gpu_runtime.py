@@ -252,6 +252,8 @@ def test_slot_allocator_grows_zeroes_and_reuses():
             assert float(st[1].min()) == 3.0            # held: untouched
     with pytest.raises(ValueError):
         alloc.release([7])
+    with pytest.raises(ValueError):
+        alloc.release([3, 3])                   # the same slot twice: nothing released
     assert alloc.in_use == 5
 
 
