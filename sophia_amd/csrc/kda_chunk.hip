@@ -193,10 +193,9 @@ constexpr size_t kSmB = kSmA + 96 * kLdKD * 2;
 constexpr size_t kSmC = kSmB + 64 * kLdKD * 2;
 constexpr size_t kSmD = kSmC + 64 * kLdT * 4;
 constexpr size_t kSmIntra = kSmD + 64 * kLdQK * 2;           // 73216
-// Backward instantiations: Q e^G and dO, transposed ([128][64] bf16, swizzled).
-constexpr size_t kSmF = kSmIntra;
-constexpr size_t kSmG = kSmF + 128 * 64 * 2;
-constexpr size_t kSmIntraBwd = kSmG + 128 * 64 * 2;
+// The backward's instantiation transposes Q e^G and dO through regions A and
+// B after their last use (step 9), so it needs no more LDS than the forward.
+constexpr size_t kSmIntraBwd = kSmIntra;
 static_assert(128 * 64 * 2 <= 96 * kLdKD * 2, "region A holds a swizzled [128][64] bf16 tile");
 static_assert(128 * 64 * 2 <= 64 * kLdKD * 2, "region B holds a swizzled [128][64] bf16 tile");
 static_assert(128 * 64 * 2 <= 64 * kLdT * 4, "region C holds a swizzled [128][64] bf16 tile");
@@ -302,7 +301,7 @@ __device__ __forceinline__ void intra_scaled_operands(
     const float (&qv)[32], const float (&kv)[32], const float (&gv)[32], float bt,
     const float *s_E, uint16_t *sKD, uint16_t *sKb, uint8_t *rec, const SwzBases &sb, int l,
     int lr, int gq, bf8 (&QSf)[4], bf8 (&KSf)[4], u4 (&kt_bits)[4], f4 &aqk_d, f4 &akk_d,
-    uint8_t *brec, uint16_t *sQt) {
+    uint8_t *brec, u4 (&qe_bits)[4]) {
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
     float qa[8], ka[8], kb[8], kd[8], kd1[8], kd2[8], kbar[8], qe[8], kt[8];
@@ -341,11 +340,10 @@ __device__ __forceinline__ void intra_scaled_operands(
     // backward's forward-state scan forms no O and reads no Q e^G.
     if constexpr (!BWD) *reinterpret_cast<u4 *>(rec + kOffQ + ((W * 4 + ks) * 64 + l) * 16) = bf8_to_bits(pack8(qe));
     if constexpr (BWD) {
-      // Kbar in A-operand order (m = rows); Q e^G transposed for Qg^T.
+      // Kbar in A-operand order (m = rows); Q e^G kept (bf16) for Qg^T, which
+      // is transposed through LDS at the end of the item.
       *reinterpret_cast<u4 *>(brec + kBOffKbar + ((W * 4 + ks) * 64 + l) * 16) = bf8_to_bits(pack8(kbar));
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        sQt[sb.b[i & 3] + 64 * (32 * ks + 16 * (i >> 2))] = f32_to_bf16_bits(qe[i]);
+      qe_bits[ks] = bf8_to_bits(pack8(qe));
     }
     // Key-side rows of this block for the later query blocks, row-major bf16.
 #pragma unroll
@@ -370,15 +368,14 @@ __device__ __forceinline__ void intra_scaled_operands(
 // Every barrier inside is a work-group barrier: a work-group running two
 // items at once runs them in lock step.
 // BWD: the backward's instantiation, which also writes the backward record,
-// T and P of the item (IntraArgs::brec / tmat / pmat) and needs kSmIntraBwd
-// bytes of LDS.
+// T and P of the item (IntraArgs::brec / tmat / pmat), in the same LDS.
 template <int QKV_DT, int G_DT, bool GATE, bool BWD = false>
 __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int first, int h, uint8_t *smem,
                                            int tid, uint8_t *rec) {
   const size_t item = static_cast<size_t>(c) * p.num_heads + h;
   uint8_t *brec = BWD ? p.brec + item * kBwdRecBytes : nullptr;
-  uint16_t *sQt = reinterpret_cast<uint16_t *>(smem + kSmF);
-  uint16_t *sDo = reinterpret_cast<uint16_t *>(smem + kSmG);
+  uint16_t *sQt = reinterpret_cast<uint16_t *>(smem + kSmA);   // backward, at the end: Q e^G transposed
+  uint16_t *sDo = reinterpret_cast<uint16_t *>(smem + kSmB);   // backward, at the end: dO transposed
   float *s_E = reinterpret_cast<float *>(smem + kSmE);
   uint16_t *sKD = reinterpret_cast<uint16_t *>(smem + kSmA);
   uint16_t *sKt = reinterpret_cast<uint16_t *>(smem + kSmA);
@@ -498,17 +495,6 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
         sV[sb.b[j] + 64 * (32 * (i >> 1) + 16 * (i & 1))] = f32_to_bf16_bits(bt * cc[j]);  // beta V^T
       }
     }
-    if constexpr (BWD) {
-      // dO of this row, transposed (rows past the sequence end are zero).
-      const int64_t drow = ltok * p.do_stride + static_cast<int64_t>(h) * kD;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const f4 d = load4(p.dout, drow + 32 * (i >> 1) + 16 * (i & 1) + 4 * gq, p.do_dtype);
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          sDo[sb.b[j] + 64 * (32 * (i >> 1) + 16 * (i & 1))] = f32_to_bf16_bits(vmask * d[j]);
-      }
-    }
   }
 
   // ---- 2. l2 norms (a row is spread over the 4 lane groups)
@@ -547,12 +533,13 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
   // ---- 4. scaled operands; diagonal 16x16 blocks of A_qk / A_kk
   bf8 QSf[4], KSf[4];           // query side (A operands), all key blocks
   u4 kt_bits[4];                // beta K e^G, bf16, operand order
+  u4 qe_bits[4];                // backward only: Q e^G, bf16 (transposed at the end)
   f4 aqk_d = {0.f, 0.f, 0.f, 0.f}, akk_d = aqk_d;
   switch (w) {
-    case 0: intra_scaled_operands<0, BWD>(qv, kv, gv, bt, s_E, sKD, sKb, rec, sb, l, lr, gq, QSf, KSf, kt_bits, aqk_d, akk_d, brec, sQt); break;
-    case 1: intra_scaled_operands<1, BWD>(qv, kv, gv, bt, s_E, sKD, sKb, rec, sb, l, lr, gq, QSf, KSf, kt_bits, aqk_d, akk_d, brec, sQt); break;
-    case 2: intra_scaled_operands<2, BWD>(qv, kv, gv, bt, s_E, sKD, sKb, rec, sb, l, lr, gq, QSf, KSf, kt_bits, aqk_d, akk_d, brec, sQt); break;
-    default: intra_scaled_operands<3, BWD>(qv, kv, gv, bt, s_E, sKD, sKb, rec, sb, l, lr, gq, QSf, KSf, kt_bits, aqk_d, akk_d, brec, sQt); break;
+    case 0: intra_scaled_operands<0, BWD>(qv, kv, gv, bt, s_E, sKD, sKb, rec, sb, l, lr, gq, QSf, KSf, kt_bits, aqk_d, akk_d, brec, qe_bits); break;
+    case 1: intra_scaled_operands<1, BWD>(qv, kv, gv, bt, s_E, sKD, sKb, rec, sb, l, lr, gq, QSf, KSf, kt_bits, aqk_d, akk_d, brec, qe_bits); break;
+    case 2: intra_scaled_operands<2, BWD>(qv, kv, gv, bt, s_E, sKD, sKb, rec, sb, l, lr, gq, QSf, KSf, kt_bits, aqk_d, akk_d, brec, qe_bits); break;
+    default: intra_scaled_operands<3, BWD>(qv, kv, gv, bt, s_E, sKD, sKb, rec, sb, l, lr, gq, QSf, KSf, kt_bits, aqk_d, akk_d, brec, qe_bits); break;
   }
   lds_barrier();
 
@@ -569,15 +556,6 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
       const u2 lo = *reinterpret_cast<const u2 *>(&sKb[swz(ch, r0)]);
       const u2 hi = *reinterpret_cast<const u2 *>(&sKb[swz(ch, r0 + 16)]);
       *reinterpret_cast<u4 *>(rec + kOffKt + ((mb * 2 + ks) * 64 + l) * 16) = u4{lo.x, lo.y, hi.x, hi.y};
-      if constexpr (BWD) {
-        const u2 qlo = *reinterpret_cast<const u2 *>(&sQt[swz(ch, r0)]);
-        const u2 qhi = *reinterpret_cast<const u2 *>(&sQt[swz(ch, r0 + 16)]);
-        *reinterpret_cast<u4 *>(brec + kBOffQt + ((mb * 2 + ks) * 64 + l) * 16) = u4{qlo.x, qlo.y, qhi.x, qhi.y};
-        // dO B operand of value-column tile nt = mb (k = the same chunk rows).
-        const u2 dlo = *reinterpret_cast<const u2 *>(&sDo[swz(ch, r0)]);
-        const u2 dhi = *reinterpret_cast<const u2 *>(&sDo[swz(ch, r0 + 16)]);
-        *reinterpret_cast<u4 *>(brec + kBOffDo + ((ks * 8 + mb) * 64 + l) * 16) = u4{dlo.x, dlo.y, dhi.x, dhi.y};
-      }
     }
   }
   lds_barrier();
@@ -811,7 +789,48 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
   // A_qk: m = chunk rows 16w + lr, k = chunk rows perm_k(ks, gq, .).  The
   // fragments of K-step 1 for rows 0..31 are zero (A_qk is lower
   // triangular): they are neither written nor read.
-  if constexpr (BWD) return;
+  if constexpr (BWD) {
+    // Qg^T and dO as fragments of the backward record, transposed through
+    // regions A and B (their last reads were in step 8): Q e^G from the
+    // registers of step 4, dO rows loaded here (rows past the sequence end
+    // are zero).
+    const int64_t drow = (valid ? tok : t0) * p.do_stride + static_cast<int64_t>(h) * kD;
+    f4 dov[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dov[i] = load4(p.dout, drow + 32 * (i >> 1) + 16 * (i & 1) + 4 * gq, p.do_dtype);
+    lds_barrier();
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t qword = qe_bits[ks][i >> 1];
+        sQt[sb.b[i & 3] + 64 * (32 * ks + 16 * (i >> 2))] =
+            static_cast<uint16_t>((i & 1) ? (qword >> 16) : (qword & 0xffffu));
+      }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        sDo[sb.b[j] + 64 * (32 * (i >> 1) + 16 * (i & 1))] = f32_to_bf16_bits(vmask * dov[i][j]);
+    lds_barrier();
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi) {
+      const int mb = 2 * w + mi;
+      const int ch = 16 * mb + lr;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int r0 = 32 * ks + 4 * gq;
+        const u2 qlo = *reinterpret_cast<const u2 *>(&sQt[swz(ch, r0)]);
+        const u2 qhi = *reinterpret_cast<const u2 *>(&sQt[swz(ch, r0 + 16)]);
+        *reinterpret_cast<u4 *>(brec + kBOffQt + ((mb * 2 + ks) * 64 + l) * 16) = u4{qlo.x, qlo.y, qhi.x, qhi.y};
+        // dO B operand of value-column tile nt = mb (k = the same chunk rows).
+        const u2 dlo = *reinterpret_cast<const u2 *>(&sDo[swz(ch, r0)]);
+        const u2 dhi = *reinterpret_cast<const u2 *>(&sDo[swz(ch, r0 + 16)]);
+        *reinterpret_cast<u4 *>(brec + kBOffDo + ((ks * 8 + mb) * 64 + l) * 16) = u4{dlo.x, dlo.y, dhi.x, dhi.y};
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
     if (ks == 1 && w < 2) break;
@@ -839,9 +858,9 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
 }
 
 // The backward's instantiation: the same item, plus the backward record, T
-// and P (one work-group per CU: kSmIntraBwd bytes of LDS).
+// and P (two work-groups per CU, as the forward's).
 template <int QKV_DT, int G_DT, bool GATE>
-__global__ __launch_bounds__(kThreads, 1) void kda_chunk_intra_bwd_kernel(IntraArgs p) {
+__global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_bwd_kernel(IntraArgs p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int h = static_cast<int>(blockIdx.x % static_cast<unsigned>(p.num_heads));
   const int c = static_cast<int>(p.max_ch - 1) - static_cast<int>(blockIdx.x / static_cast<unsigned>(p.num_heads));
