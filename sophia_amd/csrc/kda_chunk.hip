@@ -1799,11 +1799,9 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_rscan_kernel(BwdChunkArg
   }
 }
 
-// acc += x . y over the lane group's 8 k values (x[i] = A[m][kb + i],
-// y[i] = B[kb + i][n]) on fp32 MFMA: eight 16x16x4 steps, the k slot of lane
-// group g in step i being 8 g + i.  (bf16 operands here leave dg, and the
-// per-head sums dA_log / ddt_bias over it, 10-40x further from the float64
-// reference: dg is a reverse cumulative sum of terms that cancel.)
+// Products of the gradient kernel.  Plain bf16 operands here leave dg, and
+// the per-head sums dA_log / ddt_bias over it, 10-40x further from the
+// float64 reference (dg is a reverse cumulative sum of terms that cancel).
 // Split products: x = hi + lo with hi = bf16(x) and lo = bf16(x - hi) keeps
 // ~16 mantissa bits, and hi.hi + hi.lo + lo.hi (lo.lo, below 2^-16 of the
 // product, dropped) on bf16 MFMAs with fp32 accumulation takes three 16x16x32
