@@ -184,6 +184,8 @@ __device__ __forceinline__ int first_chunk(const int32_t *cu, int n, int64_t tot
 //  C: Kbar, transposed              bf16  [128][64] swizzled  steps 4-4b
 //     -> A_kk -> T = (I + A_kk)^-1  float [64][68]            steps 5-8
 //  D: A_qk                          bf16  [64][72]            steps 5-10
+//  backward instantiation, after step 9: A <- Q e^G transposed, B <- dO
+//  transposed (swizzled [128][64] bf16 each), read into the backward record
 constexpr int kLdT = 68;    // fp32 row stride of T
 constexpr int kLdKD = 136;  // bf16 row stride of key-side rows / -W
 constexpr int kLdQK = 72;   // bf16 row stride of A_qk
