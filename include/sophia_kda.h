@@ -243,9 +243,20 @@ int sophia_kda_decode_conv_step(const void *x_q, const void *x_k, const void *x_
  *   d_initial_state : [n_seqs, H, 128, 128] or NULL (not computed)
  *   dA_log          : [H] or NULL        (only with SOPHIA_KDA_GATE_IN_KERNEL)
  *   ddt_bias        : [H * 128] or NULL  (only with SOPHIA_KDA_GATE_IN_KERNEL)
+ * Rows outside [cu_seqlens[0], cu_seqlens[n_seqs]) belong to no sequence: their
+ * dq, dk, dv, dg, dbeta are zero and they add nothing to dA_log / ddt_bias.
  * workspace: device memory of sophia_kda_chunk_bwd_workspace_size() bytes,
- * 256-byte aligned.  Arithmetic is fp32 throughout; sums over tokens and value
- * columns run in a fixed order (results are deterministic).
+ * 256-byte aligned.
+ * Arithmetic.  The default chunk form follows the forward's chunk form: its
+ * per-chunk operands (the forward's records, the states and state gradients
+ * fed to the two chunk scans) are bf16 MFMA operands with fp32 accumulation
+ * and fp32 states; the per-chunk gradient products split each fp32 operand
+ * into two bf16 parts (hi + lo, ~16 mantissa bits) and sum hi*hi + hi*lo +
+ * lo*hi in fp32.  Its error against an fp64 backward is that of the forward's
+ * bf16 operands (measured 1.4e-3 to 8e-3 relative, max-norm).  With
+ * SOPHIA_KDA_BWD_RECURRENT in flags the per-token recurrence runs in fp32
+ * throughout (~1e-7 relative, several times slower).  Sums over tokens and
+ * value columns run in a fixed order in both forms (results are deterministic).
  */
 size_t sophia_kda_chunk_bwd_workspace_size(int64_t total_tokens, int n_seqs, int num_heads,
                                            int head_dim);

@@ -679,10 +679,20 @@ __global__ __launch_bounds__(256, 2) void causal_attn_kernel(FaArgs a) {
     kstart = iclamp64(a.cu_k[sq], 0, a.total_k);
     klen = static_cast<int>(iclamp64(a.cu_k[sq + 1], kstart, a.total_k) - kstart);
   }
-  if (klen < 1) return;                           // no key to attend to
-  const int off = klen > len ? klen - len : 0;    // position of query 0 among the keys
   const int q0 = (a.q_blocks - 1 - r % a.q_blocks) * kFaQ;
   if (q0 >= len) return;
+  if (klen < len) {
+    // Fewer keys than queries: no query can be placed at its own key, so the
+    // sequence's output rows are defined as zeros (never left unwritten).
+    const int rows = min(kFaQ, len - q0);
+    for (int i = tid; i < rows * (kFaD / 4); i += 256) {
+      const int64_t row = start + q0 + i / (kFaD / 4);
+      *reinterpret_cast<u2 *>(a.out + row * a.out_stride + static_cast<int64_t>(h) * kFaD + 4 * (i % (kFaD / 4))) =
+          u2{0u, 0u};
+    }
+    return;
+  }
+  const int off = klen - len;                     // position of query 0 among the keys
   const int kend = min(klen, q0 + off + kFaQ);    // keys needed by this work-group
   const int nkb = (kend + kFaK - 1) / kFaK;
   const int wq0 = q0 + 32 * w;                    // first query of this wavefront

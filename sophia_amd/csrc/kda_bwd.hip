@@ -534,13 +534,46 @@ __global__ __launch_bounds__(kD) void kda_bwd_post_kernel(BwdArgs a) {
   }
 }
 
+// Token rows [lo, hi) covered by the sequences: cu[0] .. cu[n], clamped into
+// [0, total] as every kernel clamps the offsets.
+__device__ __forceinline__ void covered_rows(const BwdArgs &a, int64_t &lo, int64_t &hi) {
+  lo = iclamp64(a.cu[0], 0, a.total);
+  hi = iclamp64(a.cu[a.n_seqs], lo, a.total);
+}
+
+// ---- rows outside every sequence ---------------------------------------------------
+// A batch whose offsets end before its last row (cu[n] < total, or cu[0] > 0)
+// has rows no sequence covers; their gradients are zero.  Grid-stride over
+// those rows only (usually none).
+constexpr int kZeroBlocks = 64;
+__global__ __launch_bounds__(256) void kda_bwd_zero_outside_kernel(BwdArgs a) {
+  int64_t lo, hi;
+  covered_rows(a, lo, hi);
+  const int64_t per_row = static_cast<int64_t>(a.num_heads) * kD;
+  const int64_t outside = (lo + (a.total - hi)) * per_row;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < outside;
+       i += static_cast<int64_t>(kZeroBlocks) * 256) {
+    const int64_t r = i / per_row;
+    const int64_t row = r < lo ? r : hi + (r - lo);
+    const int64_t e = row * per_row + (i - r * per_row);
+    a.dq[e] = 0.f;
+    a.dk[e] = 0.f;
+    a.dv[e] = 0.f;
+    a.dg[e] = 0.f;
+    if (i - r * per_row < a.num_heads) a.dbeta[row * a.num_heads + (i - r * per_row)] = 0.f;
+  }
+}
+
 // ---- gate parameters ---------------------------------------------------------------
-// g = lb sigmoid(e^A_log (z + b)): dA_log = sum dz (z + b), ddt_bias = sum dz.
+// g = lb sigmoid(e^A_log (z + b)): dA_log = sum dz (z + b), ddt_bias = sum dz,
+// over the rows the sequences cover.
 __global__ __launch_bounds__(kD) void kda_bwd_gate_partial_kernel(BwdArgs a) {
   const int h = blockIdx.x, part = blockIdx.y, c = threadIdx.x;
-  const int64_t per = (a.total + kGateParts - 1) / kGateParts;
-  const int64_t t_lo = imin64(static_cast<int64_t>(part) * per, a.total);
-  const int64_t t_hi = imin64(t_lo + per, a.total);
+  int64_t lo, hi;
+  covered_rows(a, lo, hi);
+  const int64_t per = (hi - lo + kGateParts - 1) / kGateParts;
+  const int64_t t_lo = imin64(lo + static_cast<int64_t>(part) * per, hi);
+  const int64_t t_hi = imin64(t_lo + per, hi);
   const float b = a.dt_bias[h * kD + c];
   float sb = 0.f, sa = 0.f;
   for (int64_t tok = t_lo; tok < t_hi; ++tok) {
@@ -730,6 +763,10 @@ extern "C" int sophia_kda_chunk_bwd(const void *q, const void *k, const void *v,
     hipLaunchKernelGGL(kda_bwd_post_kernel, dim3(static_cast<unsigned>(total_tokens), num_heads), dim3(kD), 0, st,
                        a);
     if (const int rc = check_launch("kda_bwd_post")) return rc;
+  }
+  if (total_tokens > 0) {
+    hipLaunchKernelGGL(kda_bwd_zero_outside_kernel, dim3(kZeroBlocks), dim3(256), 0, st, a);
+    if (const int rc = check_launch("kda_bwd_zero_outside")) return rc;
   }
   if (gate && (dA_log || ddt_bias)) {
     hipLaunchKernelGGL(kda_bwd_gate_partial_kernel, dim3(num_heads, kGateParts), dim3(kD), 0, st, a);

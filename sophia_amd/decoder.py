@@ -139,7 +139,7 @@ class SophiaMLA(nn.Module):
         unless the sequences are equal-length and start from empty caches."""
         if q.dtype == torch.bfloat16:
             ops.causal_attention(q, k, v, cu, max_len, scale=self.head_dim ** -0.5, cu_seqlens_k=cu_k,
-                                 out=out)
+                                 out=out, cu_seqlens_host=cu_host, cu_seqlens_k_host=cu_k_host)
             return
         if cu_host is None:
             n = int(q.size(0)) // max_len
@@ -176,7 +176,7 @@ class SophiaMLA(nn.Module):
         k = self.k_up(latent_full).view(bsz, klen, self.num_heads, self.head_dim)
         v = self.v_up(latent_full).view_as(k)
         q_t, k_t, v_t = (t.transpose(1, 2) for t in (q, k, v))
-        key_pad = self._resolve_key_pad(int(start_pos), bsz, klen, x.device)
+        key_pad = self._key_mask(int(start_pos), bsz, klen, x.device)
         if key_pad is None and int(start_pos) == 0 and seqlen == klen:
             rows = bsz * seqlen
             cu = torch.arange(0, rows + 1, seqlen, dtype=torch.int32, device=x.device)
@@ -195,21 +195,24 @@ class SophiaMLA(nn.Module):
             out = F.scaled_dot_product_attention(q_t, k_t, v_t, attn_mask=mask)
         return self._gate_out(x, out.transpose(1, 2))
 
-    def _resolve_key_pad(self, start_pos: int, bsz: int, k_len: int, device):
-        """attention.py:585-600: which key positions are real."""
+    def _key_mask(self, start_pos: int, bsz: int, k_len: int, device):
+        """Which of the ``k_len`` key positions of each row are real tokens, or
+        None when all are (the behaviour of attention.py:585-600).
+
+        The rule: a prompt (start_pos 0) takes the pad mask set on the module
+        before it ran (``set_pad_mask``); that mask is remembered, and keys
+        at later positions (tokens generated after the prompt) are real.  A
+        mask longer than ``k_len`` is cut to it.
+        """
         if int(start_pos) == 0:
-            mask = getattr(self, "_pad_mask", None)
-            self._key_pad = None if mask is None else mask[:bsz].bool().to(device)
-            return self._key_pad
-        cached = getattr(self, "_key_pad", None)
-        if cached is None:
+            given = getattr(self, "_pad_mask", None)
+            self._prompt_mask = None if given is None else given[:bsz].to(device=device, dtype=torch.bool)
+        prompt = getattr(self, "_prompt_mask", None)
+        if prompt is None:
             return None
-        prompt_len = int(cached.size(1))
-        if k_len <= prompt_len:
-            return cached[:bsz, :k_len]
-        grown = torch.ones((bsz, k_len), dtype=torch.bool, device=device)
-        grown[:, :prompt_len] = cached[:bsz]
-        return grown
+        known = prompt[:bsz, :k_len]
+        missing = int(k_len) - int(known.size(1))
+        return F.pad(known, (0, missing), value=True) if missing > 0 else known
 
     def forward_mixed(self, x: torch.Tensor, step: dict) -> torch.Tensor:
         """Packed continuous-batching step (``step`` from Transformer.forward_step).
@@ -607,6 +610,11 @@ class Transformer(nn.Module):
             raise ValueError("decode_slots and decode_pos need one entry per decode token")
         if n_p + D == 0:
             raise ValueError("empty step")
+        if D and not 1 <= int(max_decode_len) <= int(self.args.max_seq_len):
+            # decode rows write their latent at pos < max_decode_len: checked
+            # here, before any launch (transformer.py:155-160 raises the same)
+            raise ValueError("sequence exceeds max_seq_len" if int(max_decode_len) > 0
+                             else "max_decode_len must bound pos + 1 of every decode row")
         _require_gpu(prefill_ids if n_p else decode_ids)
         reads = any(p > 0 for p in pos)
         rect = n_p > 0 and not reads and min(lens) == max(lens)

@@ -914,7 +914,8 @@ def mla_decode_attn(qa: torch.Tensor, latent_cache: torch.Tensor, slots: torch.T
 def causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor,
                      max_len: int, *, scale: float | None = None,
                      cu_seqlens_k: torch.Tensor | None = None,
-                     out: torch.Tensor | None = None) -> torch.Tensor:
+                     out: torch.Tensor | None = None, cu_seqlens_host: torch.Tensor | None = None,
+                     cu_seqlens_k_host: torch.Tensor | None = None) -> torch.Tensor:
     """Causal self-attention within each packed sequence (the prefill
     attention of SophiaMLA, ml/runtime/model/attention.py:630-654,
     ``scaled_dot_product_attention`` with a causal mask).
@@ -925,7 +926,12 @@ def causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqle
     than queries continues after cached tokens: its queries are the last
     positions of its key range (the tril(keys - queries) mask).  ``max_len``
     (host int) must bound every sequence's query count.  Returns [rows, heads,
-    128] bf16 (or writes ``out``, which may be a row-strided view)."""
+    128] bf16 (or writes ``out``, which may be a row-strided view).
+
+    Every sequence needs at least as many keys as queries.  With the host
+    copies of the offsets (``cu_seqlens_host``, ``cu_seqlens_k_host``) that is
+    checked here (RuntimeError); without them the kernel writes zeros for the
+    rows of a sequence that has fewer keys than queries."""
     for t, name in ((q, "q"), (k, "k"), (v, "v")):
         _gpu(t, name)
         if t.dtype != torch.bfloat16:
@@ -945,6 +951,13 @@ def causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqle
         raise RuntimeError("q, k and v must have the same number of rows without cu_seqlens_k")
     if cuk is not None and int(cuk.numel()) != int(cu.numel()):
         raise RuntimeError("cu_seqlens_k must have as many entries as cu_seqlens")
+    if cu_seqlens_host is not None:
+        qo = torch.as_tensor(cu_seqlens_host).to("cpu", torch.int64)
+        ko = qo if cu_seqlens_k_host is None else torch.as_tensor(cu_seqlens_k_host).to("cpu", torch.int64)
+        if int(qo.numel()) != int(cu.numel()) or int(ko.numel()) != int(cu.numel()):
+            raise RuntimeError("host offsets must have as many entries as cu_seqlens")
+        if bool(((ko[1:] - ko[:-1]) < (qo[1:] - qo[:-1])).any()):
+            raise RuntimeError("every sequence needs at least as many keys as queries")
     y = out if out is not None else torch.empty((total, heads, hd), dtype=q.dtype, device=q.device)
     if y.dtype != torch.bfloat16 or tuple(y.shape) != (total, heads, hd):
         raise RuntimeError(f"out must be bfloat16 [{total}, {heads}, {hd}]")

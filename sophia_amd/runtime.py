@@ -107,19 +107,21 @@ def forward_cached_decode(*, model: Transformer, input_ids: torch.Tensor,
     if input_ids.dim() != 2 or int(input_ids.size(1)) <= 0:
         raise ValueError("input_ids must be [B, T] with T >= 1")
     bsz, seqlen = int(input_ids.size(0)), int(input_ids.size(1))
+    # Every check runs before the caches are touched or anything is launched.
+    cache_pos = 0 if cache_state is None else int(cache_state.cache_pos)
+    if cache_pos + seqlen > int(model.args.max_seq_len):
+        raise ValueError("sequence exceeds max_seq_len")
     if cache_state is None:
         if start_pos is not None and int(start_pos) != 0:
             raise ValueError("cache_state is required when start_pos > 0 for cached decode")
         model.ensure_batch_capacity(bsz)
         model.reset_runtime_cache()
-        cache_pos = 0
     else:
-        cache_state = cache_state.clone()
-        cache_pos = int(cache_state.cache_pos)
         if cache_pos < 0:
             raise ValueError(f"cache cache_pos must be >= 0, got {cache_pos}")
         if start_pos is not None and int(start_pos) != cache_pos:
             raise ValueError(f"start_pos ({start_pos}) must match cache cache_pos ({cache_pos})")
+        cache_state = cache_state.clone()
         batch = int(cache_state.batch_size or bsz)
         if batch <= 0:
             raise ValueError(f"cache batch_size must be > 0, got {batch}")

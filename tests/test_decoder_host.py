@@ -49,3 +49,30 @@ def test_append_with_flattened_token_rows():
     a, b = torch.randn(1, 32), torch.randn(1, 32)
     completed = _append_block(_append_block(completed, a), b)
     assert torch.equal(completed, torch.stack((a, b), dim=-2))
+
+
+def test_mla_key_mask_follows_prompt_mask_then_marks_generated_keys_real():
+    """SophiaMLA's key mask (behaviour of attention.py:585-600): the prompt's
+    keys follow the pad mask given before the prompt, later keys are real, a
+    longer mask is cut, and no mask means no masking."""
+    from sophia_amd.config import ModelArgs
+    from sophia_amd.decoder import SophiaMLA
+
+    args = ModelArgs(dim=32, num_heads=2, head_dim=128, mla_q_rank=8, mla_kv_rank=4, max_batch_size=3,
+                     max_seq_len=16)
+    mla = SophiaMLA(args)
+    assert mla._key_mask(0, 2, 5, "cpu") is None
+    assert mla._key_mask(5, 2, 6, "cpu") is None
+    prompt = torch.tensor([[False, True, True, True],
+                           [True, True, True, True],
+                           [False, False, True, True]])
+    mla._pad_mask = prompt
+    got = mla._key_mask(0, 2, 4, "cpu")
+    assert got.dtype == torch.bool and torch.equal(got, prompt[:2])
+    mla._pad_mask = None   # later steps keep the prompt's mask
+    assert torch.equal(mla._key_mask(4, 2, 3, "cpu"), prompt[:2, :3])
+    grown = mla._key_mask(4, 2, 7, "cpu")
+    assert torch.equal(grown[:, :4], prompt[:2]) and bool(grown[:, 4:].all()) and grown.shape == (2, 7)
+    assert torch.equal(mla._key_mask(4, 1, 6, "cpu"), grown[:1, :6])
+    # a new prompt without a mask clears it
+    assert mla._key_mask(0, 2, 4, "cpu") is None and mla._key_mask(4, 2, 5, "cpu") is None

@@ -369,6 +369,42 @@ def test_causal_attention_after_cached_keys_matches_reference(queries, keys, hea
     assert err <= 1e-2, err
 
 
+def test_causal_attention_with_fewer_keys_than_queries():
+    """A sequence with fewer keys than queries (0 keys, or 3 keys for 200
+    queries) has no causal alignment: with device offsets only, the kernel
+    writes zeros for its rows (never leaves them unwritten) and the other
+    sequences are unaffected; with the host offsets the call is rejected
+    before any launch."""
+    from sophia_amd import ops
+    dev = _dev()
+    g = torch.Generator(device="cpu").manual_seed(91)
+    queries, keys, heads = (5, 200, 70, 9), (9, 3, 70, 0), 2
+    tq, tk = sum(queries), sum(keys)
+    cu = torch.tensor([0] + list(np.cumsum(queries)), dtype=torch.int32)
+    cuk = torch.tensor([0] + list(np.cumsum(keys)), dtype=torch.int32)
+    q = torch.randn(tq, heads, 128, generator=g).to(dev, torch.bfloat16)
+    k = torch.randn(tk, heads, 128, generator=g).to(dev, torch.bfloat16)
+    v = torch.randn(tk, heads, 128, generator=g).to(dev, torch.bfloat16)
+    out = torch.full((tq, heads, 128), 7.0, dtype=torch.bfloat16, device=dev)
+    scale = 128 ** -0.5
+    y = ops.causal_attention(q, k, v, cu.to(dev), max(queries), scale=scale, cu_seqlens_k=cuk.to(dev), out=out)
+    torch.cuda.synchronize()
+    yc = y.float().cpu()
+    for s in (1, 3):
+        assert bool((yc[int(cu[s]):int(cu[s + 1])] == 0).all()), f"sequence {s} rows not zero"
+    qf, kf, vf = (t.float().cpu() for t in (q, k, v))
+    for s in (0, 2):
+        a, b, ka, kb = int(cu[s]), int(cu[s + 1]), int(cuk[s]), int(cuk[s + 1])
+        nq, nk = b - a, kb - ka
+        sc = torch.einsum("thd,shd->hts", qf[a:b], kf[ka:kb]) * scale
+        sc = sc.masked_fill(~torch.ones(nq, nk, dtype=torch.bool).tril(nk - nq), float("-inf"))
+        ref = torch.einsum("hts,shd->thd", torch.softmax(sc, dim=-1), vf[ka:kb])
+        assert float((yc[a:b] - ref).abs().max()) <= 1e-2 * float(ref.abs().max())
+    with pytest.raises(RuntimeError, match="at least as many keys"):
+        ops.causal_attention(q, k, v, cu.to(dev), max(queries), scale=scale, cu_seqlens_k=cuk.to(dev),
+                             cu_seqlens_host=cu, cu_seqlens_k_host=cuk)
+
+
 def test_mla_prefill_bf16_kernel_matches_sdpa_path():
     """SophiaMLA.forward in bf16 (HIP causal kernel) against the same module in
     fp32 (torch SDPA) on the same weights and input."""

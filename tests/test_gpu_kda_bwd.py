@@ -39,7 +39,10 @@ def _rel(a, b) -> float:
     return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30))
 
 
-def _inputs(cu, heads, *, seed, gated, dtype, h0=True, dht=True):
+def _inputs(cu, heads, *, seed, gated, dtype, h0=True, dht=True, gb_dtype=torch.float32):
+    """Seeded inputs; ``gb_dtype`` is the dtype of g and beta (bf16 as the
+    reference's training seam passes decay_logits / beta_logits; the oracle
+    then gets the bf16-rounded values)."""
     gen = torch.Generator().manual_seed(seed)
     total, n = cu[-1], len(cu) - 1
 
@@ -61,6 +64,8 @@ def _inputs(cu, heads, *, seed, gated, dtype, h0=True, dht=True):
         inp["k"] = torch.nn.functional.normalize(inp["k"].float(), dim=-1).to(dtype)
         inp["g"] = -5.0 * torch.rand(total, heads, D, generator=gen)
         inp["beta"] = torch.rand(total, heads, generator=gen)
+    inp["g"] = inp["g"].to(gb_dtype)
+    inp["beta"] = inp["beta"].to(gb_dtype)
     inp["h0"] = rnd(n, heads, D, D, scale=0.1) if h0 else None
     d_out = rnd(total, heads, D).to(dtype)
     d_final = rnd(n, heads, D, D, scale=0.1) if dht else None
@@ -68,7 +73,7 @@ def _inputs(cu, heads, *, seed, gated, dtype, h0=True, dht=True):
     return inp, d_out, d_final, flags
 
 
-def _hip(inp, cu, d_out, d_final, flags, recurrent=True):
+def _hip(inp, cu, d_out, d_final, flags, recurrent=True, host_offsets=True):
     dev = "cuda"
     cu_t = torch.tensor(cu, dtype=torch.int32)
     res = torch.ops.sophia.kda_chunk_bwd(
@@ -78,7 +83,7 @@ def _hip(inp, cu, d_out, d_final, flags, recurrent=True):
         None if inp.get("dt_bias") is None else inp["dt_bias"].to(dev), D ** -0.5, -5.0,
         flags["use_qk_l2norm"], flags["use_gate"], flags["use_beta_sigmoid"],
         None if inp["h0"] is None else inp["h0"].to(dev),
-        None if d_final is None else d_final.to(dev), cu_t, recurrent)
+        None if d_final is None else d_final.to(dev), cu_t if host_offsets else None, recurrent)
     names = ("q", "k", "v", "g", "beta", "h0", "A_log", "dt_bias")
     return {name: t.cpu().numpy() for name, t in zip(names, res)}
 
@@ -169,12 +174,14 @@ def test_bwd_linear_in_cotangent_at_size():
         assert err <= 1e-4, f"d{name}: {err:.3e}"
 
 
-def test_autograd_through_chunk_kda():
+@pytest.mark.parametrize("gb_dtype", [torch.float32, torch.bfloat16])
+def test_autograd_through_chunk_kda(gb_dtype):
     """ops.chunk_kda / flash_kda with requires_grad inputs: loss.backward()
     fills every leaf's .grad in its own shape and dtype with the oracle's
-    gradients (through the chunk form)."""
+    gradients (through the chunk form).  bf16 g and beta are what the
+    reference's training seam passes (decay_logits, beta_logits)."""
     cu = [0, 70, 150]
-    inp, d_out, d_final, flags = _inputs(cu, 2, seed=37, gated=True, dtype=torch.bfloat16)
+    inp, d_out, d_final, flags = _inputs(cu, 2, seed=37, gated=True, dtype=torch.bfloat16, gb_dtype=gb_dtype)
     dev = "cuda"
     leaves = {name: t.to(dev).clone().requires_grad_(True) for name, t in inp.items()}
     o, ht = ops.flash_kda(
@@ -218,25 +225,61 @@ def test_no_grad_path_unchanged():
 
 
 # ---- the chunk form -----------------------------------------------------------
-@pytest.mark.parametrize("gated,dtype", [(True, torch.float32), (True, torch.bfloat16),
-                                         (False, torch.float32), (False, torch.bfloat16)])
-def test_chunk_bwd_matches_oracle_ragged(gated, dtype):
+@pytest.mark.parametrize("gated,dtype,gb_dtype", [
+    (True, torch.float32, torch.float32), (True, torch.bfloat16, torch.float32),
+    (False, torch.float32, torch.float32), (False, torch.bfloat16, torch.float32),
+    (True, torch.bfloat16, torch.bfloat16), (False, torch.bfloat16, torch.bfloat16)])
+def test_chunk_bwd_matches_oracle_ragged(gated, dtype, gb_dtype):
     """The chunk form on a ragged batch: an empty sequence, partial and full
-    chunks, initial and final-state terms."""
+    chunks, initial and final-state terms; g and beta in fp32 or in bf16 (the
+    training seam's dtype: the bf16 g/beta instantiations of the intra and
+    gradient kernels and the gate kernels' bf16 loads)."""
     cu = [0, 37, 37, 166, 230]
-    inp, d_out, d_final, flags = _inputs(cu, 2, seed=5, gated=gated, dtype=dtype)
+    inp, d_out, d_final, flags = _inputs(cu, 2, seed=5, gated=gated, dtype=dtype, gb_dtype=gb_dtype)
     _compare(_hip(inp, cu, d_out, d_final, flags, recurrent=False),
-             _oracle(inp, cu, d_out, d_final, flags), f"chunk ragged gated={gated} {dtype}", TOL_CHUNK)
+             _oracle(inp, cu, d_out, d_final, flags), f"chunk ragged gated={gated} {dtype} g/beta {gb_dtype}",
+             TOL_CHUNK)
 
 
-@pytest.mark.parametrize("gated", [True, False])
-def test_chunk_bwd_matches_oracle_long_sequence(gated):
+@pytest.mark.parametrize("gated,gb_dtype", [(True, torch.float32), (False, torch.float32),
+                                            (True, torch.bfloat16), (False, torch.bfloat16)])
+def test_chunk_bwd_matches_oracle_long_sequence(gated, gb_dtype):
     """One 1,000-token sequence: 16 chunk steps of each chunk scan."""
     cu = [0, 1000]
     inp, d_out, d_final, flags = _inputs(cu, 1, seed=9, gated=gated, dtype=torch.bfloat16,
-                                         h0=False, dht=False)
+                                         h0=False, dht=False, gb_dtype=gb_dtype)
     _compare(_hip(inp, cu, d_out, d_final, flags, recurrent=False),
-             _oracle(inp, cu, d_out, d_final, flags), f"chunk long gated={gated}", TOL_CHUNK)
+             _oracle(inp, cu, d_out, d_final, flags), f"chunk long gated={gated} g/beta {gb_dtype}", TOL_CHUNK)
+
+
+@pytest.mark.parametrize("recurrent", [False, True])
+def test_bwd_rows_outside_the_sequences_get_zero_gradients(recurrent):
+    """Offsets that stop before the last row (cu[-1] < total) and start after
+    row 0, given on the device only (so the host cannot check them): the rows
+    no sequence covers hold NaN inputs and NaN output gradients, yet get zero
+    gradients and add nothing to dA_log / ddt_bias; the covered rows match the
+    oracle on the sequences alone."""
+    cu = [0, 37, 166]
+    inp, d_out, d_final, flags = _inputs(cu, 2, seed=83, gated=True, dtype=torch.bfloat16,
+                                         gb_dtype=torch.bfloat16)
+    want = _oracle(inp, cu, d_out, d_final, flags)
+    lead, tail = 5, 29
+    total = cu[-1] + lead + tail
+
+    def pad(t):
+        out = torch.full((total,) + tuple(t.shape[1:]), float("nan"), dtype=t.dtype)
+        out[lead:lead + cu[-1]] = t
+        return out
+
+    padded = {name: (pad(t) if name in ("q", "k", "v", "g", "beta") else t) for name, t in inp.items()}
+    cu_p = [c + lead for c in cu]
+    got = _hip(padded, cu_p, pad(d_out), d_final, flags, recurrent=recurrent, host_offsets=False)
+    inside = slice(lead, lead + cu[-1])
+    for name in ("q", "k", "v", "g", "beta"):
+        outside = np.concatenate([got[name][:lead], got[name][lead + cu[-1]:]])
+        assert np.array_equal(outside, np.zeros_like(outside)), f"d{name} outside the sequences"
+        got[name] = got[name][inside]
+    _compare(got, want, f"padded batch recurrent={recurrent}", TOL if recurrent else TOL_CHUNK)
 
 
 def test_chunk_bwd_matches_torch_autograd_restatement():

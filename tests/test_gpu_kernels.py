@@ -500,18 +500,22 @@ def test_decode_step_config3_batch256():
     assert bool((state - s0.to(dev)).abs().amax(dim=(1, 2, 3)).gt(0).all())
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_decode_conv_step_matches_separate_launches_and_oracle(dtype):
+@pytest.mark.parametrize("dtype,batch,heads,n_slots", [
+    (torch.float32, 9, 3, 10), (torch.bfloat16, 9, 3, 10),
+    (torch.bfloat16, 240, 16, 256)])   # the mixed step's 240 decode rows, 16 heads, fused conv cache [256, 6144, 3]
+def test_decode_conv_step_matches_separate_launches_and_oracle(dtype, batch, heads, n_slots):
     """sophia_kda_decode_conv_step (ShortConv step + recurrent step in one
     launch) against short_conv_step followed by kda_decode_step: the conv
     history is bit-identical; outputs and states agree to rounding (the fused
     kernel runs one work-group of 128 value columns, which sums the column
-    reductions in another order); both against the oracle.  Includes a row
-    whose slot is out of range (output 0, no cache touched)."""
+    reductions in another order); sampled rows against the float64 oracle.
+    The small case includes a row whose slot is out of range (output 0, no
+    cache touched); the large one runs the mixed step's decode shape, where
+    the channel offsets of every head (up to 3 x 2048) into the fused conv
+    cache are exercised."""
     from sophia_amd import ops
     dev = _dev()
-    rng = np.random.default_rng(21)
-    batch, heads = 9, 3
+    rng = np.random.default_rng(21 + batch)
     inner = heads * 128
     x = rng.standard_normal((batch, 3 * inner)).astype(np.float32)
     w = (rng.standard_normal((3 * inner, 4)) * 0.5).astype(np.float32)
@@ -519,9 +523,14 @@ def test_decode_conv_step_matches_separate_launches_and_oracle(dtype):
     b = rng.standard_normal((batch, heads)).astype(np.float32)
     a_log = (rng.standard_normal(heads) * 0.3).astype(np.float32)
     dtb = ko.inverse_softplus(np.exp(rng.uniform(np.log(1e-3), np.log(1e-1), inner))).astype(np.float32)
-    slots = np.array([4, 0, 9, 2, 7, 1, 8, 3, 11], dtype=np.int32)   # 11 is out of range
-    s0 = (rng.standard_normal((10, heads, 128, 128)) * 0.02).astype(np.float32)
-    c0 = rng.standard_normal((10, 3 * inner, 3)).astype(np.float32)
+    if batch == 9:
+        slots = np.array([4, 0, 9, 2, 7, 1, 8, 3, 11], dtype=np.int32)   # 11 is out of range
+        sample = np.array([0, 1, 2, 3, 4, 5, 6, 7])
+    else:
+        slots = rng.permutation(n_slots)[:batch].astype(np.int32)
+        sample = np.array([0, 57, 118, 239])
+    s0 = (rng.standard_normal((n_slots, heads, 128, 128)) * 0.02).astype(np.float32)
+    c0 = rng.standard_normal((n_slots, 3 * inner, 3)).astype(np.float32)
     xt = torch.tensor(x).to(dtype).to(dev)
     wt = torch.tensor(w).to(dtype).float().to(dev)             # taps rounded to the activation dtype
     kw = dict(A_log=torch.tensor(a_log), dt_bias=torch.tensor(dtb), state_slots=torch.tensor(slots, device=dev))
@@ -539,18 +548,26 @@ def test_decode_conv_step_matches_separate_launches_and_oracle(dtype):
     tol = 1e-4 if dtype == torch.float32 else 1e-2
     assert _rel(_np(o_b), _np(o_a)) < tol
     assert _rel(_np(st_b), _np(st_a)) < 1e-5
-    assert np.all(_np(o_b)[8] == 0.0)
-    untouched = [5, 6]
+    if batch == 9:
+        assert np.all(_np(o_b)[8] == 0.0)
+    untouched = np.setdiff1d(np.arange(n_slots), slots)
     assert torch.equal(st_b[untouched], torch.tensor(s0[untouched], device=dev))
-    # oracle: conv step then recurrent step in float64
-    ok = slots < 10
-    xs = _np(xt)[ok]
-    hist = c0[slots[ok]]
+    assert torch.equal(cs_b[untouched], torch.tensor(c0[untouched], device=dev))
+    # the history of every used slot moved by one token (the kept samples
+    # rounded to the activation dtype, as the step reads them); its last
+    # column is the new input
+    used = slots[slots < n_slots]
+    rows = np.nonzero(slots < n_slots)[0]
+    np.testing.assert_array_equal(_np(cs_b)[used][:, :, :2], _np(torch.tensor(c0[used][:, :, 1:]).to(dtype)))
+    np.testing.assert_array_equal(_np(cs_b)[used][:, :, 2], _np(xt.float())[rows])
+    # oracle on the sampled rows: conv step then recurrent step in float64
+    xs = _np(xt)[sample]
+    hist = c0[slots[sample]]
     hist_in = _np(torch.tensor(hist).to(dtype)) if dtype == torch.bfloat16 else hist
     yr, _ = ko.short_conv(xs[:, None].astype(np.float64), _np(wt).astype(np.float64), hist_in.astype(np.float64))
     yr = _np(torch.tensor(yr[:, 0]).to(dtype))
     qr, kr, vr = (yr[:, i * inner:(i + 1) * inner].reshape(-1, heads, 128) for i in range(3))
-    o_ref, s_ref = ko.kda_decode_step(qr, kr, vr, z[ok], b[ok], s0[slots[ok]], A_log=a_log, dt_bias=dtb,
-                                      dtype=np.float64)
-    assert _rel(_np(o_b)[ok], o_ref) < REL_TOL
-    assert _rel(_np(st_b)[slots[ok]], s_ref) < REL_TOL
+    o_ref, s_ref = ko.kda_decode_step(qr, kr, vr, z[sample], b[sample], s0[slots[sample]], A_log=a_log,
+                                      dt_bias=dtb, dtype=np.float64)
+    assert _rel(_np(o_b)[sample], o_ref) < REL_TOL
+    assert _rel(_np(st_b)[slots[sample]], s_ref) < REL_TOL

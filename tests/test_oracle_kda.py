@@ -289,3 +289,67 @@ def test_rms_norm_weight_matches_torch():
         np.testing.assert_allclose(ko.rms_norm(x, w, eps), ref, rtol=1e-12, atol=1e-12)
     # a scaled weight scales the output channel by channel
     np.testing.assert_allclose(ko.rms_norm(x, 2.0 * w, 1e-5), 2.0 * ko.rms_norm(x, w, 1e-5), rtol=1e-12)
+
+
+def _epilogue_params(rng, heads=2, hd=8, gate_scale=0.0):
+    """A tiny mixer (dim == inner, o_proj = identity) whose output is the
+    epilogue RMSNorm(o) * sigmoid(x Wg^T) itself."""
+    inner = heads * hd
+    p = {name: rng.standard_normal((inner, inner)) * 0.3 for name in ("q_proj.weight", "k_proj.weight",
+                                                                       "v_proj.weight")}
+    for name in ("q_conv", "k_conv", "v_conv"):
+        p[f"{name}.weight"] = rng.standard_normal((inner, 4)) * 0.4
+    p["decay_down.weight"] = rng.standard_normal((4, inner)) * 0.2
+    p["decay_up.weight"] = rng.standard_normal((inner, 4)) * 0.2
+    p["beta_proj.weight"] = rng.standard_normal((heads, inner)) * 0.3
+    p["A_log"] = np.zeros(heads)
+    p["dt_bias"] = ko.inverse_softplus(np.exp(rng.uniform(np.log(1e-3), np.log(1e-1), inner)))
+    p["output_gate.weight"] = rng.standard_normal((inner, inner)) * gate_scale
+    p["output_norm.weight"] = rng.uniform(0.5, 1.5, hd)
+    p["o_proj.weight"] = np.eye(inner)
+    return p
+
+
+def _unit_ms_defect(y, gate, w, heads, hd):
+    """max over (token, head) of |mean((y / (gate * w))^2) - 1|."""
+    unit = (y / gate).reshape(-1, heads, hd) / w
+    return np.abs((unit ** 2).mean(-1) - 1.0).max()
+
+
+@pytest.mark.parametrize("gate_scale", [0.0, 1.5])
+def test_mixer_epilogue_is_norm_then_sigmoid_gate(gate_scale):
+    """attention.py:411-420: y = o_proj(RMSNorm_head(o; w) * sigmoid(x Wg^T)).
+    With o_proj = I and a tiny eps, y / (sigmoid(x Wg^T) * w) is o scaled to unit
+    mean square in every (token, head).  Mistakes planted in a copy of the
+    epilogue (gate before the norm, sigmoid dropped, norm over the whole row,
+    norm weight dropped) each break that.  With Wg = 0 the gate is exactly 1/2."""
+    heads, hd = 2, 8
+    rng = _rng(31)
+    p = _epilogue_params(rng, heads, hd, gate_scale)
+    w = p["output_norm.weight"]
+    x = rng.standard_normal((1, 7, heads * hd))
+    y = ko.mixer_forward(p, x, num_heads=heads, head_dim=hd, norm_eps=1e-14)
+    logits = x @ p["output_gate.weight"].T
+    gate = ko.sigmoid(logits)
+    if gate_scale == 0.0:
+        np.testing.assert_array_equal(gate, 0.5)
+    assert _unit_ms_defect(y, gate, w, heads, hd) < 1e-9
+    # the recurrence's output, up to a positive scale per (token, head); the
+    # heads are given unequal scales, as raw outputs have
+    o = ((y / gate).reshape(1, 7, heads, hd) / w) * np.array([0.7, 2.9])[:, None]
+    gate4 = gate.reshape(1, 7, heads, hd)
+    planted = {
+        "dropped norm weight": (ko.rms_norm(o, np.ones(hd), 1e-14) * gate4),
+        "whole-row norm": (o / np.sqrt((o ** 2).mean((-2, -1), keepdims=True)) * w * gate4),
+    }
+    if gate_scale:
+        assert np.ptp(gate4, axis=-1).min() > 0.1   # the gate varies over channels
+        planted["gate before the norm"] = ko.rms_norm(o * gate4, w, 1e-14)
+        planted["sigmoid dropped"] = ko.rms_norm(o, w, 1e-14) * logits.reshape(1, 7, heads, hd)
+    for name, bad in planted.items():
+        assert _unit_ms_defect(bad.reshape(y.shape), gate, w, heads, hd) > 1e-2, name
+    # o_proj = P is P applied to the same epilogue output
+    proj = rng.standard_normal((heads * hd - 3, heads * hd))
+    q = dict(p, **{"o_proj.weight": proj})
+    np.testing.assert_allclose(ko.mixer_forward(q, x, num_heads=heads, head_dim=hd, norm_eps=1e-14),
+                               y @ proj.T, rtol=1e-10, atol=1e-12)

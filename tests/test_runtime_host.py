@@ -62,3 +62,38 @@ def test_release_rejects_foreign_and_repeated_slots():
         alloc.release([1])          # already released
     with pytest.raises(ValueError):
         alloc.allocate(-1)
+
+
+def test_cached_decode_past_max_seq_len_raises_before_any_device_work():
+    """forward_cached_decode rejects a step that would write past max_seq_len
+    (transformer.py:155-160: ValueError 'sequence exceeds max_seq_len') before
+    it loads a cache or launches anything: the stand-in model has nothing else."""
+    from sophia_amd.runtime import RuntimeCacheState, forward_cached_decode
+
+    model = types.SimpleNamespace(args=types.SimpleNamespace(max_seq_len=8))
+    full = RuntimeCacheState(cache=None, batch_size=1, cache_pos=8)
+    with pytest.raises(ValueError, match="sequence exceeds max_seq_len"):
+        forward_cached_decode(model=model, input_ids=torch.zeros(1, 1, dtype=torch.long), cache_state=full,
+                              start_pos=8, logits_to_keep=None)
+    near = RuntimeCacheState(cache=None, batch_size=1, cache_pos=6)
+    with pytest.raises(ValueError, match="sequence exceeds max_seq_len"):
+        forward_cached_decode(model=model, input_ids=torch.zeros(1, 3, dtype=torch.long), cache_state=near,
+                              start_pos=6, logits_to_keep=None)
+
+
+def test_mixed_step_decode_bound_is_checked_on_the_host():
+    """Transformer.forward_step: decode rows need 1 <= max_decode_len <= max_seq_len
+    (their latents are written at pos < max_decode_len); the check runs before
+    the device check, so it raises here on the CPU."""
+    from sophia_amd.config import ModelArgs
+    from sophia_amd.decoder import Transformer
+
+    args = ModelArgs(vocab_size=16, n_layers=4, ffn_hidden=8, mla_q_rank=8, mla_kv_rank=4, dim=32,
+                     num_heads=1, head_dim=128, max_seq_len=8, max_batch_size=2)
+    model = Transformer(args)
+    ids = torch.tensor([3])
+    slots = torch.tensor([0], dtype=torch.int32)
+    with pytest.raises(ValueError, match="sequence exceeds max_seq_len"):
+        model.forward_step(decode_ids=ids, decode_slots=slots, decode_pos=torch.tensor([8]), max_decode_len=9)
+    with pytest.raises(ValueError, match="max_decode_len"):
+        model.forward_step(decode_ids=ids, decode_slots=slots, decode_pos=torch.tensor([0]), max_decode_len=0)
