@@ -82,6 +82,24 @@ int sophia_gated_head_norm(const void *o, int64_t o_stride, int o_dtype, const v
                            int heads, int head_dim, int dtype, void *stream);
 
 /*
+ * Backward of sophia_gated_head_norm (training): autograd through
+ * output_norm(o) * sigmoid(output_gate(x)) (attention.py:411-420) and MLA's
+ * o * sigmoid(gate) (attention.py:655-656).  d_out: [rows, heads * head_dim]
+ * gradient of out (dtype); o, gate, norm_weight, eps, dtypes and strides as in
+ * the forward call.  Outputs: d_o (o_dtype, the gradient of o before its
+ * rounding to dtype), d_gate (dtype), and with norm_weight d_norm_weight
+ * [head_dim] fp32, summed over rows and heads in a fixed order
+ * (deterministic).  workspace: sophia_gated_head_norm_bwd_workspace_size()
+ * bytes (used only with norm_weight).  head_dim a power of two in [8, 256].
+ */
+size_t sophia_gated_head_norm_bwd_workspace_size(int64_t rows, int heads, int head_dim);
+int sophia_gated_head_norm_bwd(const void *d_out, int64_t d_out_stride, const void *o, int64_t o_stride,
+                               int o_dtype, const void *gate, int64_t gate_stride, const float *norm_weight,
+                               float eps, void *d_o, int64_t d_o_stride, void *d_gate, int64_t d_gate_stride,
+                               float *d_norm_weight, int64_t rows, int heads, int head_dim, int dtype,
+                               void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * Absorbed MLA decode attention over the fp32 latent cache; replaces the
  * decode-row attention of SophiaMLA with NoPE (ml/runtime/model/attention.py:
  * 609-657 with a cache, keys = k_up(c), values = v_up(c)), written in latent

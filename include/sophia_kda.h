@@ -103,6 +103,31 @@ int sophia_short_conv_step(const void *x, int64_t x_row_stride, void *y, int64_t
                            int read_history, void *stream);
 
 /*
+ * Backward of sophia_short_conv_fwd (training): the gradients of x and of the
+ * taps for an output gradient dy.  Replaces the backward of causal_conv1d_fn
+ * that the reference's training plugin installs as the conv forward
+ * (ml/training/pretrain/engine/sm120_concurrent_ffn.py:199-207,425-428), and
+ * autograd through CausalDepthwiseConv1d.forward (attention.py:32-60).
+ *   x, weight, conv_state, state_slots, cu_seqlens, read_history: as in the
+ *                 forward call (the history it read; the history itself gets
+ *                 no gradient).  weight: the taps the forward used, fp32 [C, K].
+ *   dy          : [total_tokens, channels] gradient of y, dtype `dtype` (x's).
+ *   dx          : [total_tokens, channels] out, dtype `dtype`; rows outside
+ *                 every sequence get zeros.
+ *   dweight     : [channels, K] fp32 out, summed over all tokens in a fixed
+ *                 order (deterministic).
+ *   x, dy, dx   : 4-element aligned rows, strides multiples of 4 elements.
+ * workspace: device memory of sophia_short_conv_bwd_workspace_size() bytes.
+ */
+size_t sophia_short_conv_bwd_workspace_size(int64_t total_tokens, int channels, int kernel_size);
+int sophia_short_conv_bwd(const void *x, int64_t x_row_stride, const void *dy, int64_t dy_row_stride,
+                          void *dx, int64_t dx_row_stride, int dtype, const float *weight,
+                          const float *conv_state, int n_state_slots, const int32_t *state_slots,
+                          const int32_t *cu_seqlens, int n_seqs, int64_t total_tokens, int channels,
+                          int kernel_size, int read_history, float *dweight, void *workspace,
+                          size_t workspace_bytes, void *stream);
+
+/*
  * Workspace bytes needed by sophia_kda_chunk_fwd for a packed batch of
  * `total_tokens` tokens in `n_seqs` sequences with `num_heads` heads
  * (head_dim 128).  Depends only on these sizes, never on the offsets.

@@ -48,6 +48,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                      _i64, _i32, _i32, _i32, _i32, _vp]),
     "sophia_short_conv_step": (_i32, [_vp, _i64, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _i32, _i32,
                                       _i32, _i32, _vp]),
+    "sophia_short_conv_bwd_workspace_size": (_sz, [_i64, _i32, _i32]),
+    "sophia_short_conv_bwd": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp,
+                                     _i32, _i64, _i32, _i32, _i32, _vp, _vp, _sz, _vp]),
     "sophia_kda_chunk_workspace_size": (_sz, [_i64, _i32, _i32, _i32]),
     "sophia_kda_chunk_fwd": (_i32, [_vp, _vp, _vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64, _i32,
                                     _vp, _vp, _f32, _f32, _u32, _vp, _vp, _i32, _i64, _i32, _i32,
@@ -71,6 +74,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "sophia_situ_glu": (_i32, [_vp, _i64, _vp, _i64, _i64, _i32, _f32, _f32, _i32, _vp]),
     "sophia_gated_head_norm": (_i32, [_vp, _i64, _i32, _vp, _i64, _vp, _f32, _vp, _i64, _i64, _i32,
                                       _i32, _i32, _vp]),
+    "sophia_gated_head_norm_bwd_workspace_size": (_sz, [_i64, _i32, _i32]),
+    "sophia_gated_head_norm_bwd": (_i32, [_vp, _i64, _vp, _i64, _i32, _vp, _i64, _vp, _f32, _vp, _i64,
+                                          _vp, _i64, _vp, _i64, _i32, _i32, _i32, _vp, _sz, _vp]),
     "sophia_mla_decode_workspace_size": (_sz, [_i64, _i32, _i32]),
     "sophia_causal_attention": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i32,
                                        _i64, _i64, _i32, _i32, _i32, _f32, _i32, _vp]),

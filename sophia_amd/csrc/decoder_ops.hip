@@ -389,6 +389,128 @@ __global__ __launch_bounds__(256) void gated_head_norm_kernel(GateArgs a) {
          8 * c, a.dtype, o);
 }
 
+// ---- gated head norm, backward (training) ---------------------------------------
+// Per head vector o (rounded to the activation dtype as the forward does),
+// r = rsqrt(mean(o^2) + eps), n = o r, s = sigmoid(gate):
+//   with the norm:    y = n w s;  dgate = dy n w s (1 - s);  dw = sum_rows dy s n;
+//                     dn = dy s w;  do = r (dn - n mean(dn n))
+//   without it (MLA): y = o s;    dgate = dy o s (1 - s);  do = dy s.
+// Each work-group takes kGnbRows rows of a 2048-column slice; its threads'
+// dw sums are reduced through LDS in a fixed order into one partial per
+// work-group, and a second kernel sums the partials in order (deterministic).
+constexpr int kGnbRows = 16;
+
+struct GateBwdArgs {
+  const void *dy;
+  int64_t dy_stride;
+  const void *o;
+  int64_t o_stride;
+  int o_dtype;
+  const void *gate;
+  int64_t gate_stride;
+  const float *norm_w;  // [head_dim] or NULL
+  float eps;
+  void *d_o;            // o's dtype
+  int64_t do_stride;
+  void *d_gate;         // the gate's dtype
+  int64_t dg_stride;
+  float *dw_part;       // [blocks][head_dim] (with the norm)
+  float *dw;            // [head_dim]
+  int rows;
+  int width;
+  int head_dim;
+  int blocks_per_row;
+  int n_blocks;
+  int dtype;
+};
+
+__global__ __launch_bounds__(256) void gated_head_norm_bwd_kernel(GateBwdArgs a) {
+  __shared__ float s_dw[256][9];
+  const int rb = blockIdx.x / a.blocks_per_row;
+  const int c = (blockIdx.x - rb * a.blocks_per_row) * 256 + threadIdx.x;
+  const int G = a.head_dim >> 3;
+  const bool valid = 8 * c < a.width;   // whole heads are valid or not
+  const bool norm = a.norm_w != nullptr;
+  const int e0 = 8 * (c & (G - 1));
+  float w[8], dwacc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    w[i] = (norm && valid) ? a.norm_w[e0 + i] : 1.f;
+    dwacc[i] = 0.f;
+  }
+  const int r_end = min(a.rows, (rb + 1) * kGnbRows);
+  for (int row = rb * kGnbRows; row < r_end; ++row) {   // uniform over the work-group
+    float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, g[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f},
+          dy[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (valid) {
+      load8(static_cast<const uint8_t *>(a.o) + static_cast<int64_t>(row) * a.o_stride * (a.o_dtype == SOPHIA_DTYPE_BF16 ? 2 : 4),
+            8 * c, a.o_dtype, o);
+      load8(static_cast<const uint8_t *>(a.gate) + static_cast<int64_t>(row) * a.gate_stride * (a.dtype == SOPHIA_DTYPE_BF16 ? 2 : 4),
+            8 * c, a.dtype, g);
+      load8(static_cast<const uint8_t *>(a.dy) + static_cast<int64_t>(row) * a.dy_stride * (a.dtype == SOPHIA_DTYPE_BF16 ? 2 : 4),
+            8 * c, a.dtype, dy);
+      if (a.o_dtype != a.dtype) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = __uint_as_float(static_cast<uint32_t>(f32_to_bf16_bits(o[i])) << 16);
+      }
+    }
+    float sg[8], d_o[8], d_g[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sg[i] = 1.0f / (1.0f + __expf(-g[i]));
+    if (norm) {   // uniform
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss = fmaf(o[i], o[i], ss);
+      for (int off = G >> 1; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+      const float r = rsqrtf(ss / static_cast<float>(a.head_dim) + a.eps);
+      float n[8], dn[8], dot = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        n[i] = o[i] * r;
+        dn[i] = dy[i] * sg[i] * w[i];
+        dot = fmaf(dn[i], n[i], dot);
+        d_g[i] = dy[i] * n[i] * w[i] * sg[i] * (1.f - sg[i]);
+        dwacc[i] = fmaf(dy[i] * sg[i], n[i], dwacc[i]);
+      }
+      for (int off = G >> 1; off > 0; off >>= 1) dot += __shfl_xor(dot, off, 64);
+      const float m = dot / static_cast<float>(a.head_dim);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) d_o[i] = r * (dn[i] - n[i] * m);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        d_o[i] = dy[i] * sg[i];
+        d_g[i] = dy[i] * o[i] * sg[i] * (1.f - sg[i]);
+      }
+    }
+    if (valid) {
+      store8(static_cast<uint8_t *>(a.d_o) + static_cast<int64_t>(row) * a.do_stride * (a.o_dtype == SOPHIA_DTYPE_BF16 ? 2 : 4),
+             8 * c, a.o_dtype, d_o);
+      store8(static_cast<uint8_t *>(a.d_gate) + static_cast<int64_t>(row) * a.dg_stride * (a.dtype == SOPHIA_DTYPE_BF16 ? 2 : 4),
+             8 * c, a.dtype, d_g);
+    }
+  }
+  if (!norm) return;
+  // threads t with the same t % G hold the same 8 weight positions
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s_dw[threadIdx.x][i] = valid ? dwacc[i] : 0.f;
+  __syncthreads();
+  if (threadIdx.x < a.head_dim) {
+    const int lane = threadIdx.x >> 3, i = threadIdx.x & 7;   // weight position 8 lane + i
+    float acc = 0.f;
+    for (int t = lane; t < 256; t += G) acc += s_dw[t][i];
+    a.dw_part[static_cast<int64_t>(blockIdx.x) * a.head_dim + threadIdx.x] = acc;
+  }
+}
+
+__global__ __launch_bounds__(256) void gated_head_norm_dw_reduce_kernel(GateBwdArgs a) {
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  if (e >= a.head_dim) return;
+  float acc = 0.f;
+  for (int b = 0; b < a.n_blocks; ++b) acc += a.dw_part[static_cast<int64_t>(b) * a.head_dim + e];
+  a.dw[e] = acc;
+}
+
 // ---------------------------------------------------------------------------
 // Absorbed MLA decode attention over fp32 latent caches.
 //
@@ -1030,4 +1152,61 @@ extern "C" int sophia_causal_attention(const void *q, int64_t q_stride, const vo
   hipLaunchKernelGGL(causal_attn_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), a);
   return check_launch("causal_attention");
+}
+
+extern "C" size_t sophia_gated_head_norm_bwd_workspace_size(int64_t rows, int heads, int head_dim) {
+  if (rows < 0 || heads <= 0 || head_dim <= 0) return 0;
+  const int64_t width = static_cast<int64_t>(heads) * head_dim;
+  const int64_t blocks = ((rows + kGnbRows - 1) / kGnbRows) * ((width / 8 + 255) / 256);
+  return static_cast<size_t>(blocks > 0 ? blocks : 1) * head_dim * sizeof(float);
+}
+
+extern "C" int sophia_gated_head_norm_bwd(const void *d_out, int64_t d_out_stride, const void *o, int64_t o_stride,
+                                          int o_dtype, const void *gate, int64_t gate_stride,
+                                          const float *norm_weight, float eps, void *d_o, int64_t d_o_stride,
+                                          void *d_gate, int64_t d_gate_stride, float *d_norm_weight, int64_t rows,
+                                          int heads, int head_dim, int dtype, void *workspace,
+                                          size_t workspace_bytes, void *stream) {
+  SOPHIA_REQUIRE((dtype == SOPHIA_DTYPE_F32 || dtype == SOPHIA_DTYPE_BF16) &&
+                     (o_dtype == SOPHIA_DTYPE_F32 || o_dtype == SOPHIA_DTYPE_BF16),
+                 "gated_head_norm_bwd: dtype not supported");
+  SOPHIA_REQUIRE(o_dtype == dtype || o_dtype == SOPHIA_DTYPE_F32,
+                 "gated_head_norm_bwd: o may be fp32 or the gate's dtype");
+  SOPHIA_REQUIRE(head_dim >= 8 && head_dim <= 256 && (head_dim & (head_dim - 1)) == 0,
+                 "gated_head_norm_bwd: head_dim must be a power of two in [8, 256]");
+  SOPHIA_REQUIRE(heads > 0 && rows >= 0 && rows <= 0x7fffffff && static_cast<int64_t>(heads) * head_dim <= (1 << 24),
+                 "gated_head_norm_bwd: bad heads / rows");
+  const int64_t width = static_cast<int64_t>(heads) * head_dim;
+  SOPHIA_REQUIRE(d_out_stride % 8 == 0 && o_stride % 8 == 0 && gate_stride % 8 == 0 && d_o_stride % 8 == 0 &&
+                     d_gate_stride % 8 == 0 && d_out_stride >= width && o_stride >= width &&
+                     gate_stride >= width && d_o_stride >= width && d_gate_stride >= width,
+                 "gated_head_norm_bwd: strides must be multiples of 8 elements and cover a row");
+  SOPHIA_REQUIRE(rows == 0 || (d_out && o && gate && d_o && d_gate), "gated_head_norm_bwd: NULL pointer");
+  SOPHIA_REQUIRE(norm_weight == nullptr || (d_norm_weight && workspace),
+                 "gated_head_norm_bwd: the norm weight needs d_norm_weight and a workspace");
+  SOPHIA_REQUIRE(aligned16(d_out) && aligned16(o) && aligned16(gate) && aligned16(d_o) && aligned16(d_gate) &&
+                     aligned16(norm_weight),
+                 "gated_head_norm_bwd: pointers must be 16-byte aligned");
+  const int blocks_per_row = static_cast<int>((width / 8 + 255) / 256);
+  const int64_t blocks = ((rows + kGnbRows - 1) / kGnbRows) * blocks_per_row;
+  SOPHIA_REQUIRE(blocks <= 0x7fffffff, "gated_head_norm_bwd: too many rows");
+  if (norm_weight) {
+    const size_t need = sophia_gated_head_norm_bwd_workspace_size(rows, heads, head_dim);
+    if (workspace_bytes < need)
+      return set_error(SOPHIA_ERR_WORKSPACE, "gated_head_norm_bwd: workspace %zu bytes < required %zu",
+                       workspace_bytes, need);
+  }
+  GateBwdArgs a{d_out, d_out_stride, o, o_stride, o_dtype, gate, gate_stride, norm_weight, eps, d_o, d_o_stride,
+                d_gate, d_gate_stride, static_cast<float *>(workspace), d_norm_weight, static_cast<int>(rows),
+                static_cast<int>(width), head_dim, blocks_per_row, static_cast<int>(blocks), dtype};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (blocks > 0) {
+    hipLaunchKernelGGL(gated_head_norm_bwd_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, a);
+    if (const int rc = check_launch("gated_head_norm_bwd")) return rc;
+  }
+  if (norm_weight) {
+    hipLaunchKernelGGL(gated_head_norm_dw_reduce_kernel, dim3((head_dim + 255) / 256), dim3(256), 0, st, a);
+    return check_launch("gated_head_norm_dw_reduce");
+  }
+  return SOPHIA_OK;
 }

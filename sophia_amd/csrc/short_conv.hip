@@ -347,6 +347,219 @@ int dispatch_step(int K, const void *x, int64_t xs, void *y, int64_t ys, const f
   return set_error(SOPHIA_ERR_INVALID, "short_conv_step: kernel_size %d not in 2..4", K);
 }
 
+// ---- backward (training) ------------------------------------------------------
+// With z[u] = sum_j w[j] X[u - (K-1) + j] (X = cat(history, x) of u's
+// sequence) and y = silu(z): dz[u] = dy[u] silu'(z[u]), silu' = s (1 + z (1 - s)),
+// s = sigmoid(z);  dx[p] = sum_j w[j] dz[p + (K-1) - j] over rows of p's own
+// sequence;  dw[j] = sum_u dz[u] X[u - (K-1) + j] (history samples included).
+// z is recomputed from x (never stored).  A thread owns 4 channels and a row
+// group of kBTiles tiles of kBRows rows: per tile it forms dz for the tile's
+// rows and the K-1 after them, writes dx of the tile's rows and adds the
+// tile's rows to its dw partial; one partial per (row group, channel) is
+// summed over row groups in a fixed order by a second kernel (deterministic).
+constexpr int kBVec = 4;
+constexpr int kBRows = 8;
+constexpr int kBTiles = 16;
+constexpr int kBLanes = 64;
+constexpr int kBGroups = 4;
+constexpr int kBGroupRows = kBRows * kBTiles;
+
+template <int DT>
+struct Vec4 {
+  float v[kBVec];
+  __device__ __forceinline__ void load(const void *base, int64_t idx) {
+    if constexpr (DT == SOPHIA_DTYPE_BF16) {
+      const u2 w = *reinterpret_cast<const u2 *>(static_cast<const uint16_t *>(base) + idx);
+      v[0] = __uint_as_float(w[0] << 16);
+      v[1] = __uint_as_float(w[0] & 0xffff0000u);
+      v[2] = __uint_as_float(w[1] << 16);
+      v[3] = __uint_as_float(w[1] & 0xffff0000u);
+    } else {
+      const f4 a = *reinterpret_cast<const f4 *>(static_cast<const float *>(base) + idx);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = a[i];
+    }
+  }
+  __device__ __forceinline__ void store(void *base, int64_t idx) const {
+    if constexpr (DT == SOPHIA_DTYPE_BF16) {
+      *reinterpret_cast<u2 *>(static_cast<uint16_t *>(base) + idx) =
+          u2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    } else {
+      *reinterpret_cast<f4 *>(static_cast<float *>(base) + idx) = f4{v[0], v[1], v[2], v[3]};
+    }
+  }
+};
+
+struct ConvBwdArgs {
+  const void *x;
+  int64_t xs;
+  const void *dy;
+  int64_t dys;
+  void *dx;
+  int64_t dxs;
+  const float *weight;
+  const float *conv_state;
+  int n_slots;
+  const int32_t *slots;
+  const int32_t *cu;
+  int n_seqs;
+  int64_t total;
+  int channels;
+  int read_history;
+  float *dw_part;   // [row groups][channels][K]
+  float *dw;        // [channels][K]
+  int n_groups;
+};
+
+template <int K, int DT>
+__global__ __launch_bounds__(256) void short_conv_bwd_kernel(ConvBwdArgs a) {
+  constexpr int HL = K - 1;
+  constexpr int R = kBRows;
+  constexpr int NZ = R + HL;   // dz rows of a tile: its R rows and the HL after them
+  const int c0 = (blockIdx.x * kBLanes + threadIdx.x) * kBVec;
+  const int grp = blockIdx.y * kBGroups + __builtin_amdgcn_readfirstlane(threadIdx.y);
+  if (c0 >= a.channels || grp >= a.n_groups) return;
+  const int64_t g0 = static_cast<int64_t>(grp) * kBGroupRows;
+  float w[kBVec][K];
+#pragma unroll
+  for (int i = 0; i < kBVec; ++i)
+#pragma unroll
+    for (int j = 0; j < K; ++j) w[i][j] = a.weight[static_cast<int64_t>(c0 + i) * K + j];
+  float dw[kBVec][K];
+#pragma unroll
+  for (int i = 0; i < kBVec; ++i)
+#pragma unroll
+    for (int j = 0; j < K; ++j) dw[i][j] = 0.f;
+  // Running sequence bounds (offsets clamped into [0, total] and monotone).
+  int s = find_seq(a.cu, a.n_seqs, g0);
+  int64_t seq_start = 0, seq_end = 0;
+  auto bounds = [&](int seq) {
+    seq_start = iclamp64(a.cu[seq], 0, a.total);
+    seq_end = iclamp64(a.cu[seq + 1], seq_start, a.total);
+  };
+  bounds(s);
+  for (int tile = 0; tile < kBTiles; ++tile) {
+    const int64_t r0 = g0 + static_cast<int64_t>(tile) * R;
+    if (r0 >= a.total) break;
+    float dz[NZ][kBVec];
+    int zs[NZ];   // sequence of row r0 + i, -1 outside every sequence
+    int ss = s;
+    int64_t st = seq_start, en = seq_end;
+#pragma unroll
+    for (int i = 0; i < NZ; ++i) {
+      const int64_t u = r0 + i;
+#pragma unroll
+      for (int ci = 0; ci < kBVec; ++ci) dz[i][ci] = 0.f;
+      zs[i] = -1;
+      if (u >= a.total) continue;
+      while (u >= en && ss + 1 < a.n_seqs) {
+        ++ss;
+        st = iclamp64(a.cu[ss], 0, a.total);
+        en = iclamp64(a.cu[ss + 1], st, a.total);
+      }
+      if (u < st || u >= en) continue;
+      zs[i] = ss;
+      const float *hist = nullptr;
+      if (HL > 0 && u - st < HL && a.read_history && a.conv_state != nullptr) {
+        const int slot = a.slots ? a.slots[ss] : ss;
+        if (slot >= 0 && slot < a.n_slots) hist = a.conv_state + static_cast<int64_t>(slot) * a.channels * HL;
+      }
+      float tap[K][kBVec];
+#pragma unroll
+      for (int j = 0; j < K; ++j) {
+        const int64_t p = u - HL + j;
+        if (p >= st) {
+          Vec4<DT> xv;
+          xv.load(a.x, p * a.xs + c0);
+#pragma unroll
+          for (int ci = 0; ci < kBVec; ++ci) tap[j][ci] = xv.v[ci];
+        } else {
+#pragma unroll
+          for (int ci = 0; ci < kBVec; ++ci)
+            tap[j][ci] = hist ? as_input_dtype<DT>(hist[static_cast<int64_t>(c0 + ci) * HL + HL + (p - st)]) : 0.f;
+        }
+      }
+      Vec4<DT> g;
+      g.load(a.dy, u * a.dys + c0);
+#pragma unroll
+      for (int ci = 0; ci < kBVec; ++ci) {
+        float z = 0.f;
+#pragma unroll
+        for (int j = 0; j < K; ++j) z = fmaf(w[ci][j], tap[j][ci], z);
+        const float sg = sigmoid_f(z);
+        dz[i][ci] = g.v[ci] * sg * (1.f + z * (1.f - sg));
+      }
+      if (i < R) {
+#pragma unroll
+        for (int ci = 0; ci < kBVec; ++ci)
+#pragma unroll
+          for (int j = 0; j < K; ++j) dw[ci][j] = fmaf(dz[i][ci], tap[j][ci], dw[ci][j]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const int64_t t = r0 + i;
+      if (t >= a.total) break;
+      Vec4<DT> out;
+#pragma unroll
+      for (int ci = 0; ci < kBVec; ++ci) {
+        float acc = 0.f;
+        if (zs[i] >= 0) {
+#pragma unroll
+          for (int j = 0; j < K; ++j)
+            if (zs[i + HL - j] == zs[i]) acc = fmaf(w[ci][j], dz[i + HL - j][ci], acc);
+        }
+        out.v[ci] = acc;   // rows outside every sequence get zero
+      }
+      out.store(a.dx, t * a.dxs + c0);
+    }
+    // the running bounds follow the first row of the next tile
+    const int64_t nxt = r0 + R;
+    while (nxt >= seq_end && s + 1 < a.n_seqs) bounds(++s);
+  }
+#pragma unroll
+  for (int ci = 0; ci < kBVec; ++ci)
+#pragma unroll
+    for (int j = 0; j < K; ++j) a.dw_part[(static_cast<int64_t>(grp) * a.channels + c0 + ci) * K + j] = dw[ci][j];
+}
+
+// dw[c][j] = sum over row groups (in order) of the partials.
+template <int K>
+__global__ __launch_bounds__(256) void short_conv_dw_reduce_kernel(ConvBwdArgs a) {
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (e >= static_cast<int64_t>(a.channels) * K) return;
+  float acc = 0.f;
+  for (int gi = 0; gi < a.n_groups; ++gi) acc += a.dw_part[static_cast<int64_t>(gi) * a.channels * K + e];
+  a.dw[e] = acc;
+}
+
+inline int conv_bwd_groups(int64_t total) { return static_cast<int>((total + kBGroupRows - 1) / kBGroupRows); }
+
+template <int K, int DT>
+int launch_bwd(const ConvBwdArgs &a, hipStream_t st) {
+  if (a.total > 0) {
+    dim3 block(kBLanes, kBGroups);
+    dim3 grid((a.channels / kBVec + kBLanes - 1) / kBLanes, (a.n_groups + kBGroups - 1) / kBGroups);
+    hipLaunchKernelGGL((short_conv_bwd_kernel<K, DT>), grid, block, 0, st, a);
+    if (const int rc = check_launch("short_conv_bwd")) return rc;
+  }
+  const int64_t n = static_cast<int64_t>(a.channels) * K;
+  hipLaunchKernelGGL((short_conv_dw_reduce_kernel<K>), dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, st,
+                     a);
+  return check_launch("short_conv_dw_reduce");
+}
+
+template <int DT>
+int dispatch_bwd(int K, const ConvBwdArgs &a, hipStream_t st) {
+  switch (K) {
+    case 1: return launch_bwd<1, DT>(a, st);
+    case 2: return launch_bwd<2, DT>(a, st);
+    case 3: return launch_bwd<3, DT>(a, st);
+    case 4: return launch_bwd<4, DT>(a, st);
+  }
+  return set_error(SOPHIA_ERR_INVALID, "short_conv_bwd: kernel_size %d not in 1..4", K);
+}
+
 }  // namespace
 }  // namespace sophia
 
@@ -414,4 +627,48 @@ extern "C" int sophia_short_conv_step(const void *x, int64_t x_row_stride, void 
   return dispatch_step<SOPHIA_DTYPE_F32>(kernel_size, x, x_row_stride, y, y_row_stride, weight,
                                          conv_state, n_state_slots, state_slots, batch, channels,
                                          read_history, st);
+}
+
+extern "C" size_t sophia_short_conv_bwd_workspace_size(int64_t total_tokens, int channels, int kernel_size) {
+  if (total_tokens < 0 || channels <= 0 || kernel_size < 1 || kernel_size > 4) return 0;
+  const size_t groups = static_cast<size_t>(conv_bwd_groups(total_tokens));
+  return (groups > 0 ? groups : 1) * static_cast<size_t>(channels) * kernel_size * sizeof(float);
+}
+
+extern "C" int sophia_short_conv_bwd(const void *x, int64_t x_row_stride, const void *dy, int64_t dy_row_stride,
+                                     void *dx, int64_t dx_row_stride, int dtype, const float *weight,
+                                     const float *conv_state, int n_state_slots, const int32_t *state_slots,
+                                     const int32_t *cu_seqlens, int n_seqs, int64_t total_tokens, int channels,
+                                     int kernel_size, int read_history, float *dweight, void *workspace,
+                                     size_t workspace_bytes, void *stream) {
+  SOPHIA_REQUIRE(dtype == SOPHIA_DTYPE_F32 || dtype == SOPHIA_DTYPE_BF16,
+                 "short_conv_bwd: dtype %d not supported", dtype);
+  SOPHIA_REQUIRE(channels > 0 && channels % kBVec == 0,
+                 "short_conv_bwd: channels (%d) must be a positive multiple of %d", channels, kBVec);
+  SOPHIA_REQUIRE(n_seqs > 0 && total_tokens >= 0 && total_tokens <= 0x7fffffffLL,
+                 "short_conv_bwd: bad n_seqs/total_tokens");
+  SOPHIA_REQUIRE(kernel_size >= 1 && kernel_size <= 4, "short_conv_bwd: kernel_size must be 1..4");
+  SOPHIA_REQUIRE(weight && cu_seqlens && dweight && workspace && (total_tokens == 0 || (x && dy && dx)),
+                 "short_conv_bwd: NULL pointer");
+  SOPHIA_REQUIRE(x_row_stride >= channels && dy_row_stride >= channels && dx_row_stride >= channels,
+                 "short_conv_bwd: row stride smaller than channels");
+  SOPHIA_REQUIRE(x_row_stride % kBVec == 0 && dy_row_stride % kBVec == 0 && dx_row_stride % kBVec == 0,
+                 "short_conv_bwd: row strides must be multiples of %d", kBVec);
+  const uintptr_t al = dtype == SOPHIA_DTYPE_BF16 ? 8 : 16;
+  SOPHIA_REQUIRE(((uintptr_t)x % al) == 0 && ((uintptr_t)dy % al) == 0 && ((uintptr_t)dx % al) == 0,
+                 "short_conv_bwd: x, dy and dx must be aligned to 4 elements");
+  SOPHIA_REQUIRE(!read_history || conv_state || kernel_size == 1, "short_conv_bwd: history requested without conv_state");
+  SOPHIA_REQUIRE(conv_state == nullptr || n_state_slots >= 0, "short_conv_bwd: n_state_slots must be >= 0");
+  const size_t need = sophia_short_conv_bwd_workspace_size(total_tokens, channels, kernel_size);
+  if (workspace_bytes < need)
+    return set_error(SOPHIA_ERR_WORKSPACE, "short_conv_bwd: workspace %zu bytes < required %zu", workspace_bytes,
+                     need);
+  const int groups = conv_bwd_groups(total_tokens);
+  SOPHIA_REQUIRE(groups / kBGroups < 65535, "short_conv_bwd: too many tokens for one launch");
+  ConvBwdArgs a{x, x_row_stride, dy, dy_row_stride, dx, dx_row_stride, weight, conv_state, n_state_slots,
+                state_slots, cu_seqlens, n_seqs, total_tokens, channels, read_history, static_cast<float *>(workspace),
+                dweight, groups};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == SOPHIA_DTYPE_BF16) return dispatch_bwd<SOPHIA_DTYPE_BF16>(kernel_size, a, st);
+  return dispatch_bwd<SOPHIA_DTYPE_F32>(kernel_size, a, st);
 }

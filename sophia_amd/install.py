@@ -8,7 +8,9 @@ plugins replace them together with ``CausalDepthwiseConv1d.forward``
 ``install_mi355x_kda`` does the same with this package's kernels:
 
 * conv modules (``forward(x, *, history=None) -> (silu(conv), next_history)``,
-  attention.py:32-60) get a forward that runs ``sophia::short_conv_fwd``;
+  attention.py:32-60) get a forward that runs ``sophia::short_conv_fwd``, or,
+  when x or the weight requires grad, the differentiable ``sophia::short_conv``
+  (backward on the HIP kernel ``sophia_short_conv_bwd``);
 * mixers get ``ops.chunk_kda`` and an in-place ``ops.fused_recurrent_kda``
   (the reference copies the final state back into the very buffer it passed
   as the initial state, attention.py:398-410, so updating it in place gives
@@ -26,25 +28,16 @@ from types import MethodType
 import torch
 from torch import nn
 
-from . import ops, torch_ops
+from . import ops
+from .kda import conv_forward
 
 
 def _conv_forward(self, x: torch.Tensor, *, history: torch.Tensor | None = None):
     """CausalDepthwiseConv1d.forward (attention.py:32-60) on the HIP kernel:
     x [B, T, C], history [B, C, K-1] or None -> (y [B, T, C], next_history in
-    x.dtype)."""
-    bsz, seqlen, channels = x.shape
-    hist_len = int(self.kernel_size) - 1
-    cu = ops.cu_for_batch(bsz, seqlen, x.device)
-    state = None
-    if hist_len > 0:
-        state = torch.zeros((bsz, channels, hist_len), dtype=torch.float32, device=x.device)
-        if history is not None:
-            state.copy_(history.to(dtype=x.dtype).float())
-    y = torch_ops.short_conv_fwd(x.reshape(bsz * seqlen, channels), self.weight.detach(), cu, state,
-                                 None, history is not None and hist_len > 0, hist_len > 0, False)
-    nxt = state.to(x.dtype) if state is not None else x.new_zeros((bsz, channels, 0))
-    return y.view(bsz, seqlen, channels), nxt
+    x.dtype), differentiable in x and the weight as the training plugin's
+    causal_conv1d_fn is (sm120_concurrent_ffn.py:199-207)."""
+    return conv_forward(self.weight, int(self.kernel_size), x, history)
 
 
 def _chunk_kda():

@@ -72,6 +72,47 @@ class RMSNorm(nn.Module):
         return F.rms_norm(x, (int(x.size(-1)),), self.weight.to(x.dtype), float(self.eps))
 
 
+def _needs_grad(*tensors) -> bool:
+    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors)
+
+
+def conv_forward(weight: torch.Tensor, kernel_size: int, x: torch.Tensor,
+                 history: torch.Tensor | None = None):
+    """CausalDepthwiseConv1d.forward (attention.py:32-60) on the HIP ShortConv:
+    x [B, T, C], history [B, C, K-1] or None -> (silu(conv) [B, T, C],
+    next_history [B, C, K-1] in x.dtype).  When x or the weight requires grad,
+    it runs the functional ``sophia::short_conv`` (autograd: dx and dweight
+    by sophia_short_conv_bwd) and next_history is the slice of cat(history, x)
+    the reference returns (differentiable in x; the history itself gets no
+    gradient); otherwise one launch writes next_history too."""
+    _require_gpu(x)
+    bsz, seqlen, channels = x.shape
+    hist_len = int(kernel_size) - 1
+    flat = x.reshape(bsz * seqlen, channels)
+    cu = ops.cu_for_batch(bsz, seqlen, x.device)
+    if _needs_grad(x, weight):
+        hist = None
+        if hist_len > 0 and history is not None:
+            hist = history.detach().to(dtype=x.dtype).float().contiguous()
+        y = torch_ops.short_conv(flat, weight, cu, hist, None, hist is not None, False)
+        if hist_len > 0:
+            prev = hist.to(x.dtype) if hist is not None else x.new_zeros((bsz, channels, hist_len))
+            nxt = torch.cat((prev, x.transpose(1, 2)[..., -hist_len:]), dim=-1)[..., -hist_len:]
+        else:
+            nxt = x.new_zeros((bsz, channels, 0))
+        return y.view(bsz, seqlen, channels), nxt
+    state = None
+    if hist_len > 0:
+        state = torch.zeros((bsz, channels, hist_len), dtype=torch.float32, device=x.device)
+        if history is not None:
+            state.copy_(history.to(dtype=x.dtype).float())
+    y = torch_ops.short_conv_fwd(flat, weight.detach(), cu, state, None,
+                                 history is not None and hist_len > 0, hist_len > 0, False)
+    next_history = (state.to(x.dtype) if state is not None
+                    else x.new_zeros((bsz, channels, 0)))
+    return y.view(bsz, seqlen, channels), next_history
+
+
 class CausalDepthwiseConv1d(nn.Module):
     """attention.py:24-60 on the HIP ShortConv kernel."""
 
@@ -84,22 +125,9 @@ class CausalDepthwiseConv1d(nn.Module):
 
     def forward(self, x: torch.Tensor, *, history: torch.Tensor | None = None):
         """x: [B, T, C]; history: [B, C, K-1] or None.  Returns
-        (silu(conv) [B, T, C], next_history [B, C, K-1] in x.dtype)."""
-        _require_gpu(x)
-        bsz, seqlen, channels = x.shape
-        hist_len = self.kernel_size - 1
-        flat = x.reshape(bsz * seqlen, channels)
-        cu = ops.cu_for_batch(bsz, seqlen, x.device)
-        state = None
-        if hist_len > 0:
-            state = torch.zeros((bsz, channels, hist_len), dtype=torch.float32, device=x.device)
-            if history is not None:
-                state.copy_(history.to(dtype=x.dtype).float())
-        y = torch_ops.short_conv_fwd(flat, self.weight.detach(), cu, state, None,
-                                     history is not None and hist_len > 0, hist_len > 0, False)
-        next_history = (state.to(x.dtype) if state is not None
-                        else x.new_zeros((bsz, channels, 0)))
-        return y.view(bsz, seqlen, channels), next_history
+        (silu(conv) [B, T, C], next_history [B, C, K-1] in x.dtype);
+        differentiable in x and the weight (``conv_forward``)."""
+        return conv_forward(self.weight, self.kernel_size, x, history)
 
 
 class SophiaKDA(nn.Module):
@@ -271,18 +299,22 @@ class SophiaKDA(nn.Module):
                 self.decay_down, self.beta_proj]
         params = tuple(m.weight for m in mods)
 
-        def build():
-            w = torch.cat([p.detach() for p in params], 0)
+        def build(parts):
+            w = torch.cat(parts, 0)
             pad = (-int(w.size(0))) % 8
             return torch.cat([w, w.new_zeros(pad, w.size(1))], 0) if pad else w
 
-        return self._cached("in", params, build, dtype)
+        if _needs_grad(*params):   # training: the fused weight is rebuilt each call, with autograd
+            return build(params).to(dtype)
+        return self._cached("in", params, lambda: build([p.detach() for p in params]), dtype)
 
     def _conv_weight(self, dtype: torch.dtype) -> torch.Tensor:
         """The q|k|v conv taps [3*inner, K] rounded to the activation dtype and
         held as fp32 (what the ShortConv kernels take), rebuilt only when a
         weight changes."""
         params = (self.q_conv.weight, self.k_conv.weight, self.v_conv.weight)
+        if _needs_grad(*params):
+            return torch.cat(params, 0).to(dtype).float().contiguous()
         return self._cached(f"conv_{dtype}", params,
                             lambda: torch.cat([p.detach() for p in params], 0).to(dtype),
                             torch.float32)
@@ -342,6 +374,19 @@ class SophiaKDA(nn.Module):
         state = self.conv_state.view(self.conv_state.size(0), 3 * self.inner_dim,
                                      self.conv_kernel - 1) if self.conv_kernel > 1 else None
         conv_w = self._conv_weight(qkv.dtype)
+        if _needs_grad(qkv, conv_w):
+            # Training: the functional conv (autograd), reading a copy of the
+            # history it convolves; the cache is then updated without grad.
+            hist = state.clone() if (read and state is not None) else None
+            y = torch_ops.short_conv(qkv, conv_w, cu, hist, slots, hist is not None, True)
+            if write and state is not None:
+                with torch.no_grad():
+                    if step:
+                        torch_ops.short_conv_step(qkv.detach(), conv_w.detach(), state, slots, read, True)
+                    else:
+                        torch_ops.short_conv_fwd(qkv.detach(), conv_w.detach(), cu, state, slots, read, True,
+                                                 True)
+            return y
         if step:
             return torch_ops.short_conv_step(qkv, conv_w, state, slots, read, True)
         return torch_ops.short_conv_fwd(qkv, conv_w, cu, state, slots, read, write, True)
@@ -351,7 +396,7 @@ class SophiaKDA(nn.Module):
         per-head norm as one HIP kernel (ops.gated_head_norm)."""
         if gate_logits.dtype != dtype:
             gate_logits = gate_logits.to(dtype)
-        out = torch_ops.gated_head_norm(o, gate_logits, self.output_norm.weight.detach(),
+        out = torch_ops.gated_head_norm(o, gate_logits, self.output_norm.weight,
                                         self.num_heads, self.head_dim, float(self.output_norm.eps))
         return self.o_proj(out)
 

@@ -132,6 +132,52 @@ def short_conv_fwd(x: torch.Tensor, weight: torch.Tensor, cu_seqlens: torch.Tens
     return y
 
 
+def short_conv_bwd(dy: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, cu_seqlens: torch.Tensor, *,
+                   conv_state: torch.Tensor | None = None, state_slots: torch.Tensor | None = None,
+                   read_history: bool = False,
+                   weight_rounded: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    """Backward of ``short_conv_fwd`` (sophia_short_conv_bwd): the gradients of
+    x and of the taps for the output gradient ``dy``, with the forward's
+    arguments (``conv_state`` is only read: the history samples the forward
+    convolved; the history gets no gradient).  Returns (dx [total, C] in
+    x.dtype, zero on rows outside every sequence; dweight [C, K] fp32, with
+    respect to the taps the forward used -- the weight rounded to x.dtype)."""
+    _gpu(x, "x")
+    _gpu(dy, "dy")
+    channels = int(x.size(1))
+    total = int(x.size(0))
+    xs = _rows(x, "x", channels)
+    if dy.dtype != x.dtype or tuple(dy.shape) != (total, channels):
+        raise RuntimeError(f"dy must be {x.dtype} [{total}, {channels}], got {dy.dtype} {tuple(dy.shape)}")
+    dys = _rows(dy, "dy", channels)
+    if weight.dim() != 2 or int(weight.size(0)) != channels:
+        raise RuntimeError(f"weight must be [{channels}, K], got {tuple(weight.shape)}")
+    kernel = int(weight.size(1))
+    w = _conv_taps(weight, x, weight_rounded)
+    cu = _int32(cu_seqlens, "cu_seqlens", x.device)
+    n = int(cu.numel()) - 1
+    if conv_state is not None:
+        _gpu(conv_state, "conv_state")
+        if (conv_state.dtype != torch.float32 or not conv_state.is_contiguous()
+                or tuple(conv_state.shape[1:]) != (channels, kernel - 1)):
+            raise RuntimeError(f"conv_state must be contiguous fp32 [slots, {channels}, {kernel - 1}]")
+    slots = _int32(state_slots, "state_slots", x.device)
+    _slot_count(slots, n)
+    dx = torch.empty((total, channels), dtype=x.dtype, device=x.device)
+    dw = torch.empty((channels, kernel), dtype=torch.float32, device=x.device)
+    lib = nat.lib()
+    need = int(lib.sophia_short_conv_bwd_workspace_size(total, channels, kernel))
+    buf, ws_addr, ws_bytes = _workspace(need, x.device)
+    rc = lib.sophia_short_conv_bwd(
+        nat.ptr(x), xs, nat.ptr(dy), dys, nat.ptr(dx), channels, nat.dtype_code(x.dtype), nat.ptr(w),
+        nat.ptr(conv_state), 0 if conv_state is None else int(conv_state.size(0)), nat.ptr(slots),
+        nat.ptr(cu), n, total, channels, kernel, int(bool(read_history) and conv_state is not None),
+        nat.ptr(dw), ws_addr, ws_bytes, nat.stream_handle(x.device))
+    nat.check(rc, "sophia_short_conv_bwd")
+    del buf
+    return dx, dw
+
+
 def short_conv_step(x: torch.Tensor, weight: torch.Tensor, conv_state: torch.Tensor, *,
                     state_slots: torch.Tensor | None = None, read_history: bool = True,
                     out: torch.Tensor | None = None, weight_rounded: bool = False) -> torch.Tensor:
@@ -909,6 +955,53 @@ def mla_decode_attn(qa: torch.Tensor, latent_cache: torch.Tensor, slots: torch.T
         heads, rank, int(splits), nat.ptr(ws), ws_bytes, nat.stream_handle(qa.device))
     nat.check(rc, "sophia_mla_decode_attn")
     return y
+
+
+def gated_head_norm_bwd(d_out: torch.Tensor, o: torch.Tensor, gate: torch.Tensor, heads: int,
+                        head_dim: int, *, norm_weight: torch.Tensor | None = None,
+                        eps: float = 1e-6) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor | None]:
+    """Backward of ``gated_head_norm`` (sophia_gated_head_norm_bwd): for the
+    output gradient ``d_out`` [rows, heads * head_dim] (gate's dtype), returns
+    (d_o in o's shape and dtype, d_gate in gate's shape and dtype, d_norm_weight
+    [head_dim] fp32 or None without the norm)."""
+    _gpu(o, "o")
+    _gpu(gate, "gate")
+    _gpu(d_out, "d_out")
+    width = int(heads) * int(head_dim)
+    o2 = o.reshape(-1, width)
+    g2 = gate.reshape(-1, width)
+    rows = int(g2.size(0))
+    if int(o2.size(0)) != rows:
+        raise RuntimeError(f"o has {int(o2.size(0))} rows, gate {rows}")
+    d2 = d_out.reshape(-1, width)
+    if d2.dtype != gate.dtype or int(d2.size(0)) != rows:
+        raise RuntimeError(f"d_out must be {gate.dtype} with {rows} rows of {width}")
+    os_ = _rows(o2, "o", width)
+    gs = _rows(g2, "gate", width)
+    ds = _rows(d2, "d_out", width)
+    if o.dtype not in (torch.float32, gate.dtype):
+        raise RuntimeError("o must be float32 or gate's dtype")
+    w = None
+    if norm_weight is not None:
+        w = norm_weight.detach().reshape(-1).to(device=gate.device, dtype=torch.float32).contiguous()
+        if int(w.numel()) != int(head_dim):
+            raise RuntimeError(f"norm_weight must hold {head_dim} values")
+        _aligned(w, "norm_weight")
+    d_o = torch.empty((rows, width), dtype=o.dtype, device=o.device)
+    d_g = torch.empty((rows, width), dtype=gate.dtype, device=gate.device)
+    d_w = torch.empty((int(head_dim),), dtype=torch.float32, device=gate.device) if w is not None else None
+    for t, name in ((o2, "o"), (g2, "gate"), (d2, "d_out")):
+        _aligned(t, name)
+    lib = nat.lib()
+    need = int(lib.sophia_gated_head_norm_bwd_workspace_size(rows, int(heads), int(head_dim)))
+    buf, ws_addr, ws_bytes = _workspace(need, gate.device)
+    rc = lib.sophia_gated_head_norm_bwd(
+        nat.ptr(d2), ds, nat.ptr(o2), os_, nat.dtype_code(o.dtype), nat.ptr(g2), gs, nat.ptr(w), float(eps),
+        nat.ptr(d_o), width, nat.ptr(d_g), width, nat.ptr(d_w), rows, int(heads), int(head_dim),
+        nat.dtype_code(gate.dtype), ws_addr, ws_bytes, nat.stream_handle(gate.device))
+    nat.check(rc, "sophia_gated_head_norm_bwd")
+    del buf
+    return d_o.view(o.shape), d_g.view(gate.shape), d_w
 
 
 def causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor,

@@ -16,6 +16,15 @@ checks every argument and launches through the C ABI on the current stream):
                             dbeta, dh0, dA_log, ddt_bias)
   sophia::kda_decode_step   (q, k, v, g, beta, state!, ...) -> o
   sophia::gated_head_norm   (o, gate, norm_weight, ...) -> y
+  sophia::short_conv        (x, weight, cu_seqlens, history, ...) -> y   (functional: the
+                            history is only read; the form training differentiates)
+  sophia::short_conv_bwd    (dy, x, weight, ...) -> (dx, dweight)
+  sophia::gated_head_norm_bwd (d_out, o, gate, norm_weight, ...) -> (d_o, d_gate, d_norm_weight)
+
+Autograd is registered for ``sophia::short_conv`` and ``sophia::gated_head_norm``
+(backward = the two ``*_bwd`` ops), so the mixer trains through them; the
+reference's training plugin installs a differentiable conv the same way
+(ml/training/pretrain/engine/sm120_concurrent_ffn.py:199-207,425-428).
 """
 
 from typing import Optional
@@ -144,5 +153,84 @@ def _(o, gate, norm_weight, heads, head_dim, eps):
     return gate.new_empty((rows, heads * head_dim))
 
 
-__all__ = ["gated_head_norm", "kda_chunk_bwd", "kda_chunk_fwd", "kda_decode_step", "short_conv_fwd",
-           "short_conv_step"]
+# ---- training: functional ShortConv and the two backward ops, with autograd
+@torch.library.custom_op(f"{_LIB}::short_conv", mutates_args=(), device_types="cuda")
+def short_conv(x: torch.Tensor, weight: torch.Tensor, cu_seqlens: torch.Tensor,
+               history: Optional[torch.Tensor], state_slots: Optional[torch.Tensor], read_history: bool,
+               weight_rounded: bool) -> torch.Tensor:
+    """ShortConv over a packed batch with the history (fp32 [slots, C, K-1])
+    only read, never written."""
+    return ops.short_conv_fwd(x, weight, cu_seqlens, conv_state=history, state_slots=state_slots,
+                              read_history=read_history, write_history=False, weight_rounded=weight_rounded)
+
+
+@short_conv.register_fake
+def _(x, weight, cu_seqlens, history, state_slots, read_history, weight_rounded):
+    return x.new_empty((x.shape[0], x.shape[1]))
+
+
+@torch.library.custom_op(f"{_LIB}::short_conv_bwd", mutates_args=(), device_types="cuda")
+def short_conv_bwd(dy: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, cu_seqlens: torch.Tensor,
+                   history: Optional[torch.Tensor], state_slots: Optional[torch.Tensor], read_history: bool,
+                   weight_rounded: bool) -> tuple[torch.Tensor, torch.Tensor]:
+    return ops.short_conv_bwd(dy, x, weight, cu_seqlens, conv_state=history, state_slots=state_slots,
+                              read_history=read_history, weight_rounded=weight_rounded)
+
+
+@short_conv_bwd.register_fake
+def _(dy, x, weight, cu_seqlens, history, state_slots, read_history, weight_rounded):
+    return (x.new_empty((x.shape[0], x.shape[1])),
+            x.new_empty((weight.shape[0], weight.shape[1]), dtype=torch.float32))
+
+
+def _short_conv_setup(ctx, inputs, output):
+    x, weight, cu_seqlens, history, state_slots, read_history, weight_rounded = inputs
+    ctx.save_for_backward(x, weight, cu_seqlens, history, state_slots)
+    ctx.flags = (bool(read_history), bool(weight_rounded))
+
+
+def _short_conv_backward(ctx, dy):
+    x, weight, cu_seqlens, history, state_slots = ctx.saved_tensors
+    dx, dw = short_conv_bwd(dy.contiguous(), x, weight, cu_seqlens, history, state_slots, *ctx.flags)
+    return dx, dw.to(weight.dtype), None, None, None, None, None
+
+
+torch.library.register_autograd(f"{_LIB}::short_conv", _short_conv_backward, setup_context=_short_conv_setup)
+
+
+@torch.library.custom_op(f"{_LIB}::gated_head_norm_bwd", mutates_args=(), device_types="cuda")
+def gated_head_norm_bwd(d_out: torch.Tensor, o: torch.Tensor, gate: torch.Tensor,
+                        norm_weight: Optional[torch.Tensor], heads: int, head_dim: int,
+                        eps: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Returns (d_o, d_gate, d_norm_weight); d_norm_weight is empty without the norm."""
+    d_o, d_g, d_w = ops.gated_head_norm_bwd(d_out, o, gate, heads, head_dim, norm_weight=norm_weight, eps=eps)
+    if d_w is None:
+        d_w = gate.new_empty((0,), dtype=torch.float32)
+    return d_o, d_g, d_w
+
+
+@gated_head_norm_bwd.register_fake
+def _(d_out, o, gate, norm_weight, heads, head_dim, eps):
+    return (o.new_empty(o.shape), gate.new_empty(gate.shape),
+            gate.new_empty((head_dim if norm_weight is not None else 0,), dtype=torch.float32))
+
+
+def _gated_head_norm_setup(ctx, inputs, output):
+    o, gate, norm_weight, heads, head_dim, eps = inputs
+    ctx.save_for_backward(o, gate, norm_weight)
+    ctx.args = (int(heads), int(head_dim), float(eps))
+
+
+def _gated_head_norm_backward(ctx, d_out):
+    o, gate, norm_weight = ctx.saved_tensors
+    d_o, d_g, d_w = gated_head_norm_bwd(d_out.contiguous(), o, gate, norm_weight, *ctx.args)
+    d_norm = None if norm_weight is None else d_w.reshape(norm_weight.shape).to(norm_weight.dtype)
+    return d_o, d_g, d_norm, None, None, None
+
+
+torch.library.register_autograd(f"{_LIB}::gated_head_norm", _gated_head_norm_backward,
+                                setup_context=_gated_head_norm_setup)
+
+
+__all__ = ["gated_head_norm", "gated_head_norm_bwd", "kda_chunk_bwd", "kda_chunk_fwd", "kda_decode_step",
+           "short_conv", "short_conv_bwd", "short_conv_fwd", "short_conv_step"]
