@@ -16,73 +16,23 @@ import threading
 
 import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 
+from ._abi import SIGNATURES, bind  # noqa: F401  (the ctypes table of the C ABI)
+from ._abi import (  # noqa: F401
+    SOPHIA_OK,
+    SOPHIA_ERR_INVALID,
+    SOPHIA_ERR_HIP,
+    SOPHIA_ERR_WORKSPACE,
+    DTYPE_F32,
+    DTYPE_BF16,
+    QK_L2NORM,
+    GATE_IN_KERNEL,
+    BETA_SIGMOID,
+    SCAN_NO_SEGMENTS,
+    BWD_RECURRENT,
+)
+
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "_lib", "libsophia_kda.so")
-
-SOPHIA_OK = 0
-SOPHIA_ERR_INVALID = 1
-SOPHIA_ERR_HIP = 2
-SOPHIA_ERR_WORKSPACE = 3
-
-DTYPE_F32 = 0
-DTYPE_BF16 = 1
-
-QK_L2NORM = 1
-GATE_IN_KERNEL = 2
-BETA_SIGMOID = 4
-SCAN_NO_SEGMENTS = 8
-BWD_RECURRENT = 16
-
-# Every symbol of include/sophia_kda.h and include/sophia_decoder.h, with its
-# ctypes signature.
-_vp = ctypes.c_void_p
-_i64 = ctypes.c_int64
-_i32 = ctypes.c_int
-_f32 = ctypes.c_float
-_u32 = ctypes.c_uint
-_sz = ctypes.c_size_t
-SIGNATURES: dict[str, tuple[object, list[object]]] = {
-    "sophia_last_error": (ctypes.c_char_p, []),
-    "sophia_abi_version": (_i32, []),
-    "sophia_short_conv_fwd": (_i32, [_vp, _i64, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _i32,
-                                     _i64, _i32, _i32, _i32, _i32, _vp]),
-    "sophia_short_conv_step": (_i32, [_vp, _i64, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _i32, _i32,
-                                      _i32, _i32, _vp]),
-    "sophia_short_conv_bwd_workspace_size": (_sz, [_i64, _i32, _i32]),
-    "sophia_short_conv_bwd": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp,
-                                     _i32, _i64, _i32, _i32, _i32, _vp, _vp, _sz, _vp]),
-    "sophia_kda_chunk_workspace_size": (_sz, [_i64, _i32, _i32, _i32]),
-    "sophia_kda_chunk_fwd": (_i32, [_vp, _vp, _vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64, _i32,
-                                    _vp, _vp, _f32, _f32, _u32, _vp, _vp, _i32, _i64, _i32, _i32,
-                                    _vp, _vp, _i32, _vp, _vp, _i64, _vp, _sz, _vp]),
-    "sophia_kda_chunk_fwd_no_alloc": (_i32, [_vp, _vp, _vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64,
-                                             _i32, _vp, _vp, _f32, _f32, _u32, _vp, _vp, _i32, _i64,
-                                             _i32, _i32, _vp, _vp, _i32, _vp, _vp, _i64, _vp]),
-    "sophia_kda_decode_step": (_i32, [_vp, _vp, _vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64, _i32,
-                                      _vp, _vp, _f32, _f32, _u32, _vp, _i32, _vp, _i32, _i32, _i32,
-                                      _i32, _vp, _i64, _vp]),
-    "sophia_kda_decode_conv_step": (_i32, [_vp, _vp, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _i64, _i32,
-                                           _vp, _i64, _i32, _vp, _vp, _f32, _f32, _u32, _vp, _i32,
-                                           _vp, _i32, _i32, _i32, _i32, _vp, _i64, _vp]),
-    "sophia_kda_chunk_bwd_workspace_size": (_sz, [_i64, _i32, _i32, _i32]),
-    "sophia_kda_chunk_bwd": (_i32, [_vp, _vp, _vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64, _i32,
-                                    _vp, _vp, _f32, _f32, _u32, _vp, _i32, _i64, _i32, _i32,
-                                    _vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
-                                    _vp, _vp, _sz, _vp]),
-    "sophia_attn_res_mix": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i32, _vp, _vp,
-                                   _f32, _vp, _f32, _vp, _i64, _i64, _i32, _i32, _vp]),
-    "sophia_situ_glu": (_i32, [_vp, _i64, _vp, _i64, _i64, _i32, _f32, _f32, _i32, _vp]),
-    "sophia_gated_head_norm": (_i32, [_vp, _i64, _i32, _vp, _i64, _vp, _f32, _vp, _i64, _i64, _i32,
-                                      _i32, _i32, _vp]),
-    "sophia_gated_head_norm_bwd_workspace_size": (_sz, [_i64, _i32, _i32]),
-    "sophia_gated_head_norm_bwd": (_i32, [_vp, _i64, _vp, _i64, _i32, _vp, _i64, _vp, _f32, _vp, _i64,
-                                          _vp, _i64, _vp, _i64, _i32, _i32, _i32, _vp, _sz, _vp]),
-    "sophia_mla_decode_workspace_size": (_sz, [_i64, _i32, _i32]),
-    "sophia_causal_attention": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i32,
-                                       _i64, _i64, _i32, _i32, _i32, _f32, _i32, _vp]),
-    "sophia_mla_decode_attn": (_i32, [_vp, _i64, _i32, _vp, _i64, _i32, _i32, _vp, _vp, _f32, _vp,
-                                      _i64, _i32, _i64, _i32, _i32, _i32, _vp, _sz, _vp]),
-}
 
 _lib = None
 _lock = threading.Lock()
@@ -103,12 +53,7 @@ def lib():
                 raise SophiaNativeError(
                     f"sophia_amd HIP library not found at {LIB_PATH}; build it with "
                     "`python -m sophia_amd.build` (hipcc, gfx950)")
-            handle = ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_GLOBAL)
-            for name, (restype, argtypes) in SIGNATURES.items():
-                fn = getattr(handle, name)
-                fn.restype = restype
-                fn.argtypes = argtypes
-            _lib = handle
+            _lib = bind(LIB_PATH, mode=ctypes.RTLD_GLOBAL)
     return _lib
 
 

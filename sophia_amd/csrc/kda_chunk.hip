@@ -34,12 +34,23 @@
 
 #include "common.hpp"
 #include "kda_chunk_bwd.hpp"
+#include "kda_plan.hpp"
 
 namespace sophia {
 namespace {
 
 constexpr int kD = 128;   // key / value head dim
 constexpr int kC = 64;    // chunk length
+static_assert(kC == plan::kChunk, "the launch plans count chunks of kC tokens");
+using plan::kMaxClasses;
+using plan::kOrderMax;
+using plan::kSegChunks;
+using plan::kSegSeqMax;
+using plan::max_segments;
+using plan::plan_scan;
+using plan::plan_segments;
+using plan::ScanPlan;
+using plan::SegPlan;
 constexpr int kThreads = 256;
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -877,7 +888,6 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_bwd_kernel(IntraA
 // ---- scan kernel -------------------------------------------------------------
 // Batches of at most kOrderMax sequences whose offsets the host also holds are
 // scanned longest sequence first.
-constexpr int kOrderMax = 16;
 struct ScanArgs {
   const int32_t *cu;
   int n_seqs;
@@ -907,7 +917,6 @@ struct ScanArgs {
   int cls_rank0, cls_rank1, cls_rank2, cls_rank3, cls_rank4;
   int cls_splits0, cls_splits1, cls_splits2, cls_splits3;
 };
-constexpr int kMaxClasses = 4;
 
 // ---- scan kernel: two roles per work-group ----------------------------------
 // Wavefronts 0..3 ("U/O" role) own chunk rows 16w..16w+15: U = Ut - W S and
@@ -1318,8 +1327,6 @@ __global__ __launch_bounds__(kScanThreads) void kda_chunk_scan_kernel(ScanArgs p
 // Launches 1 and 3 are chains of kSegChunks steps over many more work-groups.
 // Results differ from the single chain by rounding only (the bf16 operand
 // rounding of the state inside each chain, and the fp32 products of step 2).
-constexpr int kSegChunks = 64;
-constexpr int kSegSeqMax = 4;
 struct SegArgs {
   ScanArgs p;
   int n;                               // sequences (<= kSegSeqMax)
@@ -2459,129 +2466,8 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
   }
 }
 
-// Upper bound on the segments of any batch of total_tokens tokens: only a
-// sequence of at least 2 kSegChunks chunks is segmented, so the segments
-// number at most 1.5 (1 + 1 / (2 kSegChunks - 1)) total / (64 kSegChunks).
-inline int64_t max_segments(int64_t total_tokens) {
-  if (total_tokens < static_cast<int64_t>(2 * kSegChunks - 1) * kC + 1) return 0;
-  return 2 * (total_tokens / (static_cast<int64_t>(kSegChunks) * kC)) + 2;
-}
 inline size_t seg_bytes(int64_t total_tokens, int num_heads) {
   return static_cast<size_t>(max_segments(total_tokens)) * num_heads * 3 * kD * kD * sizeof(float);
-}
-
-struct SegPlan {
-  bool on = false;
-  int run[kSegSeqMax + 1] = {};
-  int cmp[kSegSeqMax + 1] = {};
-  int run_splits = 1, cmp_splits = 1;
-};
-
-// Segments are used for at most kSegSeqMax sequences with host offsets, when
-// their (sequence, head) pairs are too few to fill the chip with 4 slices
-// each and the longest has at least 2 kSegChunks chunks.
-SegPlan plan_segments(const int32_t *cu_host, int n_seqs, int num_heads, int cus, int64_t total,
-                      unsigned flags) {
-  SegPlan pl;
-  if (!cu_host || n_seqs > kSegSeqMax || (flags & SOPHIA_KDA_SCAN_NO_SEGMENTS)) return pl;
-  if (static_cast<int64_t>(n_seqs) * num_heads * 4 > cus) return pl;
-  int64_t chunks[kSegSeqMax] = {}, nmax = 0;
-  for (int i = 0; i < n_seqs; ++i) {
-    const int64_t a = iclamp64(cu_host[i], 0, total);
-    const int64_t b = iclamp64(cu_host[i + 1], a, total);
-    chunks[i] = (b - a + kC - 1) / kC;
-    nmax = chunks[i] > nmax ? chunks[i] : nmax;
-  }
-  if (nmax < 2 * kSegChunks) return pl;
-  for (int i = 0; i < n_seqs; ++i) {
-    const int64_t nseg = chunks[i] >= 2 * kSegChunks ? (chunks[i] + kSegChunks - 1) / kSegChunks : 1;
-    pl.run[i + 1] = pl.run[i] + static_cast<int>(nseg);
-    pl.cmp[i + 1] = pl.cmp[i] + static_cast<int>(nseg - 1);
-  }
-  for (int i = n_seqs + 1; i <= kSegSeqMax; ++i) {
-    pl.run[i] = pl.run[n_seqs];
-    pl.cmp[i] = pl.cmp[n_seqs];
-  }
-  if (pl.run[n_seqs] > max_segments(total)) return pl;  // cannot happen (bound above)
-  const int64_t run_pairs = static_cast<int64_t>(pl.run[n_seqs]) * num_heads;
-  const int64_t cmp_pairs = static_cast<int64_t>(pl.cmp[n_seqs]) * num_heads * 2;
-  while (pl.run_splits < 8 && run_pairs * pl.run_splits * 2 <= cus) pl.run_splits *= 2;
-  while (pl.cmp_splits < 8 && cmp_pairs * pl.cmp_splits * 2 <= cus) pl.cmp_splits *= 2;
-  pl.on = true;
-  return pl;
-}
-
-// Host-side plan of the scan launch.  Every (sequence, head) pair of the
-// batch would get the same number of work-groups (slices of the 128 value
-// columns): as many as keep every work-group resident at once.  With the
-// host copy of the offsets (and at most kOrderMax sequences), sequences are
-// taken longest first, a batch whose longest sequence has at least twice the
-// mean number of chunks gets twice that number for its longest chains, and
-// shorter chains get fewer slices: half for a chain of under 60 % of the
-// longest, a quarter under 30 % (at least one).  Measured on one MI355X,
-// the 8 sequences of U[256, 4096] tokens (56 chunks at most, 16 heads):
-// 4/4/4/2/2/1/1/1 slices 197 us per prefill call, 4 everywhere 206 us,
-// 8 on the longest chain and 4 elsewhere 214 us (a slice's step reads the
-// pair's whole -W / Q e^G / Kbar^T / A_qk record parts, so more slices per
-// chain cost more in total than they save on the chain once the chip is full).
-struct ScanPlan {
-  int n_cls = 1;
-  int block[kMaxClasses + 1] = {};
-  int rank[kMaxClasses + 1] = {};
-  int splits[kMaxClasses] = {1, 1, 1, 1};
-  uint64_t order_bits = 0xfedcba9876543210ull;
-  int64_t blocks = 0;
-};
-
-ScanPlan plan_scan(const int32_t *cu_host, int n_seqs, int num_heads, int cus) {
-  ScanPlan pl;
-  const int64_t pairs = static_cast<int64_t>(n_seqs) * num_heads;
-  int top = 1;
-  while (top < 8 && pairs * top * 2 <= static_cast<int64_t>(cus)) top *= 2;
-  if (!cu_host || n_seqs > kOrderMax) {
-    pl.splits[0] = top;
-    pl.rank[1] = n_seqs;
-    pl.blocks = (pairs + 7) / 8 * 8 * top;
-    pl.block[1] = static_cast<int>(pl.blocks);
-    return pl;
-  }
-  int order[kOrderMax];
-  int64_t chunks[kOrderMax];
-  int64_t nmax = 0, sum = 0;
-  for (int i = 0; i < n_seqs; ++i) {
-    order[i] = i;
-    chunks[i] = (static_cast<int64_t>(cu_host[i + 1]) - cu_host[i] + kC - 1) / kC;
-    nmax = chunks[i] > nmax ? chunks[i] : nmax;
-    sum += chunks[i];
-  }
-  if (top < 8 && sum > 0 && nmax * n_seqs >= 2 * sum) top *= 2;
-  std::stable_sort(order, order + n_seqs, [&](int a, int b) { return chunks[a] > chunks[b]; });
-  for (int r = 0; r < n_seqs; ++r)
-    pl.order_bits = (pl.order_bits & ~(15ull << (4 * r))) | (static_cast<uint64_t>(order[r]) << (4 * r));
-  int sp[kOrderMax];
-  for (int r = 0; r < n_seqs; ++r) {
-    const int64_t c = chunks[order[r]];
-    int v = top;
-    if (10 * c < 6 * nmax) v = top / 2;
-    if (10 * c < 3 * nmax) v = top / 4;
-    sp[r] = v < 1 ? 1 : v;
-  }
-  pl.n_cls = 0;
-  int64_t block = 0;
-  for (int r = 0; r < n_seqs;) {
-    int e = r;
-    while (e < n_seqs && sp[e] == sp[r]) ++e;
-    const int c = pl.n_cls++;
-    pl.rank[c] = r;
-    pl.block[c] = static_cast<int>(block);
-    pl.splits[c] = sp[r];
-    block += (static_cast<int64_t>(e - r) * num_heads + 7) / 8 * 8 * sp[r];
-    r = e;
-  }
-  pl.rank[pl.n_cls] = n_seqs;
-  pl.block[pl.n_cls] = static_cast<int>(block);
-  pl.blocks = block;
-  return pl;
 }
 
 // Dynamic LDS above the default limit is enabled once per (kernel, device),
@@ -2861,7 +2747,7 @@ int chunk_fwd_impl(const void *q, const void *k, const void *v, int64_t qkv_row_
                          dim3(kScanThreads), 0, st, a);
     return check_launch("kda_chunk_seg_run");
   }
-  const ScanPlan pl = plan_scan(cu_seqlens_host, n_seqs, num_heads, cus);
+  const ScanPlan pl = plan_scan(cu_seqlens_host, n_seqs, num_heads, cus, total_tokens);
   SOPHIA_REQUIRE(pl.blocks > 0 && pl.blocks <= 0x7fffffff, "kda_chunk_fwd: grid too large");
   ScanArgs sa{cu_seqlens, n_seqs, total_tokens, num_heads, max_ch, records,
               initial_state, final_state, n_state_slots, state_slots, o, o_row_stride, trash,
