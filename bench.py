@@ -33,14 +33,14 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 if HERE not in sys.path:
     sys.path.insert(0, HERE)
 
-HEADS, DIM = 16, 128
+HEADS, DIM, CHUNK = 16, 128, 64
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 # Algorithmic traffic of the prefill core per token: q, k, v, o bf16 + g fp32
 # + beta fp32 over 16 heads.
 PREFILL_BYTES_PER_TOKEN = HEADS * (4 * DIM * 2 + DIM * 4 + 4)          # 24,640
 # Causal chunk-form flops per token at C = 64: H * (5 C d + 6 d^2).
-PREFILL_FLOPS_PER_TOKEN = HEADS * (5 * 64 * DIM + 6 * DIM * DIM)      # 2,228,224
+PREFILL_FLOPS_PER_TOKEN = HEADS * (5 * CHUNK * DIM + 6 * DIM * DIM)   # 2,228,224
 METRIC = "KDA prefill tokens/s + % MFMA peak; decode-step µs and HBM GB/s at B=256"
 # HBM bytes per launch come from the rocprofv3 counter summary committed under
 # profiles/ (FETCH_SIZE and WRITE_SIZE in separate passes, calibrated on a plain
@@ -276,12 +276,22 @@ def long_prefill_bench(torch, dev, stream, steps: int, warmup: int, traffic: dic
 # Backward bytes per (token, head): q, k, v, do in bf16 and g, beta in fp32 read;
 # dq, dk, dv, dg and dbeta written in fp32.
 BWD_BYTES_PER_TOKEN = HEADS * (4 * DIM * 2 + DIM * 4 + 4 + 4 * DIM * 4 + 4)
-# Backward flops per token in the recurrent form: one forward step (decay d^2,
-# k^T S~ 2d^2, rank-1 update 2d^2) and the reverse step (q do^T 2d^2, S_t do
-# 2d^2, dS^T k 2d^2, dS u + S~ dp 4d^2, dS~ 2d^2, dalpha 2d^2, Diag(alpha) dS~
-# d^2): 20 d^2 per head.
-BWD_FLOPS_PER_TOKEN = HEADS * 20 * DIM * DIM
-FP32_PEAK_TFLOPS = 157.3
+# Backward flops per token of the chunk form (what the default backward runs),
+# per chunk of C = 64 tokens and head, counting triangular products at half
+# as the forward's 5 C^2 d + 6 C d^2 does:
+#   records (the forward's intra phase): A_kk, A_qk, W = T (beta K e^G),
+#     Ut = T (beta V): 4 C^2 d, and T = (I + A_kk)^-1: C^3 / 3;
+#   forward states: U = Ut - W S0, S1 = D S0 + Kbar^T U: 4 C d^2;
+#   reverse scan: dU = A_qk^T dO + Kbar dS1: C^2 d + 2 C d^2,
+#     dS0 = D dS1 + Qg^T dO - W^T dU: 4 C d^2;
+#   gradients: dA_qk = tril(dO U^T), Y = dU U^T (strictly lower),
+#     dXu = T^T dU: 3 C^2 d; dA_kk = -T^T Y: C^3 / 3; dQg = dO S0^T,
+#     dXw = -dXu S0^T, dKbar = U dS1^T: 6 C d^2; the products through A_qk
+#     and P into dq^, dk^: 4 C^2 d.
+# Total 12 C^2 d + 2 C^3 / 3 + 16 C d^2 per chunk and head (the split-bf16
+# products of the gradient kernel issue three MFMAs per such product; only
+# the useful flops are counted).
+BWD_FLOPS_PER_TOKEN = HEADS * (12 * CHUNK * DIM + (2 * CHUNK * CHUNK) // 3 + 16 * DIM * DIM)
 
 
 def backward_bench(torch, dev, stream, inp, steps: int, warmup: int, with_cpu: bool = False) -> dict:
@@ -310,11 +320,13 @@ def backward_bench(torch, dev, stream, inp, steps: int, warmup: int, with_cpu: b
                    "accumulation) with the norm, gate and sigmoid backward fused)",
            "tokens_per_s": round(total / (ms / 1e3), 1), "ms_per_call": round(ms, 3),
            "recurrent_form_ms_per_call": round(float(np.mean(per_rec)), 3),
-           "roofline": {"bound": "memory latency / MFMA (fp32 peak as the yardstick)", "achieved": round(tflops, 2),
-                        "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
-                        "frac": round(tflops / FP32_PEAK_TFLOPS, 4),
+           "roofline": {"bound": "mfma", "achieved": round(tflops, 2),
+                        "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                        "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
                         "flops_per_token": BWD_FLOPS_PER_TOKEN,
-                        "flops_convention": "the per-token recurrent form's 20 d^2 per head"},
+                        "flops_convention": "the chunk form's useful flops, 12 C^2 d + 2 C^3 / 3 + 16 C d^2 "
+                                            "per chunk and head (triangular products at half), against the "
+                                            "bf16 dense MFMA peak its operands run at"},
            "algorithmic_bytes_per_call": total * BWD_BYTES_PER_TOKEN,
            "GBps": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
     if with_cpu:
