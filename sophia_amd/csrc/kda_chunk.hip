@@ -1835,6 +1835,15 @@ __device__ __forceinline__ f4 mma3(const Sp8 &x, const Sp8 &y, f4 acc) {
   return mfma32(x.hi, y.hi, acc);
 }
 
+// The same split for 4 values, as bf16 bits: hi and lo words of two pairs.
+__device__ __forceinline__ void split4(const f4 &x, u2 &hi, u2 &lo) {
+  float r[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = x[i] - static_cast<float>(static_cast<__bf16>(x[i]));
+  hi = u2{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])};
+  lo = u2{pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3])};
+}
+
 __device__ __forceinline__ void load8f(const float *src, float (&x)[8]) {
   const f4 a = *reinterpret_cast<const f4 *>(src), b = *reinterpret_cast<const f4 *>(src + 4);
 #pragma unroll
@@ -1881,7 +1890,7 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
   float *sDX = sKh + 64 * kLdG;     // [64][kLdG] dU, then dXu; phase II [2][4][64][8] exchange
   float *sTP = sDX + 64 * kLdG;     // [64][kLdS] T[r][j] (j <= r) at [r][j]; P / dP [r][j] (j < r) at [j][r]
   float *sAT = sTP + 64 * kLdS;     // [64][kLdS] dA_qk (j <= r) at [r][j]; (dU U^T)[r][j] (j < r) at [j][r]
-  float *sSl = sAT + 64 * kLdS;     // [32][kLdG] rows 16i .. of S0 (0..15) and dS1 (16..31)
+  float *sSl = sAT + 64 * kLdS;     // [32][kLdG] rows 16i .. of S0 (0..15) and dS1 (16..31), split (see slb)
   float *sQb = sSl + 2 * 16 * kLdG; // [64][kLdQ] q^ columns 16i .. 16i + 15
   float *sBt = sQb + 64 * kLdQ;     // [64] beta
   float *sDg0 = sBt + 64;           // [128] e^Gamma sum_v dS1 S0
@@ -2085,11 +2094,12 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
   f4 pre[2], qpre = z4;
   const int q_r = tid >> 2, q_c = 4 * (tid & 3);
   const auto fetch2 = [&](int i) {
-    if (i < 7) pre[0] = *reinterpret_cast<const f4 *>(S0 + (16 * (i + 1) + blk_r) * kD + blk_c);
-    if (i >= 0) {
-      pre[1] = *reinterpret_cast<const f4 *>(dS1 + (16 * i + blk_r) * kD + blk_c);
-      if (tid < 256 && q_r < len) qpre = load4(a.q, (tok0 + q_r) * a.v_stride + vrow + 16 * i + q_c, a.v_dtype);
+    if (i < 7) {
+      pre[0] = *reinterpret_cast<const f4 *>(S0 + (16 * (i + 1) + blk_r) * kD + blk_c);
+      pre[1] = *reinterpret_cast<const f4 *>(dS1 + (16 * (i + 1) + blk_r) * kD + blk_c);
     }
+    if (i >= 0 && tid < 256 && q_r < len)
+      qpre = load4(a.q, (tok0 + q_r) * a.v_stride + vrow + 16 * i + q_c, a.v_dtype);
   };
   fetch2(-1);
 
@@ -2167,49 +2177,81 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
   lds_barrier();   // dXu and dP are complete
 
   // ---- 5. (phase II) column blocks: in step i the state wavefronts form
-  //         block i + 1 and the chunk wavefronts block i, finishing it from
-  //         the state wavefronts' results of step i - 1.  For rows r of
+  //         the state products of block i + 1 (dQg e^G, dXw, dKbar) and the
+  //         chunk wavefronts the products through A_qk and P of block i,
+  //         finishing it from the state wavefronts' results of step i - 1.  For rows r of
   //         block w the products through A_qk and P split e^{G_r - G_j} =
   //         e^{G_r - ref_w} e^{ref_w - G_j} (the first <= 1, the second <= 1
   //         for j before block w and <= e^80 inside it), and so do key rows j
   //         of block w with r >= 16w.  Keys j < 16 (w + 1) take the K-steps
   //         below kq, queries r >= 16 w those from st0.
+  // The S0 and dS1 rows of a block are split once, as they are stashed: row
+  // r of sSl holds the 128 hi bf16 of the row, then its 128 lo bf16 (split8's
+  // split), so every wavefront reads MFMA operands with no conversion.  The
+  // stash also forms dGamma's state term e^{Gamma_c} sum_v S0[c][v] dS1[c][v]
+  // for the channels c of the block it stashes.
+  uint8_t *const slb = reinterpret_cast<uint8_t *>(sSl);
+  const auto sl_put = [&](int row, const f4 &x) {
+    u2 hi, lo;
+    split4(x, hi, lo);
+    *reinterpret_cast<u2 *>(slb + row * (kLdG * 4) + 2 * blk_c) = hi;
+    *reinterpret_cast<u2 *>(slb + row * (kLdG * 4) + 256 + 2 * blk_c) = lo;
+  };
+  const auto sl_get = [&](int row, int col) {
+    Sp8 x;
+    x.hi = bits_to_bf8(*reinterpret_cast<const u4 *>(slb + row * (kLdG * 4) + 2 * col));
+    x.lo = bits_to_bf8(*reinterpret_cast<const u4 *>(slb + row * (kLdG * 4) + 256 + 2 * col));
+    return x;
+  };
   const auto stash2 = [&](int i) {
-    if (i < 7) *reinterpret_cast<f4 *>(sSl + blk_r * kLdG + blk_c) = pre[0];
-    if (i >= 0) {
-      *reinterpret_cast<f4 *>(sSl + (16 + blk_r) * kLdG + blk_c) = pre[1];
-      if (tid < 256) {
-        const float rq = sRq[q_r];
+    if (i < 7) {   // S0 and dS1 of block i + 1
+      sl_put(blk_r, pre[0]);
+      sl_put(16 + blk_r, pre[1]);
+      float d = ((pre[0][0] * pre[1][0]) + (pre[0][1] * pre[1][1])) + ((pre[0][2] * pre[1][2]) + (pre[0][3] * pre[1][3]));
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sQb[q_r * kLdQ + q_c + e] = qpre[e] * rq;
+      for (int off = 1; off < 32; off <<= 1) d += __shfl_xor(d, off, 64);   // the 32 threads of row blk_r
+      if ((tid & 31) == 0) {
+        const int c = 16 * (i + 1) + blk_r;
+        sDg0[c] = d * __expf(Gat(kC - 1, c));
       }
     }
+    if (i >= 0 && tid < 256) {   // q^ of block i
+      const float rq = sRq[q_r];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sQb[q_r * kLdQ + q_c + e] = qpre[e] * rq;
+    }
   };
+  // dKbar of a block, from the state wavefronts to the chunk wavefronts: T / P
+  // tile, unused in phase II (the chunk wavefronts keep dP in registers).
+  float *sX2 = sTP;
   float *sX = sDX;
   if (u == 0) {
-    // state wavefronts: dXu rows of this row block
-    Sp8 xdus[4];
+    // state wavefronts: dXu and U rows of this row block
+    Sp8 xdus[4], xus[4];
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
-      float xdu[8];
+      float xdu[8], xu[8];
       load8f(sDX + (rb + lr) * kLdG + 32 * st + 8 * gq, xdu);
       xdus[st] = split8(xdu);
+      if (rb + lr < len) {
+        load8f(Um + (rb + lr) * kD + 32 * st + 8 * gq, xu);
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) xu[k] = 0.f;
+      }
+      xus[st] = split8(xu);
     }
     lds_barrier();   // dXu is read: its tile takes the exchange
-    float s0p[4][8];   // the previous block's S0 rows (wavefront 0: e^Gamma sum_v dS1 S0)
     for (int i = -1; i < 8; ++i) {
       stash2(i);
       if (i < 7) fetch2(i + 1);
       lds_barrier();
-      float s0[4][8];
       if (i < 7) {
         const int nb = i + 1, c = 16 * nb + lr;
-#pragma unroll
-        for (int st = 0; st < 4; ++st) load8f(sSl + lr * kLdG + 32 * st + 8 * gq, s0[st]);
         f4 dq = z4, dxw = z4;
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
-          const Sp8 ss = split8(s0[st]);
+          const Sp8 ss = sl_get(lr, 32 * st + 8 * gq);
           dq = mma3(xos[st], ss, dq);
           dxw = mma3(xdus[st], ss, dxw);
         }
@@ -2222,44 +2264,17 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
         float *x = sX + (((nb & 1) * 4 + w) * 64 + l) * 8;
         *reinterpret_cast<f4 *>(x) = xq;
         *reinterpret_cast<f4 *>(x + 4) = xw;
-      }
-      if (w == 0 && i >= 0) {
-        const int c = 16 * i + lr;
-        float sdot = 0.f;
+        f4 dkb = z4;   // dKbar = U dS1^T: rows of this row block, channels c
 #pragma unroll
-        for (int st = 0; st < 4; ++st) {
-          float s1[8];
-          load8f(sSl + (16 + lr) * kLdG + 32 * st + 8 * gq, s1);
-#pragma unroll
-          for (int k = 0; k < 8; ++k) sdot += s0p[st][k] * s1[k];
-        }
-        sdot += lane_xor16(sdot);
-        sdot += lane_xor32(sdot);
-        if (gq == 0) sDg0[c] = sdot * __expf(Gat(kC - 1, c));
-      }
-      if (i < 7) {
-#pragma unroll
-        for (int st = 0; st < 4; ++st)
-#pragma unroll
-          for (int k = 0; k < 8; ++k) s0p[st][k] = s0[st][k];
+        for (int st = 0; st < 4; ++st) dkb = mma3(xus[st], sl_get(16 + lr, 32 * st + 8 * gq), dkb);
+        *reinterpret_cast<f4 *>(sX2 + (((nb & 1) * 4 + w) * 64 + l) * 4) = dkb;
       }
       lds_barrier();   // the blocks and the exchange are read
     }
   } else {
-    // chunk wavefronts: U rows and dA_qk rows / columns of this row block
-    const int jmax = 16 * (w + 1);
-    const int kq = w < 2 ? 1 : 2;
+    // chunk wavefronts: dA_qk and dP rows / columns of this row block
     const int m = rb + lr;
-    float xu[4][8], xa[2][8], xat[2][8];
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      if (m < len) {
-        load8f(Um + m * kD + 32 * st + 8 * gq, xu[st]);
-      } else {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) xu[st][k] = 0.f;
-      }
-    }
+    float xa[2][8], xat[2][8];
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
       const int kb = 32 * st + 8 * gq;
@@ -2271,109 +2286,117 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
         xat[st][k] = kk >= m ? sAT[kk * kLdS + m] : 0.f;  // dA_qk[k][m]
       }
     }
-    Sp8 xus[4], xas[2], xats[2];
-#pragma unroll
-    for (int st = 0; st < 4; ++st) xus[st] = split8(xu[st]);
+    Sp8 xas[2], xats[2], xps[2], xpts[2];
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
       xas[st] = split8(xa[st]);
       xats[st] = split8(xat[st]);
+      // dP[m][k] (k < m) and dP[k][m] (k > m): the same in every column block
+      const int kb = 32 * st + 8 * gq;
+      float xp[8], xpt[8];
+      load8f(sTP + m * kLdS + kb, xpt);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int kk = kb + k;
+        if (kk <= m) xpt[k] = 0.f;
+        xp[k] = kk < m ? sTP[kk * kLdS + m] : 0.f;
+      }
+      xps[st] = split8(xp);
+      xpts[st] = split8(xpt);
     }
     lds_barrier();   // matches the state wavefronts' barrier
-    // dG and dk^ of the previous block, written over G's and k^'s columns
-    // once every wavefront has read them (after the next barrier)
-    float pg[4] = {0.f, 0.f, 0.f, 0.f}, pk[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int i = -1; i < 8; ++i) {
-      if (i >= 1) {
+    // The column-block loop with the row block a compile-time constant W, so
+    // that which K-steps a wavefront takes and the masks it needs are known
+    // to the compiler (no branches inside the loop).
+    const auto chunk_loop = [&](auto wc) {
+      constexpr int W = decltype(wc)::value;
+      constexpr int RB = 16 * W, JMAX = 16 * (W + 1), KQ = W < 2 ? 1 : 2, ST0 = W >> 1;
+      // dG and dk^ of the previous block, written over G's and k^'s columns
+      // once every wavefront has read them (after the next barrier)
+      float pg[4] = {0.f, 0.f, 0.f, 0.f}, pk[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int i = -1; i < 8; ++i) {
+        if (i >= 1) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = rb + 4 * gq + e, c = 16 * (i - 1) + lr;
-          sG[r * kLdG + c] = pg[e];
-          sKh[r * kLdG + c] = pk[e];
-        }
-      }
-      stash2(i);
-      if (i < 7) fetch2(i + 1);
-      lds_barrier();
-      if (i >= 0) {
-        const int c = 16 * i + lr;
-        const float rwc = w == 0 ? 0.f : Gat(rb - 1, c);
-        const float gam = Gat(kC - 1, c);
-        f4 dkb = z4;
-        {
-          float s1[4][8];
-#pragma unroll
-          for (int st = 0; st < 4; ++st) load8f(sSl + (16 + lr) * kLdG + 32 * st + 8 * gq, s1[st]);
-#pragma unroll
-          for (int st = 0; st < 4; ++st) dkb = mma3(xus[st], split8(s1[st]), dkb);
-        }
-        f4 c1 = z4, c2 = z4, c34 = z4;
-#pragma unroll
-        for (int st = 0; st < 2; ++st) {
-          const int kb = 32 * st + 8 * gq;
-          float xp[8], xpt[8];   // dP[m][k] (k < m), dP[k][m] (k > m)
-          load8f(sTP + m * kLdS + kb, xpt);
-#pragma unroll
-          for (int k = 0; k < 8; ++k) {
-            const int kk = kb + k;
-            if (kk <= m) xpt[k] = 0.f;
-            xp[k] = kk < m ? sTP[kk * kLdS + m] : 0.f;
+          for (int e = 0; e < 4; ++e) {
+            const int r = RB + 4 * gq + e, c = 16 * (i - 1) + lr;
+            sG[r * kLdG + c] = pg[e];
+            sKh[r * kLdG + c] = pk[e];
           }
-          if (st < kq) {
-            float y[8];
+        }
+        stash2(i);
+        if (i < 7) fetch2(i + 1);
+        lds_barrier();
+        if (i >= 0) {
+          const int c = 16 * i + lr;
+          const float rwc = W == 0 ? 0.f : Gat(RB - 1, c);
+          const float gam = Gat(kC - 1, c);
+          f4 c1 = z4, c2 = z4, c34 = z4;
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-              const int j = kb + k;
-              y[k] = j < jmax ? Kat(j, c) * __expf(rwc - Gat(j, c)) : 0.f;
+          for (int st = 0; st < 2; ++st) {
+            const int kb = 32 * st + 8 * gq;
+            if (st < KQ) {
+              float y[8];
+#pragma unroll
+              for (int k = 0; k < 8; ++k) {
+                const int j = kb + k;
+                y[k] = j < JMAX ? Kat(j, c) * __expf(rwc - Gat(j, c)) : 0.f;
+              }
+              const Sp8 ys = split8(y);
+              c1 = mma3(xas[st], ys, c1);
+              c2 = mma3(xps[st], ys, c2);
             }
-            const Sp8 ys = split8(y);
-            c1 = mma3(xas[st], ys, c1);
-            c2 = mma3(split8(xp), ys, c2);
-          }
-          if (st >= st0) {
-            float yq[8], yk[8];
+            if (st >= ST0) {
+              float yq[8], yk[8];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-              const int r = kb + k;
-              const float f = r >= rb ? __expf(Gat(r, c) - rwc) : 0.f;
-              yq[k] = sQb[r * kLdQ + lr] * f;
-              yk[k] = Kat(r, c) * f;
+              for (int k = 0; k < 8; ++k) {
+                const int r = kb + k;
+                const float f = r >= RB ? __expf(Gat(r, c) - rwc) : 0.f;
+                yq[k] = sQb[r * kLdQ + lr] * f;
+                yk[k] = Kat(r, c) * f;
+              }
+              c34 = mma3(xats[st], split8(yq), c34);
+              c34 = mma3(xpts[st], split8(yk), c34);
             }
-            c34 = mma3(xats[st], split8(yq), c34);
-            c34 = mma3(split8(xpt), split8(yk), c34);
           }
-        }
-        // finish block i with the state wavefronts' dQg e^G and dXw
-        const float *x = sX + (((i & 1) * 4 + w) * 64 + l) * 8;
-        const f4 xq = *reinterpret_cast<const f4 *>(x), xw = *reinterpret_cast<const f4 *>(x + 4);
-        float part = 0.f;
+          // finish block i with the state wavefronts' dQg e^G, dXw and dKbar
+          const float *x = sX + (((i & 1) * 4 + W) * 64 + l) * 8;
+          const f4 xq = *reinterpret_cast<const f4 *>(x), xw = *reinterpret_cast<const f4 *>(x + 4);
+          const f4 dkb = *reinterpret_cast<const f4 *>(sX2 + (((i & 1) * 4 + W) * 64 + l) * 4);
+          float part = 0.f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = rb + 4 * gq + e;
-          const float g = Gat(r, c);
-          const float eg = __expf(g), f = __expf(gam - g), af = __expf(g - rwc), bq = __expf(rwc - g);
-          const float kv = Kat(r, c), qv = sQb[r * kLdQ + lr], bt = sBt[r];
-          const float dkbar = dkb[e] * f;                   // through Kbar = k^ e^{Gamma - G}
-          const float dkg = bt * xw[e] * eg + af * c2[e];   // through Kg = k^ e^G
-          const float dkr = bq * c34[e];                    // through the k^ e^{-G} factor
-          const float dqv = xq[e] + af * c1[e];
-          part += dkbar * kv;
-          dbr[e] += xw[e] * kv * eg;
-          pg[e] = qv * dqv + kv * (dkg - dkbar - dkr);      // dG
-          pk[e] = dkbar + dkg + dkr;                        // dk^
-          dQrow(r)[c] = dqv * sRq[r];
+          for (int e = 0; e < 4; ++e) {
+            const int r = RB + 4 * gq + e;
+            const float g = Gat(r, c);
+            const float eg = __expf(g), f = __expf(gam - g), af = __expf(g - rwc), bq = __expf(rwc - g);
+            const float kv = Kat(r, c), qv = sQb[r * kLdQ + lr], bt = sBt[r];
+            const float dkbar = dkb[e] * f;                   // through Kbar = k^ e^{Gamma - G}
+            const float dkg = bt * xw[e] * eg + af * c2[e];   // through Kg = k^ e^G
+            const float dkr = bq * c34[e];                    // through the k^ e^{-G} factor
+            const float dqv = xq[e] + af * c1[e];
+            part += dkbar * kv;
+            dbr[e] += xw[e] * kv * eg;
+            pg[e] = qv * dqv + kv * (dkg - dkbar - dkr);      // dG
+            pk[e] = dkbar + dkg + dkr;                        // dk^
+            dQrow(r)[c] = dqv * sRq[r];
+          }
+          part += lane_xor16(part);
+          part += lane_xor32(part);
+          if (gq == 0) sDgW[W * kD + c] = part;
         }
-        part += lane_xor16(part);
-        part += lane_xor32(part);
-        if (gq == 0) sDgW[w * kD + c] = part;
+        lds_barrier();   // the blocks, the exchange and G's and k^'s columns 16 i .. are read
       }
-      lds_barrier();   // the blocks, the exchange and G's and k^'s columns 16 i .. are read
-    }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int r = rb + 4 * gq + e, c = 16 * 7 + lr;
-      sG[r * kLdG + c] = pg[e];
-      sKh[r * kLdG + c] = pk[e];
+      for (int e = 0; e < 4; ++e) {
+        const int r = RB + 4 * gq + e, c = 16 * 7 + lr;
+        sG[r * kLdG + c] = pg[e];
+        sKh[r * kLdG + c] = pk[e];
+      }
+    };
+    switch (w) {
+      case 0: chunk_loop(std::integral_constant<int, 0>{}); break;
+      case 1: chunk_loop(std::integral_constant<int, 1>{}); break;
+      case 2: chunk_loop(std::integral_constant<int, 2>{}); break;
+      default: chunk_loop(std::integral_constant<int, 3>{}); break;
     }
   }
   lds_barrier();   // dG and dk^ are complete
