@@ -1855,7 +1855,7 @@ __device__ __forceinline__ void load8f(const float *src, float (&x)[8]) {
 
 constexpr int kLdG = 132;   // fp32 row strides of the gradient kernel's LDS tiles
 constexpr int kLdS = 68;
-constexpr int kLdQ = 18;    // q^ column block: rows 8 apart land 16 banks apart
+constexpr int kLdQ = 20;    // q^ column block: rows 4 apart land 16 banks apart
 constexpr int kGradThreads = 512;
 constexpr size_t kGradLdsFloats =
     3 * 64 * kLdG + 2 * 64 * kLdS + 2 * 16 * kLdG + 64 * kLdQ + 64 + 128 + 4 * 128 + 2 * 64 + 4 * 64;
@@ -2272,35 +2272,38 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
       lds_barrier();   // the blocks and the exchange are read
     }
   } else {
-    // chunk wavefronts: dA_qk and dP rows / columns of this row block
+    // chunk wavefronts: dA_qk and dP rows / columns of this row block.  The
+    // products over chunk rows k take K-step st's slot e of a lane at row
+    // kperm(st, e): rows 4 apart in the lane groups, so that the per-lane
+    // reads of G and k^ rows below land 16 banks apart (the same rows in
+    // both operands, so the products are unchanged).
+    const auto kperm = [&](int st, int e) { return 32 * st + 16 * (e >> 2) + 4 * gq + (e & 3); };
     const int m = rb + lr;
-    float xa[2][8], xat[2][8];
-#pragma unroll
-    for (int st = 0; st < 2; ++st) {
-      const int kb = 32 * st + 8 * gq;
-      load8f(sAT + m * kLdS + kb, xa[st]);    // dA_qk[m][k], k <= m
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const int kk = kb + k;
-        if (kk > m) xa[st][k] = 0.f;
-        xat[st][k] = kk >= m ? sAT[kk * kLdS + m] : 0.f;  // dA_qk[k][m]
-      }
-    }
     Sp8 xas[2], xats[2], xps[2], xpts[2];
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
-      xas[st] = split8(xa[st]);
-      xats[st] = split8(xat[st]);
-      // dP[m][k] (k < m) and dP[k][m] (k > m): the same in every column block
-      const int kb = 32 * st + 8 * gq;
-      float xp[8], xpt[8];
-      load8f(sTP + m * kLdS + kb, xpt);
+      float xa[8], xat[8], xp[8], xpt[8];
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const f4 a4 = *reinterpret_cast<const f4 *>(sAT + m * kLdS + kperm(st, 4 * h2));
+        const f4 p4 = *reinterpret_cast<const f4 *>(sTP + m * kLdS + kperm(st, 4 * h2));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          xa[4 * h2 + e] = a4[e];
+          xpt[4 * h2 + e] = p4[e];
+        }
+      }
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        const int kk = kb + k;
-        if (kk <= m) xpt[k] = 0.f;
-        xp[k] = kk < m ? sTP[kk * kLdS + m] : 0.f;
+        const int kk = kperm(st, k);
+        if (kk > m) xa[k] = 0.f;                               // dA_qk[m][k], k <= m
+        xat[k] = kk >= m ? sAT[kk * kLdS + m] : 0.f;          // dA_qk[k][m]
+        if (kk <= m) xpt[k] = 0.f;                             // dP[k][m] (k > m)
+        xp[k] = kk < m ? sTP[kk * kLdS + m] : 0.f;            // dP[m][k] (k < m)
       }
+      // the same in every column block
+      xas[st] = split8(xa);
+      xats[st] = split8(xat);
       xps[st] = split8(xp);
       xpts[st] = split8(xpt);
     }
@@ -2333,12 +2336,11 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
           f4 c1 = z4, c2 = z4, c34 = z4;
 #pragma unroll
           for (int st = 0; st < 2; ++st) {
-            const int kb = 32 * st + 8 * gq;
             if (st < KQ) {
               float y[8];
 #pragma unroll
               for (int k = 0; k < 8; ++k) {
-                const int j = kb + k;
+                const int j = kperm(st, k);
                 y[k] = j < JMAX ? Kat(j, c) * __expf(rwc - Gat(j, c)) : 0.f;
               }
               const Sp8 ys = split8(y);
@@ -2349,7 +2351,7 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
               float yq[8], yk[8];
 #pragma unroll
               for (int k = 0; k < 8; ++k) {
-                const int r = kb + k;
+                const int r = kperm(st, k);
                 const float f = r >= RB ? __expf(Gat(r, c) - rwc) : 0.f;
                 yq[k] = sQb[r * kLdQ + lr] * f;
                 yk[k] = Kat(r, c) * f;
