@@ -9,7 +9,8 @@ measured as max|hip - oracle| / max|oracle| per tensor.  Two forms:
     error of order 1);
   * the chunk form (the default, the autograd path), bf16 MFMA operands in
     its two chunk scans as in the forward, fp32 elsewhere: bound 1.5e-2
-    (measured 0.4-8e-3 on every gradient, dA_log and ddt_bias included).
+    (measured 0.4e-3 to 9.4e-3 on every gradient, dA_log and ddt_bias
+    included).
 At larger sizes the gradients are checked through properties that do not
 need the oracle: linearity in the output cotangent, and the chunk form
 against the fp32 recurrent form.
@@ -326,6 +327,45 @@ def test_chunk_bwd_is_deterministic():
     b = _hip(inp, cu, d_out, d_final, flags, recurrent=False)
     for name in a:
         np.testing.assert_array_equal(a[name], b[name])
+
+
+def test_chunk_bwd_graph_replays_equal_eager():
+    """The chunk backward captured in a HIP graph (outputs and workspace from
+    the graph's pool, host offsets given): three replays, with eager backward
+    calls on another cotangent and synchronisations between them, each equal
+    bit for bit to the eager call."""
+    cu = [0, 100, 300, 301, 520]
+    inp, d_out, d_final, flags = _inputs(cu, 4, seed=61, gated=True, dtype=torch.bfloat16)
+    dev = "cuda"
+    t = {name: x.to(dev) for name, x in inp.items()}
+    d_out_d, d_final_d = d_out.to(dev), d_final.to(dev)
+    cu_d = torch.tensor(cu, dtype=torch.int32, device=dev)
+    cu_h = torch.tensor(cu, dtype=torch.int32)
+
+    def call(do):
+        return ops.kda_chunk_bwd(t["q"], t["k"], t["v"], t["g"], t["beta"], cu_d, do, A_log=t["A_log"],
+                                 dt_bias=t["dt_bias"], initial_state=t["h0"], d_final_state=d_final_d,
+                                 cu_seqlens_cpu=cu_h, **flags)
+
+    want = [x.clone() for x in call(d_out_d)]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call(d_out_d)   # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        outs = call(d_out_d)
+    other = (d_out_d.float() * -0.5 + 0.25).to(d_out_d.dtype)
+    names = ("dq", "dk", "dv", "dg", "dbeta", "dh0", "dA_log", "ddt_bias")
+    for rep in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, w_, g_ in zip(names, want, outs):
+            assert torch.equal(w_, g_), f"replay {rep}: {name} differs from the eager call"
+        print(f"replay {rep}: all gradients bitwise equal", flush=True)
+        call(other)
+        torch.cuda.synchronize()
 
 
 def test_chunk_bwd_matches_recurrent_at_size():
