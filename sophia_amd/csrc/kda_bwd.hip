@@ -543,25 +543,12 @@ __device__ __forceinline__ void covered_rows(const BwdArgs &a, int64_t &lo, int6
 
 // ---- rows outside every sequence ---------------------------------------------------
 // A batch whose offsets end before its last row (cu[n] < total, or cu[0] > 0)
-// has rows no sequence covers; their gradients are zero.  Grid-stride over
-// those rows only (usually none).
+// has rows no sequence covers; their gradients are zero (the chunk form zeroes
+// them in its state-scan kernel).
 constexpr int kZeroBlocks = 64;
 __global__ __launch_bounds__(256) void kda_bwd_zero_outside_kernel(BwdArgs a) {
-  int64_t lo, hi;
-  covered_rows(a, lo, hi);
-  const int64_t per_row = static_cast<int64_t>(a.num_heads) * kD;
-  const int64_t outside = (lo + (a.total - hi)) * per_row;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < outside;
-       i += static_cast<int64_t>(kZeroBlocks) * 256) {
-    const int64_t r = i / per_row;
-    const int64_t row = r < lo ? r : hi + (r - lo);
-    const int64_t e = row * per_row + (i - r * per_row);
-    a.dq[e] = 0.f;
-    a.dk[e] = 0.f;
-    a.dv[e] = 0.f;
-    a.dg[e] = 0.f;
-    if (i - r * per_row < a.num_heads) a.dbeta[row * a.num_heads + (i - r * per_row)] = 0.f;
-  }
+  zero_rows_outside(a.cu, a.n_seqs, a.total, a.num_heads, a.dq, a.dk, a.dv, a.dg, a.dbeta,
+                    static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x, static_cast<int64_t>(kZeroBlocks) * 256);
 }
 
 // ---- gate parameters ---------------------------------------------------------------
@@ -764,7 +751,7 @@ extern "C" int sophia_kda_chunk_bwd(const void *q, const void *k, const void *v,
                        a);
     if (const int rc = check_launch("kda_bwd_post")) return rc;
   }
-  if (total_tokens > 0) {
+  if (recurrent && total_tokens > 0) {
     hipLaunchKernelGGL(kda_bwd_zero_outside_kernel, dim3(kZeroBlocks), dim3(256), 0, st, a);
     if (const int rc = check_launch("kda_bwd_zero_outside")) return rc;
   }

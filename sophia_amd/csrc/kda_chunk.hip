@@ -248,9 +248,10 @@ struct IntraArgs {
   uint8_t *records;
   int qkv_lines;  // bf16 q/k/v with 16-byte aligned rows: load whole lines through LDS
   // Backward instantiations only: the backward record, T = (I + A_kk)^-1 and
-  // P = A_kk / beta (fp32 [64][64] per (chunk, head)), and the output gradient.
+  // P = A_kk / beta in one fp32 [64][64] tile per (chunk, head) (T[r][c] at
+  // [r][c] for c <= r, P[r][c] at [c][r] for c < r), and the output gradient.
   uint8_t *brec;
-  float *tmat, *pmat;
+  float *tpmat;
   const void *dout;
   int64_t do_stride;
   int do_dtype;
@@ -381,7 +382,7 @@ __device__ __forceinline__ void intra_scaled_operands(
 // Every barrier inside is a work-group barrier: a work-group running two
 // items at once runs them in lock step.
 // BWD: the backward's instantiation, which also writes the backward record,
-// T and P of the item (IntraArgs::brec / tmat / pmat), in the same LDS.
+// T and P of the item (IntraArgs::brec / tpmat), in the same LDS.
 template <int QKV_DT, int G_DT, bool GATE, bool BWD = false>
 __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int first, int h, uint8_t *smem,
                                            int tid, uint8_t *rec) {
@@ -603,7 +604,17 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
         const int r = 16 * w + 4 * gq + e;
         sQK[r * kLdQK + col] = f32_to_bf16_bits(col <= r ? aqk[e] : 0.f);
         sT[r * kLdT + col] = col < r ? akk[e] * brow[e] : 0.f;
-        if constexpr (BWD) p.pmat[item * (kC * kC) + r * kC + col] = col < r ? akk[e] : 0.f;
+      }
+      if constexpr (BWD) {
+        // P[r][col] (col < r) at [col][r]: four consecutive r per lane.
+        float *tp = p.tpmat + item * (kC * kC) + col * kC + 16 * w + 4 * gq;
+        if (ib < w) {
+          *reinterpret_cast<f4 *>(tp) = akk;
+        } else if (ib == w) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (col < 16 * w + 4 * gq + e) tp[e] = akk[e];
+        }
       }
     }
   }
@@ -777,12 +788,22 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
     reinterpret_cast<float *>(rec + kOffG)[tid] = E[0] * E[1] * E[2] * E[3];
   }
   if constexpr (BWD) {
-    // T (fp32, row-major [64][64]): thread t copies row t / 4, 16 columns.
+    // T, its lower triangle (the strict upper one holds P): thread t copies
+    // row t / 4, 16 columns.
     const int r = tid >> 2, c0 = 16 * (tid & 3);
+    float *tp = p.tpmat + item * (kC * kC) + r * kC;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<f4 *>(&p.tmat[item * (kC * kC) + r * kC + c0 + 4 * i]) =
-          *reinterpret_cast<const f4 *>(&sT[r * kLdT + c0 + 4 * i]);
+    for (int i = 0; i < 4; ++i) {
+      const int c = c0 + 4 * i;
+      const f4 tv = *reinterpret_cast<const f4 *>(&sT[r * kLdT + c]);
+      if (c + 3 <= r) {
+        *reinterpret_cast<f4 *>(tp + c) = tv;
+      } else if (c <= r) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (c + e <= r) tp[c + e] = tv[e];
+      }
+    }
     // A_qk^T fragments: m = chunk rows j = 16w + lr, k = rows i perm_k(ks, gq, .).
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -1538,7 +1559,7 @@ __global__ __launch_bounds__(kScanThreads) void kda_chunk_seg_run_kernel(SegArgs
 struct BwdChunkArgs {
   ScanArgs p;                  // offsets, sizes, forward records, h0
   const uint8_t *brec;         // backward records
-  const float *tmat, *pmat;    // [max_ch][H][64][64]
+  const float *tpmat;          // [max_ch][H][64][64]: T lower, P^T strict upper
   float *s0, *u, *ds1, *du;    // [max_ch][H][128][128], [max_ch][H][64][128]
   const float *dht;            // [n_seqs][H][128][128] or NULL
   float *dh0;                  // [n_seqs][H][128][128] or NULL
@@ -1660,6 +1681,10 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_states_kernel(BwdChunkAr
   __shared__ __attribute__((aligned(16))) uint8_t sSb[4 * 8 * 64 * 16];
   __shared__ __attribute__((aligned(16))) uint8_t sUb[2 * 8 * 64 * 16];
   const ScanArgs &p = a.p;
+  if (p.total > 0)   // rows no sequence covers: zero gradients (no other kernel writes them)
+    zero_rows_outside(p.cu, p.n_seqs, p.total, p.num_heads, a.dq, a.dk, a.dv, a.dg, a.dbeta,
+                      static_cast<int64_t>(blockIdx.x) * kScanThreads + threadIdx.x,
+                      static_cast<int64_t>(gridDim.x) * kScanThreads);
   int item, half;
   seg_item(blockIdx.x, a.splits, item, half);
   const int h = item % p.num_heads;
@@ -1976,18 +2001,11 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
     *reinterpret_cast<f4 *>(&sDX[r * kLdG + blk_c]) = dv;
   }
   {
-    const float *tm = a.tmat + it * (kC * kC), *pm = a.pmat + it * (kC * kC);
+    const float *tp = a.tpmat + it * (kC * kC);   // already in sTP's layout
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const int i = tid + kGradThreads * q, r = i >> 4, c = 4 * (i & 15);
-      const f4 tv = *reinterpret_cast<const f4 *>(&tm[4 * i]);
-      const f4 pv = *reinterpret_cast<const f4 *>(&pm[4 * i]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int j = c + e;
-        if (j <= r) sTP[r * kLdS + j] = tv[e];
-        if (j < r) sTP[j * kLdS + r] = pv[e];
-      }
+      *reinterpret_cast<f4 *>(&sTP[r * kLdS + c]) = *reinterpret_cast<const f4 *>(&tp[4 * i]);
     }
   }
   if (tid < kC) {
@@ -2038,23 +2056,24 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
       vown[k][e] = r < len ? load_elem(a.v, (tok0 + r) * a.v_stride + vrow + 16 * (u + 2 * k) + lr, a.v_dtype) : 0.f;
     }
   lds_barrier();
-  // G = cumulative log-decay: each half of threads 0..255 scans 32 rows of a
-  // channel, then rows 32.. add the total of rows 0..31.
-  if (tid < 256) {
-    const int c = tid & 127, r0 = (tid >> 7) * 32;
+  // G = cumulative log-decay: each quarter of the threads scans 16 rows of a
+  // channel, then the rows of a quarter add the totals of the quarters before.
+  {
+    const int c = tid & 127, qr = tid >> 7;
     float acc = 0.f;
 #pragma unroll 8
-    for (int r = r0; r < r0 + 32; ++r) {
+    for (int r = 16 * qr; r < 16 * qr + 16; ++r) {
       acc += sG[r * kLdG + c];
       sG[r * kLdG + c] = acc;
     }
-  }
-  lds_barrier();
-  if (tid >= 128 && tid < 256) {
-    const int c = tid - 128;
-    const float base = sG[31 * kLdG + c];
+    lds_barrier();
+    float base = 0.f;
+    for (int q = 0; q < qr; ++q) base += sG[(16 * q + 15) * kLdG + c];
+    lds_barrier();
+    if (qr > 0) {
 #pragma unroll 8
-    for (int r = 32; r < 64; ++r) sG[r * kLdG + c] += base;
+      for (int r = 16 * qr; r < 16 * qr + 16; ++r) sG[r * kLdG + c] += base;
+    }
   }
 
   // ---- 2. per key block ib <= w with ib = u (mod 2): dA_qk = tril(dO U^T)
@@ -2401,6 +2420,21 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
       default: chunk_loop(std::integral_constant<int, 3>{}); break;
     }
   }
+  // The output pass's q, k and gate-input rows, issued here so that their
+  // latency overlaps the last barrier and the suffix sums below.
+  f4 zv[4], qv[4], kv[4], gbias = z4;
+  if (gate) gbias = *reinterpret_cast<const f4 *>(&a.dt_bias[h * kD + blk_c]);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = blk_r + 16 * q;
+    zv[q] = qv[q] = kv[q] = z4;
+    if (r < len) {
+      const int64_t ro = (tok0 + r) * a.v_stride + vrow + blk_c;
+      qv[q] = load4(a.q, ro, a.v_dtype);
+      kv[q] = load4(a.k, ro, a.v_dtype);
+      if (gate) zv[q] = load4(a.g, (tok0 + r) * a.g_stride + vrow + blk_c, a.g_dtype);
+    }
+  }
   lds_barrier();   // dG and dk^ are complete
 
   // ---- 6. dbeta; dg = reverse cumulative sum of dG + dGamma
@@ -2438,8 +2472,6 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
   // q^ . dq^ = q . (dq^ sRq) and k^ . dk^ = sRk (k . dk^): sums over the 32
   // threads of a row.
   {
-    f4 gbias = z4;
-    if (gate) gbias = *reinterpret_cast<const f4 *>(&a.dt_bias[h * kD + blk_c]);
     f4 dgam, tail[4];
     tail[3] = z4;
 #pragma unroll
@@ -2448,18 +2480,6 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
     for (int e = 0; e < 4; ++e) {
       const int cc = blk_c + e;
       dgam[e] = sDg0[cc] + ((sDgW[cc] + sDgW[kD + cc]) + (sDgW[2 * kD + cc] + sDgW[3 * kD + cc]));
-    }
-    f4 zv[4], qv[4], kv[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int r = blk_r + 16 * q;
-      zv[q] = qv[q] = kv[q] = z4;
-      if (r < len) {
-        const int64_t ro = (tok0 + r) * a.v_stride + vrow + blk_c;
-        qv[q] = load4(a.q, ro, a.v_dtype);
-        kv[q] = load4(a.k, ro, a.v_dtype);
-        if (gate) zv[q] = load4(a.g, (tok0 + r) * a.g_stride + vrow + blk_c, a.g_dtype);
-      }
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -2551,11 +2571,11 @@ inline size_t align256(size_t b) { return (b + 255) & ~static_cast<size_t>(255);
 }  // namespace
 
 // Scratch of the chunk-form backward, per (chunk, head): the forward and the
-// backward record, T and P, S0 and dS1, U and dU.
+// backward record, the T / P tile, S0 and dS1, U and dU.
 size_t chunk_bwd_scratch_bytes(int64_t total_tokens, int n_seqs, int num_heads) {
   const size_t items = static_cast<size_t>(max_chunks(total_tokens, n_seqs)) * num_heads;
   return align256(kTrashBytes) + align256(items * kRecBytes) + align256(items * kBwdRecBytes) +
-         2 * align256(items * kC * kC * 4) + 2 * align256(items * kD * kD * 4) + 2 * align256(items * kC * kD * 4);
+         align256(items * kC * kC * 4) + 2 * align256(items * kD * kD * 4) + 2 * align256(items * kC * kD * 4);
 }
 
 int chunk_bwd_run(const ChunkBwdIO &io, void *scratch, hipStream_t st) {
@@ -2573,8 +2593,7 @@ int chunk_bwd_run(const ChunkBwdIO &io, void *scratch, hipStream_t st) {
   void *trash = carve(kTrashBytes);
   uint8_t *records = carve(items * kRecBytes);
   uint8_t *brec = carve(items * kBwdRecBytes);
-  float *tmat = reinterpret_cast<float *>(carve(items * kC * kC * 4));
-  float *pmat = reinterpret_cast<float *>(carve(items * kC * kC * 4));
+  float *tpmat = reinterpret_cast<float *>(carve(items * kC * kC * 4));
   float *s0 = reinterpret_cast<float *>(carve(items * kD * kD * 4));
   float *ds1 = reinterpret_cast<float *>(carve(items * kD * kD * 4));
   float *u = reinterpret_cast<float *>(carve(items * kC * kD * 4));
@@ -2588,7 +2607,7 @@ int chunk_bwd_run(const ChunkBwdIO &io, void *scratch, hipStream_t st) {
     IntraArgs ia{io.q, io.k, io.v, io.qkv_stride, io.qkv_dtype, io.g, io.g_stride, io.g_dtype, io.beta,
                  io.beta_stride, io.beta_dtype, io.A_log, io.dt_bias, io.scale, io.lb, io.flags,
                  io.cu, io.n_seqs, io.total, H, max_ch, records, lines,
-                 brec, tmat, pmat, io.dout, io.do_stride, io.do_dtype};
+                 brec, tpmat, io.dout, io.do_stride, io.do_dtype};
     const dim3 grid(static_cast<unsigned>(items));
     const bool gate = (io.flags & SOPHIA_KDA_GATE_IN_KERNEL) != 0;
     const int key = (io.qkv_dtype == SOPHIA_DTYPE_BF16) * 4 + (io.g_dtype == SOPHIA_DTYPE_BF16) * 2 + gate;
@@ -2625,7 +2644,7 @@ int chunk_bwd_run(const ChunkBwdIO &io, void *scratch, hipStream_t st) {
   BwdChunkArgs a{};
   a.p = ScanArgs{io.cu, io.n_seqs, io.total, H, max_ch, records, io.h0, nullptr, io.n_seqs, nullptr, nullptr, 0,
                  trash, 0xfedcba9876543210ull, 1, 0, 0, 0, 0, 0, 0, 0, 0, 0, 1, 1, 1, 1};
-  a.brec = brec; a.tmat = tmat; a.pmat = pmat;
+  a.brec = brec; a.tpmat = tpmat;
   a.s0 = s0; a.u = u; a.ds1 = ds1; a.du = du;
   a.dht = io.dht; a.dh0 = io.dh0; a.splits = splits;
   a.q = io.q; a.k = io.k; a.v = io.v; a.v_stride = io.qkv_stride; a.v_dtype = io.qkv_dtype;

@@ -39,11 +39,35 @@ struct ChunkBwdIO {
   float *dq, *dk, *dg, *dbeta, *dv, *dh0;
 };
 
+// Rows outside every sequence (before cu[0], or from cu[n_seqs] on, both
+// clamped into [0, total]) get zero gradients of q, k, v, g and beta: thread
+// `t` of `threads` takes every threads-th element of those rows (usually
+// none).
+__device__ __forceinline__ void zero_rows_outside(const int32_t *cu, int n_seqs, int64_t total, int num_heads,
+                                                  float *dq, float *dk, float *dv, float *dg, float *dbeta,
+                                                  int64_t t, int64_t threads) {
+  const int64_t lo = cu[0] < 0 ? 0 : (cu[0] > total ? total : cu[0]);
+  const int64_t hi = cu[n_seqs] < lo ? lo : (cu[n_seqs] > total ? total : cu[n_seqs]);
+  const int64_t per_row = static_cast<int64_t>(num_heads) * 128;
+  const int64_t outside = (lo + (total - hi)) * per_row;
+  for (int64_t i = t; i < outside; i += threads) {
+    const int64_t r = i / per_row;
+    const int64_t row = r < lo ? r : hi + (r - lo);
+    const int64_t e = row * per_row + (i - r * per_row);
+    dq[e] = 0.f;
+    dk[e] = 0.f;
+    dv[e] = 0.f;
+    dg[e] = 0.f;
+    if (i - r * per_row < num_heads) dbeta[row * num_heads + (i - r * per_row)] = 0.f;
+  }
+}
+
 // Scratch bytes chunk_bwd_run needs (256-byte aligned start).
 size_t chunk_bwd_scratch_bytes(int64_t total_tokens, int n_seqs, int num_heads);
 
 // Records of every (chunk, head), the forward states, the reverse chunk scan
-// and the per-chunk gradients, on `stream`.  Returns a SOPHIA_* status.
+// and the per-chunk gradients, on `stream`; also the zero gradients of rows
+// outside every sequence.  Returns a SOPHIA_* status.
 int chunk_bwd_run(const ChunkBwdIO &io, void *scratch, hipStream_t stream);
 
 }  // namespace sophia
