@@ -1,8 +1,9 @@
 """CPU oracle for the KDA mixer hot path -- TEST INFRASTRUCTURE ONLY.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
-``cpu_baseline`` leg may import this package, and only as the checker or the
-timed CPU baseline, never as the thing measured or shipped.  The product
+``cpu_baseline`` leg may import this package, and only as the reference the
+HIP results are compared with or as the timed CPU baseline, never as the
+thing measured or shipped.  The product
 package ``sophia_amd`` does not import it and has no CPU fallback.
 
 * ``kda_oracle`` -- numpy restatement of the reference's CPU path

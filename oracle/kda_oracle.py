@@ -1,7 +1,7 @@
 """CPU oracle for the KDA mixer hot path.
 
 TEST INFRASTRUCTURE ONLY.  Nothing in the product package imports this
-module: it is the checker that ``tests/``, ``__graft_entry__.smoke()`` and the
+module: it is the reference that ``tests/``, ``__graft_entry__.smoke()`` and the
 ``cpu_baseline`` leg of ``bench.py`` compare the HIP path against.
 
 It is a plain numpy restatement of the reference's CPU path for Kimi Delta

@@ -64,7 +64,7 @@ class ModelArgs:
         if str(self.kda_backend) not in {"auto", "reference", "fla"}:
             raise ValueError(f"kda_backend must be one of auto/reference/fla, got {self.kda_backend!r}")
         if int(self.short_conv_kernel) > 4:
-            raise ValueError("short_conv_kernel must be <= 4 on this build")
+            raise ValueError("short_conv_kernel must be <= 4 (the HIP ShortConv kernels take at most 4 taps)")
         if int(self.head_dim) != 128:
             raise ValueError("the gfx950 KDA kernels are built for head_dim = 128")
 
