@@ -8,6 +8,9 @@ variant that small test batches never reach.  These tests run those exact
 calls and compare every sequence's output and final state with the fp32
 oracle (tolerance per tensor: max|y - y_ref| / max|y_ref| <= 2e-2).
 
+The backward benchmark's call (the same batch, a bf16 output gradient) is
+checked here too, the chunk form against the fp32 recurrent form.
+
 Also here: a long slow-decay prefill (gates drawn the way SophiaKDA's
 initialisation draws them, ml/runtime/model/attention.py:101-106: A_log = 0,
 dt log-uniform in [1e-3, 1e-1], so g = -5 sigmoid(z + dt_bias) is mostly in
@@ -84,6 +87,37 @@ def test_prefill_benchmark_batch_matches_oracle():
     o2 = ops.kda_chunk_fwd(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], inp["cu"],
                            use_gate=False, use_beta_sigmoid=False, final_state=state2)
     assert torch.equal(o, o2) and torch.equal(state, state2)
+
+
+def test_backward_benchmark_batch_matches_recurrent_form():
+    """The backward benchmark's call: the prefill benchmark's batch and flags
+    (l2norm in the kernel, precomputed log-decay and beta) with a bf16 output
+    gradient drawn as the benchmark draws it; the chunk form (the default, the
+    call behind the backward figure, with its launch plan for this batch)
+    against the fp32 per-token recurrent form (itself within 1e-5 of the
+    float64 oracle on smaller batches), every gradient within 1.5e-2."""
+    import bench
+    from sophia_amd import ops
+    dev = _dev()
+    lengths = bench.prefill_lengths()
+    inp = bench.make_prefill_inputs(torch, dev, lengths)
+    total = int(sum(lengths))
+    gen = torch.Generator().manual_seed(12)
+    d_out = torch.randn((total, bench.HEADS, bench.DIM), generator=gen).to(torch.bfloat16).to(dev)
+
+    def grads(recurrent):
+        return ops.kda_chunk_bwd(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], inp["cu"], d_out,
+                                 use_qk_l2norm=True, use_gate=False, use_beta_sigmoid=False,
+                                 cu_seqlens_cpu=inp["cu_cpu"], recurrent=recurrent)
+
+    got, want = grads(False), grads(True)
+    torch.cuda.synchronize()
+    for name, a, b in zip(("dq", "dk", "dv", "dg", "dbeta", "dh0"), got, want):
+        a, b = a.double().cpu(), b.double().cpu()
+        assert bool(torch.isfinite(a).all()), name
+        err = float((a - b).abs().max()) / max(float(b.abs().max()), 1e-30)
+        print(f"backward benchmark batch {name}: rel err {err:.2e}", flush=True)
+        assert err <= 1.5e-2, f"{name}: {err:.3e}"
 
 
 def test_mixed_step_prefill_shape_matches_oracle():
