@@ -274,8 +274,9 @@ def long_prefill_bench(torch, dev, stream, steps: int, warmup: int, traffic: dic
 
 
 # Backward bytes per (token, head): q, k, v, do in bf16 and g, beta in fp32 read;
-# dq, dk, dv, dg and dbeta written in fp32.
-BWD_BYTES_PER_TOKEN = HEADS * (4 * DIM * 2 + DIM * 4 + 4 + 4 * DIM * 4 + 4)
+# dq, dk, dv written in bf16 (the element type of q, k, v, as training takes
+# them), dg and dbeta in fp32.
+BWD_BYTES_PER_TOKEN = HEADS * (4 * DIM * 2 + DIM * 4 + 4 + 3 * DIM * 2 + DIM * 4 + 4)
 # Backward flops per token of the chunk form (what the default backward runs),
 # per chunk of C = 64 tokens and head, counting triangular products at half
 # as the forward's 5 C^2 d + 6 C d^2 does:
@@ -297,16 +298,18 @@ BWD_FLOPS_PER_TOKEN = HEADS * (12 * CHUNK * DIM + (2 * CHUNK * CHUNK) // 3 + 16 
 def backward_bench(torch, dev, stream, inp, steps: int, warmup: int, with_cpu: bool = False) -> dict:
     """The KDA backward (sophia_kda_chunk_bwd) over the headline prefill
     batch: gradients of q, k, v, g, beta and the initial states for a bf16
-    output gradient, with the same flags as the timed prefill."""
+    output gradient, with the same flags as the timed prefill; dq, dk, dv in
+    bf16 as the autograd function asks for them with bf16 q, k, v (the call
+    with fp32 gradients is timed beside it)."""
     from sophia_amd import ops
     total = int(inp["q"].size(0))
     gen = torch.Generator().manual_seed(12)
     d_out = torch.randn((total, HEADS, DIM), generator=gen).to(torch.bfloat16).to(dev)
 
-    def call(recurrent=False):
+    def call(recurrent=False, grad_dtype=torch.bfloat16):
         ops.kda_chunk_bwd(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], inp["cu"], d_out,
                           use_qk_l2norm=True, use_gate=False, use_beta_sigmoid=False,
-                          cu_seqlens_cpu=inp["cu_cpu"], recurrent=recurrent)
+                          cu_seqlens_cpu=inp["cu_cpu"], recurrent=recurrent, grad_dtype=grad_dtype)
 
     _, per = time_events(torch, call, steps, warmup, stream)
     ms_eager = float(np.mean(per))
@@ -315,16 +318,19 @@ def backward_bench(torch, dev, stream, inp, steps: int, warmup: int, with_cpu: b
     # the kernels alone.  The lower of the two is reported.
     ms_graph = graph_ms_per_call(torch, dev, call, max(steps // 2, 3), stream, per_graph=4)
     ms = min(ms_eager, ms_graph)
+    ms_f32 = graph_ms_per_call(torch, dev, lambda: call(grad_dtype=torch.float32), max(steps // 2, 3), stream,
+                               per_graph=4)
     _, per_rec = time_events(torch, lambda: call(True), max(steps // 2, 2), 1, stream)
     gbs = total * BWD_BYTES_PER_TOKEN / (ms / 1e3) / 1e9
     tflops = total * BWD_FLOPS_PER_TOKEN / (ms / 1e3) / 1e12
     out = {"workload": "KDA backward over the prefill batch (same lengths, flags and inputs), "
-                       "bf16 d_out, fp32 gradients",
+                       "bf16 d_out, bf16 dq / dk / dv, fp32 dg / dbeta / dh0",
            "form": "chunk (records, forward-state and reverse chunk scans on bf16 MFMA operands, "
                    "per-chunk gradients as split-bf16 MFMA products (hi*hi + hi*lo + lo*hi, fp32 "
                    "accumulation) with the norm, gate and sigmoid backward fused)",
            "tokens_per_s": round(total / (ms / 1e3), 1), "ms_per_call": round(ms, 3),
            "ms_eager": round(ms_eager, 3), "ms_graph": round(ms_graph, 3),
+           "ms_graph_fp32_grads": round(ms_f32, 3),
            "recurrent_form_ms_per_call": round(float(np.mean(per_rec)), 3),
            "roofline": {"bound": "mfma", "achieved": round(tflops, 2),
                         "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",

@@ -63,6 +63,10 @@ extern "C" {
  * fp32 arithmetic instead of the chunk form on bf16 MFMA operands (fp32
  * accumulation and state, the forward's arithmetic). */
 #define SOPHIA_KDA_BWD_RECURRENT 16u
+/* Backward switch (sophia_kda_chunk_bwd): dq, dk and dv are written as bf16
+ * (each the fp32 gradient rounded to nearest even), the element type a bf16
+ * forward's q, k, v carry; dg, dbeta and the state gradients stay fp32. */
+#define SOPHIA_KDA_BWD_GRAD_BF16 32u
 
 /* Message of the last failing call on this thread ("" if none). */
 const char *sophia_last_error(void);
@@ -260,7 +264,7 @@ int sophia_kda_decode_conv_step(const void *x_q, const void *x_k, const void *x_
  *                     dtype SOPHIA_DTYPE_F32 or _BF16.
  *   d_final_state   : [n_seqs, H, 128, 128] fp32 gradient of the final states,
  *                     or NULL (zeros).
- * Outputs, fp32, dense:
+ * Outputs, fp32 (dq, dk, dv bf16 with SOPHIA_KDA_BWD_GRAD_BF16), dense:
  *   dq, dk, dv, dg  : [total, H, 128]   (dg with respect to the g input: the
  *                                        decay logits when the gate is applied
  *                                        in the kernel, else the log-decay)
@@ -291,8 +295,8 @@ int sophia_kda_chunk_bwd(const void *q, const void *k, const void *v, int64_t qk
                          const float *dt_bias, float scale, float lower_bound, unsigned flags,
                          const int32_t *cu_seqlens, int n_seqs, int64_t total_tokens, int num_heads,
                          int head_dim, const float *initial_state, const void *d_out,
-                         int64_t d_out_row_stride, int d_out_dtype, const float *d_final_state, float *dq,
-                         float *dk, float *dv, float *dg, float *dbeta, float *d_initial_state,
+                         int64_t d_out_row_stride, int d_out_dtype, const float *d_final_state, void *dq,
+                         void *dk, void *dv, float *dg, float *dbeta, float *d_initial_state,
                          float *dA_log, float *ddt_bias, void *workspace, size_t workspace_bytes,
                          void *stream);
 

@@ -24,6 +24,7 @@ GATE_IN_KERNEL = 2
 BETA_SIGMOID = 4
 SCAN_NO_SEGMENTS = 8
 BWD_RECURRENT = 16
+BWD_GRAD_BF16 = 32
 
 # Every symbol of include/sophia_kda.h and include/sophia_decoder.h, with its
 # ctypes signature.

@@ -29,6 +29,7 @@ from ._abi import (  # noqa: F401
     BETA_SIGMOID,
     SCAN_NO_SEGMENTS,
     BWD_RECURRENT,
+    BWD_GRAD_BF16,
 )
 
 _HERE = os.path.dirname(os.path.abspath(__file__))

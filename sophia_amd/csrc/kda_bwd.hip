@@ -89,8 +89,10 @@ struct BwdArgs {
   int64_t do_stride;
   int do_dtype;
   const float *dht;       // [n_seqs, H, 128, 128] or NULL
-  // outputs (fp32)
-  float *dq, *dk, *dv, *dg, *dbeta, *dh0, *dA_log, *ddt_bias;
+  // outputs: dq, dk, dv of element type grad_dtype, the others fp32
+  void *dq, *dk, *dv;
+  int grad_dtype;
+  float *dg, *dbeta, *dh0, *dA_log, *ddt_bias;
   // workspace
   float *qh, *kh, *gl, *bt;        // prepared q^, k^, alpha = e^g, beta
   float *ckpt;                     // [pieces, H, 128, 128] states at every 8-token piece start
@@ -450,7 +452,7 @@ __global__ __launch_bounds__(kChainThreads) void kda_bwd_chain_kernel(BwdArgs a)
               dst[((static_cast<int64_t>(slice) * a.total + tok) * a.num_heads + h) * kD + row] = rsum;
             }
             if (c.rg == 0) {
-              a.dv[(tok * a.num_heads + h) * kD + c.col] = cur.bt * du;
+              store_elem(a.dv, (tok * a.num_heads + h) * kD + c.col, a.grad_dtype, cur.bt * du);
               if (l32 == 3 * kRows) a.dbp[(static_cast<int64_t>(slice) * a.total + tok) * a.num_heads + h] = rsum;
             }
           }
@@ -512,8 +514,8 @@ __global__ __launch_bounds__(kD) void kda_bwd_post_kernel(BwdArgs a) {
     dq = (lq < 1e-12f ? dyq : dyq - yq * ((s_red[0][0] + s_red[1][0]) / nq)) / nq;
     dk = (lk < 1e-12f ? dkh : dkh - yk * ((s_red[0][1] + s_red[1][1]) / nk)) / nk;
   }
-  a.dq[o] = dq;
-  a.dk[o] = dk;
+  store_elem(a.dq, o, a.grad_dtype, dq);
+  store_elem(a.dk, o, a.grad_dtype, dk);
   // alpha = e^g: dg = dalpha alpha; through the gate, dz = dg lb s (1 - s) e^A_log
   float dgv = dal * a.gl[o];
   if (a.flags & SOPHIA_KDA_GATE_IN_KERNEL) {
@@ -547,7 +549,7 @@ __device__ __forceinline__ void covered_rows(const BwdArgs &a, int64_t &lo, int6
 // them in its state-scan kernel).
 constexpr int kZeroBlocks = 64;
 __global__ __launch_bounds__(256) void kda_bwd_zero_outside_kernel(BwdArgs a) {
-  zero_rows_outside(a.cu, a.n_seqs, a.total, a.num_heads, a.dq, a.dk, a.dv, a.dg, a.dbeta,
+  zero_rows_outside(a.cu, a.n_seqs, a.total, a.num_heads, a.dq, a.dk, a.dv, a.grad_dtype, a.dg, a.dbeta,
                     static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x, static_cast<int64_t>(kZeroBlocks) * 256);
 }
 
@@ -648,7 +650,7 @@ extern "C" int sophia_kda_chunk_bwd(const void *q, const void *k, const void *v,
                                     unsigned flags, const int32_t *cu_seqlens, int n_seqs, int64_t total_tokens,
                                     int num_heads, int head_dim, const float *initial_state, const void *d_out,
                                     int64_t d_out_row_stride, int d_out_dtype, const float *d_final_state,
-                                    float *dq, float *dk, float *dv, float *dg, float *dbeta,
+                                    void *dq, void *dk, void *dv, float *dg, float *dbeta,
                                     float *d_initial_state, float *dA_log, float *ddt_bias, void *workspace,
                                     size_t workspace_bytes, void *stream) {
   SOPHIA_REQUIRE(head_dim == kD, "kda_chunk_bwd: head_dim must be 128 (got %d)", head_dim);
@@ -695,6 +697,7 @@ extern "C" int sophia_kda_chunk_bwd(const void *q, const void *k, const void *v,
   a.h0 = initial_state; a.dout = d_out; a.do_stride = d_out_row_stride; a.do_dtype = d_out_dtype;
   a.dht = d_final_state;
   a.dq = dq; a.dk = dk; a.dv = dv; a.dg = dg; a.dbeta = dbeta; a.dh0 = d_initial_state;
+  a.grad_dtype = (flags & SOPHIA_KDA_BWD_GRAD_BF16) ? SOPHIA_DTYPE_BF16 : SOPHIA_DTYPE_F32;
   a.dA_log = dA_log; a.ddt_bias = ddt_bias;
   a.qh = carve(tok * kD * 4);
   a.kh = carve(tok * kD * 4);
@@ -743,7 +746,7 @@ extern "C" int sophia_kda_chunk_bwd(const void *q, const void *k, const void *v,
     ChunkBwdIO io{q, k, v, qkv_row_stride, qkv_dtype, g, g_row_stride, g_dtype, beta, beta_row_stride,
                   beta_dtype, A_log, dt_bias, scale, lower_bound, flags, cu_seqlens, n_seqs, total_tokens,
                   num_heads, initial_state, d_out, d_out_row_stride, d_out_dtype, d_final_state,
-                  dq, dk, dg, dbeta, dv, d_initial_state};
+                  dq, dk, dg, dbeta, dv, d_initial_state, a.grad_dtype};
     if (const int rc = chunk_bwd_run(io, scratch, st)) return rc;
   }
   if (recurrent && total_tokens > 0) {

@@ -1579,7 +1579,10 @@ struct BwdChunkArgs {
   const void *dout;
   int64_t do_stride;
   int do_dtype;
-  float *dq, *dk, *dg, *dbeta, *dv;   // gradients of q, k, g, beta, v (fp32)
+  void *dq, *dk;                      // gradients of q, k (element type grad_dtype)
+  float *dg, *dbeta;                   // gradients of g, beta (fp32)
+  void *dv;                            // gradient of v (element type grad_dtype)
+  int grad_dtype;
 };
 
 // One (sequence, head, NVB value columns) of the forward scan that keeps S0
@@ -1682,7 +1685,7 @@ __global__ __launch_bounds__(kScanThreads) void kda_bwd_states_kernel(BwdChunkAr
   __shared__ __attribute__((aligned(16))) uint8_t sUb[2 * 8 * 64 * 16];
   const ScanArgs &p = a.p;
   if (p.total > 0)   // rows no sequence covers: zero gradients (no other kernel writes them)
-    zero_rows_outside(p.cu, p.n_seqs, p.total, p.num_heads, a.dq, a.dk, a.dv, a.dg, a.dbeta,
+    zero_rows_outside(p.cu, p.n_seqs, p.total, p.num_heads, a.dq, a.dk, a.dv, a.grad_dtype, a.dg, a.dbeta,
                       static_cast<int64_t>(blockIdx.x) * kScanThreads + threadIdx.x,
                       static_cast<int64_t>(gridDim.x) * kScanThreads);
   int item, half;
@@ -1908,6 +1911,8 @@ constexpr size_t kGradLdsFloats =
 // wavefront's results.  The state matrices stream through a [32][128] block
 // prefetched into registers one block ahead; every tile issues the loads of
 // all its K-steps before its first product.
+// GD: element type of dq, dk and dv.
+template <int GD>
 __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs a) {
   extern __shared__ __attribute__((aligned(16))) float gsm[];
   float *sG = gsm;                  // [64][kLdG] G (natural log); dG column blocks as phase II ends them
@@ -2154,7 +2159,7 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
       const int r = rb + 4 * gq + e;
       const float bt = sBt[r];
       dbr[e] += dxu[k][e] * vown[k][e];
-      if (r < len) a.dv[tok_off(r) * kD + c] = bt * dxu[k][e];
+      if (r < len) store_elem(a.dv, tok_off(r) * kD + c, GD, bt * dxu[k][e]);
     }
   }
   lds_barrier();   // dU is read; dA_qk and dU U^T are complete
@@ -2505,8 +2510,8 @@ __global__ __launch_bounds__(kGradThreads) void kda_bwd_grad_kernel(BwdChunkArgs
       }
       const int64_t o = tok_off(r) * kD + blk_c;
       *reinterpret_cast<f4 *>(&a.dg[o]) = d;
-      *reinterpret_cast<f4 *>(&a.dq[o]) = dqs - qv[q] * (sIq[r] * sq);
-      *reinterpret_cast<f4 *>(&a.dk[o]) = dks * rk - kv[q] * (sIk[r] * rk * rk * rk * sk);
+      store4(a.dq, o, GD, dqs - qv[q] * (sIq[r] * sq));
+      store4(a.dk, o, GD, dks * rk - kv[q] * (sIk[r] * rk * rk * rk * sk));
     }
   }
 }
@@ -2537,6 +2542,7 @@ int ensure_lds(const void *fn, size_t bytes) {
 }
 template <int QKV_DT, int G_DT, bool GATE, bool BWD>
 struct IntraKey {};
+template <int GD>
 struct GradKey {};
 
 template <int QKV_DT, int G_DT, bool GATE>
@@ -2652,7 +2658,7 @@ int chunk_bwd_run(const ChunkBwdIO &io, void *scratch, hipStream_t st) {
   a.beta = io.beta; a.beta_stride = io.beta_stride; a.beta_dtype = io.beta_dtype;
   a.A_log = io.A_log; a.dt_bias = io.dt_bias; a.scale = io.scale; a.lb = io.lb; a.flags = io.flags;
   a.dout = io.dout; a.do_stride = io.do_stride; a.do_dtype = io.do_dtype;
-  a.dq = io.dq; a.dk = io.dk; a.dg = io.dg; a.dbeta = io.dbeta; a.dv = io.dv;
+  a.dq = io.dq; a.dk = io.dk; a.dg = io.dg; a.dbeta = io.dbeta; a.dv = io.dv; a.grad_dtype = io.grad_dtype;
   hipLaunchKernelGGL(kda_bwd_states_kernel, dim3(static_cast<unsigned>(sblocks)), dim3(kScanThreads), 0, st, a);
   if (const int rc = check_launch("kda_bwd_states")) return rc;
   hipLaunchKernelGGL(kda_bwd_rscan_kernel, dim3(static_cast<unsigned>(sblocks)), dim3(kScanThreads), 0, st, a);
@@ -2660,9 +2666,15 @@ int chunk_bwd_run(const ChunkBwdIO &io, void *scratch, hipStream_t st) {
   // 4. per-chunk gradients
   if (io.total == 0) return SOPHIA_OK;
   const size_t glds = kGradLdsFloats * sizeof(float);
-  if (const int rc = ensure_lds<GradKey>(reinterpret_cast<const void *>(&kda_bwd_grad_kernel), glds)) return rc;
-  hipLaunchKernelGGL(kda_bwd_grad_kernel, dim3(static_cast<unsigned>(items)), dim3(kGradThreads), glds, st, a);
-  return check_launch("kda_bwd_grad");
+  const auto grad = [&](auto gd) {
+    constexpr int GD = decltype(gd)::value;
+    if (const int rc = ensure_lds<GradKey<GD>>(reinterpret_cast<const void *>(&kda_bwd_grad_kernel<GD>), glds))
+      return rc;
+    hipLaunchKernelGGL(kda_bwd_grad_kernel<GD>, dim3(static_cast<unsigned>(items)), dim3(kGradThreads), glds, st, a);
+    return check_launch("kda_bwd_grad");
+  };
+  return io.grad_dtype == SOPHIA_DTYPE_BF16 ? grad(std::integral_constant<int, SOPHIA_DTYPE_BF16>{})
+                                            : grad(std::integral_constant<int, SOPHIA_DTYPE_F32>{});
 }
 
 }  // namespace sophia

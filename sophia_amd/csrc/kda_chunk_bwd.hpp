@@ -7,6 +7,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "common.hpp"
+
 namespace sophia {
 
 struct ChunkBwdIO {
@@ -33,10 +35,15 @@ struct ChunkBwdIO {
   int64_t do_stride;
   int do_dtype;
   const float *dht;         // [n_seqs][H][128][128] or NULL
-  // outputs: gradients of q, k, g (the gate's input, or the log-decay
-  // itself without the gate in the kernel), v [total][H][128], of beta
-  // [total][H] (all fp32) and of the initial states (or NULL)
-  float *dq, *dk, *dg, *dbeta, *dv, *dh0;
+  // outputs: gradients of q, k, v [total][H][128] (element type grad_dtype),
+  // of g (the gate's input, or the log-decay itself without the gate in the
+  // kernel) [total][H][128] and beta [total][H] (fp32), and of the initial
+  // states (fp32, or NULL)
+  void *dq, *dk;
+  float *dg, *dbeta;
+  void *dv;
+  float *dh0;
+  int grad_dtype;
 };
 
 // Rows outside every sequence (before cu[0], or from cu[n_seqs] on, both
@@ -44,8 +51,8 @@ struct ChunkBwdIO {
 // `t` of `threads` takes every threads-th element of those rows (usually
 // none).
 __device__ __forceinline__ void zero_rows_outside(const int32_t *cu, int n_seqs, int64_t total, int num_heads,
-                                                  float *dq, float *dk, float *dv, float *dg, float *dbeta,
-                                                  int64_t t, int64_t threads) {
+                                                  void *dq, void *dk, void *dv, int grad_dtype, float *dg,
+                                                  float *dbeta, int64_t t, int64_t threads) {
   const int64_t lo = cu[0] < 0 ? 0 : (cu[0] > total ? total : cu[0]);
   const int64_t hi = cu[n_seqs] < lo ? lo : (cu[n_seqs] > total ? total : cu[n_seqs]);
   const int64_t per_row = static_cast<int64_t>(num_heads) * 128;
@@ -54,9 +61,9 @@ __device__ __forceinline__ void zero_rows_outside(const int32_t *cu, int n_seqs,
     const int64_t r = i / per_row;
     const int64_t row = r < lo ? r : hi + (r - lo);
     const int64_t e = row * per_row + (i - r * per_row);
-    dq[e] = 0.f;
-    dk[e] = 0.f;
-    dv[e] = 0.f;
+    store_elem(dq, e, grad_dtype, 0.f);
+    store_elem(dk, e, grad_dtype, 0.f);
+    store_elem(dv, e, grad_dtype, 0.f);
     dg[e] = 0.f;
     if (i - r * per_row < num_heads) dbeta[row * num_heads + (i - r * per_row)] = 0.f;
   }

@@ -334,7 +334,8 @@ def kda_chunk_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
                   lower_bound: float = -5.0, use_qk_l2norm: bool = True, use_gate: bool = True,
                   use_beta_sigmoid: bool = True, initial_state: torch.Tensor | None = None,
                   d_final_state: torch.Tensor | None = None,
-                  cu_seqlens_cpu: torch.Tensor | None = None, recurrent: bool = False):
+                  cu_seqlens_cpu: torch.Tensor | None = None, recurrent: bool = False,
+                  grad_dtype: torch.dtype = torch.float32):
     """Gradients of ``kda_chunk_fwd`` (no cache slots: one state per sequence).
 
     The HIP counterpart of FlashKDA's chunk_kda_train_bwd plus l2norm_bwd and
@@ -343,7 +344,9 @@ def kda_chunk_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
     [N, H, 128, 128] or None.  Returns fp32 (dq, dk, dv, dg, dbeta, dh0,
     dA_log, ddt_bias): dg with respect to the g input as passed, dh0
     [N, H, 128, 128], dA_log [H] and ddt_bias [H * 128] (empty without the
-    in-kernel gate).  A host ``cu_seqlens`` (or ``cu_seqlens_cpu``) is checked
+    in-kernel gate); ``grad_dtype=torch.bfloat16`` writes dq, dk and dv as
+    bf16 instead (the fp32 gradients rounded to nearest even), the element
+    type a bf16 forward's q, k, v carry.  A host ``cu_seqlens`` (or ``cu_seqlens_cpu``) is checked
     to rise from 0 to the token count.  The chunk form runs by default (bf16
     MFMA operands, fp32 accumulation and state, the forward's arithmetic);
     ``recurrent=True`` runs the per-token recurrence in fp32 instead.
@@ -383,13 +386,15 @@ def kda_chunk_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
         if t is not None:
             _nrows(t, name, n)
     a_log, dtb = _gate_params(use_gate, A_log, dt_bias, heads, device)
+    if grad_dtype not in (torch.float32, torch.bfloat16):
+        raise RuntimeError("grad_dtype must be torch.float32 or torch.bfloat16")
     if scale is None:
         scale = HEAD_DIM ** -0.5
     f32 = dict(dtype=torch.float32, device=device)
-    dq = torch.empty((total, heads, HEAD_DIM), **f32)
+    dq = torch.empty((total, heads, HEAD_DIM), dtype=grad_dtype, device=device)
     dk = torch.empty_like(dq)
     dv = torch.empty_like(dq)
-    dg = torch.empty_like(dq)
+    dg = torch.empty((total, heads, HEAD_DIM), **f32)
     dbeta = torch.empty((total, heads), **f32)
     dh0 = torch.empty((n, heads, HEAD_DIM, HEAD_DIM), **f32)
     da = torch.empty((heads if use_gate else 0,), **f32)
@@ -401,7 +406,8 @@ def kda_chunk_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
         nat.ptr(q), nat.ptr(k), nat.ptr(v), qs, nat.dtype_code(q.dtype), nat.ptr(g), gs,
         nat.dtype_code(g.dtype), nat.ptr(beta), bs, nat.dtype_code(beta.dtype), nat.ptr(a_log),
         nat.ptr(dtb), float(scale), float(lower_bound),
-        _flags(use_qk_l2norm, use_gate, use_beta_sigmoid) | (nat.BWD_RECURRENT if recurrent else 0),
+        _flags(use_qk_l2norm, use_gate, use_beta_sigmoid) | (nat.BWD_RECURRENT if recurrent else 0)
+        | (nat.BWD_GRAD_BF16 if grad_dtype == torch.bfloat16 else 0),
         nat.ptr(cu), n, total, heads, HEAD_DIM,
         nat.ptr(initial_state), nat.ptr(d_out), ds, nat.dtype_code(d_out.dtype),
         nat.ptr(d_final_state), nat.ptr(dq), nat.ptr(dk), nat.ptr(dv), nat.ptr(dg),
@@ -671,9 +677,10 @@ class ChunkKDAFunction(torch.autograd.Function):
         if do is None:
             do = torch.zeros((q.size(0), q.size(1), HEAD_DIM), dtype=torch.float32, device=q.device)
         dht = None if dht is None else dht.float().contiguous()
+        # bf16 q, k, v take their gradients as bf16 from the kernel (no casts)
         dq, dk, dv, dg, db, dh0, da, dbias = torch_ops.kda_chunk_bwd(
             q, k, v, g, beta, cu, do.contiguous(), a_log, dtb, scale, lb, use_l2, use_gate,
-            use_sig, h0, dht, ctx.cu_cpu)
+            use_sig, h0, dht, ctx.cu_cpu, False, q.dtype == torch.bfloat16)
         return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg.to(g.dtype), db.to(beta.dtype),
                 _grad_like(da, A_log) if use_gate else None,
                 _grad_like(dbias, dt_bias) if use_gate else None, None,

@@ -97,27 +97,30 @@ def kda_chunk_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
                   A_log: Optional[torch.Tensor], dt_bias: Optional[torch.Tensor], scale: float,
                   lower_bound: float, use_qk_l2norm: bool, use_gate: bool, use_beta_sigmoid: bool,
                   initial_state: Optional[torch.Tensor], d_final_state: Optional[torch.Tensor],
-                  cu_seqlens_cpu: Optional[torch.Tensor], recurrent: bool = False
-                  ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
+                  cu_seqlens_cpu: Optional[torch.Tensor], recurrent: bool = False,
+                  grad_bf16: bool = False) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
                              torch.Tensor, torch.Tensor, torch.Tensor]:
     """Prefill backward: fp32 gradients of every input (dA_log / ddt_bias empty
-    without the in-kernel gate); the chunk form, or the fp32 recurrence with
-    ``recurrent``."""
+    without the in-kernel gate; dq, dk, dv bf16 with ``grad_bf16``); the chunk
+    form, or the fp32 recurrence with ``recurrent``."""
     return ops.kda_chunk_bwd(q, k, v, g, beta, cu_seqlens, d_out, A_log=A_log, dt_bias=dt_bias,
                              scale=scale, lower_bound=lower_bound, use_qk_l2norm=use_qk_l2norm,
                              use_gate=use_gate, use_beta_sigmoid=use_beta_sigmoid,
                              initial_state=initial_state, d_final_state=d_final_state,
-                             cu_seqlens_cpu=cu_seqlens_cpu, recurrent=recurrent)
+                             cu_seqlens_cpu=cu_seqlens_cpu, recurrent=recurrent,
+                             grad_dtype=torch.bfloat16 if grad_bf16 else torch.float32)
 
 
 @kda_chunk_bwd.register_fake
 def _(q, k, v, g, beta, cu_seqlens, d_out, A_log, dt_bias, scale, lower_bound, use_qk_l2norm,
-      use_gate, use_beta_sigmoid, initial_state, d_final_state, cu_seqlens_cpu, recurrent=False):
+      use_gate, use_beta_sigmoid, initial_state, d_final_state, cu_seqlens_cpu, recurrent=False,
+      grad_bf16=False):
     total, heads, dim = q.shape
     n = cu_seqlens.shape[0] - 1
     f32 = dict(dtype=torch.float32)
-    return (q.new_empty((total, heads, dim), **f32), q.new_empty((total, heads, dim), **f32),
-            q.new_empty((total, heads, dim), **f32), q.new_empty((total, heads, dim), **f32),
+    gqkv = dict(dtype=torch.bfloat16 if grad_bf16 else torch.float32)
+    return (q.new_empty((total, heads, dim), **gqkv), q.new_empty((total, heads, dim), **gqkv),
+            q.new_empty((total, heads, dim), **gqkv), q.new_empty((total, heads, dim), **f32),
             q.new_empty((total, heads), **f32), q.new_empty((n, heads, dim, dim), **f32),
             q.new_empty((heads if use_gate else 0,), **f32),
             q.new_empty((heads * dim if use_gate else 0,), **f32))

@@ -31,6 +31,26 @@ def test_header_declares_the_entry_points():
         assert name in decls, name
 
 
+def test_header_constants_match_the_binding():
+    """Every status code, element type and flag bit #defined in
+    include/sophia_kda.h has the value the ctypes table binds."""
+    import re
+    from sophia_amd import _abi
+    path = os.path.join(os.path.dirname(__file__), "..", "include", "sophia_kda.h")
+    defs = {m.group(1): int(m.group(2)) for m in
+            re.finditer(r"^#define SOPHIA_(\w+) (\d+)u?\b", open(path).read(), re.M)}
+    names = {"OK": "SOPHIA_OK", "ERR_INVALID": "SOPHIA_ERR_INVALID", "ERR_HIP": "SOPHIA_ERR_HIP",
+             "ERR_WORKSPACE": "SOPHIA_ERR_WORKSPACE", "DTYPE_F32": "DTYPE_F32", "DTYPE_BF16": "DTYPE_BF16",
+             "KDA_QK_L2NORM": "QK_L2NORM", "KDA_GATE_IN_KERNEL": "GATE_IN_KERNEL",
+             "KDA_BETA_SIGMOID": "BETA_SIGMOID", "KDA_SCAN_NO_SEGMENTS": "SCAN_NO_SEGMENTS",
+             "KDA_BWD_RECURRENT": "BWD_RECURRENT", "KDA_BWD_GRAD_BF16": "BWD_GRAD_BF16"}
+    assert set(defs) == set(names), sorted(set(defs) ^ set(names))
+    for hname, pname in names.items():
+        assert defs[hname] == getattr(_abi, pname), hname
+    flags = [v for k, v in defs.items() if k.startswith("KDA_")]
+    assert len(set(flags)) == len(flags) and all(f & (f - 1) == 0 for f in flags)
+
+
 def test_library_exports_every_declared_symbol():
     nat = _lib()
     abi_checks.check_exports(nat.LIB_PATH, nat.SIGNATURES)

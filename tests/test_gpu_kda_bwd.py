@@ -283,6 +283,47 @@ def test_bwd_rows_outside_the_sequences_get_zero_gradients(recurrent):
     _compare(got, want, f"padded batch recurrent={recurrent}", TOL if recurrent else TOL_CHUNK)
 
 
+@pytest.mark.parametrize("recurrent", [False, True])
+def test_bf16_gradients_are_the_fp32_gradients_rounded(recurrent):
+    """grad_dtype=torch.bfloat16 (SOPHIA_KDA_BWD_GRAD_BF16, the call the
+    autograd function makes for bf16 q, k, v): dq, dk, dv equal the fp32
+    call's gradients rounded to nearest even, bit for bit, on a padded batch
+    with device-only offsets (the rows outside the sequences zero in bf16
+    too); dg, dbeta, dh0, dA_log and ddt_bias are the fp32 call's, bit for
+    bit."""
+    cu = [0, 37, 37, 166, 230]
+    inp, d_out, d_final, flags = _inputs(cu, 2, seed=91, gated=True, dtype=torch.bfloat16,
+                                         gb_dtype=torch.bfloat16)
+    lead, tail = 3, 21
+    total = cu[-1] + lead + tail
+    dev = "cuda"
+
+    def pad(t):
+        out = torch.full((total,) + tuple(t.shape[1:]), float("nan"), dtype=t.dtype)
+        out[lead:lead + cu[-1]] = t
+        return out.to(dev)
+
+    cu_d = torch.tensor([c + lead for c in cu], dtype=torch.int32, device=dev)
+    args = [pad(inp[n]) for n in ("q", "k", "v", "g", "beta")] + [cu_d, pad(d_out)]
+    kw = dict(A_log=inp["A_log"].to(dev), dt_bias=inp["dt_bias"].to(dev), initial_state=inp["h0"].to(dev),
+              d_final_state=d_final.to(dev), recurrent=recurrent, **flags)
+    f32 = ops.kda_chunk_bwd(*args, **kw)
+    b16 = ops.kda_chunk_bwd(*args, grad_dtype=torch.bfloat16, **kw)
+    torch.cuda.synchronize()
+    for i, name in enumerate(("q", "k", "v")):
+        assert b16[i].dtype == torch.bfloat16 and b16[i].shape == f32[i].shape
+        assert f32[i].dtype == torch.float32
+        assert torch.isfinite(f32[i]).all(), f"d{name}"
+        assert torch.equal(b16[i].view(torch.int16), f32[i].to(torch.bfloat16).view(torch.int16)), f"d{name}"
+        outside = torch.cat([b16[i][:lead], b16[i][lead + cu[-1]:]])
+        assert torch.equal(outside.view(torch.int16), torch.zeros_like(outside.view(torch.int16))), f"d{name}"
+    for i, name in zip(range(3, 8), ("g", "beta", "h0", "A_log", "dt_bias")):
+        assert b16[i].dtype == torch.float32
+        assert torch.equal(b16[i].view(torch.int32), f32[i].view(torch.int32)), f"d{name}"
+    with pytest.raises(RuntimeError, match="grad_dtype"):
+        ops.kda_chunk_bwd(*args, grad_dtype=torch.float16, **kw)
+
+
 def test_chunk_bwd_matches_torch_autograd_restatement():
     cu = [0, 9, 24, 90]
     inp, d_out, d_final, flags = _inputs(cu, 1, seed=13, gated=True, dtype=torch.float32)
