@@ -26,6 +26,10 @@
  *                           attention.py:330-348 (T == 1 with a cached state)
  *   sophia_kda_decode_conv_step  the two above in one launch (the conv step of
  *                           attention.py:236-257 followed by 330-348)
+ *   sophia_kda_conv_chunk_fwd  sophia_short_conv_fwd over the q, k, v channels
+ *                           followed by sophia_kda_chunk_fwd, the conv inside the
+ *                           prefill's intra-chunk kernel (the prefill rows of
+ *                           SophiaKDA.forward: attention.py:226-258 then 349-365)
  *   sophia_kda_chunk_bwd    FlashKDA's chunk_kda_train_bwd with l2norm_bwd and
  *                           fused_beta_sigmoid_bwd, as FlashKDAFunction.backward
  *                           calls them (sm120_concurrent_ffn.py:301-373)
@@ -248,6 +252,40 @@ int sophia_kda_decode_conv_step(const void *x_q, const void *x_k, const void *x_
                                 float *state, int n_state_slots, const int32_t *state_slots, int read_state,
                                 int batch, int num_heads, int head_dim, void *o, int64_t o_row_stride,
                                 void *stream);
+
+/*
+ * The prefill of a KDA layer with its ShortConv: the causal conv + SiLU of the
+ * q, k and v channels over each sequence (CausalDepthwiseConv1d.forward,
+ * attention.py:32-60, as SophiaKDA._short_convolution drives it, 226-258)
+ * computed inside the chunk prefill's intra-chunk kernel from the rows before
+ * the conv, then the prefill of sophia_kda_chunk_fwd (attention.py:349-365).
+ * The conv outputs never reach memory.
+ *   x_q, x_k, x_v : [total, H, 128] bf16 projection rows before the conv (row
+ *                   stride x_row_stride elements, a multiple of 8; 16-byte
+ *                   aligned); each conv output is rounded to bf16, as the
+ *                   separate ShortConv writes it.
+ *   conv_weight   : [3 * H * 128, kernel_size] fp32 taps (q | k | v channels),
+ *                   16-byte aligned.
+ *   conv_state    : [n_state_slots, 3 * H * 128, kernel_size - 1] fp32 histories
+ *                   (16-byte aligned) or NULL: sequence s uses slot
+ *                   state_slots[s] (or s), read when read_history != 0 (else,
+ *                   and for a slot outside [0, n_state_slots), zeros) and
+ *                   replaced by the last kernel_size - 1 rows of
+ *                   cat(history, x) of the sequence.
+ *   kernel_size   : 4.
+ * Other arguments, the workspace size and the states as sophia_kda_chunk_fwd
+ * (q, k, v being the conv outputs; n_seqs <= 65535).  Results are bitwise those
+ * of sophia_short_conv_fwd (write_history = 1) followed by sophia_kda_chunk_fwd.
+ */
+int sophia_kda_conv_chunk_fwd(const void *x_q, const void *x_k, const void *x_v, int64_t x_row_stride,
+                              int qkv_dtype, const float *conv_weight, float *conv_state, int kernel_size,
+                              int read_history, const void *g, int64_t g_row_stride, int g_dtype,
+                              const void *beta, int64_t beta_row_stride, int beta_dtype, const float *A_log,
+                              const float *dt_bias, float scale, float lower_bound, unsigned flags,
+                              const int32_t *cu_seqlens, const int32_t *cu_seqlens_host, int n_seqs,
+                              int64_t total_tokens, int num_heads, int head_dim, const float *initial_state,
+                              float *final_state, int n_state_slots, const int32_t *state_slots, void *o,
+                              int64_t o_row_stride, void *workspace, size_t workspace_bytes, void *stream);
 
 /*
  * Backward of the prefill (training).  Replaces FlashKDA's chunk_kda_train_bwd

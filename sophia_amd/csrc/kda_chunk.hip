@@ -255,6 +255,16 @@ struct IntraArgs {
   const void *dout;
   int64_t do_stride;
   int do_dtype;
+  // Fused ShortConv instantiations only (kda_chunk_conv_intra_kernel): q, k,
+  // v above are the rows before the conv; taps [3 H 128][4] fp32 (q | k | v
+  // channels, taps[c][3] multiplies the current row); histories
+  // [conv_n_slots][3 H 128][3] fp32, sequence s in slot conv_slots[s] (or s),
+  // read when conv_read (else, and for a slot out of range, zeros).
+  const float *conv_w;
+  float *conv_state;
+  const int32_t *conv_slots;
+  int conv_n_slots;
+  int conv_read;
 };
 
 __device__ __forceinline__ float fast_sigmoid(float x) {
@@ -377,15 +387,142 @@ __device__ __forceinline__ void intra_scaled_operands(
   }
 }
 
+// ---- fused ShortConv (kda_chunk_conv_intra_kernel) ----------------------------
+// q, k, v arrive as the rows before the conv (whole lines in LDS: q in region
+// A, k in C, v at stage_v; row r of wave w's 16 rows, 16-byte chunk j at chunk
+// position j ^ r).  Lane l < 48 of wave w convolves chunk l & 15 (8 channels)
+// of tensor l >> 4 (q, k, v) over the wave's 16 rows, in place, exactly as
+// short_conv_fwd_kernel does: acc = sum_j taps[j] x[t - 3 + j] by fused
+// multiply-adds from j = 0, y = acc sigmoid(acc), rounded to bf16.  The 3 rows
+// before a wave's rows: rows 13..15 of wave w - 1 (read before any wave
+// overwrites them); for wave 0 the 3 rows before the chunk, or, in the
+// sequence's first chunk, its history (rounded to bf16, as the separate conv
+// reads it) or zeros.
+struct ConvPre {
+  f4 taps[8];   // taps of channel 8j + i
+  u4 halo[6];   // wave 0: the 3 rows before the chunk (bf16, halo[0..2]) or the fp32 history [8][3]
+};
+
+__device__ __forceinline__ size_t conv_region(int tn, int w) {
+  return tn == 0 ? kSmA + w * 4096 : (tn == 1 ? kSmC + w * 4096 : stage_v(w));
+}
+
+__device__ __forceinline__ void unpack_bf16x8(u4 v, float (&x)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = __uint_as_float(v[i] << 16);
+    x[2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u);
+  }
+}
+
+// Issues the loads of the taps and of wave 0's 3 rows before the chunk.
+__device__ __forceinline__ ConvPre conv_issue(const IntraArgs &p, int s, bool first_chunk, int h, int w, int l,
+                                              int64_t t0) {
+  ConvPre cp;
+  const int tn = l >> 4, j = l & 15;
+#pragma unroll
+  for (int i = 0; i < 6; ++i) cp.halo[i] = u4{0u, 0u, 0u, 0u};
+  if (l < 48) {
+    const int64_t ch = (static_cast<int64_t>(tn) * p.num_heads + h) * kD + 8 * j;
+    const f4 *tw = reinterpret_cast<const f4 *>(p.conv_w + ch * 4);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) cp.taps[i] = tw[i];
+    if (w == 0) {
+      if (!first_chunk) {
+        const uint16_t *x = static_cast<const uint16_t *>(tn == 0 ? p.q : (tn == 1 ? p.k : p.v));
+#pragma unroll
+        for (int r = 0; r < 3; ++r)
+          cp.halo[r] = *reinterpret_cast<const u4 *>(x + (t0 - 3 + r) * p.qkv_stride + h * kD + 8 * j);
+      } else {
+        const int slot = p.conv_slots ? p.conv_slots[s] : s;
+        if (p.conv_read && p.conv_state && slot >= 0 && slot < p.conv_n_slots) {
+          const u4 *hp = reinterpret_cast<const u4 *>(
+              p.conv_state + (static_cast<int64_t>(slot) * 3 * p.num_heads * kD + ch) * 3);
+#pragma unroll
+          for (int i = 0; i < 6; ++i) cp.halo[i] = hp[i];
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) cp.taps[i] = f4{0.f, 0.f, 0.f, 0.f};
+  }
+  return cp;
+}
+
+// Convolves the wave's rows in LDS (after every wave's line copies landed).
+__device__ __forceinline__ void conv_apply(const ConvPre &cp, bool first_chunk, int w, int l, uint8_t *smem) {
+  const int tn = l >> 4, j = l & 15;
+  const bool on = l < 48;
+  float win[3][8];
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's line copies (every load so far) have landed
+  lds_barrier();                  // ... and every wave's
+  if (on) {
+    if (w > 0) {
+      const uint8_t *prev = smem + conv_region(tn, w - 1);
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        const int r = 13 + k;
+        unpack_bf16x8(*reinterpret_cast<const u4 *>(prev + r * 256 + ((j ^ r) << 4)), win[k]);
+      }
+    } else if (!first_chunk) {
+#pragma unroll
+      for (int k = 0; k < 3; ++k) unpack_bf16x8(cp.halo[k], win[k]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+          const int e = 3 * i + k;  // history [channel i][k]
+          win[k][i] = bf16_bits_to_f32(f32_to_bf16_bits(__uint_as_float(cp.halo[e >> 2][e & 3])));
+        }
+    }
+  }
+  lds_barrier();  // every window is read before any row is overwritten
+  if (!on) return;
+  uint8_t *reg = smem + conv_region(tn, w);
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    u4 rows[8];
+#pragma unroll
+    for (int rr = 0; rr < 8; ++rr) {
+      const int r = 8 * half + rr;
+      rows[rr] = *reinterpret_cast<const u4 *>(reg + r * 256 + ((j ^ r) << 4));
+    }
+#pragma unroll
+    for (int rr = 0; rr < 8; ++rr) {
+      const int r = 8 * half + rr;
+      float x[8], y[8];
+      unpack_bf16x8(rows[rr], x);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float acc = 0.f;
+        acc = fmaf(cp.taps[i][0], win[0][i], acc);
+        acc = fmaf(cp.taps[i][1], win[1][i], acc);
+        acc = fmaf(cp.taps[i][2], win[2][i], acc);
+        acc = fmaf(cp.taps[i][3], x[i], acc);
+        y[i] = acc * sigmoid_f(acc);
+        win[0][i] = win[1][i];
+        win[1][i] = win[2][i];
+        win[2][i] = x[i];
+      }
+      *reinterpret_cast<u4 *>(reg + r * 256 + ((j ^ r) << 4)) =
+          u4{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]), pack_bf16x2(y[4], y[5]), pack_bf16x2(y[6], y[7])};
+    }
+  }
+}
+
 // One (chunk c, head h) of the intra phase on 256 threads (tid 0..255, four
 // wavefronts) with kSmIntra bytes of LDS at smem; writes the record at rec.
 // Every barrier inside is a work-group barrier: a work-group running two
 // items at once runs them in lock step.
 // BWD: the backward's instantiation, which also writes the backward record,
 // T and P of the item (IntraArgs::brec / tpmat), in the same LDS.
-template <int QKV_DT, int G_DT, bool GATE, bool BWD = false>
+// CONV: q, k, v are the rows before the fused ShortConv (bf16 whole lines only).
+template <int QKV_DT, int G_DT, bool GATE, bool BWD = false, bool CONV = false>
 __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int first, int h, uint8_t *smem,
                                            int tid, uint8_t *rec) {
+  static_assert(!CONV || (QKV_DT == SOPHIA_DTYPE_BF16 && !BWD), "the fused conv takes bf16 lines, forward only");
   const size_t item = static_cast<size_t>(c) * p.num_heads + h;
   uint8_t *brec = BWD ? p.brec + item * kBwdRecBytes : nullptr;
   uint16_t *sQt = reinterpret_cast<uint16_t *>(smem + kSmA);   // backward, at the end: Q e^G transposed
@@ -445,7 +582,9 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
     Raw4<QKV_DT> rq[8], rk[8], rv[8];
     Raw4<G_DT> rg[8];
     bool lines = false;
-    if constexpr (QKV_DT == SOPHIA_DTYPE_BF16) lines = p.qkv_lines != 0;
+    if constexpr (QKV_DT == SOPHIA_DTYPE_BF16) lines = CONV || p.qkv_lines != 0;
+    ConvPre cpre;
+    if constexpr (CONV) cpre = conv_issue(p, s, c == first, h, w, l, t0);
     if (lines) {
       // Whole cache lines: each wave copies its 16 rows of q, k, v (256 B per
       // row and head) straight into LDS, four rows per instruction, 16-byte
@@ -474,6 +613,7 @@ __device__ __forceinline__ void intra_item(const IntraArgs &p, int c, int s, int
 #pragma unroll
     for (int i = 0; i < 8; ++i) rg[i].load(p.g, grow + 32 * (i >> 1) + 16 * (i & 1) + 4 * gq);
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (CONV) conv_apply(cpre, c == first, w, l, smem);
     if constexpr (QKV_DT == SOPHIA_DTYPE_BF16) {
       if (lines) {
         // Slot i = 2 ks + a holds channels 32 ks + 16 a + 4 gq .. + 3: bytes
@@ -889,6 +1029,63 @@ __global__ __launch_bounds__(kThreads, 2) void kda_chunk_intra_kernel(IntraArgs 
   if (s >= p.n_seqs) return;  // past the last chunk (uniform over the work-group)
   intra_item<QKV_DT, G_DT, GATE>(p, c, s, first, h, smem, threadIdx.x,
                                  p.records + (static_cast<size_t>(c) * p.num_heads + h) * kRecBytes);
+}
+
+// The forward with the ShortConv of q, k, v fused in: q, k, v are bf16 rows
+// before the conv (16-byte aligned, whole lines), IntraArgs::conv_* the taps
+// and histories.  Items and records as kda_chunk_intra_kernel.
+template <int G_DT, bool GATE>
+__global__ __launch_bounds__(kThreads, 2) void kda_chunk_conv_intra_kernel(IntraArgs p) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int h = static_cast<int>(blockIdx.x % static_cast<unsigned>(p.num_heads));
+  const int c = static_cast<int>(p.max_ch - 1) - static_cast<int>(blockIdx.x / static_cast<unsigned>(p.num_heads));
+  if (c < 0) return;
+  int s, first;
+  chunk_of(p.cu, p.n_seqs, p.total, c, s, first);
+  if (s >= p.n_seqs) return;
+  intra_item<SOPHIA_DTYPE_BF16, G_DT, GATE, false, true>(
+      p, c, s, first, h, smem, threadIdx.x, p.records + (static_cast<size_t>(c) * p.num_heads + h) * kRecBytes);
+}
+
+// New conv histories after kda_chunk_conv_intra_kernel has read the old ones:
+// history[slot(s)][ch][0..2] <- the last 3 rows of cat(history (bf16-rounded,
+// or zeros), x rows of sequence s), as short_conv_history_kernel writes them.
+// One thread per (sequence = blockIdx.y, tensor, head, 8-channel chunk).
+__global__ __launch_bounds__(256) void kda_conv_history_kernel(IntraArgs p) {
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  const int s = blockIdx.y;
+  const int per_tensor = p.num_heads * (kD / 8);
+  if (t >= 3 * per_tensor || s >= p.n_seqs || !p.conv_state) return;
+  const int slot = p.conv_slots ? p.conv_slots[s] : s;
+  if (slot < 0 || slot >= p.conv_n_slots) return;
+  const int tn = t / per_tensor, rem = t - tn * per_tensor;
+  const int h = rem / (kD / 8), j = rem % (kD / 8);
+  const int64_t start = iclamp64(p.cu[s], 0, p.total);
+  const int64_t end = iclamp64(p.cu[s + 1], start, p.total);
+  const uint16_t *x = static_cast<const uint16_t *>(tn == 0 ? p.q : (tn == 1 ? p.k : p.v));
+  float *hist = p.conv_state +
+                (static_cast<int64_t>(slot) * 3 * p.num_heads * kD + (static_cast<int64_t>(tn) * p.num_heads + h) * kD +
+                 8 * j) * 3;
+  float nh[8][3];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    const int64_t tau = end - 3 + k;
+    if (tau >= start) {
+      float v[8];
+      unpack_bf16x8(*reinterpret_cast<const u4 *>(x + tau * p.qkv_stride + h * kD + 8 * j), v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) nh[i][k] = v[i];
+    } else {
+      const int idx = 3 + static_cast<int>(tau - start);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        nh[i][k] = p.conv_read ? bf16_bits_to_f32(f32_to_bf16_bits(hist[i * 3 + idx])) : 0.f;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int k = 0; k < 3; ++k) hist[i * 3 + k] = nh[i][k];
 }
 
 // The backward's instantiation: the same item, plus the backward record, T
@@ -2558,6 +2755,18 @@ int launch_intra(dim3 grid, hipStream_t st, const IntraArgs &ia) {
   return check_launch("kda_chunk_intra");
 }
 
+template <int G_DT, bool GATE>
+struct ConvIntraKey {};
+
+template <int G_DT, bool GATE>
+int launch_conv_intra(dim3 grid, hipStream_t st, const IntraArgs &ia) {
+  if (const int rc = ensure_lds<ConvIntraKey<G_DT, GATE>>(
+          reinterpret_cast<const void *>(&kda_chunk_conv_intra_kernel<G_DT, GATE>), kSmIntra))
+    return rc;
+  hipLaunchKernelGGL((kda_chunk_conv_intra_kernel<G_DT, GATE>), grid, dim3(kThreads), kSmIntra, st, ia);
+  return check_launch("kda_chunk_conv_intra");
+}
+
 template <int QKV_DT, int G_DT, bool GATE>
 int launch_intra_bwd(dim3 grid, hipStream_t st, const IntraArgs &ia) {
   if (const int rc = ensure_lds<IntraKey<QKV_DT, G_DT, GATE, true>>(
@@ -2690,8 +2899,16 @@ extern "C" size_t sophia_kda_chunk_workspace_size(int64_t total_tokens, int n_se
 }
 
 namespace {
-// The body of both prefill entry points: `workspace` is either the caller's
-// buffer or this library's static scratch (sophia_kda_chunk_fwd_no_alloc).
+// The ShortConv fused into the prefill (sophia_kda_conv_chunk_fwd).
+struct ConvIO {
+  const float *weight;  // [3 H 128][4] fp32
+  float *state;         // [n_state_slots][3 H 128][3] fp32, or NULL
+  int read_history;
+};
+
+// The body of the prefill entry points: `workspace` is either the caller's
+// buffer or this library's static scratch (sophia_kda_chunk_fwd_no_alloc);
+// with `conv`, q, k, v are the rows before the fused ShortConv.
 int chunk_fwd_impl(const void *q, const void *k, const void *v, int64_t qkv_row_stride, int qkv_dtype,
                    const void *g, int64_t g_row_stride, int g_dtype, const void *beta,
                    int64_t beta_row_stride, int beta_dtype, const float *A_log, const float *dt_bias,
@@ -2699,7 +2916,7 @@ int chunk_fwd_impl(const void *q, const void *k, const void *v, int64_t qkv_row_
                    const int32_t *cu_seqlens_host, int n_seqs, int64_t total_tokens, int num_heads,
                    int head_dim, const float *initial_state, float *final_state, int n_state_slots,
                    const int32_t *state_slots, void *o, int64_t o_row_stride, void *workspace,
-                   size_t workspace_bytes, void *stream) {
+                   size_t workspace_bytes, void *stream, const ConvIO *conv = nullptr) {
   SOPHIA_REQUIRE(head_dim == kD, "kda_chunk_fwd: head_dim must be 128 (got %d)", head_dim);
   SOPHIA_REQUIRE(n_seqs > 0 && num_heads > 0 && num_heads <= 65535 && total_tokens >= 0,
                  "kda_chunk_fwd: bad n_seqs / num_heads / total_tokens");
@@ -2740,19 +2957,32 @@ int chunk_fwd_impl(const void *q, const void *k, const void *v, int64_t qkv_row_
   uint8_t *trash = static_cast<uint8_t *>(workspace);
   uint8_t *records = trash + kTrashBytes;
   int rc = SOPHIA_OK;
+  const auto a16 = [](const void *ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; };
+  const int lines = qkv_dtype == SOPHIA_DTYPE_BF16 && qkv_row_stride % 8 == 0 && a16(q) && a16(k) && a16(v);
+  IntraArgs ia{q, k, v, qkv_row_stride, qkv_dtype, g, g_row_stride, g_dtype, beta,
+               beta_row_stride, beta_dtype, A_log, dt_bias, scale, lower_bound, flags,
+               cu_seqlens, n_seqs, total_tokens, num_heads, max_ch, records, lines};
+  if (conv) {
+    SOPHIA_REQUIRE(lines || total_tokens == 0,
+                   "kda_conv_chunk_fwd: x must be bf16 rows, 16-byte aligned, row stride a multiple of 8");
+    ia.conv_w = conv->weight;
+    ia.conv_state = conv->state;
+    ia.conv_slots = state_slots;
+    ia.conv_n_slots = conv->state ? n_state_slots : 0;
+    ia.conv_read = conv->read_history;
+  }
 
   if (max_ch > 0 && total_tokens > 0) {
-    const auto a16 = [](const void *ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; };
-    const int lines = qkv_dtype == SOPHIA_DTYPE_BF16 && qkv_row_stride % 8 == 0 && a16(q) && a16(k) && a16(v);
-    IntraArgs ia{q, k, v, qkv_row_stride, qkv_dtype, g, g_row_stride, g_dtype, beta,
-                 beta_row_stride, beta_dtype, A_log, dt_bias, scale, lower_bound, flags,
-                 cu_seqlens, n_seqs, total_tokens, num_heads, max_ch, records, lines};
     SOPHIA_REQUIRE(max_ch * num_heads <= 0x7fffffff, "kda_chunk_fwd: grid too large");
     const dim3 grid(static_cast<unsigned>(max_ch * num_heads));
     const bool gate = (flags & SOPHIA_KDA_GATE_IN_KERNEL) != 0;
     const int key = (qkv_dtype == SOPHIA_DTYPE_BF16) * 4 + (g_dtype == SOPHIA_DTYPE_BF16) * 2 + gate;
     constexpr int F = SOPHIA_DTYPE_F32, B = SOPHIA_DTYPE_BF16;
-    switch (key) {
+    switch (conv ? 8 + (g_dtype == SOPHIA_DTYPE_BF16) * 2 + gate : key) {
+      case 8: rc = launch_conv_intra<F, false>(grid, st, ia); break;
+      case 9: rc = launch_conv_intra<F, true>(grid, st, ia); break;
+      case 10: rc = launch_conv_intra<B, false>(grid, st, ia); break;
+      case 11: rc = launch_conv_intra<B, true>(grid, st, ia); break;
       case 0: rc = launch_intra<F, F, false>(grid, st, ia); break;
       case 1: rc = launch_intra<F, F, true>(grid, st, ia); break;
       case 2: rc = launch_intra<F, B, false>(grid, st, ia); break;
@@ -2763,6 +2993,13 @@ int chunk_fwd_impl(const void *q, const void *k, const void *v, int64_t qkv_row_
       default: rc = launch_intra<B, B, true>(grid, st, ia); break;
     }
     if (rc) return rc;
+  }
+  if (conv && conv->state) {
+    // after the intra kernel has read the old histories
+    const int threads = 3 * num_heads * (kD / 8);
+    hipLaunchKernelGGL(kda_conv_history_kernel, dim3(static_cast<unsigned>((threads + 255) / 256),
+                                                     static_cast<unsigned>(n_seqs)), dim3(256), 0, st, ia);
+    if (const int rc2 = check_launch("kda_conv_history")) return rc2;
   }
   // The state scan is sequential over the chunks of a sequence: the 128
   // value columns of each (sequence, head) are split over 1, 2, 4 or 8
@@ -2871,6 +3108,31 @@ extern "C" int sophia_kda_chunk_fwd(const void *q, const void *k, const void *v,
                         cu_seqlens, cu_seqlens_host, n_seqs, total_tokens, num_heads, head_dim,
                         initial_state, final_state, n_state_slots, state_slots, o, o_row_stride,
                         workspace, workspace_bytes, stream);
+}
+
+extern "C" int sophia_kda_conv_chunk_fwd(const void *x_q, const void *x_k, const void *x_v,
+                                         int64_t x_row_stride, int qkv_dtype, const float *conv_weight,
+                                         float *conv_state, int kernel_size, int read_history, const void *g,
+                                         int64_t g_row_stride, int g_dtype, const void *beta,
+                                         int64_t beta_row_stride, int beta_dtype, const float *A_log,
+                                         const float *dt_bias, float scale, float lower_bound, unsigned flags,
+                                         const int32_t *cu_seqlens, const int32_t *cu_seqlens_host, int n_seqs,
+                                         int64_t total_tokens, int num_heads, int head_dim,
+                                         const float *initial_state, float *final_state, int n_state_slots,
+                                         const int32_t *state_slots, void *o, int64_t o_row_stride,
+                                         void *workspace, size_t workspace_bytes, void *stream) {
+  const auto a16 = [](const void *ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; };
+  SOPHIA_REQUIRE(kernel_size == 4, "kda_conv_chunk_fwd: kernel_size must be 4 (got %d)", kernel_size);
+  SOPHIA_REQUIRE(qkv_dtype == SOPHIA_DTYPE_BF16, "kda_conv_chunk_fwd: x must be bf16");
+  SOPHIA_REQUIRE(conv_weight && a16(conv_weight), "kda_conv_chunk_fwd: conv_weight must be 16-byte aligned");
+  SOPHIA_REQUIRE(!conv_state || a16(conv_state), "kda_conv_chunk_fwd: conv_state must be 16-byte aligned");
+  SOPHIA_REQUIRE(n_seqs > 0 && n_seqs <= 65535, "kda_conv_chunk_fwd: n_seqs must be in [1, 65535]");
+  const ConvIO conv{conv_weight, conv_state, read_history != 0};
+  return chunk_fwd_impl(x_q, x_k, x_v, x_row_stride, qkv_dtype, g, g_row_stride, g_dtype, beta,
+                        beta_row_stride, beta_dtype, A_log, dt_bias, scale, lower_bound, flags,
+                        cu_seqlens, cu_seqlens_host, n_seqs, total_tokens, num_heads, head_dim,
+                        initial_state, final_state, n_state_slots, state_slots, o, o_row_stride,
+                        workspace, workspace_bytes, stream, &conv);
 }
 
 extern "C" int sophia_kda_chunk_fwd_no_alloc(const void *q, const void *k, const void *v,

@@ -513,36 +513,50 @@ class SophiaKDA(nn.Module):
         conv_state = (self.conv_state.view(self.conv_state.size(0), 3 * i, hist)
                       if hist > 0 else None)
         conv_w = self._conv_weight(qkv.dtype)
-        conv_out = torch.empty((n, 3 * i), dtype=qkv.dtype, device=qkv.device)
-        if n_prefill > 0:
+        # The prefill rows' ShortConv runs inside the chunk prefill when the
+        # rows before the conv are bf16 whole lines (the fused projection's).
+        fused_prefill = (n_prefill > 0 and hist == 3 and qkv.dtype == torch.bfloat16
+                         and qkv.stride(1) == 1 and qkv.stride(0) % 8 == 0 and qkv.data_ptr() % 16 == 0)
+        fused_decode = n_decode > 0 and hist == 3
+        conv_out = None
+        if not (fused_prefill or n_prefill == 0) or not (fused_decode or n_decode == 0):
+            conv_out = torch.empty((n, 3 * i), dtype=qkv.dtype, device=qkv.device)
+        if n_prefill > 0 and not fused_prefill:
             ops.short_conv_fwd(qkv[:n_prefill], conv_w, cu_prefill, conv_state=conv_state,
                                state_slots=prefill_slots,
                                read_history=bool(prefill_reads_cache) and hist > 0,
                                write_history=hist > 0, out=conv_out[:n_prefill],
                                weight_rounded=True)
-        fused_decode = n_decode > 0 and hist == 3
         if n_decode > 0 and not fused_decode:
             ops.short_conv_step(qkv[n_prefill:], conv_w, conv_state, state_slots=decode_slots,
                                 read_history=True, out=conv_out[n_prefill:], weight_rounded=True)
-        q = conv_out[:, :i].unflatten(1, (h, d))
-        k = conv_out[:, i: 2 * i].unflatten(1, (h, d))
-        v = conv_out[:, 2 * i:].unflatten(1, (h, d))
         decay = self.decay_up(dd).view(n, h, d)
         o = torch.empty((n, h, d), dtype=x2.dtype, device=x2.device)
         gate_args = dict(A_log=self.A_log, dt_bias=self.dt_bias, lower_bound=self.lower_bound)
-        if n_prefill > 0:
-            ops.kda_chunk_fwd(q[:n_prefill], k[:n_prefill], v[:n_prefill], decay[:n_prefill],
-                              beta_logits[:n_prefill], cu_prefill,
-                              initial_state=self.recurrent_state if prefill_reads_cache else None,
-                              final_state=self.recurrent_state, state_slots=prefill_slots,
-                              out=o[:n_prefill], cu_seqlens_cpu=cu_prefill_host, **gate_args)
+        states = dict(initial_state=self.recurrent_state if prefill_reads_cache else None,
+                      final_state=self.recurrent_state, state_slots=prefill_slots,
+                      cu_seqlens_cpu=cu_prefill_host)
+        if fused_prefill:
+            ops.kda_conv_chunk_fwd(qkv[:n_prefill], conv_w, conv_state, decay[:n_prefill],
+                                   beta_logits[:n_prefill], cu_prefill,
+                                   read_history=bool(prefill_reads_cache), out=o[:n_prefill],
+                                   **states, **gate_args)
+        elif n_prefill > 0:
+            q = conv_out[:n_prefill, :i].unflatten(1, (h, d))
+            k = conv_out[:n_prefill, i: 2 * i].unflatten(1, (h, d))
+            v = conv_out[:n_prefill, 2 * i:].unflatten(1, (h, d))
+            ops.kda_chunk_fwd(q, k, v, decay[:n_prefill], beta_logits[:n_prefill], cu_prefill,
+                              out=o[:n_prefill], **states, **gate_args)
         if fused_decode:
             # ShortConv step and recurrent step of the decode rows in one launch.
             ops.kda_decode_conv_step(qkv[n_prefill:], conv_w, conv_state, decay[n_prefill:],
                                      beta_logits[n_prefill:], self.recurrent_state,
                                      state_slots=decode_slots, out=o[n_prefill:], **gate_args)
         elif n_decode > 0:
-            ops.kda_decode_step(q[n_prefill:], k[n_prefill:], v[n_prefill:], decay[n_prefill:],
+            q = conv_out[n_prefill:, :i].unflatten(1, (h, d))
+            k = conv_out[n_prefill:, i: 2 * i].unflatten(1, (h, d))
+            v = conv_out[n_prefill:, 2 * i:].unflatten(1, (h, d))
+            ops.kda_decode_step(q, k, v, decay[n_prefill:],
                                 beta_logits[n_prefill:], self.recurrent_state,
                                 state_slots=decode_slots, read_state=True, out=o[n_prefill:],
                                 **gate_args)

@@ -260,6 +260,62 @@ def kda_chunk_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
     ``scan_segments=False`` keeps one chain per sequence).
     Returns o [total, H, 128] in q.dtype.
     """
+    return _prefill(q, k, v, g, beta, cu_seqlens, A_log, dt_bias, scale, lower_bound, use_qk_l2norm,
+                    use_gate, use_beta_sigmoid, initial_state, final_state, state_slots, out,
+                    cu_seqlens_cpu, scan_segments, None)
+
+
+def kda_conv_chunk_fwd(x_qkv: torch.Tensor, conv_weight: torch.Tensor,
+                       conv_state: torch.Tensor | None, g: torch.Tensor, beta: torch.Tensor,
+                       cu_seqlens: torch.Tensor, *, read_history: bool = False, A_log=None,
+                       dt_bias=None, scale: float | None = None, lower_bound: float = -5.0,
+                       use_qk_l2norm: bool = True, use_gate: bool = True,
+                       use_beta_sigmoid: bool = True, initial_state: torch.Tensor | None = None,
+                       final_state: torch.Tensor | None = None,
+                       state_slots: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                       cu_seqlens_cpu: torch.Tensor | None = None,
+                       scan_segments: bool = True) -> torch.Tensor:
+    """The prefill of a KDA layer with its ShortConv fused into the chunk
+    prefill (sophia_kda_conv_chunk_fwd): ``short_conv_fwd`` of the q | k | v
+    channels (write_history=True) followed by ``kda_chunk_fwd``, bitwise, with
+    the conv outputs never written (attention.py:226-258, 349-365).
+
+    x_qkv: bf16 [total, 3 * H * 128] rows before the conv (16-byte aligned,
+    row stride a multiple of 8); conv_weight: contiguous fp32 [3 * H * 128, 4]
+    taps already rounded to bf16; conv_state: contiguous fp32 [slots,
+    3 * H * 128, 3] or None, the slot of each sequence read when
+    ``read_history`` and replaced by its last 3 rows; it shares ``state_slots``
+    (and the slot count) with initial_state / final_state.  Other arguments
+    as ``kda_chunk_fwd``.  Returns o [total, H, 128] (bf16)."""
+    _gpu(x_qkv, "x_qkv")
+    _gpu(g, "g")
+    device = x_qkv.device
+    heads = int(g.size(1)) if g.dim() == 3 else 0
+    inner = heads * HEAD_DIM
+    _rows(x_qkv, "x_qkv", 3 * inner)
+    if x_qkv.dtype != torch.bfloat16:
+        raise RuntimeError("x_qkv must be bf16")
+    if (conv_weight.dtype != torch.float32 or not conv_weight.is_contiguous()
+            or tuple(conv_weight.shape) != (3 * inner, 4) or conv_weight.device != device):
+        raise RuntimeError(f"conv_weight must be contiguous fp32 [{3 * inner}, 4] on {device}")
+    if conv_state is not None:
+        _gpu(conv_state, "conv_state")
+        if (conv_state.dtype != torch.float32 or not conv_state.is_contiguous()
+                or conv_state.dim() != 3 or tuple(conv_state.shape[1:]) != (3 * inner, 3)):
+            raise RuntimeError(f"conv_state must be contiguous fp32 [slots, {3 * inner}, 3]")
+    q = x_qkv[:, :inner].unflatten(1, (heads, HEAD_DIM))
+    k = x_qkv[:, inner: 2 * inner].unflatten(1, (heads, HEAD_DIM))
+    v = x_qkv[:, 2 * inner: 3 * inner].unflatten(1, (heads, HEAD_DIM))
+    return _prefill(q, k, v, g, beta, cu_seqlens, A_log, dt_bias, scale, lower_bound, use_qk_l2norm,
+                    use_gate, use_beta_sigmoid, initial_state, final_state, state_slots, out,
+                    cu_seqlens_cpu, scan_segments, (conv_weight, conv_state, bool(read_history)))
+
+
+def _prefill(q, k, v, g, beta, cu_seqlens, A_log, dt_bias, scale, lower_bound, use_qk_l2norm,
+             use_gate, use_beta_sigmoid, initial_state, final_state, state_slots, out,
+             cu_seqlens_cpu, scan_segments, conv):
+    """kda_chunk_fwd, or with ``conv`` = (taps, histories or None,
+    read_history) the fused-conv prefill on pre-conv q, k, v views."""
     for t, name in ((q, "q"), (k, "k"), (v, "v"), (g, "g"), (beta, "beta")):
         _gpu(t, name)
     device = q.device
@@ -298,6 +354,11 @@ def kda_chunk_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
     if len(n_slots) == 2 and n_slots[0] != n_slots[1]:
         raise RuntimeError("initial_state and final_state must have the same number of slots")
     n_slots = n_slots[0] if n_slots else 0
+    if conv is not None and conv[1] is not None:
+        conv_slots = int(conv[1].size(0))
+        if n_slots and conv_slots != n_slots:
+            raise RuntimeError("conv_state and the state tensors must have the same number of slots")
+        n_slots = conv_slots
     if state_slots is None and n_slots and n_slots < n:
         raise RuntimeError("state tensors have fewer slots than sequences")
     slots = _int32(state_slots, "state_slots", device)
@@ -314,16 +375,21 @@ def kda_chunk_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
     lib = nat.lib()
     need = int(lib.sophia_kda_chunk_workspace_size(total, n, heads, HEAD_DIM))
     buf, ws_addr, ws_bytes = _workspace(need, device)
-    rc = lib.sophia_kda_chunk_fwd(
-        nat.ptr(q), nat.ptr(k), nat.ptr(v), qs, nat.dtype_code(q.dtype), nat.ptr(g), gs,
-        nat.dtype_code(g.dtype), nat.ptr(beta), bs, nat.dtype_code(beta.dtype), nat.ptr(a_log),
-        nat.ptr(dtb), float(scale), float(lower_bound),
-        _flags(use_qk_l2norm, use_gate, use_beta_sigmoid)
-        | (0 if scan_segments else nat.SCAN_NO_SEGMENTS), nat.ptr(cu),
-        None if cu_host is None else cu_host.data_ptr(), n, total, heads, HEAD_DIM,
-        nat.ptr(initial_state), nat.ptr(final_state), n_slots, nat.ptr(slots), nat.ptr(o), os_,
-        ws_addr, ws_bytes, nat.stream_handle(device))
-    nat.check(rc, "sophia_kda_chunk_fwd")
+    common = (nat.ptr(g), gs, nat.dtype_code(g.dtype), nat.ptr(beta), bs, nat.dtype_code(beta.dtype),
+              nat.ptr(a_log), nat.ptr(dtb), float(scale), float(lower_bound),
+              _flags(use_qk_l2norm, use_gate, use_beta_sigmoid)
+              | (0 if scan_segments else nat.SCAN_NO_SEGMENTS), nat.ptr(cu),
+              None if cu_host is None else cu_host.data_ptr(), n, total, heads, HEAD_DIM,
+              nat.ptr(initial_state), nat.ptr(final_state), n_slots, nat.ptr(slots), nat.ptr(o), os_,
+              ws_addr, ws_bytes, nat.stream_handle(device))
+    if conv is None:
+        rc = lib.sophia_kda_chunk_fwd(nat.ptr(q), nat.ptr(k), nat.ptr(v), qs, nat.dtype_code(q.dtype),
+                                      *common)
+        nat.check(rc, "sophia_kda_chunk_fwd")
+    else:
+        rc = lib.sophia_kda_conv_chunk_fwd(nat.ptr(q), nat.ptr(k), nat.ptr(v), qs, nat.dtype_code(q.dtype),
+                                           nat.ptr(conv[0]), nat.ptr(conv[1]), 4, int(conv[2]), *common)
+        nat.check(rc, "sophia_kda_conv_chunk_fwd")
     del buf  # stream-ordered reuse by the caching allocator is safe
     return o
 

@@ -71,6 +71,23 @@ def check_host_side(lib, nat) -> None:
                                   -5.0, 1, 96, ctypes.addressof(host), 2, 100, 16, 128, None,
                                   None, 0, None, 256, 2048, 512, 1 << 30, None)
     assert rc == nat.SOPHIA_ERR_INVALID and "cu_seqlens_host" in nat.last_error()
+    # The fused-conv prefill: kernel size 4 and bf16 rows only; rows whose
+    # stride is not a multiple of 8 elements cannot be copied whole.
+    conv = lambda *a: lib.sophia_kda_conv_chunk_fwd(*a)  # noqa: E731
+    cargs = [16, 32, 48, 6160, 1, 64, 128, 4, 0, 80, 2048, 0, 96, 16, 0, None, None, 1.0, -5.0, 1, 112,
+             None, 2, 100, 16, 128, None, None, 0, None, 256, 2048, 512, 1 << 30, None]
+    a = list(cargs)
+    a[7] = 3
+    assert conv(*a) == nat.SOPHIA_ERR_INVALID and "kernel_size" in nat.last_error()
+    a = list(cargs)
+    a[4] = 0
+    assert conv(*a) == nat.SOPHIA_ERR_INVALID and "bf16" in nat.last_error()
+    a = list(cargs)
+    a[5] = 68
+    assert conv(*a) == nat.SOPHIA_ERR_INVALID and "conv_weight" in nat.last_error()
+    a = list(cargs)
+    a[3] = 6164
+    assert conv(*a) == nat.SOPHIA_ERR_INVALID and "stride" in nat.last_error()
     # Decoder kernels: dim not a multiple of 8, too deep, too wide, misaligned.
     mix = lambda *a: lib.sophia_attn_res_mix(*a)  # noqa: E731
     rc = mix(None, 1536, None, 0, None, 0, None, 0, 0, 0, None, None, 1e-5, None, 1e-5, None,

@@ -27,7 +27,7 @@ def test_header_declares_the_entry_points():
                  "sophia_last_error", "sophia_abi_version", "sophia_attn_res_mix",
                  "sophia_situ_glu", "sophia_gated_head_norm", "sophia_mla_decode_attn",
                  "sophia_mla_decode_workspace_size", "sophia_causal_attention",
-                 "sophia_short_conv_bwd", "sophia_gated_head_norm_bwd"):
+                 "sophia_short_conv_bwd", "sophia_gated_head_norm_bwd", "sophia_kda_conv_chunk_fwd"):
         assert name in decls, name
 
 
