@@ -29,6 +29,9 @@ from .config import ModelArgs
 from .state import LayerCacheSnapshot
 
 PAD_LOGIT = -1.0e4  # attention.py:17
+# Rows of the fused input projection are padded to a multiple of this many
+# output columns (64 bf16 = one 128-byte line).
+_PROJ_ROWS = 64
 
 
 def _inverse_softplus(value: torch.Tensor) -> torch.Tensor:
@@ -290,10 +293,12 @@ class SophiaKDA(nn.Module):
 
     def _input_weight(self, dtype: torch.dtype) -> torch.Tensor:
         """[3*inner + (inner | gate_rank) + decay_rank + heads, dim], padded
-        with zero rows to a multiple of 8: every projection of x in one GEMM,
-        whose output rows then start on 16-byte boundaries.  The q|k|v and
-        gate columns come first, at multiples of 8 columns, because the
-        ShortConv and gated-norm kernels read them with 16-byte vector loads."""
+        with zero rows to a multiple of _PROJ_ROWS: every projection of x in
+        one GEMM, whose bf16 output rows then start on 128-byte boundaries, so
+        that a head's 256 bytes of q, k or v are two whole cache lines for the
+        kernels that copy them (the fused-conv prefill).  The q|k|v and gate
+        columns come first, at multiples of 64 columns, because the ShortConv
+        and gated-norm kernels read them with 16-byte vector loads."""
         mods = [self.q_proj, self.k_proj, self.v_proj,
                 self.output_gate if self.output_gate_full_rank else self.output_gate_down,
                 self.decay_down, self.beta_proj]
@@ -301,7 +306,7 @@ class SophiaKDA(nn.Module):
 
         def build(parts):
             w = torch.cat(parts, 0)
-            pad = (-int(w.size(0))) % 8
+            pad = (-int(w.size(0))) % _PROJ_ROWS
             return torch.cat([w, w.new_zeros(pad, w.size(1))], 0) if pad else w
 
         if _needs_grad(*params):   # training: the fused weight is rebuilt each call, with autograd
