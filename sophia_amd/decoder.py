@@ -315,22 +315,23 @@ class AttentionResidualMixer(nn.Module):
         return self._query_f32
 
     def forward(self, partial_block: torch.Tensor, completed_blocks: torch.Tensor,
-                out_norm: RMSNorm | None = None, *, residual: torch.Tensor | None = None):
+                out_norm: RMSNorm | None = None, *, residual: torch.Tensor | None = None,
+                partial_out: torch.Tensor | None = None):
         """The mix; with ``out_norm``, ``out_norm(mix)`` from the same kernel.
         With ``residual``, the partial block is partial_block + residual (added
-        in the same kernel) and ``(partial_block + residual, mix)`` is returned."""
+        in the same kernel) and ``(partial_block + residual, mix)`` is returned,
+        the sum written into ``partial_out`` when given."""
         return ops.attn_res_mix(
             partial_block, completed_blocks, self.norm.weight, self._query(), self.norm.eps,
             out_norm_weight=None if out_norm is None else out_norm.weight,
-            out_eps=1e-6 if out_norm is None else out_norm.eps, residual=residual)
+            out_eps=1e-6 if out_norm is None else out_norm.eps, residual=residual,
+            partial_out=partial_out)
 
 
-def _append_block(completed: torch.Tensor, partial: torch.Tensor) -> torch.Tensor:
-    """torch.cat((completed, partial.unsqueeze(-2)), dim=-2) (blocks.py:73-76).
-    When ``completed`` is a view of a depth store with room for one more block
-    (rows spaced at least one block apart and the storage long enough), the
-    block is written in place and the enlarged view returned, so that the
-    earlier blocks are not copied again."""
+def _store_slot(completed: torch.Tensor):
+    """(completed enlarged by one block, that block's slot) when ``completed``
+    is a view of a depth store with room for one more block (rows spaced at
+    least one block apart and the storage long enough), else (None, None)."""
     n, dim = int(completed.size(-2)), int(completed.size(-1))
     strides = completed.stride()
     sizes = list(completed.shape)
@@ -341,8 +342,19 @@ def _append_block(completed: torch.Tensor, partial: torch.Tensor) -> torch.Tenso
         if all(sz > 0 for sz in sizes) and extent * completed.element_size() <= \
                 completed.untyped_storage().nbytes():
             grown = completed.as_strided(sizes, strides, completed.storage_offset())
-            grown.select(-2, n).copy_(partial)
-            return grown
+            return grown, grown.select(-2, n)
+    return None, None
+
+
+def _append_block(completed: torch.Tensor, partial: torch.Tensor) -> torch.Tensor:
+    """torch.cat((completed, partial.unsqueeze(-2)), dim=-2) (blocks.py:73-76).
+    In a depth store with room for one more block the block is written in
+    place and the enlarged view returned, so that the earlier blocks are not
+    copied again."""
+    grown, slot = _store_slot(completed)
+    if slot is not None:
+        slot.copy_(partial)
+        return grown
     return torch.cat((completed, partial.unsqueeze(-2)), dim=-2)
 
 
@@ -377,13 +389,20 @@ class SophiaBlock(nn.Module):
         mix) to add the same way.  attn_norm(attn_residual(...)) and
         ffn_norm(ffn_residual(...)) each run as one kernel: the mixes feed
         nothing but these norms."""
+        boundary = self.layer_idx % self.attn_res_block_size == 0
+        grown = slot = None
+        if boundary and pending is not None:
+            # the sum partial + pending completes a depth block: the mix
+            # writes it straight into the store's next slot
+            grown, slot = _store_slot(completed_blocks)
         if pending is None:
             attn_input = self.attn_residual(partial_block, completed_blocks, self.attn_norm)
         else:
             partial_block, attn_input = self.attn_residual(partial_block, completed_blocks,
-                                                           self.attn_norm, residual=pending)
-        if self.layer_idx % self.attn_res_block_size == 0:
-            completed_blocks = _append_block(completed_blocks, partial_block)
+                                                           self.attn_norm, residual=pending,
+                                                           partial_out=slot)
+        if boundary:
+            completed_blocks = grown if slot is not None else _append_block(completed_blocks, partial_block)
             partial_block = attn(attn_input)
             ffn_input = self.ffn_residual(partial_block, completed_blocks, self.ffn_norm)
         else:

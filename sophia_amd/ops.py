@@ -817,7 +817,7 @@ def attn_res_mix(partial: torch.Tensor, completed: torch.Tensor, norm_weight: to
                  query_weight: torch.Tensor, eps: float, *,
                  out_norm_weight: torch.Tensor | None = None, out_eps: float = 1e-6,
                  residual: torch.Tensor | None = None,
-                 out: torch.Tensor | None = None):
+                 out: torch.Tensor | None = None, partial_out: torch.Tensor | None = None):
     """AttentionResidualMixer.forward (ml/runtime/model/blocks.py:38-48) in one
     kernel: softmax over the depth axis of [completed blocks..., partial] with
     scores RMSNorm(value) . query, then the weighted sum of the values; with
@@ -834,7 +834,9 @@ def attn_res_mix(partial: torch.Tensor, completed: torch.Tensor, norm_weight: to
     ``residual`` ([..., D], same dtype): the partial block is first replaced
     by partial + residual (the residual add of SophiaBlock, blocks.py:78-86,
     rounded to the activation dtype as there); the call then returns
-    ``(partial + residual, mix)``.
+    ``(partial + residual, mix)``, the sum written into ``partial_out`` when
+    given ([..., D] of partial's dtype; rows may be strided, e.g. the next
+    slot of a depth store).
     """
     _gpu(partial, "partial")
     _gpu(completed, "completed")
@@ -884,14 +886,24 @@ def attn_res_mix(partial: torch.Tensor, completed: torch.Tensor, norm_weight: to
         r2 = residual.reshape(-1, dim)
         rs = _rows(r2, "residual", dim)
         _aligned(r2, "residual")
-        po = torch.empty((rows, dim), dtype=partial.dtype, device=partial.device)
+        if partial_out is None:
+            po = torch.empty((rows, dim), dtype=partial.dtype, device=partial.device)
+        else:
+            _gpu(partial_out, "partial_out")
+            if partial_out.dtype != partial.dtype or tuple(partial_out.shape) != tuple(partial.shape):
+                raise RuntimeError("partial_out must match partial's shape and dtype")
+            po = partial_out.view(rows, dim)
+            _aligned(po, "partial_out")
+    elif partial_out is not None:
+        raise RuntimeError("partial_out holds partial + residual: it needs a residual")
+    pos_ = _rows(po, "partial_out", dim) if po is not None else dim
     rc = nat.lib().sophia_attn_res_mix(
-        nat.ptr(p2), ps, nat.ptr(r2), rs, nat.ptr(po), dim, nat.ptr(c3) if n_blocks else None, c_row,
+        nat.ptr(p2), ps, nat.ptr(r2), rs, nat.ptr(po), pos_, nat.ptr(c3) if n_blocks else None, c_row,
         c_blk, n_blocks, nat.ptr(w), nat.ptr(q), float(eps), nat.ptr(wo), float(out_eps),
         nat.ptr(y2), dim, rows, dim, nat.dtype_code(partial.dtype), nat.stream_handle(partial.device))
     nat.check(rc, "sophia_attn_res_mix")
     if po is not None:
-        return po.view(*lead, dim), y2.view(*lead, dim)
+        return (partial_out if partial_out is not None else po.view(*lead, dim)), y2.view(*lead, dim)
     return y2.view(*lead, dim)
 
 

@@ -455,3 +455,35 @@ def test_attn_res_mix_with_residual_add(dtype, rows, n_blocks, dim):
     summed = partial + residual
     assert torch.equal(new_partial, summed)
     _check(y, _mix_ref(summed, completed, w, q, 1e-5, wo, 1e-5), dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_attn_res_mix_writes_the_sum_into_a_depth_store_slot(dtype):
+    """partial_out: the sum partial + residual written into the next slot of a
+    depth store (strided rows) while the mix reads the store's earlier
+    blocks: the slot holds the same bits as the default call's new partial
+    block, the mix is bitwise the same, and the store's other slots are
+    untouched."""
+    from sophia_amd import ops
+    dev = _dev()
+    rows, n_blocks, n_max, dim = 300, 3, 5, 1536
+    g = torch.Generator(device="cpu").manual_seed(91)
+    partial = torch.randn(rows, dim, generator=g).to(dev, dtype)
+    residual = (torch.randn(rows, dim, generator=g) * 0.5).to(dev, dtype)
+    store = (torch.randn(rows, n_max, dim, generator=g) * 2).to(dev, dtype)
+    before = store.clone()
+    w = (1 + 0.2 * torch.randn(dim, generator=g)).to(dev)
+    q = (torch.randn(dim, generator=g) * 3 / dim ** 0.5).to(dev)
+    completed = store[:, :n_blocks]
+    want_partial, want_y = ops.attn_res_mix(partial, completed, w, q, 1e-5, residual=residual)
+    slot = store[:, n_blocks]
+    got_partial, got_y = ops.attn_res_mix(partial, completed, w, q, 1e-5, residual=residual, partial_out=slot)
+    torch.cuda.synchronize()
+    assert got_partial.data_ptr() == slot.data_ptr()
+    assert torch.equal(store[:, n_blocks], want_partial)
+    assert torch.equal(got_y, want_y)
+    for b in range(n_max):
+        if b != n_blocks:
+            assert torch.equal(store[:, b], before[:, b]), b
+    with pytest.raises(RuntimeError, match="residual"):
+        ops.attn_res_mix(partial, completed, w, q, 1e-5, partial_out=slot)
