@@ -82,6 +82,31 @@ int sophia_gated_head_norm(const void *o, int64_t o_stride, int o_dtype, const v
                            int heads, int head_dim, int dtype, void *stream);
 
 /*
+ * The normalisations after MLA's down projections (ml/runtime/model/
+ * attention.py:611-614: q_norm(q_down(x)) and kv_norm(kv_down(x))) in place,
+ * and each normalised latent row written into its latent-cache slot (the
+ * cache write of attention.py:615-621, as the packed step places rows):
+ *   q_lat  : [rows, q_rank], row stride q_stride; q_lat <- RMSNorm(q_lat; q_norm_weight, q_eps)
+ *   kv_lat : [rows, kv_rank], row stride kv_stride; kv_lat <- RMSNorm(kv_lat; kv_norm_weight, kv_eps)
+ *   dtype of both; the fp32 norm weights are rounded to it first, each output
+ *   rounded once.  q_rank, kv_rank multiples of 8, q_rank + kv_rank <= 512.
+ *   latent_cache : [n_slots, max_len, kv_rank] fp32, or NULL (no cache write).
+ *     Prefill rows [0, n_prefill_rows): row i goes to
+ *     (prefill_seq_slots[i / prefill_seq_len], i % prefill_seq_len) when
+ *     prefill_seq_slots is given (equal-length prompts from position 0), else
+ *     to (prefill_row_slots[i], prefill_row_pos[i]); decode row
+ *     n_prefill_rows + j goes to (decode_slots[j], decode_pos[j]).  A slot or
+ *     position out of range writes nothing.
+ * Strides multiples of 8; pointers 16-byte aligned.
+ */
+int sophia_mla_latent_norms(void *q_lat, int64_t q_stride, void *kv_lat, int64_t kv_stride, int64_t rows,
+                            int q_rank, int kv_rank, int dtype, const float *q_norm_weight, float q_eps,
+                            const float *kv_norm_weight, float kv_eps, float *latent_cache, int n_slots,
+                            int max_len, int64_t n_prefill_rows, const int32_t *prefill_seq_slots,
+                            int prefill_seq_len, const int64_t *prefill_row_slots, const int64_t *prefill_row_pos,
+                            const int32_t *decode_slots, const int64_t *decode_pos, void *stream);
+
+/*
  * Backward of sophia_gated_head_norm (training): autograd through
  * output_norm(o) * sigmoid(output_gate(x)) (attention.py:411-420) and MLA's
  * o * sigmoid(gate) (attention.py:655-656).  d_out: [rows, heads * head_dim]

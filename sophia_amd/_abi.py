@@ -60,6 +60,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "sophia_kda_conv_chunk_fwd": (_i32, [_vp, _vp, _vp, _i64, _i32, _vp, _vp, _i32, _i32, _vp, _i64, _i32,
                                          _vp, _i64, _i32, _vp, _vp, _f32, _f32, _u32, _vp, _vp, _i32,
                                          _i64, _i32, _i32, _vp, _vp, _i32, _vp, _vp, _i64, _vp, _sz, _vp]),
+    "sophia_mla_latent_norms": (_i32, [_vp, _i64, _vp, _i64, _i64, _i32, _i32, _i32, _vp, _f32, _vp, _f32,
+                                       _vp, _i32, _i32, _i64, _vp, _i32, _vp, _vp, _vp, _vp, _vp]),
     "sophia_kda_chunk_bwd_workspace_size": (_sz, [_i64, _i32, _i32, _i32]),
     "sophia_kda_chunk_bwd": (_i32, [_vp, _vp, _vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64, _i32,
                                     _vp, _vp, _f32, _f32, _u32, _vp, _i32, _i64, _i32, _i32,

@@ -950,6 +950,83 @@ __global__ __launch_bounds__(256, 2) void causal_attn_kernel(FaArgs a) {
   }
 }
 
+// ---- MLA latent norms -----------------------------------------------------------
+// The normalisations that follow MLA's down projections (attention.py:611-614):
+// q_norm over the q_down output and kv_norm over the kv_down output, in place,
+// and the normalised latent written into its latent-cache slot as fp32 (the
+// value rounded to the activation dtype first, as latent.to(cache.dtype)
+// converts it).  One wavefront per row: lanes [0, q_rank / 8) hold 8 elements
+// of q each, the next kv_rank / 8 lanes 8 of the latent.  The norm weights are
+// fp32 and rounded to the activation dtype, as RMSNorm.forward casts them.
+struct MlaNormArgs {
+  void *q;
+  int64_t q_stride;
+  void *kv;
+  int64_t kv_stride;
+  int q_rank, kv_rank, rows;
+  const float *q_w, *kv_w;
+  float q_eps, kv_eps;
+  float *cache;                   // [n_slots][max_len][kv_rank] fp32, or NULL
+  int n_slots, max_len;
+  int n_prefill;                  // rows [0, n_prefill) are prefill rows
+  const int32_t *seq_slot;        // rectangular prefill: row i -> (seq_slot[i / seq_len], i % seq_len)
+  int seq_len;
+  const int64_t *row_slot, *row_pos;             // else: (row_slot[i], row_pos[i])
+  const int32_t *dec_slot;                       // decode row n_prefill + j -> (dec_slot[j], dec_pos[j])
+  const int64_t *dec_pos;
+};
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void mla_latent_norm_kernel(MlaNormArgs a) {
+  constexpr int kDt = BF16 ? SOPHIA_DTYPE_BF16 : SOPHIA_DTYPE_F32;
+  constexpr int kEsz = BF16 ? 2 : 4;
+  const int row = static_cast<int>(blockIdx.x) * 4 + static_cast<int>(threadIdx.x >> 6);
+  if (row >= a.rows) return;  // uniform over the wavefront
+  const int l = threadIdx.x & 63;
+  const int qc = a.q_rank / 8, kc = a.kv_rank / 8;
+  const bool isq = l < qc, iskv = l >= qc && l < qc + kc;
+  const int c = isq ? l : l - qc;  // 8-element chunk within its part
+  uint8_t *base = isq ? static_cast<uint8_t *>(a.q) + static_cast<int64_t>(row) * a.q_stride * kEsz
+                      : static_cast<uint8_t *>(a.kv) + static_cast<int64_t>(row) * a.kv_stride * kEsz;
+  float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (isq || iskv) load8(base, 8 * c, kDt, v);
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss = fmaf(v[i], v[i], ss);
+  float sq = isq ? ss : 0.f, sk = iskv ? ss : 0.f;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    sq += __shfl_xor(sq, off, 64);
+    sk += __shfl_xor(sk, off, 64);
+  }
+  if (!(isq || iskv)) return;
+  const float r = isq ? rsqrtf(sq / static_cast<float>(a.q_rank) + a.q_eps)
+                      : rsqrtf(sk / static_cast<float>(a.kv_rank) + a.kv_eps);
+  const float *w = (isq ? a.q_w : a.kv_w) + 8 * c;
+  float o[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = as_dtype(v[i] * r * as_dtype(w[i], kDt), kDt);
+  store8(base, 8 * c, kDt, o);
+  if (!iskv || !a.cache) return;
+  int64_t slot, pos;
+  if (row < a.n_prefill) {
+    if (a.seq_slot) {
+      slot = a.seq_slot[row / a.seq_len];
+      pos = row % a.seq_len;
+    } else {
+      slot = a.row_slot[row];
+      pos = a.row_pos[row];
+    }
+  } else {
+    slot = a.dec_slot[row - a.n_prefill];
+    pos = a.dec_pos[row - a.n_prefill];
+  }
+  if (slot < 0 || slot >= a.n_slots || pos < 0 || pos >= a.max_len) return;
+  f4 *dst = reinterpret_cast<f4 *>(a.cache + (slot * a.max_len + pos) * a.kv_rank + 8 * c);
+  dst[0] = f4{o[0], o[1], o[2], o[3]};
+  dst[1] = f4{o[4], o[5], o[6], o[7]};
+}
+
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 }  // namespace
@@ -1077,6 +1154,45 @@ extern "C" int sophia_gated_head_norm(const void *o, int64_t o_stride, int o_dty
   hipLaunchKernelGGL(gated_head_norm_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), a);
   return check_launch("gated_head_norm");
+}
+
+extern "C" int sophia_mla_latent_norms(void *q_lat, int64_t q_stride, void *kv_lat, int64_t kv_stride, int64_t rows,
+                                       int q_rank, int kv_rank, int dtype, const float *q_norm_weight, float q_eps,
+                                       const float *kv_norm_weight, float kv_eps, float *latent_cache, int n_slots,
+                                       int max_len, int64_t n_prefill_rows, const int32_t *prefill_seq_slots,
+                                       int prefill_seq_len, const int64_t *prefill_row_slots,
+                                       const int64_t *prefill_row_pos, const int32_t *decode_slots,
+                                       const int64_t *decode_pos, void *stream) {
+  SOPHIA_REQUIRE(dtype == SOPHIA_DTYPE_F32 || dtype == SOPHIA_DTYPE_BF16, "mla_latent_norms: dtype not supported");
+  SOPHIA_REQUIRE(q_rank > 0 && kv_rank > 0 && q_rank % 8 == 0 && kv_rank % 8 == 0 && q_rank + kv_rank <= 512,
+                 "mla_latent_norms: ranks must be positive multiples of 8 with q_rank + kv_rank <= 512");
+  SOPHIA_REQUIRE(rows >= 0 && rows <= 0x7fffffff && n_prefill_rows >= 0 && n_prefill_rows <= rows,
+                 "mla_latent_norms: bad rows / n_prefill_rows");
+  SOPHIA_REQUIRE(q_stride % 8 == 0 && kv_stride % 8 == 0 && q_stride >= q_rank && kv_stride >= kv_rank,
+                 "mla_latent_norms: strides must be multiples of 8 elements and cover a row");
+  SOPHIA_REQUIRE(rows == 0 || (q_lat && kv_lat && q_norm_weight && kv_norm_weight),
+                 "mla_latent_norms: NULL pointer");
+  SOPHIA_REQUIRE(aligned16(q_lat) && aligned16(kv_lat) && aligned16(q_norm_weight) && aligned16(kv_norm_weight) &&
+                     aligned16(latent_cache),
+                 "mla_latent_norms: pointers must be 16-byte aligned");
+  if (latent_cache) {
+    SOPHIA_REQUIRE(n_slots >= 0 && max_len >= 0, "mla_latent_norms: bad cache shape");
+    SOPHIA_REQUIRE(n_prefill_rows == 0 || (prefill_seq_slots ? prefill_seq_len > 0
+                                                              : (prefill_row_slots && prefill_row_pos)),
+                   "mla_latent_norms: prefill rows need their slots and positions");
+    SOPHIA_REQUIRE(n_prefill_rows == rows || (decode_slots && decode_pos),
+                   "mla_latent_norms: decode rows need their slots and positions");
+  }
+  if (rows == 0) return SOPHIA_OK;
+  MlaNormArgs a{q_lat, q_stride, kv_lat, kv_stride, q_rank, kv_rank, static_cast<int>(rows), q_norm_weight,
+                kv_norm_weight, q_eps, kv_eps, latent_cache, n_slots, max_len, static_cast<int>(n_prefill_rows),
+                prefill_seq_slots, prefill_seq_len, prefill_row_slots, prefill_row_pos, decode_slots, decode_pos};
+  const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
+  if (dtype == SOPHIA_DTYPE_BF16)
+    hipLaunchKernelGGL(mla_latent_norm_kernel<true>, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  else
+    hipLaunchKernelGGL(mla_latent_norm_kernel<false>, grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  return check_launch("mla_latent_norms");
 }
 
 extern "C" size_t sophia_mla_decode_workspace_size(int64_t rows, int rank, int splits) {

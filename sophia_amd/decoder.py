@@ -239,20 +239,26 @@ class SophiaMLA(nn.Module):
         npre = int(step["n_prefill_rows"])
         nd = n - npre
         h, d, r = self.num_heads, self.head_dim, self.kv_rank
-        q = self.q_up(self.q_norm(self.q_down(x))).view(n, h, d)
-        latent = self.kv_norm(self.kv_down(x))
         cache = self.latent_cache
+        # q_norm, kv_norm and the latent-cache writes of every row in one kernel
+        q_lat, latent = self.q_down(x), self.kv_down(x)
+        rect = npre > 0 and bool(step["rectangular"])
+        ops.mla_latent_norms(
+            q_lat, latent, self.q_norm.weight, self.q_norm.eps, self.kv_norm.weight, self.kv_norm.eps,
+            latent_cache=cache, n_prefill=npre,
+            prefill_seq_slots=step["prefill_slots"] if rect else None,
+            prefill_seq_len=int(step["max_prefill_len"]) if rect else 0,
+            prefill_row_slots=step["row_slot"] if npre > 0 and not rect else None,
+            prefill_row_pos=step["row_pos"] if npre > 0 and not rect else None,
+            decode_slots=step["decode_slots"] if nd > 0 else None,
+            decode_pos=step["decode_pos"] if nd > 0 else None)
+        q = self.q_up(q_lat).view(n, h, d)
         out = torch.empty((n, h, d), dtype=x.dtype, device=x.device)
         if npre > 0:
             lat_p = latent[:npre]
             cu_k = cu_k_host = None
-            if step["rectangular"]:
-                P, T = int(step["n_prefill_seqs"]), int(step["max_prefill_len"])
-                cache[step["prefill_slots"].long(), :T] = lat_p.view(P, T, r).to(cache.dtype)
-                lat_k = lat_p
-            else:
-                cache[step["row_slot"], step["row_pos"]] = lat_p.to(cache.dtype)
-                lat_k = lat_p
+            lat_k = lat_p
+            if not rect:
                 if step["reads_cache"]:
                     lat_k = cache[step["key_slot"], step["key_pos"]].to(x.dtype)
                     cu_k, cu_k_host = step["cu_keys"], step["cu_keys_host"]
@@ -261,8 +267,6 @@ class SophiaMLA(nn.Module):
             self._causal(q[:npre], k, v, step["cu_prefill"], int(step["max_prefill_len"]), out[:npre],
                          cu_k=cu_k, cu_host=step["cu_prefill_host"], cu_k_host=cu_k_host)
         if nd > 0:
-            slots = step["decode_slots"].long()
-            cache[slots, step["decode_pos"]] = latent[npre:].to(cache.dtype)
             w_k = self.k_up.weight.view(h, d, r).to(x.dtype)
             w_v = self.v_up.weight.view(h, d, r).to(x.dtype)
             qa = torch.bmm(q[npre:].transpose(0, 1).contiguous(), w_k).transpose(0, 1)   # [D, h, r]

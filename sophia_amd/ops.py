@@ -939,6 +939,73 @@ def situ_glu(gate_up: torch.Tensor, gate_softcap: float, up_softcap: float, *,
     return y2.view(*lead, hidden)
 
 
+def mla_latent_norms(q_lat: torch.Tensor, kv_lat: torch.Tensor, q_norm_weight: torch.Tensor,
+                     q_eps: float, kv_norm_weight: torch.Tensor, kv_eps: float, *,
+                     latent_cache: torch.Tensor | None = None, n_prefill: int = 0,
+                     prefill_seq_slots: torch.Tensor | None = None, prefill_seq_len: int = 0,
+                     prefill_row_slots: torch.Tensor | None = None,
+                     prefill_row_pos: torch.Tensor | None = None,
+                     decode_slots: torch.Tensor | None = None,
+                     decode_pos: torch.Tensor | None = None) -> None:
+    """MLA's q_norm(q_down(x)) and kv_norm(kv_down(x)) in place (attention.py:
+    611-614), and each normalised latent row written into ``latent_cache``
+    ([slots, max_len, kv_rank] fp32) at its slot and position (attention.py:
+    615-621): prefill rows [0, n_prefill) at (prefill_seq_slots[i //
+    prefill_seq_len], i % prefill_seq_len) for equal-length prompts from
+    position 0, else at (prefill_row_slots[i], prefill_row_pos[i]); the
+    remaining rows at (decode_slots[j], decode_pos[j]).  q_lat [rows, q_rank]
+    and kv_lat [rows, kv_rank] (dense rows, one dtype); the fp32 weights are
+    rounded to that dtype as RMSNorm.forward casts them."""
+    _gpu(q_lat, "q_lat")
+    _gpu(kv_lat, "kv_lat")
+    device = q_lat.device
+    rows, q_rank = int(q_lat.size(0)), int(q_lat.size(1))
+    kv_rank = int(kv_lat.size(1))
+    if q_lat.dim() != 2 or kv_lat.dim() != 2 or int(kv_lat.size(0)) != rows or q_lat.dtype != kv_lat.dtype:
+        raise RuntimeError("q_lat and kv_lat must be [rows, rank] of one dtype")
+    qs = _rows(q_lat, "q_lat", q_rank)
+    ks = _rows(kv_lat, "kv_lat", kv_rank)
+
+    def f32(t, n, name):
+        t = t.detach().reshape(-1).to(device=device, dtype=torch.float32).contiguous()
+        if int(t.numel()) != n:
+            raise RuntimeError(f"{name} must hold {n} values")
+        return t
+
+    qw = f32(q_norm_weight, q_rank, "q_norm_weight")
+    kw = f32(kv_norm_weight, kv_rank, "kv_norm_weight")
+    n_prefill = int(n_prefill)
+    n_slots = max_len = 0
+    if latent_cache is not None:
+        _gpu(latent_cache, "latent_cache")
+        if (latent_cache.dtype != torch.float32 or latent_cache.dim() != 3 or not latent_cache.is_contiguous()
+                or int(latent_cache.size(2)) != kv_rank):
+            raise RuntimeError(f"latent_cache must be contiguous fp32 [slots, max_len, {kv_rank}]")
+        n_slots, max_len = int(latent_cache.size(0)), int(latent_cache.size(1))
+
+    def idx(t, dtype, name, n):
+        if t is None:
+            return None
+        _gpu(t, name)
+        t = t.reshape(-1).to(dtype).contiguous()   # no copy when already so
+        if int(t.numel()) < n:
+            raise RuntimeError(f"{name} must hold at least {n} entries")
+        return t
+
+    seq_slots = idx(prefill_seq_slots, torch.int32, "prefill_seq_slots",
+                    -(-n_prefill // max(int(prefill_seq_len), 1)) if prefill_seq_slots is not None else 0)
+    row_slots = idx(prefill_row_slots, torch.int64, "prefill_row_slots", n_prefill)
+    row_pos = idx(prefill_row_pos, torch.int64, "prefill_row_pos", n_prefill)
+    dslots = idx(decode_slots, torch.int32, "decode_slots", rows - n_prefill)
+    dpos = idx(decode_pos, torch.int64, "decode_pos", rows - n_prefill)
+    rc = nat.lib().sophia_mla_latent_norms(
+        nat.ptr(q_lat), qs, nat.ptr(kv_lat), ks, rows, q_rank, kv_rank, nat.dtype_code(q_lat.dtype),
+        nat.ptr(qw), float(q_eps), nat.ptr(kw), float(kv_eps), nat.ptr(latent_cache), n_slots, max_len,
+        n_prefill, nat.ptr(seq_slots), int(prefill_seq_len), nat.ptr(row_slots), nat.ptr(row_pos),
+        nat.ptr(dslots), nat.ptr(dpos), nat.stream_handle(device))
+    nat.check(rc, "sophia_mla_latent_norms")
+
+
 def gated_head_norm(o: torch.Tensor, gate: torch.Tensor, heads: int, head_dim: int, *,
                     norm_weight: torch.Tensor | None = None, eps: float = 1e-6,
                     out: torch.Tensor | None = None) -> torch.Tensor:

@@ -487,3 +487,55 @@ def test_attn_res_mix_writes_the_sum_into_a_depth_store_slot(dtype):
             assert torch.equal(store[:, b], before[:, b]), b
     with pytest.raises(RuntimeError, match="residual"):
         ops.attn_res_mix(partial, completed, w, q, 1e-5, partial_out=slot)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("mode", ["rectangular", "ragged"])
+def test_mla_latent_norms_and_cache_rows(dtype, mode):
+    """sophia_mla_latent_norms: q_norm and kv_norm in place against torch's
+    rms_norm with the weight cast to the activation dtype (RMSNorm.forward),
+    within one rounding of that dtype; every latent row lands in its cache
+    slot and position exactly as the kernel's own output (fp32 of the rounded
+    value), slots or positions out of range write nothing, and every other
+    cache entry is untouched.  Prefill rows mapped per sequence (equal-length
+    prompts) or per row, then decode rows."""
+    from sophia_amd import ops
+    dev = _dev()
+    g = torch.Generator(device="cpu").manual_seed(7 if mode == "rectangular" else 8)
+    q_rank, kv_rank, n_slots, max_len, eps = 384, 128, 6, 12, 1e-6
+    if mode == "rectangular":
+        P, T = 3, 5
+        n_pre = P * T
+        seq_slots = torch.tensor([4, 0, 2], dtype=torch.int32, device=dev)
+        want_pre = [(int(seq_slots[i // T]), i % T) for i in range(n_pre)]
+        kw = dict(prefill_seq_slots=seq_slots, prefill_seq_len=T)
+    else:
+        want_pre = [(1, 3), (1, 4), (5, 0), (3, 11), (7, 2), (2, 12)]   # the last two: slot / position out of range
+        n_pre = len(want_pre)
+        kw = dict(prefill_row_slots=torch.tensor([s for s, _ in want_pre], device=dev),
+                  prefill_row_pos=torch.tensor([p for _, p in want_pre], device=dev))
+    want_dec = [(0, 7), (3, 0), (5, 11), (-1, 3)]                        # the last: out of range
+    rows = n_pre + len(want_dec)
+    q_lat = (torch.randn(rows, q_rank, generator=g) * 2).to(dev, dtype)
+    kv_lat = (torch.randn(rows, kv_rank, generator=g) * 0.5).to(dev, dtype)
+    qw = (1 + 0.3 * torch.randn(q_rank, generator=g)).to(dev)
+    kvw = (1 + 0.3 * torch.randn(kv_rank, generator=g)).to(dev)
+    cache = torch.randn(n_slots, max_len, kv_rank, generator=g).to(dev)
+    before = cache.clone()
+    want_q = torch.nn.functional.rms_norm(q_lat, (q_rank,), qw.to(dtype), eps)
+    want_kv = torch.nn.functional.rms_norm(kv_lat, (kv_rank,), kvw.to(dtype), eps)
+    ops.mla_latent_norms(q_lat, kv_lat, qw, eps, kvw, eps, latent_cache=cache, n_prefill=n_pre,
+                         decode_slots=torch.tensor([s for s, _ in want_dec], dtype=torch.int32, device=dev),
+                         decode_pos=torch.tensor([p for _, p in want_dec], device=dev), **kw)
+    torch.cuda.synchronize()
+    rtol = 2.0 ** -7 if dtype == torch.bfloat16 else 2e-6
+    for got, want, name in ((q_lat, want_q, "q"), (kv_lat, want_kv, "kv")):
+        err = float(((got.float() - want.float()).abs() / (want.float().abs() + 1e-6)).max())
+        print(f"{name}_norm {dtype}: max rel diff to torch {err:.2e}", flush=True)
+        assert err <= rtol, (name, err)
+    written = torch.zeros(n_slots, max_len, dtype=torch.bool, device=dev)
+    for i, (s, p) in enumerate(want_pre + want_dec):
+        if 0 <= s < n_slots and 0 <= p < max_len:
+            assert torch.equal(cache[s, p], kv_lat[i].float()), (i, s, p)
+            written[s, p] = True
+    assert torch.equal(cache[~written], before[~written])
