@@ -32,4 +32,4 @@ int check_launch(const char *what) {
 
 extern "C" const char *sophia_last_error(void) { return g_last_error; }
 
-extern "C" int sophia_abi_version(void) { return 106; }
+extern "C" int sophia_abi_version(void) { return 107; }
