@@ -61,6 +61,22 @@ class SophiaMLA(nn.Module):
         self.o_proj = RuntimeLinear(self.inner_dim, self.dim)
         self.register_buffer("latent_cache", torch.zeros(
             int(args.max_batch_size), int(args.max_seq_len), self.kv_rank), persistent=False)
+        self._v_t = None
+        self._v_t_key = None
+
+    def _v_up_t(self, dtype: torch.dtype) -> torch.Tensor:
+        """v_up's weight as [heads, kv_rank, head_dim] (the per-head blocks
+        transposed, as the decode rows' value product takes them), kept until
+        the weight changes so that no copy runs per step."""
+        w = self.v_up.weight
+        h, d, r = self.num_heads, self.head_dim, self.kv_rank
+        if torch.is_grad_enabled() and w.requires_grad:
+            return w.view(h, d, r).to(dtype).transpose(1, 2).contiguous()
+        key = (w.data_ptr(), w._version, w.dtype, dtype)
+        if self._v_t_key != key:
+            self._v_t = w.detach().view(h, d, r).to(dtype).transpose(1, 2).contiguous()
+            self._v_t_key = key
+        return self._v_t
 
     # ------------------------------------------------------------- caches
     def ensure_batch_capacity(self, batch_size: int) -> None:
@@ -268,12 +284,11 @@ class SophiaMLA(nn.Module):
                          cu_k=cu_k, cu_host=step["cu_prefill_host"], cu_k_host=cu_k_host)
         if nd > 0:
             w_k = self.k_up.weight.view(h, d, r).to(x.dtype)
-            w_v = self.v_up.weight.view(h, d, r).to(x.dtype)
             qa = torch.bmm(q[npre:].transpose(0, 1).contiguous(), w_k).transpose(0, 1)   # [D, h, r]
             # softmax over cached latents 0..pos and their weighted sum, one kernel
             ctx = ops.mla_decode_attn(qa.contiguous(), cache, step["decode_slots"], step["decode_pos"],
                                       d ** -0.5, max_len=int(step["max_decode_len"]))   # [D, h, r]
-            o = torch.bmm(ctx.transpose(0, 1).contiguous(), w_v.transpose(1, 2).contiguous())
+            o = torch.bmm(ctx.transpose(0, 1).contiguous(), self._v_up_t(x.dtype))
             out[npre:] = o.transpose(0, 1)
         return self._gate_out(x, out)
 
