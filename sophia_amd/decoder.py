@@ -63,6 +63,22 @@ class SophiaMLA(nn.Module):
             int(args.max_batch_size), int(args.max_seq_len), self.kv_rank), persistent=False)
         self._v_t = None
         self._v_t_key = None
+        self._in_w = None
+        self._in_w_key = None
+
+    def _input_weight(self, dtype: torch.dtype) -> torch.Tensor:
+        """q_down, kv_down and output_gate stacked [q_rank + kv_rank + inner,
+        dim]: the three projections of x in one GEMM (the packed step), kept
+        until a weight changes."""
+        params = (self.q_down.weight, self.kv_down.weight, self.output_gate.weight)
+        if torch.is_grad_enabled() and any(p.requires_grad for p in params):
+            return torch.cat(params, 0).to(dtype)
+        key = tuple((p.data_ptr(), p._version, p.dtype) for p in params) + (dtype,)
+        if self._in_w_key != key:
+            with torch.no_grad():
+                self._in_w = torch.cat([p.detach() for p in params], 0).to(dtype).contiguous()
+            self._in_w_key = key
+        return self._in_w
 
     def _v_up_t(self, dtype: torch.dtype) -> torch.Tensor:
         """v_up's weight as [heads, kv_rank, head_dim] (the per-head blocks
@@ -137,10 +153,12 @@ class SophiaMLA(nn.Module):
             snapshot.latent.to(self.latent_cache.device, dtype=self.latent_cache.dtype))
 
     # ------------------------------------------------------------- forward
-    def _gate_out(self, x: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    def _gate_out(self, x: torch.Tensor, out: torch.Tensor, gate: torch.Tensor | None = None) -> torch.Tensor:
         """attention.py:655-657: o_proj((o.float() * sigmoid(gate).float()).to(dtype)),
-        the gate as one HIP kernel (ops.gated_head_norm without a norm)."""
-        gate = self.output_gate(x)
+        the gate as one HIP kernel (ops.gated_head_norm without a norm);
+        ``gate``: output_gate(x) when already projected."""
+        if gate is None:
+            gate = self.output_gate(x)
         gated = ops.gated_head_norm(out.to(x.dtype), gate, self.num_heads, self.head_dim)
         return self.o_proj(gated.view(*x.shape[:-1], self.inner_dim))
 
@@ -256,8 +274,10 @@ class SophiaMLA(nn.Module):
         nd = n - npre
         h, d, r = self.num_heads, self.head_dim, self.kv_rank
         cache = self.latent_cache
-        # q_norm, kv_norm and the latent-cache writes of every row in one kernel
-        q_lat, latent = self.q_down(x), self.kv_down(x)
+        # q_down, kv_down and output_gate in one GEMM; q_norm, kv_norm and the
+        # latent-cache writes of every row in one kernel
+        y = F.linear(x, self._input_weight(x.dtype))
+        q_lat, latent, gate = y[:, :self.q_rank], y[:, self.q_rank:self.q_rank + r], y[:, self.q_rank + r:]
         rect = npre > 0 and bool(step["rectangular"])
         ops.mla_latent_norms(
             q_lat, latent, self.q_norm.weight, self.q_norm.eps, self.kv_norm.weight, self.kv_norm.eps,
@@ -290,7 +310,7 @@ class SophiaMLA(nn.Module):
                                       d ** -0.5, max_len=int(step["max_decode_len"]))   # [D, h, r]
             o = torch.bmm(ctx.transpose(0, 1).contiguous(), self._v_up_t(x.dtype))
             out[npre:] = o.transpose(0, 1)
-        return self._gate_out(x, out)
+        return self._gate_out(x, out, gate)
 
 
 class FeedForward(nn.Module):
