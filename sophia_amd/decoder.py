@@ -279,15 +279,30 @@ class SophiaMLA(nn.Module):
         y = F.linear(x, self._input_weight(x.dtype))
         q_lat, latent, gate = y[:, :self.q_rank], y[:, self.q_rank:self.q_rank + r], y[:, self.q_rank + r:]
         rect = npre > 0 and bool(step["rectangular"])
-        ops.mla_latent_norms(
-            q_lat, latent, self.q_norm.weight, self.q_norm.eps, self.kv_norm.weight, self.kv_norm.eps,
-            latent_cache=cache, n_prefill=npre,
-            prefill_seq_slots=step["prefill_slots"] if rect else None,
-            prefill_seq_len=int(step["max_prefill_len"]) if rect else 0,
-            prefill_row_slots=step["row_slot"] if npre > 0 and not rect else None,
-            prefill_row_pos=step["row_pos"] if npre > 0 and not rect else None,
-            decode_slots=step["decode_slots"] if nd > 0 else None,
-            decode_pos=step["decode_pos"] if nd > 0 else None)
+        if (self.q_rank % 8 == 0 and r % 8 == 0 and self.q_rank + r <= 512 and int(y.stride(0)) % 8 == 0
+                and x.dtype in (torch.float32, torch.bfloat16)):
+            ops.mla_latent_norms(
+                q_lat, latent, self.q_norm.weight, self.q_norm.eps, self.kv_norm.weight, self.kv_norm.eps,
+                latent_cache=cache, n_prefill=npre,
+                prefill_seq_slots=step["prefill_slots"] if rect else None,
+                prefill_seq_len=int(step["max_prefill_len"]) if rect else 0,
+                prefill_row_slots=step["row_slot"] if npre > 0 and not rect else None,
+                prefill_row_pos=step["row_pos"] if npre > 0 and not rect else None,
+                decode_slots=step["decode_slots"] if nd > 0 else None,
+                decode_pos=step["decode_pos"] if nd > 0 else None)
+        else:
+            # ranks the kernel does not take: the norms and cache writes as torch
+            # ops, and the gate copied to dense rows (its columns may start off a
+            # 16-byte boundary, which the gate kernel requires)
+            q_lat, latent, gate = self.q_norm(q_lat), self.kv_norm(latent), gate.contiguous()
+            if npre > 0:
+                if rect:
+                    T = int(step["max_prefill_len"])
+                    cache[step["prefill_slots"].long(), :T] = latent[:npre].view(-1, T, r).to(cache.dtype)
+                else:
+                    cache[step["row_slot"], step["row_pos"]] = latent[:npre].to(cache.dtype)
+            if nd > 0:
+                cache[step["decode_slots"].long(), step["decode_pos"]] = latent[npre:].to(cache.dtype)
         q = self.q_up(q_lat).view(n, h, d)
         out = torch.empty((n, h, d), dtype=x.dtype, device=x.device)
         if npre > 0:

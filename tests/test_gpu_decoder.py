@@ -39,11 +39,11 @@ def _np(t):
     return t.detach().float().cpu().numpy()
 
 
-def _model(dev, seed=0):
+def _model(dev, seed=0, **over):
     from sophia_amd.config import ModelArgs
     from sophia_amd.decoder import Transformer
     torch.manual_seed(seed)
-    args = ModelArgs(**SMALL)
+    args = ModelArgs(**{**SMALL, **over})
     model = Transformer(args)
     # non-zero residual queries so the depth mixing is exercised
     with torch.no_grad():
@@ -53,7 +53,8 @@ def _model(dev, seed=0):
     model = model.to(dev)
     params = {k: _np(v).astype(np.float64) for k, v in model.state_dict().items()}
     cfg = dict(n_layers=4, num_heads=2, norm_eps=1e-5, attn_res_block_size=4,
-               situ_gate_softcap=4.0, situ_up_softcap=25.0, mla_kv_rank=32, short_conv_kernel=4)
+               situ_gate_softcap=4.0, situ_up_softcap=25.0, mla_kv_rank=int(args.mla_kv_rank),
+               short_conv_kernel=4)
     return model, params, cfg
 
 
@@ -123,6 +124,24 @@ def test_mixed_step_matches_each_sequence_run_alone():
     for row, seq in enumerate(full):
         ref = do.decoder_forward(params, seq.numpy()[None], cfg=cfg)[0, -1]
         err = _rel(_np(logits[row]), ref)
+        assert err < REL_TOL, f"sequence {row}: {err}"
+
+
+@pytest.mark.parametrize("q_rank", [60, 544])
+def test_mixed_step_with_mla_ranks_outside_the_norm_kernel(q_rank):
+    """A q rank that is not a multiple of 8 (60), and one whose q and kv
+    latents together exceed the 512 columns one wave normalises (544 + 32):
+    the step keeps torch's norms and latent-cache writes and every sequence
+    still matches the oracle."""
+    dev = _dev()
+    model, params, cfg = _model(dev, mla_q_rank=q_rank)
+    step, full = _mixed_case(dev, model)
+    with torch.no_grad():
+        logits = model.forward_mixed(max_decode_len=40, **step)
+    for row, seq in enumerate(full):
+        ref = do.decoder_forward(params, seq.numpy()[None], cfg=cfg)[0, -1]
+        err = _rel(_np(logits[row]), ref)
+        print(f"q rank {q_rank}, sequence {row}: rel err {err:.2e}", flush=True)
         assert err < REL_TOL, f"sequence {row}: {err}"
 
 
