@@ -93,7 +93,8 @@ int sophia_gated_head_norm(const void *o, int64_t o_stride, int o_dtype, const v
  *   latent_cache : [n_slots, max_len, kv_rank] fp32, or NULL (no cache write).
  *     Prefill rows [0, n_prefill_rows): row i goes to
  *     (prefill_seq_slots[i / prefill_seq_len], i % prefill_seq_len) when
- *     prefill_seq_slots is given (equal-length prompts from position 0), else
+ *     prefill_seq_slots is given (equal-length prompts from position 0; it
+ *     holds ceil(n_prefill_rows / prefill_seq_len) entries), else
  *     to (prefill_row_slots[i], prefill_row_pos[i]); decode row
  *     n_prefill_rows + j goes to (decode_slots[j], decode_pos[j]).  A slot or
  *     position out of range writes nothing.
