@@ -125,3 +125,68 @@ def test_fused_conv_prefill_rejects_rows_it_cannot_copy_whole():
     with pytest.raises(RuntimeError, match="bf16"):
         ops.kda_conv_chunk_fwd(x[:, :3 * D].float(), taps, cs, g, beta, torch.tensor(cu, dtype=torch.int32),
                                final_state=st, **gate)
+
+
+@pytest.mark.parametrize("seed", list(range(8)))
+def test_fused_conv_prefill_random_batches(seed):
+    """Seeded random sweep: 1-12 sequences of 0-300 tokens (some empty, some of
+    1-3 tokens, whose new history mixes old history and rows; every fourth case
+    one sequence of 8,200-8,800 tokens, which the host plan cuts into segments
+    of 64 chunks), 1-4 heads, fp32 or bf16 decay logits, the three in-kernel
+    switches (l2 norm, gate, beta sigmoid), shuffled slots with one out of
+    range, histories read or not, host offsets or device offsets alone.
+    Outputs, final states and histories equal the two separate launches bit
+    for bit; slots no sequence uses keep their histories."""
+    import numpy as np
+    rng = np.random.default_rng(500 + seed)
+    n = int(rng.integers(1, 13))
+    lens = rng.integers(0, 301, size=n)
+    lens[rng.random(n) < 0.15] = 0
+    lens[rng.random(n) < 0.15] = rng.integers(1, 4)
+    if seed % 4 == 0:
+        n, lens = 1, np.array([int(rng.integers(8200, 8801))])
+    heads = int(rng.integers(1, 5))
+    g_dt = torch.bfloat16 if rng.random() < 0.5 else torch.float32
+    l2, gated, bsig = bool(rng.random() < 0.7), bool(rng.random() < 0.6), bool(rng.random() < 0.6)
+    read, host = bool(rng.random() < 0.6), seed % 3 != 2
+    n_slots = n + 3
+    slots = [int(s) for s in rng.permutation(n_slots)[:n]]
+    if n > 1:
+        slots[int(rng.integers(0, n))] = n_slots + 5        # out of range: no history, zero state
+    cu = [0] + np.cumsum(lens).tolist()
+    print(f"case {seed}: lens={lens.tolist()} heads={heads} g={g_dt} l2={l2} gate={gated} "
+          f"beta_sigmoid={bsig} read={read} host_offsets={host} slots={slots}", flush=True)
+    x, taps, cs, g, beta, st, gate, sl = _case(cu, heads, seed=seed, slots=slots, n_slots=n_slots,
+                                               g_dtype=g_dt)
+    if not gated:
+        g = -torch.rand(g.shape, device=DEV).mul(4.0).to(g_dt)   # log-decays in [-4, 0]
+        gate = {}
+    flags = dict(use_qk_l2norm=l2, use_gate=gated, use_beta_sigmoid=bsig)
+    if not l2:
+        # unnormalised keys: small pre-conv k rows keep |k|^2 well under 1, so
+        # that the delta rule's state stays bounded
+        x[:, heads * D:2 * heads * D] *= 0.05
+    if not bsig:
+        beta = torch.sigmoid(beta.float()).to(beta.dtype)
+    inner = heads * D
+    cu_d = torch.tensor(cu, dtype=torch.int32, device=DEV)
+    cu_h = torch.tensor(cu, dtype=torch.int32) if host else None
+    cs1, st1 = cs.clone(), st.clone()
+    y = torch.empty((cu[-1], 3 * inner), dtype=torch.bfloat16, device=DEV)
+    ops.short_conv_fwd(x[:, :3 * inner], taps, cu_d, conv_state=cs1, state_slots=sl, read_history=read,
+                       write_history=True, out=y, weight_rounded=True)
+    o1 = ops.kda_chunk_fwd(y[:, :inner].unflatten(1, (heads, D)), y[:, inner:2 * inner].unflatten(1, (heads, D)),
+                           y[:, 2 * inner:].unflatten(1, (heads, D)), g, beta, cu_d,
+                           initial_state=st1 if read else None, final_state=st1, state_slots=sl,
+                           cu_seqlens_cpu=cu_h, **gate, **flags)
+    cs2, st2 = cs.clone(), st.clone()
+    o2 = ops.kda_conv_chunk_fwd(x[:, :3 * inner], taps, cs2, g, beta, cu_d, read_history=read,
+                                initial_state=st2 if read else None, final_state=st2, state_slots=sl,
+                                cu_seqlens_cpu=cu_h, **gate, **flags)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o1.float()).all()
+    _assert_bitwise(o2, o1, "o")
+    _assert_bitwise(st2, st1, "final states")
+    _assert_bitwise(cs2, cs1, "conv histories")
+    for s in sorted(set(range(n_slots)) - set(slots)):
+        _assert_bitwise(cs2[s], cs[s], f"conv history of unused slot {s}")
