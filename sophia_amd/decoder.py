@@ -219,14 +219,29 @@ class SophiaMLA(nn.Module):
                          k.reshape(rows, self.num_heads, self.head_dim),
                          v.reshape(rows, self.num_heads, self.head_dim), cu, seqlen, out)
             return self._gate_out(x, out.view(bsz, seqlen, self.num_heads, self.head_dim))
-        else:
-            allow = torch.ones((seqlen, klen), dtype=torch.bool, device=x.device).tril(klen - seqlen)
-            allow = allow[None, None].expand(bsz, 1, seqlen, klen)
-            if key_pad is not None:
-                allow = allow & key_pad[:, None, None, :]
-            mask = torch.zeros((bsz, 1, seqlen, klen), dtype=q_t.dtype, device=x.device)
-            mask = mask.masked_fill(~allow, float("-inf"))
-            out = F.scaled_dot_product_attention(q_t, k_t, v_t, attn_mask=mask)
+        if key_pad is None and x.dtype == torch.bfloat16 and self.head_dim == 128:
+            # after cached keys, no padding: the HIP kernel, each row's queries
+            # being the last seqlen of its klen key positions
+            rows, h, d = bsz * seqlen, self.num_heads, self.head_dim
+            cu = torch.arange(0, rows + 1, seqlen, dtype=torch.int32, device=x.device)
+            cu_k = torch.arange(0, bsz * klen + 1, klen, dtype=torch.int32, device=x.device)
+            out = torch.empty((rows, h, d), dtype=x.dtype, device=x.device)
+            self._causal(q.reshape(rows, h, d), k.reshape(bsz * klen, h, d), v.reshape(bsz * klen, h, d), cu,
+                         seqlen, out, cu_k=cu_k)
+            return self._gate_out(x, out.view(bsz, seqlen, h, d))
+        allow = torch.ones((seqlen, klen), dtype=torch.bool, device=x.device).tril(klen - seqlen)
+        allow = allow[None, None].expand(bsz, 1, seqlen, klen)
+        if key_pad is not None:
+            allow = allow & key_pad[:, None, None, :]
+        # fp32 scores for bf16 activations too: torch's batched bf16 products
+        # on the transposed key views of the math path are avoided
+        ct = torch.float32 if x.dtype == torch.bfloat16 else q_t.dtype
+        mask = torch.zeros((bsz, 1, seqlen, klen), dtype=ct, device=x.device)
+        mask = mask.masked_fill(~allow, float("-inf"))
+        out = F.scaled_dot_product_attention(q_t.to(ct), k_t.to(ct), v_t.to(ct), attn_mask=mask)
+        # a query with no key allowed (a pad position of a left-padded prompt)
+        # gets zeros, as torch's math path gives, whichever backend ran
+        out = out.masked_fill(~allow.any(-1, keepdim=True), 0.0).to(x.dtype)
         return self._gate_out(x, out.transpose(1, 2))
 
     def _key_mask(self, start_pos: int, bsz: int, k_len: int, device):

@@ -570,10 +570,15 @@ class SophiaKDA(nn.Module):
 
 def set_pad_mask(model: nn.Module, mask: torch.Tensor | None) -> None:
     """attention.py:660-670: hang a [B, T] bool mask (True = real token) on
-    every KDA mixer, or clear it."""
+    every token mixer (KDA and, in the hybrid decoder, MLA), or clear it.
+    Clearing also forgets the prompt mask an MLA layer keeps for the keys of
+    later steps, so that an unpadded batch after a padded one sees none."""
+    from .decoder import SophiaMLA   # the decoder module imports this one
     for module in model.modules():
-        if isinstance(module, SophiaKDA):
+        if isinstance(module, (SophiaKDA, SophiaMLA)):
             module._pad_mask = mask
+            if mask is None and isinstance(module, SophiaMLA):
+                module._prompt_mask = None
 
 
 __all__ = ["CausalDepthwiseConv1d", "PAD_LOGIT", "RMSNorm", "RuntimeLinear", "SophiaKDA",

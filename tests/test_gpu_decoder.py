@@ -145,6 +145,51 @@ def test_mixed_step_with_mla_ranks_outside_the_norm_kernel(q_rank):
         assert err < REL_TOL, f"sequence {row}: {err}"
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_padded_prompt_and_cached_decode_match_the_unpadded_sequence(dtype):
+    """The whole decoder with a left-padded row (set_pad_mask on its KDA and
+    MLA layers, attention.py:660-670): the padded row's logits at its real
+    positions, and those of two cached decode steps after it, equal those of
+    the same tokens run alone without padding (KDA pad steps are identities,
+    the MLA keys of pad positions are masked, and the position-free attention
+    does not see the shift); and cached decode steps of the unpadded sequence
+    equal its one-pass logits.  bf16 runs the unpadded cached steps through the
+    HIP causal kernel (queries after cached keys) and the masked ones through
+    fp32 attention scores."""
+    from sophia_amd.kda import set_pad_mask
+    dev = _dev()
+    model, _, _ = _model(dev, seed=8)
+    if dtype == torch.bfloat16:
+        model.cast_weights_(torch.bfloat16)
+    gen = torch.Generator().manual_seed(9)
+    real, pad = 45, 7
+    seq = torch.randint(0, 512, (1, real + 2), generator=gen)
+    batch = torch.cat([torch.cat([torch.zeros(1, pad, dtype=torch.long), seq[:, :real]], 1),
+                       torch.randint(0, 512, (1, real + pad), generator=gen)], 0).to(dev)
+    mask = torch.ones(2, real + pad, dtype=torch.bool, device=dev)
+    mask[0, :pad] = False
+    nxt = torch.cat([seq[:, real:], torch.randint(0, 512, (1, 2), generator=gen)], 0).to(dev)   # [2, 2]
+    with torch.no_grad():
+        model.reset_runtime_cache()
+        set_pad_mask(model, mask)
+        padded = model(batch, start_pos=0)
+        steps = [model(nxt[:, t:t + 1], start_pos=real + pad + t) for t in range(2)]
+        set_pad_mask(model, None)
+        model.reset_runtime_cache()
+        alone = model(seq.to(dev), start_pos=0)          # all real + 2 tokens in one pass
+        model.reset_runtime_cache()
+        model(seq[:, :real].to(dev), start_pos=0)
+        cached = [model(seq[:, real + t:real + t + 1].to(dev), start_pos=real + t) for t in range(2)]
+    tol = 1e-2 if dtype == torch.float32 else 3e-2
+    err = _rel(_np(padded[0, pad:]), _np(alone[0, :real]))
+    err_steps = max(_rel(_np(steps[t][0, 0]), _np(alone[0, real + t])) for t in range(2))
+    err_cached = max(_rel(_np(cached[t][0, 0]), _np(alone[0, real + t])) for t in range(2))
+    print(f"{dtype}: padded prompt vs alone {err:.2e}, its cached steps {err_steps:.2e}, "
+          f"unpadded cached steps vs one pass {err_cached:.2e}", flush=True)
+    assert torch.isfinite(padded.float()).all()
+    assert err < tol and err_steps < tol and err_cached < tol
+
+
 def test_mixed_step_graph_replays_match_eager():
     from sophia_amd.decoder import MixedStepGraph
     dev = _dev()
