@@ -871,6 +871,9 @@ __global__ __launch_bounds__(256, 2) void causal_attn_kernel(FaArgs a) {
     __syncthreads();
     if (kb + 1 < nkb) load_block(kb + 1);
     if (k0 > wq_last) continue;  // every key of the block is after this wavefront's queries
+    // Only a block that reaches past this wavefront's first query, or past the
+    // last key, needs the causal / length mask (uniform over the wavefront).
+    const bool masked = k0 + kFaK - 1 > wq0 + off || k0 + kFaK > klen;
     // S^T tiles: st[kt][qt][i] = score(key k0 + 16 kt + 4 g + i, query wq0 + 16 qt + ln).
     f4 st[4][2];
 #pragma unroll
@@ -886,20 +889,29 @@ __global__ __launch_bounds__(256, 2) void causal_attn_kernel(FaArgs a) {
     bf8 pf[2][2];  // [kp][qt]: P^T as B operands of the value product
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
-      const int qpos = wq0 + 16 * qt + ln + off;
+      // Raw scores here; the scale (times log2 e, > 0) enters through the
+      // running max and one fused multiply-add per exponent.
       float mx = -INFINITY;
+      if (masked) {
+        const int qpos = wq0 + 16 * qt + ln + off;
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+        for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = k0 + 16 * kt + 4 * g + i;
-          const float sv = (key <= qpos && key < klen) ? st[kt][qt][i] * a.scale_log2 : -INFINITY;
-          st[kt][qt][i] = sv;
-          mx = fmaxf(mx, sv);
-        }
+          for (int i = 0; i < 4; ++i) {
+            const int key = k0 + 16 * kt + 4 * g + i;
+            const float sv = (key <= qpos && key < klen) ? st[kt][qt][i] : -INFINITY;
+            st[kt][qt][i] = sv;
+            mx = fmaxf(mx, sv);
+          }
+      } else {
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, st[kt][qt][i]);
+      }
       mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run[qt], mx);
+      const float m_new = fmaxf(m_run[qt], mx * a.scale_log2);
       // m_new is finite once key 0 has been seen, and key 0 is in the first block.
       const float alpha = __builtin_amdgcn_exp2f(m_run[qt] - m_new);
       float ps = 0.f;
@@ -907,7 +919,7 @@ __global__ __launch_bounds__(256, 2) void causal_attn_kernel(FaArgs a) {
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float pv = __builtin_amdgcn_exp2f(st[kt][qt][i] - m_new);
+          const float pv = __builtin_amdgcn_exp2f(fmaf(st[kt][qt][i], a.scale_log2, -m_new));
           st[kt][qt][i] = pv;
           ps += pv;
         }
