@@ -120,13 +120,20 @@ def _situ_ref(gu, cg=4.0, cu=25.0):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("rows,hidden", [(1, 8), (3, 24), (1000, 3968), (129, 320)])
-def test_situ_glu_matches_fp64_reference(dtype, rows, hidden):
+@pytest.mark.parametrize("u_sigma", [40.0, 0.5])
+def test_situ_glu_matches_fp64_reference(dtype, rows, hidden, u_sigma):
+    """u_sigma 40 spreads the up values over the soft cap's saturation region;
+    0.5 keeps every |u| / 25 below 1/8 (the wavefronts' series-only path for
+    the up side) except one planted value, whose wavefront takes the full
+    path."""
     from sophia_amd import ops
     dev = _dev()
     g = torch.Generator(device="cpu").manual_seed(rows + hidden)
     # spread over both soft caps' saturation regions and sigmoid's tails
-    gu = torch.randn(rows, 2 * hidden, generator=g) * torch.tensor([6.0, 40.0]).repeat_interleave(hidden)
+    gu = torch.randn(rows, 2 * hidden, generator=g) * torch.tensor([6.0, u_sigma]).repeat_interleave(hidden)
     gu[0, :4] = torch.tensor([-90.0, 90.0, 0.0, -1e-3])
+    if u_sigma < 1.0:
+        gu[rows // 2, hidden + hidden // 2] = 30.0
     gu = gu.to(dev, dtype)
     y = ops.situ_glu(gu, 4.0, 25.0)
     torch.cuda.synchronize()
