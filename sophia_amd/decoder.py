@@ -12,7 +12,8 @@ single HIP kernels (``ops.situ_glu``, ``ops.attn_res_mix``); depth blocks are
 appended in place into one store per forward.  The projections of MLA and the
 FFN run on library GEMMs and attention (hipBLASLt / SDPA through torch).
 
-Besides the reference-shaped ``Transformer.forward(input_ids, start_pos)``,
+Besides the reference-shaped ``Transformer.forward(input_ids, attention_mask,
+start_pos)`` (and ``forward_full``),
 ``Transformer.forward_mixed`` runs one continuous-batching step that the
 reference cannot express (it has one start_pos per batch,
 transformer.py:146-160): new sequences prefilled in a rectangular group,
@@ -564,8 +565,13 @@ class Transformer(nn.Module):
         if int(start_pos) + int(input_ids.size(1)) > int(self.args.max_seq_len):
             raise ValueError("sequence exceeds max_seq_len")
 
-    def forward(self, input_ids: torch.Tensor, start_pos: int = 0) -> torch.Tensor:
-        """transformer.py:169-207: logits [B, S, vocab]."""
+    def forward(self, input_ids: torch.Tensor, attention_mask: torch.Tensor | None = None,
+                start_pos: int = 0) -> torch.Tensor:
+        """transformer.py:169-207: logits [B, S, vocab].  ``attention_mask`` is
+        taken and type-checked as the reference's forward does, and, as there,
+        not used: padding reaches the mixers through ``set_pad_mask``."""
+        if attention_mask is not None and not torch.is_tensor(attention_mask):
+            raise TypeError("attention_mask must be a tensor or None")
         _require_gpu(input_ids)
         self._validate(input_ids, start_pos)
         if self.args.use_cache:
@@ -577,6 +583,53 @@ class Transformer(nn.Module):
             hidden, completed, pending = layer(hidden, completed, start_pos=start_pos,
                                                pending=pending, defer=True)
         return self.output(self._final_mix(hidden, completed, pending))
+
+    def forward_full(self, input_ids: torch.Tensor, attention_mask: torch.Tensor | None = None,
+                     start_pos: int = 0) -> torch.Tensor:
+        """transformer.py:212-218: the same as ``forward``."""
+        return self.forward(input_ids, attention_mask=attention_mask, start_pos=start_pos)
+
+    def _forward_hidden(self, input_ids: torch.Tensor, start_pos: int) -> torch.Tensor:
+        """The final depth mix before the output norm (transformer.py:169-199)."""
+        _require_gpu(input_ids)
+        self._validate(input_ids, start_pos)
+        if self.args.use_cache:
+            self.ensure_batch_capacity(int(input_ids.size(0)))
+        hidden = self.tok_embeddings(input_ids)
+        completed = depth_store(hidden, self.args.n_layers, self.args.attn_res_block_size)
+        pending = None
+        for layer in self.layers:
+            hidden, completed, pending = layer(hidden, completed, start_pos=start_pos,
+                                               pending=pending, defer=True)
+        if pending is None:
+            return self.output_attn_residual(hidden, completed)
+        return self.output_attn_residual(hidden, completed, residual=pending)[1]
+
+    def forward_with_last_hidden(self, input_ids: torch.Tensor, start_pos: int = 0,
+                                 return_all_logits: bool = True):
+        """runtime_host.py:115-143: (logits, the last position's final mix
+        [B, dim]); logits [B, S, vocab], or [B, vocab] of the last position
+        when ``return_all_logits`` is False."""
+        mix = self._forward_hidden(input_ids, int(start_pos))
+        last_hidden = mix[:, -1, :]
+        head = mix if return_all_logits else mix[:, -1:, :]
+        logits = self.output(self.norm(head))
+        return (logits if return_all_logits else logits[:, 0, :]), last_hidden
+
+    def replay_with_cache(self, input_ids: torch.Tensor, start_pos: int = 0,
+                          return_all_logits: bool = True):
+        """runtime_host.py:146-170: a prompt (start_pos 0) or one token in one
+        pass; several tokens after cached ones one at a time (the incremental
+        forward takes one token), their logits concatenated."""
+        if int(input_ids.size(1)) <= 1 or int(start_pos) == 0:
+            return self.forward_with_last_hidden(input_ids, int(start_pos), return_all_logits)
+        outputs, last_hidden = [], None
+        for offset in range(int(input_ids.size(1))):
+            logits, last_hidden = self.forward_with_last_hidden(input_ids[:, offset:offset + 1],
+                                                                int(start_pos) + offset, True)
+            outputs.append(logits)
+        combined = torch.cat(outputs, dim=1)
+        return (combined if return_all_logits else combined[:, -1, :]), last_hidden
 
     def _final_mix(self, hidden, completed, pending):
         """norm(output_attn_residual(hidden + pending, completed)) as one kernel."""

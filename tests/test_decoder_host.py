@@ -101,3 +101,18 @@ def test_set_pad_mask_reaches_every_mixer_and_clearing_forgets_the_prompt_mask()
     set_pad_mask(model, None)
     assert all(m._pad_mask is None for m in kda + mla)
     assert mla[0]._key_mask(3, 2, 4, "cpu") is None
+
+
+def test_forward_rejects_a_non_tensor_attention_mask():
+    """transformer.py:201-209: forward(input_ids, attention_mask, start_pos)
+    takes a tensor or None as the mask, checked before any device work."""
+    import pytest
+    from sophia_amd.config import ModelArgs
+    from sophia_amd.decoder import Transformer
+
+    model = Transformer(ModelArgs(vocab_size=64, n_layers=4, ffn_hidden=64, mla_q_rank=16, mla_kv_rank=8,
+                                  dim=32, num_heads=2, max_seq_len=16, max_batch_size=2))
+    with pytest.raises(TypeError, match="attention_mask"):
+        model(torch.zeros(1, 4, dtype=torch.long), [1, 1, 1, 1])
+    with pytest.raises(TypeError, match="attention_mask"):
+        model.forward_full(torch.zeros(1, 4, dtype=torch.long), attention_mask="all")

@@ -75,6 +75,43 @@ def test_decoder_forward_matches_oracle_and_cached_decode():
     assert _rel(_np(torch.cat(steps, 1)), ref) < REL_TOL
     with pytest.raises(ValueError):
         model(ids[:, :2].to(dev), start_pos=3)   # transformer.py:150-153
+    # the reference's call forms: forward(input_ids, attention_mask, start_pos), forward_full
+    with torch.no_grad():
+        model.reset_runtime_cache()
+        again = model(ids.to(dev), None, 0)
+        full = model.forward_full(ids.to(dev), attention_mask=torch.ones(2, 40, device=dev), start_pos=0)
+    assert torch.equal(again, logits) and torch.equal(full, logits)
+
+
+def test_forward_with_last_hidden_and_replay_with_cache():
+    """The runtime host's entry points (runtime_host.py:115-170):
+    forward_with_last_hidden gives forward's logits (every position, or the
+    last one) and the last position's final depth mix, whose head
+    (output(norm(.))) is that position's logits; replay_with_cache of a prompt
+    and then of several tokens after it (one at a time) gives the one-pass
+    logits."""
+    dev = _dev()
+    model, _, _ = _model(dev, seed=11)
+    ids = torch.randint(0, 512, (2, 30), generator=torch.Generator().manual_seed(12)).to(dev)
+    with torch.no_grad():
+        model.reset_runtime_cache()
+        full = model(ids, start_pos=0)
+        model.reset_runtime_cache()
+        logits, last = model.forward_with_last_hidden(ids, 0)
+        model.reset_runtime_cache()
+        last_only, _ = model.forward_with_last_hidden(ids, 0, return_all_logits=False)
+        head = model.output(model.norm(last))
+        model.reset_runtime_cache()
+        a, _ = model.replay_with_cache(ids[:, :20], 0)
+        b, last_b = model.replay_with_cache(ids[:, 20:], 20)
+    assert logits.shape == full.shape and tuple(last.shape) == (2, 256) and tuple(last_only.shape) == (2, 512)
+    assert _rel(_np(logits), _np(full)) < 1e-4
+    assert _rel(_np(last_only), _np(full[:, -1])) < 1e-4
+    assert _rel(_np(head), _np(full[:, -1])) < 1e-4
+    err = _rel(_np(torch.cat([a, b], 1)), _np(full))
+    print(f"replayed prompt + 10 cached tokens vs one pass: {err:.2e}", flush=True)
+    assert tuple(b.shape) == (2, 10, 512) and err < 5e-3
+    assert _rel(_np(last_b), _np(last)) < 5e-3
 
 
 def _mixed_case(dev, model):
